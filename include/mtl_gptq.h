@@ -1,0 +1,157 @@
+/*
+ * mtl_gptq.h -- C ABI of the MI355X (gfx950) int4 GPTQ decode hot path.
+ *
+ * Library: moss-tts-lite_amd/libmtl_hip.so (hipcc --offload-arch=gfx950).
+ *
+ * Conventions shared by every entry point
+ *   - Return 0 (MTL_OK) on success, a negative MTL_ERR_* code otherwise; no
+ *     exception or abort crosses the ABI.  mtl_status_string() names a code.
+ *   - All tensor arguments are raw DEVICE pointers to contiguous row-major
+ *     memory owned by the caller; sizes are element counts.  bf16 and fp16
+ *     values are passed as their 16-bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Launch paths do not
+ *     allocate, synchronise or read device memory from the host, so every
+ *     launch is capturable into a hipGraph.
+ *   - Entry points are stateless and reentrant.  A workspace belongs to one
+ *     stream at a time: two launches that share a workspace must be ordered.
+ *
+ * Weight layout (both contracts): `qweight` int32 [K/8, N]; the 4-bit code of
+ * input channel k = 8*i + j of output column n is bits [4j, 4j+4) of
+ * qweight[i*N + n] (AutoGPTQ order, low nibble first).
+ */
+#ifndef MTL_GPTQ_H
+#define MTL_GPTQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MTL_OK = 0,
+  MTL_ERR_INVALID_ARG = -1,   /* null pointer, bad enum value            */
+  MTL_ERR_SHAPE = -2,         /* M/K/N out of range or not divisible      */
+  MTL_ERR_GROUP = -3,         /* group size not in {32, 64, 128, 256}     */
+  MTL_ERR_ALIGN = -4,         /* pointer not 16-byte aligned              */
+  MTL_ERR_WORKSPACE = -5,     /* workspace missing or too small           */
+  MTL_ERR_LAUNCH = -6,        /* HIP launch error                         */
+  MTL_ERR_UNSUPPORTED = -7    /* valid request this build does not serve  */
+};
+
+/* Output element type of the GEMM entry points. */
+enum { MTL_OUT_BF16 = 0, MTL_OUT_F32 = 1 };
+
+/* Fused epilogues of mtl_w4_gemm_fused. */
+enum {
+  MTL_EPI_NONE = 0,       /* y = acc (bf16 or f32 per out_dtype)                       */
+  MTL_EPI_RESIDUAL = 1,   /* y = bf16(bf16(acc) + resid)        (fast.py:168,170)      */
+  MTL_EPI_SILU_MUL = 2    /* y[j] = bf16(silu(bf16 gate_j) * bf16 up_j); columns come
+                             interleaved in blocks of 32 (gate|up) (fast.py:170-171)  */
+};
+
+/* Metadata format of mtl_w4_gemm_fused. */
+enum {
+  MTL_META_GPTQ = 0,      /* scales fp16 [K/g,N] + qzeros int32 [K/g,N/8]; w=(q-z)*s  */
+  MTL_META_QSZ = 1        /* qsz bf16 [K/g,N,2] = (scale, zero); w=(q-8)*scale+zero   */
+};
+
+const char* mtl_status_string(int status);
+int mtl_abi_version(void);
+
+/* Bytes of workspace a GEMM of this shape needs (split-K partial sums and
+ * tile counters).  The counter region must be zero before first use; every
+ * launch leaves it zero again.  mtl_workspace_init() zeroes a fresh buffer. */
+int64_t mtl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t group_size);
+int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * AutoGPTQ-layout GEMM, y[M,N] = x[M,K] @ dequant(W)[K,N], fp32 accumulation.
+ * Replaces the int4 GEMM the GPTQ linear dispatches to
+ * (reference: torch._weight_int4pack_mm via kernel_linear,
+ *  moss_tts_lite/gptq.py:577-585, 689-697).
+ *   x        bf16 [M, K], 1 <= M <= 16
+ *   qweight  int32 [K/8, N]  (group-sorted rows when perm != NULL)
+ *   qzeros   int32 [K/g, N/8], nibble z; effective zero = z + zero_offset
+ *   scales   fp16 [K/g, N]
+ *   perm     NULL (no act-order), or int32 [K] from mtl_gptq_actorder_prepare:
+ *            the kernel reads x[:, perm[k]] for sorted channel k
+ *   y        bf16 or f32 [M, N] (out_dtype)
+ * K % group_size == 0, group_size in {32,64,128,256}, N % 8 == 0.
+ */
+int mtl_gptq_gemm(const void* x, int64_t M, int64_t K,
+                  const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                  const int32_t* perm, int64_t N, int32_t group_size,
+                  int32_t zero_offset, void* y, int32_t out_dtype,
+                  void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * Act-order preparation: from an AutoGPTQ qweight whose input channels are
+ * grouped by an arbitrary g_idx (desc_act=True checkpoints), write the
+ * group-contiguous copy qweight_sorted[K/8, N] and the gather index perm[K]
+ * (stable argsort of g_idx).  Every group must own exactly group_size
+ * channels; otherwise MTL_ERR_GROUP.  `scratch` needs mtl_actorder_scratch_bytes(K).
+ * This is the load-time step the GPTQ linear module runs once per layer.
+ */
+int64_t mtl_actorder_scratch_bytes(int64_t K);
+int mtl_gptq_actorder_prepare(const int32_t* qweight, const int32_t* g_idx,
+                              int64_t K, int64_t N, int32_t group_size,
+                              int32_t* qweight_sorted, int32_t* perm,
+                              void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
+ * Reference-contract GEMM: y[M,N] = x[M,K] @ W^T with
+ * W[n,k] = (q-8)*qsz[k/g,n,0] + qsz[k/g,n,1] (bf16 pair widened to fp32).
+ * Replaces torch._weight_int4pack_mm(x, packed, g, qsz) at
+ * moss_tts_lite/fast.py:118, gptq.py:582, fast_native.py:169.
+ *   packed  int32 [K/8, N] from mtl_int4pack_convert (NOT torch's tiled bytes)
+ *   qsz     bf16 [K/g, N, 2]
+ *   y       bf16 [M, N]
+ */
+int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
+                    int32_t group_size, const void* qsz, int64_t N, void* y,
+                    void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * Reference-contract packer: the reference's nibble pre-pack uint8 [N, K/2]
+ * (byte = q[n,2i]<<4 | q[n,2i+1], moss_tts_lite/fast.py:98, gptq.py:76) ->
+ * packed int32 [K/8, N].  Replaces torch.ops.aten._convert_weight_to_int4pack
+ * (fast.py:97, gptq.py:75); inner_k_tiles is accepted for signature parity and
+ * must be 2, 4 or 8 (it does not change this layout).
+ */
+int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K,
+                         int32_t inner_k_tiles, int32_t* packed, void* stream);
+
+/* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
+int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
+                     void* stream);
+
+/* Dequantise to fp32 W[K, N] (AutoGPTQ meta; perm may be NULL) -- the exact
+ * value the GEMM multiplies by; used by the bit-exact dequant checks. */
+int mtl_gptq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                     int64_t K, int64_t N, int32_t group_size, int32_t zero_offset,
+                     float* w_out, void* stream);
+/* Same for the reference contract: fp32 W[K, N] = effective_weight(q, qsz).T
+ * (moss_tts_lite/gptq.py:87-97). */
+int mtl_qsz_dequant(const int32_t* packed, const void* qsz, int64_t K, int64_t N,
+                    int32_t group_size, float* w_out, void* stream);
+
+/*
+ * General entry with a fused epilogue, used by the decode step.
+ *   meta_format  MTL_META_GPTQ (meta0 = scales fp16, qzeros) or
+ *                MTL_META_QSZ (meta0 = qsz bf16 [K/g,N,2], qzeros = NULL)
+ *   epilogue     MTL_EPI_*; RESIDUAL reads resid[M,N] bf16 (may alias y);
+ *                SILU_MUL writes y[M, N/2]
+ */
+int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweight,
+                      int32_t meta_format, const void* meta0, const int32_t* qzeros,
+                      const int32_t* perm, int64_t N, int32_t group_size,
+                      int32_t zero_offset, int32_t epilogue, const void* resid,
+                      void* y, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTL_GPTQ_H */

@@ -1,0 +1,59 @@
+"""Build recipe of ``libmtl_hip.so``: every ``csrc/*.hip`` compiled for gfx950.
+
+The library exposes only the plain C ABI declared in ``include/mtl_gptq.h`` and
+``include/mtl_decode.h`` (raw device pointers, sizes, a ``hipStream_t``), so it
+links against whichever HIP runtime the process already has loaded (torch's).
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)
+LIB_NAME = "libmtl_hip.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: the gfx950 HIP library cannot be built")
+
+
+def sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(PKG_DIR, "csrc", "*.hip")))
+
+
+def command(out: str = LIB_PATH) -> list[str]:
+    return [
+        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        # Packed fp32 VALU ops stay off: write plain float code only.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG_DIR, "csrc"),
+        *sources(), "-o", out,
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the library in-tree (always recompiles) and return its path."""
+    tmp = LIB_PATH + ".tmp"
+    cmd = command(tmp)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,215 @@
+// Load-time layout utilities of the int4 path: the reference-contract packer, code
+// unpacking, exact dequantisation and the act-order (g_idx) reorder.
+#include "mtl_common.h"
+
+namespace mtl {
+
+// prepacked uint8 [N, K/2] (byte i of row n = q[n,2i] << 4 | q[n,2i+1]) ->
+// qweight int32 [K/8, N] (code of k = 8r + j in bits [4j, 4j+4) of word (r, n)).
+__global__ void int4pack_convert_kernel(const uint8_t* __restrict__ pre, int64_t N, int64_t K,
+                                        uint32_t* __restrict__ out) {
+  const int64_t rows = K / 8;
+  const int64_t total = rows * N;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / N;
+    const int64_t n = t - r * N;
+    const uint32_t b4 = *reinterpret_cast<const uint32_t*>(pre + n * (K / 2) + r * 4);
+    uint32_t w = 0;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t byte = (b4 >> (8 * jj)) & 0xffu;
+      w |= (byte >> 4) << (4 * (2 * jj));          // even k: high nibble
+      w |= (byte & 0xfu) << (4 * (2 * jj + 1));    // odd k: low nibble
+    }
+    out[t] = w;
+  }
+}
+
+__global__ void unpack_codes_kernel(const uint32_t* __restrict__ qw, int64_t K, int64_t N,
+                                    uint8_t* __restrict__ codes) {
+  const int64_t total = (K / 8) * N;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / N;
+    const int64_t n = t - r * N;
+    const uint32_t w = qw[t];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) codes[(r * 8 + j) * N + n] = (uint8_t)((w >> (4 * j)) & 0xfu);
+  }
+}
+
+// fp32 W[K, N]; fmt GPTQ: (q - (z + zero_offset)) * s ; QSZ: (q - 8) * scale + zero.
+template <int FMT>
+__global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* __restrict__ meta0,
+                               const uint32_t* __restrict__ qzeros, int64_t K, int64_t N,
+                               int group, int zero_offset, float* __restrict__ out) {
+  const int64_t total = (K / 8) * N;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / N;
+    const int64_t n = t - r * N;
+    const uint32_t w = qw[t];
+    const int64_t grp = (r * 8) / group;
+    float s, c, d;
+    if (FMT == MTL_META_QSZ) {
+      const uint16_t* q2 = meta0 + (grp * N + n) * 2;
+      s = bf16_to_f32(q2[0]);
+      d = bf16_to_f32(q2[1]);
+      c = 8.f;
+    } else {
+      s = f16_to_f32(meta0[grp * N + n]);
+      const uint32_t z = (qzeros[grp * (N / 8) + n / 8] >> (4 * (n & 7))) & 0xfu;
+      c = (float)((int)z + zero_offset);
+      d = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float q = (float)((w >> (4 * j)) & 0xfu);
+      // (q - c) * s is exact in fp32, so this equals the unfused closed form.
+      out[(r * 8 + j) * N + n] = fmaf(q - c, s, d);
+    }
+  }
+}
+
+// Stable counting sort of channels by group: one thread per group walks g_idx in order.
+// err[0] is set when a group does not own exactly `group` channels or g_idx is out of range.
+__global__ void actorder_perm_kernel(const int32_t* __restrict__ g_idx, int64_t K, int group,
+                                     int32_t* __restrict__ perm, int32_t* __restrict__ err) {
+  const int ngroups = (int)(K / group);
+  for (int g = blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += gridDim.x * blockDim.x) {
+    int cnt = 0;
+    for (int64_t k = 0; k < K; ++k) {
+      const int gk = g_idx[k];
+      if (gk < 0 || gk >= ngroups) { err[0] = 1; continue; }
+      if (gk == g) {
+        if (cnt < group) perm[(int64_t)g * group + cnt] = (int32_t)k;
+        ++cnt;
+      }
+    }
+    if (cnt != group) err[0] = 1;
+  }
+}
+
+// qweight_sorted[r, n] nibble j = code of channel perm[8r + j] in the original layout.
+__global__ void actorder_gather_kernel(const uint32_t* __restrict__ qw, const int32_t* __restrict__ perm,
+                                       int64_t K, int64_t N, uint32_t* __restrict__ out) {
+  const int64_t total = (K / 8) * N;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = t / N;
+    const int64_t n = t - r * N;
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t k = perm[r * 8 + j];
+      const uint32_t src = qw[(k >> 3) * N + n];
+      w |= ((src >> (4 * (k & 7))) & 0xfu) << (4 * j);
+    }
+    out[t] = w;
+  }
+}
+
+__global__ void fill_u32_kernel_pack(uint32_t* p, int64_t n, uint32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+static int grid_for(int64_t total) {
+  int64_t b = (total + 255) / 256;
+  if (b > 65536) b = 65536;
+  if (b < 1) b = 1;
+  return (int)b;
+}
+
+static bool valid_group(int g) { return g == 32 || g == 64 || g == 128 || g == 256; }
+
+}  // namespace mtl
+
+using namespace mtl;
+
+extern "C" {
+
+int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K, int32_t inner_k_tiles,
+                         int32_t* packed, void* stream) {
+  if (!prepacked || !packed) return MTL_ERR_INVALID_ARG;
+  if (inner_k_tiles != 2 && inner_k_tiles != 4 && inner_k_tiles != 8) return MTL_ERR_INVALID_ARG;
+  if (N <= 0 || K <= 0 || K % 8 != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  if (reinterpret_cast<uintptr_t>(prepacked) & 3u) return MTL_ERR_ALIGN;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL(int4pack_convert_kernel, dim3(grid_for(total)), dim3(256), 0,
+                     (hipStream_t)stream, prepacked, N, K, reinterpret_cast<uint32_t*>(packed));
+  return launch_status();
+}
+
+int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes, void* stream) {
+  if (!qweight || !codes) return MTL_ERR_INVALID_ARG;
+  if (N <= 0 || K <= 0 || K % 8 != 0) return MTL_ERR_SHAPE;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL(unpack_codes_kernel, dim3(grid_for(total)), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint32_t*>(qweight), K, N, codes);
+  return launch_status();
+}
+
+int mtl_gptq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, int64_t K,
+                     int64_t N, int32_t group_size, int32_t zero_offset, float* w_out,
+                     void* stream) {
+  if (!qweight || !qzeros || !scales || !w_out) return MTL_ERR_INVALID_ARG;
+  if (!valid_group(group_size)) return MTL_ERR_GROUP;
+  if (N <= 0 || K <= 0 || K % group_size != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL((dequant_kernel<MTL_META_GPTQ>), dim3(grid_for(total)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(qweight),
+                     static_cast<const uint16_t*>(scales), reinterpret_cast<const uint32_t*>(qzeros),
+                     K, N, group_size, zero_offset, w_out);
+  return launch_status();
+}
+
+int mtl_qsz_dequant(const int32_t* packed, const void* qsz, int64_t K, int64_t N, int32_t group_size,
+                    float* w_out, void* stream) {
+  if (!packed || !qsz || !w_out) return MTL_ERR_INVALID_ARG;
+  if (!valid_group(group_size)) return MTL_ERR_GROUP;
+  if (N <= 0 || K <= 0 || K % group_size != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL((dequant_kernel<MTL_META_QSZ>), dim3(grid_for(total)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(packed),
+                     static_cast<const uint16_t*>(qsz), nullptr, K, N, group_size, 0, w_out);
+  return launch_status();
+}
+
+int64_t mtl_actorder_scratch_bytes(int64_t K) {
+  (void)K;
+  return 256;
+}
+
+int mtl_gptq_actorder_prepare(const int32_t* qweight, const int32_t* g_idx, int64_t K, int64_t N,
+                              int32_t group_size, int32_t* qweight_sorted, int32_t* perm,
+                              void* scratch, int64_t scratch_bytes, void* stream) {
+  if (!qweight || !g_idx || !qweight_sorted || !perm || !scratch) return MTL_ERR_INVALID_ARG;
+  if (qweight == qweight_sorted) return MTL_ERR_INVALID_ARG;
+  if (scratch_bytes < mtl_actorder_scratch_bytes(K)) return MTL_ERR_WORKSPACE;
+  if (!valid_group(group_size)) return MTL_ERR_GROUP;
+  if (N <= 0 || K <= 0 || K % group_size != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* err = static_cast<int32_t*>(scratch);
+  hipLaunchKernelGGL(fill_u32_kernel_pack, dim3(1), dim3(64), 0, s,
+                     reinterpret_cast<uint32_t*>(err), (int64_t)1, 0u);
+  const int ngroups = (int)(K / group_size);
+  hipLaunchKernelGGL(actorder_perm_kernel, dim3((ngroups + 63) / 64), dim3(64), 0, s, g_idx, K,
+                     group_size, perm, err);
+  if (launch_status() != MTL_OK) return MTL_ERR_LAUNCH;
+  // Load-time step: the group check needs the result on the host.
+  int32_t h_err = 0;
+  if (hipMemcpyAsync(&h_err, err, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return MTL_ERR_LAUNCH;
+  if (h_err) return MTL_ERR_GROUP;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL(actorder_gather_kernel, dim3(grid_for(total)), dim3(256), 0, s,
+                     reinterpret_cast<const uint32_t*>(qweight), perm, K, N,
+                     reinterpret_cast<uint32_t*>(qweight_sorted));
+  return launch_status();
+}
+
+}  // extern "C"

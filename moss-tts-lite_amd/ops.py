@@ -1,0 +1,226 @@
+"""Torch-facing wrappers of the C ABI (device memory and streams come from torch).
+
+Each op takes torch tensors on a HIP device, checks shapes and dtypes the way the
+torch ops they replace do (``RuntimeError`` on a bad shape or group size), and
+launches on ``torch.cuda.current_stream()``, so the launches are recorded when
+the caller is inside ``torch.cuda.graph(...)``.
+
+Replaced reference calls (moss_tts_lite/...):
+  ``torch._weight_int4pack_mm``             fast.py:118, gptq.py:582, fast_native.py:169
+  ``aten._convert_weight_to_int4pack``      fast.py:97, gptq.py:75
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+_GROUPS = (32, 64, 128, 256)
+_MAX_M = 16
+_ws_cache: dict = {}
+
+
+def _ptr(t):
+    return None if t is None else ctypes_ptr(t)
+
+
+def ctypes_ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dev_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def reserve_workspace(device, nbytes: int) -> torch.Tensor:
+    """Make sure the per-device split-K workspace holds ``nbytes``; return it.
+
+    Call before graph capture: growing allocates.  The buffer starts zeroed and
+    every GEMM launch leaves its tile counters at zero again.
+    """
+    device = torch.device(device)
+    key = _dev_index(device)
+    ws = _ws_cache.get(key)
+    nbytes = max(int(nbytes), 256)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("int4 GEMM workspace must be reserved before graph capture")
+        nbytes = ((nbytes + 4095) // 4096) * 4096
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        N.check(N.load().mtl_workspace_init(ws.data_ptr(), nbytes, _stream(device)),
+                "mtl_workspace_init")
+        _ws_cache[key] = ws
+    return ws
+
+
+def gemm_workspace_bytes(m: int, k: int, n: int, group_size: int) -> int:
+    return int(N.load().mtl_gemm_workspace_bytes(min(m, _MAX_M), k, n, group_size))
+
+
+def _check_x(x: torch.Tensor, k: int) -> torch.Tensor:
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError(f"expected x to be bfloat16, got {x.dtype}")
+    if x.shape[-1] != k:
+        raise RuntimeError(f"x has K={x.shape[-1]}, weight expects K={k}")
+    if x.device.type != "cuda":
+        raise RuntimeError("int4 GEMM runs on a HIP device")
+    return x.reshape(-1, k).contiguous()
+
+
+def _check_group(g: int, k: int) -> None:
+    if g not in _GROUPS:
+        raise RuntimeError(f"qGroupSize must be 32, 64, 128 or 256, got {g}")
+    if k % g:
+        raise RuntimeError(f"K={k} is not a multiple of group size {g}")
+
+
+def w4_gemm(x2: torch.Tensor, qweight: torch.Tensor, meta_format: int, meta0: torch.Tensor,
+            qzeros, perm, n: int, group_size: int, zero_offset: int = 0,
+            epilogue: int = N.EPI_NONE, resid=None, out: torch.Tensor | None = None,
+            out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """General launch over row chunks of at most 16: ``out[M, n or n/2]``."""
+    m, k = x2.shape
+    dev = x2.device
+    ncols = n // 2 if epilogue == N.EPI_SILU_MUL else n
+    if out is None:
+        out = torch.empty(m, ncols, dtype=out_dtype, device=dev)
+    odt = N.OUT_F32 if out.dtype == torch.float32 else N.OUT_BF16
+    ws_need = gemm_workspace_bytes(min(m, _MAX_M), k, n, group_size)
+    ws = reserve_workspace(dev, ws_need)
+    lib = N.load()
+    stream = _stream(dev)
+    for r0 in range(0, m, _MAX_M):
+        r1 = min(m, r0 + _MAX_M)
+        rs = None if resid is None else resid[r0:r1]
+        st = lib.mtl_w4_gemm_fused(
+            x2[r0:r1].data_ptr(), r1 - r0, k, qweight.data_ptr(), meta_format, meta0.data_ptr(),
+            _ptr(qzeros), _ptr(perm), n, group_size, zero_offset, epilogue,
+            None if rs is None else rs.data_ptr(), out[r0:r1].data_ptr(), odt,
+            ws.data_ptr(), ws.numel(), stream)
+        N.check(st, "mtl_w4_gemm_fused")
+    return out
+
+
+def gptq_gemm(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+              group_size: int, perm: torch.Tensor | None = None, zero_offset: int = 0,
+              out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """``x[..., K] @ dequant(W)[K, N]`` for the AutoGPTQ layout (fp32 accumulation)."""
+    k = qweight.shape[0] * 8
+    n = qweight.shape[1]
+    _check_group(group_size, k)
+    x2 = _check_x(x, k)
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise RuntimeError("qweight and qzeros must be int32")
+    if scales.dtype != torch.float16 or tuple(scales.shape) != (k // group_size, n):
+        raise RuntimeError(f"scales must be float16 [{k // group_size}, {n}]")
+    if tuple(qzeros.shape) != (k // group_size, n // 8):
+        raise RuntimeError(f"qzeros must be int32 [{k // group_size}, {n // 8}]")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != k):
+        raise RuntimeError("perm must be int32 [K]")
+    y = w4_gemm(x2, qweight.contiguous(), N.META_GPTQ, scales.contiguous(), qzeros.contiguous(),
+                perm, n, group_size, zero_offset, out_dtype=out_dtype)
+    return y.reshape(*x.shape[:-1], n)
+
+
+def weight_int4pack_mm(x: torch.Tensor, packed: torch.Tensor, q_group_size: int,
+                       q_scale_and_zeros: torch.Tensor) -> torch.Tensor:
+    """Drop-in for ``torch._weight_int4pack_mm(x, packed, qGroupSize, qScaleAndZeros)``.
+
+    ``x`` bf16 ``[M, K]``; ``packed`` from :func:`convert_weight_to_int4pack`;
+    ``qScaleAndZeros`` bf16 ``[K/g, N, 2]`` = (scale, zero) with
+    ``w = (q - 8) * scale + zero`` (moss_tts_lite/gptq.py:87-97).  Returns bf16 ``[M, N]``.
+    """
+    if x.dim() != 2:
+        raise RuntimeError(f"x must be 2-D [M, K], got {tuple(x.shape)}")
+    k = packed.shape[0] * 8
+    n = packed.shape[1]
+    _check_group(q_group_size, k)
+    x2 = _check_x(x, k)
+    qsz = q_scale_and_zeros
+    if qsz.dtype != torch.bfloat16 or tuple(qsz.shape) != (k // q_group_size, n, 2):
+        raise RuntimeError(f"qScaleAndZeros must be bfloat16 [{k // q_group_size}, {n}, 2]")
+    if packed.dtype != torch.int32:
+        raise RuntimeError("packed weight must be int32")
+    return w4_gemm(x2, packed.contiguous(), N.META_QSZ, qsz.contiguous(), None, None, n,
+                   q_group_size)
+
+
+def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) -> torch.Tensor:
+    """Drop-in for ``aten._convert_weight_to_int4pack(uint8[N, K/2], innerKTiles)``.
+
+    Input is the reference's nibble pre-pack (even k in the high nibble,
+    moss_tts_lite/fast.py:98).  Output is this build's int32 ``[K/8, N]`` layout,
+    not torch's tiled bytes.
+    """
+    if prepacked.dtype != torch.uint8 or prepacked.dim() != 2:
+        raise RuntimeError("expected a uint8 [N, K/2] tensor")
+    if inner_k_tiles not in (2, 4, 8):
+        raise RuntimeError("innerKTiles must be 2, 4 or 8")
+    n, kh = prepacked.shape
+    k = kh * 2
+    if k % 8 or n % 8:
+        raise RuntimeError(f"K={k} must be a multiple of 8 and N={n} a multiple of 8")
+    src = prepacked.contiguous()
+    out = torch.empty(k // 8, n, dtype=torch.int32, device=src.device)
+    N.check(N.load().mtl_int4pack_convert(src.data_ptr(), n, k, inner_k_tiles, out.data_ptr(),
+                                          _stream(src.device)), "mtl_int4pack_convert")
+    return out
+
+
+def unpack_codes(qweight: torch.Tensor) -> torch.Tensor:
+    """``qweight [K/8, N]`` -> codes uint8 ``[K, N]``."""
+    k = qweight.shape[0] * 8
+    n = qweight.shape[1]
+    out = torch.empty(k, n, dtype=torch.uint8, device=qweight.device)
+    N.check(N.load().mtl_unpack_codes(qweight.contiguous().data_ptr(), k, n, out.data_ptr(),
+                                      _stream(qweight.device)), "mtl_unpack_codes")
+    return out
+
+
+def gptq_dequant(qweight, qzeros, scales, group_size: int, zero_offset: int = 0) -> torch.Tensor:
+    """Exact fp32 ``W[K, N]`` of the AutoGPTQ layout (in stored row order)."""
+    k = qweight.shape[0] * 8
+    n = qweight.shape[1]
+    out = torch.empty(k, n, dtype=torch.float32, device=qweight.device)
+    N.check(N.load().mtl_gptq_dequant(qweight.contiguous().data_ptr(), qzeros.contiguous().data_ptr(),
+                                      scales.contiguous().data_ptr(), k, n, group_size, zero_offset,
+                                      out.data_ptr(), _stream(qweight.device)), "mtl_gptq_dequant")
+    return out
+
+
+def qsz_dequant(packed, qsz, group_size: int) -> torch.Tensor:
+    """Exact fp32 ``W[K, N]`` of the reference contract (``effective_weight(q, qsz).T``)."""
+    k = packed.shape[0] * 8
+    n = packed.shape[1]
+    out = torch.empty(k, n, dtype=torch.float32, device=packed.device)
+    N.check(N.load().mtl_qsz_dequant(packed.contiguous().data_ptr(), qsz.contiguous().data_ptr(),
+                                     k, n, group_size, out.data_ptr(), _stream(packed.device)),
+            "mtl_qsz_dequant")
+    return out
+
+
+def actorder_prepare(qweight: torch.Tensor, g_idx: torch.Tensor, group_size: int):
+    """Group-contiguous copy of an act-order ``qweight`` and its gather index ``perm``.
+
+    Load-time only (synchronises the stream to validate ``g_idx``).
+    """
+    k = qweight.shape[0] * 8
+    n = qweight.shape[1]
+    if g_idx.numel() != k:
+        raise RuntimeError(f"g_idx must have K={k} entries")
+    dev = qweight.device
+    g32 = g_idx.to(device=dev, dtype=torch.int32).contiguous()
+    sorted_qw = torch.empty_like(qweight)
+    perm = torch.empty(k, dtype=torch.int32, device=dev)
+    lib = N.load()
+    sb = int(lib.mtl_actorder_scratch_bytes(k))
+    scratch = torch.empty(sb, dtype=torch.uint8, device=dev)
+    N.check(lib.mtl_gptq_actorder_prepare(qweight.contiguous().data_ptr(), g32.data_ptr(), k, n,
+                                          group_size, sorted_qw.data_ptr(), perm.data_ptr(),
+                                          scratch.data_ptr(), sb, _stream(dev)),
+            "mtl_gptq_actorder_prepare")
+    return sorted_qw, perm

@@ -1,0 +1,90 @@
+"""The C-ABI library loads, exports every symbol the headers declare, and rejects bad
+arguments with the documented status codes before touching a device (CPU only)."""
+import ctypes
+
+import pytest
+
+from moss_tts_lite_amd import _native as N
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return N.load()
+
+
+def test_every_header_symbol_is_exported(lib):
+    names = N.header_symbols()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_every_bound_symbol_is_declared():
+    declared = set(N.header_symbols())
+    undeclared = [n for n in N._SIGNATURES if n not in declared and n != "mtl_tune_set_waves"]
+    assert not undeclared, undeclared
+
+
+def test_status_strings(lib):
+    assert lib.mtl_status_string(0) == b"ok"
+    assert lib.mtl_status_string(N.MTL_ERR_GROUP) == b"unsupported group size"
+    assert lib.mtl_abi_version() == 1
+
+
+def test_workspace_bytes(lib):
+    # counters (rounded to 256 B) + deepest split partials: K/128 row blocks x M x N fp32
+    assert lib.mtl_gemm_workspace_bytes(1, 4096, 24576, 128) == 512 + 32 * 24576 * 4  # 96 tiles
+    assert lib.mtl_gemm_workspace_bytes(0, 4096, 4096, 128) == 0
+    assert lib.mtl_gemm_workspace_bytes(17, 4096, 4096, 128) == 0
+
+
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: every call below fails validation
+
+
+@pytest.mark.parametrize("group,expect", [(16, N.MTL_ERR_GROUP), (96, N.MTL_ERR_GROUP),
+                                          (512, N.MTL_ERR_GROUP)])
+def test_gemm_rejects_group_sizes(lib, group, expect):
+    st = lib.mtl_gptq_gemm(FAKE, 1, 4096, FAKE, FAKE, FAKE, None, 4096, group, 0, FAKE, 0,
+                           None, 0, None)
+    assert st == expect
+
+
+def test_gemm_rejects_bad_shapes(lib):
+    args = lambda m, k, n: lib.mtl_gptq_gemm(FAKE, m, k, FAKE, FAKE, FAKE, None, n, 128, 0,  # noqa: E731
+                                             FAKE, 0, None, 0, None)
+    assert args(0, 4096, 4096) == N.MTL_ERR_SHAPE
+    assert args(17, 4096, 4096) == N.MTL_ERR_SHAPE
+    assert args(1, 4000, 4096) == N.MTL_ERR_SHAPE     # K not a multiple of the group
+    assert args(1, 4096, 4100) == N.MTL_ERR_SHAPE     # N not a multiple of 8
+
+
+def test_gemm_rejects_null_and_misaligned(lib):
+    assert lib.mtl_gptq_gemm(None, 1, 4096, FAKE, FAKE, FAKE, None, 4096, 128, 0, FAKE, 0,
+                             None, 0, None) == N.MTL_ERR_INVALID_ARG
+    odd = ctypes.c_void_p(0x1008)
+    assert lib.mtl_gptq_gemm(FAKE, 1, 4096, odd, FAKE, FAKE, None, 4096, 128, 0, FAKE, 0,
+                             None, 0, None) == N.MTL_ERR_ALIGN
+
+
+def test_gemm_needs_workspace_for_split_k(lib):
+    # 4096 x 24576 splits K across workgroups, so a missing workspace is an error
+    st = lib.mtl_gptq_gemm(FAKE, 1, 4096, FAKE, FAKE, FAKE, None, 24576, 128, 0, FAKE, 0,
+                           None, 0, None)
+    assert st == N.MTL_ERR_WORKSPACE
+
+
+def test_fused_epilogue_validation(lib):
+    st = lib.mtl_w4_gemm_fused(FAKE, 1, 4096, FAKE, N.META_QSZ, FAKE, None, None, 4128, 128, 0,
+                               N.EPI_SILU_MUL, None, FAKE, 0, None, 0, None)
+    assert st == N.MTL_ERR_SHAPE        # SiLU*up pairs need N % 64 == 0
+    st = lib.mtl_w4_gemm_fused(FAKE, 1, 4096, FAKE, N.META_QSZ, FAKE, None, None, 4096, 128, 0,
+                               N.EPI_RESIDUAL, None, FAKE, 0, None, 0, None)
+    assert st == N.MTL_ERR_INVALID_ARG  # residual epilogue without a residual
+    st = lib.mtl_w4_gemm_fused(FAKE, 1, 4096, FAKE, N.META_QSZ, FAKE, None, FAKE, 4096, 128, 0,
+                               N.EPI_NONE, None, FAKE, 0, None, 0, None)
+    assert st == N.MTL_ERR_INVALID_ARG  # act-order gather is a GPTQ-meta feature
+
+
+def test_converter_validation(lib):
+    assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE

@@ -1,0 +1,276 @@
+"""GPU parity of the int4 GEMV / skinny GEMM and its load-time utilities.
+
+Bars: bit-exact for unpacked codes, packed layouts, act-order index and dequantised
+weights; GEMM output within rel-L2 1e-3 (fp32 output, fp32 accumulation) and 1e-2
+(bf16 output) of the oracle's float64 product -- the reference's own kernel gate is
+rel < 5e-3 at bf16 (tests/test_quant.py:96-119), which the bf16 cases also meet.
+"""
+import numpy as np
+import pytest
+import torch
+
+from moss_tts_lite_amd import _native as N
+from moss_tts_lite_amd import ops
+from oracle import gptq_ref as G
+from oracle import synth
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 1e-2
+
+
+def t_i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+
+
+def t_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def t_f16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.float16)).to(dev)
+
+
+def rel_l2(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def run_gptq(case, dev, act_order, out_dtype=torch.float32, zero_offset=0):
+    qw = t_i32(case["qweight"], dev)
+    qz = t_i32(case["qzeros"], dev)
+    sc = t_f16(case["scales"], dev)
+    x = t_bf16(case["x_bits"], dev)
+    perm = None
+    if act_order:
+        qw, perm = ops.actorder_prepare(qw, torch.from_numpy(case["g_idx"]).to(dev), case["group"])
+    y = ops.gptq_gemm(x, qw, qz, sc, case["group"], perm=perm, zero_offset=zero_offset,
+                      out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+# ------------------------------------------------------------------ bit-exact utilities
+
+def test_unpack_codes_bit_exact(dev):
+    r = np.random.default_rng(1)
+    qw = synth.random_qweight(r, 512, 264)
+    got = ops.unpack_codes(t_i32(qw, dev)).cpu().numpy()
+    assert np.array_equal(got, G.unpack_qweight(qw))
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+@pytest.mark.parametrize("zero_offset", [0, 1])
+def test_gptq_dequant_bit_exact(dev, group, zero_offset):
+    case = synth.gptq_case(k=1024, n=136, group=group, seed=group + zero_offset, with_ref=False)
+    got = ops.gptq_dequant(t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev),
+                           t_f16(case["scales"], dev), group, zero_offset).cpu().numpy()
+    ref = G.gptq_dequant(case["qweight"], case["qzeros"], case["scales"], None, group, zero_offset)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_qsz_dequant_bit_exact(dev, group):
+    case = synth.qsz_case(k=512, n=96, group=group, seed=group)
+    packed = t_i32(G.qweight_from_reference_codes(case["q"]), dev)
+    got = ops.qsz_dequant(packed, t_bf16(case["qsz"], dev), group).cpu().numpy()
+    ref = G.effective_weight(case["q"], case["qsz"], group).T
+    assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(ref).view(np.uint32))
+
+
+def test_int4pack_convert_bit_exact(dev):
+    r = np.random.default_rng(2)
+    q = r.integers(0, 16, size=(200, 384)).astype(np.uint8)      # [N, K]
+    pre = G.prepack_u8(q)
+    got = ops.convert_weight_to_int4pack(torch.from_numpy(pre).to(dev), 8).cpu().numpy()
+    assert np.array_equal(got, G.int4pack_from_prepacked(pre))
+    assert np.array_equal(G.unpack_qweight(got), q.T)
+
+
+def test_actorder_prepare_bit_exact(dev):
+    case = synth.gptq_case(k=2048, n=264, group=128, act_order=True, seed=3, with_ref=False)
+    qs, perm = ops.actorder_prepare(t_i32(case["qweight"], dev),
+                                    torch.from_numpy(case["g_idx"]).to(dev), 128)
+    ref_qs, ref_perm = G.actorder_sort(case["qweight"], case["g_idx"], 128)
+    assert np.array_equal(perm.cpu().numpy(), ref_perm)
+    assert np.array_equal(qs.cpu().numpy(), ref_qs)
+
+
+def test_actorder_prepare_rejects_uneven_groups(dev):
+    g_idx = torch.tensor([0] * 160 + [1] * 96, dtype=torch.int32, device=dev)
+    qw = torch.zeros(32, 8, dtype=torch.int32, device=dev)
+    with pytest.raises(N.MtlError):
+        ops.actorder_prepare(qw, g_idx, 128)
+
+
+# ------------------------------------------------------------------ GEMM parity
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("act_order", [False, True])
+def test_gptq_gemm_rows(dev, m, act_order):
+    case = synth.gptq_case(k=1024, n=768, m=m, group=128, act_order=act_order, seed=10 + m)
+    y = run_gptq(case, dev, act_order)
+    err = rel_l2(y, case["y_ref"])
+    print(f"gptq M={m} act={act_order} rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+def test_gptq_gemm_groups(dev, group):
+    case = synth.gptq_case(k=2048, n=512, m=2, group=group, act_order=True, seed=group)
+    for odt, tol in ((torch.float32, TOL_F32), (torch.bfloat16, TOL_BF16)):
+        err = rel_l2(run_gptq(case, dev, True, out_dtype=odt), case["y_ref"])
+        print(f"gptq g={group} {odt} rel_l2={err:.2e}")
+        assert err < tol
+
+
+@pytest.mark.parametrize("k,n", [(32, 8), (96, 24), (256, 264), (640, 1000), (12288, 264)])
+def test_gptq_gemm_ragged_shapes(dev, k, n):
+    group = 32
+    case = synth.gptq_case(k=k, n=n, m=3, group=group, act_order=False, seed=k + n)
+    err = rel_l2(run_gptq(case, dev, False), case["y_ref"])
+    print(f"gptq K={k} N={n} rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+def test_gptq_zero_offset_v1_checkpoints(dev):
+    case = synth.gptq_case(k=512, n=256, m=1, group=128, seed=77, with_ref=False)
+    x = bf16_bits_to_f32(case["x_bits"])
+    ref = synth.chunked_gptq_gemm(x, case["qweight"], case["qzeros"], case["scales"],
+                                  case["g_idx"], 128, zero_offset=1)
+    err = rel_l2(run_gptq(case, dev, False, zero_offset=1), ref)
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("name,k,n", [("qkv", 4096, 6144), ("o", 4096, 4096),
+                                      ("gate_up", 4096, 24576), ("down", 12288, 4096)])
+def test_gptq_gemm_full_size_actorder(dev, name, k, n):
+    cols = np.random.default_rng(0).choice(n, size=512, replace=False)
+    cols.sort()
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, act_order=True, seed=1234, ref_cols=cols)
+    y = run_gptq(case, dev, True)
+    err = rel_l2(y[:, cols], case["y_ref"])
+    print(f"{name} K={k} N={n} act-order rel_l2={err:.2e} (512 sampled columns)")
+    assert err < TOL_F32
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_gate_up_skinny_batch(dev, m):
+    cols = np.arange(0, 24576, 48)
+    case = synth.gptq_case(k=4096, n=24576, m=m, group=128, act_order=False, seed=99 + m,
+                           ref_cols=cols)
+    y = run_gptq(case, dev, False)
+    err = rel_l2(y[:, cols], case["y_ref"])
+    print(f"gate_up M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+# ------------------------------------------------------------------ reference contract
+
+@pytest.mark.parametrize("n,k,m", [(512, 512, 8), (1024, 4096, 8), (4096, 4096, 1)])
+def test_int4pack_mm_matches_effective_weight(dev, n, k, m):
+    # Mirrors the reference's G2 gate (tests/test_quant.py:96-119): kernel vs
+    # x.float() @ effective_weight(q, qsz).T, rel < 5e-3.
+    case = synth.qsz_case(k=k, n=n, m=m, group=128, seed=n)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(case["prepacked"]).to(dev), 8)
+    y = ops.weight_int4pack_mm(t_bf16(case["x_bits"], dev), packed, 128, t_bf16(case["qsz"], dev))
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (m, n)
+    err = rel_l2(y.float().cpu().numpy(), case["y_ref"])
+    print(f"int4pack_mm N={n} K={k} M={m} rel_l2={err:.2e}")
+    assert err < 5e-3
+
+
+def test_int4pack_group_sizes_like_g9(dev):
+    # reference G9 (tests/test_quant.py:427-457): 32..256 accepted, 16 rejected
+    case = synth.qsz_case(k=4096, n=256, m=4, group=128, seed=1)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(case["prepacked"]).to(dev), 8)
+    x = t_bf16(case["x_bits"], dev)
+    w = synth.reference_weight(256, 4096, seed=1)
+    for g in (32, 64, 128, 256):
+        q, s, mn = G.rtn_quantize(w, g)
+        qsz = G.pack_qsz(s, mn)
+        pk = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+        y = ops.weight_int4pack_mm(x, pk, g, t_bf16(qsz, dev)).float().cpu().numpy()
+        ref = G.int4pack_mm(bf16_bits_to_f32(case["x_bits"]), q, qsz, g)
+        assert rel_l2(y, ref) < 5e-3
+    q, s, mn = G.rtn_quantize(w, 16)
+    with pytest.raises(RuntimeError):
+        ops.weight_int4pack_mm(x, packed, 16, t_bf16(G.pack_qsz(s, mn), dev))
+
+
+# ------------------------------------------------------------------ fused epilogues
+
+def test_residual_epilogue(dev):
+    case = synth.qsz_case(k=1024, n=512, m=1, group=128, seed=5)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(case["prepacked"]).to(dev), 8)
+    x = t_bf16(case["x_bits"], dev).reshape(1, -1)
+    resid_bits = f32_to_bf16_bits(np.random.default_rng(6).standard_normal((1, 512)).astype(np.float32))
+    resid = t_bf16(resid_bits, dev)
+    y = ops.w4_gemm(x, packed, N.META_QSZ, t_bf16(case["qsz"], dev), None, None, 512, 128,
+                    epilogue=N.EPI_RESIDUAL, resid=resid)
+    # h + linear(x): the linear output is rounded to bf16, then added in fp32 and rounded
+    lin = bf16_bits_to_f32(f32_to_bf16_bits(case["y_ref"].astype(np.float32)))
+    ref = bf16_bits_to_f32(f32_to_bf16_bits(lin + bf16_bits_to_f32(resid_bits)))
+    got = y.float().cpu().numpy()
+    assert rel_l2(got, ref) < TOL_BF16
+    # in place (y aliases the residual), as the decode step uses it
+    y2 = ops.w4_gemm(x, packed, N.META_QSZ, t_bf16(case["qsz"], dev), None, None, 512, 128,
+                     epilogue=N.EPI_RESIDUAL, resid=resid, out=resid)
+    assert torch.equal(y2, y)
+
+
+def test_silu_mul_epilogue(dev):
+    k, inter = 1024, 256
+    case = synth.gptq_case(k=k, n=2 * inter, m=2, group=128, seed=12)
+    # interleave gate/up columns in blocks of 32 as the fused layout requires
+    order = np.concatenate([np.r_[b * 32:(b + 1) * 32, inter + b * 32:inter + (b + 1) * 32]
+                            for b in range(inter // 32)])
+    qw = case["qweight"][:, order]
+    sc = case["scales"][:, order]
+    z = G.unpack_qzeros(case["qzeros"])[:, order]
+    qz = G.pack_qzeros(z)
+    x = t_bf16(case["x_bits"], dev)
+    y = ops.w4_gemm(x, t_i32(qw, dev), N.META_GPTQ, t_f16(sc, dev), t_i32(qz, dev), None,
+                    2 * inter, 128, epilogue=N.EPI_SILU_MUL)
+    assert tuple(y.shape) == (2, inter)
+    yr = case["y_ref"].astype(np.float32)
+    g = bf16_bits_to_f32(f32_to_bf16_bits(yr[:, :inter]))
+    u = bf16_bits_to_f32(f32_to_bf16_bits(yr[:, inter:]))
+    sg = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.0 + np.exp(-g))))
+    ref = bf16_bits_to_f32(f32_to_bf16_bits(sg * u))
+    err = rel_l2(y.float().cpu().numpy(), ref)
+    print(f"silu_mul rel_l2={err:.2e}")
+    assert err < TOL_BF16
+
+
+# ------------------------------------------------------------------ determinism + graphs
+
+def test_deterministic_and_graph_replay(dev):
+    case = synth.gptq_case(k=4096, n=24576, m=1, group=128, act_order=True, seed=4, with_ref=False)
+    qw, perm = ops.actorder_prepare(t_i32(case["qweight"], dev),
+                                    torch.from_numpy(case["g_idx"]).to(dev), 128)
+    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    x = t_bf16(case["x_bits"], dev)
+    y0 = ops.gptq_gemm(x, qw, qz, sc, 128, perm=perm)
+    y1 = ops.gptq_gemm(x, qw, qz, sc, 128, perm=perm)
+    assert torch.equal(y0, y1)
+    out = torch.empty_like(y0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.w4_gemm(x.reshape(1, -1), qw, N.META_GPTQ, sc, qz, perm, 24576, 128, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.w4_gemm(x.reshape(1, -1), qw, N.META_GPTQ, sc, qz, perm, 24576, 128, out=out)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y0), f"replay {i}"
+        ops.gptq_gemm(x, qw, qz, sc, 128, perm=perm)   # eager work between replays

@@ -1,0 +1,193 @@
+"""Pins the oracle's int4 formats and dequant closed forms.
+
+Each check is chosen so that a plausible slip in the oracle fails it: brute force
+on tiny inputs, known-answer words, torch's independent CPU int4 kernel, and the
+exact special cases of the closed forms.  Nothing here retypes a formula as its
+own check.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gptq_ref as G
+from oracle import synth
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+
+
+# ---------------------------------------------------------------- nibble orders
+
+def test_qweight_known_answer_low_nibble_first():
+    codes = np.arange(1, 9, dtype=np.uint8).reshape(8, 1)          # k = 0..7 -> 1..8
+    w = G.pack_qweight(codes)
+    assert w.shape == (1, 1)
+    assert w.view(np.uint32)[0, 0] == 0x87654321
+
+
+def test_qzeros_known_answer_along_n():
+    z = np.array([[9, 8, 7, 6, 5, 4, 3, 2]], dtype=np.uint8)
+    assert G.pack_qzeros(z).view(np.uint32)[0, 0] == 0x23456789
+
+
+def test_reference_prepack_even_k_high_nibble():
+    q = np.array([[0xA, 0x3, 0x1, 0xF]], dtype=np.uint8)
+    assert G.prepack_u8(q).tolist() == [[0xA3, 0x1F]]
+
+
+@pytest.mark.parametrize("k,n", [(8, 8), (64, 24), (256, 40)])
+def test_pack_round_trips(k, n):
+    r = np.random.default_rng(k + n)
+    codes = r.integers(0, 16, size=(k, n)).astype(np.uint8)
+    assert np.array_equal(G.unpack_qweight(G.pack_qweight(codes)), codes)
+    z = r.integers(0, 16, size=(k // 8, n)).astype(np.uint8)
+    assert np.array_equal(G.unpack_qzeros(G.pack_qzeros(z)), z)
+    qn = codes.T.copy()
+    assert np.array_equal(G.unprepack_u8(G.prepack_u8(qn)), qn)
+    # reference pre-pack -> device layout keeps every (n, k) code
+    assert np.array_equal(G.unpack_qweight(G.int4pack_from_prepacked(G.prepack_u8(qn))), codes)
+
+
+def test_pack_brute_force_bits():
+    r = np.random.default_rng(3)
+    codes = r.integers(0, 16, size=(16, 5)).astype(np.uint8)
+    w = G.pack_qweight(codes).view(np.uint32)
+    for k in range(16):
+        for n in range(5):
+            assert (int(w[k // 8, n]) >> (4 * (k % 8))) & 0xF == codes[k, n]
+
+
+# ---------------------------------------------------------------- RTN + qsz
+
+def test_rtn_brute_force_nearest_grid_point():
+    r = np.random.default_rng(11)
+    w = (r.standard_normal((6, 64)) * 0.05).astype(np.float32)
+    w = bf16_bits_to_f32(f32_to_bf16_bits(w))
+    q, s, mn = G.rtn_quantize(w, 32)
+    for n in range(6):
+        for k in range(64):
+            g = k // 32
+            t = float(np.float32(np.float32(w[n, k]) - mn[n, g]) / np.float32(s[n, g]))
+            cands = sorted(range(16), key=lambda c: (abs(t - c), c % 2))   # ties -> even
+            assert q[n, k] == cands[0], (n, k, t)
+    # the group extremes land on the grid ends
+    wg = w.reshape(6, 2, 32)
+    for n in range(6):
+        for g in range(2):
+            assert q[n, g * 32 + int(np.argmin(wg[n, g]))] == 0
+            assert q[n, g * 32 + int(np.argmax(wg[n, g]))] == 15
+
+
+def test_rtn_scale_floor():
+    w = np.zeros((2, 64), dtype=np.float32)
+    q, s, mn = G.rtn_quantize(w, 32)
+    assert np.all(s == np.float32(1e-6)) and np.all(q == 0) and np.all(mn == 0)
+
+
+def test_qsz_rounding_matches_torch():
+    r = np.random.default_rng(5)
+    s = r.uniform(1e-4, 1e-2, size=(7, 4)).astype(np.float32)
+    mn = (-r.uniform(0, 0.3, size=(7, 4))).astype(np.float32)
+    qsz = G.pack_qsz(s, mn)
+    ts, tm = torch.from_numpy(s), torch.from_numpy(mn)
+    ref = torch.stack([ts, tm + 8.0 * ts], -1).bfloat16().transpose(0, 1).contiguous()
+    assert np.array_equal(qsz, ref.view(torch.int16).numpy().view(np.uint16))
+
+
+# ---------------------------------------------------------------- dequant closed forms
+
+def test_effective_weight_special_cases():
+    r = np.random.default_rng(9)
+    n, k, g = 4, 64, 32
+    s = r.uniform(1e-3, 1e-2, size=(n, k // g)).astype(np.float32)
+    mn = (-r.uniform(0, 0.1, size=(n, k // g))).astype(np.float32)
+    qsz = G.pack_qsz(s, mn)
+    scale = bf16_bits_to_f32(qsz[:, :, 0]).T
+    zero = bf16_bits_to_f32(qsz[:, :, 1]).T
+    # q == 8 gives the stored zero exactly; each code step adds exactly one scale
+    w8 = G.effective_weight(np.full((n, k), 8, np.uint8), qsz, g).reshape(n, k // g, g)
+    assert np.array_equal(w8, np.broadcast_to(zero[..., None], w8.shape))
+    for q in range(16):
+        wq = G.effective_weight(np.full((n, k), q, np.uint8), qsz, g).reshape(n, k // g, g)
+        exact = (np.float64(q) - 8.0) * scale.astype(np.float64) + zero.astype(np.float64)
+        assert np.allclose(wq[..., 0], exact, rtol=0, atol=np.abs(exact).max() * 2 ** -23)
+    # storage-rounded scale/min reproduce the same grid
+    s_eff, mn_eff = G.bf16_effective_scale_zero(s, mn)
+    assert np.array_equal(s_eff, scale.astype(np.float32))
+
+
+def test_effective_weight_matches_torch_cpu_int4_kernel():
+    # torch's own CPU int4 op uses the same (scale, zero) contract independently.
+    n, k, g = 64, 512, 128
+    w = synth.reference_weight(n, k, seed=3)
+    q, s, mn = G.rtn_quantize(w, g)
+    qsz = G.pack_qsz(s, mn)
+    r = np.random.default_rng(4)
+    x = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal((4, k)).astype(np.float32)))
+    ours = G.int4pack_mm(x, q, qsz, g)
+    tq = torch.from_numpy(q.astype(np.int32))
+    packed = torch.ops.aten._convert_weight_to_int4pack_for_cpu(tq, 1)
+    tqsz = torch.from_numpy(qsz.view(np.int16)).view(torch.bfloat16)
+    tx = torch.from_numpy(x).bfloat16()
+    theirs = torch.ops.aten._weight_int4pack_mm_for_cpu(tx, packed, g, tqsz).float().numpy()
+    rel = np.linalg.norm(theirs - ours) / np.linalg.norm(ours)
+    assert rel < 5e-3, rel
+    # a transposed operand or a dropped zero term is far outside this band
+    bad = G.int4pack_mm(x, q, np.stack([qsz[..., 0], qsz[..., 0]], -1), g)
+    assert np.linalg.norm(theirs - bad) / np.linalg.norm(bad) > 0.1
+
+
+def test_gptq_dequant_brute_force():
+    r = np.random.default_rng(21)
+    k, n, g = 64, 16, 32
+    codes = r.integers(0, 16, size=(k, n)).astype(np.uint8)
+    z = r.integers(0, 16, size=(k // g, n)).astype(np.uint8)
+    s = r.uniform(0.002, 0.02, size=(k // g, n)).astype(np.float16)
+    perm = r.permutation(k)
+    g_idx = G.actorder_g_idx(perm, g)
+    for zo in (0, 1):
+        w = G.gptq_dequant(G.pack_qweight(codes), G.pack_qzeros(z), s.view(np.uint16), g_idx, g, zo)
+        for kk in range(k):
+            for nn in range(n):
+                gg = int(g_idx[kk])
+                want = (int(codes[kk, nn]) - int(z[gg, nn]) - zo) * float(s[gg, nn])
+                assert w[kk, nn] == np.float32(want)
+
+
+def test_actorder_g_idx_definition():
+    perm = np.array([3, 0, 2, 1, 7, 5, 6, 4])
+    gi = G.actorder_g_idx(perm, 4)
+    assert gi.tolist() == [0, 0, 0, 0, 1, 1, 1, 1]
+    # g_idx[perm[r]] == r // 4
+    assert all(gi[perm[r]] == r // 4 for r in range(8))
+
+
+def test_actorder_sort_invariance():
+    case = synth.gptq_case(k=512, n=64, m=3, group=128, act_order=True, seed=5)
+    qs, perm = G.actorder_sort(case["qweight"], case["g_idx"], 128)
+    # sorted channel r is original channel perm[r]; its group is r // 128
+    w_orig = G.gptq_dequant(case["qweight"], case["qzeros"], case["scales"], case["g_idx"], 128)
+    w_sorted = G.gptq_dequant(qs, case["qzeros"], case["scales"], None, 128)
+    assert np.array_equal(w_sorted, w_orig[perm])
+    x = bf16_bits_to_f32(case["x_bits"])
+    assert np.allclose(G.gemm_f64(x[:, perm], w_sorted), case["y_ref"], rtol=1e-12, atol=1e-9)
+
+
+def test_actorder_sort_rejects_uneven_groups():
+    g_idx = np.array([0] * 9 + [1] * 7, dtype=np.int32)
+    qw = np.zeros((2, 8), dtype=np.int32)
+    with pytest.raises(ValueError):
+        G.actorder_sort(qw, g_idx, 8)
+
+
+def test_gptq_gemm_against_float64_brute_force():
+    case = synth.gptq_case(k=64, n=8, m=2, group=32, act_order=True, seed=8)
+    x = bf16_bits_to_f32(case["x_bits"]).astype(np.float64)
+    codes = G.unpack_qweight(case["qweight"])
+    z = G.unpack_qzeros(case["qzeros"])
+    s = case["scales"].view(np.float16).astype(np.float64)
+    for m in range(2):
+        for n in range(8):
+            acc = 0.0
+            for k in range(64):
+                gg = case["g_idx"][k]
+                acc += x[m, k] * (int(codes[k, n]) - int(z[gg, n])) * s[gg, n]
+            assert abs(acc - case["y_ref"][m, n]) <= 1e-9 * max(1.0, abs(acc))
