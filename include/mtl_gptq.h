@@ -59,9 +59,9 @@ enum {
 const char* mtl_status_string(int status);
 int mtl_abi_version(void);
 
-/* Bytes of workspace a GEMM of this shape needs (split-K partial sums and
- * tile counters).  The counter region must be zero before first use; every
- * launch leaves it zero again.  mtl_workspace_init() zeroes a fresh buffer. */
+/* Bytes of workspace a GEMM of this shape needs: a 16 KB tile-counter region
+ * followed by fp32 split-K partial tiles.  The counters must be zero before
+ * first use (mtl_workspace_init zero-fills); every launch leaves them zero. */
 int64_t mtl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t group_size);
 int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream);
 

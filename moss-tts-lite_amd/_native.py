@@ -41,6 +41,7 @@ _SIGNATURES = {
                                  _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i32,
                                  _c_void_p, _i64, _c_void_p]),
     "mtl_tune_set_waves": (_i32, [_i32]),
+    "mtl_tune_set_reduce": (_i32, [_i32]),
 }
 
 MTL_OK = 0

@@ -8,15 +8,15 @@
 // written as w = (q - c) * s + d.  Since (q - c) * s is exact in fp32, both equal the
 // exact dequantised weight.
 //
-// Work decomposition (one launch, no atomics on outputs, deterministic):
+// Work decomposition (deterministic, no atomics):
 //   * a wave owns a 256-column tile (64 lanes x 4 columns = one 16-byte qweight load per
 //     lane per row, 1 KB contiguous per wave) and 16 qweight rows (128 input channels);
 //     it issues all 16 loads up front, so the whole weight slice of the chip is in flight;
 //   * a workgroup stacks 1, 2 or 4 waves along K and reduces them through LDS;
-//   * blockIdx.y splits K further; each workgroup writes its fp32 partial tile, and the
-//     last workgroup to finish a tile (agent-scope counter) sums the partials in split
-//     order, applies the epilogue and resets the counter, so the next launch needs no
-//     memset and graph replays are bitwise repeatable.
+//   * blockIdx.y splits K further; each workgroup publishes an fp32 partial tile and
+//     the last workgroup of the tile (agent-scope counter) sums the splits in split
+//     order, applies the epilogue and resets the counter, so results (and graph
+//     replays) are bitwise repeatable and the next launch needs no memset.
 //
 // Inner loop: a qweight word holds 8 codes; OR-ing nibble pairs into 0x4300 gives the
 // bf16 pair (128 + q_j, 128 + q_{j+4}), and x is staged in LDS in the same pair order,
@@ -34,6 +34,8 @@ constexpr int kTileN = 256;        // output columns per wave tile
 constexpr int kRowsPerWave = 16;   // qweight rows (x 8 input channels) per wave
 constexpr int kMaxWaves = 4;       // waves stacked along K in one workgroup
 constexpr int kMaxM = 16;
+// Cache policy of the weight stream (read once per step): non-temporal.
+constexpr int kStreamAux = 2;
 
 struct W4Args {
   const uint16_t* x;        // bf16 [M, K]
@@ -44,7 +46,8 @@ struct W4Args {
   const uint16_t* resid;    // RESIDUAL epilogue input [M, N]
   void* y;
   float* partial;           // [splits, M, N]
-  unsigned* counters;       // [col_tiles]
+  unsigned* counters;       // [col_tiles], zero between launches
+  int inkernel_reduce;      // 1: last workgroup reduces; 0: w4_reduce_kernel does
   int M, K, N, group, zero_offset, splits, epilogue, out_f32;
 };
 
@@ -142,7 +145,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   for (int r = 0; r < RB; ++r) {
     const int row = wrow0 + r < rows_total ? wrow0 + r : rows_last;
     wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          qrsrc, voff, row * N * 4, 0));
+                                          qrsrc, voff, row * N * 4, kStreamAux));
   }
 
   if (PERM) load_x();
@@ -264,34 +267,70 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
     }
   }
 
-  // 7. Cross-workgroup split-K: publish the partial tile; the last workgroup of the
-  //    tile sums all partials in split order and resets the tile counter.
+  // 7. Split-K.  Every workgroup publishes its fp32 partial tile.  With an in-kernel
+  //    reduction the partials travel as relaxed agent-scope atomics (coherent across
+  //    XCDs without a whole-L2 writeback), a per-tile counter names the last workgroup,
+  //    and that one sums all splits in split order (loads batched 8 deep) and resets
+  //    the counter.  Otherwise w4_reduce_kernel (or a fused consumer) sums them.
   if (a.splits > 1) {
+    float* pbase = a.partial + (size_t)split * M * N + col0;
+    if (!a.inkernel_reduce) {
+      if (col_ok) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+          if (m < M)
+            *reinterpret_cast<float4*>(pbase + (size_t)m * N) =
+                make_float4(tot[m][0], tot[m][1], tot[m][2], tot[m][3]);
+      }
+      return;
+    }
     if (col_ok) {
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        if (m < M)
-          *reinterpret_cast<float4*>(a.partial + ((size_t)split * M + m) * N + col0) =
-              make_float4(tot[m][0], tot[m][1], tot[m][2], tot[m][3]);
+        if (m < M) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            __hip_atomic_store(pbase + (size_t)m * N + c, tot[m][c], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);   // every partial store acknowledged before the count
     int last = 0;
-    if (lane == 0) last = atomicAdd(&a.counters[tile], 1u) == (unsigned)(a.splits - 1);
+    if (lane == 0)
+      last = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(a.splits - 1);
     last = __builtin_amdgcn_readfirstlane(__shfl(last, 0));
     if (!last) return;
-    __threadfence();
+    const int S = a.splits;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      float s4[4] = {0.f, 0.f, 0.f, 0.f};
       if (col_ok && m < M) {
-        for (int sp = 0; sp < a.splits; ++sp) {
-          const float4 v = ld_f4(a.partial + ((size_t)sp * M + m) * N + col0);
-          s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+        const float* q = a.partial + (size_t)m * N + col0;
+        const size_t stride = (size_t)M * N;
+        for (int s0 = 0; s0 < S; s0 += 8) {
+          float v[8][4];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int sp = s0 + j < S ? s0 + j : S - 1;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              v[j][c] = __hip_atomic_load(q + sp * stride + c, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (s0 + j < S) {
+#pragma unroll
+              for (int c = 0; c < 4; ++c) s4[c] += v[j][c];
+            }
         }
       }
-      tot[m][0] = s.x; tot[m][1] = s.y; tot[m][2] = s.z; tot[m][3] = s.w;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) tot[m][c] = s4[c];
     }
-    if (lane == 0) a.counters[tile] = 0u;
+    if (lane == 0)
+      __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // 8. Epilogue, 4 consecutive columns per lane.
@@ -343,6 +382,79 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   }
 }
 
+// Sum the split-K partial tiles in split order and apply the epilogue.  One thread
+// per 4 consecutive output columns of one row (for SILU_MUL: 4 gate columns and their
+// 4 up partners 32 columns to the right).
+__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
+  g = round_bf16(g);
+  const float sg = round_bf16(g / (1.0f + expf(-g)));
+  return f32_to_bf16(sg * round_bf16(u));
+}
+
+__global__ void __launch_bounds__(256) w4_reduce_kernel(W4Args a) {
+  const int N = a.N, M = a.M;
+  const int S = a.splits;
+  const int quads = (a.epilogue == MTL_EPI_SILU_MUL) ? N / 8 : N / 4;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * quads) return;
+  const int m = t / quads;
+  const int q = t - m * quads;
+  if (a.epilogue == MTL_EPI_SILU_MUL) {
+    // quad q covers gate columns 64*(q/8) + 4*(q%8) .. +3, up columns +32
+    const int col = 64 * (q >> 3) + 4 * (q & 7);
+    float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+    const float* base = a.partial + (size_t)m * N + col;
+    const size_t stride = (size_t)M * N;
+    for (int s0 = 0; s0 < S; s0 += 8) {   // 8 independent loads in flight, summed in order
+      float4 vg[8], vu[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sp = s0 + j < S ? s0 + j : S - 1;
+        vg[j] = ld_f4(base + sp * stride);
+        vu[j] = ld_f4(base + sp * stride + 32);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < S) {
+          g[0] += vg[j].x; g[1] += vg[j].y; g[2] += vg[j].z; g[3] += vg[j].w;
+          u[0] += vu[j].x; u[1] += vu[j].y; u[2] += vu[j].z; u[3] += vu[j].w;
+        }
+    }
+    const int o = 32 * (q >> 3) + 4 * (q & 7);
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + (size_t)m * (N / 2) + o) =
+        u32x2{silu_mul_bf16(g[0], u[0]) | (silu_mul_bf16(g[1], u[1]) << 16),
+              silu_mul_bf16(g[2], u[2]) | (silu_mul_bf16(g[3], u[3]) << 16)};
+    return;
+  }
+  const int col = 4 * q;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const float* base = a.partial + (size_t)m * N + col;
+  const size_t stride = (size_t)M * N;
+  for (int s0 = 0; s0 < S; s0 += 8) {   // 8 independent loads in flight, summed in order
+    float4 p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = ld_f4(base + (s0 + j < S ? s0 + j : S - 1) * stride);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < S) { v[0] += p[j].x; v[1] += p[j].y; v[2] += p[j].z; v[3] += p[j].w; }
+  }
+  const size_t o = (size_t)m * N + col;
+  if (a.epilogue == MTL_EPI_RESIDUAL) {
+    const u32x2 rr = *reinterpret_cast<const u32x2*>(a.resid + o);
+    v[0] = round_bf16(v[0]) + bf16_to_f32(rr.x & 0xffffu);
+    v[1] = round_bf16(v[1]) + bf16_to_f32(rr.x >> 16);
+    v[2] = round_bf16(v[2]) + bf16_to_f32(rr.y & 0xffffu);
+    v[3] = round_bf16(v[3]) + bf16_to_f32(rr.y >> 16);
+  }
+  if (a.out_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + o) =
+        u32x2{f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
+              f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
+  }
+}
+
 // ----------------------------------------------------------------------------
 // Launch planning
 // ----------------------------------------------------------------------------
@@ -362,13 +474,9 @@ static Plan plan_for(int64_t K, int64_t N) {
   if (g_tune_waves == 1 || g_tune_waves == 2 || g_tune_waves == 4) {
     w = g_tune_waves;
   } else {
-    // Fill the chip: prefer the widest workgroup that still gives >= 2 per CU.
-    const int cands[3] = {4, 2, 1};
-    for (int i = 0; i < 3; ++i) {
-      const int c = cands[i];
-      const int wgs = p.col_tiles * ((p.row_blocks + c - 1) / c);
-      if (wgs >= 512 || c == 1) { w = c; break; }
-    }
+    // Four waves per workgroup measured best on every decode shape (fewest splits,
+    // so the least split-K traffic and counter work).
+    w = 4;
   }
   while (w > 1 && w > p.row_blocks) w >>= 1;
   p.waves = w;
@@ -376,10 +484,10 @@ static Plan plan_for(int64_t K, int64_t N) {
   return p;
 }
 
-static int64_t counters_bytes(int64_t N) {
-  const int64_t tiles = (N + kTileN - 1) / kTileN;
-  return ((tiles * 4 + 255) / 256) * 256;
-}
+// Workspace = a fixed tile-counter region (so partial tiles of one shape never land on
+// another shape's counters) followed by the fp32 partial tiles [splits, M, N].
+constexpr int64_t kCounterBytes = 16384;   // 4096 column tiles: N <= 1M
+static int g_inkernel_reduce = 1;
 
 template <int MR, int RPG>
 static void launch_fmt(const W4Args& a, int fmt, dim3 grid, dim3 block, hipStream_t s) {
@@ -414,6 +522,7 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   if (M < 1 || M > kMaxM || K <= 0 || N <= 0) return MTL_ERR_SHAPE;
   if (K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (epilogue == MTL_EPI_SILU_MUL && N % 64 != 0) return MTL_ERR_SHAPE;
+  if ((N + kTileN - 1) / kTileN > kCounterBytes / 4) return MTL_ERR_SHAPE;
   // The weight buffer's byte size and row offsets are 32-bit in the buffer descriptor.
   if (K * N / 2 >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
   if (!aligned16(qweight) || !aligned16(x) || (perm && !aligned16(perm))) return MTL_ERR_ALIGN;
@@ -437,13 +546,13 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   a.out_f32 = out_dtype == MTL_OUT_F32;
   a.partial = nullptr;
   a.counters = nullptr;
+  a.inkernel_reduce = g_inkernel_reduce;
   if (p.splits > 1) {
-    const int64_t cb = counters_bytes(N);
-    const int64_t need = cb + (int64_t)p.splits * M * N * 4;
+    const int64_t need = kCounterBytes + (int64_t)p.splits * M * N * 4;
     if (!workspace || ws_bytes < need) return MTL_ERR_WORKSPACE;
     if (!aligned16(workspace)) return MTL_ERR_ALIGN;
     a.counters = static_cast<unsigned*>(workspace);
-    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + cb);
+    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   }
   const dim3 grid(p.col_tiles, p.splits);
   const dim3 block(64 * p.waves);
@@ -454,6 +563,10 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
     case 4: launch_rpg<4>(a, fmt, grid, block, stream); break;
     case 8: launch_rpg<8>(a, fmt, grid, block, stream); break;
     default: launch_rpg<16>(a, fmt, grid, block, stream); break;
+  }
+  if (p.splits > 1 && !a.inkernel_reduce) {
+    const int quads = (int)(M * (epilogue == MTL_EPI_SILU_MUL ? N / 8 : N / 4));
+    hipLaunchKernelGGL(w4_reduce_kernel, dim3((quads + 255) / 256), dim3(256), 0, stream, a);
   }
   return launch_status();
 }
@@ -491,7 +604,7 @@ int64_t mtl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t group_
   (void)group_size;
   const int64_t row_blocks = (K / 8 + kRowsPerWave - 1) / kRowsPerWave;
   // Sized for the deepest split (one wave per workgroup), so any plan fits.
-  return counters_bytes(N) + row_blocks * M * N * 4;
+  return kCounterBytes + row_blocks * M * N * 4;
 }
 
 int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream) {
@@ -533,6 +646,13 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
 
 // Tuning knob for launch-shape sweeps: force 1, 2 or 4 waves per workgroup (0 restores
 // the heuristic).  Process-wide; not for concurrent use.
+// Split-K reduction: 1 = in-kernel (last workgroup of a tile), 0 = separate kernel.
+int mtl_tune_set_reduce(int32_t inkernel) {
+  if (inkernel != 0 && inkernel != 1) return MTL_ERR_INVALID_ARG;
+  g_inkernel_reduce = inkernel;
+  return MTL_OK;
+}
+
 int mtl_tune_set_waves(int32_t waves) {
   if (waves != 0 && waves != 1 && waves != 2 && waves != 4) return MTL_ERR_INVALID_ARG;
   g_tune_waves = waves;
