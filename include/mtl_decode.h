@@ -1,0 +1,86 @@
+/*
+ * mtl_decode.h -- C ABI of the batch-1 decode-step kernels around the int4 GEMV
+ * (MI355X / gfx950).  Same conventions as mtl_gptq.h: 0 = MTL_OK, negative =
+ * MTL_ERR_*, raw device pointers, bf16 as 16-bit patterns, a hipStream_t, no
+ * allocation or host synchronisation, capturable into a hipGraph.
+ *
+ * The decode position is read from device memory (`pos`, int64), so one
+ * captured step serves every cache length (the reference captures one graph
+ * per length: moss_tts_lite/fast_native.py:369-386).
+ */
+#ifndef MTL_DECODE_H
+#define MTL_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * RMSNorm over rows, op for op as the reference's Qwen3RMSNorm
+ * (moss_tts_lite/model.py:34-40): out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))
+ * with fp32 statistics.  x, w, out bf16; x [rows, n], w [n]; out may alias x.
+ */
+int mtl_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int64_t n,
+                float eps, void* stream);
+
+/*
+ * Embedding lookup and sum (moss_tts_lite/model.py:156-161, fast.py:123-128):
+ * out = bf16(...bf16(T0[ids[0]] + T1[ids[1]]) + ...), each table bf16 [vocab_i, hidden].
+ *   ids     int64 [n_tables] (device)
+ *   tables  device array of n_tables table base pointers
+ *   vocabs  device array of n_tables row counts (ids outside [0, vocab) read as 0)
+ */
+int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* tables,
+                  const int64_t* vocabs, int64_t hidden, void* out, void* stream);
+
+/*
+ * Per-head q/k RMSNorm, RoPE and KV-cache write for one decode position
+ * (moss_tts_lite/fast.py:134-147, model.py:175-185).
+ *   qkv      bf16 [(n_heads + 2*n_kv_heads) * head_dim] = q | k | v projections
+ *   q_norm_w, k_norm_w  bf16 [head_dim]
+ *   cos_tab, sin_tab    bf16 [max_seq, head_dim] (model.py:115-124)
+ *   pos      int64 device scalar; positions outside [0, max_seq) write nothing
+ *   q_out    bf16 [n_heads * head_dim] (normed, rotated)
+ *   k_cache, v_cache  bf16 [n_kv_heads, max_seq, head_dim] of this layer
+ * head_dim must be 128.
+ */
+int mtl_qk_norm_rope_kv(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                        const void* cos_tab, const void* sin_tab, const int64_t* pos,
+                        void* q_out, void* k_cache, void* v_cache, int32_t n_heads,
+                        int32_t n_kv_heads, int32_t head_dim, int64_t max_seq, float eps,
+                        void* stream);
+
+/*
+ * GQA decode attention over cache positions [0, pos] (the reference's SDPA call at
+ * moss_tts_lite/fast.py:149-162, exact length pos + 1): split over the sequence
+ * in chunks, fp32 softmax, chunk partials combined in chunk order.
+ *   q    bf16 [n_heads * head_dim];  out bf16 [n_heads * head_dim]
+ *   scale  softmax scale (1/sqrt(head_dim) in the reference)
+ * head_dim must be 128; n_heads % n_kv_heads == 0.
+ */
+int64_t mtl_decode_attention_workspace_bytes(int32_t n_heads, int32_t head_dim);
+int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                         const int64_t* pos, void* out, int32_t n_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int64_t max_seq, float scale, void* workspace,
+                         int64_t ws_bytes, void* stream);
+
+/*
+ * bf16 output head with greedy selection: logits[n] = bf16(sum_k W[n,k] x[k])
+ * (moss_tts_lite/fast.py:180, F.linear with a bf16 weight [N, K]) and
+ * token_out[0] = argmax(logits) (first maximum; NaN counts as the maximum).
+ * Either output may be NULL.  K % 8 == 0.
+ */
+int64_t mtl_head_workspace_bytes(int64_t N);
+int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, void* logits,
+                         int64_t* token_out, void* workspace, int64_t ws_bytes, void* stream);
+
+/* pos[0] += 1 on the device (ends a captured decode step). */
+int mtl_advance_position(int64_t* pos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTL_DECODE_H */

@@ -40,6 +40,20 @@ _SIGNATURES = {
     "mtl_w4_gemm_fused": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _c_void_p,
                                  _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _c_void_p, _i32,
                                  _c_void_p, _i64, _c_void_p]),
+    # mtl_decode.h
+    "mtl_rmsnorm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, ctypes.c_float, _c_void_p]),
+    "mtl_embed_sum": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "mtl_qk_norm_rope_kv": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                   _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64,
+                                   ctypes.c_float, _c_void_p]),
+    "mtl_decode_attention_workspace_bytes": (_i64, [_i32, _i32]),
+    "mtl_decode_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32,
+                                    _i32, _i64, ctypes.c_float, _c_void_p, _i64, _c_void_p]),
+    "mtl_head_workspace_bytes": (_i64, [_i64]),
+    "mtl_bf16_gemv_argmax": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
+                                    _c_void_p, _i64, _c_void_p]),
+    "mtl_advance_position": (_i32, [_c_void_p, _c_void_p]),
+    # tuning knobs (not part of the headers)
     "mtl_tune_set_waves": (_i32, [_i32]),
     "mtl_tune_set_reduce": (_i32, [_i32]),
 }

@@ -1,0 +1,213 @@
+"""GPTQ linear module and the reference's int4 format helpers (torch, device resident).
+
+``GPTQLinear`` carries the AutoGPTQ buffers ``qweight`` int32 ``[K/8, N]``,
+``qzeros`` int32 ``[K/g, N/8]``, ``scales`` fp16 ``[K/g, N]`` and ``g_idx`` int32
+``[K]`` unchanged; :meth:`GPTQLinear.post_init` builds the device-side group-sorted
+copy an act-order checkpoint needs and forward runs the gfx950 int4 GEMV.
+
+The helpers mirror moss_tts_lite/gptq.py:35-97 on torch tensors
+(``rtn_quantize``, ``pack_fast``, ``pack_qsz_only``, ``effective_weight``) and
+``kernel_linear`` mirrors gptq.py:577-585 on this build's op.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+from . import ops
+
+__all__ = ["GPTQLinear", "fuse_gptq_linears", "group_scales_from_weight", "rtn_quantize",
+           "pack_fast", "pack_qsz_only", "effective_weight", "kernel_linear",
+           "interleave_gate_up"]
+
+
+class GPTQLinear(torch.nn.Module):
+    """4-bit GPTQ linear, ``y = x @ dequant(qweight)`` with AutoGPTQ buffers.
+
+    Dequant: ``w[k, n] = (q[k, n] - (z[g_idx[k], n] + zero_offset)) * s[g_idx[k], n]``;
+    ``zero_offset`` is 0 for checkpoints storing ``z`` and 1 for ones storing ``z - 1``.
+    """
+
+    def __init__(self, in_features: int, out_features: int, group_size: int = 128,
+                 bias: bool = False, zero_offset: int = 0, device=None):
+        super().__init__()
+        if group_size not in (32, 64, 128, 256):
+            raise ValueError("group_size must be 32/64/128/256")
+        if in_features % group_size or out_features % 8:
+            raise ValueError("in_features must divide by group_size and out_features by 8")
+        if bias:
+            raise ValueError("the int4 decode path has no bias term")
+        self.in_features, self.out_features = in_features, out_features
+        self.group_size = group_size
+        self.zero_offset = int(zero_offset)
+        g = in_features // group_size
+        self.register_buffer("qweight", torch.zeros(in_features // 8, out_features, dtype=torch.int32, device=device))
+        self.register_buffer("qzeros", torch.zeros(g, out_features // 8, dtype=torch.int32, device=device))
+        self.register_buffer("scales", torch.zeros(g, out_features, dtype=torch.float16, device=device))
+        self.register_buffer("g_idx", (torch.arange(in_features, dtype=torch.int32, device=device)
+                                       // group_size).to(torch.int32))
+        self._kernel_qweight: torch.Tensor | None = None
+        self._perm: torch.Tensor | None = None
+
+    @classmethod
+    def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
+                     zero_offset: int = 0) -> "GPTQLinear":
+        k = qweight.shape[0] * 8
+        n = qweight.shape[1]
+        m = cls(k, n, group_size, zero_offset=zero_offset, device=qweight.device)
+        m.qweight = qweight.contiguous()
+        m.qzeros = qzeros.contiguous()
+        m.scales = scales.contiguous()
+        if g_idx is not None:
+            m.g_idx = g_idx.to(device=qweight.device, dtype=torch.int32).contiguous()
+        return m
+
+    def is_act_order(self) -> bool:
+        trivial = torch.arange(self.in_features, device=self.g_idx.device, dtype=torch.int32) \
+            // self.group_size
+        return not torch.equal(self.g_idx, trivial)
+
+    @torch.no_grad()
+    def post_init(self) -> "GPTQLinear":
+        """Build the kernel-side weight: for act-order, the group-sorted copy and gather index."""
+        if self.is_act_order():
+            self._kernel_qweight, self._perm = ops.actorder_prepare(self.qweight, self.g_idx,
+                                                                    self.group_size)
+        else:
+            self._kernel_qweight, self._perm = self.qweight, None
+        return self
+
+    def kernel_args(self):
+        if self._kernel_qweight is None:
+            self.post_init()
+        return self._kernel_qweight, self.qzeros, self.scales, self._perm
+
+    def drop_original(self) -> None:
+        """Free the unsorted ``qweight`` once the sorted copy exists (load-time memory)."""
+        if self._perm is not None:
+            self.qweight = torch.empty(0, dtype=torch.int32, device=self.qweight.device)
+
+    def forward(self, x: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        qw, qz, sc, perm = self.kernel_args()
+        return ops.gptq_gemm(x, qw, qz, sc, self.group_size, perm=perm,
+                             zero_offset=self.zero_offset, out_dtype=out_dtype)
+
+    def dequantize(self) -> torch.Tensor:
+        """Exact fp32 ``W[K, N]`` in the original input-channel order."""
+        qw, qz, sc, perm = self.kernel_args()
+        w = ops.gptq_dequant(qw, qz, sc, self.group_size, self.zero_offset)
+        if perm is None:
+            return w
+        out = torch.empty_like(w)
+        out[perm.long()] = w
+        return out
+
+
+def fuse_gptq_linears(parts: list[GPTQLinear]) -> GPTQLinear:
+    """Concatenate GPTQ linears along the output dim (same input, same g_idx).
+
+    Bitwise neutral per output column: each column's K accumulation is untouched
+    (the reference fuses (q,k) and (gate,up) the same way, fast_native.py:146-161).
+    """
+    g = parts[0].group_size
+    for p in parts[1:]:
+        if p.group_size != g or p.in_features != parts[0].in_features:
+            raise ValueError("fused linears need the same K and group size")
+        if not torch.equal(p.g_idx, parts[0].g_idx) or p.zero_offset != parts[0].zero_offset:
+            raise ValueError("fused linears need the same g_idx and zero convention")
+    return GPTQLinear.from_buffers(torch.cat([p.qweight for p in parts], 1),
+                                   torch.cat([p.qzeros for p in parts], 1),
+                                   torch.cat([p.scales for p in parts], 1), parts[0].g_idx,
+                                   g, parts[0].zero_offset)
+
+
+def interleave_gate_up(gate: GPTQLinear, up: GPTQLinear, block: int = 32) -> GPTQLinear:
+    """Fuse gate and up into one linear whose columns alternate 32-wide blocks
+    ``[gate 0:32 | up 0:32 | gate 32:64 | ...]``: the layout the SiLU*up epilogue reads."""
+    n = gate.out_features
+    if up.out_features != n or n % block:
+        raise ValueError("gate and up need the same N, a multiple of 32")
+    fused = fuse_gptq_linears([gate, up])
+    dev = gate.qweight.device
+    b = torch.arange(n // block, device=dev)
+    cols = torch.stack([b * block, n + b * block], 1).reshape(-1, 1) + torch.arange(block, device=dev)
+    cols = cols.reshape(-1)
+    zeros = _unpack_cols(fused.qzeros)[:, cols]
+    return GPTQLinear.from_buffers(fused.qweight[:, cols].contiguous(), _pack_cols(zeros),
+                                   fused.scales[:, cols].contiguous(), fused.g_idx,
+                                   fused.group_size, fused.zero_offset)
+
+
+def _unpack_cols(qzeros: torch.Tensor) -> torch.Tensor:
+    z = qzeros.to(torch.int64) & 0xFFFFFFFF
+    return torch.stack([(z >> (4 * j)) & 0xF for j in range(8)], -1).reshape(qzeros.shape[0], -1)
+
+
+def _pack_cols(z: torch.Tensor) -> torch.Tensor:
+    z = z.to(torch.int64).reshape(z.shape[0], -1, 8)
+    w = torch.zeros(z.shape[:2], dtype=torch.int64, device=z.device)
+    for j in range(8):
+        w |= (z[..., j] & 0xF) << (4 * j)
+    return ((w + 2**31) % 2**32 - 2**31).to(torch.int32)
+
+
+# ---------------------------------------------------------------------------------
+# The reference's (codes, qsz) format helpers (moss_tts_lite/gptq.py:35-97)
+# ---------------------------------------------------------------------------------
+
+def group_scales_from_weight(w2d: torch.Tensor, group_size: int = 128):
+    """Per-(row, group) ``s = clamp((max - min)/15, 1e-6)`` and ``min`` (gptq.py:35-45)."""
+    n, k = w2d.shape
+    if k % group_size:
+        raise ValueError(f"K={k} not divisible by group_size={group_size}")
+    wg = w2d.reshape(n, k // group_size, group_size)
+    mx, mn = wg.amax(-1), wg.amin(-1)
+    return ((mx - mn) / 15.0).clamp(min=1e-6), mn
+
+
+def rtn_quantize(w2d: torch.Tensor, group_size: int = 128):
+    """Round-to-nearest codes ``uint8 [N, K]`` plus ``(s, mn)`` (gptq.py:54-64)."""
+    w = w2d.float()
+    n, k = w.shape
+    s, mn = group_scales_from_weight(w, group_size)
+    wg = w.reshape(n, k // group_size, group_size)
+    q = ((wg - mn.unsqueeze(-1)) / s.unsqueeze(-1)).round().clamp(0, 15).to(torch.uint8)
+    return q.reshape(n, k), s, mn
+
+
+def pack_qsz_only(s: torch.Tensor, mn: torch.Tensor, group_size: int = 128) -> torch.Tensor:
+    """``qsz`` bf16 ``[K/g, N, 2]`` = (scale, mn + 8 scale) (gptq.py:79-85)."""
+    del group_size
+    return torch.stack([s, mn + 8.0 * s], -1).bfloat16().transpose(0, 1).contiguous()
+
+
+def pack_fast(q: torch.Tensor, s: torch.Tensor, mn: torch.Tensor, inner_k_tiles: int = 8):
+    """``(packed, qsz)`` for :func:`ops.weight_int4pack_mm` (gptq.py:66-77): the same
+    nibble pre-pack as the reference, converted to this build's layout."""
+    q = q.to(torch.uint8).contiguous()
+    qsz = pack_qsz_only(s, mn)
+    pre = (q[:, 1::2] | (q[:, 0::2] << 4)).contiguous()
+    return ops.convert_weight_to_int4pack(pre, inner_k_tiles), qsz
+
+
+def effective_weight(q: torch.Tensor, qsz: torch.Tensor, group_size: int = 128,
+                     dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``w = (q - 8) * scale + zero`` (gptq.py:87-97)."""
+    n, k = q.shape
+    scale = qsz[:, :, 0].t().to(dtype)
+    zero = qsz[:, :, 1].t().to(dtype)
+    qf = q.to(dtype).reshape(n, k // group_size, group_size)
+    return ((qf - 8.0) * scale.unsqueeze(-1) + zero.unsqueeze(-1)).reshape(n, k)
+
+
+def kernel_linear(x: torch.Tensor, packed: torch.Tensor, g: int, qsz: torch.Tensor,
+                  out_dtype: torch.dtype) -> torch.Tensor:
+    """int4 GEMM shaped like ``F.linear`` (gptq.py:577-585)."""
+    shp = x.shape
+    out = ops.weight_int4pack_mm(x.reshape(-1, shp[-1]), packed, g, qsz)
+    if out.dtype != out_dtype:
+        out = out.to(out_dtype)
+    return out.reshape(*shp[:-1], qsz.shape[1])
+
+
+del N

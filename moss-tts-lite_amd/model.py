@@ -1,0 +1,150 @@
+"""Device-resident int4 GPTQ backbone of the decode step (Qwen3-8B-shaped stand-in).
+
+Mirrors the state ``MossTTSModel`` owns (moss_tts_lite/model.py:46-124): embedding,
+per-layer norms and projections, final norm, output head, RoPE tables and the dense
+bf16 KV cache ``[layers, kv_heads, max_seq, head_dim]`` (model.py:110-112).  The
+seven projections of a layer are held as four GPTQ linears: fused q|k|v, o,
+gate/up interleaved in 32-column blocks (the layout the fused SiLU*up epilogue
+reads), and down.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import torch
+
+from .gptq import GPTQLinear
+
+ROPE_THETA = 1_000_000.0
+RMS_EPS = 1e-6
+
+
+@dataclasses.dataclass
+class BackboneConfig:
+    hidden: int = 4096
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 12288
+    n_layers: int = 36
+    vocab: int = 151936
+    group_size: int = 128
+    act_order: bool = True
+    rope_theta: float = ROPE_THETA
+    eps: float = RMS_EPS
+    max_seq: int = 2048
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def validate(self) -> None:
+        if self.head_dim != 128:
+            raise ValueError("head_dim must be 128")
+        if self.n_heads % self.n_kv_heads:
+            raise ValueError("n_heads must be a multiple of n_kv_heads")
+        if self.n_heads * self.head_dim != self.hidden:
+            raise ValueError("hidden must equal n_heads * head_dim")
+        if self.intermediate % 64 or self.hidden % self.group_size or \
+                self.intermediate % self.group_size:
+            raise ValueError("intermediate must be a multiple of 64 and of the group size")
+
+
+def rope_tables(n: int, head_dim: int, theta: float, device, dtype=torch.bfloat16):
+    """cos/sin ``[n, head_dim]``: the reference's fp32 chain (model.py:115-124)."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    pos = torch.arange(n, dtype=torch.float32)
+    freqs = torch.outer(pos, inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype).to(device), emb.sin().to(dtype).to(device)
+
+
+class Int4Backbone:
+    """Weights, caches and tables of the decoder on one device."""
+
+    def __init__(self, cfg: BackboneConfig, weights: dict, device="cuda"):
+        cfg.validate()
+        self.cfg = cfg
+        self.device = torch.device(device)
+        dev = self.device
+
+        def T(t):
+            return t.to(device=dev, dtype=torch.bfloat16).contiguous()
+
+        self.embed_tokens = T(weights["embed_tokens"])
+        self.final_norm = T(weights["final_norm"])
+        self.head = T(weights["head"])
+        self.layers = []
+        for lw in weights["layers"]:
+            lyr = {k: T(lw[k]) for k in ("input_layernorm", "post_attention_layernorm",
+                                         "q_norm", "k_norm")}
+            for k in ("qkv", "o", "gate_up", "down"):
+                lin = lw[k]
+                if not isinstance(lin, GPTQLinear):
+                    raise TypeError(f"layer weight {k} must be a GPTQLinear")
+                lin.post_init()
+                lin.drop_original()
+                lyr[k] = lin
+            self.layers.append(lyr)
+        self.rope_cos, self.rope_sin = rope_tables(cfg.max_seq, cfg.head_dim, cfg.rope_theta, dev)
+        self.k_cache = torch.zeros(cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, cfg.head_dim,
+                                   dtype=torch.bfloat16, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+
+    def reset_cache(self) -> None:
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+
+def _random_gptq(gen, dev, k: int, n: int, g: int, perm: torch.Tensor | None) -> GPTQLinear:
+    """A GPTQ linear with the benchmark distributions: nibbles uniform 0..15, scales
+    U(0.002, 0.02), zero nibbles uniform 6..9, act-order g_idx from ``perm``."""
+    qweight = torch.randint(-2**31, 2**31 - 1, (k // 8, n), dtype=torch.int32, device=dev,
+                            generator=gen)
+    scales = (torch.rand(k // g, n, device=dev, generator=gen) * 0.018 + 0.002).half()
+    z = torch.randint(6, 10, (k // g, n), dtype=torch.int64, device=dev, generator=gen)
+    z = z.reshape(k // g, n // 8, 8)
+    zw = torch.zeros(k // g, n // 8, dtype=torch.int64, device=dev)
+    for j in range(8):
+        zw |= z[..., j] << (4 * j)
+    qzeros = ((zw + 2**31) % 2**32 - 2**31).to(torch.int32)
+    g_idx = None
+    if perm is not None:
+        g_idx = torch.empty(k, dtype=torch.int32, device=dev)
+        g_idx[perm] = (torch.arange(k, device=dev) // g).to(torch.int32)
+    return GPTQLinear.from_buffers(qweight, qzeros, scales, g_idx, g)
+
+
+def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda") -> dict:
+    """Random-init weights of the configured shape, generated on the device."""
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    h, g = cfg.hidden, cfg.group_size
+
+    def normal(*shape, std):
+        return (torch.randn(*shape, device=dev, generator=gen) * std).bfloat16()
+
+    def norm_w(n):
+        return (1.0 + torch.randn(n, device=dev, generator=gen) * 0.05).bfloat16()
+
+    def perm(k):
+        return torch.randperm(k, device=dev, generator=gen) if cfg.act_order else None
+
+    layers = []
+    for _ in range(cfg.n_layers):
+        layers.append({
+            "input_layernorm": norm_w(h), "post_attention_layernorm": norm_w(h),
+            "q_norm": norm_w(cfg.head_dim), "k_norm": norm_w(cfg.head_dim),
+            "qkv": _random_gptq(gen, dev, h, cfg.qkv_out, g, perm(h)),
+            "o": _random_gptq(gen, dev, h, h, g, perm(h)),
+            "gate_up": _random_gptq(gen, dev, h, 2 * cfg.intermediate, g, perm(h)),
+            "down": _random_gptq(gen, dev, cfg.intermediate, h, g, perm(cfg.intermediate)),
+        })
+    return {"embed_tokens": normal(cfg.vocab, h, std=1.0), "final_norm": norm_w(h),
+            "head": normal(cfg.vocab, h, std=0.02), "layers": layers}
+
+
+def attention_scale(cfg: BackboneConfig) -> float:
+    return 1.0 / math.sqrt(cfg.head_dim)

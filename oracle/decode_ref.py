@@ -1,0 +1,113 @@
+"""One batch-1 decode step of the Qwen3-shaped backbone on the CPU (oracle; test
+infrastructure only).
+
+Restates moss_tts_lite/model.py:34-44 (RMSNorm, rotate_half), 115-124 (RoPE tables),
+163-197 (the layer) and fast.py:123-194 (the step pieces) in numpy.  Every bf16
+tensor op of the reference computes in fp32 and rounds to bf16; the oracle does the
+same at the same points.  Linear layers and attention accumulate in float64 (the
+exact result the fp32 kernels approximate), then round.
+
+Pinning: ``rms_norm`` against torch's own bf16 chain and closed-form properties;
+``rope_tables`` against float64 trigonometry (<= 1 bf16 ulp); ``attention`` against a
+float64 brute-force softmax and torch's CPU SDPA; see tests/test_oracle_decode.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import round_bf16
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Qwen3RMSNorm on bf16 values (model.py:34-40): fp32 mean of squares, then
+    ``bf16(w * bf16(x * rsqrt(mean + eps)))``; reduces over the last axis."""
+    x = np.asarray(x, np.float32)
+    var = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    return round_bf16(np.asarray(w, np.float32) * round_bf16(x * r))
+
+
+def rotate_half(x: np.ndarray) -> np.ndarray:
+    """``cat(-x2, x1)`` over the last axis (model.py:42-44)."""
+    h = x.shape[-1] // 2
+    return np.concatenate([-x[..., h:], x[..., :h]], axis=-1)
+
+
+def rope_tables(n: int, head_dim: int, theta: float = 1e6):
+    """cos/sin ``[n, head_dim]`` as bf16 values (model.py:115-124): the fp32 chain
+    ``inv = 1/theta**(2i/d)``, ``freqs = pos*inv`` duplicated, cos/sin, rounded to bf16."""
+    i = np.arange(0, head_dim, 2, dtype=np.float32)
+    inv = (np.float32(1.0) / np.power(np.float32(theta), i / np.float32(head_dim))).astype(np.float32)
+    freqs = np.outer(np.arange(n, dtype=np.float32), inv).astype(np.float32)
+    emb = np.concatenate([freqs, freqs], axis=-1)
+    return round_bf16(np.cos(emb.astype(np.float64)).astype(np.float32)), \
+        round_bf16(np.sin(emb.astype(np.float64)).astype(np.float32))
+
+
+def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """``x*cos + rotate_half(x)*sin`` with each bf16 op rounded (fast.py:141-144)."""
+    return round_bf16(round_bf16(x * cos) + round_bf16(rotate_half(x) * sin))
+
+
+def linear(x: np.ndarray, w_kn: np.ndarray) -> np.ndarray:
+    """bf16 output of ``x @ W`` accumulated exactly enough (float64)."""
+    return round_bf16((np.asarray(x, np.float64) @ np.asarray(w_kn, np.float64)).astype(np.float32))
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """GQA decode attention: q ``[H, D]``, k/v ``[Hkv, L, D]`` -> bf16 ``[H, D]``."""
+    h, d = q.shape
+    hkv = k.shape[0]
+    rep = h // hkv
+    out = np.empty((h, d), np.float64)
+    for i in range(h):
+        kk = k[i // rep].astype(np.float64)
+        s = kk @ q[i].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        out[i] = (p / p.sum()) @ v[i // rep].astype(np.float64)
+    return round_bf16(out.astype(np.float32))
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """``F.silu(g) * u`` on bf16 tensors (fast.py:170-171)."""
+    g = np.asarray(g, np.float32)
+    sg = round_bf16((g / (np.float32(1.0) + np.exp(-g.astype(np.float64)).astype(np.float32))))
+    return round_bf16(sg * np.asarray(u, np.float32))
+
+
+def decoder_layer(h: np.ndarray, lw: dict, k_cache: np.ndarray, v_cache: np.ndarray, pos: int,
+                  cos: np.ndarray, sin: np.ndarray, n_heads: int, n_kv: int, head_dim: int,
+                  eps: float = 1e-6):
+    """One layer at decode position ``pos`` (model.py:163-197); updates the caches in place.
+
+    ``lw`` holds float32 weights: norms (bf16 values), ``q, k, v, o, gate, up, down`` as
+    ``[K, N]`` matrices.  Returns the new residual stream (bf16 values, ``[hidden]``).
+    """
+    x = rms_norm(h, lw["input_layernorm"], eps)
+    q = linear(x, lw["q"]).reshape(n_heads, head_dim)
+    k = linear(x, lw["k"]).reshape(n_kv, head_dim)
+    v = linear(x, lw["v"]).reshape(n_kv, head_dim)
+    q = rms_norm(q, lw["q_norm"], eps)
+    k = rms_norm(k, lw["k_norm"], eps)
+    q = apply_rope(q, cos[pos], sin[pos])
+    k = apply_rope(k, cos[pos], sin[pos])
+    k_cache[:, pos] = k
+    v_cache[:, pos] = v
+    a = attention(q, k_cache[:, :pos + 1], v_cache[:, :pos + 1], 1.0 / np.sqrt(head_dim))
+    h = round_bf16(h + linear(a.reshape(-1), lw["o"]))
+    x = rms_norm(h, lw["post_attention_layernorm"], eps)
+    act = silu_mul(linear(x, lw["gate"]), linear(x, lw["up"]))
+    return round_bf16(h + linear(act, lw["down"]))
+
+
+def decode_step(token: int, pos: int, weights: dict, k_cache, v_cache, cos, sin, n_heads: int,
+                n_kv: int, head_dim: int, eps: float = 1e-6):
+    """Whole step (fast.py:123-194 with a single text head): returns
+    ``(logits bf16 [vocab], final hidden, greedy token)``."""
+    h = np.asarray(weights["embed_tokens"][token], np.float32)
+    for li, lw in enumerate(weights["layers"]):
+        h = decoder_layer(h, lw, k_cache[li], v_cache[li], pos, cos, sin, n_heads, n_kv,
+                          head_dim, eps)
+    hf = rms_norm(h, weights["final_norm"], eps)
+    logits = round_bf16((np.asarray(weights["head"], np.float64) @ hf.astype(np.float64)).astype(np.float32))
+    return logits, hf, int(np.argmax(logits))

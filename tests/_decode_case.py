@@ -1,0 +1,81 @@
+"""Builds one decode-step case twice from the same seeded numpy buffers: the device
+``Int4Backbone`` (AutoGPTQ buffers, act-order) and the oracle's float weights."""
+import numpy as np
+import torch
+
+from moss_tts_lite_amd.gptq import GPTQLinear
+from moss_tts_lite_amd.model import BackboneConfig, Int4Backbone
+from oracle import gptq_ref as G
+from oracle import synth
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+
+
+def small_config(**kw) -> BackboneConfig:
+    base = dict(hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=1024,
+                n_layers=2, vocab=1000, group_size=128, act_order=True, max_seq=96)
+    base.update(kw)
+    return BackboneConfig(**base)
+
+
+def _bf16_bits(r, shape, std=1.0, mean=0.0):
+    return f32_to_bf16_bits((mean + std * r.standard_normal(size=shape)).astype(np.float32))
+
+
+def _gptq_np(r, k, n, g, act_order):
+    qweight = synth.random_qweight(r, k, n)
+    scales = synth.random_scales(r, k // g, n)
+    qzeros = synth.random_qzeros(r, k // g, n)
+    g_idx = G.actorder_g_idx(r.permutation(k), g) if act_order else G.trivial_g_idx(k, g)
+    return dict(qweight=qweight, qzeros=qzeros, scales=scales, g_idx=g_idx)
+
+
+def _to_linear(d, g, dev):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    return GPTQLinear.from_buffers(t(d["qweight"]), t(d["qzeros"]),
+                                   t(d["scales"].view(np.float16)), t(d["g_idx"]), g)
+
+
+def _dequant(d, g):
+    return G.gptq_dequant(d["qweight"], d["qzeros"], d["scales"], d["g_idx"], g)
+
+
+def gate_up_columns(inter: int):
+    """Fused column index of gate[j] and up[j] in the 32-column interleave."""
+    j = np.arange(inter)
+    gate = (j // 32) * 64 + j % 32
+    return gate, gate + 32
+
+
+def build_case(cfg: BackboneConfig, seed: int, dev):
+    r = synth.rng(seed)
+    h, g, hd = cfg.hidden, cfg.group_size, cfg.head_dim
+    np_layers, dev_layers = [], []
+    for _ in range(cfg.n_layers):
+        norms = {k: _bf16_bits(r, n, std=0.05, mean=1.0) for k, n in
+                 (("input_layernorm", h), ("post_attention_layernorm", h), ("q_norm", hd),
+                  ("k_norm", hd))}
+        lin = {"qkv": _gptq_np(r, h, cfg.qkv_out, g, cfg.act_order),
+               "o": _gptq_np(r, h, h, g, cfg.act_order),
+               "gate_up": _gptq_np(r, h, 2 * cfg.intermediate, g, cfg.act_order),
+               "down": _gptq_np(r, cfg.intermediate, h, g, cfg.act_order)}
+        w_qkv = _dequant(lin["qkv"], g)
+        qn, kn = cfg.n_heads * hd, cfg.n_kv_heads * hd
+        w_gu = _dequant(lin["gate_up"], g)
+        gcol, ucol = gate_up_columns(cfg.intermediate)
+        lw = {k: bf16_bits_to_f32(v) for k, v in norms.items()}
+        lw.update(q=w_qkv[:, :qn], k=w_qkv[:, qn:qn + kn], v=w_qkv[:, qn + kn:],
+                  o=_dequant(lin["o"], g), gate=w_gu[:, gcol], up=w_gu[:, ucol],
+                  down=_dequant(lin["down"], g))
+        np_layers.append(lw)
+        dl = {k: torch.from_numpy(v.view(np.int16)).view(torch.bfloat16) for k, v in norms.items()}
+        dl.update({k: _to_linear(v, g, dev) for k, v in lin.items()})
+        dev_layers.append(dl)
+    emb = _bf16_bits(r, (cfg.vocab, h), std=1.0)
+    head = _bf16_bits(r, (cfg.vocab, h), std=0.02)
+    fnorm = _bf16_bits(r, h, std=0.05, mean=1.0)
+    t16 = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    model = Int4Backbone(cfg, {"embed_tokens": t16(emb), "final_norm": t16(fnorm),
+                               "head": t16(head), "layers": dev_layers}, dev)
+    oracle_w = {"embed_tokens": bf16_bits_to_f32(emb), "final_norm": bf16_bits_to_f32(fnorm),
+                "head": bf16_bits_to_f32(head), "layers": np_layers}
+    return model, oracle_w

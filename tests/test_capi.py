@@ -19,6 +19,12 @@ def test_every_header_symbol_is_exported(lib):
     assert not missing, missing
 
 
+def test_every_header_symbol_has_a_signature():
+    # ctypes without argtypes would pass Python ints as 32-bit C ints (truncated pointers)
+    missing = [n for n in N.header_symbols() if n not in N._SIGNATURES]
+    assert not missing, missing
+
+
 def test_every_bound_symbol_is_declared():
     declared = set(N.header_symbols())
     undeclared = [n for n in N._SIGNATURES if n not in declared and not n.startswith("mtl_tune_")]
@@ -83,6 +89,23 @@ def test_fused_epilogue_validation(lib):
     st = lib.mtl_w4_gemm_fused(FAKE, 1, 4096, FAKE, N.META_QSZ, FAKE, None, FAKE, 4096, 128, 0,
                                N.EPI_NONE, None, FAKE, 0, None, 0, None)
     assert st == N.MTL_ERR_INVALID_ARG  # act-order gather is a GPTQ-meta feature
+
+
+def test_decode_entry_validation(lib):
+    import ctypes as C
+    eps = C.c_float(1e-6)
+    assert lib.mtl_rmsnorm(FAKE, FAKE, FAKE, 1, 4100, eps, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_rmsnorm(None, FAKE, FAKE, 1, 4096, eps, None) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_qk_norm_rope_kv(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 64,
+                                   64, eps, None) == N.MTL_ERR_UNSUPPORTED
+    assert lib.mtl_qk_norm_rope_kv(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 6, 128,
+                                   64, eps, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_decode_attention_workspace_bytes(32, 128) == 32 * 16 * 132 * 4
+    assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 2048, C.c_float(0.1),
+                                    None, 0, None) == N.MTL_ERR_WORKSPACE
+    assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
+                                    None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG
 
 
 def test_converter_validation(lib):

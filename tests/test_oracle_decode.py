@@ -1,0 +1,100 @@
+"""Pins the oracle's decode-step math (CPU): RMSNorm, RoPE, attention, SiLU*up.
+
+Checks come from independent implementations (torch's CPU ops), float64 closed forms
+and exact invariants, so a dropped term, a wrong sign or a transposed operand fails.
+"""
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle import decode_ref as D
+from oracle.bf16 import round_bf16
+
+
+def _bf(r, shape, std=1.0):
+    return round_bf16((r.standard_normal(shape) * std).astype(np.float32))
+
+
+def test_rms_norm_matches_torch_bf16_chain_within_one_ulp():
+    r = np.random.default_rng(0)
+    x = _bf(r, (16, 4096), 3.0)
+    w = round_bf16((1 + 0.1 * r.standard_normal(4096)).astype(np.float32))
+    ours = D.rms_norm(x, w)
+    tx, tw = torch.from_numpy(x).bfloat16(), torch.from_numpy(w).bfloat16()
+    xf = tx.float()
+    ref = (tw * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).bfloat16()).float().numpy()
+    ulp = np.abs(ref) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(ours - ref) <= ulp)
+    # and against torch's fused rms_norm (no intermediate rounding): close, not equal
+    fused = F.rms_norm(xf, (4096,), tw.float(), 1e-6).numpy()
+    assert np.abs(ours - fused).max() <= 2 * (np.abs(fused).max() * 2.0 ** -8)
+
+
+def test_rms_norm_invariants():
+    r = np.random.default_rng(1)
+    x = _bf(r, (4, 256))
+    w = np.ones(256, np.float32)
+    # exact scale invariance for power-of-two scaling
+    assert np.array_equal(D.rms_norm(x, w), D.rms_norm(x * np.float32(8.0), w))
+    # a constant vector normalises to +-1 (up to eps)
+    c = np.full((1, 128), 0.5, np.float32)
+    assert np.allclose(D.rms_norm(c, np.ones(128, np.float32)), 1.0, atol=2 ** -7)
+
+
+def test_rope_tables_match_float64_trig():
+    cos, sin = D.rope_tables(2048, 128, 1e6)
+    i = np.arange(0, 128, 2, dtype=np.float64)
+    inv = 1.0 / (1e6 ** (i / 128))
+    ang = np.outer(np.arange(2048, dtype=np.float64), np.concatenate([inv, inv]))
+    # within one bf16 ulp of the exact values (the fp32 argument rounding moves them)
+    assert np.all(np.abs(cos - np.cos(ang)) <= 2.0 ** -8 + 1e-3 * (ang / 2048))
+    assert np.all(np.abs(sin - np.sin(ang)) <= 2.0 ** -8 + 1e-3 * (ang / 2048))
+    # position 0: cos = 1, sin = 0 exactly; the two halves are duplicated
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    assert np.array_equal(cos[:, :64], cos[:, 64:])
+
+
+def test_rope_rotation_properties():
+    r = np.random.default_rng(2)
+    x = _bf(r, (8, 128))
+    cos, sin = D.rope_tables(100, 128)
+    assert np.array_equal(D.apply_rope(x, cos[0], sin[0]), x)   # identity at position 0
+    y = D.apply_rope(x, cos[57], sin[57])
+    # each (i, i+64) pair is rotated: pair norms preserved up to bf16 rounding
+    n0 = x[:, :64] ** 2 + x[:, 64:] ** 2
+    n1 = y[:, :64] ** 2 + y[:, 64:] ** 2
+    assert np.allclose(n1, n0, rtol=3e-2, atol=1e-3)
+    # sign convention: rotate_half(x) = cat(-x2, x1)
+    assert np.array_equal(D.rotate_half(np.arange(4.0)), np.array([-2.0, -3.0, 0.0, 1.0]))
+
+
+def test_attention_matches_torch_sdpa():
+    r = np.random.default_rng(3)
+    q = _bf(r, (8, 128))
+    k = _bf(r, (2, 37, 128))
+    v = _bf(r, (2, 37, 128))
+    ours = D.attention(q, k, v, 1 / np.sqrt(128))
+    tq = torch.from_numpy(q).double().view(1, 8, 1, 128)
+    tk = torch.from_numpy(k).double().repeat_interleave(4, 0).view(1, 8, 37, 128)
+    tv = torch.from_numpy(v).double().repeat_interleave(4, 0).view(1, 8, 37, 128)
+    ref = F.scaled_dot_product_attention(tq, tk, tv).view(8, 128).float().numpy()
+    assert np.all(np.abs(ours - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+
+
+def test_attention_special_cases():
+    v = np.arange(3 * 128, dtype=np.float32).reshape(1, 3, 128) / 64
+    k = np.zeros((1, 3, 128), np.float32)
+    q = np.ones((1, 128), np.float32)
+    # equal scores -> plain mean of the values
+    assert np.allclose(D.attention(q, k, v, 1.0), round_bf16(v.mean(1)))
+    # one position -> that value row
+    assert np.array_equal(D.attention(q, k[:, :1], v[:, :1], 1.0), round_bf16(v[:, 0]))
+
+
+def test_silu_mul_matches_torch():
+    r = np.random.default_rng(4)
+    g, u = _bf(r, 4096, 3.0), _bf(r, 4096)
+    tg, tu = torch.from_numpy(g).bfloat16(), torch.from_numpy(u).bfloat16()
+    ref = (F.silu(tg) * tu).float().numpy()
+    ours = D.silu_mul(g, u)
+    assert np.all(np.abs(ours - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
