@@ -186,8 +186,6 @@ def cpu_baseline_gemv(budget_s: float = 12.0):
 def bench_decode(args, torch):
     import numpy as np
 
-    from moss_tts_lite_amd import _native as N
-    from moss_tts_lite_amd import ops
     from moss_tts_lite_amd.fast import FastDecoder
     from moss_tts_lite_amd.model import BackboneConfig, Int4Backbone, random_weights
 
@@ -221,34 +219,33 @@ def bench_decode(args, torch):
     del toks
     final_pos = int(dec.pos.item())
 
-    # Dominant kernel, live: the gate_up int4 GEMV of the model's own 36 layers (1.9 GB of
-    # distinct weights, so no Infinity-Cache reuse), event pairs on the launch stream,
-    # queued behind a GPU spin so host launch overhead never shows.
-    lib = N.load()
-    x = dec.x
+    # Dominant kernel, live: each int4 GEMV launch of the step exactly as the captured plan
+    # issues it, over the model's own 36 layers (1.9 GB of distinct gate_up weights, so no
+    # Infinity-Cache reuse), event pairs on the launch stream, queued behind a GPU spin so
+    # host launch overhead never shows.
     reps = 4 * cfg.n_layers
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(reps)]
-    torch.cuda.synchronize()
-    torch.cuda._sleep(int(2e8))
-    for i, (a, b) in enumerate(evs):
-        lin = model.layers[i % cfg.n_layers]["gate_up"]
-        qw, qz, sc, perm = lin.kernel_args()
-        a.record()
-        ops.w4_gemm(x.view(1, -1), qw, N.META_GPTQ, sc, qz, perm, 2 * cfg.intermediate,
-                    cfg.group_size, epilogue=N.EPI_SILU_MUL, out=dec.act.view(1, -1))
-        b.record()
-    torch.cuda.synchronize()
-    us = [a.elapsed_time(b) * 1e3 for a, b in evs]
-    gu_us = sum(us) / len(us)
-    gu_bytes = algo_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size, True)
+    gemv_us = {}
+    for name in ("gate_up", "down", "qkv", "o"):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(2e8))
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            dec.run_gemv(i % cfg.n_layers, name)
+            b.record()
+        torch.cuda.synchronize()
+        us = [a.elapsed_time(b) * 1e3 for a, b in evs]
+        gemv_us[name] = sum(us) / len(us)
+    gu_us = gemv_us["gate_up"]
+    gu_bytes = algo_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size, False)
     layer_bytes = sum(algo_bytes(1, k, n, cfg.group_size, True) for k, n in
                       ((cfg.hidden, cfg.qkv_out), (cfg.hidden, cfg.hidden),
                        (cfg.hidden, 2 * cfg.intermediate), (cfg.intermediate, cfg.hidden)))
     avg_len = (prompt_len + args.warmup + 1 + final_pos) / 2
     kv_bytes = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim * 2 * avg_len
     step_bytes = cfg.n_layers * layer_bytes + 2 * cfg.vocab * cfg.hidden + kv_bytes
-    del np, lib
+    del np
     return dict(
         value=round(1000.0 / ms_step, 2), unit="steps/s", ms_per_step=ms_step, steps=args.steps,
         dtype="int4 GPTQ weights, bf16 activations, fp32 accumulate",
@@ -259,11 +256,18 @@ def bench_decode(args, torch):
                 "step_bytes_avg": int(step_bytes),
                 "step_hbm_gbs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
                 "host_enqueue_ms_per_step": round(host_s * 1e3 / args.steps, 4),
-                "setup_s": round(setup_s, 1), "gate_up_us": round(gu_us, 3)},
+                "setup_s": round(setup_s, 1), "plan": dec.plan,
+                "gemv_us": {k: round(v, 3) for k, v in gemv_us.items()},
+                "gemv_gbs": {k: round(algo_bytes(1, kk, nn, cfg.group_size, False) / gemv_us[k]
+                                      / 1e3, 1) for k, kk, nn in
+                             (("gate_up", cfg.hidden, 2 * cfg.intermediate),
+                              ("down", cfg.intermediate, cfg.hidden),
+                              ("qkv", cfg.hidden, cfg.qkv_out), ("o", cfg.hidden, cfg.hidden))}},
         roofline={"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1),
                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
-                  "kernel": "w4_gemm_kernel<1,16,GPTQ,perm> gate_up 4096x24576 M=1 (+SiLU*up)",
+                  "kernel": "w4_gemm_kernel<1,16,GPTQ,rmsnorm-staged> gate_up 4096x24576 M=1 "
+                            "(split-K partials, as launched in the decode step)",
                   "bytes_per_launch": gu_bytes},
     )
 

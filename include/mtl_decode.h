@@ -53,18 +53,43 @@ int mtl_qk_norm_rope_kv(const void* qkv, const void* q_norm_w, const void* k_nor
                         void* stream);
 
 /*
+ * Same, with the projection given as the fp32 split-K partials of the q|k|v GEMV
+ * ([splits, (n_heads + 2*n_kv_heads)*head_dim], from mtl_w4_gemm_partials): each
+ * projection value is bf16(sum over splits, in split order) before the norm.
+ */
+int mtl_qk_norm_rope_kv_partials(const float* partials, int32_t splits, const void* q_norm_w,
+                                 const void* k_norm_w, const void* cos_tab, const void* sin_tab,
+                                 const int64_t* pos, void* q_out, void* k_cache, void* v_cache,
+                                 int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                 int64_t max_seq, float eps, void* stream);
+
+/*
+ * Residual add + RMSNorm of the fused step (moss_tts_lite/fast.py:168-169 then
+ * model.py:34-40).  With partials (fp32 [splits, n] of the o or down GEMV):
+ * h_out = bf16(bf16(sum of partials) + resid) (h_out may alias resid); without:
+ * h = resid.  Then x = RMSNorm(h, w), written as x_out[j] = x[gather[j]] (the act-order
+ * input order of the next int4 GEMV) or x_out = x when gather is NULL.  n % 4 == 0,
+ * n <= 16384.
+ */
+int mtl_residual_rmsnorm(const float* partials, int32_t splits, const void* resid, void* h_out,
+                         const void* w, void* x_out, const int32_t* gather, int64_t n, float eps,
+                         void* stream);
+
+/*
  * GQA decode attention over cache positions [0, pos] (the reference's SDPA call at
  * moss_tts_lite/fast.py:149-162, exact length pos + 1): split over the sequence
  * in chunks, fp32 softmax, chunk partials combined in chunk order.
  *   q    bf16 [n_heads * head_dim];  out bf16 [n_heads * head_dim]
+ *   out_index  NULL, or int32 [n_heads * head_dim]: value i is written to
+ *              out[out_index[i]] (the act-order input order of the o projection)
  *   scale  softmax scale (1/sqrt(head_dim) in the reference)
  * head_dim must be 128; n_heads % n_kv_heads == 0.
  */
 int64_t mtl_decode_attention_workspace_bytes(int32_t n_heads, int32_t head_dim);
 int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
-                         const int64_t* pos, void* out, int32_t n_heads, int32_t n_kv_heads,
-                         int32_t head_dim, int64_t max_seq, float scale, void* workspace,
-                         int64_t ws_bytes, void* stream);
+                         const int64_t* pos, void* out, const int32_t* out_index, int32_t n_heads,
+                         int32_t n_kv_heads, int32_t head_dim, int64_t max_seq, float scale,
+                         void* workspace, int64_t ws_bytes, void* stream);
 
 /*
  * bf16 output head with greedy selection: logits[n] = bf16(sum_k W[n,k] x[k])
@@ -75,6 +100,40 @@ int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache
 int64_t mtl_head_workspace_bytes(int64_t N);
 int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, void* logits,
                          int64_t* token_out, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * Residual add of the norm-staged step (moss_tts_lite/fast.py:168-169): with partials
+ * (fp32 [splits, n] of the o or down GEMV) h = bf16(bf16(sum of partials) + h) in place;
+ * without, h is only read.  slots float[16] receives the sum of squares of h over 16
+ * equal blocks (consumed by mtl_w4_gemm_norm_partials / mtl_bf16_gemv_argmax_norm, which
+ * apply the RMSNorm of model.py:34-40).  h_ord (optional) receives h scattered into the
+ * next int4 GEMV's act-order input order: h_ord[scatter[i]] = h[i] (scatter NULL: copy).
+ * n % 64 == 0.
+ */
+int mtl_residual_add(const float* partials, int32_t splits, void* h, const int32_t* scatter,
+                     void* h_ord, float* slots, int64_t n, void* stream);
+
+/*
+ * mtl_qk_norm_rope_kv_partials and mtl_decode_attention in one pass: q/k RMSNorm,
+ * RoPE and the KV write of position pos are done inside the attention workgroups
+ * from the q|k|v split-K partials (fast.py:134-162).  n_heads / n_kv_heads <= 4.
+ * The q/k/v projections of position pos are not written anywhere except the cache.
+ */
+int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const void* q_norm_w,
+                               const void* k_norm_w, const void* cos_tab, const void* sin_tab,
+                               void* k_cache, void* v_cache, const int64_t* pos, void* out,
+                               const int32_t* out_index, int32_t n_heads, int32_t n_kv_heads,
+                               int32_t head_dim, int64_t max_seq, float scale, float eps,
+                               void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * mtl_bf16_gemv_argmax on x = RMSNorm(h, norm_w) (the final norm, model.py:34-40 and
+ * fast.py:179-180), with h's block sums of squares in slots[16] (mtl_residual_add).
+ */
+int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
+                              const void* w, int64_t N, int64_t K, void* logits,
+                              int64_t* token_out, void* workspace, int64_t ws_bytes,
+                              void* stream);
 
 /* pos[0] += 1 on the device (ends a captured decode step). */
 int mtl_advance_position(int64_t* pos, void* stream);

@@ -150,6 +150,35 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
                       void* y, int32_t out_dtype, void* workspace, int64_t ws_bytes,
                       void* stream);
 
+/*
+ * Partials-only launch for fused consumers (the decode step): writes the fp32
+ * split-K partial tiles partials[splits, M, N] (splits = mtl_w4_gemm_splits(K, N))
+ * and nothing else; the consumer sums them in split order.  The activation comes
+ * from x (bf16 [M, K], through perm when given) or, when xpart is set (M = 1),
+ * from the fp32 partials of an interleaved gate|up GEMV ([xsplits, 2K], 32-column
+ * gate|up blocks): x[j] = bf16(silu(bf16 gate_j) * bf16 up_j) (fast.py:170-171).
+ * AutoGPTQ meta only.
+ */
+int32_t mtl_w4_gemm_splits(int64_t K, int64_t N);
+int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
+                         int64_t M, int64_t K, const int32_t* qweight, const void* scales,
+                         const int32_t* qzeros, const int32_t* perm, int64_t N, int32_t group_size,
+                         int32_t zero_offset, float* partials, int64_t partials_bytes,
+                         void* stream);
+
+/*
+ * Partials-only launch (M = 1) whose activation is RMSNorm(h) computed while staging
+ * (moss_tts_lite/model.py:34-40): x[j] = bf16(w[j] * bf16(h[j] * r)),
+ * r = rsqrt(sum(slots[0..15]) / K + eps).  h and w are bf16 [K], already in this
+ * GEMV's act-order input order (w is the norm weight gathered by the same perm);
+ * slots float[16] are the block sums of squares from mtl_residual_add.
+ */
+int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
+                              int64_t K, const int32_t* qweight, const void* scales,
+                              const int32_t* qzeros, int64_t N, int32_t group_size,
+                              int32_t zero_offset, float* partials, int64_t partials_bytes,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,13 +47,35 @@ _SIGNATURES = {
                                    _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64,
                                    ctypes.c_float, _c_void_p]),
     "mtl_decode_attention_workspace_bytes": (_i64, [_i32, _i32]),
-    "mtl_decode_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32,
-                                    _i32, _i64, ctypes.c_float, _c_void_p, _i64, _c_void_p]),
+    "mtl_decode_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                    _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p, _i64,
+                                    _c_void_p]),
+    "mtl_qk_norm_rope_kv_partials": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                            _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p]),
+    "mtl_residual_rmsnorm": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                    _c_void_p, _i64, ctypes.c_float, _c_void_p]),
     "mtl_head_workspace_bytes": (_i64, [_i64]),
     "mtl_bf16_gemv_argmax": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                                     _c_void_p, _i64, _c_void_p]),
     "mtl_advance_position": (_i32, [_c_void_p, _c_void_p]),
+    "mtl_residual_add": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                _c_void_p]),
+    "mtl_decode_attention_fused": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p,
+                                          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                          _c_void_p, _i32, _i32, _i32, _i64, ctypes.c_float,
+                                          ctypes.c_float, _c_void_p, _i64, _c_void_p]),
+    "mtl_bf16_gemv_argmax_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
+                                         _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                         _i64, _c_void_p]),
     # tuning knobs (not part of the headers)
+    "mtl_w4_gemm_splits": (_i32, [_i64, _i64]),
+    "mtl_w4_gemm_partials": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _c_void_p,
+                                    _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _c_void_p,
+                                    _i64, _c_void_p]),
+    "mtl_w4_gemm_norm_partials": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
+                                         _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32,
+                                         _c_void_p, _i64, _c_void_p]),
     "mtl_tune_set_waves": (_i32, [_i32]),
     "mtl_tune_set_reduce": (_i32, [_i32]),
 }

@@ -43,11 +43,18 @@ struct W4Args {
   const uint16_t* meta0;    // GPTQ: fp16 scales [G, N]; QSZ: bf16 qsz [G, N, 2]
   const uint32_t* qzeros;   // GPTQ: [G, N/8]
   const int32_t* perm;      // optional act-order gather index [K]
+  const float* xpart;       // XSRC_SILU_PART: gate|up partials [xsplits, M, xpart_ld]
+  int xsplits, xpart_ld;
+  const uint16_t* hn;       // XSRC_RMSNORM: residual stream h [K] (act-order order)
+  const uint16_t* wn;       //               norm weight [K] (same order)
+  const float* slots;       //               per-block sums of squares of h [nslots]
+  float eps;
   const uint16_t* resid;    // RESIDUAL epilogue input [M, N]
   void* y;
   float* partial;           // [splits, M, N]
   unsigned* counters;       // [col_tiles], zero between launches
   int inkernel_reduce;      // 1: last workgroup reduces; 0: w4_reduce_kernel does
+  int partials_only;        // 1: always publish [splits, M, N] partials, no epilogue
   int M, K, N, group, zero_offset, splits, epilogue, out_f32;
 };
 
@@ -63,8 +70,29 @@ __device__ __forceinline__ float4 ld_f4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-template <int MR, int RPG, int FMT, bool PERM>
+// bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
+__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
+  g = round_bf16(g);
+  const float sg = round_bf16(g / (1.0f + expf(-g)));
+  return f32_to_bf16(sg * round_bf16(u));
+}
+
+// Where the kernel reads its activation row from.
+enum : int {
+  XSRC_BF16 = 0,      // x bf16 [M, K]
+  XSRC_PERM = 1,      // x bf16 [M, K] read through the act-order index: x[:, perm[k]]
+  XSRC_SILU_PART = 2, // x = SiLU(gate) * up from the fp32 split-K partials of an
+                      // interleaved gate|up GEMV (the down projection's input)
+  XSRC_RMSNORM = 3    // x = bf16(w * bf16(h * r)): RMSNorm applied while staging, from the
+                      // residual stream h and norm weight w (both already in the weight's
+                      // act-order input order) and r = rsqrt(sum(slots)/K + eps)
+};
+
+constexpr int kNormSlots = 16;   // sums of squares published by the residual kernel
+
+template <int MR, int RPG, int FMT, int XSRC>
 __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
+  constexpr bool PERM = XSRC == XSRC_PERM || XSRC == XSRC_SILU_PART;   // x staged after weights
   constexpr int RB = kRowsPerWave;
   constexpr int NCH = RB / RPG;            // metadata chunks per wave
   constexpr int XIT = (MR * RB + 63) / 64; // x staging items per lane
@@ -93,6 +121,9 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   //    staging waits only on them; with act-order the gather needs the index first, so
   //    it is issued after the weight stream and overlaps it instead.
   u32x4 xv[XIT];
+  bool xok[XIT];
+  u32x4 wv[XSRC == XSRC_RMSNORM ? XIT : 1];
+  float4 slot4[XSRC == XSRC_RMSNORM ? kNormSlots / 4 : 1];
   auto load_x = [&]() {
 #pragma unroll
     for (int it = 0; it < XIT; ++it) {
@@ -103,7 +134,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
       const size_t xoff = (size_t)(m < M ? m : M - 1) * a.K;
       const int rc = row < rows_total ? row : rows_last;
       u32x4 v;
-      if (PERM) {
+      if (XSRC == XSRC_PERM) {
         const u32x4 p0 = *reinterpret_cast<const u32x4*>(a.perm + rc * 8);
         const u32x4 p1 = *reinterpret_cast<const u32x4*>(a.perm + rc * 8 + 4);
         const uint32_t e0 = a.x[xoff + p0.x], e1 = a.x[xoff + p0.y];
@@ -111,13 +142,52 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
         const uint32_t e4 = a.x[xoff + p1.x], e5 = a.x[xoff + p1.y];
         const uint32_t e6 = a.x[xoff + p1.z], e7 = a.x[xoff + p1.w];
         v = u32x4{e0 | (e1 << 16), e2 | (e3 << 16), e4 | (e5 << 16), e6 | (e7 << 16)};
+      } else if (XSRC == XSRC_SILU_PART) {
+        // channels 8rc..8rc+7 of the intermediate; their gate columns are contiguous in
+        // the 32-column interleave and the up columns sit 32 to the right.
+        const int j0 = rc * 8;
+        const float* pb = a.xpart + (size_t)(m < M ? m : M - 1) * a.xpart_ld +
+                          64 * (j0 >> 5) + (j0 & 31);
+        const size_t ss = (size_t)M * a.xpart_ld;
+        float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < a.xsplits; s0 += 8) {   // 32 loads in flight, summed in order
+          float4 G[8][2], U[8][2];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int sp = s0 + j < a.xsplits ? s0 + j : a.xsplits - 1;
+            const float* q = pb + sp * ss;
+            G[j][0] = ld_f4(q); G[j][1] = ld_f4(q + 4);
+            U[j][0] = ld_f4(q + 32); U[j][1] = ld_f4(q + 36);
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (s0 + j < a.xsplits) {
+              g[0] += G[j][0].x; g[1] += G[j][0].y; g[2] += G[j][0].z; g[3] += G[j][0].w;
+              g[4] += G[j][1].x; g[5] += G[j][1].y; g[6] += G[j][1].z; g[7] += G[j][1].w;
+              u[0] += U[j][0].x; u[1] += U[j][0].y; u[2] += U[j][0].z; u[3] += U[j][0].w;
+              u[4] += U[j][1].x; u[5] += U[j][1].y; u[6] += U[j][1].z; u[7] += U[j][1].w;
+            }
+        }
+        v = u32x4{silu_mul_bf16(g[0], u[0]) | (silu_mul_bf16(g[1], u[1]) << 16),
+                  silu_mul_bf16(g[2], u[2]) | (silu_mul_bf16(g[3], u[3]) << 16),
+                  silu_mul_bf16(g[4], u[4]) | (silu_mul_bf16(g[5], u[5]) << 16),
+                  silu_mul_bf16(g[6], u[6]) | (silu_mul_bf16(g[7], u[7]) << 16)};
+      } else if (XSRC == XSRC_RMSNORM) {   // raw h now, normalised once the scale is known
+        v = *reinterpret_cast<const u32x4*>(a.hn + rc * 8);
+        wv[it] = *reinterpret_cast<const u32x4*>(a.wn + rc * 8);
       } else {
         v = *reinterpret_cast<const u32x4*>(a.x + xoff + rc * 8);
       }
-      xv[it] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+      xv[it] = v;     // masked after the weight stream is issued (step 4)
+      xok[it] = ok;
     }
   };
   if (!PERM) load_x();
+  if (XSRC == XSRC_RMSNORM) {
+#pragma unroll
+    for (int i = 0; i < kNormSlots / 4; ++i) slot4[i] = ld_f4(a.slots + 4 * i);
+  }
 
   // 2. Group metadata of the lane's 4 columns, one entry per RPG-row chunk.
   const int colc = col_ok ? col0 : N - 4;
@@ -154,11 +224,34 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. x into LDS in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7) with row sums.
+  float norm_r = 0.f;
+  if (XSRC == XSRC_RMSNORM) {   // RMSNorm scale: rsqrt(mean(h^2) + eps), slots summed in order
+    float ssum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormSlots / 4; ++i)
+      ssum += ((slot4[i].x + slot4[i].y) + (slot4[i].z + slot4[i].w));
+    norm_r = rsqrtf(ssum / (float)a.K + a.eps);
+  }
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int item = lane + 64 * it;
     if (item < MR * RB) {
-      const u32x4 v = xv[it];
+      u32x4 v = xv[it];
+      if (XSRC == XSRC_RMSNORM) {   // x = bf16(w * bf16(h * r)), model.py:34-40
+        const uint32_t hh[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t ww[4] = {wv[it].x, wv[it].y, wv[it].z, wv[it].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t lo = f32_to_bf16(round_bf16(
+              bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * norm_r)));
+          const uint32_t hi = f32_to_bf16(round_bf16(
+              bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * norm_r)));
+          o[c] = lo | (hi << 16);
+        }
+        v = u32x4{o[0], o[1], o[2], o[3]};
+      }
+      if (!xok[it]) v = u32x4{0u, 0u, 0u, 0u};
       const uint32_t e0 = v.x & 0xffffu, e1 = v.x >> 16, e2 = v.y & 0xffffu, e3 = v.y >> 16;
       const uint32_t e4 = v.z & 0xffffu, e5 = v.z >> 16, e6 = v.w & 0xffffu, e7 = v.w >> 16;
       xs[wave][item / RB][item % RB] =
@@ -272,9 +365,9 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   //    XCDs without a whole-L2 writeback), a per-tile counter names the last workgroup,
   //    and that one sums all splits in split order (loads batched 8 deep) and resets
   //    the counter.  Otherwise w4_reduce_kernel (or a fused consumer) sums them.
-  if (a.splits > 1) {
+  if (a.splits > 1 || a.partials_only) {
     float* pbase = a.partial + (size_t)split * M * N + col0;
-    if (!a.inkernel_reduce) {
+    if (!a.inkernel_reduce || a.partials_only) {
       if (col_ok) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
@@ -385,12 +478,6 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
 // Sum the split-K partial tiles in split order and apply the epilogue.  One thread
 // per 4 consecutive output columns of one row (for SILU_MUL: 4 gate columns and their
 // 4 up partners 32 columns to the right).
-__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
-  g = round_bf16(g);
-  const float sg = round_bf16(g / (1.0f + expf(-g)));
-  return f32_to_bf16(sg * round_bf16(u));
-}
-
 __global__ void __launch_bounds__(256) w4_reduce_kernel(W4Args a) {
   const int N = a.N, M = a.M;
   const int S = a.splits;
@@ -492,11 +579,15 @@ static int g_inkernel_reduce = 1;
 template <int MR, int RPG>
 static void launch_fmt(const W4Args& a, int fmt, dim3 grid, dim3 block, hipStream_t s) {
   if (fmt == MTL_META_QSZ)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_QSZ, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_QSZ, XSRC_BF16>), grid, block, 0, s, a);
+  else if (a.xpart)
+    hipLaunchKernelGGL((w4_gemm_kernel<1, RPG, MTL_META_GPTQ, XSRC_SILU_PART>), grid, block, 0, s, a);
+  else if (a.hn)
+    hipLaunchKernelGGL((w4_gemm_kernel<1, RPG, MTL_META_GPTQ, XSRC_RMSNORM>), grid, block, 0, s, a);
   else if (a.perm)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, true>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, XSRC_PERM>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, XSRC_BF16>), grid, block, 0, s, a);
 }
 
 template <int MR>
@@ -546,6 +637,14 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   a.out_f32 = out_dtype == MTL_OUT_F32;
   a.partial = nullptr;
   a.counters = nullptr;
+  a.xpart = nullptr;
+  a.xsplits = 0;
+  a.xpart_ld = 0;
+  a.hn = nullptr;
+  a.wn = nullptr;
+  a.slots = nullptr;
+  a.eps = 0.f;
+  a.partials_only = 0;
   a.inkernel_reduce = g_inkernel_reduce;
   if (p.splits > 1) {
     const int64_t need = kCounterBytes + (int64_t)p.splits * M * N * 4;
@@ -568,6 +667,115 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
     const int quads = (int)(M * (epilogue == MTL_EPI_SILU_MUL ? N / 8 : N / 4));
     hipLaunchKernelGGL(w4_reduce_kernel, dim3((quads + 255) / 256), dim3(256), 0, stream, a);
   }
+  return launch_status();
+}
+
+// Partials-only launch for fused consumers: writes fp32 [splits, M, N] into `partials`
+// (splits = w4_splits(K)); x comes from `x` (bf16, optionally through `perm`) or, when
+// `xpart` is set, from the gate|up partials of the previous GEMV (SiLU*up, M = 1).
+static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
+                            int64_t M, int64_t K, const int32_t* qweight, const void* meta0,
+                            const int32_t* qzeros, const int32_t* perm, int64_t N, int group,
+                            int zero_offset, float* partials, int64_t partials_bytes,
+                            hipStream_t stream) {
+  if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !partials)
+    return MTL_ERR_INVALID_ARG;
+  if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
+  if (M < 1 || M > kMaxM || K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0)
+    return MTL_ERR_SHAPE;
+  if (K * N / 2 >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (xpart) {
+    if (M != 1) return MTL_ERR_UNSUPPORTED;
+    if (perm) return MTL_ERR_INVALID_ARG;
+    if (xsplits < 1 || xpart_ld != 2 * K) return MTL_ERR_SHAPE;
+    if (!aligned16(xpart)) return MTL_ERR_ALIGN;
+  } else if (!aligned16(x)) {
+    return MTL_ERR_ALIGN;
+  }
+  if (!aligned16(qweight) || !aligned16(partials) || (perm && !aligned16(perm)))
+    return MTL_ERR_ALIGN;
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  const Plan p = plan_for(K, N);
+  if (partials_bytes < (int64_t)p.splits * M * N * 4) return MTL_ERR_WORKSPACE;
+  W4Args a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.qweight = reinterpret_cast<const u32x4*>(qweight);
+  a.meta0 = static_cast<const uint16_t*>(meta0);
+  a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
+  a.perm = perm;
+  a.xpart = xpart;
+  a.xsplits = xsplits;
+  a.xpart_ld = (int)xpart_ld;
+  a.hn = nullptr;
+  a.wn = nullptr;
+  a.slots = nullptr;
+  a.eps = 0.f;
+  a.resid = nullptr;
+  a.y = nullptr;
+  a.partial = partials;
+  a.counters = nullptr;
+  a.M = (int)M; a.K = (int)K; a.N = (int)N;
+  a.group = group; a.zero_offset = zero_offset;
+  a.splits = p.splits;
+  a.epilogue = MTL_EPI_NONE;
+  a.out_f32 = 1;
+  a.inkernel_reduce = 0;
+  a.partials_only = 1;
+  const dim3 grid(p.col_tiles, p.splits);
+  const dim3 block(64 * p.waves);
+  const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
+  switch (mr) {
+    case 1: launch_rpg<1>(a, MTL_META_GPTQ, grid, block, stream); break;
+    case 2: launch_rpg<2>(a, MTL_META_GPTQ, grid, block, stream); break;
+    case 4: launch_rpg<4>(a, MTL_META_GPTQ, grid, block, stream); break;
+    case 8: launch_rpg<8>(a, MTL_META_GPTQ, grid, block, stream); break;
+    default: launch_rpg<16>(a, MTL_META_GPTQ, grid, block, stream); break;
+  }
+  return launch_status();
+}
+
+// Partials-only launch whose input is RMSNorm(h) computed while staging (M = 1).
+static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const float* slots,
+                                 float eps, int64_t K, const int32_t* qweight,
+                                 const void* meta0, const int32_t* qzeros, int64_t N, int group,
+                                 int zero_offset, float* partials, int64_t partials_bytes,
+                                 hipStream_t stream) {
+  if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !partials)
+    return MTL_ERR_INVALID_ARG;
+  if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
+  if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  if (!aligned16(slots)) return MTL_ERR_ALIGN;
+  if (K * N / 2 >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
+    return MTL_ERR_ALIGN;
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  const Plan p = plan_for(K, N);
+  if (partials_bytes < (int64_t)p.splits * N * 4) return MTL_ERR_WORKSPACE;
+  W4Args a;
+  a.x = nullptr;
+  a.qweight = reinterpret_cast<const u32x4*>(qweight);
+  a.meta0 = static_cast<const uint16_t*>(meta0);
+  a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
+  a.perm = nullptr;
+  a.xpart = nullptr;
+  a.xsplits = 0;
+  a.xpart_ld = 0;
+  a.hn = static_cast<const uint16_t*>(h_ord);
+  a.wn = static_cast<const uint16_t*>(w_ord);
+  a.slots = slots;
+  a.eps = eps;
+  a.resid = nullptr;
+  a.y = nullptr;
+  a.partial = partials;
+  a.counters = nullptr;
+  a.M = 1; a.K = (int)K; a.N = (int)N;
+  a.group = group; a.zero_offset = zero_offset;
+  a.splits = p.splits;
+  a.epilogue = MTL_EPI_NONE;
+  a.out_f32 = 1;
+  a.inkernel_reduce = 0;
+  a.partials_only = 1;
+  launch_rpg<1>(a, MTL_META_GPTQ, dim3(p.col_tiles, p.splits), dim3(64 * p.waves), stream);
   return launch_status();
 }
 
@@ -615,6 +823,30 @@ int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream) {
   hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
                      static_cast<uint32_t*>(workspace), n, 0u);
   return launch_status();
+}
+
+int32_t mtl_w4_gemm_splits(int64_t K, int64_t N) {
+  if (K <= 0 || N <= 0 || K % 8 != 0) return 0;
+  return plan_for(K, N).splits;
+}
+
+int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
+                         int64_t M, int64_t K, const int32_t* qweight, const void* scales,
+                         const int32_t* qzeros, const int32_t* perm, int64_t N, int32_t group_size,
+                         int32_t zero_offset, float* partials, int64_t partials_bytes,
+                         void* stream) {
+  return w4_gemm_partials(x, xpart, xsplits, xpart_ld, M, K, qweight, scales, qzeros, perm, N,
+                          group_size, zero_offset, partials, partials_bytes, (hipStream_t)stream);
+}
+
+int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
+                              int64_t K, const int32_t* qweight, const void* scales,
+                              const int32_t* qzeros, int64_t N, int32_t group_size,
+                              int32_t zero_offset, float* partials, int64_t partials_bytes,
+                              void* stream) {
+  return w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N,
+                               group_size, zero_offset, partials, partials_bytes,
+                               (hipStream_t)stream);
 }
 
 int mtl_gptq_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight,

@@ -14,6 +14,20 @@ fast_native.py:369-386), and greedy decoding chains steps without a host sync.
 Every launch is a plain C-ABI call on torch's current stream; the launch plan (all
 pointers, sizes, workspaces) is built once, so eager steps and graph capture issue the
 identical kernel sequence.
+
+Three launch plans produce the same step:
+
+* ``"staged"`` (default): each int4 GEMV publishes only its split-K partials and the
+  consumer folds the reduction in.  A 16-workgroup residual add sums the o/down
+  partials into ``h``, publishes 16 block sums of squares and scatters ``h`` into the
+  next GEMV's act-order input order; that GEMV applies RMSNorm while staging its input
+  (norm weight pre-gathered by the same order).  The attention kernel rebuilds q/k/v
+  from the q|k|v partials (q/k norm, RoPE, KV write inside), its combine scatters into
+  the o projection's input order, down stages SiLU*up from the gate|up partials and the
+  head applies the final norm.  8 launches per layer.
+* ``"partials"``: the same partials hand-off, with a single-workgroup residual+RMSNorm
+  kernel and a separate q/k norm+RoPE kernel (9 launches per layer).
+* ``"unfused"``: each GEMV runs to completion (in-kernel reduction and epilogue).
 """
 from __future__ import annotations
 
@@ -26,11 +40,30 @@ from . import ops
 from .model import Int4Backbone, attention_scale
 
 
+def _inverse(perm: torch.Tensor | None) -> torch.Tensor | None:
+    """``inv[perm[j]] = j`` (int32), or None for the identity."""
+    if perm is None:
+        return None
+    inv = torch.empty_like(perm)
+    inv[perm.long()] = torch.arange(perm.numel(), dtype=torch.int32, device=perm.device)
+    return inv
+
+
+def _gather(w: torch.Tensor, perm: torch.Tensor | None) -> torch.Tensor:
+    return w if perm is None else w[perm.long()].contiguous()
+
+
 class FastDecoder:
     """One decode step over an :class:`Int4Backbone` (eager or hipGraph replay)."""
 
-    def __init__(self, model: Int4Backbone):
+    PLANS = ("staged", "partials", "unfused")
+
+    def __init__(self, model: Int4Backbone, plan: str = "staged"):
+        if plan not in self.PLANS:
+            raise ValueError(f"plan must be one of {self.PLANS}")
         self.m = model
+        self.plan = plan
+        self.fused = plan != "unfused"
         cfg = model.cfg
         dev = model.device
         self.dev = dev
@@ -56,17 +89,131 @@ class FastDecoder:
                                    dtype=torch.uint8, device=dev)
         self.head_ws = torch.zeros(int(lib.mtl_head_workspace_bytes(cfg.vocab)), dtype=torch.uint8,
                                    device=dev)
+        # fused plan: per-GEMV split-K partial buffers and the act-order input buffers
+        self.splits = {name: int(lib.mtl_w4_gemm_splits(k, n)) for name, k, n in
+                       (("qkv", cfg.hidden, cfg.qkv_out), ("o", cfg.hidden, cfg.hidden),
+                        ("gate_up", cfg.hidden, 2 * cfg.intermediate),
+                        ("down", cfg.intermediate, cfg.hidden))}
+        cols = {"qkv": cfg.qkv_out, "o": cfg.hidden, "gate_up": 2 * cfg.intermediate,
+                "down": cfg.hidden}
+        self.part = {k: torch.zeros(self.splits[k] * cols[k], dtype=torch.float32, device=dev)
+                     for k in cols}
+        self.x_qkv = torch.zeros(cfg.hidden, dtype=bf, device=dev)
+        self.x_o = torch.zeros(cfg.hidden, dtype=bf, device=dev)
+        self.x_gu = torch.zeros(cfg.hidden, dtype=bf, device=dev)
+        self.slots = torch.zeros(16, dtype=torch.float32, device=dev)
+        self.inv_perm_o, self.inv_perm_qkv, self.inv_perm_gu = [], [], []
+        self.norm_qkv, self.norm_gu = [], []      # norm weights gathered by the GEMV's perm
+        for lyr in model.layers:
+            self.inv_perm_o.append(_inverse(lyr["o"].kernel_args()[3]))
+            pq, pg = lyr["qkv"].kernel_args()[3], lyr["gate_up"].kernel_args()[3]
+            self.inv_perm_qkv.append(_inverse(pq))
+            self.inv_perm_gu.append(_inverse(pg))
+            self.norm_qkv.append(_gather(lyr["input_layernorm"], pq))
+            self.norm_gu.append(_gather(lyr["post_attention_layernorm"], pg))
         self._build_plan()
         self.graph: torch.cuda.CUDAGraph | None = None
 
     # -- launch plan ------------------------------------------------------------------
-    def _gemm(self, x, lin, n, epilogue, resid, y):
+    def _gemm(self, x, lin, n, epilogue, resid, y, no_perm=False):
         qw, qz, sc, perm = lin.kernel_args()
+        if no_perm:
+            perm = None
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         return ("mtl_w4_gemm_fused",
                 (x.data_ptr(), 1, lin.in_features, qw.data_ptr(), N.META_GPTQ, sc.data_ptr(),
                  qz.data_ptr(), p(perm), n, lin.group_size, lin.zero_offset, epilogue, p(resid),
                  y.data_ptr(), N.OUT_BF16, self.ws.data_ptr(), self.ws.numel()))
+
+    def _partials(self, x, xpart_name, lin, n, name):
+        """Partials-only GEMV; its input is already in the weight's act-order row order."""
+        qw, qz, sc, _ = lin.kernel_args()
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        xpart = self.part[xpart_name] if xpart_name else None
+        xs = self.splits[xpart_name] if xpart_name else 0
+        out = self.part[name]
+        return ("mtl_w4_gemm_partials",
+                (p(x), p(xpart), xs, 2 * lin.in_features if xpart_name else 0, 1,
+                 lin.in_features, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(),
+                 None, n, lin.group_size,
+                 lin.zero_offset, out.data_ptr(), out.numel() * 4))
+
+    def _layer_plan_fused(self, li: int) -> list:
+        m, cfg = self.m, self.m.cfg
+        lyr = m.layers[li]
+        kc, vc = m.k_cache[li], m.v_cache[li]
+        scale = ctypes.c_float(attention_scale(cfg))
+        eps = ctypes.c_float(cfg.eps)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        prev = self.part["down"] if li > 0 else None
+        perm_qkv = lyr["qkv"].kernel_args()[3]
+        perm_gu = lyr["gate_up"].kernel_args()[3]
+        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+            raise RuntimeError("fused plan needs gate|up columns in the down input order")
+        return [
+            ("mtl_residual_rmsnorm", (p(prev), self.splits["down"], self.h.data_ptr(),
+                                      self.h.data_ptr(), lyr["input_layernorm"].data_ptr(),
+                                      self.x_qkv.data_ptr(), p(perm_qkv), cfg.hidden, eps)),
+            self._partials(self.x_qkv, None, lyr["qkv"], cfg.qkv_out, "qkv"),
+            ("mtl_qk_norm_rope_kv_partials", (self.part["qkv"].data_ptr(), self.splits["qkv"],
+                                              lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(),
+                                              m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
+                                              self.pos.data_ptr(), self.q.data_ptr(),
+                                              kc.data_ptr(), vc.data_ptr(), cfg.n_heads,
+                                              cfg.n_kv_heads, cfg.head_dim, cfg.max_seq, eps)),
+            ("mtl_decode_attention", (self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                      self.pos.data_ptr(), self.x_o.data_ptr(),
+                                      p(self.inv_perm_o[li]), cfg.n_heads, cfg.n_kv_heads,
+                                      cfg.head_dim, cfg.max_seq, scale, self.attn_ws.data_ptr(),
+                                      self.attn_ws.numel())),
+            self._partials(self.x_o, None, lyr["o"], cfg.hidden, "o"),
+            ("mtl_residual_rmsnorm", (self.part["o"].data_ptr(), self.splits["o"], self.h.data_ptr(),
+                                      self.h.data_ptr(), lyr["post_attention_layernorm"].data_ptr(),
+                                      self.x_gu.data_ptr(), p(perm_gu), cfg.hidden, eps)),
+            self._partials(self.x_gu, None, lyr["gate_up"], 2 * cfg.intermediate, "gate_up"),
+            self._partials(None, "gate_up", lyr["down"], cfg.hidden, "down"),
+        ]
+
+    def _layer_plan_staged(self, li: int) -> list:
+        m, cfg = self.m, self.m.cfg
+        lyr = m.layers[li]
+        kc, vc = m.k_cache[li], m.v_cache[li]
+        scale = ctypes.c_float(attention_scale(cfg))
+        eps = ctypes.c_float(cfg.eps)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        prev = self.part["down"] if li > 0 else None
+        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+            raise RuntimeError("staged plan needs gate|up columns in the down input order")
+        return [
+            ("mtl_residual_add", (p(prev), self.splits["down"], self.h.data_ptr(),
+                                  p(self.inv_perm_qkv[li]), self.x_qkv.data_ptr(),
+                                  self.slots.data_ptr(), cfg.hidden)),
+            self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"], cfg.qkv_out, "qkv"),
+            ("mtl_decode_attention_fused", (self.part["qkv"].data_ptr(), self.splits["qkv"],
+                                            lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(),
+                                            m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
+                                            kc.data_ptr(), vc.data_ptr(), self.pos.data_ptr(),
+                                            self.x_o.data_ptr(), p(self.inv_perm_o[li]),
+                                            cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                            cfg.max_seq, scale, eps, self.attn_ws.data_ptr(),
+                                            self.attn_ws.numel())),
+            self._partials(self.x_o, None, lyr["o"], cfg.hidden, "o"),
+            ("mtl_residual_add", (self.part["o"].data_ptr(), self.splits["o"], self.h.data_ptr(),
+                                  p(self.inv_perm_gu[li]), self.x_gu.data_ptr(),
+                                  self.slots.data_ptr(), cfg.hidden)),
+            self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"],
+                                2 * cfg.intermediate, "gate_up"),
+            self._partials(None, "gate_up", lyr["down"], cfg.hidden, "down"),
+        ]
+
+    def _norm_partials(self, h_ord, w_ord, lin, n, name):
+        qw, qz, sc, _ = lin.kernel_args()
+        out = self.part[name]
+        return ("mtl_w4_gemm_norm_partials",
+                (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
+                 ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
+                 qz.data_ptr(), n, lin.group_size, lin.zero_offset, out.data_ptr(),
+                 out.numel() * 4))
 
     def _layer_plan(self, li: int) -> list:
         m, cfg = self.m, self.m.cfg
@@ -84,14 +231,16 @@ class FastDecoder:
                                      kc.data_ptr(), vc.data_ptr(), cfg.n_heads, cfg.n_kv_heads,
                                      cfg.head_dim, cfg.max_seq, eps)),
             ("mtl_decode_attention", (self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                      self.pos.data_ptr(), self.attn.data_ptr(), cfg.n_heads,
+                                      self.pos.data_ptr(), self.attn.data_ptr(), None, cfg.n_heads,
                                       cfg.n_kv_heads, cfg.head_dim, cfg.max_seq, scale,
                                       self.attn_ws.data_ptr(), self.attn_ws.numel())),
             self._gemm(self.attn, lyr["o"], cfg.hidden, N.EPI_RESIDUAL, self.h, self.h),
             ("mtl_rmsnorm", (self.h.data_ptr(), lyr["post_attention_layernorm"].data_ptr(),
                              self.x.data_ptr(), 1, cfg.hidden, eps)),
             self._gemm(self.x, lyr["gate_up"], 2 * cfg.intermediate, N.EPI_SILU_MUL, None, self.act),
-            self._gemm(self.act, lyr["down"], cfg.hidden, N.EPI_RESIDUAL, self.h, self.h),
+            # gate|up already emits the SiLU*up channels in the down input order
+            self._gemm(self.act, lyr["down"], cfg.hidden, N.EPI_RESIDUAL, self.h, self.h,
+                       no_perm=lyr["act_in_down_order"]),
         ]
 
     def _build_plan(self) -> None:
@@ -99,20 +248,56 @@ class FastDecoder:
         lib = N.load()
         self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), 1, self.table_ptrs.data_ptr(),
                                           self.vocabs.data_ptr(), cfg.hidden, self.h.data_ptr()))]
-        self._layers = [self._layer_plan(li) for li in range(cfg.n_layers)]
-        self._final = [
-            ("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(), self.h_final.data_ptr(),
-                             1, cfg.hidden, ctypes.c_float(cfg.eps))),
-            ("mtl_bf16_gemv_argmax", (self.h_final.data_ptr(), m.head.data_ptr(), cfg.vocab,
-                                      cfg.hidden, self.logits.data_ptr(),
-                                      ctypes.c_void_p(self.ids.data_ptr()),
-                                      self.head_ws.data_ptr(), self.head_ws.numel())),
-            ("mtl_advance_position", (ctypes.c_void_p(self.pos.data_ptr()),)),
-        ]
+        eps = ctypes.c_float(cfg.eps)
+        head = ("mtl_bf16_gemv_argmax", (self.h_final.data_ptr(), m.head.data_ptr(), cfg.vocab,
+                                         cfg.hidden, self.logits.data_ptr(),
+                                         ctypes.c_void_p(self.ids.data_ptr()),
+                                         self.head_ws.data_ptr(), self.head_ws.numel()))
+        if self.plan == "staged":
+            self._layers = [self._layer_plan_staged(li) for li in range(cfg.n_layers)]
+            final = [self._flush_staged(),
+                     ("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
+                                                    self.slots.data_ptr(), eps, m.head.data_ptr(),
+                                                    cfg.vocab, cfg.hidden, self.logits.data_ptr(),
+                                                    ctypes.c_void_p(self.ids.data_ptr()),
+                                                    self.head_ws.data_ptr(),
+                                                    self.head_ws.numel()))]
+        elif self.plan == "partials":
+            self._layers = [self._layer_plan_fused(li) for li in range(cfg.n_layers)]
+            final = [("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
+                                               self.h.data_ptr(), self.h.data_ptr(),
+                                               m.final_norm.data_ptr(), self.h_final.data_ptr(),
+                                               None, cfg.hidden, eps)), head]
+        else:
+            self._layers = [self._layer_plan(li) for li in range(cfg.n_layers)]
+            final = [("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(),
+                                      self.h_final.data_ptr(), 1, cfg.hidden, eps)), head]
+        self._final = final + [("mtl_advance_position", (ctypes.c_void_p(self.pos.data_ptr()),))]
         self._fns = {name: getattr(lib, name) for name in
                      ("mtl_rmsnorm", "mtl_w4_gemm_fused", "mtl_qk_norm_rope_kv",
                       "mtl_decode_attention", "mtl_embed_sum", "mtl_bf16_gemv_argmax",
-                      "mtl_advance_position")}
+                      "mtl_advance_position", "mtl_w4_gemm_partials",
+                      "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
+                      "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
+                      "mtl_bf16_gemv_argmax_norm")}
+
+    def _flush_staged(self):
+        return ("mtl_residual_add", (self.part["down"].data_ptr(), self.splits["down"],
+                                     self.h.data_ptr(), None, None, self.slots.data_ptr(),
+                                     self.m.cfg.hidden))
+
+    # position of each int4 GEMV launch inside a layer's plan
+    _GEMV_AT = {"staged": {"qkv": 1, "o": 3, "gate_up": 5, "down": 6},
+                "partials": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7},
+                "unfused": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7}}
+
+    def gemv_launch(self, li: int, name: str):
+        """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
+        return self._layers[li][self._GEMV_AT[self.plan][name]]
+
+    def run_gemv(self, li: int, name: str) -> None:
+        """Issue only that GEMV (timing; its inputs are whatever the buffers hold)."""
+        self._run([self.gemv_launch(li, name)])
 
     def _run(self, plan) -> None:
         stream = torch.cuda.current_stream(self.dev).cuda_stream
@@ -121,8 +306,25 @@ class FastDecoder:
 
     # -- eager pieces -----------------------------------------------------------------
     def run_layer(self, li: int) -> None:
-        """One decoder layer on ``self.h`` at position ``self.pos`` (writes KV)."""
+        """One decoder layer on ``self.h`` at position ``self.pos`` (writes KV).
+
+        In the partials plans the layer's residual add of the down projection happens at the
+        start of the next layer (or the final norm); :meth:`flush_residual` applies it.
+        """
         self._run(self._layers[li])
+
+    def flush_residual(self) -> None:
+        """Partials plans: fold the pending down-projection partials into ``self.h``."""
+        if self.plan == "staged":
+            self._run([self._flush_staged()])
+        elif self.plan == "partials":
+            cfg = self.m.cfg
+            lyr0 = self.m.layers[0]
+            self._run([("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
+                                                 self.h.data_ptr(), self.h.data_ptr(),
+                                                 lyr0["input_layernorm"].data_ptr(),
+                                                 self.x.data_ptr(), None, cfg.hidden,
+                                                 ctypes.c_float(cfg.eps)))])
 
     def run_step(self) -> None:
         """One whole decode step, eager: token ``ids`` at ``pos`` -> next token in ``ids``."""

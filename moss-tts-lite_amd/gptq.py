@@ -87,6 +87,28 @@ class GPTQLinear(torch.nn.Module):
         if self._perm is not None:
             self.qweight = torch.empty(0, dtype=torch.int32, device=self.qweight.device)
 
+    @torch.no_grad()
+    def reorder_output_columns(self, cols: torch.Tensor) -> "GPTQLinear":
+        """Permute the output columns in place: new column c is old column ``cols[c]``.
+
+        Used at load time so a producer writes its output directly in the act-order
+        input order of its consumer (bitwise neutral per column).
+        """
+        cols = cols.to(device=self.scales.device, dtype=torch.long)
+        if cols.numel() != self.out_features:
+            raise ValueError("cols must list every output column once")
+        if self._kernel_qweight is None:
+            self.post_init()
+        sorted_separately = self._kernel_qweight is not self.qweight
+        self._kernel_qweight = self._kernel_qweight[:, cols].contiguous()
+        if sorted_separately and self.qweight.numel():
+            self.qweight = self.qweight[:, cols].contiguous()
+        elif not sorted_separately:
+            self.qweight = self._kernel_qweight
+        self.scales = self.scales[:, cols].contiguous()
+        self.qzeros = _pack_cols(_unpack_cols(self.qzeros)[:, cols])
+        return self
+
     def forward(self, x: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
         qw, qz, sc, perm = self.kernel_args()
         return ops.gptq_gemm(x, qw, qz, sc, self.group_size, perm=perm,

@@ -51,6 +51,21 @@ class BackboneConfig:
             raise ValueError("intermediate must be a multiple of 64 and of the group size")
 
 
+def gate_up_columns_for(order: torch.Tensor, block: int = 32) -> torch.Tensor:
+    """Fused gate|up column order that emits intermediate channel ``order[j]`` at j.
+
+    Fused column of (gate, j) is ``64*(j//32) + j%32`` and of (up, j) that plus 32.
+    """
+    order = order.to(torch.long)
+    j = torch.arange(order.numel(), device=order.device)
+    new_g = 2 * block * (j // block) + j % block
+    old_g = 2 * block * (order // block) + order % block
+    cols = torch.empty(2 * order.numel(), dtype=torch.long, device=order.device)
+    cols[new_g] = old_g
+    cols[new_g + block] = old_g + block
+    return cols
+
+
 def rope_tables(n: int, head_dim: int, theta: float, device, dtype=torch.bfloat16):
     """cos/sin ``[n, head_dim]``: the reference's fp32 chain (model.py:115-124)."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
@@ -86,6 +101,12 @@ class Int4Backbone:
                 lin.post_init()
                 lin.drop_original()
                 lyr[k] = lin
+            # gate|up emits its SiLU*up channels already in the down projection's
+            # act-order input order, so the down GEMV reads them without a gather.
+            perm_down = lyr["down"].kernel_args()[3]
+            lyr["act_in_down_order"] = perm_down is not None
+            if perm_down is not None:
+                lyr["gate_up"].reorder_output_columns(gate_up_columns_for(perm_down))
             self.layers.append(lyr)
         self.rope_cos, self.rope_sin = rope_tables(cfg.max_seq, cfg.head_dim, cfg.rope_theta, dev)
         self.k_cache = torch.zeros(cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, cfg.head_dim,

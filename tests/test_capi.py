@@ -101,8 +101,18 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_qk_norm_rope_kv(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 6, 128,
                                    64, eps, None) == N.MTL_ERR_SHAPE
     assert lib.mtl_decode_attention_workspace_bytes(32, 128) == 32 * 16 * 132 * 4
-    assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, 128, 2048, C.c_float(0.1),
-                                    None, 0, None) == N.MTL_ERR_WORKSPACE
+    assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, None, 32, 8, 128, 2048,
+                                    C.c_float(0.1), None, 0, None) == N.MTL_ERR_WORKSPACE
+    assert lib.mtl_residual_rmsnorm(None, 0, FAKE, FAKE, FAKE, FAKE, None, 4098, eps,
+                                    None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_residual_rmsnorm(FAKE, 0, FAKE, FAKE, FAKE, FAKE, None, 4096, eps,
+                                    None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_w4_gemm_splits(4096, 24576) == 8 and lib.mtl_w4_gemm_splits(12288, 4096) == 24
+    # partials entry: x and xpart are exclusive; the gate|up source needs M = 1
+    assert lib.mtl_w4_gemm_partials(FAKE, FAKE, 8, 8192, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
+                                    128, 0, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_w4_gemm_partials(None, FAKE, 8, 8192, 2, 4096, FAKE, FAKE, FAKE, None, 4096,
+                                    128, 0, FAKE, 1 << 30, None) == N.MTL_ERR_UNSUPPORTED
     assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG

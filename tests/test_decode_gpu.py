@@ -134,7 +134,7 @@ def test_decode_attention_kernel(dev, lib, length):
     tpos = torch.tensor([length - 1], dtype=torch.int64, device=dev)
     scale = 1 / np.sqrt(128)
     N.check(lib.mtl_decode_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tpos.data_ptr(),
-                                     out.data_ptr(), H, Hkv, 128, S, ctypes.c_float(scale),
+                                     out.data_ptr(), None, H, Hkv, 128, S, ctypes.c_float(scale),
                                      ws.data_ptr(), ws.numel(), stream()), "attention")
     ref = D.attention(q, kc[:, :length], vc[:, :length], scale)
     err = rel_l2(fb(out).reshape(H, 128), ref)
@@ -217,6 +217,46 @@ def test_mini_model_steps_match_oracle_and_graph_is_bitwise(dev):
         assert torch.equal(dec.logits, e_logits[i]), f"replay {i} differs from eager"
 
 
+def test_launch_plans_agree(dev):
+    cfg = small_config()
+    model, ow = build_case(cfg, seed=21, dev=dev)
+    prompt = torch.tensor([3, 1, 4, 1, 5, 9, 2, 6])
+    out = {}
+    for plan in FastDecoder.PLANS:
+        dec = FastDecoder(model, plan=plan)
+        dec.prefill(prompt)
+        toks, logits = [], []
+        for _ in range(6):
+            toks.append(int(dec.ids.item()))
+            dec.run_step()
+            logits.append(fb(dec.logits))
+        out[plan] = (toks, logits)
+    for plan in ("staged", "partials"):
+        for i in range(6):
+            err = rel_l2(out[plan][1][i], out["unfused"][1][i])
+            print(f"step {i}: {plan} vs unfused logits rel_l2={err:.2e}")
+            assert err < 5e-3
+
+
+@pytest.mark.parametrize("plan", ["staged", "partials"])
+def test_plan_graph_replay_is_bitwise(dev, plan):
+    cfg = small_config()
+    model, _ = build_case(cfg, seed=23, dev=dev)
+    dec = FastDecoder(model, plan=plan)
+    prompt = torch.tensor([8, 6, 7, 5, 3, 0, 9])
+    dec.prefill(prompt)
+    eager = []
+    for _ in range(5):
+        dec.run_step()
+        eager.append((int(dec.ids.item()), dec.logits.clone()))
+    dec.prefill(prompt)
+    dec.capture()
+    for i in range(5):
+        dec.graph.replay()
+        assert int(dec.ids.item()) == eager[i][0]
+        assert torch.equal(dec.logits, eager[i][1]), f"{plan}: replay {i} differs from eager"
+
+
 def test_full_size_layer_config3(dev):
     # One Qwen3-8B-shaped layer at position 2048 over a bf16 KV cache of 2048 past
     # positions ~N(0,1), act-order int4 projections.
@@ -234,6 +274,7 @@ def test_full_size_layer_config3(dev):
     dec.h.copy_(tb(h0, dev))
     dec.pos.fill_(2048)
     dec.run_layer(0)
+    dec.flush_residual()
     torch.cuda.synchronize()
     cos, sin = fb(model.rope_cos), fb(model.rope_sin)
     h1 = D.decoder_layer(h0, ow["layers"][0], kc[0], vc[0], 2048, cos, sin, 32, 8, 128)
@@ -241,3 +282,232 @@ def test_full_size_layer_config3(dev):
     kerr = rel_l2(fb(model.k_cache)[0, :, 2048], kc[0, :, 2048])
     print(f"config3 layer: h rel_l2={err:.2e} k_cache[2048] rel_l2={kerr:.2e}")
     assert err < 1e-2 and kerr < 1e-2
+
+
+def _seq_sum(parts):
+    acc = np.zeros(parts.shape[1:], np.float32)
+    for p in parts:                       # split order, fp32, as the kernels sum
+        acc = (acc + p).astype(np.float32)
+    return acc
+
+
+def test_gemm_partials_sum_to_the_single_launch_result(dev, lib):
+    from moss_tts_lite_amd import ops
+    from oracle import synth
+    case = synth.gptq_case(k=4096, n=6144, m=1, group=128, seed=3, with_ref=False)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    qw, qz = t(case["qweight"]), t(case["qzeros"])
+    sc = t(case["scales"].view(np.float16))
+    x = t(case["x_bits"].view(np.int16)).view(torch.bfloat16)
+    S = int(lib.mtl_w4_gemm_splits(4096, 6144))
+    part = torch.empty(S * 6144, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_w4_gemm_partials(x.data_ptr(), None, 0, 0, 1, 4096, qw.data_ptr(), sc.data_ptr(),
+                                     qz.data_ptr(), None, 6144, 128, 0, part.data_ptr(),
+                                     part.numel() * 4, stream()), "partials")
+    whole = ops.gptq_gemm(x, qw, qz, sc, 128, out_dtype=torch.float32)
+    summed = _seq_sum(part.view(S, 6144).cpu().numpy())
+    assert np.array_equal(summed, whole.cpu().numpy()[0])
+
+
+def test_down_reads_silu_mul_from_gate_up_partials(dev, lib):
+    from moss_tts_lite_amd import ops
+    from oracle import synth
+    inter = 1024
+    gu = synth.gptq_case(k=512, n=2 * inter, m=1, group=128, seed=4, with_ref=False)
+    dn = synth.gptq_case(k=inter, n=512, m=1, group=128, seed=5, with_ref=False)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    x = t(gu["x_bits"].view(np.int16)).view(torch.bfloat16)
+    gq, gz, gs = t(gu["qweight"]), t(gu["qzeros"]), t(gu["scales"].view(np.float16))
+    dq, dz, ds = t(dn["qweight"]), t(dn["qzeros"]), t(dn["scales"].view(np.float16))
+    S = int(lib.mtl_w4_gemm_splits(512, 2 * inter))
+    pgu = torch.empty(S * 2 * inter, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_w4_gemm_partials(x.data_ptr(), None, 0, 0, 1, 512, gq.data_ptr(), gs.data_ptr(),
+                                     gz.data_ptr(), None, 2 * inter, 128, 0, pgu.data_ptr(),
+                                     pgu.numel() * 4, stream()), "gate_up partials")
+    act = ops.w4_gemm(x.view(1, -1), gq, N.META_GPTQ, gs, gz, None, 2 * inter, 128,
+                      epilogue=N.EPI_SILU_MUL)
+    Sd = int(lib.mtl_w4_gemm_splits(inter, 512))
+    p1 = torch.empty(Sd * 512, dtype=torch.float32, device=dev)
+    p2 = torch.empty_like(p1)
+    N.check(lib.mtl_w4_gemm_partials(act.data_ptr(), None, 0, 0, 1, inter, dq.data_ptr(), ds.data_ptr(),
+                                     dz.data_ptr(), None, 512, 128, 0, p1.data_ptr(), p1.numel() * 4,
+                                     stream()), "down from act")
+    N.check(lib.mtl_w4_gemm_partials(None, pgu.data_ptr(), S, 2 * inter, 1, inter, dq.data_ptr(),
+                                     ds.data_ptr(), dz.data_ptr(), None, 512, 128, 0, p2.data_ptr(),
+                                     p2.numel() * 4, stream()), "down from gate_up partials")
+    assert torch.equal(p1, p2)
+
+
+def test_qk_rope_from_partials_matches_bf16_input(dev, lib):
+    from moss_tts_lite_amd.model import rope_tables
+    r = np.random.default_rng(8)
+    H, Hkv, S_, pos, splits = 32, 8, 64, 11, 8
+    ncols = (H + 2 * Hkv) * 128
+    parts = (r.standard_normal((splits, ncols)) * 0.5).astype(np.float32)
+    qkv = round_bf16(_seq_sum(parts))
+    qn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
+    kn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
+    cos, sin = rope_tables(S_, 128, 1e6, dev)
+    tpos = torch.tensor([pos], dtype=torch.int64, device=dev)
+    res = []
+    for use_part in (False, True):
+        kc = torch.zeros(Hkv, S_, 128, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        q_out = torch.zeros(H * 128, dtype=torch.bfloat16, device=dev)
+        args = (tb(qn, dev), tb(kn, dev))
+        if use_part:
+            tp = torch.from_numpy(parts).to(dev)
+            st = lib.mtl_qk_norm_rope_kv_partials(tp.data_ptr(), splits, args[0].data_ptr(),
+                                                  args[1].data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                                  tpos.data_ptr(), q_out.data_ptr(), kc.data_ptr(),
+                                                  vc.data_ptr(), H, Hkv, 128, S_,
+                                                  ctypes.c_float(1e-6), stream())
+        else:
+            tq = tb(qkv, dev)
+            st = lib.mtl_qk_norm_rope_kv(tq.data_ptr(), args[0].data_ptr(), args[1].data_ptr(),
+                                         cos.data_ptr(), sin.data_ptr(), tpos.data_ptr(),
+                                         q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), H, Hkv, 128,
+                                         S_, ctypes.c_float(1e-6), stream())
+        N.check(st, "qk_rope")
+        res.append((q_out, kc, vc))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
+def test_residual_rmsnorm_with_partials_and_gather(dev, lib):
+    r = np.random.default_rng(9)
+    n, S = 4096, 24
+    parts = (r.standard_normal((S, n)) * 0.3).astype(np.float32)
+    resid = round_bf16(r.standard_normal(n).astype(np.float32))
+    w = round_bf16((1 + 0.1 * r.standard_normal(n)).astype(np.float32))
+    gather = r.permutation(n).astype(np.int32)
+    tp = torch.from_numpy(parts).to(dev)
+    th = tb(resid, dev)
+    x_out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    tg = torch.from_numpy(gather).to(dev)
+    tw = tb(w, dev)
+    N.check(lib.mtl_residual_rmsnorm(tp.data_ptr(), S, th.data_ptr(), th.data_ptr(), tw.data_ptr(),
+                                     x_out.data_ptr(), tg.data_ptr(), n, ctypes.c_float(1e-6), stream()),
+            "residual_rmsnorm")
+    h = round_bf16(round_bf16(_seq_sum(parts)) + resid)
+    assert np.array_equal(fb(th), h)                    # h updated in place, bit-exact
+    x = D.rms_norm(h, w)
+    assert max_ulps(fb(x_out), x[gather]) <= 1.0
+
+
+def test_residual_add_slots_and_scatter(dev, lib):
+    r = np.random.default_rng(12)
+    n, S = 4096, 24
+    parts = (r.standard_normal((S, n)) * 0.3).astype(np.float32)
+    resid = round_bf16(r.standard_normal(n).astype(np.float32))
+    scatter = r.permutation(n).astype(np.int32)
+    tp = torch.from_numpy(parts).to(dev)
+    th = tb(resid, dev)
+    h_ord = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    slots = torch.zeros(16, dtype=torch.float32, device=dev)
+    ts = torch.from_numpy(scatter).to(dev)
+    N.check(lib.mtl_residual_add(tp.data_ptr(), S, th.data_ptr(), ts.data_ptr(), h_ord.data_ptr(),
+                                 slots.data_ptr(), n, stream()), "residual_add")
+    h = round_bf16(round_bf16(_seq_sum(parts)) + resid)
+    assert np.array_equal(fb(th), h)                       # in place, bit-exact
+    ho = np.empty_like(h)
+    ho[scatter] = h
+    assert np.array_equal(fb(h_ord), ho)                  # scattered, bit-exact
+    blocks = (h.astype(np.float64) ** 2).reshape(16, -1).sum(1)
+    assert np.allclose(slots.cpu().numpy(), blocks, rtol=1e-5)
+    # without partials: h is only read; without scatter: plain copy
+    h2 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    N.check(lib.mtl_residual_add(None, 0, th.data_ptr(), None, h2.data_ptr(), slots.data_ptr(), n,
+                                 stream()), "residual_add copy")
+    assert torch.equal(h2, th)
+
+
+def test_gemm_norm_partials_match_oracle(dev, lib):
+    from oracle import gptq_ref as G
+    from oracle import synth
+    K, Nn = 4096, 6144
+    case = synth.gptq_case(k=K, n=Nn, m=1, group=128, act_order=True, seed=31, with_ref=False)
+    qs, ps = G.actorder_sort(case["qweight"], case["g_idx"], 128)  # group-sorted rows + perm
+    r = np.random.default_rng(32)
+    h = round_bf16(r.standard_normal(K).astype(np.float32))
+    w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    slots = t((h.astype(np.float32) ** 2).reshape(16, -1).sum(1, dtype=np.float32))
+    S = int(lib.mtl_w4_gemm_splits(K, Nn))
+    part = torch.empty(S * Nn, dtype=torch.float32, device=dev)
+    qw, qz, sc = t(qs), t(case["qzeros"]), t(case["scales"].view(np.float16))
+    th, tw = tb(h[ps], dev), tb(w[ps], dev)   # named: a temporary's memory could be reused
+    N.check(lib.mtl_w4_gemm_norm_partials(th.data_ptr(), tw.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), K, qw.data_ptr(),
+                                          sc.data_ptr(), qz.data_ptr(), Nn, 128, 0, part.data_ptr(),
+                                          part.numel() * 4, stream()), "norm partials")
+    y = _seq_sum(part.view(S, Nn).cpu().numpy())
+    x = D.rms_norm(h, w)
+    ref = G.gptq_gemm(x[None], case["qweight"], case["qzeros"], case["scales"], case["g_idx"],
+                      128)[0]
+    err = rel_l2(y, ref)
+    print(f"norm-staged GEMV rel_l2={err:.2e}")
+    assert err < 1e-3
+
+
+@pytest.mark.parametrize("pos,max_seq", [(11, 64), (700, 1024), (0, 64), (1023, 1024)])
+def test_attention_fused_matches_two_kernel_path(dev, lib, pos, max_seq):
+    from moss_tts_lite_amd.model import rope_tables
+    r = np.random.default_rng(40 + pos)
+    H, Hkv, splits = 32, 8, 8
+    ncols = (H + 2 * Hkv) * 128
+    parts = torch.from_numpy((r.standard_normal((splits, ncols)) * 0.5).astype(np.float32)).to(dev)
+    qn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
+    kn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
+    cos, sin = rope_tables(max_seq, 128, 1e6, dev)
+    tpos = torch.tensor([pos], dtype=torch.int64, device=dev)
+    cache = tb(r.standard_normal((2, Hkv, max_seq, 128)).astype(np.float32), dev)
+    ws = torch.zeros(int(lib.mtl_decode_attention_workspace_bytes(H, 128)), dtype=torch.uint8,
+                     device=dev)
+    out_index = torch.from_numpy(r.permutation(H * 128).astype(np.int32)).to(dev)
+    scale, eps = ctypes.c_float(128 ** -0.5), ctypes.c_float(1e-6)
+    res = []
+    for fused in (False, True):
+        kc, vc = cache[0].clone(), cache[1].clone()
+        out = torch.zeros(H * 128, dtype=torch.bfloat16, device=dev)
+        if fused:
+            N.check(lib.mtl_decode_attention_fused(
+                parts.data_ptr(), splits, qn.data_ptr(), kn.data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), kc.data_ptr(), vc.data_ptr(), tpos.data_ptr(), out.data_ptr(),
+                out_index.data_ptr(), H, Hkv, 128, max_seq, scale, eps, ws.data_ptr(), ws.numel(),
+                stream()), "attention fused")
+        else:
+            q = torch.zeros(H * 128, dtype=torch.bfloat16, device=dev)
+            N.check(lib.mtl_qk_norm_rope_kv_partials(
+                parts.data_ptr(), splits, qn.data_ptr(), kn.data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), tpos.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), H,
+                Hkv, 128, max_seq, eps, stream()), "qk rope")
+            N.check(lib.mtl_decode_attention(
+                q.data_ptr(), kc.data_ptr(), vc.data_ptr(), tpos.data_ptr(), out.data_ptr(),
+                out_index.data_ptr(), H, Hkv, 128, max_seq, scale, ws.data_ptr(), ws.numel(),
+                stream()), "attention")
+        res.append((out, kc, vc))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
+def test_head_norm_argmax_matches_oracle(dev, lib):
+    r = np.random.default_rng(50)
+    V, K = 20011, 4096
+    h = round_bf16((2 * r.standard_normal(K)).astype(np.float32))
+    w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
+    W = round_bf16((r.standard_normal((V, K)) * 0.02).astype(np.float32))
+    slots = torch.from_numpy((h ** 2).reshape(16, -1).sum(1, dtype=np.float32)).to(dev)
+    tW, th, tw = tb(W, dev), tb(h, dev), tb(w, dev)
+    logits = torch.zeros(V, dtype=torch.bfloat16, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    ws = torch.zeros(int(lib.mtl_head_workspace_bytes(V)), dtype=torch.uint8, device=dev)
+    N.check(lib.mtl_bf16_gemv_argmax_norm(th.data_ptr(), tw.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), tW.data_ptr(), V, K,
+                                          logits.data_ptr(), tok.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), stream()), "head norm")
+    x = D.rms_norm(h, w)
+    ref = round_bf16((W.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+    assert rel_l2(fb(logits), ref) < 1e-2
+    srt = np.sort(ref)
+    if srt[-1] - srt[-2] > 0.05:
+        assert int(tok.item()) == int(np.argmax(ref))
+    assert int(tok.item()) == int(np.argmax(fb(logits)))
