@@ -77,13 +77,18 @@ int mtl_residual_rmsnorm(const float* partials, int32_t splits, const void* resi
 
 /*
  * GQA decode attention over cache positions [0, pos] (the reference's SDPA call at
- * moss_tts_lite/fast.py:149-162, exact length pos + 1): split over the sequence
- * in chunks, fp32 softmax, chunk partials combined in chunk order.
+ * moss_tts_lite/fast.py:149-162, exact length pos + 1): one launch, split over the
+ * sequence in chunks of at most 64 positions (up to 64 chunks), fp32 softmax, chunk
+ * results merged in chunk order by the last workgroup of each kv head.
  *   q    bf16 [n_heads * head_dim];  out bf16 [n_heads * head_dim]
  *   out_index  NULL, or int32 [n_heads * head_dim]: value i is written to
  *              out[out_index[i]] (the act-order input order of the o projection)
  *   scale  softmax scale (1/sqrt(head_dim) in the reference)
- * head_dim must be 128; n_heads % n_kv_heads == 0.
+ *   workspace  mtl_decode_attention_workspace_bytes(n_heads, head_dim) bytes, 16-byte
+ *              aligned, ZERO-FILLED before its first use (every launch leaves its
+ *              counters zero again); one stream at a time.
+ * head_dim must be 128; n_heads % n_kv_heads == 0, n_heads / n_kv_heads <= 8.
+ * pos < 0 writes nothing; pos >= max_seq attends over [0, max_seq).
  */
 int64_t mtl_decode_attention_workspace_bytes(int32_t n_heads, int32_t head_dim);
 int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
@@ -116,7 +121,7 @@ int mtl_residual_add(const float* partials, int32_t splits, void* h, const int32
 /*
  * mtl_qk_norm_rope_kv_partials and mtl_decode_attention in one pass: q/k RMSNorm,
  * RoPE and the KV write of position pos are done inside the attention workgroups
- * from the q|k|v split-K partials (fast.py:134-162).  n_heads / n_kv_heads <= 4.
+ * from the q|k|v split-K partials (fast.py:134-162).  Same workspace and limits.
  * The q/k/v projections of position pos are not written anywhere except the cache.
  */
 int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const void* q_norm_w,

@@ -284,84 +284,25 @@ __global__ void __launch_bounds__(64) qk_norm_rope_kv_kernel(
 }
 
 // ----------------------------------------------------------------------------------
-// GQA decode attention, split over the sequence.  Grid (kv head, chunk); wave w of a
-// workgroup serves q head kvh*n_rep + w (+4, ...).  Scores are lane-per-position dot
-// products against the wave-uniform q; the value sum is dims-per-lane.  Each chunk
-// writes (max, sum, o[128]) and attn_combine_kernel merges chunks in order.
+// GQA decode attention over positions [0, pos] (fast.py:149-162), split over the
+// sequence.  Grid (kv head, chunk): nch = min(ceil(L / 64), 64) chunks of at most
+// ceil(L / nch) positions, so for L <= 4096 a workgroup scores at most 64 positions in
+// one pass with every K and V load in flight at once.  Wave w of a workgroup serves q
+// head kvh * n_rep + w (+4, ...).  Scores are lane-per-position dot products against the
+// wave-uniform q; the value sum gives each lane 8 dims of 16 positions (u32x4 loads),
+// reduced across the 4 position groups at the end.  Each chunk publishes
+// (max, sum, o[128]); the last workgroup of a kv head to finish (agent-scope counter)
+// merges that head group's chunks in chunk order, so there is no second launch.
+// With FROM_PART, q/k RMSNorm, RoPE and the KV write of position pos run in the
+// prologue from the q|k|v split-K partials (fast.py:134-147); the workgroup holding pos
+// uses its LDS copy of k/v for that position.
 // ----------------------------------------------------------------------------------
-constexpr int kAttnChunks = 16;
-constexpr int kAttnPart = 132;   // m, l, 2 pad, o[128]
+constexpr int kAttnBlock = 64;        // positions per pass
+constexpr int kAttnMaxChunks = 64;
+constexpr int kAttnMaxRep = 8;        // q heads per kv head
+constexpr int kAttnPart = 132;        // m, l, 2 pad, o[128]
+constexpr int kAttnCounterBytes = 1024;
 
-__global__ void __launch_bounds__(256) attn_partial_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int64_t* __restrict__ pos_ptr,
-    float* __restrict__ part, int H, int Hkv, int64_t max_seq, float scale) {
-  constexpr int D = 128;
-  const int kvh = blockIdx.x, c = blockIdx.y;
-  const int wave = wave_id(), lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  const int n_rep = H / Hkv;
-  int64_t L = *pos_ptr + 1;
-  if (L < 0) L = 0;
-  if (L > max_seq) L = max_seq;
-  const int clen = (int)((L + kAttnChunks - 1) / kAttnChunks);
-  const int p0 = c * clen;
-  const int p1 = (int)(p0 + clen < L ? p0 + clen : L);
-  const uint16_t* kbase = kc + (size_t)kvh * max_seq * D;
-  const uint16_t* vbase = vc + (size_t)kvh * max_seq * D;
-  for (int hr = wave; hr < n_rep; hr += nw) {
-    const int h = kvh * n_rep + hr;
-    const uint32_t* qh = reinterpret_cast<const uint32_t*>(q + (size_t)h * D);
-    uint32_t qv[64];
-#pragma unroll
-    for (int i = 0; i < 64; ++i) qv[i] = qh[i];
-    float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int base = p0; base < p1; base += 64) {
-      const int p = base + lane;
-      float s = -INFINITY;
-      if (p < p1) {
-        const u32x4* kr = reinterpret_cast<const u32x4*>(kbase + (size_t)p * D);
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const u32x4 kk = kr[i];
-          acc = dot2_bf16(kk.x, qv[4 * i + 0], acc);
-          acc = dot2_bf16(kk.y, qv[4 * i + 1], acc);
-          acc = dot2_bf16(kk.z, qv[4 * i + 2], acc);
-          acc = dot2_bf16(kk.w, qv[4 * i + 3], acc);
-        }
-        s = acc * scale;
-      }
-      const float mn = fmaxf(m, wave_max(s));
-      const float e = (p < p1) ? expf(s - mn) : 0.f;
-      const float corr = expf(m - mn);
-      l = fmaf(l, corr, wave_sum(e));
-      o0 *= corr;
-      o1 *= corr;
-      const int cnt = p1 - base < 64 ? p1 - base : 64;
-      const uint32_t* vr = reinterpret_cast<const uint32_t*>(vbase + (size_t)base * D) + lane;
-#pragma unroll 16
-      for (int j = 0; j < cnt; ++j) {
-        const float ej = __shfl(e, j);
-        const uint32_t vv = vr[(size_t)j * (D / 2)];
-        o0 = fmaf(ej, lo_bf(vv), o0);
-        o1 = fmaf(ej, hi_bf(vv), o1);
-      }
-      m = mn;
-    }
-    float* ph = part + ((size_t)h * kAttnChunks + c) * kAttnPart;
-    if (lane == 0) {
-      ph[0] = m;
-      ph[1] = l;
-    }
-    ph[4 + 2 * lane] = o0;
-    ph[5 + 2 * lane] = o1;
-  }
-}
-
-// Same attention, with q/k RMSNorm + RoPE + the KV write of position pos folded in: each
-// workgroup rebuilds its q heads from the q|k|v split-K partials; the workgroup whose
-// chunk holds pos also builds k and v there, writes them to the cache and uses its LDS
-// copy for that position (fast.py:134-162).
 __device__ __forceinline__ void head_from_partials(const float* __restrict__ part, int splits,
                                                    int ncols, int head, int t, float& x0,
                                                    float& x1) {
@@ -383,6 +324,9 @@ __device__ __forceinline__ void head_from_partials(const float* __restrict__ par
   x1 = round_bf16(a1);
 }
 
+// RMSNorm over the 128 dims of one head (lane t holds dims t and t+64), then RoPE:
+// q*cos + rotate_half(q)*sin, each product and the sum rounded to bf16 as separate bf16
+// tensor ops (model.py:34-44, fast.py:141-144).
 __device__ __forceinline__ void norm_rope_pair(float x0, float x1, const uint16_t* w,
                                                const uint16_t* cr, const uint16_t* sr, int t,
                                                float eps, float& o0, float& o1) {
@@ -395,134 +339,226 @@ __device__ __forceinline__ void norm_rope_pair(float x0, float x1, const uint16_
   o1 = round_bf16(round_bf16(n1 * bf16_to_f32(cr[t + 64])) + round_bf16(n0 * bf16_to_f32(sr[t + 64])));
 }
 
-__global__ void __launch_bounds__(256) attn_fused_kernel(
-    const float* __restrict__ qkv_part, int splits, const uint16_t* __restrict__ qn,
-    const uint16_t* __restrict__ kn, const uint16_t* __restrict__ cos_tab,
-    const uint16_t* __restrict__ sin_tab, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-    const int64_t* __restrict__ pos_ptr, float* __restrict__ part, int H, int Hkv,
-    int64_t max_seq, float scale, float eps) {
+struct AttnArgs {
+  const uint16_t* q;          // bf16 [H*128] (plain variant)
+  const float* qkv_part;      // fp32 [splits, (H+2Hkv)*128] (FROM_PART variant)
+  int splits;
+  const uint16_t* qn;
+  const uint16_t* kn;
+  const uint16_t* cos_tab;
+  const uint16_t* sin_tab;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int64_t* pos;
+  uint16_t* out;
+  const int32_t* out_index;
+  float* part;                // [H, kAttnMaxChunks, kAttnPart]
+  uint32_t* counters;         // [Hkv], zero between launches
+  int H, Hkv;
+  int64_t max_seq;
+  float scale, eps;
+};
+
+template <bool FROM_PART>
+__global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   constexpr int D = 128;
-  __shared__ uint32_t q_lds[4][D / 2];       // normed+rotated q heads (bf16 pairs)
-  __shared__ uint32_t kpos[D / 2], vpos[D / 2];
+  __shared__ u32x4 q_lds[kAttnMaxRep][16];
+  __shared__ u32x4 kpos[16], vpos[16];
+  __shared__ float e_lds[4][kAttnBlock];
+  __shared__ float w_lds[4][kAttnMaxChunks];
+  __shared__ int last_flag;
   const int kvh = blockIdx.x, c = blockIdx.y;
-  const int wave = wave_id(), lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  const int n_rep = H / Hkv;
-  const int ncols = (H + 2 * Hkv) * D;
-  const int64_t pos = *pos_ptr;
-  int64_t L = pos + 1;
-  if (L < 0) L = 0;
-  if (L > max_seq) L = max_seq;
-  const int clen = (int)((L + kAttnChunks - 1) / kAttnChunks);
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+  const int n_rep = a.H / a.Hkv;
+  const int64_t pos = *a.pos;
+  int64_t L64 = pos + 1;
+  if (L64 < 0) L64 = 0;
+  if (L64 > a.max_seq) L64 = a.max_seq;
+  const int L = (int)L64;
+  int nch = (L + kAttnBlock - 1) / kAttnBlock;
+  if (nch > kAttnMaxChunks) nch = kAttnMaxChunks;
+  if (c >= nch) return;                               // uniform over the workgroup
+  const int clen = (L + nch - 1) / nch;
   const int p0 = c * clen;
-  const int p1 = (int)(p0 + clen < L ? p0 + clen : L);
+  const int p1 = p0 + clen < L ? p0 + clen : L;       // p0 < p1 unless the chunk is empty
   const bool has_pos = pos >= p0 && pos < p1;
-  const uint16_t* cr = cos_tab + (pos >= 0 && pos < max_seq ? pos : 0) * D;
-  const uint16_t* sr = sin_tab + (pos >= 0 && pos < max_seq ? pos : 0) * D;
-  uint16_t* kbase = kc + (size_t)kvh * max_seq * D;
-  uint16_t* vbase = vc + (size_t)kvh * max_seq * D;
-  // prologue: k and v of position pos (only the workgroup that scores it)
-  if (has_pos && wave < 2) {
-    float x0, x1;
-    head_from_partials(qkv_part, splits, ncols, (wave == 0 ? H : H + Hkv) + kvh, lane, x0, x1);
-    if (wave == 0) norm_rope_pair(x0, x1, kn, cr, sr, lane, eps, x0, x1);
-    const uint32_t b0 = f32_to_bf16(x0), b1 = f32_to_bf16(x1);
-    uint16_t* dst = (wave == 0 ? kbase : vbase) + (size_t)pos * D;
-    dst[lane] = (uint16_t)b0;
-    dst[lane + 64] = (uint16_t)b1;
-    uint16_t* l16 = reinterpret_cast<uint16_t*>(wave == 0 ? kpos : vpos);
-    l16[lane] = (uint16_t)b0;
-    l16[lane + 64] = (uint16_t)b1;
-  }
-  for (int hr = wave; hr < n_rep; hr += nw) {
-    const int h = kvh * n_rep + hr;
-    float x0, x1;
-    head_from_partials(qkv_part, splits, ncols, h, lane, x0, x1);
-    norm_rope_pair(x0, x1, qn, cr, sr, lane, eps, x0, x1);
-    uint16_t* l16 = reinterpret_cast<uint16_t*>(q_lds[hr & 3]);
-    l16[lane] = (uint16_t)f32_to_bf16(x0);
-    l16[lane + 64] = (uint16_t)f32_to_bf16(x1);
+  const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
+  const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
+  const int dg = lane & 15, ps = lane >> 4;           // value pass: dims 8dg.., positions ps+4i
+
+  // 1. First block's K rows and V slices, issued before the q prologue.
+  u32x4 kr[16], vr[16];
+  auto load_block = [&](int base) {
+    const int last = p1 - 1 > 0 ? p1 - 1 : 0;
+    const int pk = base + lane < p1 ? base + lane : last;
+    const u32x4* krow = reinterpret_cast<const u32x4*>(kbase + (size_t)pk * D);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kr[i] = krow[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int pv = base + ps + 4 * i < p1 ? base + ps + 4 * i : last;
+      vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pv * D + 8 * dg);
+    }
+  };
+  if (p0 < p1) load_block(p0);
+
+  // 2. Prologue: q heads into LDS; k/v of position pos (cache + LDS) where it is scored.
+  const size_t prow = (size_t)(pos >= 0 && pos < a.max_seq ? pos : 0) * D;
+  if (FROM_PART) {
+    const int ncols = (a.H + 2 * a.Hkv) * D;
+    const uint16_t* cr = a.cos_tab + prow;
+    const uint16_t* sr = a.sin_tab + prow;
+    if (has_pos && wave < 2) {
+      float x0, x1;
+      head_from_partials(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh,
+                         lane, x0, x1);
+      if (wave == 0) norm_rope_pair(x0, x1, a.kn, cr, sr, lane, a.eps, x0, x1);
+      const uint32_t b0 = f32_to_bf16(x0), b1 = f32_to_bf16(x1);
+      uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.max_seq + pos) * D;
+      dst[lane] = (uint16_t)b0;
+      dst[lane + 64] = (uint16_t)b1;
+      uint16_t* l16 = reinterpret_cast<uint16_t*>(wave == 0 ? kpos : vpos);
+      l16[lane] = (uint16_t)b0;
+      l16[lane + 64] = (uint16_t)b1;
+    }
+    for (int hr = wave; hr < n_rep; hr += 4) {
+      float x0, x1;
+      head_from_partials(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, x0, x1);
+      norm_rope_pair(x0, x1, a.qn, cr, sr, lane, a.eps, x0, x1);
+      uint16_t* l16 = reinterpret_cast<uint16_t*>(q_lds[hr]);
+      l16[lane] = (uint16_t)f32_to_bf16(x0);
+      l16[lane + 64] = (uint16_t)f32_to_bf16(x1);
+    }
+  } else {
+    for (int hr = wave; hr < n_rep; hr += 4)
+      if (lane < 16)
+        q_lds[hr][lane] =
+            reinterpret_cast<const u32x4*>(a.q + (size_t)(kvh * n_rep + hr) * D)[lane];
+    if (has_pos && wave < 2 && lane < 16)   // the cache already holds k/v of pos
+      (wave == 0 ? kpos : vpos)[lane] =
+          reinterpret_cast<const u32x4*>((wave == 0 ? kbase : vbase) + (size_t)pos * D)[lane];
   }
   __syncthreads();
-  for (int hr = wave; hr < n_rep; hr += nw) {
+
+  // 3. Scores, softmax and the value sum, one 64-position block at a time.
+  for (int hr = wave; hr < n_rep; hr += 4) {
     const int h = kvh * n_rep + hr;
-    uint32_t qv[64];
+    float m = -INFINITY, l = 0.f;
+    float o[8];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) qv[i] = q_lds[hr & 3][i];
-    float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int base = p0; base < p1; base += 64) {
+    for (int j = 0; j < 8; ++j) o[j] = 0.f;
+    for (int base = p0; base < p1; base += kAttnBlock) {
+      if (base != p0 || hr != wave) load_block(base);
       const int p = base + lane;
-      float s = -INFINITY;
-      if (p < p1) {
-        float acc = 0.f;
-        if (p == pos) {
+      float acc = 0.f;
+      if (p == pos) {
 #pragma unroll
-          for (int i = 0; i < 64; ++i) acc = dot2_bf16(kpos[i], qv[i], acc);
-        } else {
-          const u32x4* kr = reinterpret_cast<const u32x4*>(kbase + (size_t)p * D);
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const u32x4 kk = kr[i];
-            acc = dot2_bf16(kk.x, qv[4 * i + 0], acc);
-            acc = dot2_bf16(kk.y, qv[4 * i + 1], acc);
-            acc = dot2_bf16(kk.z, qv[4 * i + 2], acc);
-            acc = dot2_bf16(kk.w, qv[4 * i + 3], acc);
-          }
-        }
-        s = acc * scale;
+        for (int i = 0; i < 16; ++i) kr[i] = kpos[i];
       }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const u32x4 qq = q_lds[hr][i];
+        acc = dot2_bf16(kr[i].x, qq.x, acc);
+        acc = dot2_bf16(kr[i].y, qq.y, acc);
+        acc = dot2_bf16(kr[i].z, qq.z, acc);
+        acc = dot2_bf16(kr[i].w, qq.w, acc);
+      }
+      const float s = p < p1 ? acc * a.scale : -INFINITY;
       const float mn = fmaxf(m, wave_max(s));
-      const float e = (p < p1) ? expf(s - mn) : 0.f;
+      const float e = p < p1 ? expf(s - mn) : 0.f;
       const float corr = expf(m - mn);
       l = fmaf(l, corr, wave_sum(e));
-      o0 *= corr;
-      o1 *= corr;
-      const int cnt = p1 - base < 64 ? p1 - base : 64;
-      const uint32_t* vr = reinterpret_cast<const uint32_t*>(vbase + (size_t)base * D) + lane;
-#pragma unroll 16
-      for (int j = 0; j < cnt; ++j) {
-        const float ej = __shfl(e, j);
-        const uint32_t vv = (base + j == pos) ? vpos[lane] : vr[(size_t)j * (D / 2)];
-        o0 = fmaf(ej, lo_bf(vv), o0);
-        o1 = fmaf(ej, hi_bf(vv), o1);
-      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] *= corr;
       m = mn;
+      e_lds[wave][(lane & 3) * 16 + (lane >> 2)] = e;   // position ps+4i at ps*16+i
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float ei = e_lds[wave][ps * 16 + i];
+        const u32x4 v = (base + ps + 4 * i == pos) ? vpos[dg] : vr[i];
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          o[2 * j] = fmaf(ei, lo_bf(w4[j]), o[2 * j]);
+          o[2 * j + 1] = fmaf(ei, hi_bf(w4[j]), o[2 * j + 1]);
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    float* ph = part + ((size_t)h * kAttnChunks + c) * kAttnPart;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[j] += __shfl_xor(o[j], 16);
+      o[j] += __shfl_xor(o[j], 32);
+    }
+    // publish (m, l, o) with agent-scope stores: visible to the merging workgroup on
+    // any XCD without a whole-L2 writeback
+    float* ph = a.part + ((size_t)h * kAttnMaxChunks + c) * kAttnPart;
     if (lane == 0) {
-      ph[0] = m;
-      ph[1] = l;
+      __hip_atomic_store(ph, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ph + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    ph[4 + 2 * lane] = o0;
-    ph[5 + 2 * lane] = o1;
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        __hip_atomic_store(ph + 4 + 8 * dg + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-}
 
-__global__ void __launch_bounds__(128) attn_combine_kernel(const float* __restrict__ part,
-                                                           uint16_t* __restrict__ out,
-                                                           const int32_t* __restrict__ out_index) {
-  const int h = blockIdx.x, t = threadIdx.x;
-  const float* ph = part + (size_t)h * kAttnChunks * kAttnPart;
-  float mc[kAttnChunks], lc[kAttnChunks], oc[kAttnChunks];
-#pragma unroll
-  for (int c = 0; c < kAttnChunks; ++c) {   // every load issued before any use
-    mc[c] = ph[c * kAttnPart];
-    lc[c] = ph[c * kAttnPart + 1];
-    oc[c] = ph[c * kAttnPart + 4 + t];
-  }
-  float M = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < kAttnChunks; ++c)
-    if (lc[c] > 0.f) M = fmaxf(M, mc[c]);
-  float Ls = 0.f, o = 0.f;
-#pragma unroll
-  for (int c = 0; c < kAttnChunks; ++c)
-    if (lc[c] > 0.f) {
-      const float wgt = expf(mc[c] - M);
-      Ls = fmaf(wgt, lc[c], Ls);
-      o = fmaf(wgt, oc[c], o);
+  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order.
+  __builtin_amdgcn_s_waitcnt(0);      // every partial store acknowledged before the count
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nch - 1);
+  __syncthreads();
+  if (!last_flag) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&a.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int hr = wave; hr < n_rep; hr += 4) {
+    const int h = kvh * n_rep + hr;
+    const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
+    float mc = -INFINITY, lc = 0.f;
+    if (lane < nch) {
+      mc = __hip_atomic_load(ph + (size_t)lane * kAttnPart, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      lc = __hip_atomic_load(ph + (size_t)lane * kAttnPart + 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     }
-  const int i = h * 128 + t;
-  out[out_index ? out_index[i] : i] = (uint16_t)f32_to_bf16(Ls > 0.f ? o / Ls : 0.f);
+    const float M = wave_max(lc > 0.f ? mc : -INFINITY);
+    const float wc = lc > 0.f ? expf(mc - M) : 0.f;
+    const float Ls = wave_sum(wc * lc);
+    w_lds[wave][lane] = wc;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float o0 = 0.f, o1 = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      float v0[16], v1[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int cc = c0 + j < nch ? c0 + j : nch - 1;
+        const float* src = ph + (size_t)cc * kAttnPart + 4 + 2 * lane;
+        v0[j] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v1[j] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (c0 + j < nch) {
+          const float wj = w_lds[wave][c0 + j];
+          o0 = fmaf(wj, v0[j], o0);
+          o1 = fmaf(wj, v1[j], o1);
+        }
+    }
+    const int i0 = h * D + 2 * lane;
+    const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
+    a.out[a.out_index ? a.out_index[i0] : i0] = (uint16_t)f32_to_bf16(r0);
+    a.out[a.out_index ? a.out_index[i0 + 1] : i0 + 1] = (uint16_t)f32_to_bf16(r1);
+  }
 }
 
 // ----------------------------------------------------------------------------------
@@ -749,7 +785,33 @@ int mtl_residual_rmsnorm(const float* partials, int32_t splits, const void* resi
 
 int64_t mtl_decode_attention_workspace_bytes(int32_t n_heads, int32_t head_dim) {
   if (n_heads < 1 || head_dim != 128) return 0;
-  return (int64_t)n_heads * kAttnChunks * kAttnPart * 4;
+  return kAttnCounterBytes + (int64_t)n_heads * kAttnMaxChunks * kAttnPart * 4;
+}
+
+static int attn_check(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                      void* workspace, int64_t ws_bytes, const void* k_cache,
+                      const void* v_cache) {
+  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
+  if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 ||
+      n_heads / n_kv_heads > kAttnMaxRep || n_kv_heads * 4 > kAttnCounterBytes ||
+      max_seq < 1 || max_seq > (1 << 24))
+    return MTL_ERR_SHAPE;
+  if (!workspace || ws_bytes < mtl_decode_attention_workspace_bytes(n_heads, head_dim))
+    return MTL_ERR_WORKSPACE;
+  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(workspace)) return MTL_ERR_ALIGN;
+  return MTL_OK;
+}
+
+static void attn_launch(AttnArgs& a, void* workspace, bool from_part, hipStream_t s) {
+  a.counters = static_cast<uint32_t*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kAttnCounterBytes);
+  int64_t ch = (a.max_seq + kAttnBlock - 1) / kAttnBlock;
+  if (ch > kAttnMaxChunks) ch = kAttnMaxChunks;
+  const dim3 grid(a.Hkv, (unsigned)ch);
+  if (from_part)
+    hipLaunchKernelGGL(attn_decode_kernel<true>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(attn_decode_kernel<false>, grid, dim3(256), 0, s, a);
 }
 
 int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
@@ -757,20 +819,22 @@ int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache
                          int32_t n_kv_heads, int32_t head_dim, int64_t max_seq, float scale,
                          void* workspace, int64_t ws_bytes, void* stream) {
   if (!q || !k_cache || !v_cache || !pos || !out) return MTL_ERR_INVALID_ARG;
-  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
-  if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 || max_seq < 1 ||
-      max_seq > (1 << 24))
-    return MTL_ERR_SHAPE;
-  if (!workspace || ws_bytes < mtl_decode_attention_workspace_bytes(n_heads, head_dim))
-    return MTL_ERR_WORKSPACE;
-  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(q)) return MTL_ERR_ALIGN;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(n_kv_heads, kAttnChunks), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k_cache),
-                     static_cast<const uint16_t*>(v_cache), pos, static_cast<float*>(workspace),
-                     n_heads, n_kv_heads, max_seq, scale);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(128), 0, s,
-                     static_cast<const float*>(workspace), static_cast<uint16_t*>(out), out_index);
+  const int st = attn_check(n_heads, n_kv_heads, head_dim, max_seq, workspace, ws_bytes, k_cache,
+                            v_cache);
+  if (st != MTL_OK) return st;
+  if (!aligned16(q)) return MTL_ERR_ALIGN;
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.kc = const_cast<uint16_t*>(static_cast<const uint16_t*>(k_cache));
+  a.vc = const_cast<uint16_t*>(static_cast<const uint16_t*>(v_cache));
+  a.pos = pos;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_index = out_index;
+  a.H = n_heads;
+  a.Hkv = n_kv_heads;
+  a.max_seq = max_seq;
+  a.scale = scale;
+  attn_launch(a, workspace, false, (hipStream_t)stream);
   return launch_status();
 }
 
@@ -819,22 +883,28 @@ int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const 
   if (!qkv_partials || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !k_cache || !v_cache ||
       !pos || !out)
     return MTL_ERR_INVALID_ARG;
-  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
-  if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 4 ||
-      max_seq < 1 || max_seq > (1 << 24) || splits < 1)
-    return MTL_ERR_SHAPE;
-  if (!workspace || ws_bytes < mtl_decode_attention_workspace_bytes(n_heads, head_dim))
-    return MTL_ERR_WORKSPACE;
-  if (!aligned16(k_cache) || !aligned16(v_cache)) return MTL_ERR_ALIGN;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(attn_fused_kernel, dim3(n_kv_heads, kAttnChunks), dim3(256), 0, s,
-                     qkv_partials, splits, static_cast<const uint16_t*>(q_norm_w),
-                     static_cast<const uint16_t*>(k_norm_w), static_cast<const uint16_t*>(cos_tab),
-                     static_cast<const uint16_t*>(sin_tab), static_cast<uint16_t*>(k_cache),
-                     static_cast<uint16_t*>(v_cache), pos, static_cast<float*>(workspace), n_heads,
-                     n_kv_heads, max_seq, scale, eps);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(128), 0, s,
-                     static_cast<const float*>(workspace), static_cast<uint16_t*>(out), out_index);
+  const int st = attn_check(n_heads, n_kv_heads, head_dim, max_seq, workspace, ws_bytes, k_cache,
+                            v_cache);
+  if (st != MTL_OK) return st;
+  if (splits < 1) return MTL_ERR_SHAPE;
+  AttnArgs a{};
+  a.qkv_part = qkv_partials;
+  a.splits = splits;
+  a.qn = static_cast<const uint16_t*>(q_norm_w);
+  a.kn = static_cast<const uint16_t*>(k_norm_w);
+  a.cos_tab = static_cast<const uint16_t*>(cos_tab);
+  a.sin_tab = static_cast<const uint16_t*>(sin_tab);
+  a.kc = static_cast<uint16_t*>(k_cache);
+  a.vc = static_cast<uint16_t*>(v_cache);
+  a.pos = pos;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_index = out_index;
+  a.H = n_heads;
+  a.Hkv = n_kv_heads;
+  a.max_seq = max_seq;
+  a.scale = scale;
+  a.eps = eps;
+  attn_launch(a, workspace, true, (hipStream_t)stream);
   return launch_status();
 }
 

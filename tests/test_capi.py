@@ -100,7 +100,7 @@ def test_decode_entry_validation(lib):
                                    64, eps, None) == N.MTL_ERR_UNSUPPORTED
     assert lib.mtl_qk_norm_rope_kv(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 6, 128,
                                    64, eps, None) == N.MTL_ERR_SHAPE
-    assert lib.mtl_decode_attention_workspace_bytes(32, 128) == 32 * 16 * 132 * 4
+    assert lib.mtl_decode_attention_workspace_bytes(32, 128) == 1024 + 32 * 64 * 132 * 4
     assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, None, 32, 8, 128, 2048,
                                     C.c_float(0.1), None, 0, None) == N.MTL_ERR_WORKSPACE
     assert lib.mtl_residual_rmsnorm(None, 0, FAKE, FAKE, FAKE, FAKE, None, 4098, eps,

@@ -121,25 +121,31 @@ def test_qk_norm_rope_kv_kernel(dev, lib):
     assert not kc2.any()
 
 
-@pytest.mark.parametrize("length", [1, 2, 16, 63, 64, 65, 1000, 2049])
-def test_decode_attention_kernel(dev, lib, length):
+@pytest.mark.parametrize("length,S", [(1, 2112), (2, 2112), (16, 2112), (63, 2112), (64, 2112),
+                                      (65, 2112), (1000, 2112), (2049, 2112), (4096, 4096),
+                                      (5000, 8192), (8192, 8192)])
+def test_decode_attention_kernel(dev, lib, length, S):
+    # lengths past 4096 take the multi-block path (64 chunks of more than 64 positions);
+    # the second launch reuses the workspace, whose merge counters must be back at zero
     r = np.random.default_rng(length)
-    H, Hkv, S = 32, 8, 2112
+    H, Hkv = 32, 8
     kc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
     vc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
     q = round_bf16(r.standard_normal((H, 128)).astype(np.float32))
     tk, tv, tq = tb(kc, dev), tb(vc, dev), tb(q, dev)
     out = torch.empty(H * 128, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(int(lib.mtl_decode_attention_workspace_bytes(H, 128)), dtype=torch.uint8, device=dev)
-    tpos = torch.tensor([length - 1], dtype=torch.int64, device=dev)
+    ws = torch.zeros(int(lib.mtl_decode_attention_workspace_bytes(H, 128)), dtype=torch.uint8, device=dev)
     scale = 1 / np.sqrt(128)
-    N.check(lib.mtl_decode_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tpos.data_ptr(),
-                                     out.data_ptr(), None, H, Hkv, 128, S, ctypes.c_float(scale),
-                                     ws.data_ptr(), ws.numel(), stream()), "attention")
-    ref = D.attention(q, kc[:, :length], vc[:, :length], scale)
-    err = rel_l2(fb(out).reshape(H, 128), ref)
-    print(f"attention L={length} rel_l2={err:.2e}")
-    assert err < 1e-2
+    for n in (length, length // 2 + 1):
+        tpos = torch.tensor([n - 1], dtype=torch.int64, device=dev)
+        N.check(lib.mtl_decode_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tpos.data_ptr(),
+                                         out.data_ptr(), None, H, Hkv, 128, S, ctypes.c_float(scale),
+                                         ws.data_ptr(), ws.numel(), stream()), "attention")
+        ref = D.attention(q, kc[:, :n], vc[:, :n], scale)
+        err = rel_l2(fb(out).reshape(H, 128), ref)
+        print(f"attention L={n} rel_l2={err:.2e}")
+        assert err < 1e-2
+    assert not ws[:1024].any()           # merge counters left at zero
 
 
 def test_head_gemv_argmax(dev, lib):
