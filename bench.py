@@ -32,6 +32,9 @@ GEMV_SHAPES = (("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576),
 GROUP = 128
 
 
+COPY_BYTES = 256 << 20
+
+
 def algo_bytes(m: int, k: int, n: int, g: int, act_order: bool) -> int:
     """Algorithmic HBM bytes of one int4 GEMM launch (AutoGPTQ layout)."""
     return (n * k // 2 + 2 * n * k // g + n * k // (2 * g) + (4 * k if act_order else 0)
@@ -272,6 +275,32 @@ def bench_decode(args, torch):
     )
 
 
+def bench_kernels(args, torch):
+    """Counter-collection workload: a plain 256 MiB device copy (the calibration kernel
+    for the FETCH_SIZE / WRITE_SIZE counters), then each int4 GEMV of the decode step
+    exactly as the captured plan launches it, over the model's 36 layers, --steps times."""
+    from moss_tts_lite_amd.fast import FastDecoder
+    from moss_tts_lite_amd.model import BackboneConfig, Int4Backbone, random_weights
+
+    dev = torch.device("cuda:0")
+    cfg = BackboneConfig(max_seq=1536)
+    model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev), dev)
+    dec = FastDecoder(model)
+    dec.prefill(torch.randint(0, cfg.vocab, (16,), generator=torch.Generator().manual_seed(1)))
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for name in ("gate_up", "down", "qkv", "o"):
+        for i in range(args.steps):
+            dec.run_gemv(i % cfg.n_layers, name)
+        torch.cuda.synchronize()
+    print(json.dumps({"workload": "kernels", "copy_bytes": COPY_BYTES,
+                      "gemv_launches_each": args.steps}))
+
+
 def cpu_baseline_decode(budget_s: float = 20.0):
     """The oracle's restatement of the reference CPU path (dequantise each layer's
     weights, float64 products, the step's bf16 rounding) on one full-size layer plus the
@@ -336,7 +365,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -348,6 +377,10 @@ def main():
     import __graft_entry__
 
     pkg = __graft_entry__.import_package()
+    if args.workload == "kernels":
+        args.steps = 72 if args.steps is None else args.steps
+        bench_kernels(args, torch)
+        return
     if args.workload == "decode":
         args.warmup = 16 if args.warmup is None else args.warmup
         args.steps = 1024 - args.warmup if args.steps is None else args.steps

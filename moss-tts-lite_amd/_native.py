@@ -76,7 +76,6 @@ _SIGNATURES = {
     "mtl_w4_gemm_norm_partials": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                          _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32,
                                          _c_void_p, _i64, _c_void_p]),
-    "mtl_tune_set_waves": (_i32, [_i32]),
     "mtl_tune_set_reduce": (_i32, [_i32]),
 }
 

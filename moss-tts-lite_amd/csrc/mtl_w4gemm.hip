@@ -8,19 +8,23 @@
 // written as w = (q - c) * s + d.  Since (q - c) * s is exact in fp32, both equal the
 // exact dequantised weight.
 //
-// Work decomposition (deterministic, no atomics):
-//   * a wave owns a 256-column tile (64 lanes x 4 columns = one 16-byte qweight load per
-//     lane per row, 1 KB contiguous per wave) and 16 qweight rows (128 input channels);
-//     it issues all 16 loads up front, so the whole weight slice of the chip is in flight;
-//   * a workgroup stacks 1, 2 or 4 waves along K and reduces them through LDS;
-//   * blockIdx.y splits K further; each workgroup publishes an fp32 partial tile and
-//     the last workgroup of the tile (agent-scope counter) sums the splits in split
-//     order, applies the epilogue and resets the counter, so results (and graph
-//     replays) are bitwise repeatable and the next launch needs no memset.
+// Work decomposition (deterministic, no atomics on the data):
+//   * a workgroup owns a 256-column tile and one split of 512 input channels; its 4
+//     waves sit side by side along N (64 columns each) and share the LDS copy of x;
+//   * per 32-channel row quad, lane l issues one 16-byte buffer load: qweight row
+//     4q + l/16, columns 4*(l%16)..+3 -- exactly the B operand of
+//     v_mfma_f32_16x16x32_bf16 for those 4 columns.  All 16 loads of a lane are in
+//     flight before the first wait;
+//   * blockIdx.y splits K; each workgroup publishes an fp32 partial tile and the last
+//     workgroup of the tile (agent-scope counter) sums the splits in split order,
+//     applies the epilogue and resets the counter, so results (and graph replays) are
+//     bitwise repeatable and the next launch needs no memset.  Fused consumers may
+//     instead read the partial tiles themselves.
 //
 // Inner loop: a qweight word holds 8 codes; OR-ing nibble pairs into 0x4300 gives the
-// bf16 pair (128 + q_j, 128 + q_{j+4}), and x is staged in LDS in the same pair order,
-// so 7 integer ops + 4 v_dot2c_f32_bf16 handle 8 MACs.  Per group (g/8 rows) the
+// bf16 pair (128 + q_j, 128 + q_{j+4}) (one v_and_or_b32 each), so one word is the 8-value
+// B fragment of an MFMA whose A fragment is x staged in LDS in the same pair order (all
+// 16 A rows = x for M = 1, one row per x row otherwise).  Per group (g/32 quads) the
 // accumulated sum A = sum x*(128+q) and X = sum x give
 //     sum x*w = s * (A - (128 + c) * X) + d * X.
 #include "mtl_common.h"
@@ -30,9 +34,10 @@ namespace mtl {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTileN = 256;        // output columns per wave tile
-constexpr int kRowsPerWave = 16;   // qweight rows (x 8 input channels) per wave
-constexpr int kMaxWaves = 4;       // waves stacked along K in one workgroup
+constexpr int kTileN = 256;        // output columns per workgroup (4 waves)
+constexpr int kWaveN = 64;         // output columns per wave (16 lanes x 4)
+constexpr int kRowQuads = 16;      // qweight row quads (4 rows = 32 channels) per split
+constexpr int kRowsPerWG = 4 * kRowQuads;   // qweight rows per split: 512 input channels
 constexpr int kMaxM = 16;
 // Cache policy of the weight stream (read once per step): non-temporal.
 constexpr int kStreamAux = 2;
@@ -58,14 +63,6 @@ struct W4Args {
   int M, K, N, group, zero_offset, splits, epilogue, out_f32;
 };
 
-// (a & m) | o in one VALU op; the constants live in registers because gfx9 VOP3
-// encodings take no literal.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-  return r;
-}
-
 __device__ __forceinline__ float4 ld_f4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
@@ -90,51 +87,98 @@ enum : int {
 
 constexpr int kNormSlots = 16;   // sums of squares published by the residual kernel
 
-template <int MR, int RPG, int FMT, int XSRC>
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// The 8 codes of one qweight word as the bf16 MFMA operand (128+q_j, 128+q_{j+4}),
+// j = 0..3: one v_and_or_b32 per pair (plus a shift for j > 0).
+// Plain integer code (not the inline-asm and_or): the compiler must see these VALU
+// writes to insert the wait states an MFMA operand read needs after them.  `lo` and
+// `magic` are held in VGPRs (vgpr_const), so each pair selects to one v_and_or_b32.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+  return r;
+}
+
+__device__ __forceinline__ bf16x8_t unpack_codes8(uint32_t w, uint32_t lo, uint32_t magic) {
+  const u32x4 p{(w & lo) | magic, ((w >> 4) & lo) | magic, ((w >> 8) & lo) | magic,
+                ((w >> 12) & lo) | magic};
+  return __builtin_bit_cast(bf16x8_t, p);
+}
+
+// x item (8 channels) in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7), and its sum.
+__device__ __forceinline__ u32x4 pair_order(u32x4 v, float& sum) {
+  const uint32_t e0 = v.x & 0xffffu, e1 = v.x >> 16, e2 = v.y & 0xffffu, e3 = v.y >> 16;
+  const uint32_t e4 = v.z & 0xffffu, e5 = v.z >> 16, e6 = v.w & 0xffffu, e7 = v.w >> 16;
+  sum = ((bf16_to_f32(e0) + bf16_to_f32(e1)) + (bf16_to_f32(e2) + bf16_to_f32(e3))) +
+        ((bf16_to_f32(e4) + bf16_to_f32(e5)) + (bf16_to_f32(e6) + bf16_to_f32(e7)));
+  return u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
+}
+
+// x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40).
+__device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
+  const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t lo = f32_to_bf16(round_bf16(
+        bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * r)));
+    const uint32_t hi = f32_to_bf16(round_bf16(
+        bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * r)));
+    o[c] = lo | (hi << 16);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// The int4 GEMV / skinny GEMM.  Workgroup = 4 waves side by side along N (64 columns
+// each: lane l owns columns 4*(l%16)..+3) over one split of 512 input channels (64
+// qweight rows = 16 row quads).  Per row quad, lane l loads the 16-byte word group of
+// qweight row 4q + l/16, i.e. exactly the B operand of v_mfma_f32_16x16x32_bf16 for
+// its 4 columns; the A operand is x (row m = l%16, or row 0 broadcast when MR = 1).
+// GR = row quads per quantisation group (group / 32).
+template <int MR, int GR, int FMT, int XSRC>
 __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
-  constexpr bool PERM = XSRC == XSRC_PERM || XSRC == XSRC_SILU_PART;   // x staged after weights
-  constexpr int RB = kRowsPerWave;
-  constexpr int NCH = RB / RPG;            // metadata chunks per wave
-  constexpr int XIT = (MR * RB + 63) / 64; // x staging items per lane
-  __shared__ u32x4 xs[kMaxWaves][MR][RB];
-  __shared__ float xsum[kMaxWaves][MR][RB];
-  __shared__ float4 red[kMaxWaves][MR][64];
+  constexpr bool LATE_X = XSRC == XSRC_PERM;  // the gather needs perm: x after the weights
+  constexpr int NG = kRowQuads / GR;          // groups per split
+  constexpr int GI = 4 * GR;                  // x items (8 channels) per group
+  constexpr int XPT = MR == 1 ? 1 : 4;        // staging items per thread
+  __shared__ u32x4 xa[MR][kRowsPerWG];        // x in pair order, one item per qweight row
+  __shared__ float xg[MR][NG];                // per-group sums of x
+  __shared__ float ytile[MR][kTileN];         // workgroup result, for the epilogue mapping
+  __shared__ uint32_t xn[XSRC == XSRC_SILU_PART ? kRowsPerWG : 1][4];   // SiLU*up items
 
-  const int nw = blockDim.x >> 6;
   const int wave = wave_id();
-  const int lane = threadIdx.x & 63;
-  const int tile = blockIdx.x;
-  const int split = blockIdx.y;
-  const int N = a.N;
-  const int M = a.M;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int lg = lane >> 4, lj = lane & 15;
+  const int tile = blockIdx.x, split = blockIdx.y;
+  const int N = a.N, M = a.M;
   const int rows_total = a.K >> 3;
-  const int wrow0 = __builtin_amdgcn_readfirstlane((split * nw + wave) * RB);
-  const int col0 = tile * kTileN + lane * 4;
-  const bool col_ok = col0 < N;
+  const int row0 = split * kRowsPerWG;
+  const int col = tile * kTileN + wave * kWaveN + 4 * lj;
+  const bool col_ok = col < N;
 
-  // Loads below are branch-free so the waitcnt pass can count them exactly: rows past
-  // K/8 are clamped to the last row (their x is staged as 0, so they add exactly 0) and
-  // columns past N read 0 through the buffer range check.
-  const int rows_last = rows_total - 1;
-
-  // 1. x for this wave's rows.  Without act-order these loads go first, so the LDS
-  //    staging waits only on them; with act-order the gather needs the index first, so
-  //    it is issued after the weight stream and overlaps it instead.
-  u32x4 xv[XIT];
-  bool xok[XIT];
-  u32x4 wv[XSRC == XSRC_RMSNORM ? XIT : 1];
+  // 1. x items this thread stages: (m, i) = (t/64 + 4j, t%64) for MR = 16, (0, t) for
+  //    MR = 1 (threads 0..63).  Raw values now; transformed once the loads are back.
+  u32x4 xv[XPT], wv[XSRC == XSRC_RMSNORM ? XPT : 1];
+  bool xok[XPT];
   float4 slot4[XSRC == XSRC_RMSNORM ? kNormSlots / 4 : 1];
+  const bool stager = MR > 1 || t < kRowsPerWG;
   auto load_x = [&]() {
 #pragma unroll
-    for (int it = 0; it < XIT; ++it) {
-      const int item = lane + 64 * it;
-      const int m = item / RB;
-      const int row = wrow0 + (item % RB);
-      const bool ok = item < MR * RB && m < M && row < rows_total;
-      const size_t xoff = (size_t)(m < M ? m : M - 1) * a.K;
-      const int rc = row < rows_total ? row : rows_last;
-      u32x4 v;
-      if (XSRC == XSRC_PERM) {
+    for (int j = 0; j < XPT; ++j) {
+      const int m = MR == 1 ? 0 : (t >> 6) + 4 * j;
+      const int i = MR == 1 ? t : (t & 63);
+      const int row = row0 + (i < kRowsPerWG ? i : 0);
+      xok[j] = stager && m < M && row < rows_total;
+      const int rc = row < rows_total ? row : rows_total - 1;
+      const int mc = m < M ? m : M - 1;
+      const size_t xoff = (size_t)mc * a.K;
+      u32x4 v{0u, 0u, 0u, 0u};
+      if (!stager) {
+      } else if (XSRC == XSRC_PERM) {
         const u32x4 p0 = *reinterpret_cast<const u32x4*>(a.perm + rc * 8);
         const u32x4 p1 = *reinterpret_cast<const u32x4*>(a.perm + rc * 8 + 4);
         const uint32_t e0 = a.x[xoff + p0.x], e1 = a.x[xoff + p0.y];
@@ -143,177 +187,148 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
         const uint32_t e6 = a.x[xoff + p1.z], e7 = a.x[xoff + p1.w];
         v = u32x4{e0 | (e1 << 16), e2 | (e3 << 16), e4 | (e5 << 16), e6 | (e7 << 16)};
       } else if (XSRC == XSRC_SILU_PART) {
-        // channels 8rc..8rc+7 of the intermediate; their gate columns are contiguous in
-        // the 32-column interleave and the up columns sit 32 to the right.
-        const int j0 = rc * 8;
-        const float* pb = a.xpart + (size_t)(m < M ? m : M - 1) * a.xpart_ld +
-                          64 * (j0 >> 5) + (j0 & 31);
-        const size_t ss = (size_t)M * a.xpart_ld;
-        float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < a.xsplits; s0 += 8) {   // 32 loads in flight, summed in order
-          float4 G[8][2], U[8][2];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int sp = s0 + j < a.xsplits ? s0 + j : a.xsplits - 1;
-            const float* q = pb + sp * ss;
-            G[j][0] = ld_f4(q); G[j][1] = ld_f4(q + 4);
-            U[j][0] = ld_f4(q + 32); U[j][1] = ld_f4(q + 36);
-          }
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (s0 + j < a.xsplits) {
-              g[0] += G[j][0].x; g[1] += G[j][0].y; g[2] += G[j][0].z; g[3] += G[j][0].w;
-              g[4] += G[j][1].x; g[5] += G[j][1].y; g[6] += G[j][1].z; g[7] += G[j][1].w;
-              u[0] += U[j][0].x; u[1] += U[j][0].y; u[2] += U[j][0].z; u[3] += U[j][0].w;
-              u[4] += U[j][1].x; u[5] += U[j][1].y; u[6] += U[j][1].z; u[7] += U[j][1].w;
-            }
-        }
-        v = u32x4{silu_mul_bf16(g[0], u[0]) | (silu_mul_bf16(g[1], u[1]) << 16),
-                  silu_mul_bf16(g[2], u[2]) | (silu_mul_bf16(g[3], u[3]) << 16),
-                  silu_mul_bf16(g[4], u[4]) | (silu_mul_bf16(g[5], u[5]) << 16),
-                  silu_mul_bf16(g[6], u[6]) | (silu_mul_bf16(g[7], u[7]) << 16)};
-      } else if (XSRC == XSRC_RMSNORM) {   // raw h now, normalised once the scale is known
+        // staged four threads per item below
+      } else if (XSRC == XSRC_RMSNORM) {
         v = *reinterpret_cast<const u32x4*>(a.hn + rc * 8);
-        wv[it] = *reinterpret_cast<const u32x4*>(a.wn + rc * 8);
+        wv[j] = *reinterpret_cast<const u32x4*>(a.wn + rc * 8);
       } else {
         v = *reinterpret_cast<const u32x4*>(a.x + xoff + rc * 8);
       }
-      xv[it] = v;     // masked after the weight stream is issued (step 4)
-      xok[it] = ok;
+      xv[j] = v;
     }
   };
-  if (!PERM) load_x();
+  if (!LATE_X) load_x();
+  // SiLU(gate)*up staging (M = 1): thread t computes channels 2*(t%4), +1 of item t/4
+  // from the gate|up split-K partials (gate columns contiguous in the 32-column
+  // interleave, up columns 32 to the right), summing the splits in order.  The first 8
+  // splits are loaded here, ahead of the weight stream.
+  const int s_row = row0 + (t >> 2);
+  const float* s_pb = nullptr;
+  float2 sG[XSRC == XSRC_SILU_PART ? 8 : 1], sU[XSRC == XSRC_SILU_PART ? 8 : 1];
+  auto silu_batch = [&](int s0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int sp = s0 + q < a.xsplits ? s0 + q : a.xsplits - 1;
+      sG[q] = *reinterpret_cast<const float2*>(s_pb + (size_t)sp * a.xpart_ld);
+      sU[q] = *reinterpret_cast<const float2*>(s_pb + (size_t)sp * a.xpart_ld + 32);
+    }
+  };
+  if (XSRC == XSRC_SILU_PART) {
+    const int j0 = (s_row < rows_total ? s_row : rows_total - 1) * 8;
+    s_pb = a.xpart + 64 * (j0 >> 5) + (j0 & 31) + 2 * (t & 3);
+    silu_batch(0);
+  }
   if (XSRC == XSRC_RMSNORM) {
 #pragma unroll
     for (int i = 0; i < kNormSlots / 4; ++i) slot4[i] = ld_f4(a.slots + 4 * i);
   }
 
-  // 2. Group metadata of the lane's 4 columns, one entry per RPG-row chunk.
-  const int colc = col_ok ? col0 : N - 4;
-  u32x4 meta[NCH];
+  // 2. Group metadata of the lane's 4 columns, one entry per group of the split.
+  const int colc = col_ok ? col : N - 4;
+  const int ngroups = a.K / a.group;
+  u32x4 meta[NG];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int row = wrow0 + c * RPG;
-    const int grp = ((row < rows_total ? row : rows_last) * 8) / a.group;
+  for (int g = 0; g < NG; ++g) {
+    int grp = (row0 * 8) / a.group + g;
+    grp = grp < ngroups ? grp : ngroups - 1;
     if (FMT == MTL_META_QSZ) {
-      meta[c] = *reinterpret_cast<const u32x4*>(a.meta0 + ((size_t)grp * N + colc) * 2);
+      meta[g] = *reinterpret_cast<const u32x4*>(a.meta0 + ((size_t)grp * N + colc) * 2);
     } else {
       const u32x2 s = *reinterpret_cast<const u32x2*>(a.meta0 + (size_t)grp * N + colc);
       const uint32_t zw = a.qzeros[(size_t)grp * (N >> 3) + (colc >> 3)];
-      meta[c] = u32x4{s.x, s.y, zw >> ((colc & 7) * 4), 0u};
+      meta[g] = u32x4{s.x, s.y, zw >> ((colc & 7) * 4), 0u};
     }
   }
 
-  // 3. Stream the weight slice: RB independent 16-byte buffer loads per lane with a
-  //    scalar row offset.
+  // 3. The weight stream: 16 independent 16-byte buffer loads per lane, uniform row
+  //    offset per quad; rows past K/8 and columns past N read 0 through the range check.
   const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.qweight), (short)0, (int)((int64_t)rows_total * N * 4), 0x00020000);
-  const int voff = col_ok ? col0 * 4 : 0x7ffffff0;
-  u32x4 wq[RB];
+  u32x4 wq[kRowQuads];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const int row = wrow0 + r < rows_total ? wrow0 + r : rows_last;
-    wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          qrsrc, voff, row * N * 4, kStreamAux));
+  for (int q = 0; q < kRowQuads; ++q) {
+    const int row = row0 + 4 * q + lg;
+    const int voff = (col_ok && row < rows_total) ? (lg * N + col) * 4 : 0x7ffffff0;
+    wq[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          qrsrc, voff, (row0 + 4 * q) * N * 4, kStreamAux));
   }
 
-  if (PERM) load_x();
+  if (LATE_X) load_x();
   // Keep the scheduler from hoisting the uses of x above the weight stream: every load
   // of the wave is in flight before the first wait.
   __builtin_amdgcn_sched_barrier(0);
 
-  // 4. x into LDS in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7) with row sums.
-  float norm_r = 0.f;
-  if (XSRC == XSRC_RMSNORM) {   // RMSNorm scale: rsqrt(mean(h^2) + eps), slots summed in order
-    float ssum = 0.f;
+  // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
+  if (XSRC == XSRC_SILU_PART) {
+    float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+    for (int s0 = 0; s0 < a.xsplits; s0 += 8) {
+      if (s0 > 0) silu_batch(s0);
 #pragma unroll
-    for (int i = 0; i < kNormSlots / 4; ++i)
-      ssum += ((slot4[i].x + slot4[i].y) + (slot4[i].z + slot4[i].w));
-    norm_r = rsqrtf(ssum / (float)a.K + a.eps);
-  }
-#pragma unroll
-  for (int it = 0; it < XIT; ++it) {
-    const int item = lane + 64 * it;
-    if (item < MR * RB) {
-      u32x4 v = xv[it];
-      if (XSRC == XSRC_RMSNORM) {   // x = bf16(w * bf16(h * r)), model.py:34-40
-        const uint32_t hh[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t ww[4] = {wv[it].x, wv[it].y, wv[it].z, wv[it].w};
-        uint32_t o[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t lo = f32_to_bf16(round_bf16(
-              bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * norm_r)));
-          const uint32_t hi = f32_to_bf16(round_bf16(
-              bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * norm_r)));
-          o[c] = lo | (hi << 16);
+      for (int q = 0; q < 8; ++q)
+        if (s0 + q < a.xsplits) {
+          g0 += sG[q].x; g1 += sG[q].y;
+          u0 += sU[q].x; u1 += sU[q].y;
         }
-        v = u32x4{o[0], o[1], o[2], o[3]};
-      }
-      if (!xok[it]) v = u32x4{0u, 0u, 0u, 0u};
-      const uint32_t e0 = v.x & 0xffffu, e1 = v.x >> 16, e2 = v.y & 0xffffu, e3 = v.y >> 16;
-      const uint32_t e4 = v.z & 0xffffu, e5 = v.z >> 16, e6 = v.w & 0xffffu, e7 = v.w >> 16;
-      xs[wave][item / RB][item % RB] =
-          u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
-      xsum[wave][item / RB][item % RB] =
-          ((bf16_to_f32(e0) + bf16_to_f32(e1)) + (bf16_to_f32(e2) + bf16_to_f32(e3))) +
-          ((bf16_to_f32(e4) + bf16_to_f32(e5)) + (bf16_to_f32(e6) + bf16_to_f32(e7)));
     }
+    xn[t >> 2][t & 3] =
+        s_row < rows_total ? silu_mul_bf16(g0, u0) | (silu_mul_bf16(g1, u1) << 16) : 0u;
+    __syncthreads();
+    if (stager) xv[0] = u32x4{xn[t][0], xn[t][1], xn[t][2], xn[t][3]};
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  // 5. Dot products, one group chunk at a time.
-  float tot[MR][4];
+  if (stager) {
+    float norm_r = 0.f;
+    if (XSRC == XSRC_RMSNORM) {   // rsqrt(mean(h^2) + eps), slots summed in order
+      float ssum = 0.f;
 #pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) tot[m][c] = 0.f;
-
-  const uint32_t kMagic = __builtin_amdgcn_readfirstlane(0x43004300u);  // bf16 (128, 128)
-  const uint32_t kLo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-#pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) {
-    float acc[MR][4];
-    float X[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      X[m] = 0.f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] = 0.f;
+      for (int i = 0; i < kNormSlots / 4; ++i)
+        ssum += ((slot4[i].x + slot4[i].y) + (slot4[i].z + slot4[i].w));
+      norm_r = rsqrtf(ssum / (float)a.K + a.eps);
     }
 #pragma unroll
-    for (int rr = 0; rr < RPG; ++rr) {
-      const int r = ch * RPG + rr;
-      const uint32_t w[4] = {wq[r].x, wq[r].y, wq[r].z, wq[r].w};
-      uint32_t p[4][4];
+    for (int j = 0; j < XPT; ++j) {
+      const int m = MR == 1 ? 0 : (t >> 6) + 4 * j;
+      const int i = MR == 1 ? t : (t & 63);
+      u32x4 v = xv[j];
+      if (XSRC == XSRC_RMSNORM) v = rmsnorm8(v, wv[j], norm_r);
+      if (!xok[j]) v = u32x4{0u, 0u, 0u, 0u};
+      float s;
+      xa[m][i] = pair_order(v, s);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        p[c][0] = and_or(w[c], kLo, kMagic);
-        p[c][1] = and_or(w[c] >> 4, kLo, kMagic);
-        p[c][2] = and_or(w[c] >> 8, kLo, kMagic);
-        p[c][3] = and_or(w[c] >> 12, kLo, kMagic);
-      }
+      for (int o = 1; o < GI; o <<= 1) s += __shfl_xor(s, o);
+      if ((i & (GI - 1)) == 0) xg[m][i / GI] = s;
+    }
+  }
+  __syncthreads();
+
+  // 5. MFMA over the row quads, one quantisation group at a time; per group
+  //    y += s * (A - (128 + c) * X) (+ d * X for the qsz contract).
+  const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
+  const uint32_t kLo = vgpr_const(0x000F000Fu);
+  constexpr int NR = MR == 1 ? 1 : 4;         // result rows held per lane
+  float tot[4][NR];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const u32x4 xp = xs[wave][m][r];
-        X[m] += xsum[wave][m][r];
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          float t = acc[m][c];
-          t = dot2_bf16(p[c][0], xp.x, t);
-          t = dot2_bf16(p[c][1], xp.y, t);
-          t = dot2_bf16(p[c][2], xp.z, t);
-          t = dot2_bf16(p[c][3], xp.w, t);
-          acc[m][c] = t;
-        }
-      }
+    for (int r = 0; r < NR; ++r) tot[c][r] = 0.f;
+  const int am = MR == 1 ? 0 : lj;            // A operand row of this lane
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    floatx4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < GR; ++q) {
+      const int rq = g * GR + q;
+      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[am][4 * rq + lg]);
+      const uint32_t w[4] = {wq[rq].x, wq[rq].y, wq[rq].z, wq[rq].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, unpack_codes8(w[c], kLo, kMagic),
+                                                         acc[c], 0, 0, 0);
     }
     float sc[4], cz[4], dz[4];
     if (FMT == MTL_META_QSZ) {
-      const uint32_t mw[4] = {meta[ch].x, meta[ch].y, meta[ch].z, meta[ch].w};
+      const uint32_t mw[4] = {meta[g].x, meta[g].y, meta[g].z, meta[g].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         sc[c] = bf16_to_f32(mw[c] & 0xffffu);
@@ -321,44 +336,51 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
         cz[c] = 136.f;   // 128 (bf16 magic) + 8 (offset-binary centre)
       }
     } else {
-      sc[0] = f16_to_f32(meta[ch].x & 0xffffu);
-      sc[1] = f16_to_f32(meta[ch].x >> 16);
-      sc[2] = f16_to_f32(meta[ch].y & 0xffffu);
-      sc[3] = f16_to_f32(meta[ch].y >> 16);
+      sc[0] = f16_to_f32(meta[g].x & 0xffffu);
+      sc[1] = f16_to_f32(meta[g].x >> 16);
+      sc[2] = f16_to_f32(meta[g].y & 0xffffu);
+      sc[3] = f16_to_f32(meta[g].y >> 16);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        cz[c] = (float)(128 + (int)((meta[ch].z >> (4 * c)) & 0xfu) + a.zero_offset);
+        cz[c] = (float)(128 + (int)((meta[g].z >> (4 * c)) & 0xfu) + a.zero_offset);
         dz[c] = 0.f;
       }
     }
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int r = 0; r < NR; ++r) {
+      const float X = xg[MR == 1 ? 0 : 4 * lg + r][g];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const float t = fmaf(-cz[c], X[m], acc[m][c]);
-        float v = fmaf(sc[c], t, tot[m][c]);
-        if (FMT == MTL_META_QSZ) v = fmaf(dz[c], X[m], v);
-        tot[m][c] = v;
+        const float tt = fmaf(-cz[c], X, acc[c][r]);
+        float v = fmaf(sc[c], tt, tot[c][r]);
+        if (FMT == MTL_META_QSZ) v = fmaf(dz[c], X, v);
+        tot[c][r] = v;
       }
+    }
   }
 
-  // 6. Reduce the waves of the workgroup into wave 0 (fixed order 0, 1, 2, 3).
-  if (nw > 1) {
-    if (wave > 0) {
+  // 6. Result tile to LDS, then re-read as 4 consecutive columns per thread: thread t
+  //    owns columns tile*256 + 4*(t%64) of rows t/64, t/64 + 4, ...
 #pragma unroll
-      for (int m = 0; m < MR; ++m)
-        red[wave][m][lane] = make_float4(tot[m][0], tot[m][1], tot[m][2], tot[m][3]);
-    }
-    __syncthreads();
-    if (wave > 0) return;
-    for (int w2 = 1; w2 < nw; ++w2) {
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float4 v = red[w2][m][lane];
-        tot[m][0] += v.x; tot[m][1] += v.y; tot[m][2] += v.z; tot[m][3] += v.w;
-      }
-    }
+  for (int r = 0; r < NR; ++r) {
+    const int m = MR == 1 ? 0 : 4 * lg + r;
+    if ((MR == 1 && lg == 0) || (MR > 1 && m < M))
+      *reinterpret_cast<float4*>(&ytile[m][wave * kWaveN + 4 * lj]) =
+          make_float4(tot[0][r], tot[1][r], tot[2][r], tot[3][r]);
   }
+  __syncthreads();
+  constexpr int RPT = MR == 1 ? 1 : 4;        // rows per thread in the epilogue mapping
+  const int ecol = tile * kTileN + 4 * lane;
+  const bool ecol_ok = ecol < N;
+  float v[RPT][4];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    const int m = wave + 4 * j;
+    const float4 y4 = (m < MR) ? *reinterpret_cast<const float4*>(&ytile[m < MR ? m : 0][4 * lane])
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[j][0] = y4.x; v[j][1] = y4.y; v[j][2] = y4.z; v[j][3] = y4.w;
+  }
+  const bool active = MR == 1 ? wave == 0 : true;   // MR = 1: wave 0 carries row 0
 
   // 7. Split-K.  Every workgroup publishes its fp32 partial tile.  With an in-kernel
   //    reduction the partials travel as relaxed agent-scope atomics (coherent across
@@ -366,110 +388,114 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   //    and that one sums all splits in split order (loads batched 8 deep) and resets
   //    the counter.  Otherwise w4_reduce_kernel (or a fused consumer) sums them.
   if (a.splits > 1 || a.partials_only) {
-    float* pbase = a.partial + (size_t)split * M * N + col0;
+    float* pbase = a.partial + (size_t)split * M * N + ecol;
     if (!a.inkernel_reduce || a.partials_only) {
-      if (col_ok) {
+      if (active && ecol_ok) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
+        for (int j = 0; j < RPT; ++j) {
+          const int m = wave + 4 * j;
           if (m < M)
             *reinterpret_cast<float4*>(pbase + (size_t)m * N) =
-                make_float4(tot[m][0], tot[m][1], tot[m][2], tot[m][3]);
+                make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+        }
       }
       return;
     }
-    if (col_ok) {
+    if (active && ecol_ok) {
 #pragma unroll
-      for (int m = 0; m < MR; ++m)
+      for (int j = 0; j < RPT; ++j) {
+        const int m = wave + 4 * j;
         if (m < M) {
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            __hip_atomic_store(pbase + (size_t)m * N + c, tot[m][c], __ATOMIC_RELAXED,
+            __hip_atomic_store(pbase + (size_t)m * N + c, v[j][c], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);   // every partial store acknowledged before the count
-    int last = 0;
-    if (lane == 0)
-      last = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(a.splits - 1);
-    last = __builtin_amdgcn_readfirstlane(__shfl(last, 0));
-    if (!last) return;
+    __syncthreads();
+    __shared__ int last_flag;
+    if (t == 0)
+      last_flag = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(a.splits - 1);
+    __syncthreads();
+    if (!last_flag) return;
+    if (t == 0)
+      __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int S = a.splits;
+    const size_t stride = (size_t)M * N;
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
+    for (int j = 0; j < RPT; ++j) {
+      const int m = wave + 4 * j;
       float s4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (col_ok && m < M) {
-        const float* q = a.partial + (size_t)m * N + col0;
-        const size_t stride = (size_t)M * N;
+      if (active && ecol_ok && m < M) {
+        const float* q = a.partial + (size_t)m * N + ecol;
         for (int s0 = 0; s0 < S; s0 += 8) {
-          float v[8][4];
+          float pv[8][4];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int sp = s0 + j < S ? s0 + j : S - 1;
+          for (int jj = 0; jj < 8; ++jj) {
+            const int sp = s0 + jj < S ? s0 + jj : S - 1;
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              v[j][c] = __hip_atomic_load(q + sp * stride + c, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
+              pv[jj][c] = __hip_atomic_load(q + sp * stride + c, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
           }
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (s0 + j < S) {
+          for (int jj = 0; jj < 8; ++jj)
+            if (s0 + jj < S) {
 #pragma unroll
-              for (int c = 0; c < 4; ++c) s4[c] += v[j][c];
+              for (int c = 0; c < 4; ++c) s4[c] += pv[jj][c];
             }
         }
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) tot[m][c] = s4[c];
+      for (int c = 0; c < 4; ++c) v[j][c] = s4[c];
     }
-    if (lane == 0)
-      __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (!active) return;
 
-  // 8. Epilogue, 4 consecutive columns per lane.
+  // 8. Epilogue, 4 consecutive columns per thread.
   if (a.epilogue == MTL_EPI_SILU_MUL) {
     // Fused columns come in blocks of 64 = 32 gate | 32 up; lane l (l%16 < 8) holds
     // gate columns whose up partners sit 8 lanes higher.
     const int no = N >> 1;
     const int lb = lane & 15;
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
+    for (int j = 0; j < RPT; ++j) {
+      const int m = wave + 4 * j;
       float u[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) u[c] = __shfl_down(tot[m][c], 8);
-      if (m < M && col_ok && lb < 8) {
+      for (int c = 0; c < 4; ++c) u[c] = __shfl_down(v[j][c], 8);
+      if (m < M && ecol_ok && lb < 8) {
         const int o = tile * (kTileN / 2) + (lane >> 4) * 32 + lb * 4;
         uint32_t h[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float g = round_bf16(tot[m][c]);
-          const float sg = round_bf16(g / (1.0f + expf(-g)));
-          h[c] = f32_to_bf16(sg * round_bf16(u[c]));
-        }
+        for (int c = 0; c < 4; ++c) h[c] = silu_mul_bf16(v[j][c], u[c]);
         *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + (size_t)m * no + o) =
             u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
     }
-  } else if (col_ok) {
+  } else if (ecol_ok) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
+    for (int j = 0; j < RPT; ++j) {
+      const int m = wave + 4 * j;
       if (m >= M) continue;
-      const size_t o = (size_t)m * N + col0;
-      float v[4] = {tot[m][0], tot[m][1], tot[m][2], tot[m][3]};
+      const size_t o = (size_t)m * N + ecol;
+      float y[4] = {v[j][0], v[j][1], v[j][2], v[j][3]};
       if (a.epilogue == MTL_EPI_RESIDUAL) {
         const u32x2 rr = *reinterpret_cast<const u32x2*>(a.resid + o);
-        v[0] = round_bf16(v[0]) + bf16_to_f32(rr.x & 0xffffu);
-        v[1] = round_bf16(v[1]) + bf16_to_f32(rr.x >> 16);
-        v[2] = round_bf16(v[2]) + bf16_to_f32(rr.y & 0xffffu);
-        v[3] = round_bf16(v[3]) + bf16_to_f32(rr.y >> 16);
+        y[0] = round_bf16(y[0]) + bf16_to_f32(rr.x & 0xffffu);
+        y[1] = round_bf16(y[1]) + bf16_to_f32(rr.x >> 16);
+        y[2] = round_bf16(y[2]) + bf16_to_f32(rr.y & 0xffffu);
+        y[3] = round_bf16(y[3]) + bf16_to_f32(rr.y >> 16);
       }
       if (a.out_f32) {
-        *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) =
-            make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(static_cast<float*>(a.y) + o) = make_float4(y[0], y[1], y[2], y[3]);
       } else {
         *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + o) =
-            u32x2{f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16),
-                  f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16)};
+            u32x2{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
+                  f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
       }
     }
   }
@@ -546,28 +572,15 @@ __global__ void __launch_bounds__(256) w4_reduce_kernel(W4Args a) {
 // Launch planning
 // ----------------------------------------------------------------------------
 
-static int g_tune_waves = 0;   // 0: heuristic; 1, 2, 4: forced waves per workgroup
-
 struct Plan {
-  int waves, splits, col_tiles, row_blocks;
+  int splits, col_tiles;
 };
 
 static Plan plan_for(int64_t K, int64_t N) {
   Plan p;
   const int rows = (int)(K / 8);
-  p.row_blocks = (rows + kRowsPerWave - 1) / kRowsPerWave;
+  p.splits = (rows + kRowsPerWG - 1) / kRowsPerWG;
   p.col_tiles = (int)((N + kTileN - 1) / kTileN);
-  int w = 1;
-  if (g_tune_waves == 1 || g_tune_waves == 2 || g_tune_waves == 4) {
-    w = g_tune_waves;
-  } else {
-    // Four waves per workgroup measured best on every decode shape (fewest splits,
-    // so the least split-K traffic and counter work).
-    w = 4;
-  }
-  while (w > 1 && w > p.row_blocks) w >>= 1;
-  p.waves = w;
-  p.splits = (p.row_blocks + w - 1) / w;
   return p;
 }
 
@@ -576,26 +589,66 @@ static Plan plan_for(int64_t K, int64_t N) {
 constexpr int64_t kCounterBytes = 16384;   // 4096 column tiles: N <= 1M
 static int g_inkernel_reduce = 1;
 
-template <int MR, int RPG>
-static void launch_fmt(const W4Args& a, int fmt, dim3 grid, dim3 block, hipStream_t s) {
+template <int MR, int GR>
+static void launch_fmt(const W4Args& a, int fmt, dim3 grid, hipStream_t s) {
+  const dim3 block(256);
   if (fmt == MTL_META_QSZ)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_QSZ, XSRC_BF16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_QSZ, XSRC_BF16>), grid, block, 0, s, a);
   else if (a.xpart)
-    hipLaunchKernelGGL((w4_gemm_kernel<1, RPG, MTL_META_GPTQ, XSRC_SILU_PART>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_SILU_PART>), grid, block, 0, s, a);
   else if (a.hn)
-    hipLaunchKernelGGL((w4_gemm_kernel<1, RPG, MTL_META_GPTQ, XSRC_RMSNORM>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_RMSNORM>), grid, block, 0, s, a);
   else if (a.perm)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, XSRC_PERM>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_PERM>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, RPG, MTL_META_GPTQ, XSRC_BF16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_BF16>), grid, block, 0, s, a);
 }
 
+// Row quads per quantisation group: group / 32.
 template <int MR>
-static void launch_rpg(const W4Args& a, int fmt, dim3 grid, dim3 block, hipStream_t s) {
-  const int rpg = a.group / 8 < kRowsPerWave ? a.group / 8 : kRowsPerWave;
-  if (rpg == 4) launch_fmt<MR, 4>(a, fmt, grid, block, s);
-  else if (rpg == 8) launch_fmt<MR, 8>(a, fmt, grid, block, s);
-  else launch_fmt<MR, 16>(a, fmt, grid, block, s);
+static void launch_gr(const W4Args& a, int fmt, dim3 grid, hipStream_t s) {
+  switch (a.group) {
+    case 32: launch_fmt<MR, 1>(a, fmt, grid, s); break;
+    case 64: launch_fmt<MR, 2>(a, fmt, grid, s); break;
+    case 128: launch_fmt<MR, 4>(a, fmt, grid, s); break;
+    default: launch_fmt<MR, 8>(a, fmt, grid, s); break;
+  }
+}
+
+static void launch_w4(const W4Args& a, int fmt, const Plan& p, hipStream_t s) {
+  const dim3 grid(p.col_tiles, p.splits);
+  if (a.M == 1) launch_gr<1>(a, fmt, grid, s);
+  else launch_gr<16>(a, fmt, grid, s);
+}
+
+// The buffer descriptor's size and offsets are 32-bit: the weight rows of the last
+// split (up to 64 past K/8) must stay addressable.
+static bool weight_fits(int64_t K, int64_t N) {
+  return (K / 8 + kRowsPerWG) * N * 4 < ((int64_t)1 << 31);
+}
+
+static W4Args blank_args() {
+  W4Args a;
+  a.x = nullptr;
+  a.qweight = nullptr;
+  a.meta0 = nullptr;
+  a.qzeros = nullptr;
+  a.perm = nullptr;
+  a.xpart = nullptr;
+  a.xsplits = 0;
+  a.xpart_ld = 0;
+  a.hn = nullptr;
+  a.wn = nullptr;
+  a.slots = nullptr;
+  a.eps = 0.f;
+  a.resid = nullptr;
+  a.y = nullptr;
+  a.partial = nullptr;
+  a.counters = nullptr;
+  a.inkernel_reduce = 0;
+  a.partials_only = 0;
+  a.M = a.K = a.N = a.group = a.zero_offset = a.splits = a.epilogue = a.out_f32 = 0;
+  return a;
 }
 
 static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, int fmt,
@@ -614,15 +667,14 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   if (K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (epilogue == MTL_EPI_SILU_MUL && N % 64 != 0) return MTL_ERR_SHAPE;
   if ((N + kTileN - 1) / kTileN > kCounterBytes / 4) return MTL_ERR_SHAPE;
-  // The weight buffer's byte size and row offsets are 32-bit in the buffer descriptor.
-  if (K * N / 2 >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (!weight_fits(K, N) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
   if (!aligned16(qweight) || !aligned16(x) || (perm && !aligned16(perm))) return MTL_ERR_ALIGN;
   if (perm && fmt != MTL_META_GPTQ) return MTL_ERR_INVALID_ARG;
   if (fmt == MTL_META_QSZ && !aligned16(meta0)) return MTL_ERR_ALIGN;
   if (fmt == MTL_META_GPTQ && (reinterpret_cast<uintptr_t>(meta0) & 7u)) return MTL_ERR_ALIGN;
 
   const Plan p = plan_for(K, N);
-  W4Args a;
+  W4Args a = blank_args();
   a.x = static_cast<const uint16_t*>(x);
   a.qweight = reinterpret_cast<const u32x4*>(qweight);
   a.meta0 = static_cast<const uint16_t*>(meta0);
@@ -635,16 +687,6 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   a.splits = p.splits;
   a.epilogue = epilogue;
   a.out_f32 = out_dtype == MTL_OUT_F32;
-  a.partial = nullptr;
-  a.counters = nullptr;
-  a.xpart = nullptr;
-  a.xsplits = 0;
-  a.xpart_ld = 0;
-  a.hn = nullptr;
-  a.wn = nullptr;
-  a.slots = nullptr;
-  a.eps = 0.f;
-  a.partials_only = 0;
   a.inkernel_reduce = g_inkernel_reduce;
   if (p.splits > 1) {
     const int64_t need = kCounterBytes + (int64_t)p.splits * M * N * 4;
@@ -653,16 +695,7 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
     a.counters = static_cast<unsigned*>(workspace);
     a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   }
-  const dim3 grid(p.col_tiles, p.splits);
-  const dim3 block(64 * p.waves);
-  const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
-  switch (mr) {
-    case 1: launch_rpg<1>(a, fmt, grid, block, stream); break;
-    case 2: launch_rpg<2>(a, fmt, grid, block, stream); break;
-    case 4: launch_rpg<4>(a, fmt, grid, block, stream); break;
-    case 8: launch_rpg<8>(a, fmt, grid, block, stream); break;
-    default: launch_rpg<16>(a, fmt, grid, block, stream); break;
-  }
+  launch_w4(a, fmt, p, stream);
   if (p.splits > 1 && !a.inkernel_reduce) {
     const int quads = (int)(M * (epilogue == MTL_EPI_SILU_MUL ? N / 8 : N / 4));
     hipLaunchKernelGGL(w4_reduce_kernel, dim3((quads + 255) / 256), dim3(256), 0, stream, a);
@@ -683,7 +716,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (M < 1 || M > kMaxM || K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0)
     return MTL_ERR_SHAPE;
-  if (K * N / 2 >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (!weight_fits(K, N) || M * K >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
   if (xpart) {
     if (M != 1) return MTL_ERR_UNSUPPORTED;
     if (perm) return MTL_ERR_INVALID_ARG;
@@ -697,7 +730,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   const Plan p = plan_for(K, N);
   if (partials_bytes < (int64_t)p.splits * M * N * 4) return MTL_ERR_WORKSPACE;
-  W4Args a;
+  W4Args a = blank_args();
   a.x = static_cast<const uint16_t*>(x);
   a.qweight = reinterpret_cast<const u32x4*>(qweight);
   a.meta0 = static_cast<const uint16_t*>(meta0);
@@ -706,31 +739,14 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   a.xpart = xpart;
   a.xsplits = xsplits;
   a.xpart_ld = (int)xpart_ld;
-  a.hn = nullptr;
-  a.wn = nullptr;
-  a.slots = nullptr;
-  a.eps = 0.f;
-  a.resid = nullptr;
-  a.y = nullptr;
   a.partial = partials;
-  a.counters = nullptr;
   a.M = (int)M; a.K = (int)K; a.N = (int)N;
   a.group = group; a.zero_offset = zero_offset;
   a.splits = p.splits;
   a.epilogue = MTL_EPI_NONE;
   a.out_f32 = 1;
-  a.inkernel_reduce = 0;
   a.partials_only = 1;
-  const dim3 grid(p.col_tiles, p.splits);
-  const dim3 block(64 * p.waves);
-  const int mr = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
-  switch (mr) {
-    case 1: launch_rpg<1>(a, MTL_META_GPTQ, grid, block, stream); break;
-    case 2: launch_rpg<2>(a, MTL_META_GPTQ, grid, block, stream); break;
-    case 4: launch_rpg<4>(a, MTL_META_GPTQ, grid, block, stream); break;
-    case 8: launch_rpg<8>(a, MTL_META_GPTQ, grid, block, stream); break;
-    default: launch_rpg<16>(a, MTL_META_GPTQ, grid, block, stream); break;
-  }
+  launch_w4(a, MTL_META_GPTQ, p, stream);
   return launch_status();
 }
 
@@ -745,37 +761,28 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (!aligned16(slots)) return MTL_ERR_ALIGN;
-  if (K * N / 2 >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (!weight_fits(K, N)) return MTL_ERR_SHAPE;
   if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   const Plan p = plan_for(K, N);
   if (partials_bytes < (int64_t)p.splits * N * 4) return MTL_ERR_WORKSPACE;
-  W4Args a;
-  a.x = nullptr;
+  W4Args a = blank_args();
   a.qweight = reinterpret_cast<const u32x4*>(qweight);
   a.meta0 = static_cast<const uint16_t*>(meta0);
   a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
-  a.perm = nullptr;
-  a.xpart = nullptr;
-  a.xsplits = 0;
-  a.xpart_ld = 0;
   a.hn = static_cast<const uint16_t*>(h_ord);
   a.wn = static_cast<const uint16_t*>(w_ord);
   a.slots = slots;
   a.eps = eps;
-  a.resid = nullptr;
-  a.y = nullptr;
   a.partial = partials;
-  a.counters = nullptr;
   a.M = 1; a.K = (int)K; a.N = (int)N;
   a.group = group; a.zero_offset = zero_offset;
   a.splits = p.splits;
   a.epilogue = MTL_EPI_NONE;
   a.out_f32 = 1;
-  a.inkernel_reduce = 0;
   a.partials_only = 1;
-  launch_rpg<1>(a, MTL_META_GPTQ, dim3(p.col_tiles, p.splits), dim3(64 * p.waves), stream);
+  launch_w4(a, MTL_META_GPTQ, p, stream);
   return launch_status();
 }
 
@@ -810,9 +817,8 @@ int mtl_abi_version(void) { return 1; }
 int64_t mtl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t group_size) {
   if (M < 1 || M > kMaxM || K <= 0 || N <= 0 || K % 8 != 0) return 0;
   (void)group_size;
-  const int64_t row_blocks = (K / 8 + kRowsPerWave - 1) / kRowsPerWave;
-  // Sized for the deepest split (one wave per workgroup), so any plan fits.
-  return kCounterBytes + row_blocks * M * N * 4;
+  const int64_t splits = (K / 8 + kRowsPerWG - 1) / kRowsPerWG;
+  return kCounterBytes + splits * M * N * 4;
 }
 
 int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream) {
@@ -876,8 +882,7 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
                  (hipStream_t)stream);
 }
 
-// Tuning knob for launch-shape sweeps: force 1, 2 or 4 waves per workgroup (0 restores
-// the heuristic).  Process-wide; not for concurrent use.
+// Tuning knobs for launch-shape sweeps; process-wide, not for concurrent use.
 // Split-K reduction: 1 = in-kernel (last workgroup of a tile), 0 = separate kernel.
 int mtl_tune_set_reduce(int32_t inkernel) {
   if (inkernel != 0 && inkernel != 1) return MTL_ERR_INVALID_ARG;
@@ -885,10 +890,6 @@ int mtl_tune_set_reduce(int32_t inkernel) {
   return MTL_OK;
 }
 
-int mtl_tune_set_waves(int32_t waves) {
-  if (waves != 0 && waves != 1 && waves != 2 && waves != 4) return MTL_ERR_INVALID_ARG;
-  g_tune_waves = waves;
-  return MTL_OK;
-}
+
 
 }  // extern "C"

@@ -31,6 +31,10 @@ def test_every_bound_symbol_is_declared():
     assert not undeclared, undeclared
 
 
+def test_tune_knobs_validate(lib):
+    assert lib.mtl_tune_set_reduce(2) == N.MTL_ERR_INVALID_ARG
+
+
 def test_status_strings(lib):
     assert lib.mtl_status_string(0) == b"ok"
     assert lib.mtl_status_string(N.MTL_ERR_GROUP) == b"unsupported group size"
@@ -38,8 +42,9 @@ def test_status_strings(lib):
 
 
 def test_workspace_bytes(lib):
-    # 16 KB tile counters + deepest split partials: K/128 row blocks x M x N fp32
-    assert lib.mtl_gemm_workspace_bytes(1, 4096, 24576, 128) == 16384 + 32 * 24576 * 4
+    # 16 KB tile counters + split partials: one split per 512 input channels, M x N fp32
+    assert lib.mtl_gemm_workspace_bytes(1, 4096, 24576, 128) == 16384 + 8 * 24576 * 4
+    assert lib.mtl_gemm_workspace_bytes(3, 12288, 4096, 128) == 16384 + 24 * 3 * 4096 * 4
     assert lib.mtl_gemm_workspace_bytes(0, 4096, 4096, 128) == 0
     assert lib.mtl_gemm_workspace_bytes(17, 4096, 4096, 128) == 0
 

@@ -127,6 +127,20 @@ def test_gptq_gemm_groups(dev, group):
         assert err < tol
 
 
+@pytest.mark.parametrize("group,k,n", [(32, 1024, 520), (64, 2048, 768), (128, 4096, 1032),
+                                      (256, 4608, 264)])
+@pytest.mark.parametrize("m", [1, 5])
+def test_group_layouts_ragged(dev, group, k, n, m):
+    # every row-quads-per-group variant, M = 1 (broadcast A) and M > 1 (padded A), with
+    # and without act-order, N not a multiple of the 256-column tile, K not a multiple
+    # of the 512-channel split
+    for act in (False, True):
+        case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=act, seed=m + group + k)
+        err = rel_l2(run_gptq(case, dev, act), case["y_ref"])
+        print(f"g={group} K={k} N={n} M={m} act={act} rel_l2={err:.2e}")
+        assert err < TOL_F32
+
+
 @pytest.mark.parametrize("k,n", [(32, 8), (96, 24), (256, 264), (640, 1000), (12288, 264)])
 def test_gptq_gemm_ragged_shapes(dev, k, n):
     group = 32
