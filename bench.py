@@ -224,22 +224,20 @@ def bench_decode(args, torch):
 
     # Dominant kernel, live: each int4 GEMV launch of the step exactly as the captured plan
     # issues it, over the model's own 36 layers (1.9 GB of distinct gate_up weights, so no
-    # Infinity-Cache reuse), event pairs on the launch stream, queued behind a GPU spin so
-    # host launch overhead never shows.
+    # Infinity-Cache reuse): 144 launches back to back between one event pair on the
+    # launch stream, queued behind a GPU spin so host launch overhead never shows.
     reps = 4 * cfg.n_layers
     gemv_us = {}
     for name in ("gate_up", "down", "qkv", "o"):
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(reps)]
+        a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         torch.cuda._sleep(int(2e8))
-        for i, (a, b) in enumerate(evs):
-            a.record()
+        a_ev.record()
+        for i in range(reps):
             dec.run_gemv(i % cfg.n_layers, name)
-            b.record()
+        b_ev.record()
         torch.cuda.synchronize()
-        us = [a.elapsed_time(b) * 1e3 for a, b in evs]
-        gemv_us[name] = sum(us) / len(us)
+        gemv_us[name] = a_ev.elapsed_time(b_ev) * 1e3 / reps
     gu_us = gemv_us["gate_up"]
     gu_bytes = algo_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size, False)
     layer_bytes = sum(algo_bytes(1, k, n, cfg.group_size, True) for k, n in
@@ -268,11 +266,27 @@ def bench_decode(args, torch):
                               ("qkv", cfg.hidden, cfg.qkv_out), ("o", cfg.hidden, cfg.hidden))}},
         roofline={"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1),
                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                  "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4), "traffic": None,
-                  "kernel": "w4_gemm_kernel<1,16,GPTQ,rmsnorm-staged> gate_up 4096x24576 M=1 "
+                  "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
+                  "traffic": profiled_traffic("gate_up"),
+                  "kernel": "w4_gemm_kernel<1,4,GPTQ,XSRC_RMSNORM> gate_up 4096x24576 M=1 "
                             "(split-K partials, as launched in the decode step)",
                   "bytes_per_launch": gu_bytes},
     )
+
+
+def profiled_traffic(name: str):
+    """HBM bytes per launch of one decode-step GEMV, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (copy-kernel calibrated); None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "gemv_traffic_decode_shapes.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes {name}:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def bench_kernels(args, torch):
