@@ -140,6 +140,16 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
                               int64_t* token_out, void* workspace, int64_t ws_bytes,
                               void* stream);
 
+/*
+ * bf16 GEMV without selection: out[n] = bf16(sum_k W[n,k] x[k]) for W bf16 [N, K]
+ * (F.linear with a bf16 weight: the text, audio and 2-way heads of
+ * moss_tts_lite/fast.py:174-194, and bf16-kept projections, gptq.py:689-697).  When
+ * pad_period > 0, rows with n % pad_period == pad_index are written as -inf (the audio
+ * heads' pad code, fast.py:181-182).  K % 8 == 0, K <= 12288.
+ */
+int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,
+                  int64_t pad_period, int64_t pad_index, void* stream);
+
 /* pos[0] += 1 on the device (ends a captured decode step). */
 int mtl_advance_position(int64_t* pos, void* stream);
 

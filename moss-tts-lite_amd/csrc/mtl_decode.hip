@@ -568,7 +568,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 // are merged in row order.
 // ----------------------------------------------------------------------------------
 constexpr int kHeadWGs = 1024;
-constexpr int kHeadKit = 16;     // K <= 8192
+constexpr int kHeadKitMax = 24;  // K <= 12288 (512 channels per item)
 
 __device__ __forceinline__ bool better(float va, long long ia, float vb, long long ib) {
   if (ia < 0) return false;
@@ -579,6 +579,7 @@ __device__ __forceinline__ bool better(float va, long long ia, float vb, long lo
   return va > vb || (va == vb && ia < ib);
 }
 
+template <int kHeadKit>
 __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ w,
                                                         int64_t N, int K,
@@ -587,7 +588,8 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
                                                         long long* __restrict__ part_i,
                                                         const uint16_t* __restrict__ norm_w,
                                                         const float* __restrict__ slots,
-                                                        float eps) {
+                                                        float eps, int64_t pad_period,
+                                                        int64_t pad_index) {
   __shared__ float sv[4];
   __shared__ long long si[4];
   const int wave = wave_id(), lane = threadIdx.x & 63;
@@ -641,7 +643,8 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
       }
     }
     acc = wave_sum(acc);
-    const uint32_t hb = f32_to_bf16(acc);
+    uint32_t hb = f32_to_bf16(acc);
+    if (pad_period > 0 && r % pad_period == pad_index) hb = 0xff80u;   // -inf
     if (logits && lane == 0) logits[r] = (uint16_t)hb;
     const float lv = bf16_to_f32(hb);
     if (better(lv, r, best, bidx)) {
@@ -649,6 +652,7 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
       bidx = r;
     }
   }
+  if (!part_v) return;   // logits only
   if (lane == 0) {
     sv[wave] = best;
     si[wave] = bidx;
@@ -665,6 +669,17 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
     part_v[blockIdx.x] = b;
     part_i[blockIdx.x] = bi;
   }
+}
+
+// Launch the head GEMV with x held in ceil(K/512) items of 8 channels per lane.
+template <typename... Args>
+static void launch_head(int64_t K, hipStream_t s, Args... args) {
+  if (K <= 4096)
+    hipLaunchKernelGGL(head_gemv_kernel<8>, dim3(kHeadWGs), dim3(256), 0, s, args...);
+  else if (K <= 8192)
+    hipLaunchKernelGGL(head_gemv_kernel<16>, dim3(kHeadWGs), dim3(256), 0, s, args...);
+  else
+    hipLaunchKernelGGL(head_gemv_kernel<24>, dim3(kHeadWGs), dim3(256), 0, s, args...);
 }
 
 __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restrict__ part_v,
@@ -846,16 +861,16 @@ int64_t mtl_head_workspace_bytes(int64_t N) {
 int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, void* logits,
                          int64_t* token_out, void* workspace, int64_t ws_bytes, void* stream) {
   if (!x || !w) return MTL_ERR_INVALID_ARG;
-  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKit) return MTL_ERR_SHAPE;
+  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(w)) return MTL_ERR_ALIGN;
   if (!workspace || ws_bytes < mtl_head_workspace_bytes(N)) return MTL_ERR_WORKSPACE;
   if (!aligned16(workspace)) return MTL_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   float* pv = static_cast<float*>(workspace);
   long long* pi = reinterpret_cast<long long*>(static_cast<char*>(workspace) + kHeadWGs * 4);
-  hipLaunchKernelGGL(head_gemv_kernel, dim3(kHeadWGs), dim3(256), 0, s,
+  launch_head(K, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), N, (int)K,
-                     static_cast<uint16_t*>(logits), pv, pi, nullptr, nullptr, 0.f);
+                     static_cast<uint16_t*>(logits), pv, pi, nullptr, nullptr, 0.f, 0, 0);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
                        token_out);
@@ -913,20 +928,34 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
                               int64_t* token_out, void* workspace, int64_t ws_bytes,
                               void* stream) {
   if (!h || !norm_w || !slots || !w) return MTL_ERR_INVALID_ARG;
-  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKit) return MTL_ERR_SHAPE;
+  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w)) return MTL_ERR_ALIGN;
   if (!workspace || ws_bytes < mtl_head_workspace_bytes(N)) return MTL_ERR_WORKSPACE;
   if (!aligned16(workspace)) return MTL_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
   float* pv = static_cast<float*>(workspace);
   long long* pi = reinterpret_cast<long long*>(static_cast<char*>(workspace) + kHeadWGs * 4);
-  hipLaunchKernelGGL(head_gemv_kernel, dim3(kHeadWGs), dim3(256), 0, s,
+  launch_head(K, s,
                      static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w), N, (int)K,
                      static_cast<uint16_t*>(logits), pv, pi, static_cast<const uint16_t*>(norm_w),
-                     slots, eps);
+                     slots, eps, 0, 0);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
                        token_out);
+  return launch_status();
+}
+
+int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,
+                  int64_t pad_period, int64_t pad_index, void* stream) {
+  if (!x || !w || !out) return MTL_ERR_INVALID_ARG;
+  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
+  if (pad_period < 0 || (pad_period > 0 && (pad_index < 0 || pad_index >= pad_period)))
+    return MTL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w)) return MTL_ERR_ALIGN;
+  launch_head(K, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), N, (int)K,
+                     static_cast<uint16_t*>(out), nullptr, nullptr, nullptr, nullptr, 0.f,
+                     pad_period, pad_index);
   return launch_status();
 }
 

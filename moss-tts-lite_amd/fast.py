@@ -68,7 +68,7 @@ class FastDecoder:
         dev = model.device
         self.dev = dev
         bf = torch.bfloat16
-        self.ids = torch.zeros(1, dtype=torch.int64, device=dev)      # token fed to the step
+        self._alloc_io()
         self.pos = torch.zeros(1, dtype=torch.int64, device=dev)      # its cache position
         self.h = torch.zeros(cfg.hidden, dtype=bf, device=dev)        # residual stream
         self.x = torch.zeros(cfg.hidden, dtype=bf, device=dev)        # normed input
@@ -77,9 +77,6 @@ class FastDecoder:
         self.attn = torch.zeros(cfg.hidden, dtype=bf, device=dev)
         self.act = torch.zeros(cfg.intermediate, dtype=bf, device=dev)
         self.h_final = torch.zeros(cfg.hidden, dtype=bf, device=dev)
-        self.logits = torch.zeros(cfg.vocab, dtype=bf, device=dev)
-        self.table_ptrs = torch.tensor([model.embed_tokens.data_ptr()], dtype=torch.int64, device=dev)
-        self.vocabs = torch.tensor([cfg.vocab], dtype=torch.int64, device=dev)
         gemm_ws = max(ops.gemm_workspace_bytes(1, cfg.hidden, cfg.qkv_out, cfg.group_size),
                       ops.gemm_workspace_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size),
                       ops.gemm_workspace_bytes(1, cfg.intermediate, cfg.hidden, cfg.group_size))
@@ -113,6 +110,15 @@ class FastDecoder:
             self.norm_gu.append(_gather(lyr["post_attention_layernorm"], pg))
         self._build_plan()
         self.graph: torch.cuda.CUDAGraph | None = None
+
+    def _alloc_io(self) -> None:
+        """Step inputs/outputs: the token id fed in, logits and the greedy token out."""
+        cfg, dev = self.m.cfg, self.m.device
+        self.ids = torch.zeros(1, dtype=torch.int64, device=dev)      # token fed to the step
+        self.logits = torch.zeros(cfg.vocab, dtype=torch.bfloat16, device=dev)
+        self.table_ptrs = torch.tensor([self.m.embed_tokens.data_ptr()], dtype=torch.int64,
+                                       device=dev)
+        self.vocabs = torch.tensor([cfg.vocab], dtype=torch.int64, device=dev)
 
     # -- launch plan ------------------------------------------------------------------
     def _gemm(self, x, lin, n, epilogue, resid, y, no_perm=False):
@@ -244,17 +250,43 @@ class FastDecoder:
         ]
 
     def _build_plan(self) -> None:
-        m, cfg = self.m, self.m.cfg
+        cfg = self.m.cfg
         lib = N.load()
-        self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), 1, self.table_ptrs.data_ptr(),
-                                          self.vocabs.data_ptr(), cfg.hidden, self.h.data_ptr()))]
-        eps = ctypes.c_float(cfg.eps)
-        head = ("mtl_bf16_gemv_argmax", (self.h_final.data_ptr(), m.head.data_ptr(), cfg.vocab,
-                                         cfg.hidden, self.logits.data_ptr(),
-                                         ctypes.c_void_p(self.ids.data_ptr()),
-                                         self.head_ws.data_ptr(), self.head_ws.numel()))
+        self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), self.table_ptrs.numel(),
+                                          self.table_ptrs.data_ptr(), self.vocabs.data_ptr(),
+                                          cfg.hidden, self.h.data_ptr()))]
         if self.plan == "staged":
             self._layers = [self._layer_plan_staged(li) for li in range(cfg.n_layers)]
+        elif self.plan == "partials":
+            self._layers = [self._layer_plan_fused(li) for li in range(cfg.n_layers)]
+        else:
+            self._layers = [self._layer_plan(li) for li in range(cfg.n_layers)]
+        self._final = self._final_plan()
+        self._fns = {name: getattr(lib, name) for name in
+                     ("mtl_rmsnorm", "mtl_w4_gemm_fused", "mtl_qk_norm_rope_kv",
+                      "mtl_decode_attention", "mtl_embed_sum", "mtl_bf16_gemv_argmax",
+                      "mtl_advance_position", "mtl_w4_gemm_partials",
+                      "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
+                      "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
+                      "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv")}
+
+    def _final_norm_plan(self) -> list:
+        """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
+        m, cfg = self.m, self.m.cfg
+        eps = ctypes.c_float(cfg.eps)
+        if self.plan == "unfused":
+            return [("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(),
+                                     self.h_final.data_ptr(), 1, cfg.hidden, eps))]
+        return [("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
+                                          self.h.data_ptr(), self.h.data_ptr(),
+                                          m.final_norm.data_ptr(), self.h_final.data_ptr(),
+                                          None, cfg.hidden, eps))]
+
+    def _final_plan(self) -> list:
+        """Final norm, head, greedy token into ``ids``, position + 1."""
+        m, cfg = self.m, self.m.cfg
+        eps = ctypes.c_float(cfg.eps)
+        if self.plan == "staged":   # the head applies the final norm while staging
             final = [self._flush_staged(),
                      ("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
                                                     self.slots.data_ptr(), eps, m.head.data_ptr(),
@@ -262,24 +294,13 @@ class FastDecoder:
                                                     ctypes.c_void_p(self.ids.data_ptr()),
                                                     self.head_ws.data_ptr(),
                                                     self.head_ws.numel()))]
-        elif self.plan == "partials":
-            self._layers = [self._layer_plan_fused(li) for li in range(cfg.n_layers)]
-            final = [("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
-                                               self.h.data_ptr(), self.h.data_ptr(),
-                                               m.final_norm.data_ptr(), self.h_final.data_ptr(),
-                                               None, cfg.hidden, eps)), head]
         else:
-            self._layers = [self._layer_plan(li) for li in range(cfg.n_layers)]
-            final = [("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(),
-                                      self.h_final.data_ptr(), 1, cfg.hidden, eps)), head]
-        self._final = final + [("mtl_advance_position", (ctypes.c_void_p(self.pos.data_ptr()),))]
-        self._fns = {name: getattr(lib, name) for name in
-                     ("mtl_rmsnorm", "mtl_w4_gemm_fused", "mtl_qk_norm_rope_kv",
-                      "mtl_decode_attention", "mtl_embed_sum", "mtl_bf16_gemv_argmax",
-                      "mtl_advance_position", "mtl_w4_gemm_partials",
-                      "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
-                      "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
-                      "mtl_bf16_gemv_argmax_norm")}
+            final = self._final_norm_plan() + [
+                ("mtl_bf16_gemv_argmax", (self.h_final.data_ptr(), m.head.data_ptr(), cfg.vocab,
+                                          cfg.hidden, self.logits.data_ptr(),
+                                          ctypes.c_void_p(self.ids.data_ptr()),
+                                          self.head_ws.data_ptr(), self.head_ws.numel()))]
+        return final + [("mtl_advance_position", (ctypes.c_void_p(self.pos.data_ptr()),))]
 
     def _flush_staged(self):
         return ("mtl_residual_add", (self.part["down"].data_ptr(), self.splits["down"],
@@ -392,3 +413,115 @@ class FastDecoder:
                 self.run_step()
             out[i:i + 1].copy_(self.ids)
         return out
+
+
+class FastMossDecoder(FastDecoder):
+    """The MOSS-TTS decode step on the int4 backbone: 33-way summed embedding of one
+    row of ids, the layers, final norm and the output heads -- text logits + 32 audio
+    heads (pad code -inf), or in the audio2 variant the 2-way head + audio heads
+    (moss_tts_lite/fast.py:123-194).  Mirrors ``FastMossTTS.capture()/step(row, pos,
+    audio2)`` (fast.py:272-325): the host passes the position; one graph per variant
+    serves every cache length.
+    """
+
+    def __init__(self, model: Int4Backbone, plan: str = "staged"):
+        if model.cfg.n_vq < 1:
+            raise ValueError("FastMossDecoder needs a MOSS-shaped backbone (cfg.n_vq > 0)")
+        self.graphs: dict | None = None
+        super().__init__(model, plan)
+
+    def _alloc_io(self) -> None:
+        m, cfg, dev = self.m, self.m.cfg, self.m.device
+        bf = torch.bfloat16
+        self.ids = torch.zeros(1 + cfg.n_vq, dtype=torch.int64, device=dev)   # ids_row
+        self.table_ptrs = torch.tensor([m.embed_tokens.data_ptr()] +
+                                       [t.data_ptr() for t in m.emb_ext], dtype=torch.int64,
+                                       device=dev)
+        self.vocabs = torch.tensor([cfg.vocab] + [cfg.audio_vocab] * cfg.n_vq, dtype=torch.int64,
+                                   device=dev)
+        self.lt = torch.zeros(cfg.vocab, dtype=bf, device=dev)
+        self.la = torch.zeros(cfg.n_vq, cfg.audio_vocab, dtype=bf, device=dev)
+        self.two = torch.zeros(2, dtype=bf, device=dev)
+        self.logits = self.lt
+
+    def _final_plan(self) -> list:
+        return self._final_variant(audio2=False)
+
+    def _final_variant(self, audio2: bool) -> list:
+        m, cfg = self.m, self.m.cfg
+        hf = self.h_final.data_ptr()
+        audio = ("mtl_bf16_gemv", (hf, m.head_audio.data_ptr(), cfg.n_vq * cfg.audio_vocab,
+                                   cfg.hidden, self.la.data_ptr(), cfg.audio_vocab,
+                                   cfg.audio_pad_code))
+        if audio2:
+            first = ("mtl_bf16_gemv", (hf, m.head_2way.data_ptr(), 2, cfg.hidden,
+                                       self.two.data_ptr(), 0, 0))
+        else:
+            first = ("mtl_bf16_gemv", (hf, m.head.data_ptr(), cfg.vocab, cfg.hidden,
+                                       self.lt.data_ptr(), 0, 0))
+        return self._final_norm_plan() + [first, audio]
+
+    def run_step(self, audio2: bool = False) -> None:
+        """One whole step, eager, at the position in ``pos`` (not advanced)."""
+        self._run(self._embed)
+        for plan in self._layers:
+            self._run(plan)
+        self._run(self._final_variant(audio2))
+
+    def capture(self) -> None:
+        """Capture one whole-step graph per head variant (text, audio2)."""
+        if self.graphs is not None:
+            return
+        saved_ids, saved_pos = self.ids.clone(), self.pos.clone()
+        s = torch.cuda.Stream(self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            for audio2 in (False, True, False):
+                self.run_step(audio2)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.synchronize(self.dev)
+        self.graphs = {}
+        for audio2 in (False, True):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.run_step(audio2)
+            self.graphs[audio2] = g
+        torch.cuda.synchronize(self.dev)
+        self.ids.copy_(saved_ids)
+        self.pos.copy_(saved_pos)
+
+    def step(self, row: torch.Tensor | None, pos: int, audio2: bool = False):
+        """Replay one decode step for ``row`` ([1 + n_vq] ids) at cache position ``pos``.
+
+        Returns ``(lt, la, h_final, two)`` like ``FastMossTTS.step``: the text logits
+        (stale in the audio2 variant), audio logits ``[n_vq, audio_vocab]``, the normed
+        final hidden state and the 2-way logits (stale in the text variant).
+        """
+        if self.graphs is None:
+            raise RuntimeError("call capture() first")
+        if row is not None:
+            src = row.reshape(-1)
+            if src.data_ptr() != self.ids.data_ptr():
+                self.ids.copy_(src)
+        self.pos.fill_(int(pos))
+        self.graphs[bool(audio2)].replay()
+        return self.lt, self.la, self.h_final, self.two
+
+    def prefill(self, rows: torch.Tensor) -> torch.Tensor:
+        """Fill the KV cache with a prompt of ``rows`` ([L, 1 + n_vq] ids), one eager
+        step per row; returns ``h_final`` of the last row (the prompt's hidden state)."""
+        rows = rows.to(device=self.dev, dtype=torch.int64).reshape(-1, 1 + self.m.cfg.n_vq)
+        if rows.shape[0] > self.m.cfg.max_seq:
+            raise ValueError("prompt longer than the KV cache")
+        self.m.reset_cache()
+        for t in range(rows.shape[0]):
+            self.ids.copy_(rows[t])
+            self.pos.fill_(t)
+            self._run(self._embed)
+            for plan in self._layers:
+                self._run(plan)
+        self._run(self._final_norm_plan())
+        return self.h_final
+
+    def generate(self, n_steps: int, use_graph: bool = True) -> torch.Tensor:
+        raise NotImplementedError("MOSS sampling runs on the host per step; call step()")

@@ -18,7 +18,9 @@ from . import ops
 
 __all__ = ["GPTQLinear", "fuse_gptq_linears", "group_scales_from_weight", "rtn_quantize",
            "pack_fast", "pack_qsz_only", "effective_weight", "kernel_linear",
-           "interleave_gate_up"]
+           "interleave_gate_up", "bf16_linear", "W4Dispatch", "load_gptq_state", "LIN_NAMES"]
+
+LIN_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
 
 class GPTQLinear(torch.nn.Module):
@@ -232,4 +234,103 @@ def kernel_linear(x: torch.Tensor, packed: torch.Tensor, g: int, qsz: torch.Tens
     return out.reshape(*shp[:-1], qsz.shape[1])
 
 
-del N
+def bf16_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, W)`` for a bf16 weight ``[N, K]`` on the gfx950 bf16 GEMV (one
+    launch per row of ``x``): the path of linears kept in bf16 (gptq.py:689-693)."""
+    if w.dtype != torch.bfloat16 or w.dim() != 2:
+        raise RuntimeError("weight must be bfloat16 [N, K]")
+    n, k = w.shape
+    shp = x.shape
+    if shp[-1] != k:
+        raise RuntimeError(f"x has {shp[-1]} features, weight expects {k}")
+    x2 = x.reshape(-1, k).to(torch.bfloat16).contiguous()
+    w = w.contiguous()
+    out = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x.device)
+    lib = N.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    for r in range(x2.shape[0]):
+        N.check(lib.mtl_bf16_gemv(x2[r].data_ptr(), w.data_ptr(), n, k, out[r].data_ptr(), 0, 0,
+                                  stream), "mtl_bf16_gemv")
+    return out.reshape(*shp[:-1], n)
+
+
+class W4Dispatch:
+    """The reference's per-linear int4 dispatch on this build's kernels.
+
+    Mirrors ``FastMossTTS._quantize/_linear`` (moss_tts_lite/fast.py:73-121) and
+    ``GptqMossTTS._quantize/_linear`` (gptq.py:641-697): ``qlayers[li]`` maps each
+    quantised linear name to ``(packed, qsz)`` (``packed`` in this build's ``[K/8, N]``
+    layout from :func:`ops.convert_weight_to_int4pack`), ``group_size_map[li][name]``
+    holds its group size, and linears listed in ``bf16_keep`` (a layer index keeps the
+    whole layer, an ``(li, name)`` pair one linear) stay bf16 and run
+    :func:`bf16_linear`.  A layer with nothing quantised has ``qlayers[li] = None``.
+    """
+
+    def __init__(self, layers: list, w4_group_size: int = 128, bf16_keep=(),
+                 group_size_map: dict | None = None, state: dict | None = None):
+        if w4_group_size not in (32, 64, 128, 256):
+            raise ValueError("w4_group_size must be 32/64/128/256")
+        self.layers = layers                       # per layer: name -> bf16 weight [N, K]
+        self.w4_group_size = w4_group_size
+        keep = set(bf16_keep)
+        self._keep_layers = {int(x) for x in keep if isinstance(x, int)}
+        self._keep_linears = {(int(a), b) for a, b in (x for x in keep if not isinstance(x, int))}
+        gmap = {(int(a), b): int(g) for (a, b), g in (group_size_map or {}).items()}
+        self.group_size_map = {li: {name: gmap.get((li, name), w4_group_size) for name in LIN_NAMES}
+                               for li in range(len(layers))}
+        for li, gm in self.group_size_map.items():
+            for name, g in gm.items():
+                if g not in (32, 64, 128, 256):
+                    raise ValueError(f"group size {g} of layer {li} {name} not in 32/64/128/256")
+        self.qlayers = []
+        for li, lyr in enumerate(layers):
+            if li in self._keep_layers:
+                self.qlayers.append(None)
+                continue
+            qd = {}
+            for name in LIN_NAMES:
+                if (li, name) in self._keep_linears or name not in lyr:
+                    continue
+                g = self.group_size_map[li][name]
+                rec = None if state is None else state[li][name]
+                if rec is None:            # round-to-nearest from the bf16 weight (fast.py:86-101)
+                    q, sc, mn = rtn_quantize(lyr[name], g)
+                    qd[name] = pack_fast(q, sc, mn)
+                else:                      # calibrated codes + qsz (gptq.py:504-509, 664-687)
+                    dev = lyr[name].device
+                    q = rec["q"].to(device=dev, dtype=torch.uint8)
+                    pre = (q[:, 1::2] | (q[:, 0::2] << 4)).contiguous()
+                    qd[name] = (ops.convert_weight_to_int4pack(pre, 8),
+                                rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous())
+                lyr.pop(name)
+            self.qlayers.append(qd if qd else None)
+
+    def _linear(self, x: torch.Tensor, li: int, name: str) -> torch.Tensor:
+        """``F.linear``-shaped projection ``x[..., K] -> [..., N]`` in the active mode."""
+        qd = self.qlayers[li]
+        if qd is None or name not in qd:
+            return bf16_linear(x, self.layers[li][name])
+        packed, qsz = qd[name]
+        return kernel_linear(x, packed, self.group_size_map[li][name], qsz, torch.bfloat16)
+
+
+def load_gptq_state(path: str):
+    """Read an offline GPTQ state and its ``.meta.json`` (gptq.py:608-626) with loaders
+    that execute nothing from the file: returns ``(state, group_size_map, bf16_keep)``."""
+    import json
+    import os
+    state = torch.load(path, map_location="cpu", weights_only=True)
+    meta_path = path + ".meta.json"
+    if not os.path.isfile(meta_path):
+        raise FileNotFoundError(f"{meta_path} not found: per-linear group sizes and bf16 keeps "
+                                "cannot be inferred from the weights alone")
+    with open(meta_path) as f:
+        meta = json.load(f)
+    gmap = {}
+    for key, val in meta.get("group_size_map", {}).items():
+        layer, name = key.split(":")
+        gmap[(int(layer), name)] = int(val)
+    keep = [(int(x.split(":")[0]), x.split(":")[1]) for x in meta.get("bf16_linears", [])]
+    keep += [int(x) for x in meta.get("bf16_layers", [])]
+    return state, gmap, keep
+

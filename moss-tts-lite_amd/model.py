@@ -34,6 +34,13 @@ class BackboneConfig:
     rope_theta: float = ROPE_THETA
     eps: float = RMS_EPS
     max_seq: int = 2048
+    # MOSS-TTS output side (moss_tts_lite/model.py:9-24, 89-101): n_vq audio codebooks,
+    # each with an embedding table and a head of audio_vocab rows (pad code masked to
+    # -inf), and a 2-way head made of two text-head rows.  n_vq = 0: one text head.
+    n_vq: int = 0
+    audio_vocab: int = 1025
+    audio_pad_code: int = 1024
+    two_way_ids: tuple = (151656, 151662)
 
     @property
     def qkv_out(self) -> int:
@@ -49,6 +56,19 @@ class BackboneConfig:
         if self.intermediate % 64 or self.hidden % self.group_size or \
                 self.intermediate % self.group_size:
             raise ValueError("intermediate must be a multiple of 64 and of the group size")
+        if self.n_vq:
+            if not 0 <= self.audio_pad_code < self.audio_vocab:
+                raise ValueError("audio_pad_code must index an audio head row")
+            if len(self.two_way_ids) != 2 or not all(0 <= i < self.vocab for i in self.two_way_ids):
+                raise ValueError("two_way_ids must be two text-vocabulary rows")
+
+
+def moss_config(**kw) -> BackboneConfig:
+    """MOSS-TTS shape: Qwen3-8B backbone, text vocabulary 155648 (model.py:14), 32 audio
+    codebooks of 1025 codes (model.py:9-12)."""
+    base = dict(vocab=155648, n_vq=32)
+    base.update(kw)
+    return BackboneConfig(**base)
 
 
 def gate_up_columns_for(order: torch.Tensor, block: int = 32) -> torch.Tensor:
@@ -90,6 +110,15 @@ class Int4Backbone:
         self.embed_tokens = T(weights["embed_tokens"])
         self.final_norm = T(weights["final_norm"])
         self.head = T(weights["head"])
+        self.emb_ext, self.head_audio, self.head_2way = [], None, None
+        if cfg.n_vq:
+            self.emb_ext = [T(t) for t in weights["emb_ext"]]
+            if len(self.emb_ext) != cfg.n_vq:
+                raise ValueError("need one audio embedding table per codebook")
+            # the 32 audio heads stacked as one [n_vq * audio_vocab, hidden] matrix
+            self.head_audio = T(weights["head_audio"]).reshape(cfg.n_vq * cfg.audio_vocab,
+                                                               cfg.hidden)
+            self.head_2way = self.head[list(cfg.two_way_ids)].contiguous()
         self.layers = []
         for lw in weights["layers"]:
             lyr = {k: T(lw[k]) for k in ("input_layernorm", "post_attention_layernorm",
@@ -163,8 +192,12 @@ def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda") -> dict
             "gate_up": _random_gptq(gen, dev, h, 2 * cfg.intermediate, g, perm(h)),
             "down": _random_gptq(gen, dev, cfg.intermediate, h, g, perm(cfg.intermediate)),
         })
-    return {"embed_tokens": normal(cfg.vocab, h, std=1.0), "final_norm": norm_w(h),
-            "head": normal(cfg.vocab, h, std=0.02), "layers": layers}
+    out = {"embed_tokens": normal(cfg.vocab, h, std=1.0), "final_norm": norm_w(h),
+           "head": normal(cfg.vocab, h, std=0.02), "layers": layers}
+    if cfg.n_vq:
+        out["emb_ext"] = [normal(cfg.audio_vocab, h, std=1.0) for _ in range(cfg.n_vq)]
+        out["head_audio"] = normal(cfg.n_vq, cfg.audio_vocab, h, std=0.02)
+    return out
 
 
 def attention_scale(cfg: BackboneConfig) -> float:

@@ -100,6 +100,48 @@ def decoder_layer(h: np.ndarray, lw: dict, k_cache: np.ndarray, v_cache: np.ndar
     return round_bf16(h + linear(act, lw["down"]))
 
 
+def embed_sum(ids, tables) -> np.ndarray:
+    """Sum of one embedding row per table, left to right, each add a bf16 tensor op
+    (model.py:156-161, fast.py:123-128): ``tables[0][ids[0]] + tables[1][ids[1]] + ...``."""
+    h = np.asarray(tables[0][int(ids[0])], np.float32)
+    for t, i in zip(tables[1:], ids[1:]):
+        h = round_bf16(h + np.asarray(t[int(i)], np.float32))
+    return h
+
+
+def bf16_linear_rows(hf: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """``F.linear(hf, W)`` for a bf16 weight ``[N, K]``: float64 products, bf16 out."""
+    return round_bf16((np.asarray(w, np.float64) @ hf.astype(np.float64)).astype(np.float32))
+
+
+def moss_heads(hf: np.ndarray, head_text, head_audio, head_2way, pad_code: int,
+               audio2: bool):
+    """The MOSS output heads (fast.py:174-194): text logits ``lt`` (None in the audio2
+    variant), audio logits ``la [n_vq, V]`` with column ``pad_code`` set to -inf, and
+    the 2-way logits (audio2 only, None otherwise)."""
+    la = np.stack([bf16_linear_rows(hf, w) for w in head_audio], 0)
+    la[:, pad_code] = -np.inf
+    if audio2:
+        return None, la, bf16_linear_rows(hf, head_2way)
+    return bf16_linear_rows(hf, head_text), la, None
+
+
+def moss_decode_step(row, pos: int, weights: dict, k_cache, v_cache, cos, sin, n_heads: int,
+                     n_kv: int, head_dim: int, pad_code: int, audio2: bool = False,
+                     eps: float = 1e-6):
+    """One MOSS step (fast.py:123-194): 33-way embedding of ``row``, the layers at
+    ``pos``, final norm and heads.  Returns ``(lt, la, hf, two)`` as ``FastMossTTS.step``
+    (fast.py:307-325) does, with None for the head the variant skips."""
+    h = embed_sum(row, [weights["embed_tokens"]] + list(weights["emb_ext"]))
+    for li, lw in enumerate(weights["layers"]):
+        h = decoder_layer(h, lw, k_cache[li], v_cache[li], pos, cos, sin, n_heads, n_kv,
+                          head_dim, eps)
+    hf = rms_norm(h, weights["final_norm"], eps)
+    lt, la, two = moss_heads(hf, weights["head"], weights["head_audio"], weights["head_2way"],
+                             pad_code, audio2)
+    return lt, la, hf, two
+
+
 def decode_step(token: int, pos: int, weights: dict, k_cache, v_cache, cos, sin, n_heads: int,
                 n_kv: int, head_dim: int, eps: float = 1e-6):
     """Whole step (fast.py:123-194 with a single text head): returns

@@ -74,8 +74,16 @@ def build_case(cfg: BackboneConfig, seed: int, dev):
     head = _bf16_bits(r, (cfg.vocab, h), std=0.02)
     fnorm = _bf16_bits(r, h, std=0.05, mean=1.0)
     t16 = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
-    model = Int4Backbone(cfg, {"embed_tokens": t16(emb), "final_norm": t16(fnorm),
-                               "head": t16(head), "layers": dev_layers}, dev)
+    dev_w = {"embed_tokens": t16(emb), "final_norm": t16(fnorm), "head": t16(head),
+             "layers": dev_layers}
     oracle_w = {"embed_tokens": bf16_bits_to_f32(emb), "final_norm": bf16_bits_to_f32(fnorm),
                 "head": bf16_bits_to_f32(head), "layers": np_layers}
+    if cfg.n_vq:
+        ext = [_bf16_bits(r, (cfg.audio_vocab, h), std=1.0) for _ in range(cfg.n_vq)]
+        ha = _bf16_bits(r, (cfg.n_vq, cfg.audio_vocab, h), std=0.02)
+        dev_w.update(emb_ext=[t16(e) for e in ext], head_audio=t16(ha))
+        oracle_w.update(emb_ext=[bf16_bits_to_f32(e) for e in ext],
+                        head_audio=bf16_bits_to_f32(ha),
+                        head_2way=bf16_bits_to_f32(head)[list(cfg.two_way_ids)])
+    model = Int4Backbone(cfg, dev_w, dev)
     return model, oracle_w

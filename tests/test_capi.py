@@ -126,3 +126,21 @@ def test_decode_entry_validation(lib):
 def test_converter_validation(lib):
     assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE
+
+
+def test_load_gptq_state_safe_loader(tmp_path):
+    # the reference's offline GPTQ state layout (gptq.py:504-509) + meta json (gptq.py:608-626)
+    import json
+    import torch
+    from moss_tts_lite_amd.gptq import load_gptq_state
+    state = {0: {"q": {"q": torch.zeros(8, 256, dtype=torch.uint8),
+                       "qsz": torch.zeros(2, 8, 2, dtype=torch.bfloat16)}}}
+    p = tmp_path / "state.pt"
+    torch.save(state, p)
+    with pytest.raises(FileNotFoundError):
+        load_gptq_state(str(p))
+    (tmp_path / "state.pt.meta.json").write_text(json.dumps(
+        {"group_size_map": {"0:q": 32}, "bf16_linears": ["1:down"], "bf16_layers": [3]}))
+    st, gmap, keep = load_gptq_state(str(p))
+    assert gmap == {(0, "q"): 32} and keep == [(1, "down"), 3]
+    assert torch.equal(st[0]["q"]["q"], state[0]["q"]["q"])

@@ -517,3 +517,47 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     if srt[-1] - srt[-2] > 0.05:
         assert int(tok.item()) == int(np.argmax(ref))
     assert int(tok.item()) == int(np.argmax(fb(logits)))
+
+
+@pytest.mark.parametrize("plan", ["staged", "unfused"])
+def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
+    # MOSS step: 33-way (here 1 + 4) embedding, layers, final norm, text + audio heads
+    # (pad code -inf) or the audio2 variant (2-way + audio heads); graph == eager.
+    from moss_tts_lite_amd.fast import FastMossDecoder
+    cfg = small_config(vocab=2000, n_vq=4, audio_vocab=1025, audio_pad_code=1024,
+                       two_way_ids=(1500, 1777))
+    model, ow = build_case(cfg, seed=31, dev=dev)
+    dec = FastMossDecoder(model, plan=plan)
+    r = np.random.default_rng(3)
+    rows = np.concatenate([r.integers(0, cfg.vocab, (7, 1)), r.integers(0, 1025, (7, cfg.n_vq))], 1)
+    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    okc, ovc = _oracle_caches(model)
+    # prompt rows 0..4 through the oracle, then steps at positions 5, 6 (text, audio2)
+    for p in range(5):
+        D.moss_decode_step(rows[p], p, ow, okc, ovc, cos, sin, cfg.n_heads, cfg.n_kv_heads, 128,
+                           cfg.audio_pad_code)
+    hf_dev = dec.prefill(torch.from_numpy(rows[:5]))
+    dec.capture()
+    eager = {}
+    for p, audio2 in ((5, False), (6, True)):
+        lt, la, hf, two = D.moss_decode_step(rows[p], p, ow, okc, ovc, cos, sin, cfg.n_heads,
+                                             cfg.n_kv_heads, 128, cfg.audio_pad_code, audio2)
+        g_lt, g_la, g_hf, g_two = (t.clone() for t in dec.step(torch.from_numpy(rows[p]), p, audio2))
+        assert np.all(np.isneginf(fb(g_la)[:, cfg.audio_pad_code]))
+        keep = np.arange(cfg.audio_vocab) != cfg.audio_pad_code
+        errs = [rel_l2(fb(g_hf), hf), rel_l2(fb(g_la)[:, keep], la[:, keep])]
+        errs.append(rel_l2(fb(g_two), two) if audio2 else rel_l2(fb(g_lt), lt))
+        print(f"{plan} pos={p} audio2={audio2} rel_l2 hf/la/{'two' if audio2 else 'lt'} = "
+              + " ".join(f"{e:.2e}" for e in errs))
+        assert max(errs) < 1e-2
+        eager[audio2] = (g_lt, g_la, g_hf, g_two)
+    # graph replays are bitwise equal to the eager step at the same position
+    for p, audio2 in ((5, False), (6, True)):
+        dec.ids.copy_(torch.from_numpy(rows[p]))
+        dec.pos.fill_(p)
+        dec.run_step(audio2)
+        e = [t.clone() for t in (dec.lt, dec.la, dec.h_final, dec.two)]
+        out = dec.step(torch.from_numpy(rows[p]), p, audio2)
+        for a, b in zip(e, out):
+            assert torch.equal(a, b)
+    del hf_dev, eager

@@ -288,3 +288,41 @@ def test_deterministic_and_graph_replay(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, y0), f"replay {i}"
         ops.gptq_gemm(x, qw, qz, sc, 128, perm=perm)   # eager work between replays
+
+
+# ------------------------------------------------------------------ per-linear dispatch
+
+def test_w4_dispatch_modes(dev):
+    # FastMossTTS/GptqMossTTS-style dispatch (fast.py:107-121, gptq.py:689-697): RTN int4
+    # at the default group, a per-linear group override, bf16-kept linears and layers
+    from moss_tts_lite_amd.gptq import W4Dispatch, effective_weight, LIN_NAMES
+    r = np.random.default_rng(0)
+    shapes = {"q": (512, 256), "k": (128, 256), "v": (128, 256), "o": (256, 512),
+              "gate": (384, 256), "up": (384, 256), "down": (256, 384)}
+    def layer():
+        return {n: torch.from_numpy((r.standard_normal(s) * 0.05).astype(np.float32))
+                .to(dev).bfloat16() for n, s in shapes.items()}
+    layers = [layer() for _ in range(3)]
+    orig = [{n: w.float().cpu().numpy() for n, w in lyr.items()} for lyr in layers]
+    disp = W4Dispatch(layers, w4_group_size=128, bf16_keep=[2, (1, "down")],
+                      group_size_map={(0, "o"): 32, (1, "q"): 64})
+    assert disp.qlayers[2] is None and "down" not in disp.qlayers[1]
+    assert disp.group_size_map[0]["o"] == 32 and disp.group_size_map[0]["q"] == 128
+    x = torch.from_numpy(r.standard_normal((3, 512)).astype(np.float32)).to(dev).bfloat16()
+    for li in range(3):
+        for name in LIN_NAMES:
+            k = shapes[name][1]
+            xi = x[:, :k]
+            got = disp._linear(xi.reshape(1, 3, k), li, name).float().cpu().numpy()[0]
+            xf = xi.float().cpu().numpy().astype(np.float64)
+            if disp.qlayers[li] is None or name not in disp.qlayers[li]:
+                ref = xf @ orig[li][name].astype(np.float64).T          # bf16 kept
+            else:
+                packed, qsz = disp.qlayers[li][name]
+                g = disp.group_size_map[li][name]
+                assert qsz.shape == (k // g, shapes[name][0], 2)
+                codes = ops.unpack_codes(packed).t()                    # [N, K]
+                w = effective_weight(codes, qsz, g).double().cpu().numpy()
+                ref = xf @ w.T
+            err = rel_l2(got, ref)
+            assert err < TOL_BF16, (li, name, err)

@@ -98,3 +98,32 @@ def test_silu_mul_matches_torch():
     ref = (F.silu(tg) * tu).float().numpy()
     ours = D.silu_mul(g, u)
     assert np.all(np.abs(ours - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+
+
+def test_embed_sum_matches_torch_bf16_adds():
+    # the reference's 33-way embedding: F.embedding per table, bf16 adds left to right
+    r = np.random.default_rng(5)
+    tables = [_bf(r, (50, 64))] + [_bf(r, (9, 64)) for _ in range(4)]
+    ids = [7, 3, 8, 0, 5]
+    tt = [torch.from_numpy(t).bfloat16() for t in tables]
+    h = F.embedding(torch.tensor([ids[0]]), tt[0])
+    for t, i in zip(tt[1:], ids[1:]):
+        h = h + F.embedding(torch.tensor([i]), t)
+    assert np.array_equal(D.embed_sum(ids, tables), h[0].float().numpy())
+
+
+def test_moss_heads_layout_and_pad():
+    r = np.random.default_rng(6)
+    hf = _bf(r, 64)
+    text = _bf(r, (300, 64), 0.02)
+    audio = _bf(r, (3, 17, 64), 0.02)
+    two_ids = [250, 260]
+    lt, la, two = D.moss_heads(hf, text, audio, text[two_ids], pad_code=16, audio2=False)
+    assert two is None and la.shape == (3, 17) and lt.shape == (300,)
+    assert np.all(np.isneginf(la[:, 16])) and np.all(np.isfinite(la[:, :16]))
+    ref = (torch.from_numpy(audio).double() @ torch.from_numpy(hf).double()).float()
+    assert np.array_equal(la[:, :16], ref.bfloat16().float().numpy()[:, :16])
+    lt2, la2, two2 = D.moss_heads(hf, text, audio, text[two_ids], pad_code=16, audio2=True)
+    assert lt2 is None and np.array_equal(la2, la)
+    # the 2-way head is the text head's rows at the two slot ids (model.py head_2way)
+    assert np.array_equal(two2, lt[two_ids])
