@@ -138,18 +138,26 @@ __device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
 // qweight row 4q + l/16, i.e. exactly the B operand of v_mfma_f32_16x16x32_bf16 for
 // its 4 columns; the A operand is x (row m = l%16, or row 0 broadcast when MR = 1).
 // GR = row quads per quantisation group (group / 32).
-template <int MR, int GR, int FMT, int XSRC>
-__global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
+// KW = waves stacked along K (1, 2 or 4): wave w covers columns (w % 4) * 64 of the
+// tile and row quads (w / 4) * 16/KW .. +16/KW of the split; the KW partial tiles are
+// summed through LDS in fixed order.  KW > 1 serves M = 1.
+template <int MR, int GR, int FMT, int XSRC, int KW>
+__global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   constexpr bool LATE_X = XSRC == XSRC_PERM;  // the gather needs perm: x after the weights
   constexpr int NG = kRowQuads / GR;          // groups per split
+  constexpr int RQW = kRowQuads / KW;         // row quads per wave
+  constexpr int NGW = RQW / GR;               // groups per wave
+  static_assert(RQW % GR == 0, "a wave must cover whole quantisation groups");
+  static_assert(MR == 1 || KW == 1, "K-stacked waves serve M = 1");
   constexpr int GI = 4 * GR;                  // x items (8 channels) per group
   constexpr int XPT = MR == 1 ? 1 : 4;        // staging items per thread
   __shared__ u32x4 xa[MR][kRowsPerWG];        // x in pair order, one item per qweight row
   __shared__ float xg[MR][NG];                // per-group sums of x
-  __shared__ float ytile[MR][kTileN];         // workgroup result, for the epilogue mapping
+  __shared__ float ytile[KW][MR][kTileN];     // per-K-slice results, for the epilogue mapping
   __shared__ uint32_t xn[XSRC == XSRC_SILU_PART ? kRowsPerWG : 1][4];   // SiLU*up items
 
   const int wave = wave_id();
+  const int wn = wave & 3, wk = wave >> 2;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int lg = lane >> 4, lj = lane & 15;
@@ -157,7 +165,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   const int N = a.N, M = a.M;
   const int rows_total = a.K >> 3;
   const int row0 = split * kRowsPerWG;
-  const int col = tile * kTileN + wave * kWaveN + 4 * lj;
+  const int col = tile * kTileN + wn * kWaveN + 4 * lj;
   const bool col_ok = col < N;
 
   // 1. x items this thread stages: (m, i) = (t/64 + 4j, t%64) for MR = 16, (0, t) for
@@ -213,7 +221,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
       sU[q] = *reinterpret_cast<const float2*>(s_pb + (size_t)sp * a.xpart_ld + 32);
     }
   };
-  if (XSRC == XSRC_SILU_PART) {
+  if (XSRC == XSRC_SILU_PART && t < 4 * kRowsPerWG) {
     const int j0 = (s_row < rows_total ? s_row : rows_total - 1) * 8;
     s_pb = a.xpart + 64 * (j0 >> 5) + (j0 & 31) + 2 * (t & 3);
     silu_batch(0);
@@ -226,10 +234,10 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   // 2. Group metadata of the lane's 4 columns, one entry per group of the split.
   const int colc = col_ok ? col : N - 4;
   const int ngroups = a.K / a.group;
-  u32x4 meta[NG];
+  u32x4 meta[NGW];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    int grp = (row0 * 8) / a.group + g;
+  for (int g = 0; g < NGW; ++g) {
+    int grp = (row0 * 8) / (32 * GR) + wk * NGW + g;
     grp = grp < ngroups ? grp : ngroups - 1;
     if (FMT == MTL_META_QSZ) {
       meta[g] = *reinterpret_cast<const u32x4*>(a.meta0 + ((size_t)grp * N + colc) * 2);
@@ -244,13 +252,14 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   //    offset per quad; rows past K/8 and columns past N read 0 through the range check.
   const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.qweight), (short)0, (int)((int64_t)rows_total * N * 4), 0x00020000);
-  u32x4 wq[kRowQuads];
+  u32x4 wq[RQW];
 #pragma unroll
-  for (int q = 0; q < kRowQuads; ++q) {
-    const int row = row0 + 4 * q + lg;
+  for (int q = 0; q < RQW; ++q) {
+    const int gq = wk * RQW + q;              // row quad within the split
+    const int row = row0 + 4 * gq + lg;
     const int voff = (col_ok && row < rows_total) ? (lg * N + col) * 4 : 0x7ffffff0;
     wq[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          qrsrc, voff, (row0 + 4 * q) * N * 4, kStreamAux));
+                                          qrsrc, voff, (row0 + 4 * gq) * N * 4, kStreamAux));
   }
 
   if (LATE_X) load_x();
@@ -260,18 +269,20 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
 
   // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
   if (XSRC == XSRC_SILU_PART) {
-    float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-    for (int s0 = 0; s0 < a.xsplits; s0 += 8) {
-      if (s0 > 0) silu_batch(s0);
+    if (t < 4 * kRowsPerWG) {
+      float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+      for (int s0 = 0; s0 < a.xsplits; s0 += 8) {
+        if (s0 > 0) silu_batch(s0);
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        if (s0 + q < a.xsplits) {
-          g0 += sG[q].x; g1 += sG[q].y;
-          u0 += sU[q].x; u1 += sU[q].y;
-        }
+        for (int q = 0; q < 8; ++q)
+          if (s0 + q < a.xsplits) {
+            g0 += sG[q].x; g1 += sG[q].y;
+            u0 += sU[q].x; u1 += sU[q].y;
+          }
+      }
+      xn[t >> 2][t & 3] =
+          s_row < rows_total ? silu_mul_bf16(g0, u0) | (silu_mul_bf16(g1, u1) << 16) : 0u;
     }
-    xn[t >> 2][t & 3] =
-        s_row < rows_total ? silu_mul_bf16(g0, u0) | (silu_mul_bf16(g1, u1) << 16) : 0u;
     __syncthreads();
     if (stager) xv[0] = u32x4{xn[t][0], xn[t][1], xn[t][2], xn[t][3]};
   }
@@ -312,14 +323,14 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
     for (int r = 0; r < NR; ++r) tot[c][r] = 0.f;
   const int am = MR == 1 ? 0 : lj;            // A operand row of this lane
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
+  for (int g = 0; g < NGW; ++g) {
     floatx4 acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < GR; ++q) {
       const int rq = g * GR + q;
-      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[am][4 * rq + lg]);
+      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[am][4 * (wk * RQW + rq) + lg]);
       const uint32_t w[4] = {wq[rq].x, wq[rq].y, wq[rq].z, wq[rq].w};
 #pragma unroll
       for (int c = 0; c < 4; ++c)
@@ -348,7 +359,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const float X = xg[MR == 1 ? 0 : 4 * lg + r][g];
+      const float X = xg[MR == 1 ? 0 : 4 * lg + r][wk * NGW + g];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float tt = fmaf(-cz[c], X, acc[c][r]);
@@ -365,7 +376,7 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
   for (int r = 0; r < NR; ++r) {
     const int m = MR == 1 ? 0 : 4 * lg + r;
     if ((MR == 1 && lg == 0) || (MR > 1 && m < M))
-      *reinterpret_cast<float4*>(&ytile[m][wave * kWaveN + 4 * lj]) =
+      *reinterpret_cast<float4*>(&ytile[wk][m][wn * kWaveN + 4 * lj]) =
           make_float4(tot[0][r], tot[1][r], tot[2][r], tot[3][r]);
   }
   __syncthreads();
@@ -376,11 +387,17 @@ __global__ void __launch_bounds__(256) w4_gemm_kernel(W4Args a) {
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const int m = wave + 4 * j;
-    const float4 y4 = (m < MR) ? *reinterpret_cast<const float4*>(&ytile[m < MR ? m : 0][4 * lane])
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-    v[j][0] = y4.x; v[j][1] = y4.y; v[j][2] = y4.z; v[j][3] = y4.w;
+    v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.f;
+    if (m < MR) {
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {           // K slices summed in order
+        const float4 y4 = *reinterpret_cast<const float4*>(&ytile[k][m][4 * lane]);
+        v[j][0] += y4.x; v[j][1] += y4.y; v[j][2] += y4.z; v[j][3] += y4.w;
+      }
+    }
   }
-  const bool active = MR == 1 ? wave == 0 : true;   // MR = 1: wave 0 carries row 0
+  // MR = 1: wave 0 carries row 0; threads past 255 (KW > 1) only join the barriers
+  const bool active = (MR == 1 ? wave == 0 : true) && t < kTileN;
 
   // 7. Split-K.  Every workgroup publishes its fp32 partial tile.  With an in-kernel
   //    reduction the partials travel as relaxed agent-scope atomics (coherent across
@@ -573,14 +590,23 @@ __global__ void __launch_bounds__(256) w4_reduce_kernel(W4Args a) {
 // ----------------------------------------------------------------------------
 
 struct Plan {
-  int splits, col_tiles;
+  int splits, col_tiles, kw;
 };
 
-static Plan plan_for(int64_t K, int64_t N) {
+// kw > 1 (waves stacked along K) for M = 1, so small shapes still put about 2 waves on
+// every SIMD; a wave must cover whole groups.  Every M = 1 launch of a shape (partials
+// only or reduced in the kernel) uses the same kw, so their sums agree bit for bit.
+static Plan plan_for(int64_t K, int64_t N, int64_t M = 1, int group = 128) {
   Plan p;
   const int rows = (int)(K / 8);
   p.splits = (rows + kRowsPerWG - 1) / kRowsPerWG;
   p.col_tiles = (int)((N + kTileN - 1) / kTileN);
+  p.kw = 1;
+  const int64_t waves = (int64_t)p.splits * p.col_tiles * 4;
+  if (M == 1 && waves < 1536) {   // measured: stacking does not pay from 1536 waves up
+    const int gr = group / 32;
+    while (p.kw < 4 && waves * p.kw < 2048 && (kRowQuads / (2 * p.kw)) % gr == 0) p.kw *= 2;
+  }
   return p;
 }
 
@@ -589,36 +615,48 @@ static Plan plan_for(int64_t K, int64_t N) {
 constexpr int64_t kCounterBytes = 16384;   // 4096 column tiles: N <= 1M
 static int g_inkernel_reduce = 1;
 
-template <int MR, int GR>
+template <int MR, int GR, int KW>
 static void launch_fmt(const W4Args& a, int fmt, dim3 grid, hipStream_t s) {
-  const dim3 block(256);
+  const dim3 block(256 * KW);
   if (fmt == MTL_META_QSZ)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_QSZ, XSRC_BF16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_QSZ, XSRC_BF16, KW>), grid, block, 0, s, a);
   else if (a.xpart)
-    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_SILU_PART>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_SILU_PART, KW>), grid, block, 0, s, a);
   else if (a.hn)
-    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_RMSNORM>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<1, GR, MTL_META_GPTQ, XSRC_RMSNORM, KW>), grid, block, 0, s, a);
   else if (a.perm)
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_PERM>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_PERM, KW>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_BF16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((w4_gemm_kernel<MR, GR, MTL_META_GPTQ, XSRC_BF16, KW>), grid, block, 0, s, a);
+}
+
+template <int MR, int GR>
+static void launch_kw(const W4Args& a, int fmt, int kw, dim3 grid, hipStream_t s) {
+  if constexpr (MR == 1) {
+    if (kw == 4) {
+      if constexpr (kRowQuads / 4 % GR == 0) { launch_fmt<MR, GR, 4>(a, fmt, grid, s); return; }
+    } else if (kw == 2) {
+      if constexpr (kRowQuads / 2 % GR == 0) { launch_fmt<MR, GR, 2>(a, fmt, grid, s); return; }
+    }
+  }
+  launch_fmt<MR, GR, 1>(a, fmt, grid, s);
 }
 
 // Row quads per quantisation group: group / 32.
 template <int MR>
-static void launch_gr(const W4Args& a, int fmt, dim3 grid, hipStream_t s) {
+static void launch_gr(const W4Args& a, int fmt, int kw, dim3 grid, hipStream_t s) {
   switch (a.group) {
-    case 32: launch_fmt<MR, 1>(a, fmt, grid, s); break;
-    case 64: launch_fmt<MR, 2>(a, fmt, grid, s); break;
-    case 128: launch_fmt<MR, 4>(a, fmt, grid, s); break;
-    default: launch_fmt<MR, 8>(a, fmt, grid, s); break;
+    case 32: launch_kw<MR, 1>(a, fmt, kw, grid, s); break;
+    case 64: launch_kw<MR, 2>(a, fmt, kw, grid, s); break;
+    case 128: launch_kw<MR, 4>(a, fmt, kw, grid, s); break;
+    default: launch_kw<MR, 8>(a, fmt, kw, grid, s); break;
   }
 }
 
 static void launch_w4(const W4Args& a, int fmt, const Plan& p, hipStream_t s) {
   const dim3 grid(p.col_tiles, p.splits);
-  if (a.M == 1) launch_gr<1>(a, fmt, grid, s);
-  else launch_gr<16>(a, fmt, grid, s);
+  if (a.M == 1) launch_gr<1>(a, fmt, p.kw, grid, s);
+  else launch_gr<16>(a, fmt, 1, grid, s);
 }
 
 // The buffer descriptor's size and offsets are 32-bit: the weight rows of the last
@@ -673,7 +711,7 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   if (fmt == MTL_META_QSZ && !aligned16(meta0)) return MTL_ERR_ALIGN;
   if (fmt == MTL_META_GPTQ && (reinterpret_cast<uintptr_t>(meta0) & 7u)) return MTL_ERR_ALIGN;
 
-  const Plan p = plan_for(K, N);
+  const Plan p = plan_for(K, N, M, group);
   W4Args a = blank_args();
   a.x = static_cast<const uint16_t*>(x);
   a.qweight = reinterpret_cast<const u32x4*>(qweight);
@@ -728,7 +766,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   if (!aligned16(qweight) || !aligned16(partials) || (perm && !aligned16(perm)))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
-  const Plan p = plan_for(K, N);
+  const Plan p = plan_for(K, N, M, group);
   if (partials_bytes < (int64_t)p.splits * M * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
   a.x = static_cast<const uint16_t*>(x);
@@ -765,7 +803,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
-  const Plan p = plan_for(K, N);
+  const Plan p = plan_for(K, N, 1, group);
   if (partials_bytes < (int64_t)p.splits * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
   a.qweight = reinterpret_cast<const u32x4*>(qweight);
