@@ -198,7 +198,7 @@ def bench_decode(args, torch):
     cfg = BackboneConfig(max_seq=max(1536, ((total + 255) // 256) * 256))
     t0 = time.time()
     model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev), dev)
-    dec = FastDecoder(model)
+    dec = FastDecoder(model, plan=args.plan)
     gen = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen)
     dec.prefill(prompt)
@@ -381,6 +381,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--plan", default="staged", choices=["fused", "staged", "partials", "unfused"],
+                    help="decode launch plan (decode workload)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

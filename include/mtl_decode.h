@@ -109,11 +109,11 @@ int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, voi
 /*
  * Residual add of the norm-staged step (moss_tts_lite/fast.py:168-169): with partials
  * (fp32 [splits, n] of the o or down GEMV) h = bf16(bf16(sum of partials) + h) in place;
- * without, h is only read.  slots float[16] receives the sum of squares of h over 16
- * equal blocks (consumed by mtl_w4_gemm_norm_partials / mtl_bf16_gemv_argmax_norm, which
- * apply the RMSNorm of model.py:34-40).  h_ord (optional) receives h scattered into the
- * next int4 GEMV's act-order input order: h_ord[scatter[i]] = h[i] (scatter NULL: copy).
- * n % 64 == 0.
+ * without, h is only read.  slots[b] receives the sum of squares of h over columns
+ * 256b .. 256b+255 (consumed by mtl_w4_gemm_norm_partials / mtl_bf16_gemv_argmax_norm,
+ * which apply the RMSNorm of model.py:34-40).  h_ord (optional) receives h scattered
+ * into the next int4 GEMV's act-order input order: h_ord[scatter[i]] = h[i] (scatter
+ * NULL: copy).  n % 4 == 0, n <= 16384.
  */
 int mtl_residual_add(const float* partials, int32_t splits, void* h, const int32_t* scatter,
                      void* h_ord, float* slots, int64_t n, void* stream);
@@ -133,7 +133,7 @@ int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const 
 
 /*
  * mtl_bf16_gemv_argmax on x = RMSNorm(h, norm_w) (the final norm, model.py:34-40 and
- * fast.py:179-180), with h's block sums of squares in slots[16] (mtl_residual_add).
+ * fast.py:179-180), with h's sums of squares per 256 columns in slots.
  */
 int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
                               const void* w, int64_t N, int64_t K, void* logits,

@@ -169,15 +169,33 @@ int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int
 /*
  * Partials-only launch (M = 1) whose activation is RMSNorm(h) computed while staging
  * (moss_tts_lite/model.py:34-40): x[j] = bf16(w[j] * bf16(h[j] * r)),
- * r = rsqrt(sum(slots[0..15]) / K + eps).  h and w are bf16 [K], already in this
- * GEMV's act-order input order (w is the norm weight gathered by the same perm);
- * slots float[16] are the block sums of squares from mtl_residual_add.
+ * r = rsqrt(sum(slots[0 .. ceil(K/256) - 1]) / K + eps).  h and w are bf16 [K], already
+ * in this GEMV's act-order input order (w is the norm weight gathered by the same
+ * perm); slots are the sums of squares of h per 256 columns (mtl_residual_add,
+ * mtl_w4_gemm_residual).
  */
 int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
                               int64_t K, const int32_t* qweight, const void* scales,
                               const int32_t* qzeros, int64_t N, int32_t group_size,
                               int32_t zero_offset, float* partials, int64_t partials_bytes,
                               void* stream);
+
+/*
+ * M = 1 GEMV whose epilogue is the decode step's residual add (moss_tts_lite/fast.py:
+ * 168-171), split-K reduced inside the kernel: h[n] = bf16(bf16((x @ W)[n]) + h[n]) in
+ * place, h scattered into the next RMSNorm-staged GEMV's act-order input order
+ * (h_ord[scatter[n]] = h[n]; scatter NULL: h_ord[n] = h[n]; h_ord NULL: no copy), and
+ * slots[b] = sum of h^2 over columns 256b .. 256b+255 (what mtl_w4_gemm_norm_partials
+ * and mtl_bf16_gemv_argmax_norm consume).  x is bf16 [K] or, with xpart, SiLU*up of an
+ * interleaved gate|up GEMV's partials (as mtl_w4_gemm_partials).  workspace: as
+ * mtl_gptq_gemm (counters zero before first use; every launch leaves them zero).
+ * N <= 16384.
+ */
+int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
+                         int64_t K, const int32_t* qweight, const void* scales,
+                         const int32_t* qzeros, int64_t N, int32_t group_size, int32_t zero_offset,
+                         void* h, const int32_t* scatter, void* h_ord, float* slots,
+                         void* workspace, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

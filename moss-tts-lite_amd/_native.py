@@ -74,6 +74,9 @@ _SIGNATURES = {
     "mtl_w4_gemm_partials": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _c_void_p,
                                     _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _c_void_p,
                                     _i64, _c_void_p]),
+    "mtl_w4_gemm_residual": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _c_void_p,
+                                    _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
+                                    _c_void_p, _c_void_p, _i64, _c_void_p]),
     "mtl_w4_gemm_norm_partials": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                          _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32,
                                          _c_void_p, _i64, _c_void_p]),

@@ -41,6 +41,24 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
+// Butterfly sum over the 64 lanes of a wave (fixed order: bitwise repeatable).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Sums of squares of the residual stream h travel between kernels as one slot per
+// 256-column block (slots[b] = sum over h[256b .. 256b+255] of h^2); the RMSNorm that
+// consumes them sums the ceil(n/256) slots with one wave.
+constexpr int kSlotCols = 256;
+constexpr int kMaxSlots = 64;   // hidden <= 16384
+
+__device__ __forceinline__ float slot_total(const float* slots, int n, int lane) {
+  const int ns = (n + kSlotCols - 1) / kSlotCols;
+  return wave_sum(lane < ns ? slots[lane] : 0.f);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int launch_status() {

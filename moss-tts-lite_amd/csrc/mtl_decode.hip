@@ -11,12 +11,6 @@ namespace mtl {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -153,20 +147,17 @@ __global__ void __launch_bounds__(kNormThreads) residual_rmsnorm_kernel(
 
 // ----------------------------------------------------------------------------------
 // Residual add without the norm (the next int4 GEMV applies RMSNorm while staging):
-// h = bf16(bf16(sum of split-K partials) + h) over 16 blocks of the hidden dim; each
-// block publishes its sum of squares (slots[16]) and scatters h into the next GEMV's
-// act-order input order (h_ord[scatter[i]] = h[i]).
+// h = bf16(bf16(sum of split-K partials) + h), one workgroup per 256-column block;
+// each block publishes its sum of squares (slots[b]) and scatters h into the next
+// GEMV's act-order input order (h_ord[scatter[i]] = h[i]).
 // ----------------------------------------------------------------------------------
-constexpr int kNormSlots = 16;
-
 __global__ void __launch_bounds__(64) residual_add_kernel(
     const float* __restrict__ part, int splits, uint16_t* h, const int32_t* __restrict__ scatter,
     uint16_t* __restrict__ h_ord, float* __restrict__ slots, int n) {
   const int b = blockIdx.x, t = threadIdx.x;
-  const int per = n / kNormSlots;
+  const int i = b * kSlotCols + 4 * t;   // this thread's 4 columns
   float ss = 0.f;
-  for (int q = t; q < per / 4; q += 64) {
-    const int i = b * per + 4 * q;
+  if (i < n) {
     const uint2 rr = *reinterpret_cast<const uint2*>(h + i);
     float hv[4] = {lo_bf(rr.x), hi_bf(rr.x), lo_bf(rr.y), hi_bf(rr.y)};
     if (part) {
@@ -604,10 +595,7 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
     xv[i] = (i < kit && k < K) ? *reinterpret_cast<const u32x4*>(x + k) : u32x4{0u, 0u, 0u, 0u};
   }
   if (norm_w) {   // x is the residual stream: apply the final RMSNorm here (model.py:34-40)
-    float ssum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kNormSlots; ++i) ssum += slots[i];
-    const float r = rsqrtf(ssum / (float)K + eps);
+    const float r = rsqrtf(slot_total(slots, K, lane) / (float)K + eps);
 #pragma unroll
     for (int i = 0; i < kHeadKit; ++i) {
       const int k = 512 * i + 8 * lane;
@@ -880,10 +868,11 @@ int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, voi
 int mtl_residual_add(const float* partials, int32_t splits, void* h, const int32_t* scatter,
                      void* h_ord, float* slots, int64_t n, void* stream) {
   if (!h || !slots) return MTL_ERR_INVALID_ARG;
-  if (n < 64 || n % 64 != 0 || n > (1 << 20)) return MTL_ERR_SHAPE;
+  if (n < 4 || n % 4 != 0 || n > kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
   if (partials && splits < 1) return MTL_ERR_SHAPE;
   if ((partials && !aligned16(partials)) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
-  hipLaunchKernelGGL(residual_add_kernel, dim3(kNormSlots), dim3(64), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + kSlotCols - 1) / kSlotCols)),
+                     dim3(64), 0, (hipStream_t)stream,
                      partials, splits, static_cast<uint16_t*>(h), scatter,
                      static_cast<uint16_t*>(h_ord), slots, (int)n);
   return launch_status();

@@ -52,8 +52,11 @@ struct W4Args {
   int xsplits, xpart_ld;
   const uint16_t* hn;       // XSRC_RMSNORM: residual stream h [K] (act-order order)
   const uint16_t* wn;       //               norm weight [K] (same order)
-  const float* slots;       //               per-block sums of squares of h [nslots]
+  const float* slots;       //               sums of squares of h, one per 256 columns
   float eps;
+  uint16_t* h_ord;          // EPI_RESIDUAL_SLOTS: h scattered into the next GEMV's order
+  const int32_t* scatter;   //   h_ord[scatter[n]] = h[n] (NULL: h_ord[n] = h[n])
+  float* slots_out;         //   slots_out[tile] = sum of h^2 over the tile's 256 columns
   const uint16_t* resid;    // RESIDUAL epilogue input [M, N]
   void* y;
   float* partial;           // [splits, M, N]
@@ -85,7 +88,9 @@ enum : int {
                       // act-order input order) and r = rsqrt(sum(slots)/K + eps)
 };
 
-constexpr int kNormSlots = 16;   // sums of squares published by the residual kernel
+// Internal epilogue of mtl_w4_gemm_residual: h = bf16(bf16(acc) + h) in place, h scattered
+// to h_ord, per-tile sums of squares of h to slots_out (M = 1, reduced in the kernel).
+constexpr int kEpiResidualSlots = 3;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -172,7 +177,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   //    MR = 1 (threads 0..63).  Raw values now; transformed once the loads are back.
   u32x4 xv[XPT], wv[XSRC == XSRC_RMSNORM ? XPT : 1];
   bool xok[XPT];
-  float4 slot4[XSRC == XSRC_RMSNORM ? kNormSlots / 4 : 1];
+  float slot_v = 0.f;                         // XSRC_RMSNORM: lane's sum-of-squares slot
   const bool stager = MR > 1 || t < kRowsPerWG;
   auto load_x = [&]() {
 #pragma unroll
@@ -227,8 +232,8 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
     silu_batch(0);
   }
   if (XSRC == XSRC_RMSNORM) {
-#pragma unroll
-    for (int i = 0; i < kNormSlots / 4; ++i) slot4[i] = ld_f4(a.slots + 4 * i);
+    const int ns = (a.K + kSlotCols - 1) / kSlotCols;
+    if (stager && lane < ns) slot_v = a.slots[lane];
   }
 
   // 2. Group metadata of the lane's 4 columns, one entry per group of the split.
@@ -288,13 +293,8 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   }
   if (stager) {
     float norm_r = 0.f;
-    if (XSRC == XSRC_RMSNORM) {   // rsqrt(mean(h^2) + eps), slots summed in order
-      float ssum = 0.f;
-#pragma unroll
-      for (int i = 0; i < kNormSlots / 4; ++i)
-        ssum += ((slot4[i].x + slot4[i].y) + (slot4[i].z + slot4[i].w));
-      norm_r = rsqrtf(ssum / (float)a.K + a.eps);
-    }
+    if (XSRC == XSRC_RMSNORM)     // rsqrt(mean(h^2) + eps) from the slots (one wave)
+      norm_r = rsqrtf(wave_sum(slot_v) / (float)a.K + a.eps);
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
       const int m = MR == 1 ? 0 : (t >> 6) + 4 * j;
@@ -402,8 +402,9 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   // 7. Split-K.  Every workgroup publishes its fp32 partial tile.  With an in-kernel
   //    reduction the partials travel as relaxed agent-scope atomics (coherent across
   //    XCDs without a whole-L2 writeback), a per-tile counter names the last workgroup,
-  //    and that one sums all splits in split order (loads batched 8 deep) and resets
-  //    the counter.  Otherwise w4_reduce_kernel (or a fused consumer) sums them.
+  //    and that one sums all splits in split order (one column per thread, up to 32
+  //    loads in flight) and resets the counter.  Otherwise w4_reduce_kernel (or a
+  //    fused consumer) sums them.
   if (a.splits > 1 || a.partials_only) {
     float* pbase = a.partial + (size_t)split * M * N + ecol;
     if (!a.inkernel_reduce || a.partials_only) {
@@ -418,16 +419,19 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
       }
       return;
     }
-    if (active && ecol_ok) {
+    // publish and reduce one column per thread (threads 0..255), all split loads of a
+    // row in flight together; the sums then go through LDS to the epilogue mapping
+    const int pc = t & (kTileN - 1);
+    const int pcol = tile * kTileN + pc;
+    const bool pub = t < kTileN && pcol < N;
+    const int mrows = MR < M ? MR : M;
+    if (pub) {
+      for (int m = 0; m < mrows; ++m) {
+        float val = 0.f;
 #pragma unroll
-      for (int j = 0; j < RPT; ++j) {
-        const int m = wave + 4 * j;
-        if (m < M) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            __hip_atomic_store(pbase + (size_t)m * N + c, v[j][c], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int k = 0; k < KW; ++k) val += ytile[k][m][pc];   // as the epilogue mapping sums
+        __hip_atomic_store(a.partial + ((size_t)split * M + m) * N + pcol, val, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);   // every partial store acknowledged before the count
@@ -441,38 +445,61 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
     if (t == 0)
       __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int S = a.splits;
-    const size_t stride = (size_t)M * N;
+    if (pub) {
+      for (int m = 0; m < mrows; ++m) {
+        const float* q = a.partial + (size_t)m * N + pcol;
+        float sum = 0.f;
+        for (int s0 = 0; s0 < S; s0 += 32) {
+          float pv[32];
+#pragma unroll
+          for (int jj = 0; jj < 32; ++jj) {
+            const int sp = s0 + jj < S ? s0 + jj : S - 1;
+            pv[jj] = __hip_atomic_load(q + (size_t)sp * M * N, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int jj = 0; jj < 32; ++jj)
+            if (s0 + jj < S) sum += pv[jj];                  // split order
+        }
+        ytile[0][m][pc] = sum;
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const int m = wave + 4 * j;
-      float s4[4] = {0.f, 0.f, 0.f, 0.f};
-      if (active && ecol_ok && m < M) {
-        const float* q = a.partial + (size_t)m * N + ecol;
-        for (int s0 = 0; s0 < S; s0 += 8) {
-          float pv[8][4];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            const int sp = s0 + jj < S ? s0 + jj : S - 1;
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              pv[jj][c] = __hip_atomic_load(q + sp * stride + c, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-          }
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj)
-            if (s0 + jj < S) {
-#pragma unroll
-              for (int c = 0; c < 4; ++c) s4[c] += pv[jj][c];
-            }
-        }
+      if (m < MR) {
+        const float4 y4 = *reinterpret_cast<const float4*>(&ytile[0][m][4 * lane]);
+        v[j][0] = y4.x; v[j][1] = y4.y; v[j][2] = y4.z; v[j][3] = y4.w;
       }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) v[j][c] = s4[c];
     }
   }
   if (!active) return;
 
   // 8. Epilogue, 4 consecutive columns per thread.
+  if (MR == 1 && a.epilogue == kEpiResidualSlots) {
+    // the residual add of fast.py:168-171, publishing what the next RMSNorm needs
+    float ss = 0.f;
+    if (ecol_ok) {
+      const u32x2 rr = *reinterpret_cast<const u32x2*>(a.resid + ecol);
+      float hv[4] = {bf16_to_f32(rr.x & 0xffffu), bf16_to_f32(rr.x >> 16),
+                     bf16_to_f32(rr.y & 0xffffu), bf16_to_f32(rr.y >> 16)};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) hv[c] = round_bf16(round_bf16(v[0][c]) + hv[c]);
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + ecol) =
+          u32x2{f32_to_bf16(hv[0]) | (f32_to_bf16(hv[1]) << 16),
+                f32_to_bf16(hv[2]) | (f32_to_bf16(hv[3]) << 16)};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        ss = fmaf(hv[c], hv[c], ss);
+        if (a.h_ord)
+          a.h_ord[a.scatter ? a.scatter[ecol + c] : ecol + c] = (uint16_t)f32_to_bf16(hv[c]);
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) a.slots_out[tile] = ss;
+    return;
+  }
   if (a.epilogue == MTL_EPI_SILU_MUL) {
     // Fused columns come in blocks of 64 = 32 gate | 32 up; lane l (l%16 < 8) holds
     // gate columns whose up partners sit 8 lanes higher.
@@ -679,6 +706,9 @@ static W4Args blank_args() {
   a.wn = nullptr;
   a.slots = nullptr;
   a.eps = 0.f;
+  a.h_ord = nullptr;
+  a.scatter = nullptr;
+  a.slots_out = nullptr;
   a.resid = nullptr;
   a.y = nullptr;
   a.partial = nullptr;
@@ -799,7 +829,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (!aligned16(slots)) return MTL_ERR_ALIGN;
-  if (!weight_fits(K, N)) return MTL_ERR_SHAPE;
+  if (!weight_fits(K, N) || K > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
   if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
@@ -820,6 +850,59 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   a.epilogue = MTL_EPI_NONE;
   a.out_f32 = 1;
   a.partials_only = 1;
+  launch_w4(a, MTL_META_GPTQ, p, stream);
+  return launch_status();
+}
+
+// M = 1 GEMV whose epilogue is the decode step's residual add (reduced in the kernel):
+// h = bf16(bf16(x @ W) + h); h_ord[scatter[n]] = h[n]; slots[tile] = sum of h^2 over each
+// 256-column tile.  x from `x` (bf16) or the gate|up partials (`xpart`, SiLU*up).
+static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
+                            int64_t K, const int32_t* qweight, const void* meta0,
+                            const int32_t* qzeros, int64_t N, int group, int zero_offset,
+                            void* h, const int32_t* scatter, void* h_ord, float* slots,
+                            void* workspace, int64_t ws_bytes, hipStream_t stream) {
+  if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !h || !slots)
+    return MTL_ERR_INVALID_ARG;
+  if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
+  if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  if (N > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
+  if (!weight_fits(K, N)) return MTL_ERR_SHAPE;
+  if (xpart) {
+    if (xsplits < 1 || xpart_ld != 2 * K) return MTL_ERR_SHAPE;
+    if (!aligned16(xpart)) return MTL_ERR_ALIGN;
+  } else if (!aligned16(x)) {
+    return MTL_ERR_ALIGN;
+  }
+  if (!aligned16(qweight) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  const Plan p = plan_for(K, N, 1, group);
+  W4Args a = blank_args();
+  if (p.splits > 1) {
+    const int64_t need = kCounterBytes + (int64_t)p.splits * N * 4;
+    if (!workspace || ws_bytes < need) return MTL_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MTL_ERR_ALIGN;
+    a.counters = static_cast<unsigned*>(workspace);
+    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  }
+  a.x = static_cast<const uint16_t*>(x);
+  a.qweight = reinterpret_cast<const u32x4*>(qweight);
+  a.meta0 = static_cast<const uint16_t*>(meta0);
+  a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
+  a.xpart = xpart;
+  a.xsplits = xsplits;
+  a.xpart_ld = (int)xpart_ld;
+  a.resid = static_cast<const uint16_t*>(h);
+  a.y = h;
+  a.h_ord = static_cast<uint16_t*>(h_ord);
+  a.scatter = scatter;
+  a.slots_out = slots;
+  a.M = 1; a.K = (int)K; a.N = (int)N;
+  a.group = group; a.zero_offset = zero_offset;
+  a.splits = p.splits;
+  a.epilogue = kEpiResidualSlots;
+  a.out_f32 = 0;
+  a.inkernel_reduce = 1;
   launch_w4(a, MTL_META_GPTQ, p, stream);
   return launch_status();
 }
@@ -891,6 +974,16 @@ int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, 
   return w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N,
                                group_size, zero_offset, partials, partials_bytes,
                                (hipStream_t)stream);
+}
+
+int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
+                         int64_t K, const int32_t* qweight, const void* scales,
+                         const int32_t* qzeros, int64_t N, int32_t group_size, int32_t zero_offset,
+                         void* h, const int32_t* scatter, void* h_ord, float* slots,
+                         void* workspace, int64_t ws_bytes, void* stream) {
+  return w4_gemm_residual(x, xpart, xsplits, xpart_ld, K, qweight, scales, qzeros, N, group_size,
+                          zero_offset, h, scatter, h_ord, slots, workspace, ws_bytes,
+                          (hipStream_t)stream);
 }
 
 int mtl_gptq_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight,

@@ -15,7 +15,7 @@ Every launch is a plain C-ABI call on torch's current stream; the launch plan (a
 pointers, sizes, workspaces) is built once, so eager steps and graph capture issue the
 identical kernel sequence.
 
-Three launch plans produce the same step:
+Four launch plans produce the same step:
 
 * ``"staged"`` (default): each int4 GEMV publishes only its split-K partials and the
   consumer folds the reduction in.  A 16-workgroup residual add sums the o/down
@@ -25,6 +25,11 @@ Three launch plans produce the same step:
   from the q|k|v partials (q/k norm, RoPE, KV write inside), its combine scatters into
   the o projection's input order, down stages SiLU*up from the gate|up partials and the
   head applies the final norm.  8 launches per layer.
+* ``"fused"``: five launches per layer.  As ``"staged"``, except that the o and down
+  GEMVs reduce their split-K partials inside the kernel and apply the residual add in
+  their epilogue, publishing the sums of squares and the scattered copy of ``h`` the
+  next RMSNorm-staged GEMV reads.  Bitwise equal to ``"staged"``; measured slower on
+  MI355X (the in-kernel cross-workgroup hand-off costs more than the separate kernel).
 * ``"partials"``: the same partials hand-off, with a single-workgroup residual+RMSNorm
   kernel and a separate q/k norm+RoPE kernel (9 launches per layer).
 * ``"unfused"``: each GEMV runs to completion (in-kernel reduction and epilogue).
@@ -56,7 +61,7 @@ def _gather(w: torch.Tensor, perm: torch.Tensor | None) -> torch.Tensor:
 class FastDecoder:
     """One decode step over an :class:`Int4Backbone` (eager or hipGraph replay)."""
 
-    PLANS = ("staged", "partials", "unfused")
+    PLANS = ("fused", "staged", "partials", "unfused")
 
     def __init__(self, model: Int4Backbone, plan: str = "staged"):
         if plan not in self.PLANS:
@@ -98,7 +103,12 @@ class FastDecoder:
         self.x_qkv = torch.zeros(cfg.hidden, dtype=bf, device=dev)
         self.x_o = torch.zeros(cfg.hidden, dtype=bf, device=dev)
         self.x_gu = torch.zeros(cfg.hidden, dtype=bf, device=dev)
-        self.slots = torch.zeros(16, dtype=torch.float32, device=dev)
+        self.slots = torch.zeros(64, dtype=torch.float32, device=dev)   # sum h^2 per 256 cols
+        # split-K workspace of the residual GEMVs (o, down): counters stay zero between launches
+        self.res_ws = torch.zeros(max(ops.gemm_workspace_bytes(1, cfg.hidden, cfg.hidden, cfg.group_size),
+                                      ops.gemm_workspace_bytes(1, cfg.intermediate, cfg.hidden,
+                                                               cfg.group_size)),
+                                  dtype=torch.uint8, device=dev)
         self.inv_perm_o, self.inv_perm_qkv, self.inv_perm_gu = [], [], []
         self.norm_qkv, self.norm_gu = [], []      # norm weights gathered by the GEMV's perm
         for lyr in model.layers:
@@ -212,6 +222,53 @@ class FastDecoder:
             self._partials(None, "gate_up", lyr["down"], cfg.hidden, "down"),
         ]
 
+    def _layer_plan_resid(self, li: int) -> list:
+        """Five launches: q|k|v (RMSNorm staged), attention, o with the residual add in
+        its epilogue, gate|up (RMSNorm staged), down with the residual add."""
+        m, cfg = self.m, self.m.cfg
+        lyr = m.layers[li]
+        kc, vc = m.k_cache[li], m.v_cache[li]
+        scale = ctypes.c_float(attention_scale(cfg))
+        eps = ctypes.c_float(cfg.eps)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+            raise RuntimeError("fused plan needs gate|up columns in the down input order")
+        last = li + 1 == cfg.n_layers
+        plan = []
+        if li == 0:   # statistics and act-order copy of the embedding output
+            plan.append(("mtl_residual_add", (None, 0, self.h.data_ptr(), p(self.inv_perm_qkv[0]),
+                                              self.x_qkv.data_ptr(), self.slots.data_ptr(),
+                                              cfg.hidden)))
+        plan += [
+            self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"], cfg.qkv_out, "qkv"),
+            ("mtl_decode_attention_fused", (self.part["qkv"].data_ptr(), self.splits["qkv"],
+                                            lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(),
+                                            m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
+                                            kc.data_ptr(), vc.data_ptr(), self.pos.data_ptr(),
+                                            self.x_o.data_ptr(), p(self.inv_perm_o[li]),
+                                            cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                            cfg.max_seq, scale, eps, self.attn_ws.data_ptr(),
+                                            self.attn_ws.numel())),
+            self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu),
+            self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"],
+                                2 * cfg.intermediate, "gate_up"),
+            self._residual(None, "gate_up", lyr["down"],
+                           None if last else self.inv_perm_qkv[li + 1],
+                           None if last else self.x_qkv),
+        ]
+        return plan
+
+    def _residual(self, x, xpart_name, lin, scatter, h_ord):
+        qw, qz, sc, _ = lin.kernel_args()
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        xpart = self.part[xpart_name] if xpart_name else None
+        return ("mtl_w4_gemm_residual",
+                (p(x), p(xpart), self.splits[xpart_name] if xpart_name else 0,
+                 2 * lin.in_features if xpart_name else 0, lin.in_features, qw.data_ptr(),
+                 sc.data_ptr(), qz.data_ptr(), lin.out_features, lin.group_size,
+                 lin.zero_offset, self.h.data_ptr(), p(scatter), p(h_ord),
+                 self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel()))
+
     def _norm_partials(self, h_ord, w_ord, lin, n, name):
         qw, qz, sc, _ = lin.kernel_args()
         out = self.part[name]
@@ -255,7 +312,9 @@ class FastDecoder:
         self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), self.table_ptrs.numel(),
                                           self.table_ptrs.data_ptr(), self.vocabs.data_ptr(),
                                           cfg.hidden, self.h.data_ptr()))]
-        if self.plan == "staged":
+        if self.plan == "fused":
+            self._layers = [self._layer_plan_resid(li) for li in range(cfg.n_layers)]
+        elif self.plan == "staged":
             self._layers = [self._layer_plan_staged(li) for li in range(cfg.n_layers)]
         elif self.plan == "partials":
             self._layers = [self._layer_plan_fused(li) for li in range(cfg.n_layers)]
@@ -268,13 +327,13 @@ class FastDecoder:
                       "mtl_advance_position", "mtl_w4_gemm_partials",
                       "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
                       "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
-                      "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv")}
+                      "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
         m, cfg = self.m, self.m.cfg
         eps = ctypes.c_float(cfg.eps)
-        if self.plan == "unfused":
+        if self.plan in ("unfused", "fused"):   # h is complete
             return [("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(),
                                      self.h_final.data_ptr(), 1, cfg.hidden, eps))]
         return [("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
@@ -286,9 +345,9 @@ class FastDecoder:
         """Final norm, head, greedy token into ``ids``, position + 1."""
         m, cfg = self.m, self.m.cfg
         eps = ctypes.c_float(cfg.eps)
-        if self.plan == "staged":   # the head applies the final norm while staging
-            final = [self._flush_staged(),
-                     ("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
+        if self.plan in ("staged", "fused"):   # the head applies the final norm while staging
+            final = [] if self.plan == "fused" else [self._flush_staged()]
+            final += [("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
                                                     self.slots.data_ptr(), eps, m.head.data_ptr(),
                                                     cfg.vocab, cfg.hidden, self.logits.data_ptr(),
                                                     ctypes.c_void_p(self.ids.data_ptr()),
@@ -308,13 +367,15 @@ class FastDecoder:
                                      self.m.cfg.hidden))
 
     # position of each int4 GEMV launch inside a layer's plan
-    _GEMV_AT = {"staged": {"qkv": 1, "o": 3, "gate_up": 5, "down": 6},
+    _GEMV_AT = {"fused": {"qkv": 0, "o": 2, "gate_up": 3, "down": 4},
+                "staged": {"qkv": 1, "o": 3, "gate_up": 5, "down": 6},
                 "partials": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7},
                 "unfused": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7}}
 
     def gemv_launch(self, li: int, name: str):
         """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
-        return self._layers[li][self._GEMV_AT[self.plan][name]]
+        shift = 1 if self.plan == "fused" and li == 0 else 0   # layer 0 opens with the stats
+        return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:
         """Issue only that GEMV (timing; its inputs are whatever the buffers hold)."""
@@ -335,7 +396,8 @@ class FastDecoder:
         self._run(self._layers[li])
 
     def flush_residual(self) -> None:
-        """Partials plans: fold the pending down-projection partials into ``self.h``."""
+        """Partials plans: fold the pending down-projection partials into ``self.h``
+        (the fused and unfused plans leave nothing pending)."""
         if self.plan == "staged":
             self._run([self._flush_staged()])
         elif self.plan == "partials":

@@ -237,14 +237,19 @@ def test_launch_plans_agree(dev):
             dec.run_step()
             logits.append(fb(dec.logits))
         out[plan] = (toks, logits)
-    for plan in ("staged", "partials"):
+    for plan in ("fused", "staged", "partials"):
         for i in range(6):
             err = rel_l2(out[plan][1][i], out["unfused"][1][i])
             print(f"step {i}: {plan} vs unfused logits rel_l2={err:.2e}")
             assert err < 5e-3
+    # the fused plan only moves the residual add into the GEMV epilogue: same sums in the
+    # same order as partials + residual kernel, so the steps agree bit for bit
+    assert out["fused"][0] == out["staged"][0]
+    for i in range(6):
+        assert np.array_equal(out["fused"][1][i], out["staged"][1][i]), f"step {i}"
 
 
-@pytest.mark.parametrize("plan", ["staged", "partials"])
+@pytest.mark.parametrize("plan", ["fused", "staged", "partials"])
 def test_plan_graph_replay_is_bitwise(dev, plan):
     cfg = small_config()
     model, _ = build_case(cfg, seed=23, dev=dev)
@@ -519,7 +524,7 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     assert int(tok.item()) == int(np.argmax(fb(logits)))
 
 
-@pytest.mark.parametrize("plan", ["staged", "unfused"])
+@pytest.mark.parametrize("plan", ["fused", "unfused"])
 def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
     # MOSS step: 33-way (here 1 + 4) embedding, layers, final norm, text + audio heads
     # (pad code -inf) or the audio2 variant (2-way + audio heads); graph == eager.
@@ -561,3 +566,49 @@ def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
         for a, b in zip(e, out):
             assert torch.equal(a, b)
     del hf_dev, eager
+
+
+@pytest.mark.parametrize("src", ["bf16", "silu"])
+def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
+    # mtl_w4_gemm_residual == mtl_w4_gemm_partials + mtl_residual_add, bit for bit
+    # (h in place, scattered copy, per-256-column sums of squares), on the o shape
+    # (bf16 x, K=4096) and the down shape (SiLU*up of gate|up partials, K=12288)
+    from oracle import synth
+    from moss_tts_lite_amd import ops
+    n = 4096
+    k = 4096 if src == "bf16" else 12288
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=61 if src == "bf16" else 62,
+                           with_ref=False)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    qw, qz, sc = t(case["qweight"]), t(case["qzeros"]), t(case["scales"].view(np.float16))
+    r = np.random.default_rng(63)
+    h0 = tb(r.standard_normal(n).astype(np.float32), dev)
+    scatter = torch.from_numpy(r.permutation(n).astype(np.int32)).to(dev)
+    if src == "bf16":
+        x = t(case["x_bits"].view(np.int16)).view(torch.bfloat16)
+        xpart, xs, ld = None, 0, 0
+    else:
+        x = None
+        xs = 8
+        xpart = torch.from_numpy((r.standard_normal((xs, 2 * k)) * 0.5).astype(np.float32)).to(dev)
+        ld = 2 * k
+    p = lambda v: None if v is None else v.data_ptr()  # noqa: E731
+    S = int(lib.mtl_w4_gemm_splits(k, n))
+    part = torch.empty(S * n, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_w4_gemm_partials(p(x), p(xpart), xs, ld, 1, k, qw.data_ptr(), sc.data_ptr(),
+                                     qz.data_ptr(), None, n, 128, 0, part.data_ptr(),
+                                     part.numel() * 4, stream()), "partials")
+    h_a, ord_a = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    slots_a = torch.zeros(64, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_residual_add(part.data_ptr(), S, h_a.data_ptr(), scatter.data_ptr(),
+                                 ord_a.data_ptr(), slots_a.data_ptr(), n, stream()), "residual_add")
+    ws = torch.zeros(ops.gemm_workspace_bytes(1, k, n, 128), dtype=torch.uint8, device=dev)
+    for rep in range(2):     # the second launch checks the counters were left at zero
+        h_b, ord_b = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
+        slots_b = torch.zeros(64, dtype=torch.float32, device=dev)
+        N.check(lib.mtl_w4_gemm_residual(p(x), p(xpart), xs, ld, k, qw.data_ptr(), sc.data_ptr(),
+                                         qz.data_ptr(), n, 128, 0, h_b.data_ptr(),
+                                         scatter.data_ptr(), ord_b.data_ptr(), slots_b.data_ptr(),
+                                         ws.data_ptr(), ws.numel(), stream()), "residual gemv")
+        assert torch.equal(h_a, h_b) and torch.equal(ord_a, ord_b)
+        assert torch.equal(slots_a[:n // 256], slots_b[:n // 256])
