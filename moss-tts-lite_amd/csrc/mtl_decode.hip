@@ -294,22 +294,39 @@ constexpr int kAttnMaxRep = 8;        // q heads per kv head
 constexpr int kAttnPart = 132;        // m, l, 2 pad, o[128]
 constexpr int kAttnCounterBytes = 1024;
 
-__device__ __forceinline__ void head_from_partials(const float* __restrict__ part, int splits,
-                                                   int ncols, int head, int t, float& x0,
-                                                   float& x1) {
+// The first 8 split-K partials of one head's dims (t, t+64), loaded ahead of use; the
+// sum (with any further splits) comes later from head_sum.
+struct HeadPart {
+  float v0[8], v1[8];
+};
+
+__device__ __forceinline__ void head_issue(const float* __restrict__ part, int splits, int ncols,
+                                           int head, int t, HeadPart& hp) {
   const float* p0 = part + (size_t)head * 128 + t;
-  float a0 = 0.f, a1 = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    float v0[8], v1[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const size_t off = (size_t)(s0 + j < splits ? s0 + j : splits - 1) * ncols;
-      v0[j] = p0[off];
-      v1[j] = p0[off + 64];
+  for (int j = 0; j < 8; ++j) {
+    const size_t off = (size_t)(j < splits ? j : splits - 1) * ncols;
+    hp.v0[j] = p0[off];
+    hp.v1[j] = p0[off + 64];
+  }
+}
+
+__device__ __forceinline__ void head_sum(const float* __restrict__ part, int splits, int ncols,
+                                         int head, int t, HeadPart& hp, float& x0, float& x1) {
+  float a0 = 0.f, a1 = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {   // splits summed in order
+    if (s0 > 0) {
+      const float* p0 = part + (size_t)head * 128 + t;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const size_t off = (size_t)(s0 + j < splits ? s0 + j : splits - 1) * ncols;
+        hp.v0[j] = p0[off];
+        hp.v1[j] = p0[off + 64];
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (s0 + j < splits) { a0 += v0[j]; a1 += v1[j]; }
+      if (s0 + j < splits) { a0 += hp.v0[j]; a1 += hp.v1[j]; }
   }
   x0 = round_bf16(a0);
   x1 = round_bf16(a1);
@@ -361,6 +378,12 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int n_rep = a.H / a.Hkv;
+  // 0. The q|k|v partials of this wave's first q head (and, on waves 0/1, of this kv
+  //    head's k or v) do not depend on the position: in flight before it is read.
+  const int ncols = (a.H + 2 * a.Hkv) * D;
+  HeadPart hq, hkv;
+  if (FROM_PART && wave < n_rep)
+    head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + wave, lane, hq);
   const int64_t pos = *a.pos;
   int64_t L64 = pos + 1;
   if (L64 < 0) L64 = 0;
@@ -392,17 +415,18 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     }
   };
   if (p0 < p1) load_block(p0);
+  if (FROM_PART && has_pos && wave < 2)   // k (wave 0) or v (wave 1) of position pos
+    head_issue(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv);
 
   // 2. Prologue: q heads into LDS; k/v of position pos (cache + LDS) where it is scored.
   const size_t prow = (size_t)(pos >= 0 && pos < a.max_seq ? pos : 0) * D;
   if (FROM_PART) {
-    const int ncols = (a.H + 2 * a.Hkv) * D;
     const uint16_t* cr = a.cos_tab + prow;
     const uint16_t* sr = a.sin_tab + prow;
     if (has_pos && wave < 2) {
       float x0, x1;
-      head_from_partials(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh,
-                         lane, x0, x1);
+      head_sum(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv,
+               x0, x1);
       if (wave == 0) norm_rope_pair(x0, x1, a.kn, cr, sr, lane, a.eps, x0, x1);
       const uint32_t b0 = f32_to_bf16(x0), b1 = f32_to_bf16(x1);
       uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.max_seq + pos) * D;
@@ -414,7 +438,8 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
     }
     for (int hr = wave; hr < n_rep; hr += 4) {
       float x0, x1;
-      head_from_partials(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, x0, x1);
+      if (hr != wave) head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, hq);
+      head_sum(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, hq, x0, x1);
       norm_rope_pair(x0, x1, a.qn, cr, sr, lane, a.eps, x0, x1);
       uint16_t* l16 = reinterpret_cast<uint16_t*>(q_lds[hr]);
       l16[lane] = (uint16_t)f32_to_bf16(x0);
@@ -513,38 +538,43 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   for (int hr = wave; hr < n_rep; hr += 4) {
     const int h = kvh * n_rep + hr;
     const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
+    // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1 as 64-bit
+    // agent-scope loads, all issued before any use
+    typedef unsigned long long u64;
     float mc = -INFINITY, lc = 0.f;
     if (lane < nch) {
-      mc = __hip_atomic_load(ph + (size_t)lane * kAttnPart, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      lc = __hip_atomic_load(ph + (size_t)lane * kAttnPart + 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+      const u64 ml = __hip_atomic_load(reinterpret_cast<const u64*>(ph + (size_t)lane * kAttnPart),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mc = __uint_as_float((uint32_t)ml);
+      lc = __uint_as_float((uint32_t)(ml >> 32));
     }
-    const float M = wave_max(lc > 0.f ? mc : -INFINITY);
-    const float wc = lc > 0.f ? expf(mc - M) : 0.f;
-    const float Ls = wave_sum(wc * lc);
-    w_lds[wave][lane] = wc;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float o0 = 0.f, o1 = 0.f;
     for (int c0 = 0; c0 < nch; c0 += 16) {
-      float v0[16], v1[16];
+      u64 ov[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int cc = c0 + j < nch ? c0 + j : nch - 1;
-        const float* src = ph + (size_t)cc * kAttnPart + 4 + 2 * lane;
-        v0[j] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        v1[j] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int j = 0; j < 16; ++j)
+        if (c0 + j < nch)
+          ov[j] = __hip_atomic_load(
+              reinterpret_cast<const u64*>(ph + (size_t)(c0 + j) * kAttnPart + 4 + 2 * lane),
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c0 == 0) {
+        const float M = wave_max(lc > 0.f ? mc : -INFINITY);
+        const float wc = lc > 0.f ? expf(mc - M) : 0.f;
+        w_lds[wave][lane] = wc;
+        lc = wave_sum(wc * lc);                        // Ls from here on
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (c0 + j < nch) {
           const float wj = w_lds[wave][c0 + j];
-          o0 = fmaf(wj, v0[j], o0);
-          o1 = fmaf(wj, v1[j], o1);
+          o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
+          o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
         }
     }
+    const float Ls = lc;
     const int i0 = h * D + 2 * lane;
     const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
     a.out[a.out_index ? a.out_index[i0] : i0] = (uint16_t)f32_to_bf16(r0);
