@@ -162,14 +162,14 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
     float hv[4] = {lo_bf(rr.x), hi_bf(rr.x), lo_bf(rr.y), hi_bf(rr.y)};
     if (part) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int s0 = 0; s0 < splits; s0 += 8) {   // 8 independent loads, summed in order
-        float4 pv[8];
+      for (int s0 = 0; s0 < splits; s0 += 32) {   // up to 32 loads in flight, summed in order
+        float4 pv[32];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          pv[j] = *reinterpret_cast<const float4*>(
-              part + (size_t)(s0 + j < splits ? s0 + j : splits - 1) * n + i);
+        for (int j = 0; j < 32; ++j)
+          if (s0 + j < splits)
+            pv[j] = *reinterpret_cast<const float4*>(part + (size_t)(s0 + j) * n + i);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 32; ++j)
           if (s0 + j < splits) {
             acc[0] += pv[j].x; acc[1] += pv[j].y; acc[2] += pv[j].z; acc[3] += pv[j].w;
           }
@@ -646,28 +646,48 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
   }
   float best = 0.f;
   long long bidx = -1;
-  for (int64_t r = r0; r < r1; ++r) {
-    const uint16_t* wr = w + r * K;
-    float acc = 0.f;
+  constexpr int RB = kHeadKit <= 8 ? 2 : 1;   // rows per pass: their loads in flight together
+  for (int64_t rb = r0; rb < r1; rb += RB) {
+    u32x4 ww[RB][kHeadKit];
 #pragma unroll
-    for (int i = 0; i < kHeadKit; ++i) {
-      const int k = 512 * i + 8 * lane;
-      if (i < kit && k < K) {
-        const u32x4 ww = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + k));
-        acc = dot2_bf16(ww.x, xv[i].x, acc);
-        acc = dot2_bf16(ww.y, xv[i].y, acc);
-        acc = dot2_bf16(ww.z, xv[i].z, acc);
-        acc = dot2_bf16(ww.w, xv[i].w, acc);
+    for (int j = 0; j < RB; ++j) {
+      const int64_t r = rb + j < r1 ? rb + j : r1 - 1;
+      const uint16_t* wr = w + r * K;
+#pragma unroll
+      for (int i = 0; i < kHeadKit; ++i) {
+        const int k = 512 * i + 8 * lane;
+        if (i < kit && k < K)
+          ww[j][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + k));
       }
     }
-    acc = wave_sum(acc);
-    uint32_t hb = f32_to_bf16(acc);
-    if (pad_period > 0 && r % pad_period == pad_index) hb = 0xff80u;   // -inf
-    if (logits && lane == 0) logits[r] = (uint16_t)hb;
-    const float lv = bf16_to_f32(hb);
-    if (better(lv, r, best, bidx)) {
-      best = lv;
-      bidx = r;
+    float acc[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      acc[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < kHeadKit; ++i) {
+        const int k = 512 * i + 8 * lane;
+        if (i < kit && k < K) {
+          acc[j] = dot2_bf16(ww[j][i].x, xv[i].x, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].y, xv[i].y, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].z, xv[i].z, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].w, xv[i].w, acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const int64_t r = rb + j;
+      if (r >= r1) break;
+      const float sum = wave_sum(acc[j]);
+      uint32_t hb = f32_to_bf16(sum);
+      if (pad_period > 0 && r % pad_period == pad_index) hb = 0xff80u;   // -inf
+      if (logits && lane == 0) logits[r] = (uint16_t)hb;
+      const float lv = bf16_to_f32(hb);
+      if (better(lv, r, best, bidx)) {   // rows in ascending order: first maximum kept
+        best = lv;
+        bidx = r;
+      }
     }
   }
   if (!part_v) return;   // logits only
