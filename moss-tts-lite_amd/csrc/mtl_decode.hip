@@ -162,14 +162,14 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
     float hv[4] = {lo_bf(rr.x), hi_bf(rr.x), lo_bf(rr.y), hi_bf(rr.y)};
     if (part) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int s0 = 0; s0 < splits; s0 += 32) {   // up to 32 loads in flight, summed in order
-        float4 pv[32];
+      for (int s0 = 0; s0 < splits; s0 += 8) {   // 8 independent loads, summed in order
+        float4 pv[8];
 #pragma unroll
-        for (int j = 0; j < 32; ++j)
-          if (s0 + j < splits)
-            pv[j] = *reinterpret_cast<const float4*>(part + (size_t)(s0 + j) * n + i);
+        for (int j = 0; j < 8; ++j)
+          pv[j] = *reinterpret_cast<const float4*>(
+              part + (size_t)(s0 + j < splits ? s0 + j : splits - 1) * n + i);
 #pragma unroll
-        for (int j = 0; j < 32; ++j)
+        for (int j = 0; j < 8; ++j)
           if (s0 + j < splits) {
             acc[0] += pv[j].x; acc[1] += pv[j].y; acc[2] += pv[j].z; acc[3] += pv[j].w;
           }
