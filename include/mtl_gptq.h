@@ -50,6 +50,13 @@ enum {
                              interleaved in blocks of 32 (gate|up) (fast.py:170-171)  */
 };
 
+/* Weight layout of the decode-step GEMV entries (mtl_w4_gemm_partials,
+ * mtl_w4_gemm_norm_partials, mtl_w4_gemm_residual). */
+enum {
+  MTL_LAYOUT_ROWS = 0,    /* qweight int32 [K/8, N] as everywhere else                  */
+  MTL_LAYOUT_TILED = 1    /* mtl_w4_tile output (M = 1, N % 64 == 0, no perm)           */
+};
+
 /* Metadata format of mtl_w4_gemm_fused. */
 enum {
   MTL_META_GPTQ = 0,      /* scales fp16 [K/g,N] + qzeros int32 [K/g,N/8]; w=(q-z)*s  */
@@ -122,6 +129,17 @@ int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
 int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K,
                          int32_t inner_k_tiles, int32_t* packed, void* stream);
 
+/*
+ * Wave-contiguous copy of a qweight [K/8, N] for the decode-step GEMVs (load time):
+ * 16-byte word l of 1 KB block ((s * N/64 + cg) * 16 + q) holds row 64s + 4q + l/16,
+ * columns 64cg + 4(l%16) .. +3; rows past K/8 are zero.  Each GEMV wave then streams
+ * 16 consecutive 1 KB blocks instead of 64 strided 256-byte pieces.  N % 64 == 0.
+ * No reference counterpart (the reference's packed layout is torch's own).
+ */
+int64_t mtl_w4_tiled_bytes(int64_t K, int64_t N);
+int mtl_w4_tile(const int32_t* qweight, int64_t K, int64_t N, int32_t* tiled, int64_t tiled_bytes,
+                void* stream);
+
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
                      void* stream);
@@ -157,14 +175,15 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
  * from x (bf16 [M, K], through perm when given) or, when xpart is set (M = 1),
  * from the fp32 partials of an interleaved gate|up GEMV ([xsplits, 2K], 32-column
  * gate|up blocks): x[j] = bf16(silu(bf16 gate_j) * bf16 up_j) (fast.py:170-171).
- * AutoGPTQ meta only.
+ * AutoGPTQ meta only.  layout: MTL_LAYOUT_ROWS, or MTL_LAYOUT_TILED with qweight from
+ * mtl_w4_tile (M = 1, no perm).
  */
 int32_t mtl_w4_gemm_splits(int64_t K, int64_t N);
 int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
                          int64_t M, int64_t K, const int32_t* qweight, const void* scales,
                          const int32_t* qzeros, const int32_t* perm, int64_t N, int32_t group_size,
-                         int32_t zero_offset, float* partials, int64_t partials_bytes,
-                         void* stream);
+                         int32_t zero_offset, int32_t layout, float* partials,
+                         int64_t partials_bytes, void* stream);
 
 /*
  * Partials-only launch (M = 1) whose activation is RMSNorm(h) computed while staging
@@ -177,8 +196,8 @@ int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int
 int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
                               int64_t K, const int32_t* qweight, const void* scales,
                               const int32_t* qzeros, int64_t N, int32_t group_size,
-                              int32_t zero_offset, float* partials, int64_t partials_bytes,
-                              void* stream);
+                              int32_t zero_offset, int32_t layout, float* partials,
+                              int64_t partials_bytes, void* stream);
 
 /*
  * M = 1 GEMV whose epilogue is the decode step's residual add (moss_tts_lite/fast.py:
@@ -194,8 +213,8 @@ int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, 
 int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
                          int64_t K, const int32_t* qweight, const void* scales,
                          const int32_t* qzeros, int64_t N, int32_t group_size, int32_t zero_offset,
-                         void* h, const int32_t* scatter, void* h_ord, float* slots,
-                         void* workspace, int64_t ws_bytes, void* stream);
+                         int32_t layout, void* h, const int32_t* scatter, void* h_ord,
+                         float* slots, void* workspace, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

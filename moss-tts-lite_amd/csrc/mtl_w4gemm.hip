@@ -57,6 +57,7 @@ struct W4Args {
   uint16_t* h_ord;          // EPI_RESIDUAL_SLOTS: h scattered into the next GEMV's order
   const int32_t* scatter;   //   h_ord[scatter[n]] = h[n] (NULL: h_ord[n] = h[n])
   float* slots_out;         //   slots_out[tile] = sum of h^2 over the tile's 256 columns
+  int tiled;                // qweight in the wave-contiguous layout of mtl_w4_tile
   const uint16_t* resid;    // RESIDUAL epilogue input [M, N]
   void* y;
   float* partial;           // [splits, M, N]
@@ -255,16 +256,28 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
 
   // 3. The weight stream: 16 independent 16-byte buffer loads per lane, uniform row
   //    offset per quad; rows past K/8 and columns past N read 0 through the range check.
+  const int splits_total = (rows_total + kRowsPerWG - 1) / kRowsPerWG;
   const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<u32x4*>(a.qweight), (short)0, (int)((int64_t)rows_total * N * 4), 0x00020000);
+      const_cast<u32x4*>(a.qweight), (short)0,
+      (int)(a.tiled ? (int64_t)splits_total * N * 4 * kRowsPerWG : (int64_t)rows_total * N * 4),
+      0x00020000);
+  // tiled: the wave's 16 row quads are 16 consecutive 1 KB blocks
+  const int tblk = (split * (N / kWaveN) + tile * (kTileN / kWaveN) + wn) * kRowQuads;
   u32x4 wq[RQW];
 #pragma unroll
   for (int q = 0; q < RQW; ++q) {
     const int gq = wk * RQW + q;              // row quad within the split
     const int row = row0 + 4 * gq + lg;
-    const int voff = (col_ok && row < rows_total) ? (lg * N + col) * 4 : 0x7ffffff0;
-    wq[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          qrsrc, voff, (row0 + 4 * gq) * N * 4, kStreamAux));
+    int voff, soff;
+    if (a.tiled) {
+      voff = col_ok ? lane * 16 : 0x7ffffff0;
+      soff = (tblk + gq) * 1024;
+    } else {
+      voff = (col_ok && row < rows_total) ? (lg * N + col) * 4 : 0x7ffffff0;
+      soff = (row0 + 4 * gq) * N * 4;
+    }
+    wq[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrsrc, voff, soff,
+                                                                            kStreamAux));
   }
 
   if (LATE_X) load_x();
@@ -709,6 +722,7 @@ static W4Args blank_args() {
   a.h_ord = nullptr;
   a.scatter = nullptr;
   a.slots_out = nullptr;
+  a.tiled = 0;
   a.resid = nullptr;
   a.y = nullptr;
   a.partial = nullptr;
@@ -774,11 +788,18 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
 // Partials-only launch for fused consumers: writes fp32 [splits, M, N] into `partials`
 // (splits = w4_splits(K)); x comes from `x` (bf16, optionally through `perm`) or, when
 // `xpart` is set, from the gate|up partials of the previous GEMV (SiLU*up, M = 1).
+static int check_layout(int layout, int64_t M, int64_t N, const int32_t* perm) {
+  if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED) return MTL_ERR_INVALID_ARG;
+  if (layout == MTL_LAYOUT_TILED && (N % kWaveN != 0 || M != 1 || perm)) return MTL_ERR_SHAPE;
+  return MTL_OK;
+}
+
 static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
                             int64_t M, int64_t K, const int32_t* qweight, const void* meta0,
                             const int32_t* qzeros, const int32_t* perm, int64_t N, int group,
-                            int zero_offset, float* partials, int64_t partials_bytes,
+                            int zero_offset, int layout, float* partials, int64_t partials_bytes,
                             hipStream_t stream) {
+  if (const int st = check_layout(layout, M, N, perm)) return st;
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -808,6 +829,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   a.xsplits = xsplits;
   a.xpart_ld = (int)xpart_ld;
   a.partial = partials;
+  a.tiled = layout == MTL_LAYOUT_TILED;
   a.M = (int)M; a.K = (int)K; a.N = (int)N;
   a.group = group; a.zero_offset = zero_offset;
   a.splits = p.splits;
@@ -822,8 +844,9 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
 static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const float* slots,
                                  float eps, int64_t K, const int32_t* qweight,
                                  const void* meta0, const int32_t* qzeros, int64_t N, int group,
-                                 int zero_offset, float* partials, int64_t partials_bytes,
-                                 hipStream_t stream) {
+                                 int zero_offset, int layout, float* partials,
+                                 int64_t partials_bytes, hipStream_t stream) {
+  if (const int st = check_layout(layout, 1, N, nullptr)) return st;
   if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -844,6 +867,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   a.slots = slots;
   a.eps = eps;
   a.partial = partials;
+  a.tiled = layout == MTL_LAYOUT_TILED;
   a.M = 1; a.K = (int)K; a.N = (int)N;
   a.group = group; a.zero_offset = zero_offset;
   a.splits = p.splits;
@@ -860,10 +884,12 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
 static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
                             int64_t K, const int32_t* qweight, const void* meta0,
                             const int32_t* qzeros, int64_t N, int group, int zero_offset,
-                            void* h, const int32_t* scatter, void* h_ord, float* slots,
-                            void* workspace, int64_t ws_bytes, hipStream_t stream) {
+                            int layout, void* h, const int32_t* scatter, void* h_ord,
+                            float* slots, void* workspace, int64_t ws_bytes,
+                            hipStream_t stream) {
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !h || !slots)
     return MTL_ERR_INVALID_ARG;
+  if (const int st = check_layout(layout, 1, N, nullptr)) return st;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (N > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
@@ -897,6 +923,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
   a.h_ord = static_cast<uint16_t*>(h_ord);
   a.scatter = scatter;
   a.slots_out = slots;
+  a.tiled = layout == MTL_LAYOUT_TILED;
   a.M = 1; a.K = (int)K; a.N = (int)N;
   a.group = group; a.zero_offset = zero_offset;
   a.splits = p.splits;
@@ -960,29 +987,30 @@ int32_t mtl_w4_gemm_splits(int64_t K, int64_t N) {
 int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
                          int64_t M, int64_t K, const int32_t* qweight, const void* scales,
                          const int32_t* qzeros, const int32_t* perm, int64_t N, int32_t group_size,
-                         int32_t zero_offset, float* partials, int64_t partials_bytes,
-                         void* stream) {
+                         int32_t zero_offset, int32_t layout, float* partials,
+                         int64_t partials_bytes, void* stream) {
   return w4_gemm_partials(x, xpart, xsplits, xpart_ld, M, K, qweight, scales, qzeros, perm, N,
-                          group_size, zero_offset, partials, partials_bytes, (hipStream_t)stream);
+                          group_size, zero_offset, layout, partials, partials_bytes,
+                          (hipStream_t)stream);
 }
 
 int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
                               int64_t K, const int32_t* qweight, const void* scales,
                               const int32_t* qzeros, int64_t N, int32_t group_size,
-                              int32_t zero_offset, float* partials, int64_t partials_bytes,
-                              void* stream) {
+                              int32_t zero_offset, int32_t layout, float* partials,
+                              int64_t partials_bytes, void* stream) {
   return w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N,
-                               group_size, zero_offset, partials, partials_bytes,
+                               group_size, zero_offset, layout, partials, partials_bytes,
                                (hipStream_t)stream);
 }
 
 int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
                          int64_t K, const int32_t* qweight, const void* scales,
                          const int32_t* qzeros, int64_t N, int32_t group_size, int32_t zero_offset,
-                         void* h, const int32_t* scatter, void* h_ord, float* slots,
-                         void* workspace, int64_t ws_bytes, void* stream) {
+                         int32_t layout, void* h, const int32_t* scatter, void* h_ord,
+                         float* slots, void* workspace, int64_t ws_bytes, void* stream) {
   return w4_gemm_residual(x, xpart, xsplits, xpart_ld, K, qweight, scales, qzeros, N, group_size,
-                          zero_offset, h, scatter, h_ord, slots, workspace, ws_bytes,
+                          zero_offset, layout, h, scatter, h_ord, slots, workspace, ws_bytes,
                           (hipStream_t)stream);
 }
 

@@ -39,6 +39,24 @@ __global__ void unpack_codes_kernel(const uint32_t* __restrict__ qw, int64_t K, 
   }
 }
 
+// Wave-contiguous layout of the GEMV weight stream: 16-byte word l of 1 KB block
+// ((s * N/64 + cg) * 16 + q) holds qweight row 64s + 4q + l/16, columns 64cg + 4(l%16)..+3
+// (rows past K/8 are zero).  One GEMV wave then reads 16 consecutive blocks.
+__global__ void tile_weights_kernel(const uint4* __restrict__ qw, int64_t rows, int64_t N,
+                                    int64_t splits, uint4* __restrict__ out) {
+  const int64_t ncg = N / 64;
+  const int64_t total = splits * ncg * 16 * 64;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t l = t & 63, blk = t >> 6;
+    const int64_t q = blk & 15, sc = blk >> 4;
+    const int64_t cg = sc % ncg, s = sc / ncg;
+    const int64_t row = 64 * s + 4 * q + (l >> 4);
+    const int64_t col = 64 * cg + 4 * (l & 15);
+    out[t] = row < rows ? qw[(row * N + col) >> 2] : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
 // fp32 W[K, N]; fmt GPTQ: (q - (z + zero_offset)) * s ; QSZ: (q - 8) * scale + zero.
 template <int FMT>
 __global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* __restrict__ meta0,
@@ -140,6 +158,26 @@ int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K, int32_t
   const int64_t total = (K / 8) * N;
   hipLaunchKernelGGL(int4pack_convert_kernel, dim3(grid_for(total)), dim3(256), 0,
                      (hipStream_t)stream, prepacked, N, K, reinterpret_cast<uint32_t*>(packed));
+  return launch_status();
+}
+
+int64_t mtl_w4_tiled_bytes(int64_t K, int64_t N) {
+  if (K <= 0 || N <= 0 || K % 8 != 0 || N % 64 != 0) return 0;
+  const int64_t splits = (K / 8 + 63) / 64;
+  return splits * (N / 64) * 16 * 1024;
+}
+
+int mtl_w4_tile(const int32_t* qweight, int64_t K, int64_t N, int32_t* tiled, int64_t tiled_bytes,
+                void* stream) {
+  if (!qweight || !tiled) return MTL_ERR_INVALID_ARG;
+  if (K <= 0 || N <= 0 || K % 8 != 0 || N % 64 != 0) return MTL_ERR_SHAPE;
+  const int64_t need = mtl_w4_tiled_bytes(K, N);
+  if (tiled_bytes < need) return MTL_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(qweight) & 15u) || (reinterpret_cast<uintptr_t>(tiled) & 15u))
+    return MTL_ERR_ALIGN;
+  hipLaunchKernelGGL(tile_weights_kernel, dim3(grid_for(need / 16)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint4*>(qweight), K / 8, N,
+                     (K / 8 + 63) / 64, reinterpret_cast<uint4*>(tiled));
   return launch_status();
 }
 

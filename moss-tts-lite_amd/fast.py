@@ -143,7 +143,8 @@ class FastDecoder:
 
     def _partials(self, x, xpart_name, lin, n, name):
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
-        qw, qz, sc, _ = lin.kernel_args()
+        _, qz, sc, _ = lin.kernel_args()
+        qw, layout = lin.stream_weight()
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
@@ -152,7 +153,7 @@ class FastDecoder:
                 (p(x), p(xpart), xs, 2 * lin.in_features if xpart_name else 0, 1,
                  lin.in_features, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(),
                  None, n, lin.group_size,
-                 lin.zero_offset, out.data_ptr(), out.numel() * 4))
+                 lin.zero_offset, layout, out.data_ptr(), out.numel() * 4))
 
     def _layer_plan_fused(self, li: int) -> list:
         m, cfg = self.m, self.m.cfg
@@ -259,23 +260,25 @@ class FastDecoder:
         return plan
 
     def _residual(self, x, xpart_name, lin, scatter, h_ord):
-        qw, qz, sc, _ = lin.kernel_args()
+        _, qz, sc, _ = lin.kernel_args()
+        qw, layout = lin.stream_weight()
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         return ("mtl_w4_gemm_residual",
                 (p(x), p(xpart), self.splits[xpart_name] if xpart_name else 0,
                  2 * lin.in_features if xpart_name else 0, lin.in_features, qw.data_ptr(),
                  sc.data_ptr(), qz.data_ptr(), lin.out_features, lin.group_size,
-                 lin.zero_offset, self.h.data_ptr(), p(scatter), p(h_ord),
+                 lin.zero_offset, layout, self.h.data_ptr(), p(scatter), p(h_ord),
                  self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel()))
 
     def _norm_partials(self, h_ord, w_ord, lin, n, name):
-        qw, qz, sc, _ = lin.kernel_args()
+        _, qz, sc, _ = lin.kernel_args()
+        qw, layout = lin.stream_weight()
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
-                 qz.data_ptr(), n, lin.group_size, lin.zero_offset, out.data_ptr(),
+                 qz.data_ptr(), n, lin.group_size, lin.zero_offset, layout, out.data_ptr(),
                  out.numel() * 4))
 
     def _layer_plan(self, li: int) -> list:

@@ -50,6 +50,7 @@ class GPTQLinear(torch.nn.Module):
                                        // group_size).to(torch.int32))
         self._kernel_qweight: torch.Tensor | None = None
         self._perm: torch.Tensor | None = None
+        self._tiled: torch.Tensor | None = None
 
     @classmethod
     def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
@@ -84,6 +85,17 @@ class GPTQLinear(torch.nn.Module):
             self.post_init()
         return self._kernel_qweight, self.qzeros, self.scales, self._perm
 
+    def stream_weight(self):
+        """``(pointer tensor, layout)`` of the weight the decode-step GEMVs stream: the
+        wave-contiguous tiled copy of the kernel weight (built once) when N % 64 == 0,
+        else the kernel weight in row layout."""
+        qw = self.kernel_args()[0]
+        if self.out_features % 64:
+            return qw, N.LAYOUT_ROWS
+        if self._tiled is None:
+            self._tiled = ops.tile_weights(qw)
+        return self._tiled, N.LAYOUT_TILED
+
     def drop_original(self) -> None:
         """Free the unsorted ``qweight`` once the sorted copy exists (load-time memory)."""
         if self._perm is not None:
@@ -101,6 +113,7 @@ class GPTQLinear(torch.nn.Module):
             raise ValueError("cols must list every output column once")
         if self._kernel_qweight is None:
             self.post_init()
+        self._tiled = None
         sorted_separately = self._kernel_qweight is not self.qweight
         self._kernel_qweight = self._kernel_qweight[:, cols].contiguous()
         if sorted_separately and self.qweight.numel():

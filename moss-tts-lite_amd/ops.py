@@ -171,6 +171,23 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
     return out
 
 
+def tile_weights(qweight: torch.Tensor) -> torch.Tensor:
+    """Wave-contiguous copy of ``qweight [K/8, N]`` for the decode-step GEMVs
+    (``mtl_w4_tile``); N must be a multiple of 64."""
+    if qweight.dtype != torch.int32 or qweight.dim() != 2:
+        raise RuntimeError("qweight must be int32 [K/8, N]")
+    k, n = qweight.shape[0] * 8, qweight.shape[1]
+    lib = N.load()
+    nbytes = int(lib.mtl_w4_tiled_bytes(k, n))
+    if nbytes <= 0:
+        raise RuntimeError(f"no tiled layout for K={k}, N={n} (N must be a multiple of 64)")
+    src = qweight.contiguous()
+    out = torch.empty(nbytes // 4, dtype=torch.int32, device=src.device)
+    N.check(lib.mtl_w4_tile(src.data_ptr(), k, n, out.data_ptr(), nbytes, _stream(src.device)),
+            "mtl_w4_tile")
+    return out
+
+
 def unpack_codes(qweight: torch.Tensor) -> torch.Tensor:
     """``qweight [K/8, N]`` -> codes uint8 ``[K, N]``."""
     k = qweight.shape[0] * 8

@@ -115,9 +115,16 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_w4_gemm_splits(4096, 24576) == 8 and lib.mtl_w4_gemm_splits(12288, 4096) == 24
     # partials entry: x and xpart are exclusive; the gate|up source needs M = 1
     assert lib.mtl_w4_gemm_partials(FAKE, FAKE, 8, 8192, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
-                                    128, 0, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
+                                    128, 0, 0, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_w4_gemm_partials(None, FAKE, 8, 8192, 2, 4096, FAKE, FAKE, FAKE, None, 4096,
-                                    128, 0, FAKE, 1 << 30, None) == N.MTL_ERR_UNSUPPORTED
+                                    128, 0, 0, FAKE, 1 << 30, None) == N.MTL_ERR_UNSUPPORTED
+    # the tiled layout needs N % 64 == 0, M = 1 and no gather index
+    assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4104,
+                                    128, 0, 1, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
+                                    128, 0, 2, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_w4_tiled_bytes(4096, 24576) == 8 * 384 * 16 * 1024
+    assert lib.mtl_w4_tiled_bytes(4096, 24600) == 0
     assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG

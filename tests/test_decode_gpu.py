@@ -313,7 +313,7 @@ def test_gemm_partials_sum_to_the_single_launch_result(dev, lib):
     S = int(lib.mtl_w4_gemm_splits(4096, 6144))
     part = torch.empty(S * 6144, dtype=torch.float32, device=dev)
     N.check(lib.mtl_w4_gemm_partials(x.data_ptr(), None, 0, 0, 1, 4096, qw.data_ptr(), sc.data_ptr(),
-                                     qz.data_ptr(), None, 6144, 128, 0, part.data_ptr(),
+                                     qz.data_ptr(), None, 6144, 128, 0, 0, part.data_ptr(),
                                      part.numel() * 4, stream()), "partials")
     whole = ops.gptq_gemm(x, qw, qz, sc, 128, out_dtype=torch.float32)
     summed = _seq_sum(part.view(S, 6144).cpu().numpy())
@@ -333,7 +333,7 @@ def test_down_reads_silu_mul_from_gate_up_partials(dev, lib):
     S = int(lib.mtl_w4_gemm_splits(512, 2 * inter))
     pgu = torch.empty(S * 2 * inter, dtype=torch.float32, device=dev)
     N.check(lib.mtl_w4_gemm_partials(x.data_ptr(), None, 0, 0, 1, 512, gq.data_ptr(), gs.data_ptr(),
-                                     gz.data_ptr(), None, 2 * inter, 128, 0, pgu.data_ptr(),
+                                     gz.data_ptr(), None, 2 * inter, 128, 0, 0, pgu.data_ptr(),
                                      pgu.numel() * 4, stream()), "gate_up partials")
     act = ops.w4_gemm(x.view(1, -1), gq, N.META_GPTQ, gs, gz, None, 2 * inter, 128,
                       epilogue=N.EPI_SILU_MUL)
@@ -341,10 +341,10 @@ def test_down_reads_silu_mul_from_gate_up_partials(dev, lib):
     p1 = torch.empty(Sd * 512, dtype=torch.float32, device=dev)
     p2 = torch.empty_like(p1)
     N.check(lib.mtl_w4_gemm_partials(act.data_ptr(), None, 0, 0, 1, inter, dq.data_ptr(), ds.data_ptr(),
-                                     dz.data_ptr(), None, 512, 128, 0, p1.data_ptr(), p1.numel() * 4,
+                                     dz.data_ptr(), None, 512, 128, 0, 0, p1.data_ptr(), p1.numel() * 4,
                                      stream()), "down from act")
     N.check(lib.mtl_w4_gemm_partials(None, pgu.data_ptr(), S, 2 * inter, 1, inter, dq.data_ptr(),
-                                     ds.data_ptr(), dz.data_ptr(), None, 512, 128, 0, p2.data_ptr(),
+                                     ds.data_ptr(), dz.data_ptr(), None, 512, 128, 0, 0, p2.data_ptr(),
                                      p2.numel() * 4, stream()), "down from gate_up partials")
     assert torch.equal(p1, p2)
 
@@ -449,7 +449,7 @@ def test_gemm_norm_partials_match_oracle(dev, lib):
     qw, qz, sc = t(qs), t(case["qzeros"]), t(case["scales"].view(np.float16))
     th, tw = tb(h[ps], dev), tb(w[ps], dev)   # named: a temporary's memory could be reused
     N.check(lib.mtl_w4_gemm_norm_partials(th.data_ptr(), tw.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), K, qw.data_ptr(),
-                                          sc.data_ptr(), qz.data_ptr(), Nn, 128, 0, part.data_ptr(),
+                                          sc.data_ptr(), qz.data_ptr(), Nn, 128, 0, 0, part.data_ptr(),
                                           part.numel() * 4, stream()), "norm partials")
     y = _seq_sum(part.view(S, Nn).cpu().numpy())
     x = D.rms_norm(h, w)
@@ -596,7 +596,7 @@ def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
     S = int(lib.mtl_w4_gemm_splits(k, n))
     part = torch.empty(S * n, dtype=torch.float32, device=dev)
     N.check(lib.mtl_w4_gemm_partials(p(x), p(xpart), xs, ld, 1, k, qw.data_ptr(), sc.data_ptr(),
-                                     qz.data_ptr(), None, n, 128, 0, part.data_ptr(),
+                                     qz.data_ptr(), None, n, 128, 0, 0, part.data_ptr(),
                                      part.numel() * 4, stream()), "partials")
     h_a, ord_a = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
     slots_a = torch.zeros(64, dtype=torch.float32, device=dev)
@@ -607,7 +607,7 @@ def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
         h_b, ord_b = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
         slots_b = torch.zeros(64, dtype=torch.float32, device=dev)
         N.check(lib.mtl_w4_gemm_residual(p(x), p(xpart), xs, ld, k, qw.data_ptr(), sc.data_ptr(),
-                                         qz.data_ptr(), n, 128, 0, h_b.data_ptr(),
+                                         qz.data_ptr(), n, 128, 0, 0, h_b.data_ptr(),
                                          scatter.data_ptr(), ord_b.data_ptr(), slots_b.data_ptr(),
                                          ws.data_ptr(), ws.numel(), stream()), "residual gemv")
         assert torch.equal(h_a, h_b) and torch.equal(ord_a, ord_b)

@@ -326,3 +326,61 @@ def test_w4_dispatch_modes(dev):
                 ref = xf @ w.T
             err = rel_l2(got, ref)
             assert err < TOL_BF16, (li, name, err)
+
+
+# ------------------------------------------------------------------ tiled weight stream
+
+def _tile_np(qweight: np.ndarray) -> np.ndarray:
+    """The documented layout: word l of block ((s*N/64 + cg)*16 + q) = row 64s+4q+l/16,
+    columns 64cg+4(l%16)..+3; rows past K/8 zero."""
+    rows, n = qweight.shape
+    splits = (rows + 63) // 64
+    pad = np.zeros((splits * 64, n), np.uint32)
+    pad[:rows] = qweight.view(np.uint32)
+    t = pad.reshape(splits, 16, 4, n // 64, 16, 4)       # s, q, l/16, cg, l%16, word
+    return np.ascontiguousarray(t.transpose(0, 3, 1, 2, 4, 5)).reshape(-1)
+
+
+@pytest.mark.parametrize("k,n", [(1024, 128), (4608, 320)])
+def test_tile_layout_bit_exact(dev, k, n):
+    qw = synth.random_qweight(synth.rng(k + n), k, n)
+    out = ops.tile_weights(t_i32(qw, dev)).cpu().numpy().view(np.uint32)
+    assert np.array_equal(out, _tile_np(qw))
+
+
+@pytest.mark.parametrize("k,n,src", [(4096, 24576, "norm"), (12288, 4096, "silu"),
+                                     (4096, 6144, "norm"), (4096, 4096, "bf16"),
+                                     (4608, 320, "bf16")])
+def test_tiled_stream_equals_row_stream(dev, k, n, src):
+    # same arithmetic, only the weight addresses differ: partials bit for bit
+    import ctypes
+    lib = N.load()
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=k + n, with_ref=False)
+    qw, qz, sc = t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    tiled = ops.tile_weights(qw)
+    r = np.random.default_rng(5)
+    S = int(lib.mtl_w4_gemm_splits(k, n))
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for w, layout in ((qw, N.LAYOUT_ROWS), (tiled, N.LAYOUT_TILED)):
+        part = torch.zeros(S * n, dtype=torch.float32, device=dev)
+        if src == "norm":
+            h = t_bf16(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)), dev) if not outs else h
+            wn = t_bf16(f32_to_bf16_bits(np.ones(k, np.float32)), dev) if not outs else wn
+            slots = torch.ones(64, dtype=torch.float32, device=dev) * float(k) / 64
+            N.check(lib.mtl_w4_gemm_norm_partials(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                                  ctypes.c_float(1e-6), k, w.data_ptr(), sc.data_ptr(),
+                                                  qz.data_ptr(), n, 128, 0, layout, part.data_ptr(),
+                                                  part.numel() * 4, st), "norm partials")
+        elif src == "silu":
+            xp = torch.from_numpy(r.standard_normal((8, 2 * k)).astype(np.float32)).to(dev) if not outs else xp
+            N.check(lib.mtl_w4_gemm_partials(None, xp.data_ptr(), 8, 2 * k, 1, k, w.data_ptr(),
+                                             sc.data_ptr(), qz.data_ptr(), None, n, 128, 0, layout,
+                                             part.data_ptr(), part.numel() * 4, st), "silu partials")
+        else:
+            x = t_bf16(case["x_bits"], dev)
+            N.check(lib.mtl_w4_gemm_partials(x.data_ptr(), None, 0, 0, 1, k, w.data_ptr(),
+                                             sc.data_ptr(), qz.data_ptr(), None, n, 128, 0, layout,
+                                             part.data_ptr(), part.numel() * 4, st), "partials")
+        outs.append(part)
+    assert torch.equal(outs[0], outs[1])
