@@ -299,7 +299,7 @@ def bench_kernels(args, torch):
     dev = torch.device("cuda:0")
     cfg = BackboneConfig(max_seq=1536)
     model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev), dev)
-    dec = FastDecoder(model)
+    dec = FastDecoder(model, plan=args.plan)
     dec.prefill(torch.randint(0, cfg.vocab, (16,), generator=torch.Generator().manual_seed(1)))
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -381,7 +381,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--plan", default="staged", choices=["fused", "staged", "partials", "unfused"],
+    ap.add_argument("--plan", default="staged",
+                    choices=["strip", "fused", "staged", "partials", "unfused"],
                     help="decode launch plan (decode workload)")
     args = ap.parse_args()
     if args.gpus != 1:

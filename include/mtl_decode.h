@@ -110,7 +110,7 @@ int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, voi
  * Residual add of the norm-staged step (moss_tts_lite/fast.py:168-169): with partials
  * (fp32 [splits, n] of the o or down GEMV) h = bf16(bf16(sum of partials) + h) in place;
  * without, h is only read.  slots[b] receives the sum of squares of h over columns
- * 256b .. 256b+255 (consumed by mtl_w4_gemm_norm_partials / mtl_bf16_gemv_argmax_norm,
+ * 16b .. 16b+15 (consumed by mtl_w4_gemm_norm_partials / mtl_bf16_gemv_argmax_norm,
  * which apply the RMSNorm of model.py:34-40).  h_ord (optional) receives h scattered
  * into the next int4 GEMV's act-order input order: h_ord[scatter[i]] = h[i] (scatter
  * NULL: copy).  n % 4 == 0, n <= 16384.
@@ -133,7 +133,7 @@ int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const 
 
 /*
  * mtl_bf16_gemv_argmax on x = RMSNorm(h, norm_w) (the final norm, model.py:34-40 and
- * fast.py:179-180), with h's sums of squares per 256 columns in slots.
+ * fast.py:179-180), with h's sums of squares per 16 columns in slots (16-byte aligned).
  */
 int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
                               const void* w, int64_t N, int64_t K, void* logits,

@@ -54,7 +54,9 @@ enum {
  * mtl_w4_gemm_norm_partials, mtl_w4_gemm_residual). */
 enum {
   MTL_LAYOUT_ROWS = 0,    /* qweight int32 [K/8, N] as everywhere else                  */
-  MTL_LAYOUT_TILED = 1    /* mtl_w4_tile output (M = 1, N % 64 == 0, no perm)           */
+  MTL_LAYOUT_TILED = 1,   /* mtl_w4_tile output (M = 1, N % 64 == 0, no perm)           */
+  MTL_LAYOUT_STRIP = 2    /* mtl_w4_strip output (M = 1, N % 16 == 0, K % 256 == 0,
+                             K <= 16384, no perm): full-K strip GEMV, no split-K       */
 };
 
 /* Metadata format of mtl_w4_gemm_fused. */
@@ -140,6 +142,18 @@ int64_t mtl_w4_tiled_bytes(int64_t K, int64_t N);
 int mtl_w4_tile(const int32_t* qweight, int64_t K, int64_t N, int32_t* tiled, int64_t tiled_bytes,
                 void* stream);
 
+/*
+ * Column-strip copy of a qweight [K/8, N] for the full-K strip GEMV (load time): 1 KB
+ * block (s * K/128 + b) holds columns 16s .. 16s+15 over input channels 128b .. 128b+127,
+ * its 16-byte word l the words (row 16b + 4j + l/16, column 16s + l%16), j = 0..3.  A
+ * strip's blocks are consecutive, so one workgroup streams one contiguous K*8-byte run.
+ * N % 16 == 0, K % 256 == 0; mtl_w4_strip_bytes returns 0 for other shapes.
+ * No reference counterpart (the reference's packed layout is torch's own).
+ */
+int64_t mtl_w4_strip_bytes(int64_t K, int64_t N);
+int mtl_w4_strip(const int32_t* qweight, int64_t K, int64_t N, int32_t* strip, int64_t strip_bytes,
+                 void* stream);
+
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
                      void* stream);
@@ -176,7 +190,9 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
  * from the fp32 partials of an interleaved gate|up GEMV ([xsplits, 2K], 32-column
  * gate|up blocks): x[j] = bf16(silu(bf16 gate_j) * bf16 up_j) (fast.py:170-171).
  * AutoGPTQ meta only.  layout: MTL_LAYOUT_ROWS, or MTL_LAYOUT_TILED with qweight from
- * mtl_w4_tile (M = 1, no perm).
+ * mtl_w4_tile (M = 1, no perm), or MTL_LAYOUT_STRIP with qweight from mtl_w4_strip: each
+ * workgroup then sums all of K itself and partials holds ONE split, the final fp32 sums
+ * [N] (consumers pass xsplits = 1).
  */
 int32_t mtl_w4_gemm_splits(int64_t K, int64_t N);
 int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
@@ -188,10 +204,10 @@ int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int
 /*
  * Partials-only launch (M = 1) whose activation is RMSNorm(h) computed while staging
  * (moss_tts_lite/model.py:34-40): x[j] = bf16(w[j] * bf16(h[j] * r)),
- * r = rsqrt(sum(slots[0 .. ceil(K/256) - 1]) / K + eps).  h and w are bf16 [K], already
+ * r = rsqrt(sum(slots[0 .. ceil(K/16) - 1]) / K + eps).  h and w are bf16 [K], already
  * in this GEMV's act-order input order (w is the norm weight gathered by the same
- * perm); slots are the sums of squares of h per 256 columns (mtl_residual_add,
- * mtl_w4_gemm_residual).
+ * perm); slots (16-byte aligned) are the sums of squares of h per 16 columns
+ * (mtl_residual_add, mtl_w4_gemm_residual).  layout as mtl_w4_gemm_partials.
  */
 int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, float eps,
                               int64_t K, const int32_t* qweight, const void* scales,
@@ -201,20 +217,33 @@ int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, 
 
 /*
  * M = 1 GEMV whose epilogue is the decode step's residual add (moss_tts_lite/fast.py:
- * 168-171), split-K reduced inside the kernel: h[n] = bf16(bf16((x @ W)[n]) + h[n]) in
- * place, h scattered into the next RMSNorm-staged GEMV's act-order input order
- * (h_ord[scatter[n]] = h[n]; scatter NULL: h_ord[n] = h[n]; h_ord NULL: no copy), and
- * slots[b] = sum of h^2 over columns 256b .. 256b+255 (what mtl_w4_gemm_norm_partials
- * and mtl_bf16_gemv_argmax_norm consume).  x is bf16 [K] or, with xpart, SiLU*up of an
- * interleaved gate|up GEMV's partials (as mtl_w4_gemm_partials).  workspace: as
- * mtl_gptq_gemm (counters zero before first use; every launch leaves them zero).
- * N <= 16384.
+ * 168-171): h[n] = bf16(bf16((x @ W)[n]) + h[n]) in place, h scattered into the next
+ * RMSNorm-staged GEMV's act-order input order (h_ord[scatter[n]] = h[n]; scatter NULL:
+ * h_ord[n] = h[n]; h_ord NULL: no copy), and slots[b] = sum of h^2 over columns
+ * 16b .. 16b+15 (what mtl_w4_gemm_norm_partials and mtl_bf16_gemv_argmax_norm consume).
+ * x is bf16 [K] or, with xpart, SiLU*up of an interleaved gate|up GEMV's partials (as
+ * mtl_w4_gemm_partials).  Layouts ROWS and TILED reduce split-K inside the kernel and
+ * need the workspace of mtl_gptq_gemm (counters zero before first use; every launch
+ * leaves them zero); MTL_LAYOUT_STRIP needs none (workspace may be NULL).  N <= 16384.
  */
 int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,
                          int64_t K, const int32_t* qweight, const void* scales,
                          const int32_t* qzeros, int64_t N, int32_t group_size, int32_t zero_offset,
                          int32_t layout, void* h, const int32_t* scatter, void* h_ord,
                          float* slots, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * M = 1 gate|up GEMV with RMSNorm staging (as mtl_w4_gemm_norm_partials) whose epilogue is
+ * the SwiGLU product of moss_tts_lite/fast.py:170-171: act[j] = bf16(silu(bf16 g_j) *
+ * bf16 u_j), where the N fused columns come in 64-column blocks of 32 gate | 32 up
+ * (act has N/2 entries, 8-byte aligned).  MTL_LAYOUT_STRIP only (N % 64 == 0,
+ * K % 256 == 0, K <= 8192: one workgroup holds 2 strips x 8 K slices of at most 8 blocks);
+ * other layouts return MTL_ERR_UNSUPPORTED.
+ */
+int mtl_w4_gemm_norm_silu(const void* h, const void* w, const float* slots, float eps, int64_t K,
+                          const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                          int64_t N, int32_t group_size, int32_t zero_offset, int32_t layout,
+                          void* act, void* stream);
 
 #ifdef __cplusplus
 }

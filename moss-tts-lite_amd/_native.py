@@ -80,9 +80,17 @@ _SIGNATURES = {
     "mtl_w4_gemm_norm_partials": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                          _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                          _c_void_p, _i64, _c_void_p]),
+    "mtl_w4_gemm_norm_silu": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
+                                     _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                     _c_void_p, _c_void_p]),
     "mtl_w4_tiled_bytes": (_i64, [_i64, _i64]),
     "mtl_w4_tile": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
+    "mtl_w4_strip_bytes": (_i64, [_i64, _i64]),
+    "mtl_w4_strip": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "mtl_tune_set_reduce": (_i32, [_i32]),
+    "mtl_tune_set_strip_nb": (_i32, [_i32]),
+    "mtl_tune_set_strip_xcd": (_i32, [_i32]),
+    "mtl_tune_set_strip_ct": (_i32, [_i32]),
 }
 
 MTL_OK = 0
@@ -95,7 +103,7 @@ MTL_ERR_LAUNCH = -6
 MTL_ERR_UNSUPPORTED = -7
 
 OUT_BF16, OUT_F32 = 0, 1
-LAYOUT_ROWS, LAYOUT_TILED = 0, 1
+LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_STRIP = 0, 1, 2
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 META_GPTQ, META_QSZ = 0, 1
 

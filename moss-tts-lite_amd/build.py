@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
@@ -30,26 +31,42 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(PKG_DIR, "csrc", "*.hip")))
 
 
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # Packed fp32 VALU ops stay off: write plain float code only.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG_DIR, "csrc"),
+]
+
+
 def command(out: str = LIB_PATH) -> list[str]:
-    return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-        # Packed fp32 VALU ops stay off: write plain float code only.
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", os.path.join(ROOT, "include"), "-I", os.path.join(PKG_DIR, "csrc"),
-        *sources(), "-o", out,
-    ]
+    """One-invocation form of the build (every source, then link)."""
+    return [hipcc(), *FLAGS, "-shared", *sources(), "-o", out]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile the library in-tree (always recompiles) and return its path."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = command(tmp)
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the library in-tree (always recompiles; one hipcc per source, in
+    parallel) and return its path."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    with tempfile.TemporaryDirectory(prefix="mtl_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.basename(src) + ".o") for src in sources()]
+        cmds = [[hipcc(), *FLAGS, "-c", src, "-o", obj] for src, obj in zip(sources(), objs)]
+        with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+            errs = list(pool.map(_run, cmds))
+        tmp = LIB_PATH + ".tmp"
+        errs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", *objs, "-o", tmp]))
+    err = "\n".join(e for e in errs if e.strip())
+    if verbose and err:
         print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH

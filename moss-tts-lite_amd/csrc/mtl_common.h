@@ -49,14 +49,40 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Sums of squares of the residual stream h travel between kernels as one slot per
-// 256-column block (slots[b] = sum over h[256b .. 256b+255] of h^2); the RMSNorm that
-// consumes them sums the ceil(n/256) slots with one wave.
-constexpr int kSlotCols = 256;
-constexpr int kMaxSlots = 64;   // hidden <= 16384
+// 16-column block: slots[b] = sum over h[16b .. 16b+15] of h^2, formed as four fma chains
+// over 4 consecutive columns (lanes 4i .. 4i+3) joined by slot_combine.  Every producer
+// uses that order, so every launch plan sees the same slot values.  The RMSNorm that
+// consumes them sums the ceil(n/16) slots with one wave (slot_part + wave_sum).
+constexpr int kSlotCols = 16;
+constexpr int kMaxSlots = 1024;   // hidden <= 16384
+
+__device__ __forceinline__ float slot_combine(float ss) {
+  ss += __shfl_xor(ss, 1);
+  return ss + __shfl_xor(ss, 2);
+}
+
+// This lane's share of the slot total: slots 4*lane .. +3, then +256, ... (fixed order).
+// slots must be 16-byte aligned.
+__device__ __forceinline__ float slot_part(const float* slots, int n, int lane) {
+  const int ns = (n + kSlotCols - 1) / kSlotCols;
+  float s = 0.f;
+  for (int b = 4 * lane; b < ns; b += 256) {
+    float4 v;
+    if (b + 4 <= ns) {
+      v = *reinterpret_cast<const float4*>(slots + b);
+    } else {
+      v.x = slots[b];
+      v.y = b + 1 < ns ? slots[b + 1] : 0.f;
+      v.z = b + 2 < ns ? slots[b + 2] : 0.f;
+      v.w = 0.f;
+    }
+    s += (v.x + v.y) + (v.z + v.w);
+  }
+  return s;
+}
 
 __device__ __forceinline__ float slot_total(const float* slots, int n, int lane) {
-  const int ns = (n + kSlotCols - 1) / kSlotCols;
-  return wave_sum(lane < ns ? slots[lane] : 0.f);
+  return wave_sum(slot_part(slots, n, lane));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

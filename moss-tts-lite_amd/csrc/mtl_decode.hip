@@ -147,15 +147,17 @@ __global__ void __launch_bounds__(kNormThreads) residual_rmsnorm_kernel(
 
 // ----------------------------------------------------------------------------------
 // Residual add without the norm (the next int4 GEMV applies RMSNorm while staging):
-// h = bf16(bf16(sum of split-K partials) + h), one workgroup per 256-column block;
-// each block publishes its sum of squares (slots[b]) and scatters h into the next
-// GEMV's act-order input order (h_ord[scatter[i]] = h[i]).
+// h = bf16(bf16(sum of split-K partials) + h), one 64-thread workgroup per 256-column
+// block; it publishes the sums of squares per 16 columns (slots) and scatters h into the
+// next GEMV's act-order input order (h_ord[scatter[i]] = h[i]).
 // ----------------------------------------------------------------------------------
+constexpr int kResidCols = 256;
+
 __global__ void __launch_bounds__(64) residual_add_kernel(
     const float* __restrict__ part, int splits, uint16_t* h, const int32_t* __restrict__ scatter,
     uint16_t* __restrict__ h_ord, float* __restrict__ slots, int n) {
   const int b = blockIdx.x, t = threadIdx.x;
-  const int i = b * kSlotCols + 4 * t;   // this thread's 4 columns
+  const int i = b * kResidCols + 4 * t;   // this thread's 4 columns
   float ss = 0.f;
   if (i < n) {
     const uint2 rr = *reinterpret_cast<const uint2*>(h + i);
@@ -186,8 +188,8 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
       if (h_ord) h_ord[scatter ? scatter[i + c] : i + c] = (uint16_t)f32_to_bf16(hv[c]);
     }
   }
-  ss = wave_sum(ss);
-  if (t == 0) slots[b] = ss;
+  ss = slot_combine(ss);
+  if ((t & 3) == 0 && i < n) slots[i / kSlotCols] = ss;
 }
 
 // ----------------------------------------------------------------------------------
@@ -921,7 +923,7 @@ int mtl_residual_add(const float* partials, int32_t splits, void* h, const int32
   if (n < 4 || n % 4 != 0 || n > kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
   if (partials && splits < 1) return MTL_ERR_SHAPE;
   if ((partials && !aligned16(partials)) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
-  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + kSlotCols - 1) / kSlotCols)),
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + kResidCols - 1) / kResidCols)),
                      dim3(64), 0, (hipStream_t)stream,
                      partials, splits, static_cast<uint16_t*>(h), scatter,
                      static_cast<uint16_t*>(h_ord), slots, (int)n);
@@ -968,7 +970,8 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
                               void* stream) {
   if (!h || !norm_w || !slots || !w) return MTL_ERR_INVALID_ARG;
   if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
-  if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w)) return MTL_ERR_ALIGN;
+  if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w) || !aligned16(slots))
+    return MTL_ERR_ALIGN;
   if (!workspace || ws_bytes < mtl_head_workspace_bytes(N)) return MTL_ERR_WORKSPACE;
   if (!aligned16(workspace)) return MTL_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;

@@ -1,0 +1,123 @@
+// Inner pieces shared by the int4 GEMV kernels for gfx950 (mtl_w4gemm.hip: split-K tiles,
+// mtl_w4strip.hip: full-K column strips): code unpacking into MFMA operands, x staging
+// transforms, and the activation sources.
+#pragma once
+
+#include "mtl_common.h"
+
+namespace mtl {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+
+// bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
+__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
+  g = round_bf16(g);
+  const float sg = round_bf16(g / (1.0f + expf(-g)));
+  return f32_to_bf16(sg * round_bf16(u));
+}
+
+// Where a GEMV kernel reads its activation row from.
+enum : int {
+  XSRC_BF16 = 0,      // x bf16 [M, K]
+  XSRC_PERM = 1,      // x bf16 [M, K] read through the act-order index: x[:, perm[k]]
+  XSRC_SILU_PART = 2, // x = SiLU(gate) * up from the fp32 split-K partials of an
+                      // interleaved gate|up GEMV (the down projection's input)
+  XSRC_RMSNORM = 3    // x = bf16(w * bf16(h * r)): RMSNorm applied while staging, from the
+                      // residual stream h and norm weight w (both already in the weight's
+                      // act-order input order) and r = rsqrt(sum(slots)/K + eps)
+};
+
+// The 8 codes of one qweight word as the bf16 MFMA operand (128+q_j, 128+q_{j+4}),
+// j = 0..3: one v_and_or_b32 per pair (plus a shift for j > 0).
+// Plain integer code (not the inline-asm and_or): the compiler must see these VALU
+// writes to insert the wait states an MFMA operand read needs after them.  `lo` and
+// `magic` are held in VGPRs (vgpr_const), so each pair selects to one v_and_or_b32.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+  return r;
+}
+
+__device__ __forceinline__ bf16x8_t unpack_codes8(uint32_t w, uint32_t lo, uint32_t magic) {
+  const u32x4 p{(w & lo) | magic, ((w >> 4) & lo) | magic, ((w >> 8) & lo) | magic,
+                ((w >> 12) & lo) | magic};
+  return __builtin_bit_cast(bf16x8_t, p);
+}
+
+// x item (8 channels) in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7), and its sum.
+__device__ __forceinline__ u32x4 pair_order(u32x4 v, float& sum) {
+  const uint32_t e0 = v.x & 0xffffu, e1 = v.x >> 16, e2 = v.y & 0xffffu, e3 = v.y >> 16;
+  const uint32_t e4 = v.z & 0xffffu, e5 = v.z >> 16, e6 = v.w & 0xffffu, e7 = v.w >> 16;
+  sum = ((bf16_to_f32(e0) + bf16_to_f32(e1)) + (bf16_to_f32(e2) + bf16_to_f32(e3))) +
+        ((bf16_to_f32(e4) + bf16_to_f32(e5)) + (bf16_to_f32(e6) + bf16_to_f32(e7)));
+  return u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
+}
+
+// x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40).
+__device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
+  const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t lo = f32_to_bf16(round_bf16(
+        bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * r)));
+    const uint32_t hi = f32_to_bf16(round_bf16(
+        bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * r)));
+    o[c] = lo | (hi << 16);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// Arguments of the full-K strip GEMV (mtl_w4strip.hip), M = 1, AutoGPTQ meta.  The source
+// of x is xpart (SiLU*up), else hn (RMSNorm), else x; the epilogue is SiLU*up into act
+// when act is set (RMSNorm source only), the residual add when h is set, else an fp32
+// store to y.
+struct StripArgs {
+  const u32x4* w;             // strip layout of mtl_w4_strip
+  const uint16_t* scales;     // fp16 [G, N]
+  const uint32_t* qzeros;     // int32 [G, N/8]
+  const uint16_t* x;          // bf16 [K] in the weight's input order
+  const float* xpart;         // gate|up partials [xsplits, xpart_ld]
+  int xsplits, xpart_ld;
+  const uint16_t* hn;         // residual stream h [K] (input order), norm weight [K],
+  const uint16_t* wn;         //   sums of squares of h per 16 columns
+  const float* slots;
+  float eps;
+  float* y;                   // fp32 [N]
+  uint16_t* h;                // bf16 [N], updated in place
+  const int32_t* scatter;     // h_ord[scatter[n]] = h[n] (NULL: identity)
+  uint16_t* h_ord;            // may be NULL
+  float* slots_out;           // one sum of squares per 16 columns
+  uint16_t* act;              // bf16 [N/2]: silu(gate) * up, 32-column gate|up interleave
+  int K, N, group, zero_offset, kblocks, xcd_order;
+};
+
+enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };
+
+// Blocks (128 input channels) per wave of the strip GEMV for this K with ct strips per
+// workgroup; 0: unsupported.
+int strip_blocks_per_wave(int64_t K, int ct);
+// Launch the strip GEMV; shapes, pointers and alignment are checked by the caller.
+int strip_launch(const StripArgs& a, hipStream_t stream);
+
+// The residual add of the decode step (fast.py:168-171) on 4 consecutive columns:
+// h = bf16(bf16(acc) + h); returns their sum of squares (fixed fma order).
+__device__ __forceinline__ float residual4(const float acc[4], float hv[4]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    hv[c] = round_bf16(round_bf16(acc[c]) + hv[c]);
+    ss = fmaf(hv[c], hv[c], ss);
+  }
+  return ss;
+}
+
+}  // namespace mtl

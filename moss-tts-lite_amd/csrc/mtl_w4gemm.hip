@@ -27,12 +27,9 @@
 // 16 A rows = x for M = 1, one row per x row otherwise).  Per group (g/32 quads) the
 // accumulated sum A = sum x*(128+q) and X = sum x give
 //     sum x*w = s * (A - (128 + c) * X) + d * X.
-#include "mtl_common.h"
+#include "mtl_w4core.h"
 
 namespace mtl {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileN = 256;        // output columns per workgroup (4 waves)
 constexpr int kWaveN = 64;         // output columns per wave (16 lanes x 4)
@@ -52,11 +49,11 @@ struct W4Args {
   int xsplits, xpart_ld;
   const uint16_t* hn;       // XSRC_RMSNORM: residual stream h [K] (act-order order)
   const uint16_t* wn;       //               norm weight [K] (same order)
-  const float* slots;       //               sums of squares of h, one per 256 columns
+  const float* slots;       //               sums of squares of h, one per 16 columns
   float eps;
   uint16_t* h_ord;          // EPI_RESIDUAL_SLOTS: h scattered into the next GEMV's order
   const int32_t* scatter;   //   h_ord[scatter[n]] = h[n] (NULL: h_ord[n] = h[n])
-  float* slots_out;         //   slots_out[tile] = sum of h^2 over the tile's 256 columns
+  float* slots_out;         //   one sum of h^2 per 16 columns
   int tiled;                // qweight in the wave-contiguous layout of mtl_w4_tile
   const uint16_t* resid;    // RESIDUAL epilogue input [M, N]
   void* y;
@@ -67,76 +64,9 @@ struct W4Args {
   int M, K, N, group, zero_offset, splits, epilogue, out_f32;
 };
 
-__device__ __forceinline__ float4 ld_f4(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
-}
-
-// bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
-__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
-  g = round_bf16(g);
-  const float sg = round_bf16(g / (1.0f + expf(-g)));
-  return f32_to_bf16(sg * round_bf16(u));
-}
-
-// Where the kernel reads its activation row from.
-enum : int {
-  XSRC_BF16 = 0,      // x bf16 [M, K]
-  XSRC_PERM = 1,      // x bf16 [M, K] read through the act-order index: x[:, perm[k]]
-  XSRC_SILU_PART = 2, // x = SiLU(gate) * up from the fp32 split-K partials of an
-                      // interleaved gate|up GEMV (the down projection's input)
-  XSRC_RMSNORM = 3    // x = bf16(w * bf16(h * r)): RMSNorm applied while staging, from the
-                      // residual stream h and norm weight w (both already in the weight's
-                      // act-order input order) and r = rsqrt(sum(slots)/K + eps)
-};
-
 // Internal epilogue of mtl_w4_gemm_residual: h = bf16(bf16(acc) + h) in place, h scattered
-// to h_ord, per-tile sums of squares of h to slots_out (M = 1, reduced in the kernel).
+// to h_ord, sums of squares of h per 16 columns to slots_out (M = 1, reduced in the kernel).
 constexpr int kEpiResidualSlots = 3;
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-// The 8 codes of one qweight word as the bf16 MFMA operand (128+q_j, 128+q_{j+4}),
-// j = 0..3: one v_and_or_b32 per pair (plus a shift for j > 0).
-// Plain integer code (not the inline-asm and_or): the compiler must see these VALU
-// writes to insert the wait states an MFMA operand read needs after them.  `lo` and
-// `magic` are held in VGPRs (vgpr_const), so each pair selects to one v_and_or_b32.
-__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
-  return r;
-}
-
-__device__ __forceinline__ bf16x8_t unpack_codes8(uint32_t w, uint32_t lo, uint32_t magic) {
-  const u32x4 p{(w & lo) | magic, ((w >> 4) & lo) | magic, ((w >> 8) & lo) | magic,
-                ((w >> 12) & lo) | magic};
-  return __builtin_bit_cast(bf16x8_t, p);
-}
-
-// x item (8 channels) in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7), and its sum.
-__device__ __forceinline__ u32x4 pair_order(u32x4 v, float& sum) {
-  const uint32_t e0 = v.x & 0xffffu, e1 = v.x >> 16, e2 = v.y & 0xffffu, e3 = v.y >> 16;
-  const uint32_t e4 = v.z & 0xffffu, e5 = v.z >> 16, e6 = v.w & 0xffffu, e7 = v.w >> 16;
-  sum = ((bf16_to_f32(e0) + bf16_to_f32(e1)) + (bf16_to_f32(e2) + bf16_to_f32(e3))) +
-        ((bf16_to_f32(e4) + bf16_to_f32(e5)) + (bf16_to_f32(e6) + bf16_to_f32(e7)));
-  return u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
-}
-
-// x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40).
-__device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
-  const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint32_t lo = f32_to_bf16(round_bf16(
-        bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * r)));
-    const uint32_t hi = f32_to_bf16(round_bf16(
-        bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * r)));
-    o[c] = lo | (hi << 16);
-  }
-  return u32x4{o[0], o[1], o[2], o[3]};
-}
 
 // The int4 GEMV / skinny GEMM.  Workgroup = 4 waves side by side along N (64 columns
 // each: lane l owns columns 4*(l%16)..+3) over one split of 512 input channels (64
@@ -232,10 +162,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
     s_pb = a.xpart + 64 * (j0 >> 5) + (j0 & 31) + 2 * (t & 3);
     silu_batch(0);
   }
-  if (XSRC == XSRC_RMSNORM) {
-    const int ns = (a.K + kSlotCols - 1) / kSlotCols;
-    if (stager && lane < ns) slot_v = a.slots[lane];
-  }
+  if (XSRC == XSRC_RMSNORM && stager) slot_v = slot_part(a.slots, a.K, lane);
 
   // 2. Group metadata of the lane's 4 columns, one entry per group of the split.
   const int colc = col_ok ? col : N - 4;
@@ -509,8 +436,8 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
           a.h_ord[a.scatter ? a.scatter[ecol + c] : ecol + c] = (uint16_t)f32_to_bf16(hv[c]);
       }
     }
-    ss = wave_sum(ss);
-    if (lane == 0) a.slots_out[tile] = ss;
+    ss = slot_combine(ss);
+    if ((lane & 3) == 0 && ecol_ok) a.slots_out[ecol / kSlotCols] = ss;
     return;
   }
   if (a.epilogue == MTL_EPI_SILU_MUL) {
@@ -788,10 +715,42 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
 // Partials-only launch for fused consumers: writes fp32 [splits, M, N] into `partials`
 // (splits = w4_splits(K)); x comes from `x` (bf16, optionally through `perm`) or, when
 // `xpart` is set, from the gate|up partials of the previous GEMV (SiLU*up, M = 1).
-static int check_layout(int layout, int64_t M, int64_t N, const int32_t* perm) {
-  if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED) return MTL_ERR_INVALID_ARG;
+static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32_t* perm) {
+  if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED && layout != MTL_LAYOUT_STRIP)
+    return MTL_ERR_INVALID_ARG;
   if (layout == MTL_LAYOUT_TILED && (N % kWaveN != 0 || M != 1 || perm)) return MTL_ERR_SHAPE;
+  if (layout == MTL_LAYOUT_STRIP &&
+      (M != 1 || perm || N <= 0 || N % 16 != 0 || !strip_blocks_per_wave(K, 1) ||
+       N * K / 2 >= ((int64_t)1 << 31)))
+    return MTL_ERR_SHAPE;
   return MTL_OK;
+}
+
+// The strip GEMV's arguments common to every entry point.
+static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
+                            const int32_t* qzeros, int64_t N, int group, int zero_offset) {
+  StripArgs a;
+  a.w = reinterpret_cast<const u32x4*>(w);
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
+  a.x = nullptr;
+  a.xpart = nullptr;
+  a.xsplits = 0;
+  a.xpart_ld = 0;
+  a.hn = a.wn = nullptr;
+  a.slots = nullptr;
+  a.eps = 0.f;
+  a.y = nullptr;
+  a.h = nullptr;
+  a.scatter = nullptr;
+  a.h_ord = nullptr;
+  a.slots_out = nullptr;
+  a.act = nullptr;
+  a.K = (int)K; a.N = (int)N;
+  a.group = group; a.zero_offset = zero_offset;
+  a.kblocks = 0;
+  a.xcd_order = 0;
+  return a;
 }
 
 static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
@@ -799,7 +758,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
                             const int32_t* qzeros, const int32_t* perm, int64_t N, int group,
                             int zero_offset, int layout, float* partials, int64_t partials_bytes,
                             hipStream_t stream) {
-  if (const int st = check_layout(layout, M, N, perm)) return st;
+  if (const int st = check_layout(layout, M, K, N, perm)) return st;
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -817,6 +776,16 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   if (!aligned16(qweight) || !aligned16(partials) || (perm && !aligned16(perm)))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
+    if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    sa.x = static_cast<const uint16_t*>(x);
+    sa.xpart = xpart;
+    sa.xsplits = xsplits;
+    sa.xpart_ld = (int)xpart_ld;
+    sa.y = partials;
+    return strip_launch(sa, stream);
+  }
   const Plan p = plan_for(K, N, M, group);
   if (partials_bytes < (int64_t)p.splits * M * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
@@ -846,7 +815,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
                                  const void* meta0, const int32_t* qzeros, int64_t N, int group,
                                  int zero_offset, int layout, float* partials,
                                  int64_t partials_bytes, hipStream_t stream) {
-  if (const int st = check_layout(layout, 1, N, nullptr)) return st;
+  if (const int st = check_layout(layout, 1, K, N, nullptr)) return st;
   if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -856,6 +825,16 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
     return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
+    if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    sa.hn = static_cast<const uint16_t*>(h_ord);
+    sa.wn = static_cast<const uint16_t*>(w_ord);
+    sa.slots = slots;
+    sa.eps = eps;
+    sa.y = partials;
+    return strip_launch(sa, stream);
+  }
   const Plan p = plan_for(K, N, 1, group);
   if (partials_bytes < (int64_t)p.splits * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
@@ -879,8 +858,9 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
 }
 
 // M = 1 GEMV whose epilogue is the decode step's residual add (reduced in the kernel):
-// h = bf16(bf16(x @ W) + h); h_ord[scatter[n]] = h[n]; slots[tile] = sum of h^2 over each
-// 256-column tile.  x from `x` (bf16) or the gate|up partials (`xpart`, SiLU*up).
+// h = bf16(bf16(x @ W) + h); h_ord[scatter[n]] = h[n]; slots[b] = sum of h^2 over columns
+// 16b..16b+15.  x from `x` (bf16) or the gate|up partials (`xpart`, SiLU*up).  With the
+// strip layout the full-K strip GEMV runs instead: no workspace, no split-K.
 static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int64_t xpart_ld,
                             int64_t K, const int32_t* qweight, const void* meta0,
                             const int32_t* qzeros, int64_t N, int group, int zero_offset,
@@ -889,7 +869,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
                             hipStream_t stream) {
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !h || !slots)
     return MTL_ERR_INVALID_ARG;
-  if (const int st = check_layout(layout, 1, N, nullptr)) return st;
+  if (const int st = check_layout(layout, 1, K, N, nullptr)) return st;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (N > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
@@ -902,6 +882,19 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
   }
   if (!aligned16(qweight) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
+  if (layout == MTL_LAYOUT_STRIP) {
+    if (!aligned16(slots)) return MTL_ERR_ALIGN;
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    sa.x = static_cast<const uint16_t*>(x);
+    sa.xpart = xpart;
+    sa.xsplits = xsplits;
+    sa.xpart_ld = (int)xpart_ld;
+    sa.h = static_cast<uint16_t*>(h);
+    sa.scatter = scatter;
+    sa.h_ord = static_cast<uint16_t*>(h_ord);
+    sa.slots_out = slots;
+    return strip_launch(sa, stream);
+  }
   const Plan p = plan_for(K, N, 1, group);
   W4Args a = blank_args();
   if (p.splits > 1) {
@@ -932,6 +925,31 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
   a.inkernel_reduce = 1;
   launch_w4(a, MTL_META_GPTQ, p, stream);
   return launch_status();
+}
+
+// M = 1 gate|up GEMV with RMSNorm staging whose epilogue is SiLU(gate)*up (strip layout
+// only): act[j] = bf16(silu(bf16 gate_j) * bf16 up_j), columns in 32-column gate|up blocks.
+static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* slots, float eps,
+                             int64_t K, const int32_t* qweight, const void* meta0,
+                             const int32_t* qzeros, int64_t N, int group, int zero_offset,
+                             int layout, void* act, hipStream_t stream) {
+  if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !act)
+    return MTL_ERR_INVALID_ARG;
+  if (layout != MTL_LAYOUT_STRIP) return MTL_ERR_UNSUPPORTED;
+  if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
+  if (K <= 0 || N <= 0 || K % group != 0 || N % 64 != 0 || !strip_blocks_per_wave(K, 2) ||
+      N * K / 2 >= ((int64_t)1 << 31) || K > (int64_t)kSlotCols * kMaxSlots)
+    return MTL_ERR_SHAPE;
+  if (!aligned16(slots) || !aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) ||
+      (reinterpret_cast<uintptr_t>(act) & 7u) || (reinterpret_cast<uintptr_t>(meta0) & 7u))
+    return MTL_ERR_ALIGN;
+  StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+  sa.hn = static_cast<const uint16_t*>(h_ord);
+  sa.wn = static_cast<const uint16_t*>(w_ord);
+  sa.slots = slots;
+  sa.eps = eps;
+  sa.act = static_cast<uint16_t*>(act);
+  return strip_launch(sa, stream);
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
@@ -1012,6 +1030,14 @@ int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int
   return w4_gemm_residual(x, xpart, xsplits, xpart_ld, K, qweight, scales, qzeros, N, group_size,
                           zero_offset, layout, h, scatter, h_ord, slots, workspace, ws_bytes,
                           (hipStream_t)stream);
+}
+
+int mtl_w4_gemm_norm_silu(const void* h, const void* w, const float* slots, float eps, int64_t K,
+                          const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                          int64_t N, int32_t group_size, int32_t zero_offset, int32_t layout,
+                          void* act, void* stream) {
+  return w4_gemm_norm_silu(h, w, slots, eps, K, qweight, scales, qzeros, N, group_size,
+                           zero_offset, layout, act, (hipStream_t)stream);
 }
 
 int mtl_gptq_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight,

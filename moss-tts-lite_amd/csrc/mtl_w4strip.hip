@@ -1,0 +1,380 @@
+// int4 GEMV over full-K column strips for gfx950 (M = 1, AutoGPTQ meta).
+//
+// A workgroup owns CT strips of 16 output columns over the whole input dimension K, so
+// no split-K partial leaves the workgroup: the epilogue holds final sums and applies the
+// decode step's residual add (publishing the RMSNorm statistics and the act-order copy
+// of h), SiLU(gate)*up of an interleaved gate|up projection, or hands the fp32 results
+// to the next kernel as a single "split".  This removes the cross-workgroup reduction (a
+// kernel boundary, or a last-workgroup hand-off) from every int4 GEMV of the step.
+//
+// Weight layout (mtl_w4_strip): 1 KB block (s * K/128 + b) holds columns 16s..16s+15 over
+// input channels 128b..128b+127.  Its 16-byte word l holds the qweight words
+// (k-octet 16b + 4j + l/16, column 16s + l%16), j = 0..3.  Word j of lane l is the B
+// operand of v_mfma_f32_16x16x32_bf16 number j over channels 128b + 32j .. +31 (lane l
+// supplies rows 8(l/16) .. +7 of column l%16), so one 1 KB load per wave feeds four
+// MFMAs, and a strip's K/128 blocks are consecutive in memory.
+//
+// Wave w of a workgroup serves strip w % CT over K slice w / CT (KW slices of NB blocks,
+// KW * NB = K/128).  The CT waves of a slice stage its x once into LDS; the KW per-slice
+// column sums of a strip meet in LDS and are added in slice order, so results are
+// bitwise repeatable.
+#include "mtl_w4core.h"
+
+namespace mtl {
+
+constexpr int kStripCols = 16;
+constexpr int kStripBlockK = 128;     // input channels per 1 KB block
+constexpr int kStripMaxWaves = 16;
+constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
+
+static int g_strip_nb = 0;            // tuning override of blocks per wave (0: auto)
+static int g_strip_ct = 0;            // tuning override of strips per workgroup (0: auto)
+static int g_strip_xcd = 1;           // 1: XCD-contiguous strip order (see the kernel)
+
+template <int GR, int XSRC, int EPI, int NB, int CT>
+__global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs a) {
+  constexpr int ITEMS = 16 * NB;               // x items (8 channels) per K slice
+  constexpr int STAGERS = 64 * CT;             // threads that stage one slice
+  constexpr int ROUNDS = (ITEMS + STAGERS - 1) / STAGERS;
+  constexpr int NGW = 4 * NB / GR;             // quantisation groups per slice
+  constexpr int GI = 4 * GR;                   // x items per group
+  static_assert((4 * NB) % GR == 0, "a slice must cover whole quantisation groups");
+  static_assert(64 % GI == 0 && ITEMS % GI == 0, "a wave must stage whole groups");
+  static_assert(EPI != STRIP_EPI_SILU || CT == 2, "SiLU*up pairs a gate strip with its up strip");
+  extern __shared__ u32x4 xa_all[];            // [KW][ITEMS] x items in pair order
+  __shared__ float xg[kStripMaxWaves][NGW];    // per-slice group sums of x
+  __shared__ float ytile[kStripMaxWaves][kStripCols];   // [slice * CT + strip][column]
+
+  const int wave = wave_id();
+  const int kw = (blockDim.x >> 6) / CT;       // K slices
+  const int lane = threadIdx.x & 63;
+  const int lg = lane >> 4, lj = lane & 15;
+  const int cs = wave % CT, ks = wave / CT;    // this wave's strip and slice
+  // Workgroups go to the 8 XCDs round robin; with xcd_order, XCD x runs the contiguous
+  // workgroups x*G/8 .. (x+1)*G/8 - 1, so the cache lines of scales and zeros that
+  // neighbouring strips share are fetched into one L2 only.
+  const int G = gridDim.x;
+  const int wg = a.xcd_order ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  // SiLU*up: the gate strip 4*(wg/2) + wg%2 and its up partner two strips (32 columns)
+  // to the right; otherwise CT consecutive strips.
+  const int s0 = EPI == STRIP_EPI_SILU ? 4 * (wg >> 1) + (wg & 1) : wg * CT;
+  const int s = s0 + (EPI == STRIP_EPI_SILU ? 2 * cs : cs);
+  const int N = a.N;
+  const int col = s * kStripCols + lj;
+  const int item0 = ks * ITEMS;                // first x item of the slice
+  u32x4* xa = xa_all + ks * ITEMS;
+
+  // 1. Activation loads of this thread's items of the slice (raw; transformed once the
+  //    weights are in flight).  Every item index is below K/8: K = 128 * KW * NB.
+  const int tt = cs * 64 + lane;               // thread index among the slice's stagers
+  u32x4 xv[ROUNDS], wv[XSRC == XSRC_RMSNORM ? ROUNDS : 1];
+  float4 sg[XSRC == XSRC_SILU_PART ? ROUNDS : 1][2], su[XSRC == XSRC_SILU_PART ? ROUNDS : 1][2];
+  const float* sbase[XSRC == XSRC_SILU_PART ? ROUNDS : 1];
+  bool iok[ROUNDS];
+#pragma unroll
+  for (int r = 0; r < ROUNDS; ++r) {
+    const int i = r * STAGERS + tt;
+    iok[r] = i < ITEMS;
+    const int it = item0 + (iok[r] ? i : 0);
+    if (XSRC == XSRC_BF16) {
+      xv[r] = *reinterpret_cast<const u32x4*>(a.x + (size_t)it * 8);
+    } else if (XSRC == XSRC_RMSNORM) {
+      xv[r] = *reinterpret_cast<const u32x4*>(a.hn + (size_t)it * 8);
+      wv[r] = *reinterpret_cast<const u32x4*>(a.wn + (size_t)it * 8);
+    } else {
+      // channels 8it..8it+7 sit in one 32-column block of the gate|up interleave:
+      // gate columns 64*(j/32) + j%32, their up partners 32 columns to the right
+      xv[r] = u32x4{0u, 0u, 0u, 0u};
+      const int j0 = it * 8;
+      sbase[r] = a.xpart + 64 * (j0 >> 5) + (j0 & 31);
+      sg[r][0] = ld_f4(sbase[r]);
+      sg[r][1] = ld_f4(sbase[r] + 4);
+      su[r][0] = ld_f4(sbase[r] + 32);
+      su[r][1] = ld_f4(sbase[r] + 36);
+    }
+  }
+  const bool stages = cs * 64 < ITEMS;         // wave-uniform: this wave stages items
+  float slot_v = 0.f;
+  if (XSRC == XSRC_RMSNORM && stages) slot_v = slot_part(a.slots, a.K, lane);
+
+  // 2. Group metadata of the lane's column, one entry per group of the slice.
+  const int grp0 = item0 * 8 / a.group;
+  uint32_t sraw[NGW], zraw[NGW];
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+    sraw[g] = a.scales[(size_t)(grp0 + g) * N + col];
+    zraw[g] = a.qzeros[(size_t)(grp0 + g) * (N >> 3) + (col >> 3)];
+  }
+
+  // 3. The weight stream: NB consecutive 1 KB blocks per wave, all in flight at once.
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / kStripCols) * a.kblocks * 1024),
+      0x00020000);
+  const int blk0 = s * a.kblocks + ks * NB;
+  u32x4 wq[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    wq[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          wrsrc, lane * 16, (blk0 + b) * 1024, kStripAux));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
+  if (stages) {
+    float norm_r = 0.f;
+    if (XSRC == XSRC_RMSNORM) norm_r = rsqrtf(wave_sum(slot_v) / (float)a.K + a.eps);
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      u32x4 v = xv[r];
+      if (XSRC == XSRC_RMSNORM) {
+        v = rmsnorm8(v, wv[r], norm_r);
+      } else if (XSRC == XSRC_SILU_PART) {
+        float g[8] = {sg[r][0].x, sg[r][0].y, sg[r][0].z, sg[r][0].w,
+                      sg[r][1].x, sg[r][1].y, sg[r][1].z, sg[r][1].w};
+        float u[8] = {su[r][0].x, su[r][0].y, su[r][0].z, su[r][0].w,
+                      su[r][1].x, su[r][1].y, su[r][1].z, su[r][1].w};
+        for (int sp = 1; sp < a.xsplits; ++sp) {     // further splits, summed in split order
+          const float* p = sbase[r] + (size_t)sp * a.xpart_ld;
+          const float4 g0 = ld_f4(p), g1 = ld_f4(p + 4), u0 = ld_f4(p + 32), u1 = ld_f4(p + 36);
+          g[0] += g0.x; g[1] += g0.y; g[2] += g0.z; g[3] += g0.w;
+          g[4] += g1.x; g[5] += g1.y; g[6] += g1.z; g[7] += g1.w;
+          u[0] += u0.x; u[1] += u0.y; u[2] += u0.z; u[3] += u0.w;
+          u[4] += u1.x; u[5] += u1.y; u[6] += u1.z; u[7] += u1.w;
+        }
+        v = u32x4{silu_mul_bf16(g[0], u[0]) | (silu_mul_bf16(g[1], u[1]) << 16),
+                  silu_mul_bf16(g[2], u[2]) | (silu_mul_bf16(g[3], u[3]) << 16),
+                  silu_mul_bf16(g[4], u[4]) | (silu_mul_bf16(g[5], u[5]) << 16),
+                  silu_mul_bf16(g[6], u[6]) | (silu_mul_bf16(g[7], u[7]) << 16)};
+      }
+      float sum;
+      const u32x4 pv = pair_order(v, sum);
+#pragma unroll
+      for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
+      const int i = r * STAGERS + tt;
+      if (iok[r]) {
+        xa[i] = pv;
+        if ((i & (GI - 1)) == 0) xg[ks][i / GI] = sum;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 5. MFMA over the slice's row quads, one quantisation group at a time:
+  //    y += s * (A - (128 + z) * X).  All 16 A rows are x, so every accumulator row holds
+  //    the lane's column; up to four independent accumulators per group.
+  const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
+  const uint32_t kLo = vgpr_const(0x000F000Fu);
+  constexpr int NA = GR < 4 ? GR : 4;
+  float tot = 0.f;
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+    floatx4 acc[NA];
+#pragma unroll
+    for (int c = 0; c < NA; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < GR; ++q) {
+      const int rq = g * GR + q;                 // row quad within the slice
+      const u32x4 w4 = wq[rq >> 2];
+      const uint32_t w = (rq & 3) == 0 ? w4.x : (rq & 3) == 1 ? w4.y : (rq & 3) == 2 ? w4.z : w4.w;
+      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[4 * rq + lg]);
+      acc[q % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, unpack_codes8(w, kLo, kMagic),
+                                                           acc[q % NA], 0, 0, 0);
+    }
+    float A = acc[0][0];
+#pragma unroll
+    for (int c = 1; c < NA; ++c) A += acc[c][0];
+    const float sc = f16_to_f32(sraw[g] & 0xffffu);
+    const float cz = (float)(128 + (int)((zraw[g] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
+    tot = fmaf(sc, fmaf(-cz, xg[ks][g], A), tot);
+  }
+
+  // 6. Per-slice column sums meet in LDS; wave 0 adds them in slice order, four columns
+  //    per lane (lanes 0 .. 4*CT-1 own columns s0*16 + 4*lane .. +3).
+  if (lg == 0) ytile[wave][lj] = tot;
+  __syncthreads();
+  if (wave != 0) return;
+  const int q4 = lane & (4 * CT - 1);
+  const int ec = q4 >> 2;                        // strip of these columns
+  float y[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < kw; ++k) {
+    const float4 t4 = *reinterpret_cast<const float4*>(&ytile[k * CT + ec][4 * (q4 & 3)]);
+    y[0] += t4.x; y[1] += t4.y; y[2] += t4.z; y[3] += t4.w;
+  }
+  const int c0 = s0 * kStripCols + 4 * q4;
+  const bool owner = lane < 4 * CT;
+  if (EPI == STRIP_EPI_STORE) {
+    if (owner) *reinterpret_cast<float4*>(a.y + c0) = make_float4(y[0], y[1], y[2], y[3]);
+    return;
+  }
+  if (EPI == STRIP_EPI_SILU) {
+    // lanes 0..3 hold gate columns 4*lane..+3 of the gate strip and take their up
+    // partners from lanes 4..7; gate column 16*s0 + i is SwiGLU output 32*(wg/2) +
+    // 16*(wg%2) + i (64-column blocks of 32 gate | 32 up)
+    float u[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) u[e] = __shfl_down(y[e], 4);
+    if (lane < 4) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = silu_mul_bf16(y[e], u[e]);
+      *reinterpret_cast<u32x2*>(a.act + (size_t)(wg >> 1) * 32 + (wg & 1) * 16 + 4 * lane) =
+          u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    }
+    return;
+  }
+  // 7. Residual epilogue (fast.py:168-171): h = bf16(bf16(y) + h) in place, h scattered to
+  //    the next GEMV's input order, and each strip's sum of squares as one slot.
+  const u32x2 rr = *reinterpret_cast<const u32x2*>(a.h + c0);
+  float hv[4] = {bf16_to_f32(rr.x & 0xffffu), bf16_to_f32(rr.x >> 16),
+                 bf16_to_f32(rr.y & 0xffffu), bf16_to_f32(rr.y >> 16)};
+  float ss = residual4(y, hv);
+  ss = slot_combine(ss);
+  if (owner) {
+    *reinterpret_cast<u32x2*>(a.h + c0) =
+        u32x2{f32_to_bf16(hv[0]) | (f32_to_bf16(hv[1]) << 16),
+              f32_to_bf16(hv[2]) | (f32_to_bf16(hv[3]) << 16)};
+    if (a.h_ord) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        a.h_ord[a.scatter ? a.scatter[c0 + c] : c0 + c] = (uint16_t)f32_to_bf16(hv[c]);
+    }
+    if ((lane & 3) == 0) a.slots_out[s0 + ec] = ss;
+  }
+}
+
+// Blocks per wave for K/128 = kb blocks with ct strips per workgroup: KW * ct <= 16
+// waves, even NB (whole groups up to g = 256), 4 where it fits.
+static int blocks_per_wave(int64_t K, int ct) {
+  if (K <= 0 || K % (2 * kStripBlockK) != 0) return 0;
+  const int64_t kb = K / kStripBlockK;
+  const int64_t maxkw = kStripMaxWaves / ct;
+  if (g_strip_nb) return (kb % g_strip_nb == 0 && kb / g_strip_nb <= maxkw) ? g_strip_nb : 0;
+  for (const int nb : {4, 6, 8, 2})
+    if (kb % nb == 0 && kb / nb <= maxkw) return nb;
+  return 0;
+}
+
+// K limit of the strip GEMV with ct strips per workgroup (16 waves of 8 blocks / ct).
+int strip_blocks_per_wave(int64_t K, int ct) { return blocks_per_wave(K, ct); }
+
+// Strips per workgroup: 2 for SiLU*up (a gate strip and its up strip), else the tuning
+// override for RMSNorm-staged stores, else 1.
+static int strips_per_wg(const StripArgs& a) {
+  if (a.act) return 2;
+  if (a.hn && !a.h && g_strip_ct) return g_strip_ct;
+  return 1;
+}
+
+template <int GR, int XSRC, int EPI, int CT>
+static void strip_nb(const StripArgs& a, int nb, hipStream_t st) {
+  const dim3 grid(a.N / (kStripCols * CT));
+  const dim3 block(64 * CT * (a.kblocks / nb));
+  const size_t lds = (size_t)(a.kblocks / nb) * 16 * nb * sizeof(u32x4);
+  switch (nb) {
+    case 2: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 2, CT>), grid, block, lds, st, a); break;
+    case 4: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 4, CT>), grid, block, lds, st, a); break;
+    case 6: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 6, CT>), grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 8, CT>), grid, block, lds, st, a); break;
+  }
+}
+
+template <int GR>
+static void strip_variant(const StripArgs& a, int nb, int ct, hipStream_t st) {
+  if (a.act) {
+    strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 2>(a, nb, st);
+  } else if (a.h) {
+    if (a.xpart) strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_RESID, 1>(a, nb, st);
+    else strip_nb<GR, XSRC_BF16, STRIP_EPI_RESID, 1>(a, nb, st);
+  } else if (a.hn) {
+    if (ct == 4) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 4>(a, nb, st);
+    else if (ct == 2) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 2>(a, nb, st);
+    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1>(a, nb, st);
+  } else if (a.xpart) {
+    strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1>(a, nb, st);
+  } else {
+    strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1>(a, nb, st);
+  }
+}
+
+// Shapes, pointers and alignment are checked by the entry points.
+int strip_launch(const StripArgs& args, hipStream_t st) {
+  StripArgs a = args;
+  const int ct = strips_per_wg(a);
+  const int nb = blocks_per_wave(a.K, ct);
+  if (!nb || a.N % (kStripCols * ct) != 0) return MTL_ERR_SHAPE;
+  a.kblocks = a.K / kStripBlockK;
+  a.xcd_order = g_strip_xcd && (a.N / (kStripCols * ct)) % 8 == 0;
+  switch (a.group) {
+    case 32: strip_variant<1>(a, nb, ct, st); break;
+    case 64: strip_variant<2>(a, nb, ct, st); break;
+    case 128: strip_variant<4>(a, nb, ct, st); break;
+    default: strip_variant<8>(a, nb, ct, st); break;
+  }
+  return launch_status();
+}
+
+// Strip layout (see the top of this file); rows past K/8 never occur (K % 256 == 0).
+__global__ void strip_weights_kernel(const uint32_t* __restrict__ qw, int64_t K, int64_t N,
+                                     uint4* __restrict__ out) {
+  const int64_t kb = K / kStripBlockK;
+  const int64_t total = (N / kStripCols) * kb * 64;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t l = t & 63, blk = t >> 6;
+    const int64_t b = blk % kb, s = blk / kb;
+    const int64_t col = kStripCols * s + (l & 15);
+    const int64_t row = 16 * b + (l >> 4);
+    out[t] = make_uint4(qw[(row + 0) * N + col], qw[(row + 4) * N + col],
+                        qw[(row + 8) * N + col], qw[(row + 12) * N + col]);
+  }
+}
+
+}  // namespace mtl
+
+using namespace mtl;
+
+extern "C" {
+
+int64_t mtl_w4_strip_bytes(int64_t K, int64_t N) {
+  if (K <= 0 || N <= 0 || N % kStripCols != 0 || K % (2 * kStripBlockK) != 0) return 0;
+  return N * K / 2;
+}
+
+int mtl_w4_strip(const int32_t* qweight, int64_t K, int64_t N, int32_t* strip,
+                 int64_t strip_bytes, void* stream) {
+  if (!qweight || !strip) return MTL_ERR_INVALID_ARG;
+  const int64_t need = mtl_w4_strip_bytes(K, N);
+  if (!need || need >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  if (strip_bytes < need) return MTL_ERR_WORKSPACE;
+  if (!aligned16(strip) || !aligned16(qweight)) return MTL_ERR_ALIGN;
+  const int64_t total = need / 16;
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(strip_weights_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const uint32_t*>(qweight), K, N,
+                     reinterpret_cast<uint4*>(strip));
+  return launch_status();
+}
+
+// Tuning knobs for launch-shape sweeps (process-wide, not for concurrent use).
+// Blocks per wave of the strip GEMV (0 = automatic).
+int mtl_tune_set_strip_nb(int32_t nb) {
+  if (nb != 0 && nb != 2 && nb != 4 && nb != 6 && nb != 8) return MTL_ERR_INVALID_ARG;
+  g_strip_nb = nb;
+  return MTL_OK;
+}
+
+// Strips per workgroup of the RMSNorm-staged store (0 = automatic, 1, 2 or 4).
+int mtl_tune_set_strip_ct(int32_t ct) {
+  if (ct != 0 && ct != 1 && ct != 2 && ct != 4) return MTL_ERR_INVALID_ARG;
+  g_strip_ct = ct;
+  return MTL_OK;
+}
+
+// 1 = XCD-contiguous strip order (default), 0 = workgroup id order.
+int mtl_tune_set_strip_xcd(int32_t on) {
+  if (on != 0 && on != 1) return MTL_ERR_INVALID_ARG;
+  g_strip_xcd = on;
+  return MTL_OK;
+}
+
+}  // extern "C"

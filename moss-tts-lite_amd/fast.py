@@ -15,7 +15,16 @@ Every launch is a plain C-ABI call on torch's current stream; the launch plan (a
 pointers, sizes, workspaces) is built once, so eager steps and graph capture issue the
 identical kernel sequence.
 
-Four launch plans produce the same step:
+Five launch plans produce the same step:
+
+* ``"strip"``: five launches per layer, with no split-K anywhere.  Every int4 GEMV runs
+  as the full-K strip GEMV (a workgroup owns 16-column strips over all of K): q|k|v hands
+  its final fp32 sums to the attention as a single split, gate|up applies SiLU*up in its
+  epilogue and down reads that bf16 product, and o and down apply the residual add in
+  their epilogue (publishing the sums of squares and the scattered copy of ``h`` the next
+  RMSNorm-staged GEMV reads).
+  Its GEMV sums run in a different order than the split-K plans', so it agrees with
+  them to rounding, not bitwise.
 
 * ``"staged"`` (default): each int4 GEMV publishes only its split-K partials and the
   consumer folds the reduction in.  A 16-workgroup residual add sums the o/down
@@ -61,7 +70,7 @@ def _gather(w: torch.Tensor, perm: torch.Tensor | None) -> torch.Tensor:
 class FastDecoder:
     """One decode step over an :class:`Int4Backbone` (eager or hipGraph replay)."""
 
-    PLANS = ("fused", "staged", "partials", "unfused")
+    PLANS = ("strip", "fused", "staged", "partials", "unfused")
 
     def __init__(self, model: Int4Backbone, plan: str = "staged"):
         if plan not in self.PLANS:
@@ -69,6 +78,7 @@ class FastDecoder:
         self.m = model
         self.plan = plan
         self.fused = plan != "unfused"
+        self.strip = plan == "strip"       # full-K strip GEMVs: one "split" each
         cfg = model.cfg
         dev = model.device
         self.dev = dev
@@ -92,7 +102,8 @@ class FastDecoder:
         self.head_ws = torch.zeros(int(lib.mtl_head_workspace_bytes(cfg.vocab)), dtype=torch.uint8,
                                    device=dev)
         # fused plan: per-GEMV split-K partial buffers and the act-order input buffers
-        self.splits = {name: int(lib.mtl_w4_gemm_splits(k, n)) for name, k, n in
+        self.splits = {name: 1 if self.strip else int(lib.mtl_w4_gemm_splits(k, n))
+                       for name, k, n in
                        (("qkv", cfg.hidden, cfg.qkv_out), ("o", cfg.hidden, cfg.hidden),
                         ("gate_up", cfg.hidden, 2 * cfg.intermediate),
                         ("down", cfg.intermediate, cfg.hidden))}
@@ -103,7 +114,7 @@ class FastDecoder:
         self.x_qkv = torch.zeros(cfg.hidden, dtype=bf, device=dev)
         self.x_o = torch.zeros(cfg.hidden, dtype=bf, device=dev)
         self.x_gu = torch.zeros(cfg.hidden, dtype=bf, device=dev)
-        self.slots = torch.zeros(64, dtype=torch.float32, device=dev)   # sum h^2 per 256 cols
+        self.slots = torch.zeros(1024, dtype=torch.float32, device=dev)   # sum h^2 per 16 cols
         # split-K workspace of the residual GEMVs (o, down): counters stay zero between launches
         self.res_ws = torch.zeros(max(ops.gemm_workspace_bytes(1, cfg.hidden, cfg.hidden, cfg.group_size),
                                       ops.gemm_workspace_bytes(1, cfg.intermediate, cfg.hidden,
@@ -144,7 +155,7 @@ class FastDecoder:
     def _partials(self, x, xpart_name, lin, n, name):
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight()
+        qw, layout = lin.stream_weight(self.strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
@@ -251,17 +262,36 @@ class FastDecoder:
                                             cfg.max_seq, scale, eps, self.attn_ws.data_ptr(),
                                             self.attn_ws.numel())),
             self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu),
-            self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"],
-                                2 * cfg.intermediate, "gate_up"),
-            self._residual(None, "gate_up", lyr["down"],
-                           None if last else self.inv_perm_qkv[li + 1],
-                           None if last else self.x_qkv),
         ]
+        if self.strip:   # SiLU*up in the gate|up epilogue; down reads the bf16 product
+            plan += [
+                self._norm_silu(self.x_gu, self.norm_gu[li], lyr["gate_up"]),
+                self._residual(self.act, None, lyr["down"],
+                               None if last else self.inv_perm_qkv[li + 1],
+                               None if last else self.x_qkv),
+            ]
+        else:
+            plan += [
+                self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"],
+                                    2 * cfg.intermediate, "gate_up"),
+                self._residual(None, "gate_up", lyr["down"],
+                               None if last else self.inv_perm_qkv[li + 1],
+                               None if last else self.x_qkv),
+            ]
         return plan
+
+    def _norm_silu(self, h_ord, w_ord, lin):
+        _, qz, sc, _ = lin.kernel_args()
+        qw, layout = lin.stream_weight(True)
+        return ("mtl_w4_gemm_norm_silu",
+                (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
+                 ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
+                 qz.data_ptr(), lin.out_features, lin.group_size, lin.zero_offset, layout,
+                 self.act.data_ptr()))
 
     def _residual(self, x, xpart_name, lin, scatter, h_ord):
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight()
+        qw, layout = lin.stream_weight(self.strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         return ("mtl_w4_gemm_residual",
@@ -273,7 +303,7 @@ class FastDecoder:
 
     def _norm_partials(self, h_ord, w_ord, lin, n, name):
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight()
+        qw, layout = lin.stream_weight(self.strip)
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
@@ -315,7 +345,7 @@ class FastDecoder:
         self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), self.table_ptrs.numel(),
                                           self.table_ptrs.data_ptr(), self.vocabs.data_ptr(),
                                           cfg.hidden, self.h.data_ptr()))]
-        if self.plan == "fused":
+        if self.plan in ("fused", "strip"):
             self._layers = [self._layer_plan_resid(li) for li in range(cfg.n_layers)]
         elif self.plan == "staged":
             self._layers = [self._layer_plan_staged(li) for li in range(cfg.n_layers)]
@@ -330,13 +360,14 @@ class FastDecoder:
                       "mtl_advance_position", "mtl_w4_gemm_partials",
                       "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
                       "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
-                      "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual")}
+                      "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual",
+                      "mtl_w4_gemm_norm_silu")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
         m, cfg = self.m, self.m.cfg
         eps = ctypes.c_float(cfg.eps)
-        if self.plan in ("unfused", "fused"):   # h is complete
+        if self.plan in ("unfused", "fused", "strip"):   # h is complete
             return [("mtl_rmsnorm", (self.h.data_ptr(), m.final_norm.data_ptr(),
                                      self.h_final.data_ptr(), 1, cfg.hidden, eps))]
         return [("mtl_residual_rmsnorm", (self.part["down"].data_ptr(), self.splits["down"],
@@ -348,8 +379,8 @@ class FastDecoder:
         """Final norm, head, greedy token into ``ids``, position + 1."""
         m, cfg = self.m, self.m.cfg
         eps = ctypes.c_float(cfg.eps)
-        if self.plan in ("staged", "fused"):   # the head applies the final norm while staging
-            final = [] if self.plan == "fused" else [self._flush_staged()]
+        if self.plan in ("staged", "fused", "strip"):   # the head applies the final norm
+            final = [] if self.plan != "staged" else [self._flush_staged()]
             final += [("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
                                                     self.slots.data_ptr(), eps, m.head.data_ptr(),
                                                     cfg.vocab, cfg.hidden, self.logits.data_ptr(),
@@ -371,13 +402,14 @@ class FastDecoder:
 
     # position of each int4 GEMV launch inside a layer's plan
     _GEMV_AT = {"fused": {"qkv": 0, "o": 2, "gate_up": 3, "down": 4},
+                "strip": {"qkv": 0, "o": 2, "gate_up": 3, "down": 4},
                 "staged": {"qkv": 1, "o": 3, "gate_up": 5, "down": 6},
                 "partials": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7},
                 "unfused": {"qkv": 1, "o": 4, "gate_up": 6, "down": 7}}
 
     def gemv_launch(self, li: int, name: str):
         """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
-        shift = 1 if self.plan == "fused" and li == 0 else 0   # layer 0 opens with the stats
+        shift = 1 if self.plan in ("fused", "strip") and li == 0 else 0   # layer 0: the stats
         return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:

@@ -51,6 +51,7 @@ class GPTQLinear(torch.nn.Module):
         self._kernel_qweight: torch.Tensor | None = None
         self._perm: torch.Tensor | None = None
         self._tiled: torch.Tensor | None = None
+        self._strip: torch.Tensor | None = None
 
     @classmethod
     def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
@@ -85,11 +86,24 @@ class GPTQLinear(torch.nn.Module):
             self.post_init()
         return self._kernel_qweight, self.qzeros, self.scales, self._perm
 
-    def stream_weight(self):
-        """``(pointer tensor, layout)`` of the weight the decode-step GEMVs stream: the
-        wave-contiguous tiled copy of the kernel weight (built once) when N % 64 == 0,
-        else the kernel weight in row layout."""
+    def supports_strip(self) -> bool:
+        return self.out_features % 16 == 0 and self.in_features % 256 == 0 \
+            and self.in_features <= 16384
+
+    def stream_weight(self, strip: bool = False):
+        """``(pointer tensor, layout)`` of the weight the decode-step GEMVs stream.
+
+        ``strip=False``: the wave-contiguous tiled copy of the kernel weight (split-K
+        GEMV) when N % 64 == 0, else the kernel weight in row layout.  ``strip=True``:
+        the column-strip copy for the full-K strip GEMV.  Copies are built once."""
         qw = self.kernel_args()[0]
+        if strip:
+            if not self.supports_strip():
+                raise RuntimeError(f"no strip layout for K={self.in_features}, "
+                                   f"N={self.out_features}")
+            if self._strip is None:
+                self._strip = ops.strip_weights(qw)
+            return self._strip, N.LAYOUT_STRIP
         if self.out_features % 64:
             return qw, N.LAYOUT_ROWS
         if self._tiled is None:
@@ -113,7 +127,7 @@ class GPTQLinear(torch.nn.Module):
             raise ValueError("cols must list every output column once")
         if self._kernel_qweight is None:
             self.post_init()
-        self._tiled = None
+        self._tiled = self._strip = None
         sorted_separately = self._kernel_qweight is not self.qweight
         self._kernel_qweight = self._kernel_qweight[:, cols].contiguous()
         if sorted_separately and self.qweight.numel():

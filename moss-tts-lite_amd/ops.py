@@ -188,6 +188,23 @@ def tile_weights(qweight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def strip_weights(qweight: torch.Tensor) -> torch.Tensor:
+    """Column-strip copy of ``qweight [K/8, N]`` for the full-K strip GEMV
+    (``mtl_w4_strip``); N must be a multiple of 16 and K of 256."""
+    if qweight.dtype != torch.int32 or qweight.dim() != 2:
+        raise RuntimeError("qweight must be int32 [K/8, N]")
+    k, n = qweight.shape[0] * 8, qweight.shape[1]
+    lib = N.load()
+    nbytes = int(lib.mtl_w4_strip_bytes(k, n))
+    if nbytes <= 0:
+        raise RuntimeError(f"no strip layout for K={k}, N={n} (N % 16 == 0 and K % 256 == 0)")
+    src = qweight.contiguous()
+    out = torch.empty(nbytes // 4, dtype=torch.int32, device=src.device)
+    N.check(lib.mtl_w4_strip(src.data_ptr(), k, n, out.data_ptr(), nbytes, _stream(src.device)),
+            "mtl_w4_strip")
+    return out
+
+
 def unpack_codes(qweight: torch.Tensor) -> torch.Tensor:
     """``qweight [K/8, N]`` -> codes uint8 ``[K, N]``."""
     k = qweight.shape[0] * 8

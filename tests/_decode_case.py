@@ -87,3 +87,17 @@ def build_case(cfg: BackboneConfig, seed: int, dev):
                         head_2way=bf16_bits_to_f32(head)[list(cfg.two_way_ids)])
     model = Int4Backbone(cfg, dev_w, dev)
     return model, oracle_w
+
+
+def slots16(h) -> np.ndarray:
+    """Sums of squares of h per 16 columns in the kernels' fixed order: four float32
+    chains over 4 consecutive columns (h*h is exact for bf16 h, so the fma is an add),
+    joined as (c0 + c1) + (c2 + c3)."""
+    h = np.asarray(h, np.float32).reshape(-1)
+    pad = np.zeros(((h.size + 15) // 16) * 16, np.float32)
+    pad[:h.size] = h
+    sq = pad.reshape(-1, 4, 4) ** 2                   # slot, chain, column
+    c = np.zeros(sq.shape[:2], np.float32)
+    for j in range(4):
+        c = (c + sq[:, :, j]).astype(np.float32)
+    return ((c[:, 0] + c[:, 1]) + (c[:, 2] + c[:, 3])).astype(np.float32)

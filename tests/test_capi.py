@@ -122,9 +122,25 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4104,
                                     128, 0, 1, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
     assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
-                                    128, 0, 2, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
+                                    128, 0, 3, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_w4_tiled_bytes(4096, 24576) == 8 * 384 * 16 * 1024
     assert lib.mtl_w4_tiled_bytes(4096, 24600) == 0
+    # the strip layout needs N % 16 == 0, K % 256 == 0 (K <= 16384), M = 1, no gather index
+    strip = N.LAYOUT_STRIP
+    part = lambda m, k, n, perm=None: lib.mtl_w4_gemm_partials(  # noqa: E731
+        FAKE, None, 0, 0, m, k, FAKE, FAKE, FAKE, perm, n, 128, 0, strip, FAKE, 1 << 30, None)
+    assert part(1, 4096, 4104) == N.MTL_ERR_SHAPE
+    assert part(1, 4224, 4096) == N.MTL_ERR_SHAPE
+    assert part(1, 32768, 4096) == N.MTL_ERR_SHAPE
+    assert part(2, 4096, 4096) == N.MTL_ERR_SHAPE
+    assert part(1, 4096, 4096, FAKE) == N.MTL_ERR_SHAPE
+    assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096, 128,
+                                    0, strip, FAKE, 4096 * 4 - 4, None) == N.MTL_ERR_WORKSPACE
+    assert lib.mtl_w4_strip_bytes(4096, 24576) == 4096 * 24576 // 2
+    assert lib.mtl_w4_strip_bytes(4096, 24584) == 0 and lib.mtl_w4_strip_bytes(4224, 4096) == 0
+    assert lib.mtl_w4_strip(FAKE, 4096, 24584, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_w4_strip(FAKE, 4096, 4096, FAKE, 100, None) == N.MTL_ERR_WORKSPACE
+    assert lib.mtl_tune_set_strip_nb(3) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG

@@ -17,7 +17,7 @@ from moss_tts_lite_amd.fast import FastDecoder
 from moss_tts_lite_amd.model import BackboneConfig
 from oracle import decode_ref as D
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
-from tests._decode_case import build_case, small_config
+from tests._decode_case import build_case, slots16, small_config
 
 pytestmark = pytest.mark.gpu
 
@@ -180,10 +180,11 @@ def _oracle_caches(model):
     return kc, kc.copy()
 
 
-def test_mini_model_steps_match_oracle_and_graph_is_bitwise(dev):
+@pytest.mark.parametrize("plan", ["staged", "strip"])
+def test_mini_model_steps_match_oracle_and_graph_is_bitwise(dev, plan):
     cfg = small_config()
     model, ow = build_case(cfg, seed=11, dev=dev)
-    dec = FastDecoder(model)
+    dec = FastDecoder(model, plan=plan)
     cos, sin = fb(model.rope_cos), fb(model.rope_sin)
     prompt = [5, 17, 999, 0, 42, 7]
     # oracle: prompt then greedy decode
@@ -237,11 +238,15 @@ def test_launch_plans_agree(dev):
             dec.run_step()
             logits.append(fb(dec.logits))
         out[plan] = (toks, logits)
-    for plan in ("fused", "staged", "partials"):
+    # the split-K plans share the GEMV summation order with "unfused"; the strip plan sums
+    # in another order, so it differs by bf16 rounding noise that the attention softmax
+    # amplifies (its distance to the float64 oracle is held to the same bar as the
+    # others' in test_mini_model_steps_match_oracle_and_graph_is_bitwise)
+    for plan, bar in (("fused", 5e-3), ("staged", 5e-3), ("partials", 5e-3), ("strip", 2e-2)):
         for i in range(6):
             err = rel_l2(out[plan][1][i], out["unfused"][1][i])
             print(f"step {i}: {plan} vs unfused logits rel_l2={err:.2e}")
-            assert err < 5e-3
+            assert err < bar
     # the fused plan only moves the residual add into the GEMV epilogue: same sums in the
     # same order as partials + residual kernel, so the steps agree bit for bit
     assert out["fused"][0] == out["staged"][0]
@@ -249,7 +254,7 @@ def test_launch_plans_agree(dev):
         assert np.array_equal(out["fused"][1][i], out["staged"][1][i]), f"step {i}"
 
 
-@pytest.mark.parametrize("plan", ["fused", "staged", "partials"])
+@pytest.mark.parametrize("plan", ["strip", "fused", "staged", "partials"])
 def test_plan_graph_replay_is_bitwise(dev, plan):
     cfg = small_config()
     model, _ = build_case(cfg, seed=23, dev=dev)
@@ -415,7 +420,7 @@ def test_residual_add_slots_and_scatter(dev, lib):
     tp = torch.from_numpy(parts).to(dev)
     th = tb(resid, dev)
     h_ord = torch.zeros(n, dtype=torch.bfloat16, device=dev)
-    slots = torch.zeros(16, dtype=torch.float32, device=dev)
+    slots = torch.zeros(256, dtype=torch.float32, device=dev)
     ts = torch.from_numpy(scatter).to(dev)
     N.check(lib.mtl_residual_add(tp.data_ptr(), S, th.data_ptr(), ts.data_ptr(), h_ord.data_ptr(),
                                  slots.data_ptr(), n, stream()), "residual_add")
@@ -424,8 +429,9 @@ def test_residual_add_slots_and_scatter(dev, lib):
     ho = np.empty_like(h)
     ho[scatter] = h
     assert np.array_equal(fb(h_ord), ho)                  # scattered, bit-exact
-    blocks = (h.astype(np.float64) ** 2).reshape(16, -1).sum(1)
+    blocks = (h.astype(np.float64) ** 2).reshape(256, -1).sum(1)
     assert np.allclose(slots.cpu().numpy(), blocks, rtol=1e-5)
+    assert np.array_equal(slots.cpu().numpy(), slots16(h))   # the documented order, bitwise
     # without partials: h is only read; without scatter: plain copy
     h2 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
     N.check(lib.mtl_residual_add(None, 0, th.data_ptr(), None, h2.data_ptr(), slots.data_ptr(), n,
@@ -443,7 +449,7 @@ def test_gemm_norm_partials_match_oracle(dev, lib):
     h = round_bf16(r.standard_normal(K).astype(np.float32))
     w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    slots = t((h.astype(np.float32) ** 2).reshape(16, -1).sum(1, dtype=np.float32))
+    slots = t(slots16(h))
     S = int(lib.mtl_w4_gemm_splits(K, Nn))
     part = torch.empty(S * Nn, dtype=torch.float32, device=dev)
     qw, qz, sc = t(qs), t(case["qzeros"]), t(case["scales"].view(np.float16))
@@ -507,7 +513,7 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     h = round_bf16((2 * r.standard_normal(K)).astype(np.float32))
     w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
     W = round_bf16((r.standard_normal((V, K)) * 0.02).astype(np.float32))
-    slots = torch.from_numpy((h ** 2).reshape(16, -1).sum(1, dtype=np.float32)).to(dev)
+    slots = torch.from_numpy(slots16(h)).to(dev)
     tW, th, tw = tb(W, dev), tb(h, dev), tb(w, dev)
     logits = torch.zeros(V, dtype=torch.bfloat16, device=dev)
     tok = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -524,7 +530,7 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     assert int(tok.item()) == int(np.argmax(fb(logits)))
 
 
-@pytest.mark.parametrize("plan", ["fused", "unfused"])
+@pytest.mark.parametrize("plan", ["strip", "fused", "unfused"])
 def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
     # MOSS step: 33-way (here 1 + 4) embedding, layers, final norm, text + audio heads
     # (pad code -inf) or the audio2 variant (2-way + audio heads); graph == eager.
@@ -571,7 +577,7 @@ def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
 @pytest.mark.parametrize("src", ["bf16", "silu"])
 def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
     # mtl_w4_gemm_residual == mtl_w4_gemm_partials + mtl_residual_add, bit for bit
-    # (h in place, scattered copy, per-256-column sums of squares), on the o shape
+    # (h in place, scattered copy, per-16-column sums of squares), on the o shape
     # (bf16 x, K=4096) and the down shape (SiLU*up of gate|up partials, K=12288)
     from oracle import synth
     from moss_tts_lite_amd import ops
@@ -599,16 +605,16 @@ def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
                                      qz.data_ptr(), None, n, 128, 0, 0, part.data_ptr(),
                                      part.numel() * 4, stream()), "partials")
     h_a, ord_a = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
-    slots_a = torch.zeros(64, dtype=torch.float32, device=dev)
+    slots_a = torch.zeros(1024, dtype=torch.float32, device=dev)
     N.check(lib.mtl_residual_add(part.data_ptr(), S, h_a.data_ptr(), scatter.data_ptr(),
                                  ord_a.data_ptr(), slots_a.data_ptr(), n, stream()), "residual_add")
     ws = torch.zeros(ops.gemm_workspace_bytes(1, k, n, 128), dtype=torch.uint8, device=dev)
     for rep in range(2):     # the second launch checks the counters were left at zero
         h_b, ord_b = h0.clone(), torch.zeros(n, dtype=torch.bfloat16, device=dev)
-        slots_b = torch.zeros(64, dtype=torch.float32, device=dev)
+        slots_b = torch.zeros(1024, dtype=torch.float32, device=dev)
         N.check(lib.mtl_w4_gemm_residual(p(x), p(xpart), xs, ld, k, qw.data_ptr(), sc.data_ptr(),
                                          qz.data_ptr(), n, 128, 0, 0, h_b.data_ptr(),
                                          scatter.data_ptr(), ord_b.data_ptr(), slots_b.data_ptr(),
                                          ws.data_ptr(), ws.numel(), stream()), "residual gemv")
         assert torch.equal(h_a, h_b) and torch.equal(ord_a, ord_b)
-        assert torch.equal(slots_a[:n // 256], slots_b[:n // 256])
+        assert torch.equal(slots_a[:n // 16], slots_b[:n // 16])

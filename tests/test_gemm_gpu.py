@@ -367,7 +367,7 @@ def test_tiled_stream_equals_row_stream(dev, k, n, src):
         if src == "norm":
             h = t_bf16(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)), dev) if not outs else h
             wn = t_bf16(f32_to_bf16_bits(np.ones(k, np.float32)), dev) if not outs else wn
-            slots = torch.ones(64, dtype=torch.float32, device=dev) * float(k) / 64
+            slots = torch.ones(1024, dtype=torch.float32, device=dev) * 16.0   # sum = k
             N.check(lib.mtl_w4_gemm_norm_partials(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
                                                   ctypes.c_float(1e-6), k, w.data_ptr(), sc.data_ptr(),
                                                   qz.data_ptr(), n, 128, 0, layout, part.data_ptr(),
@@ -384,3 +384,216 @@ def test_tiled_stream_equals_row_stream(dev, k, n, src):
                                              part.data_ptr(), part.numel() * 4, st), "partials")
         outs.append(part)
     assert torch.equal(outs[0], outs[1])
+
+
+# ------------------------------------------------------------------ full-K strip GEMV
+
+def _strip_np(qweight: np.ndarray) -> np.ndarray:
+    """The documented layout: 16-byte word l of 1 KB block (s*K/128 + b) holds the words
+    (row 16b + 4j + l/16, column 16s + l%16), j = 0..3."""
+    rows, n = qweight.shape
+    w = qweight.view(np.uint32).reshape(rows // 16, 4, 4, n // 16, 16)   # b, j, l/16, s, l%16
+    return np.ascontiguousarray(w.transpose(3, 0, 2, 4, 1)).reshape(-1)
+
+
+@pytest.mark.parametrize("k,n", [(1024, 128), (4608, 336)])
+def test_strip_layout_bit_exact(dev, k, n):
+    qw = synth.random_qweight(synth.rng(k + n + 1), k, n)
+    out = ops.strip_weights(t_i32(qw, dev)).cpu().numpy().view(np.uint32)
+    assert np.array_equal(out, _strip_np(qw))
+
+
+def _strip_partials(lib, case, dev, src, x=None, xp=None, h=None, wn=None, slots=None):
+    """One strip launch through the partials (or norm-partials) entry: fp32 [N]."""
+    import ctypes
+    k, n, g = case["k"], case["n"], case["group"]
+    qw = ops.strip_weights(t_i32(case["qweight"], dev))
+    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    y = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    if src == "norm":
+        N.check(lib.mtl_w4_gemm_norm_partials(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                              ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
+                                              qz.data_ptr(), n, g, 0, N.LAYOUT_STRIP, y.data_ptr(),
+                                              y.numel() * 4, st), "strip norm")
+    else:
+        N.check(lib.mtl_w4_gemm_partials(None if x is None else x.data_ptr(),
+                                         None if xp is None else xp.data_ptr(),
+                                         0 if xp is None else xp.shape[0], 0 if xp is None else 2 * k,
+                                         1, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), None, n,
+                                         g, 0, N.LAYOUT_STRIP, y.data_ptr(), y.numel() * 4, st),
+                "strip partials")
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("group,k,n", [(32, 1024, 528), (64, 2048, 768), (128, 4096, 6144),
+                                       (128, 12288, 4096), (256, 4096, 4112), (128, 512, 1024)])
+def test_strip_gemv_matches_oracle(dev, group, k, n):
+    lib = N.load()
+    case = synth.gptq_case(k=k, n=n, m=1, group=group, seed=group + k + n)
+    y = _strip_partials(lib, case, dev, "bf16", x=t_bf16(case["x_bits"], dev))
+    err = rel_l2(y.cpu().numpy(), case["y_ref"][0])
+    print(f"strip g{group} {k}x{n} rel_l2={err:.2e}")
+    assert err < TOL_F32
+    # repeatable bit for bit
+    assert torch.equal(y, _strip_partials(lib, case, dev, "bf16", x=t_bf16(case["x_bits"], dev)))
+
+
+def test_strip_norm_staging_matches_oracle(dev):
+    from oracle import decode_ref as D
+    from tests._decode_case import slots16
+    lib = N.load()
+    k, n = 4096, 6144
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=77, with_ref=False)
+    r = np.random.default_rng(78)
+    hf = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)))
+    wf = bf16_bits_to_f32(f32_to_bf16_bits((1 + 0.1 * r.standard_normal(k)).astype(np.float32)))
+    h, wn = t_bf16(f32_to_bf16_bits(hf), dev), t_bf16(f32_to_bf16_bits(wf), dev)
+    slots = torch.from_numpy(slots16(hf)).to(dev)
+    y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots)
+    x = D.rms_norm(hf, wf)
+    ref = G.gptq_gemm(x[None], case["qweight"], case["qzeros"], case["scales"], case["g_idx"], 128)[0]
+    err = rel_l2(y.cpu().numpy(), ref)
+    print(f"strip norm-staged rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("xsplits", [1, 8])
+def test_strip_silu_staging_matches_split_k(dev, xsplits):
+    # same SiLU*up staging (bitwise equal x) as the split-K GEMV; only the fp32 summation
+    # order of the product differs
+    import ctypes  # noqa: F401
+    lib = N.load()
+    k, n = 12288, 4096
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=91, with_ref=False)
+    r = np.random.default_rng(92)
+    xp = torch.from_numpy((r.standard_normal((xsplits, 2 * k)) * 0.5).astype(np.float32)).to(dev)
+    y = _strip_partials(lib, case, dev, "silu", xp=xp)
+    qw, qz, sc = t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    S = int(lib.mtl_w4_gemm_splits(k, n))
+    part = torch.zeros(S * n, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_w4_gemm_partials(None, xp.data_ptr(), xsplits, 2 * k, 1, k, qw.data_ptr(),
+                                     sc.data_ptr(), qz.data_ptr(), None, n, 128, 0, N.LAYOUT_ROWS,
+                                     part.data_ptr(), part.numel() * 4,
+                                     torch.cuda.current_stream().cuda_stream), "split-k silu")
+    ref = part.view(S, n).double().sum(0).cpu().numpy()
+    err = rel_l2(y.cpu().numpy(), ref)
+    print(f"strip silu xsplits={xsplits} vs split-K rel_l2={err:.2e}")
+    assert err < 1e-5
+
+
+@pytest.mark.parametrize("src", ["bf16", "silu"])
+def test_strip_residual_epilogue(dev, src):
+    # h = bf16(bf16(y) + h) with y the strip GEMV's own sums (store path), the scattered
+    # copy and the per-16-column slots, bit for bit; equal to the store path followed by
+    # mtl_residual_add over that single split
+    from tests._decode_case import slots16
+    lib = N.load()
+    k, n = (4096, 4096) if src == "bf16" else (12288, 4096)
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=5 + k, with_ref=False)
+    r = np.random.default_rng(6)
+    x = xp = None
+    if src == "bf16":
+        x = t_bf16(case["x_bits"], dev)
+    else:
+        xp = torch.from_numpy((r.standard_normal((1, 2 * k)) * 0.5).astype(np.float32)).to(dev)
+    y = _strip_partials(lib, case, dev, src, x=x, xp=xp)
+    h0f = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(n).astype(np.float32)))
+    scatter = torch.from_numpy(r.permutation(n).astype(np.int32)).to(dev)
+    qw = ops.strip_weights(t_i32(case["qweight"], dev))
+    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    st = torch.cuda.current_stream().cuda_stream
+    for rep in range(2):
+        h = t_bf16(f32_to_bf16_bits(h0f), dev)
+        h_ord = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+        slots = torch.zeros(1024, dtype=torch.float32, device=dev)
+        N.check(lib.mtl_w4_gemm_residual(None if x is None else x.data_ptr(),
+                                         None if xp is None else xp.data_ptr(),
+                                         0 if xp is None else 1, 0 if xp is None else 2 * k, k,
+                                         qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), n, 128, 0,
+                                         N.LAYOUT_STRIP, h.data_ptr(), scatter.data_ptr(),
+                                         h_ord.data_ptr(), slots.data_ptr(), None, 0, st),
+                "strip residual")
+        torch.cuda.synchronize()
+        yv = y.cpu().numpy()
+        hv = bf16_bits_to_f32(f32_to_bf16_bits(
+            bf16_bits_to_f32(f32_to_bf16_bits(yv)) + h0f))
+        got = h.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got, f32_to_bf16_bits(hv)), f"rep {rep}"
+        ho = np.empty(n, np.uint16)
+        ho[scatter.cpu().numpy()] = f32_to_bf16_bits(hv)
+        assert np.array_equal(h_ord.view(torch.int16).cpu().numpy().view(np.uint16), ho)
+        assert np.array_equal(slots[:n // 16].cpu().numpy(), slots16(hv))
+    # the same through mtl_residual_add over the store path's single split
+    h2 = t_bf16(f32_to_bf16_bits(h0f), dev)
+    o2 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    s2 = torch.zeros(1024, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_residual_add(y.data_ptr(), 1, h2.data_ptr(), scatter.data_ptr(), o2.data_ptr(),
+                                 s2.data_ptr(), n, st), "residual_add")
+    torch.cuda.synchronize()
+    assert torch.equal(h2, h) and torch.equal(o2, h_ord) and torch.equal(s2, slots)
+
+
+def test_strip_blocks_per_wave_knob(dev):
+    # every launch shape of the strip GEMV computes the same product (rounding aside)
+    lib = N.load()
+    case = synth.gptq_case(k=4096, n=1024, m=1, group=128, seed=3)
+    x = t_bf16(case["x_bits"], dev)
+    outs = {}
+    try:
+        for nb in (0, 2, 4, 8):
+            assert lib.mtl_tune_set_strip_nb(nb) == 0
+            outs[nb] = _strip_partials(lib, case, dev, "bf16", x=x).cpu().numpy()
+    finally:
+        lib.mtl_tune_set_strip_nb(0)
+    for nb, y in outs.items():
+        assert rel_l2(y, case["y_ref"][0]) < TOL_F32, nb
+    assert np.array_equal(outs[0], outs[4])     # automatic choice for K = 4096
+
+
+def test_strip_norm_silu_epilogue(dev):
+    # gate|up with RMSNorm staging and the SiLU*up epilogue (a gate strip and its up
+    # strip per workgroup): act equals bf16(silu(bf16 g) * bf16 u) of the strip sums taken
+    # with the same K slicing (4 blocks per wave for K = 4096), to float32 libm rounding,
+    # and the float64 oracle within the bf16 bar
+    import ctypes
+    from oracle import decode_ref as D
+    from tests._decode_case import slots16
+    lib = N.load()
+    k, n = 4096, 2048
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=123, with_ref=False)
+    r = np.random.default_rng(124)
+    hf = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)))
+    wf = bf16_bits_to_f32(f32_to_bf16_bits((1 + 0.1 * r.standard_normal(k)).astype(np.float32)))
+    h, wn = t_bf16(f32_to_bf16_bits(hf), dev), t_bf16(f32_to_bf16_bits(wf), dev)
+    slots = torch.from_numpy(slots16(hf)).to(dev)
+    qw = ops.strip_weights(t_i32(case["qweight"], dev))
+    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    act = torch.zeros(n // 2, dtype=torch.bfloat16, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                     ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
+                                     qz.data_ptr(), n, 128, 0, N.LAYOUT_ROWS, act.data_ptr(),
+                                     st) == N.MTL_ERR_UNSUPPORTED
+    N.check(lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                      ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
+                                      qz.data_ptr(), n, 128, 0, N.LAYOUT_STRIP, act.data_ptr(), st),
+            "norm silu")
+    y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots).cpu().numpy()
+    j = np.arange(n // 2)
+    gcol = (j // 32) * 64 + j % 32
+    rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
+    g = rb(y[gcol])
+    sg = rb(g / (np.float32(1) + np.exp(-g)))
+    ref_bits = f32_to_bf16_bits((sg * rb(y[gcol + 32])).astype(np.float32))
+    got_bits = act.view(torch.int16).cpu().numpy().view(np.uint16)
+    ulps = np.abs(got_bits.astype(np.int32) - ref_bits.astype(np.int32))
+    assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99
+    x = D.rms_norm(hf, wf)
+    y64 = G.gptq_gemm(x[None], case["qweight"], case["qzeros"], case["scales"], case["g_idx"], 128)[0]
+    g64, u64 = y64[gcol], y64[gcol + 32]
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    err = rel_l2(bf16_bits_to_f32(got_bits), ref)
+    print(f"strip norm+silu rel_l2={err:.2e}")
+    assert err < TOL_BF16
