@@ -267,22 +267,30 @@ def bench_decode(args, torch):
         roofline={"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1),
                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
-                  "traffic": profiled_traffic("gate_up"),
-                  "kernel": "w4_gemm_kernel<1,4,GPTQ,XSRC_RMSNORM> gate_up 4096x24576 M=1 "
-                            "(split-K partials, as launched in the decode step)",
+                  "traffic": profiled_traffic("gate_up", dec.plan),
+                  "kernel": GATE_UP_KERNEL.get(dec.plan, "gate_up 4096x24576 M=1")
+                            + " (as launched in the decode step)",
                   "bytes_per_launch": gu_bytes},
     )
 
 
-def profiled_traffic(name: str):
-    """HBM bytes per launch of one decode-step GEMV, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (copy-kernel calibrated); None if absent."""
+# The gate|up launch of each decode plan (the dominant kernel of the step).
+GATE_UP_KERNEL = {
+    "strip": "w4_strip_kernel<g128, RMSNORM, SILU, 4 blocks/wave, 2 strips> gate_up 4096x24576 "
+             "M=1 (full-K strips, SiLU*up epilogue)",
+    "staged": "w4_gemm_kernel<1,4,GPTQ,XSRC_RMSNORM> gate_up 4096x24576 M=1 (split-K partials)",
+}
+
+
+def profiled_traffic(name: str, plan: str):
+    """HBM bytes per launch of one decode-step GEMV of that plan, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-kernel calibrated); None if absent."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "gemv_traffic_decode_shapes.md")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith(f"traffic_bytes {name}:"):
+                if line.startswith(f"traffic_bytes {plan} {name}:"):
                     return int(line.split(":")[1])
     except OSError:
         pass
@@ -381,7 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--plan", default="staged",
+    ap.add_argument("--plan", default="strip",
                     choices=["strip", "fused", "staged", "partials", "unfused"],
                     help="decode launch plan (decode workload)")
     args = ap.parse_args()

@@ -52,7 +52,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // 16-column block: slots[b] = sum over h[16b .. 16b+15] of h^2, formed as four fma chains
 // over 4 consecutive columns (lanes 4i .. 4i+3) joined by slot_combine.  Every producer
 // uses that order, so every launch plan sees the same slot values.  The RMSNorm that
-// consumes them sums the ceil(n/16) slots with one wave (slot_part + wave_sum).
+// consumes them sums the ceil(n/16) slots with one wave (slot_issue, slot_finish, wave_sum).
 constexpr int kSlotCols = 16;
 constexpr int kMaxSlots = 1024;   // hidden <= 16384
 
@@ -61,28 +61,46 @@ __device__ __forceinline__ float slot_combine(float ss) {
   return ss + __shfl_xor(ss, 2);
 }
 
-// This lane's share of the slot total: slots 4*lane .. +3, then +256, ... (fixed order).
-// slots must be 16-byte aligned.
-__device__ __forceinline__ float slot_part(const float* slots, int n, int lane) {
+// A wave reads the slots as float4 chunks: lane l sums slots 4l .. 4l+3, then +256, ...
+// (fixed order).  slot_issue only loads (uniform branches, clamped in-bounds addresses), so
+// a kernel can put the loads in flight and sum them once other loads are issued too.
+// A slot buffer holds ceil(ns / 4) * 4 floats, ns = ceil(n / 16).
+struct SlotLoad {
+  float4 v[kMaxSlots / 256];
+};
+
+__device__ __forceinline__ void slot_issue(const float* slots, int n, int lane, SlotLoad& sl) {
   const int ns = (n + kSlotCols - 1) / kSlotCols;
-  float s = 0.f;
-  for (int b = 4 * lane; b < ns; b += 256) {
-    float4 v;
-    if (b + 4 <= ns) {
-      v = *reinterpret_cast<const float4*>(slots + b);
-    } else {
-      v.x = slots[b];
-      v.y = b + 1 < ns ? slots[b + 1] : 0.f;
-      v.z = b + 2 < ns ? slots[b + 2] : 0.f;
-      v.w = 0.f;
+  const int nch = (ns + 255) / 256;
+#pragma unroll
+  for (int it = 0; it < kMaxSlots / 256; ++it) {
+    if (it < nch) {
+      const int b = 4 * lane + 256 * it;
+      sl.v[it] = *reinterpret_cast<const float4*>(slots + (b < ns ? b : 0));
     }
-    s += (v.x + v.y) + (v.z + v.w);
+  }
+}
+
+__device__ __forceinline__ float slot_finish(const SlotLoad& sl, int n, int lane) {
+  const int ns = (n + kSlotCols - 1) / kSlotCols;
+  const int nch = (ns + 255) / 256;
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < kMaxSlots / 256; ++it) {
+    if (it < nch) {
+      const int b = 4 * lane + 256 * it;
+      const float4 v = sl.v[it];
+      s += ((b < ns ? v.x : 0.f) + (b + 1 < ns ? v.y : 0.f)) +
+           ((b + 2 < ns ? v.z : 0.f) + (b + 3 < ns ? v.w : 0.f));
+    }
   }
   return s;
 }
 
 __device__ __forceinline__ float slot_total(const float* slots, int n, int lane) {
-  return wave_sum(slot_part(slots, n, lane));
+  SlotLoad sl;
+  slot_issue(slots, n, lane, sl);
+  return wave_sum(slot_finish(sl, n, lane));
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

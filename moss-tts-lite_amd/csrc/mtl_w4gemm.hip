@@ -108,7 +108,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   //    MR = 1 (threads 0..63).  Raw values now; transformed once the loads are back.
   u32x4 xv[XPT], wv[XSRC == XSRC_RMSNORM ? XPT : 1];
   bool xok[XPT];
-  float slot_v = 0.f;                         // XSRC_RMSNORM: lane's sum-of-squares slot
+  SlotLoad slot_l;                            // XSRC_RMSNORM: the sums of squares of h
   const bool stager = MR > 1 || t < kRowsPerWG;
   auto load_x = [&]() {
 #pragma unroll
@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
     s_pb = a.xpart + 64 * (j0 >> 5) + (j0 & 31) + 2 * (t & 3);
     silu_batch(0);
   }
-  if (XSRC == XSRC_RMSNORM && stager) slot_v = slot_part(a.slots, a.K, lane);
+  if (XSRC == XSRC_RMSNORM && stager) slot_issue(a.slots, a.K, lane, slot_l);
 
   // 2. Group metadata of the lane's 4 columns, one entry per group of the split.
   const int colc = col_ok ? col : N - 4;
@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   if (stager) {
     float norm_r = 0.f;
     if (XSRC == XSRC_RMSNORM)     // rsqrt(mean(h^2) + eps) from the slots (one wave)
-      norm_r = rsqrtf(wave_sum(slot_v) / (float)a.K + a.eps);
+      norm_r = rsqrtf(wave_sum(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
       const int m = MR == 1 ? 0 : (t >> 6) + 4 * j;
@@ -726,6 +726,11 @@ static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32
   return MTL_OK;
 }
 
+// The strip GEMV reads 16 scales (32 B) and 16 zero nibbles (8 B) of a strip at a time.
+static bool strip_meta_aligned(const void* scales, const int32_t* qzeros) {
+  return aligned16(scales) && (reinterpret_cast<uintptr_t>(qzeros) & 7u) == 0;
+}
+
 // The strip GEMV's arguments common to every entry point.
 static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
                             const int32_t* qzeros, int64_t N, int group, int zero_offset) {
@@ -778,6 +783,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
     if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
+    if (!strip_meta_aligned(meta0, qzeros)) return MTL_ERR_ALIGN;
     StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
     sa.x = static_cast<const uint16_t*>(x);
     sa.xpart = xpart;
@@ -827,6 +833,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
     if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
+    if (!strip_meta_aligned(meta0, qzeros)) return MTL_ERR_ALIGN;
     StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
     sa.hn = static_cast<const uint16_t*>(h_ord);
     sa.wn = static_cast<const uint16_t*>(w_ord);
@@ -883,7 +890,8 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
   if (!aligned16(qweight) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   if (layout == MTL_LAYOUT_STRIP) {
-    if (!aligned16(slots)) return MTL_ERR_ALIGN;
+    if (!aligned16(slots) || (scatter && !aligned16(scatter)) || !strip_meta_aligned(meta0, qzeros))
+      return MTL_ERR_ALIGN;
     StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
     sa.x = static_cast<const uint16_t*>(x);
     sa.xpart = xpart;
@@ -941,7 +949,7 @@ static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* 
       N * K / 2 >= ((int64_t)1 << 31) || K > (int64_t)kSlotCols * kMaxSlots)
     return MTL_ERR_SHAPE;
   if (!aligned16(slots) || !aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) ||
-      (reinterpret_cast<uintptr_t>(act) & 7u) || (reinterpret_cast<uintptr_t>(meta0) & 7u))
+      (reinterpret_cast<uintptr_t>(act) & 7u) || !strip_meta_aligned(meta0, qzeros))
     return MTL_ERR_ALIGN;
   StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
   sa.hn = static_cast<const uint16_t*>(h_ord);

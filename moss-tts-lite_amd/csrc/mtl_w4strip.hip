@@ -25,6 +25,10 @@ namespace mtl {
 constexpr int kStripCols = 16;
 constexpr int kStripBlockK = 128;     // input channels per 1 KB block
 constexpr int kStripMaxWaves = 16;
+// Waves per workgroup allowed at NB blocks per wave (16 blocks: at most 8 waves, so the
+// kernel may use up to 256 VGPRs), and the occupancy its register allocation must leave.
+constexpr int strip_max_waves(int nb) { return nb >= 16 ? 8 : kStripMaxWaves; }
+constexpr int strip_min_occupancy(int nb) { return 1; }
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
 
 static int g_strip_nb = 0;            // tuning override of blocks per wave (0: auto)
@@ -32,7 +36,8 @@ static int g_strip_ct = 0;            // tuning override of strips per workgroup
 static int g_strip_xcd = 1;           // 1: XCD-contiguous strip order (see the kernel)
 
 template <int GR, int XSRC, int EPI, int NB, int CT>
-__global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs a) {
+__global__ void __launch_bounds__(64 * strip_max_waves(NB), strip_min_occupancy(NB))
+w4_strip_kernel(StripArgs a) {
   constexpr int ITEMS = 16 * NB;               // x items (8 channels) per K slice
   constexpr int STAGERS = 64 * CT;             // threads that stage one slice
   constexpr int ROUNDS = (ITEMS + STAGERS - 1) / STAGERS;
@@ -94,8 +99,19 @@ __global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs
     }
   }
   const bool stages = cs * 64 < ITEMS;         // wave-uniform: this wave stages items
-  float slot_v = 0.f;
-  if (XSRC == XSRC_RMSNORM && stages) slot_v = slot_part(a.slots, a.K, lane);
+  SlotLoad slot_l;
+  if (XSRC == XSRC_RMSNORM && stages) slot_issue(a.slots, a.K, lane, slot_l);
+  // residual epilogue inputs of wave 0's column owners, read ahead of everything else
+  u32x2 h_pre{0u, 0u};
+  int32_t sc_pre[4] = {0, 0, 0, 0};
+  const int c_own = (EPI == STRIP_EPI_SILU ? 0 : s0 * kStripCols) + 4 * (lane & (4 * CT - 1));
+  if (EPI == STRIP_EPI_RESID && wave == 0) {
+    h_pre = *reinterpret_cast<const u32x2*>(a.h + c_own);
+    if (a.h_ord && a.scatter) {
+      const int4 p4 = *reinterpret_cast<const int4*>(a.scatter + c_own);
+      sc_pre[0] = p4.x; sc_pre[1] = p4.y; sc_pre[2] = p4.z; sc_pre[3] = p4.w;
+    }
+  }
 
   // 2. Group metadata of the lane's column, one entry per group of the slice.
   const int grp0 = item0 * 8 / a.group;
@@ -121,7 +137,8 @@ __global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs
   // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
   if (stages) {
     float norm_r = 0.f;
-    if (XSRC == XSRC_RMSNORM) norm_r = rsqrtf(wave_sum(slot_v) / (float)a.K + a.eps);
+    if (XSRC == XSRC_RMSNORM)
+      norm_r = rsqrtf(wave_sum(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
       u32x4 v = xv[r];
@@ -223,7 +240,7 @@ __global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs
   }
   // 7. Residual epilogue (fast.py:168-171): h = bf16(bf16(y) + h) in place, h scattered to
   //    the next GEMV's input order, and each strip's sum of squares as one slot.
-  const u32x2 rr = *reinterpret_cast<const u32x2*>(a.h + c0);
+  const u32x2 rr = h_pre;
   float hv[4] = {bf16_to_f32(rr.x & 0xffffu), bf16_to_f32(rr.x >> 16),
                  bf16_to_f32(rr.y & 0xffffu), bf16_to_f32(rr.y >> 16)};
   float ss = residual4(y, hv);
@@ -235,21 +252,24 @@ __global__ void __launch_bounds__(64 * kStripMaxWaves) w4_strip_kernel(StripArgs
     if (a.h_ord) {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        a.h_ord[a.scatter ? a.scatter[c0 + c] : c0 + c] = (uint16_t)f32_to_bf16(hv[c]);
+        a.h_ord[a.scatter ? sc_pre[c] : c0 + c] = (uint16_t)f32_to_bf16(hv[c]);
     }
     if ((lane & 3) == 0) a.slots_out[s0 + ec] = ss;
   }
 }
 
-// Blocks per wave for K/128 = kb blocks with ct strips per workgroup: KW * ct <= 16
-// waves, even NB (whole groups up to g = 256), 4 where it fits.
+// Blocks per wave for K/128 = kb blocks with ct strips per workgroup: KW * ct waves within
+// strip_max_waves(NB), even NB (whole groups up to g = 256), 4 where it fits.
+static bool nb_fits(int64_t kb, int nb, int ct) {
+  return kb % nb == 0 && (kb / nb) * ct <= strip_max_waves(nb);
+}
+
 static int blocks_per_wave(int64_t K, int ct) {
   if (K <= 0 || K % (2 * kStripBlockK) != 0) return 0;
   const int64_t kb = K / kStripBlockK;
-  const int64_t maxkw = kStripMaxWaves / ct;
-  if (g_strip_nb) return (kb % g_strip_nb == 0 && kb / g_strip_nb <= maxkw) ? g_strip_nb : 0;
-  for (const int nb : {4, 6, 8, 2})
-    if (kb % nb == 0 && kb / nb <= maxkw) return nb;
+  if (g_strip_nb) return nb_fits(kb, g_strip_nb, ct) ? g_strip_nb : 0;
+  for (const int nb : {4, 6, 8, 2, 16})
+    if (nb_fits(kb, nb, ct)) return nb;
   return 0;
 }
 
@@ -273,7 +293,8 @@ static void strip_nb(const StripArgs& a, int nb, hipStream_t st) {
     case 2: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 2, CT>), grid, block, lds, st, a); break;
     case 4: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 4, CT>), grid, block, lds, st, a); break;
     case 6: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 6, CT>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 8, CT>), grid, block, lds, st, a); break;
+    case 8: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 8, CT>), grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 16, CT>), grid, block, lds, st, a); break;
   }
 }
 
@@ -358,7 +379,7 @@ int mtl_w4_strip(const int32_t* qweight, int64_t K, int64_t N, int32_t* strip,
 // Tuning knobs for launch-shape sweeps (process-wide, not for concurrent use).
 // Blocks per wave of the strip GEMV (0 = automatic).
 int mtl_tune_set_strip_nb(int32_t nb) {
-  if (nb != 0 && nb != 2 && nb != 4 && nb != 6 && nb != 8) return MTL_ERR_INVALID_ARG;
+  if (nb != 0 && nb != 2 && nb != 4 && nb != 6 && nb != 8 && nb != 16) return MTL_ERR_INVALID_ARG;
   g_strip_nb = nb;
   return MTL_OK;
 }

@@ -17,16 +17,16 @@ identical kernel sequence.
 
 Five launch plans produce the same step:
 
-* ``"strip"``: five launches per layer, with no split-K anywhere.  Every int4 GEMV runs
-  as the full-K strip GEMV (a workgroup owns 16-column strips over all of K): q|k|v hands
-  its final fp32 sums to the attention as a single split, gate|up applies SiLU*up in its
-  epilogue and down reads that bf16 product, and o and down apply the residual add in
-  their epilogue (publishing the sums of squares and the scattered copy of ``h`` the next
-  RMSNorm-staged GEMV reads).
-  Its GEMV sums run in a different order than the split-K plans', so it agrees with
-  them to rounding, not bitwise.
+* ``"strip"`` (default): five launches per layer and no cross-workgroup reduction after
+  the attention.  o, gate|up and down run as the full-K strip GEMV (a workgroup owns
+  16-column strips over all of K): gate|up applies SiLU*up in its epilogue and down reads
+  that bf16 product, and o and down apply the residual add in their epilogue (publishing
+  the sums of squares and the scattered copy of ``h`` the next RMSNorm-staged GEMV reads).
+  q|k|v keeps the split-K GEMV (``split_k=("qkv",)``), whose partials the attention sums
+  anyway; ``split_k=()`` runs it as a strip too (one "split").  Its GEMV sums run in a
+  different order than the split-K plans', so it agrees with them to rounding, not bitwise.
 
-* ``"staged"`` (default): each int4 GEMV publishes only its split-K partials and the
+* ``"staged"``: each int4 GEMV publishes only its split-K partials and the
   consumer folds the reduction in.  A 16-workgroup residual add sums the o/down
   partials into ``h``, publishes 16 block sums of squares and scatters ``h`` into the
   next GEMV's act-order input order; that GEMV applies RMSNorm while staging its input
@@ -72,13 +72,21 @@ class FastDecoder:
 
     PLANS = ("strip", "fused", "staged", "partials", "unfused")
 
-    def __init__(self, model: Int4Backbone, plan: str = "staged"):
+    def __init__(self, model: Int4Backbone, plan: str = "strip", split_k: tuple | None = None):
         if plan not in self.PLANS:
             raise ValueError(f"plan must be one of {self.PLANS}")
+        if split_k is None:   # measured fastest: q|k|v keeps split-K (the attention sums it)
+            split_k = ("qkv",) if plan == "strip" else ()
+        if not set(split_k) <= {"qkv", "gate_up"} or (split_k and plan != "strip"):
+            raise ValueError("split_k names GEMVs of the strip plan: 'qkv', 'gate_up'")
         self.m = model
         self.plan = plan
         self.fused = plan != "unfused"
-        self.strip = plan == "strip"       # full-K strip GEMVs: one "split" each
+        self.strip = plan == "strip"
+        # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
+        # keep the split-K kernel and hand their partials to the consumer
+        self.strip_gemv = {name: self.strip and name not in split_k
+                           for name in ("qkv", "o", "gate_up", "down")}
         cfg = model.cfg
         dev = model.device
         self.dev = dev
@@ -102,7 +110,7 @@ class FastDecoder:
         self.head_ws = torch.zeros(int(lib.mtl_head_workspace_bytes(cfg.vocab)), dtype=torch.uint8,
                                    device=dev)
         # fused plan: per-GEMV split-K partial buffers and the act-order input buffers
-        self.splits = {name: 1 if self.strip else int(lib.mtl_w4_gemm_splits(k, n))
+        self.splits = {name: 1 if self.strip_gemv[name] else int(lib.mtl_w4_gemm_splits(k, n))
                        for name, k, n in
                        (("qkv", cfg.hidden, cfg.qkv_out), ("o", cfg.hidden, cfg.hidden),
                         ("gate_up", cfg.hidden, 2 * cfg.intermediate),
@@ -155,7 +163,7 @@ class FastDecoder:
     def _partials(self, x, xpart_name, lin, n, name):
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip)
+        qw, layout = lin.stream_weight(self.strip_gemv[name])
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
@@ -263,7 +271,7 @@ class FastDecoder:
                                             self.attn_ws.numel())),
             self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu),
         ]
-        if self.strip:   # SiLU*up in the gate|up epilogue; down reads the bf16 product
+        if self.strip_gemv["gate_up"]:   # SiLU*up in the epilogue; down reads the product
             plan += [
                 self._norm_silu(self.x_gu, self.norm_gu[li], lyr["gate_up"]),
                 self._residual(self.act, None, lyr["down"],
@@ -303,7 +311,7 @@ class FastDecoder:
 
     def _norm_partials(self, h_ord, w_ord, lin, n, name):
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip)
+        qw, layout = lin.stream_weight(self.strip_gemv[name])
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),

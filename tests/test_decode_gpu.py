@@ -254,11 +254,12 @@ def test_launch_plans_agree(dev):
         assert np.array_equal(out["fused"][1][i], out["staged"][1][i]), f"step {i}"
 
 
-@pytest.mark.parametrize("plan", ["strip", "fused", "staged", "partials"])
-def test_plan_graph_replay_is_bitwise(dev, plan):
+@pytest.mark.parametrize("plan,split_k", [("strip", None), ("strip", ()), ("fused", None),
+                                          ("staged", None), ("partials", None)])
+def test_plan_graph_replay_is_bitwise(dev, plan, split_k):
     cfg = small_config()
     model, _ = build_case(cfg, seed=23, dev=dev)
-    dec = FastDecoder(model, plan=plan)
+    dec = FastDecoder(model, plan=plan, split_k=split_k)
     prompt = torch.tensor([8, 6, 7, 5, 3, 0, 9])
     dec.prefill(prompt)
     eager = []
