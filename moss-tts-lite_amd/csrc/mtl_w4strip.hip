@@ -29,6 +29,8 @@ constexpr int kStripMaxWaves = 16;
 // kernel may use up to 256 VGPRs), and the occupancy its register allocation must leave.
 constexpr int strip_max_waves(int nb) { return nb >= 16 ? 8 : kStripMaxWaves; }
 constexpr int strip_min_occupancy(int nb) { return 1; }
+// Blocks in flight per wave (the load ring).
+constexpr int strip_window(int nb) { return nb < 4 ? nb : 4; }
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
 
 static int g_strip_nb = 0;            // tuning override of blocks per wave (0: auto)
@@ -113,25 +115,42 @@ w4_strip_kernel(StripArgs a) {
     }
   }
 
-  // 2. Group metadata of the lane's column, one entry per group of the slice.
+  // 2-3. The weight stream and its group metadata, WIN blocks in flight per wave: block b
+  //      and the scales/zeros of the groups starting in it go to ring slot b % WIN, and
+  //      block b + WIN is issued into that slot as soon as block b's operands are out.
+  //      Loads complete in issue order, so waiting for block b never waits for a later
+  //      one, and the unpack and MFMA work overlaps the rest of the stream.
+  constexpr int WIN = strip_window(NB);
+  constexpr int MB = GR <= 4 ? 4 / GR : 1;     // groups starting in one block
   const int grp0 = item0 * 8 / a.group;
-  uint32_t sraw[NGW], zraw[NGW];
-#pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-    sraw[g] = a.scales[(size_t)(grp0 + g) * N + col];
-    zraw[g] = a.qzeros[(size_t)(grp0 + g) * (N >> 3) + (col >> 3)];
-  }
-
-  // 3. The weight stream: NB consecutive 1 KB blocks per wave, all in flight at once.
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / kStripCols) * a.kblocks * 1024),
       0x00020000);
   const int blk0 = s * a.kblocks + ks * NB;
-  u32x4 wq[NB];
+  // metadata through buffer loads too: a uniform (SGPR) row offset per group and one
+  // per-lane column offset, so no 64-bit address is held per group
+  const int ngroups = a.K / a.group;
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.scales), (short)0, ngroups * N * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 3) * 4, 0x00020000);
+  u32x4 wq[WIN];
+  uint32_t ms[WIN][MB], mz[WIN][MB];
+  auto issue = [&](int b) {
+    const int r = b % WIN;
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
-    wq[b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+    for (int m = 0; m < MB; ++m) {
+      if (GR <= 4 || (b & 1) == 0) {           // g = 256: one group per block pair
+        const int g = grp0 + (GR <= 4 ? b * MB + m : b >> 1);
+        ms[r][m] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, col * 2, g * N * 2, 0);
+        mz[r][m] = __builtin_amdgcn_raw_buffer_load_b32(zrsrc, (col >> 3) * 4, g * (N >> 3) * 4, 0);
+      }
+    }
+    wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                           wrsrc, lane * 16, (blk0 + b) * 1024, kStripAux));
+  };
+#pragma unroll
+  for (int b = 0; b < WIN; ++b) issue(b);
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
@@ -175,33 +194,53 @@ w4_strip_kernel(StripArgs a) {
   }
   __syncthreads();
 
-  // 5. MFMA over the slice's row quads, one quantisation group at a time:
-  //    y += s * (A - (128 + z) * X).  All 16 A rows are x, so every accumulator row holds
-  //    the lane's column; up to four independent accumulators per group.
+  // 5. MFMA over the slice's row quads, block by block as the ring delivers them; per
+  //    quantisation group y += s * (A - (128 + z) * X).  All 16 A rows are x, so every
+  //    accumulator row holds the lane's column; up to four independent accumulators.
   const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
   const uint32_t kLo = vgpr_const(0x000F000Fu);
   constexpr int NA = GR < 4 ? GR : 4;
   float tot = 0.f;
+  float cur_s = 0.f, cur_z = 0.f;               // g = 256: the group of this block pair
+  floatx4 acc[NA];
 #pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-    floatx4 acc[NA];
+  for (int b = 0; b < NB; ++b) {
+    const int r = b % WIN;
+    const u32x4 w4 = wq[r];
+    float gs[MB], gz[MB];                       // scale and 128 + zero of the block's groups
 #pragma unroll
-    for (int c = 0; c < NA; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MB; ++m) {
+      gs[m] = f16_to_f32(ms[r][m] & 0xffffu);
+      gz[m] = (float)(128 + (int)((mz[r][m] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
+    }
+    if (GR == 8 && (b & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
+    // keep the compiler from hoisting later ring loads (and their registers) above here:
+    // an empty asm with a memory clobber orders the loads at the IR level, the
+    // scheduling barrier in the machine scheduler
+    asm volatile("" ::: "memory");
+    if (b + WIN < NB) issue(b + WIN);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < GR; ++q) {
-      const int rq = g * GR + q;                 // row quad within the slice
-      const u32x4 w4 = wq[rq >> 2];
-      const uint32_t w = (rq & 3) == 0 ? w4.x : (rq & 3) == 1 ? w4.y : (rq & 3) == 2 ? w4.z : w4.w;
+    for (int j = 0; j < 4; ++j) {
+      const int rq = 4 * b + j;                 // row quad within the slice
+      const int q = rq % GR;
+      if (q == 0) {
+#pragma unroll
+        for (int c = 0; c < NA; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+      const uint32_t w = j == 0 ? w4.x : j == 1 ? w4.y : j == 2 ? w4.z : w4.w;
       const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[4 * rq + lg]);
       acc[q % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, unpack_codes8(w, kLo, kMagic),
                                                            acc[q % NA], 0, 0, 0);
-    }
-    float A = acc[0][0];
+      if (q == GR - 1) {
+        float Asum = acc[0][0];
 #pragma unroll
-    for (int c = 1; c < NA; ++c) A += acc[c][0];
-    const float sc = f16_to_f32(sraw[g] & 0xffffu);
-    const float cz = (float)(128 + (int)((zraw[g] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
-    tot = fmaf(sc, fmaf(-cz, xg[ks][g], A), tot);
+        for (int c = 1; c < NA; ++c) Asum += acc[c][0];
+        const float sc = GR == 8 ? cur_s : gs[j / GR];
+        const float cz = GR == 8 ? cur_z : gz[j / GR];
+        tot = fmaf(sc, fmaf(-cz, xg[ks][rq / GR], Asum), tot);
+      }
+    }
   }
 
   // 6. Per-slice column sums meet in LDS; wave 0 adds them in slice order, four columns
@@ -259,7 +298,8 @@ w4_strip_kernel(StripArgs a) {
 }
 
 // Blocks per wave for K/128 = kb blocks with ct strips per workgroup: KW * ct waves within
-// strip_max_waves(NB), even NB (whole groups up to g = 256), 4 where it fits.
+// strip_max_waves(NB), even NB (whole groups up to g = 256), 8 where it fits (measured
+// fastest on the decode shapes with the 4-block load ring; 4 and 16 are slower).
 static bool nb_fits(int64_t kb, int nb, int ct) {
   return kb % nb == 0 && (kb / nb) * ct <= strip_max_waves(nb);
 }
@@ -268,7 +308,7 @@ static int blocks_per_wave(int64_t K, int ct) {
   if (K <= 0 || K % (2 * kStripBlockK) != 0) return 0;
   const int64_t kb = K / kStripBlockK;
   if (g_strip_nb) return nb_fits(kb, g_strip_nb, ct) ? g_strip_nb : 0;
-  for (const int nb : {4, 6, 8, 2, 16})
+  for (const int nb : {8, 4, 6, 2, 16})
     if (nb_fits(kb, nb, ct)) return nb;
   return 0;
 }
