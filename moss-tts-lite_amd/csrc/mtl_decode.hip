@@ -367,7 +367,62 @@ struct AttnArgs {
   int H, Hkv;
   int64_t max_seq;
   float scale, eps;
+  int fixed_chunks;           // chunks are the fixed blocks [64c, 64c + 64)
 };
+
+static int g_attn_fixed = 1;  // tuning knob: fixed 64-position chunks where max_seq allows
+
+// The merge of one kv head's chunk partials (m, l, o[128]) per q head, in chunk order,
+// by the last workgroup of that kv head to finish; out[h*128 + d] (through out_index).
+__device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, int n_rep,
+                                           int wave, int lane, float (*w_lds)[kAttnMaxChunks]) {
+  constexpr int D = 128;
+  for (int hr = wave; hr < n_rep; hr += 4) {
+    const int h = kvh * n_rep + hr;
+    const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
+    // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1 as 64-bit
+    // agent-scope loads, all issued before any use
+    typedef unsigned long long u64;
+    float mc = -INFINITY, lc = 0.f;
+    if (lane < nch) {
+      const u64 ml = __hip_atomic_load(reinterpret_cast<const u64*>(ph + (size_t)lane * kAttnPart),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mc = __uint_as_float((uint32_t)ml);
+      lc = __uint_as_float((uint32_t)(ml >> 32));
+    }
+    float o0 = 0.f, o1 = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      u64 ov[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (c0 + j < nch)
+          ov[j] = __hip_atomic_load(
+              reinterpret_cast<const u64*>(ph + (size_t)(c0 + j) * kAttnPart + 4 + 2 * lane),
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c0 == 0) {
+        const float M = wave_max(lc > 0.f ? mc : -INFINITY);
+        const float wc = lc > 0.f ? expf(mc - M) : 0.f;
+        w_lds[wave][lane] = wc;
+        lc = wave_sum(wc * lc);                        // Ls from here on
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (c0 + j < nch) {
+          const float wj = w_lds[wave][c0 + j];
+          o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
+          o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
+        }
+    }
+    const float Ls = lc;
+    const int i0 = h * D + 2 * lane;
+    const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
+    a.out[a.out_index ? a.out_index[i0] : i0] = (uint16_t)f32_to_bf16(r0);
+    a.out[a.out_index ? a.out_index[i0 + 1] : i0 + 1] = (uint16_t)f32_to_bf16(r1);
+  }
+}
 
 template <bool FROM_PART>
 __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
@@ -386,6 +441,31 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   HeadPart hq, hkv;
   if (FROM_PART && wave < n_rep)
     head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + wave, lane, hq);
+  const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
+  const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
+  const int dg = lane & 15, ps = lane >> 4;           // value pass: dims 8dg.., positions ps+4i
+  u32x4 kr[16], vr[16];
+  // K rows and V slices of positions [base, base + 64) of this kv head, clamped to `last`
+  // (a position in the cache)
+  auto load_k = [&](int base, int last) {
+    const int pk = base + lane < last ? base + lane : last;
+    const u32x4* krow = reinterpret_cast<const u32x4*>(kbase + (size_t)pk * D);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kr[i] = krow[i];
+  };
+  auto load_v = [&](int base, int last) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int pv = base + ps + 4 * i < last ? base + ps + 4 * i : last;
+      vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pv * D + 8 * dg);
+    }
+  };
+  // With max_seq <= 64 * 64 every chunk is the fixed block [64c, 64c + 64), so its K rows
+  // load before the position is known (rows at or past the length are masked); V, needed
+  // only after the scores, waits for the position (chunks past the length load nothing
+  // more).
+  const bool fixed = a.fixed_chunks;
+  if (fixed) load_k(c * kAttnBlock, (int)a.max_seq - 1);
   const int64_t pos = *a.pos;
   int64_t L64 = pos + 1;
   if (L64 < 0) L64 = 0;
@@ -394,29 +474,18 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   int nch = (L + kAttnBlock - 1) / kAttnBlock;
   if (nch > kAttnMaxChunks) nch = kAttnMaxChunks;
   if (c >= nch) return;                               // uniform over the workgroup
-  const int clen = (L + nch - 1) / nch;
+  const int clen = fixed ? kAttnBlock : (L + nch - 1) / nch;
   const int p0 = c * clen;
   const int p1 = p0 + clen < L ? p0 + clen : L;       // p0 < p1 unless the chunk is empty
   const bool has_pos = pos >= p0 && pos < p1;
-  const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
-  const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
-  const int dg = lane & 15, ps = lane >> 4;           // value pass: dims 8dg.., positions ps+4i
 
-  // 1. First block's K rows and V slices, issued before the q prologue.
-  u32x4 kr[16], vr[16];
+  // 1. The first block's V slices (and, unless fixed, K rows), before the q prologue.
   auto load_block = [&](int base) {
-    const int last = p1 - 1 > 0 ? p1 - 1 : 0;
-    const int pk = base + lane < p1 ? base + lane : last;
-    const u32x4* krow = reinterpret_cast<const u32x4*>(kbase + (size_t)pk * D);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) kr[i] = krow[i];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int pv = base + ps + 4 * i < p1 ? base + ps + 4 * i : last;
-      vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pv * D + 8 * dg);
-    }
+    load_k(base, p1 - 1 > 0 ? p1 - 1 : 0);
+    load_v(base, p1 - 1 > 0 ? p1 - 1 : 0);
   };
-  if (p0 < p1) load_block(p0);
+  if (fixed) load_v(p0, p1 - 1 > 0 ? p1 - 1 : 0);
+  else if (p0 < p1) load_block(p0);
   if (FROM_PART && has_pos && wave < 2)   // k (wave 0) or v (wave 1) of position pos
     head_issue(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv);
 
@@ -496,7 +565,8 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float ei = e_lds[wave][ps * 16 + i];
-        const u32x4 v = (base + ps + 4 * i == pos) ? vpos[dg] : vr[i];
+        const int pv = base + ps + 4 * i;
+        const u32x4 v = pv == pos ? vpos[dg] : pv < p1 ? vr[i] : u32x4{0u, 0u, 0u, 0u};
         const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -537,51 +607,197 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   if (!last_flag) return;
   if (threadIdx.x == 0)
     __hip_atomic_store(&a.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int hr = wave; hr < n_rep; hr += 4) {
-    const int h = kvh * n_rep + hr;
-    const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
-    // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1 as 64-bit
-    // agent-scope loads, all issued before any use
-    typedef unsigned long long u64;
-    float mc = -INFINITY, lc = 0.f;
-    if (lane < nch) {
-      const u64 ml = __hip_atomic_load(reinterpret_cast<const u64*>(ph + (size_t)lane * kAttnPart),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      mc = __uint_as_float((uint32_t)ml);
-      lc = __uint_as_float((uint32_t)(ml >> 32));
-    }
-    float o0 = 0.f, o1 = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-      u64 ov[16];
+  attn_merge(a, kvh, nch, n_rep, wave, lane, w_lds);
+}
+
+// ----------------------------------------------------------------------------------
+// Tile form of the decode attention, for max_seq <= 64 * 64: chunk c is the fixed block
+// [64c, 64c + 64) of positions.  The workgroup loads the chunk's K and V rows once, before
+// the position is read, and stages them in LDS.  Wave w scores positions 16w .. 16w+15
+// against every q head of the kv head with four v_mfma_f32_16x16x32_bf16 (A = K rows,
+// B = the q heads as columns).  The chunk softmax max and sum meet across the 4 waves
+// in LDS, and e * v is summed on the VALU: a wave per q head, a lane per 8 dims x 16
+// positions, reduced over the 4 position quarters.  The published (m, l, o[128]) per q
+// head and the merge are those of attn_decode_kernel.
+// ----------------------------------------------------------------------------------
+template <bool FROM_PART>
+__global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
+  constexpr int D = 128, P = kAttnBlock;
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ u32x4 k_lds[P][16];                // the chunk's K rows, 8 dims per item
+  __shared__ u32x4 v_lds[P][16];
+  __shared__ u32x4 q_lds[16][16];               // q heads (rows past n_rep zero)
+  __shared__ float e_lds[kAttnMaxRep][P];       // exp(s - m) per q head and position
+  __shared__ float red_m[4][16], red_l[4][16];  // per-wave max / sum per q head
+  __shared__ float w_lds[4][kAttnMaxChunks];
+  __shared__ int last_flag;
+  const int kvh = blockIdx.x, c = blockIdx.y;
+  const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
+  const int n_rep = a.H / a.Hkv;
+  // 0. Loads that do not depend on the position: this wave's first q head partials and
+  //    the chunk's K/V rows (thread t: items t + 256j = row item/16, dims 8*(item%16)).
+  const int ncols = (a.H + 2 * a.Hkv) * D;
+  HeadPart hq, hkv;
+  if (FROM_PART && wave < n_rep)
+    head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + wave, lane, hq);
+  const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
+  const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
+  const int last_row = (int)a.max_seq - 1;
+  u32x4 kv[4], vv[4];
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (c0 + j < nch)
-          ov[j] = __hip_atomic_load(
-              reinterpret_cast<const u64*>(ph + (size_t)(c0 + j) * kAttnPart + 4 + 2 * lane),
-              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (c0 == 0) {
-        const float M = wave_max(lc > 0.f ? mc : -INFINITY);
-        const float wc = lc > 0.f ? expf(mc - M) : 0.f;
-        w_lds[wave][lane] = wc;
-        lc = wave_sum(wc * lc);                        // Ls from here on
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (c0 + j < nch) {
-          const float wj = w_lds[wave][c0 + j];
-          o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
-          o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
-        }
-    }
-    const float Ls = lc;
-    const int i0 = h * D + 2 * lane;
-    const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
-    a.out[a.out_index ? a.out_index[i0] : i0] = (uint16_t)f32_to_bf16(r0);
-    a.out[a.out_index ? a.out_index[i0 + 1] : i0 + 1] = (uint16_t)f32_to_bf16(r1);
+  for (int j = 0; j < 4; ++j) {
+    const int item = t + 256 * j;
+    int p = c * P + (item >> 4);
+    p = p < last_row ? p : last_row;
+    kv[j] = *reinterpret_cast<const u32x4*>(kbase + (size_t)p * D + 8 * (item & 15));
+    vv[j] = *reinterpret_cast<const u32x4*>(vbase + (size_t)p * D + 8 * (item & 15));
   }
+  const int64_t pos = *a.pos;
+  int64_t L64 = pos + 1;
+  if (L64 < 0) L64 = 0;
+  if (L64 > a.max_seq) L64 = a.max_seq;
+  const int L = (int)L64;
+  const int nch = (L + P - 1) / P;
+  if (c >= nch) return;                               // uniform over the workgroup
+  const int p0 = c * P;
+  const int p1 = p0 + P < L ? p0 + P : L;
+  const bool has_pos = pos >= p0 && pos < p1;
+  if (FROM_PART && has_pos && wave < 2)   // k (wave 0) or v (wave 1) of position pos
+    head_issue(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv);
+
+  // 1. Prologue: q heads into LDS; k/v of position pos into the cache and the LDS tile.
+  const size_t prow = (size_t)(pos >= 0 && pos < a.max_seq ? pos : 0) * D;
+  if (FROM_PART) {
+    const uint16_t* cr = a.cos_tab + prow;
+    const uint16_t* sr = a.sin_tab + prow;
+    if (has_pos && wave < 2) {
+      float x0, x1;
+      head_sum(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv,
+               x0, x1);
+      if (wave == 0) norm_rope_pair(x0, x1, a.kn, cr, sr, lane, a.eps, x0, x1);
+      const uint32_t b0 = f32_to_bf16(x0), b1 = f32_to_bf16(x1);
+      uint16_t* dst = (wave == 0 ? a.kc : a.vc) + ((size_t)kvh * a.max_seq + pos) * D;
+      dst[lane] = (uint16_t)b0;
+      dst[lane + 64] = (uint16_t)b1;
+      uint16_t* l16 = reinterpret_cast<uint16_t*>((wave == 0 ? k_lds : v_lds)[pos - p0]);
+      l16[lane] = (uint16_t)b0;
+      l16[lane + 64] = (uint16_t)b1;
+    }
+    for (int hr = wave; hr < n_rep; hr += 4) {
+      float x0, x1;
+      if (hr != wave) head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, hq);
+      head_sum(a.qkv_part, a.splits, ncols, kvh * n_rep + hr, lane, hq, x0, x1);
+      norm_rope_pair(x0, x1, a.qn, cr, sr, lane, a.eps, x0, x1);
+      uint16_t* l16 = reinterpret_cast<uint16_t*>(q_lds[hr]);
+      l16[lane] = (uint16_t)f32_to_bf16(x0);
+      l16[lane + 64] = (uint16_t)f32_to_bf16(x1);
+    }
+  } else {
+    for (int hr = wave; hr < n_rep; hr += 4)
+      if (lane < 16)
+        q_lds[hr][lane] =
+            reinterpret_cast<const u32x4*>(a.q + (size_t)(kvh * n_rep + hr) * D)[lane];
+  }
+  for (int i = n_rep * 16 + t; i < 16 * 16; i += 256) q_lds[i >> 4][i & 15] = u32x4{0u, 0u, 0u, 0u};
+  // the chunk's rows; rows at or past the length are zero, and the row of pos comes from
+  // the prologue when it computed k/v there
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int item = t + 256 * j;
+    const int row = item >> 4, p = p0 + row;
+    if (FROM_PART && p == pos) continue;
+    const u32x4 z{0u, 0u, 0u, 0u};
+    k_lds[row][item & 15] = p < p1 ? kv[j] : z;
+    v_lds[row][item & 15] = p < p1 ? vv[j] : z;
+  }
+  __syncthreads();
+
+  // 2. Scores s[p][h] = K[p] . q[h] on MFMA; lane l holds positions 16w + 4(l/16) + r of
+  //    q head l%16.  Chunk softmax: max and sum per head across the 4 waves.
+  f4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bf16x8 A = __builtin_bit_cast(bf16x8, k_lds[16 * wave + (lane & 15)][4 * k + (lane >> 4)]);
+    const bf16x8 B = __builtin_bit_cast(bf16x8, q_lds[lane & 15][4 * k + (lane >> 4)]);
+    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, S, 0, 0, 0);
+  }
+  const int hd = lane & 15, g = lane >> 4;
+  float sv[4], mloc = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = p0 + 16 * wave + 4 * g + r;
+    sv[r] = p < p1 ? S[r] * a.scale : -INFINITY;
+    mloc = fmaxf(mloc, sv[r]);
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+  if (g == 0) red_m[wave][hd] = mloc;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red_m[0][hd], red_m[1][hd]), fmaxf(red_m[2][hd], red_m[3][hd]));
+  float lsum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float e = expf(sv[r] - M);                  // 0 for masked positions
+    if (hd < n_rep) e_lds[hd][16 * wave + 4 * g + r] = e;
+    lsum += e;
+  }
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (g == 0) red_l[wave][hd] = lsum;
+  __syncthreads();
+
+  // 3. o[h] = sum_p e[h][p] v[p]: wave = q head (4 per pass), lane = 8 dims (l%16) x 16
+  //    positions (l/16 quarter); quarters reduced by shuffles; then publish (m, l, o).
+  const int dg = lane & 15, pq = lane >> 4;
+  for (int hp = 0; hp < n_rep; hp += 4) {
+    const int hr = hp + wave;
+    if (hr >= n_rep) break;                           // uniform over the wave
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 16 * pq + i;
+      const float e = e_lds[hr][row];
+      const u32x4 v = v_lds[row][dg];
+      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[2 * j] = fmaf(e, lo_bf(w4[j]), o[2 * j]);
+        o[2 * j + 1] = fmaf(e, hi_bf(w4[j]), o[2 * j + 1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[j] += __shfl_xor(o[j], 16);
+      o[j] += __shfl_xor(o[j], 32);
+    }
+    const float mh = fmaxf(fmaxf(red_m[0][hr], red_m[1][hr]), fmaxf(red_m[2][hr], red_m[3][hr]));
+    const float lh = (red_l[0][hr] + red_l[1][hr]) + (red_l[2][hr] + red_l[3][hr]);
+    float* ph = a.part + ((size_t)(kvh * n_rep + hr) * kAttnMaxChunks + c) * kAttnPart;
+    if (lane == 0) {
+      __hip_atomic_store(ph, mh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ph + 1, lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        __hip_atomic_store(ph + 4 + 8 * dg + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order.
+  __builtin_amdgcn_s_waitcnt(0);      // every partial store acknowledged before the count
+  __syncthreads();
+  if (t == 0)
+    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nch - 1);
+  __syncthreads();
+  if (!last_flag) return;
+  if (t == 0)
+    __hip_atomic_store(&a.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  attn_merge(a, kvh, nch, n_rep, wave, lane, w_lds);
 }
 
 // ----------------------------------------------------------------------------------
@@ -860,13 +1076,18 @@ static int attn_check(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int
 static void attn_launch(AttnArgs& a, void* workspace, bool from_part, hipStream_t s) {
   a.counters = static_cast<uint32_t*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kAttnCounterBytes);
+  a.fixed_chunks = g_attn_fixed && a.max_seq <= kAttnBlock * kAttnMaxChunks;
   int64_t ch = (a.max_seq + kAttnBlock - 1) / kAttnBlock;
   if (ch > kAttnMaxChunks) ch = kAttnMaxChunks;
   const dim3 grid(a.Hkv, (unsigned)ch);
-  if (from_part)
+  if (a.fixed_chunks) {
+    if (from_part) hipLaunchKernelGGL(attn_tile_kernel<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(attn_tile_kernel<false>, grid, dim3(256), 0, s, a);
+  } else if (from_part) {
     hipLaunchKernelGGL(attn_decode_kernel<true>, grid, dim3(256), 0, s, a);
-  else
+  } else {
     hipLaunchKernelGGL(attn_decode_kernel<false>, grid, dim3(256), 0, s, a);
+  }
 }
 
 int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
@@ -999,6 +1220,14 @@ int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,
                      static_cast<uint16_t*>(out), nullptr, nullptr, nullptr, nullptr, 0.f,
                      pad_period, pad_index);
   return launch_status();
+}
+
+// Tuning knob (process-wide): 1 = the tile attention kernel (fixed 64-position chunks,
+// MFMA scores) when max_seq <= 4096, 0 = the chunked kernel with length-sized chunks.
+int mtl_tune_set_attn_fixed(int32_t on) {
+  if (on != 0 && on != 1) return MTL_ERR_INVALID_ARG;
+  g_attn_fixed = on;
+  return MTL_OK;
 }
 
 int mtl_advance_position(int64_t* pos, void* stream) {
