@@ -14,17 +14,31 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// float32 -> bf16 bits, round to nearest even; every NaN -> 0x7FC0 (c10 rule).
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two float32 -> packed bf16 bits (lo | hi << 16), round to nearest even: one
+// v_cvt_pk_bf16_f32.  NaN bits are whatever the instruction makes of them, so this is for
+// values that stay in registers (MFMA operands, intermediate roundings).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
-// Round a float32 to the nearest bf16 value, kept in float32.
+// float32 -> bf16 bits, round to nearest even; every NaN -> 0x7FC0 (c10 rule).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  const uint32_t b = cvt_pk_bf16(f, 0.f) & 0xffffu;
+  return f != f ? 0x7fc0u : b;
+}
+
+// Round a float32 to the nearest bf16 value, kept in float32 (a NaN stays a NaN).
 __device__ __forceinline__ float round_bf16(float f) {
-  return bf16_to_f32(f32_to_bf16(f));
+  return bf16_to_f32(cvt_pk_bf16(f, 0.f) & 0xffffu);
+}
+
+// Round two float32 values to bf16, kept in float32, with one conversion.
+__device__ __forceinline__ void round_bf16x2(float lo, float hi, float& rlo, float& rhi) {
+  const uint32_t p = cvt_pk_bf16(lo, hi);
+  rlo = __uint_as_float(p << 16);
+  rhi = __uint_as_float(p & 0xffff0000u);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {

@@ -60,18 +60,19 @@ __device__ __forceinline__ u32x4 pair_order(u32x4 v, float& sum) {
   return u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
 }
 
-// x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40).
+// x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40), two values
+// per v_cvt_pk_bf16_f32.  The result is an MFMA operand, so NaN bits are not normalised.
 __device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
   const uint32_t hh[4] = {h.x, h.y, h.z, h.w};
   const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
   uint32_t o[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const uint32_t lo = f32_to_bf16(round_bf16(
-        bf16_to_f32(ww[c] & 0xffffu) * round_bf16(bf16_to_f32(hh[c] & 0xffffu) * r)));
-    const uint32_t hi = f32_to_bf16(round_bf16(
-        bf16_to_f32(ww[c] >> 16) * round_bf16(bf16_to_f32(hh[c] >> 16) * r)));
-    o[c] = lo | (hi << 16);
+    float nlo, nhi;
+    round_bf16x2(__uint_as_float(hh[c] << 16) * r, __uint_as_float(hh[c] & 0xffff0000u) * r,
+                 nlo, nhi);
+    o[c] = cvt_pk_bf16(__uint_as_float(ww[c] << 16) * nlo,
+                       __uint_as_float(ww[c] & 0xffff0000u) * nhi);
   }
   return u32x4{o[0], o[1], o[2], o[3]};
 }
