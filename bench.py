@@ -276,7 +276,7 @@ def bench_decode(args, torch):
 
 # The gate|up launch of each decode plan (the dominant kernel of the step).
 GATE_UP_KERNEL = {
-    "strip": "w4_strip_kernel<g128, RMSNORM, SILU, 4 blocks/wave, 2 strips> gate_up 4096x24576 "
+    "strip": "w4_strip_kernel<g128, RMSNORM, SILU, 8 blocks/wave, 2 strips> gate_up 4096x24576 "
              "M=1 (full-K strips, SiLU*up epilogue)",
     "staged": "w4_gemm_kernel<1,4,GPTQ,XSRC_RMSNORM> gate_up 4096x24576 M=1 (split-K partials)",
 }
