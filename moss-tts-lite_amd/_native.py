@@ -91,6 +91,7 @@ _SIGNATURES = {
     "mtl_tune_set_strip_nb": (_i32, [_i32]),
     "mtl_tune_set_strip_xcd": (_i32, [_i32]),
     "mtl_tune_set_strip_ct": (_i32, [_i32]),
+    "mtl_tune_set_strip_full": (_i32, [_i32]),
     "mtl_tune_set_attn_fixed": (_i32, [_i32]),
 }
 

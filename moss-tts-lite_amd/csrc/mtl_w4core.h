@@ -104,8 +104,8 @@ struct StripArgs {
 enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };
 
 // Blocks (128 input channels) per wave of the strip GEMV for this K with ct strips per
-// workgroup; 0: unsupported.
-int strip_blocks_per_wave(int64_t K, int ct);
+// workgroup at this group size; 0: unsupported.
+int strip_blocks_per_wave(int64_t K, int ct, int group);
 // Launch the strip GEMV; shapes, pointers and alignment are checked by the caller.
 int strip_launch(const StripArgs& a, hipStream_t stream);
 

@@ -715,12 +715,14 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
 // Partials-only launch for fused consumers: writes fp32 [splits, M, N] into `partials`
 // (splits = w4_splits(K)); x comes from `x` (bf16, optionally through `perm`) or, when
 // `xpart` is set, from the gate|up partials of the previous GEMV (SiLU*up, M = 1).
-static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32_t* perm) {
+static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32_t* perm,
+                        int group) {
   if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED && layout != MTL_LAYOUT_STRIP)
     return MTL_ERR_INVALID_ARG;
   if (layout == MTL_LAYOUT_TILED && (N % kWaveN != 0 || M != 1 || perm)) return MTL_ERR_SHAPE;
   if (layout == MTL_LAYOUT_STRIP &&
-      (M != 1 || perm || N <= 0 || N % 16 != 0 || !strip_blocks_per_wave(K, 1) ||
+      (M != 1 || perm || N <= 0 || N % 16 != 0 || K > 16384 ||
+       !strip_blocks_per_wave(K, 1, group) ||
        N * K / 2 >= ((int64_t)1 << 31)))
     return MTL_ERR_SHAPE;
   return MTL_OK;
@@ -763,7 +765,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
                             const int32_t* qzeros, const int32_t* perm, int64_t N, int group,
                             int zero_offset, int layout, float* partials, int64_t partials_bytes,
                             hipStream_t stream) {
-  if (const int st = check_layout(layout, M, K, N, perm)) return st;
+  if (const int st = check_layout(layout, M, K, N, perm, group)) return st;
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -821,7 +823,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
                                  const void* meta0, const int32_t* qzeros, int64_t N, int group,
                                  int zero_offset, int layout, float* partials,
                                  int64_t partials_bytes, hipStream_t stream) {
-  if (const int st = check_layout(layout, 1, K, N, nullptr)) return st;
+  if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -876,7 +878,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
                             hipStream_t stream) {
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !h || !slots)
     return MTL_ERR_INVALID_ARG;
-  if (const int st = check_layout(layout, 1, K, N, nullptr)) return st;
+  if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
   if (N > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
@@ -945,7 +947,8 @@ static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* 
     return MTL_ERR_INVALID_ARG;
   if (layout != MTL_LAYOUT_STRIP) return MTL_ERR_UNSUPPORTED;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
-  if (K <= 0 || N <= 0 || K % group != 0 || N % 64 != 0 || !strip_blocks_per_wave(K, 2) ||
+  if (K <= 0 || N <= 0 || K % group != 0 || N % 64 != 0 || K > 16384 ||
+      !strip_blocks_per_wave(K, 2, group) ||
       N * K / 2 >= ((int64_t)1 << 31) || K > (int64_t)kSlotCols * kMaxSlots)
     return MTL_ERR_SHAPE;
   if (!aligned16(slots) || !aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) ||

@@ -25,20 +25,26 @@ namespace mtl {
 constexpr int kStripCols = 16;
 constexpr int kStripBlockK = 128;     // input channels per 1 KB block
 constexpr int kStripMaxWaves = 16;
-// Waves per workgroup allowed at NB blocks per wave (16 blocks: at most 8 waves, so the
-// kernel may use up to 256 VGPRs), and the occupancy its register allocation must leave.
-constexpr int strip_max_waves(int nb) { return nb >= 16 ? 8 : kStripMaxWaves; }
-constexpr int strip_min_occupancy(int nb) { return 1; }
-// Blocks in flight per wave (the load ring).
-constexpr int strip_window(int nb) { return nb < 4 ? nb : 4; }
+// Blocks in flight per wave (the load ring, a divisor of NB): the default ring of 4 (all of
+// them for NB of 2 and 4, and for NB = 6 at g >= 128; 2 at g <= 64, whose 2 or 4 groups per
+// block bring as many metadata registers), or the deep ring of 8 (g >= 128, NB >= 8).
+constexpr int strip_ring(int gr, int nb) { return nb == 6 ? (gr <= 2 ? 2 : 6) : nb < 4 ? nb : 4; }
+constexpr int strip_deep_ring(int gr, int nb) { return gr <= 2 || nb < 8 ? strip_ring(gr, nb) : 8; }
+// Waves per workgroup allowed (GR = g / 32, NB blocks per wave, WIN in flight): 16 (128
+// VGPRs each); 12 (168 VGPRs) for the deep ring at NB = 16; 8 at g = 32 from NB = 8 on,
+// whose metadata needs more than 128 VGPRs.
+constexpr int strip_max_waves(int gr, int nb, int win) {
+  return gr == 1 && nb >= 8 ? 8 : nb >= 16 && win > 4 ? 12 : kStripMaxWaves;
+}
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
 
 static int g_strip_nb = 0;            // tuning override of blocks per wave (0: auto)
 static int g_strip_ct = 0;            // tuning override of strips per workgroup (0: auto)
 static int g_strip_xcd = 1;           // 1: XCD-contiguous strip order (see the kernel)
+static int g_strip_full = -1;         // tuning override: 1 all blocks in flight, 0 ring, -1 auto
 
-template <int GR, int XSRC, int EPI, int NB, int CT>
-__global__ void __launch_bounds__(64 * strip_max_waves(NB), strip_min_occupancy(NB))
+template <int GR, int XSRC, int EPI, int NB, int CT, int WIN>
+__global__ void __launch_bounds__(64 * strip_max_waves(GR, NB, WIN), 1)
 w4_strip_kernel(StripArgs a) {
   constexpr int ITEMS = 16 * NB;               // x items (8 channels) per K slice
   constexpr int STAGERS = 64 * CT;             // threads that stage one slice
@@ -47,7 +53,8 @@ w4_strip_kernel(StripArgs a) {
   constexpr int GI = 4 * GR;                   // x items per group
   static_assert((4 * NB) % GR == 0, "a slice must cover whole quantisation groups");
   static_assert(64 % GI == 0 && ITEMS % GI == 0, "a wave must stage whole groups");
-  static_assert(EPI != STRIP_EPI_SILU || CT == 2, "SiLU*up pairs a gate strip with its up strip");
+  static_assert(EPI != STRIP_EPI_SILU || CT % 2 == 0, "SiLU*up pairs gate strips with up strips");
+  static_assert(WIN >= 1 && WIN <= NB && NB % WIN == 0, "ring window");
   extern __shared__ u32x4 xa_all[];            // [KW][ITEMS] x items in pair order
   __shared__ float xg[kStripMaxWaves][NGW];    // per-slice group sums of x
   __shared__ float ytile[kStripMaxWaves][kStripCols];   // [slice * CT + strip][column]
@@ -62,10 +69,17 @@ w4_strip_kernel(StripArgs a) {
   // neighbouring strips share are fetched into one L2 only.
   const int G = gridDim.x;
   const int wg = a.xcd_order ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
-  // SiLU*up: the gate strip 4*(wg/2) + wg%2 and its up partner two strips (32 columns)
-  // to the right; otherwise CT consecutive strips.
-  const int s0 = EPI == STRIP_EPI_SILU ? 4 * (wg >> 1) + (wg & 1) : wg * CT;
-  const int s = s0 + (EPI == STRIP_EPI_SILU ? 2 * cs : cs);
+  // SiLU*up: the workgroup holds P = CT/2 (gate, up) strip pairs; pair p is the gate strip
+  // 4*(p/2) + p%2 and its up partner two strips (32 columns) to the right, in the gate|up
+  // interleave of 32-column blocks.  Waves cs < P serve the gate strips of pairs
+  // P*wg + cs, waves cs >= P their up strips.  Otherwise CT consecutive strips.
+  constexpr int P = CT / 2;
+  const int s0 = EPI == STRIP_EPI_SILU ? 0 : wg * CT;
+  int s = s0 + cs;
+  if (EPI == STRIP_EPI_SILU) {
+    const int p = P * wg + cs % P;
+    s = 4 * (p >> 1) + (p & 1) + (cs >= P ? 2 : 0);
+  }
   const int N = a.N;
   const int col = s * kStripCols + lj;
   const int item0 = ks * ITEMS;                // first x item of the slice
@@ -106,7 +120,7 @@ w4_strip_kernel(StripArgs a) {
   // residual epilogue inputs of wave 0's column owners, read ahead of everything else
   u32x2 h_pre{0u, 0u};
   int32_t sc_pre[4] = {0, 0, 0, 0};
-  const int c_own = (EPI == STRIP_EPI_SILU ? 0 : s0 * kStripCols) + 4 * (lane & (4 * CT - 1));
+  const int c_own = (EPI == STRIP_EPI_SILU ? 0 : s0 * kStripCols) + 4 * (lane % (4 * CT));
   if (EPI == STRIP_EPI_RESID && wave == 0) {
     h_pre = *reinterpret_cast<const u32x2*>(a.h + c_own);
     if (a.h_ord && a.scatter) {
@@ -120,7 +134,6 @@ w4_strip_kernel(StripArgs a) {
   //      block b + WIN is issued into that slot as soon as block b's operands are out.
   //      Loads complete in issue order, so waiting for block b never waits for a later
   //      one, and the unpack and MFMA work overlaps the rest of the stream.
-  constexpr int WIN = strip_window(NB);
   constexpr int MB = GR <= 4 ? 4 / GR : 1;     // groups starting in one block
   const int grp0 = item0 * 8 / a.group;
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -136,11 +149,11 @@ w4_strip_kernel(StripArgs a) {
       const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 3) * 4, 0x00020000);
   u32x4 wq[WIN];
   uint32_t ms[WIN][MB], mz[WIN][MB];
-  auto issue = [&](int b) {
-    const int r = b % WIN;
+  // block b into ring slot r (r = b % WIN, a compile-time index at every call)
+  auto issue = [&](int r, int b) {
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      if (GR <= 4 || (b & 1) == 0) {           // g = 256: one group per block pair
+      if (GR <= 4 || (r & 1) == 0) {           // g = 256: one group per block pair (b, r alike in parity)
         const int g = grp0 + (GR <= 4 ? b * MB + m : b >> 1);
         ms[r][m] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, col * 2, g * N * 2, 0);
         mz[r][m] = __builtin_amdgcn_raw_buffer_load_b32(zrsrc, (col >> 3) * 4, g * (N >> 3) * 4, 0);
@@ -150,7 +163,7 @@ w4_strip_kernel(StripArgs a) {
                                           wrsrc, lane * 16, (blk0 + b) * 1024, kStripAux));
   };
 #pragma unroll
-  for (int b = 0; b < WIN; ++b) issue(b);
+  for (int b = 0; b < WIN; ++b) issue(b, b);
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
@@ -196,59 +209,69 @@ w4_strip_kernel(StripArgs a) {
 
   // 5. MFMA over the slice's row quads, block by block as the ring delivers them; per
   //    quantisation group y += s * (A - (128 + z) * X).  All 16 A rows are x, so every
-  //    accumulator row holds the lane's column; up to four independent accumulators.
+  //    accumulator row holds the lane's column.  One accumulator chains the MFMAs of a
+  //    group (the other waves of the SIMD cover the dependency): fewer registers, so every
+  //    workgroup of the launch is resident at once (measured 7 % faster than four).
   const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
   const uint32_t kLo = vgpr_const(0x000F000Fu);
-  constexpr int NA = GR < 4 ? GR : 4;
   float tot = 0.f;
   float cur_s = 0.f, cur_z = 0.f;               // g = 256: the group of this block pair
-  floatx4 acc[NA];
+  floatx4 acc;
+  // Ring turns with the WIN ring slots unrolled inside, so ring indexes stay compile-time.
+  // Up to 8 blocks the turns are unrolled too (measured faster); at 16 they stay a loop,
+  // so a 16-block wave needs no more registers than a 4-block one.  The last turn is
+  // peeled: it issues no refills, so inside the loop every refill is unconditional and the
+  // waits stay exact (a refill under a run-time branch makes the compiler wait for every
+  // outstanding load).  Groups never straddle a turn: 4 * WIN row quads hold whole groups
+  // (WIN even for g = 256), so q and the group of a block are fixed
+  // per slot.
+  static_assert(GR != 8 || WIN % 2 == 0, "g = 256 pairs blocks within a ring turn");
+  auto turn = [&](const int b0, const bool refill) {
 #pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int r = b % WIN;
-    const u32x4 w4 = wq[r];
-    float gs[MB], gz[MB];                       // scale and 128 + zero of the block's groups
+    for (int r = 0; r < WIN; ++r) {
+      const int b = b0 + r;
+      const u32x4 w4 = wq[r];
+      float gs[MB], gz[MB];                     // scale and 128 + zero of the block's groups
 #pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      gs[m] = f16_to_f32(ms[r][m] & 0xffffu);
-      gz[m] = (float)(128 + (int)((mz[r][m] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
-    }
-    if (GR == 8 && (b & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
-    // keep the compiler from hoisting later ring loads (and their registers) above here:
-    // an empty asm with a memory clobber orders the loads at the IR level, the
-    // scheduling barrier in the machine scheduler
-    asm volatile("" ::: "memory");
-    if (b + WIN < NB) issue(b + WIN);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rq = 4 * b + j;                 // row quad within the slice
-      const int q = rq % GR;
-      if (q == 0) {
-#pragma unroll
-        for (int c = 0; c < NA; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < MB; ++m) {
+        gs[m] = f16_to_f32(ms[r][m] & 0xffffu);
+        gz[m] = (float)(128 + (int)((mz[r][m] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
       }
-      const uint32_t w = j == 0 ? w4.x : j == 1 ? w4.y : j == 2 ? w4.z : w4.w;
-      const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[4 * rq + lg]);
-      acc[q % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, unpack_codes8(w, kLo, kMagic),
-                                                           acc[q % NA], 0, 0, 0);
-      if (q == GR - 1) {
-        float Asum = acc[0][0];
+      if (GR == 8 && (r & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
+      // keep the compiler from hoisting later ring loads (and their registers) above here:
+      // an empty asm with a memory clobber orders the loads at the IR level, the
+      // scheduling barrier in the machine scheduler
+      asm volatile("" ::: "memory");
+      if (refill) issue(r, b + WIN);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 1; c < NA; ++c) Asum += acc[c][0];
-        const float sc = GR == 8 ? cur_s : gs[j / GR];
-        const float cz = GR == 8 ? cur_z : gz[j / GR];
-        tot = fmaf(sc, fmaf(-cz, xg[ks][rq / GR], Asum), tot);
+      for (int j = 0; j < 4; ++j) {
+        const int rq = 4 * b + j;               // row quad within the slice
+        const int q = (4 * r + j) % GR;         // == rq % GR: 4 * b0 is a multiple of GR
+        if (q == 0) acc = floatx4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t w = j == 0 ? w4.x : j == 1 ? w4.y : j == 2 ? w4.z : w4.w;
+        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, xa[4 * rq + lg]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, unpack_codes8(w, kLo, kMagic), acc, 0, 0, 0);
+        if (q == GR - 1) {
+          const float Asum = acc[0];
+          const float sc = GR == 8 ? cur_s : gs[j / GR];
+          const float cz = GR == 8 ? cur_z : gz[j / GR];
+          tot = fmaf(sc, fmaf(-cz, xg[ks][rq / GR], Asum), tot);
+        }
       }
     }
-  }
+  };
+  constexpr int kTurnUnroll = NB <= 8 ? NB / WIN : 1;
+#pragma unroll kTurnUnroll
+  for (int b0 = 0; b0 < NB - WIN; b0 += WIN) turn(b0, true);
+  turn(NB - WIN, false);
 
   // 6. Per-slice column sums meet in LDS; wave 0 adds them in slice order, four columns
   //    per lane (lanes 0 .. 4*CT-1 own columns s0*16 + 4*lane .. +3).
   if (lg == 0) ytile[wave][lj] = tot;
   __syncthreads();
   if (wave != 0) return;
-  const int q4 = lane & (4 * CT - 1);
+  const int q4 = lane % (4 * CT);                // CT need not be a power of two
   const int ec = q4 >> 2;                        // strip of these columns
   float y[4] = {0.f, 0.f, 0.f, 0.f};
   for (int k = 0; k < kw; ++k) {
@@ -262,17 +285,17 @@ w4_strip_kernel(StripArgs a) {
     return;
   }
   if (EPI == STRIP_EPI_SILU) {
-    // lanes 0..3 hold gate columns 4*lane..+3 of the gate strip and take their up
-    // partners from lanes 4..7; gate column 16*s0 + i is SwiGLU output 32*(wg/2) +
-    // 16*(wg%2) + i (64-column blocks of 32 gate | 32 up)
+    // lanes 0..4P-1 hold gate columns 4*(lane%4)..+3 of pair P*wg + lane/4 and take their
+    // up partners from lanes 4P..8P-1; column i of pair p's gate strip is SwiGLU output
+    // 16*p + i (64-column blocks of 32 gate | 32 up), so lane l writes 16*P*wg + 4*l ..
     float u[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) u[e] = __shfl_down(y[e], 4);
-    if (lane < 4) {
+    for (int e = 0; e < 4; ++e) u[e] = __shfl_down(y[e], 4 * P);
+    if (lane < 4 * P) {
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = silu_mul_bf16(y[e], u[e]);
-      *reinterpret_cast<u32x2*>(a.act + (size_t)(wg >> 1) * 32 + (wg & 1) * 16 + 4 * lane) =
+      *reinterpret_cast<u32x2*>(a.act + (size_t)wg * 16 * P + 4 * lane) =
           u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
     }
     return;
@@ -297,78 +320,107 @@ w4_strip_kernel(StripArgs a) {
   }
 }
 
-// Blocks per wave for K/128 = kb blocks with ct strips per workgroup: KW * ct waves within
-// strip_max_waves(NB), even NB (whole groups up to g = 256), 8 where it fits (measured
-// fastest on the decode shapes with the 4-block load ring; 4 and 16 are slower).
-static bool nb_fits(int64_t kb, int nb, int ct) {
-  return kb % nb == 0 && (kb / nb) * ct <= strip_max_waves(nb);
+// Launch geometry: CT strips per workgroup, NB blocks per wave, the deep ring (full) or
+// the default one.  A workgroup has (K/128 / NB) * CT waves within
+// strip_max_waves.
+struct StripGeom {
+  int ct, nb, full;
+};
+
+static bool nb_fits(int64_t kb, int nb, int ct, int full, int gr) {
+  const int win = full ? strip_deep_ring(gr, nb) : strip_ring(gr, nb);
+  return kb % nb == 0 && (kb / nb) * ct <= strip_max_waves(gr, nb, win);
 }
 
-static int blocks_per_wave(int64_t K, int ct) {
+// Blocks per wave for K/128 = kb blocks: even NB (whole groups up to g = 256), 8 where it
+// fits (measured fastest on the decode shapes with the 4-block load ring; 4 and 16 are
+// slower), else the first of 4, 6, 2, 16 that fits.
+static int blocks_per_wave(int64_t K, int ct, int full, int group) {
   if (K <= 0 || K % (2 * kStripBlockK) != 0) return 0;
   const int64_t kb = K / kStripBlockK;
-  if (g_strip_nb) return nb_fits(kb, g_strip_nb, ct) ? g_strip_nb : 0;
+  const int gr = group / 32;
+  if (g_strip_nb) return nb_fits(kb, g_strip_nb, ct, full, gr) ? g_strip_nb : 0;
   for (const int nb : {8, 4, 6, 2, 16})
-    if (nb_fits(kb, nb, ct)) return nb;
+    if (nb_fits(kb, nb, ct, full, gr)) return nb;
   return 0;
 }
 
-// K limit of the strip GEMV with ct strips per workgroup (16 waves of 8 blocks / ct).
-int strip_blocks_per_wave(int64_t K, int ct) { return blocks_per_wave(K, ct); }
+// Blocks per wave of the strip GEMV with ct strips per workgroup at this group size (0: the
+// shape does not fit); group sizes other than 32, 64, 128, 256 are checked as 32.
+int strip_blocks_per_wave(int64_t K, int ct, int group) {
+  const bool known = group == 32 || group == 64 || group == 128 || group == 256;
+  return blocks_per_wave(K, ct, 0, known ? group : 32);
+}
 
-// Strips per workgroup: 2 for SiLU*up (a gate strip and its up strip), else the tuning
-// override for RMSNorm-staged stores, else 1.
-static int strips_per_wg(const StripArgs& a) {
-  if (a.act) return 2;
-  if (a.hn && !a.h && g_strip_ct) return g_strip_ct;
-  return 1;
+// Strips per workgroup.  SiLU*up: 2 (one gate|up pair), or 6 (three pairs: 256 workgroups
+// of 12 waves on the 4096 x 24576 projection) on the tuning override where N and K allow.
+// RMSNorm-staged stores: the tuning override (1, 2, 4), else 1.  Others: 1.
+static StripGeom strip_geometry(const StripArgs& a) {
+  StripGeom g{1, 0, g_strip_full > 0 ? 1 : 0};
+  if (a.act) {
+    g.ct = 2;
+    if (g_strip_ct == 6 && a.N % (16 * 6) == 0 && blocks_per_wave(a.K, 6, g.full, a.group))
+      g.ct = 6;
+  } else if (a.hn && !a.h && g_strip_ct && g_strip_ct != 6) {
+    g.ct = g_strip_ct;
+  }
+  g.nb = blocks_per_wave(a.K, g.ct, g.full, a.group);
+  if (strip_deep_ring(a.group / 32, g.nb) == strip_ring(a.group / 32, g.nb)) g.full = 0;
+  return g;
 }
 
 template <int GR, int XSRC, int EPI, int CT>
-static void strip_nb(const StripArgs& a, int nb, hipStream_t st) {
+static void strip_nb(const StripArgs& a, const StripGeom& g, hipStream_t st) {
   const dim3 grid(a.N / (kStripCols * CT));
-  const dim3 block(64 * CT * (a.kblocks / nb));
-  const size_t lds = (size_t)(a.kblocks / nb) * 16 * nb * sizeof(u32x4);
-  switch (nb) {
-    case 2: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 2, CT>), grid, block, lds, st, a); break;
-    case 4: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 4, CT>), grid, block, lds, st, a); break;
-    case 6: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 6, CT>), grid, block, lds, st, a); break;
-    case 8: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 8, CT>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, 16, CT>), grid, block, lds, st, a); break;
+  const dim3 block(64 * CT * (a.kblocks / g.nb));
+  const size_t lds = (size_t)(a.kblocks / g.nb) * 16 * g.nb * sizeof(u32x4);
+#define MTL_STRIP_LAUNCH(NB_, WIN_) \
+  hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, NB_, CT, WIN_>), grid, block, lds, st, a)
+  switch (g.nb) {
+    case 2: MTL_STRIP_LAUNCH(2, 2); break;
+    case 4: MTL_STRIP_LAUNCH(4, 4); break;
+    case 6: MTL_STRIP_LAUNCH(6, strip_ring(GR, 6)); break;
+    case 8:
+      if (g.full) MTL_STRIP_LAUNCH(8, strip_deep_ring(GR, 8)); else MTL_STRIP_LAUNCH(8, 4);
+      break;
+    default:
+      if (g.full) MTL_STRIP_LAUNCH(16, strip_deep_ring(GR, 16)); else MTL_STRIP_LAUNCH(16, 4);
+      break;
   }
+#undef MTL_STRIP_LAUNCH
 }
 
 template <int GR>
-static void strip_variant(const StripArgs& a, int nb, int ct, hipStream_t st) {
+static void strip_variant(const StripArgs& a, const StripGeom& g, hipStream_t st) {
   if (a.act) {
-    strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 2>(a, nb, st);
+    if (g.ct == 6) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 6>(a, g, st);
+    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 2>(a, g, st);
   } else if (a.h) {
-    if (a.xpart) strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_RESID, 1>(a, nb, st);
-    else strip_nb<GR, XSRC_BF16, STRIP_EPI_RESID, 1>(a, nb, st);
+    if (a.xpart) strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_RESID, 1>(a, g, st);
+    else strip_nb<GR, XSRC_BF16, STRIP_EPI_RESID, 1>(a, g, st);
   } else if (a.hn) {
-    if (ct == 4) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 4>(a, nb, st);
-    else if (ct == 2) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 2>(a, nb, st);
-    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1>(a, nb, st);
+    if (g.ct == 4) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 4>(a, g, st);
+    else if (g.ct == 2) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 2>(a, g, st);
+    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1>(a, g, st);
   } else if (a.xpart) {
-    strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1>(a, nb, st);
+    strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1>(a, g, st);
   } else {
-    strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1>(a, nb, st);
+    strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1>(a, g, st);
   }
 }
 
 // Shapes, pointers and alignment are checked by the entry points.
 int strip_launch(const StripArgs& args, hipStream_t st) {
   StripArgs a = args;
-  const int ct = strips_per_wg(a);
-  const int nb = blocks_per_wave(a.K, ct);
-  if (!nb || a.N % (kStripCols * ct) != 0) return MTL_ERR_SHAPE;
+  const StripGeom g = strip_geometry(a);
+  if (!g.nb || a.N % (kStripCols * g.ct) != 0) return MTL_ERR_SHAPE;
   a.kblocks = a.K / kStripBlockK;
-  a.xcd_order = g_strip_xcd && (a.N / (kStripCols * ct)) % 8 == 0;
+  a.xcd_order = g_strip_xcd && (a.N / (kStripCols * g.ct)) % 8 == 0;
   switch (a.group) {
-    case 32: strip_variant<1>(a, nb, ct, st); break;
-    case 64: strip_variant<2>(a, nb, ct, st); break;
-    case 128: strip_variant<4>(a, nb, ct, st); break;
-    default: strip_variant<8>(a, nb, ct, st); break;
+    case 32: strip_variant<1>(a, g, st); break;
+    case 64: strip_variant<2>(a, g, st); break;
+    case 128: strip_variant<4>(a, g, st); break;
+    default: strip_variant<8>(a, g, st); break;
   }
   return launch_status();
 }
@@ -424,10 +476,19 @@ int mtl_tune_set_strip_nb(int32_t nb) {
   return MTL_OK;
 }
 
-// Strips per workgroup of the RMSNorm-staged store (0 = automatic, 1, 2 or 4).
+// Strips per workgroup (0 = automatic): 1, 2 or 4 for the RMSNorm-staged store, 2 or 6
+// for SiLU*up (other values leave that family automatic).
 int mtl_tune_set_strip_ct(int32_t ct) {
-  if (ct != 0 && ct != 1 && ct != 2 && ct != 4) return MTL_ERR_INVALID_ARG;
+  if (ct != 0 && ct != 1 && ct != 2 && ct != 4 && ct != 6) return MTL_ERR_INVALID_ARG;
   g_strip_ct = ct;
+  return MTL_OK;
+}
+
+// Blocks in flight per wave: 1 = the deep ring (8 blocks for waves of 8 or 16), 0 = the
+// default 4-block ring, -1 = automatic.
+int mtl_tune_set_strip_full(int32_t full) {
+  if (full < -1 || full > 1) return MTL_ERR_INVALID_ARG;
+  g_strip_full = full;
   return MTL_OK;
 }
 

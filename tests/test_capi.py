@@ -141,6 +141,8 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_w4_strip(FAKE, 4096, 24584, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
     assert lib.mtl_w4_strip(FAKE, 4096, 4096, FAKE, 100, None) == N.MTL_ERR_WORKSPACE
     assert lib.mtl_tune_set_strip_nb(3) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_tune_set_strip_ct(3) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_tune_set_strip_full(2) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG

@@ -535,6 +535,26 @@ def test_strip_residual_epilogue(dev, src):
     assert torch.equal(h2, h) and torch.equal(o2, h_ord) and torch.equal(s2, slots)
 
 
+@pytest.mark.parametrize("k,n,nb", [(4096, 1024, 8), (4096, 1024, 16), (12288, 512, 8)])
+def test_strip_ring_depth_is_bitwise_neutral(dev, k, n, nb):
+    # the deep load ring (8 blocks in flight) changes when loads are issued, not the
+    # arithmetic: outputs equal the default 4-block ring's bit for bit
+    lib = N.load()
+    case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=k + n + nb)
+    x = t_bf16(case["x_bits"], dev)
+    outs = []
+    try:
+        assert lib.mtl_tune_set_strip_nb(nb) == 0
+        for full in (0, 1):
+            assert lib.mtl_tune_set_strip_full(full) == 0
+            outs.append(_strip_partials(lib, case, dev, "bf16", x=x))
+    finally:
+        lib.mtl_tune_set_strip_nb(0)
+        lib.mtl_tune_set_strip_full(-1)
+    assert rel_l2(outs[0].cpu().numpy(), case["y_ref"][0]) < TOL_F32
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_strip_blocks_per_wave_knob(dev):
     # every launch shape of the strip GEMV computes the same product (rounding aside)
     lib = N.load()
@@ -552,16 +572,18 @@ def test_strip_blocks_per_wave_knob(dev):
     assert np.array_equal(outs[0], outs[8])     # automatic choice for K = 4096
 
 
-def test_strip_norm_silu_epilogue(dev):
-    # gate|up with RMSNorm staging and the SiLU*up epilogue (a gate strip and its up
-    # strip per workgroup): act equals bf16(silu(bf16 g) * bf16 u) of the strip sums taken
-    # with the same K slicing (8 blocks per wave for K = 4096), to float32 libm rounding,
-    # and the float64 oracle within the bf16 bar
+@pytest.mark.parametrize("n,ct,nb", [(2048, 0, 0), (3072, 6, 16)])
+def test_strip_norm_silu_epilogue(dev, n, ct, nb):
+    # gate|up with RMSNorm staging and the SiLU*up epilogue (one gate|up strip pair per
+    # workgroup by default, three with ct = 6): act equals bf16(silu(bf16 g) * bf16 u) of
+    # the strip sums taken with the same K slicing (8 blocks per wave for K = 4096 by
+    # default, 16 with three pairs), to float32 libm rounding, and the float64 oracle
+    # within the bf16 bar
     import ctypes
     from oracle import decode_ref as D
     from tests._decode_case import slots16
     lib = N.load()
-    k, n = 4096, 2048
+    k = 4096
     case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=123, with_ref=False)
     r = np.random.default_rng(124)
     hf = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)))
@@ -576,11 +598,18 @@ def test_strip_norm_silu_epilogue(dev):
                                      ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
                                      qz.data_ptr(), n, 128, 0, N.LAYOUT_ROWS, act.data_ptr(),
                                      st) == N.MTL_ERR_UNSUPPORTED
-    N.check(lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
-                                      ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
-                                      qz.data_ptr(), n, 128, 0, N.LAYOUT_STRIP, act.data_ptr(), st),
-            "norm silu")
-    y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots).cpu().numpy()
+    try:
+        assert lib.mtl_tune_set_strip_ct(ct) == 0
+        N.check(lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                          ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
+                                          qz.data_ptr(), n, 128, 0, N.LAYOUT_STRIP, act.data_ptr(),
+                                          st), "norm silu")
+        assert lib.mtl_tune_set_strip_ct(0) == 0
+        assert lib.mtl_tune_set_strip_nb(nb) == 0
+        y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots).cpu().numpy()
+    finally:
+        lib.mtl_tune_set_strip_ct(0)
+        lib.mtl_tune_set_strip_nb(0)
     j = np.arange(n // 2)
     gcol = (j // 32) * 64 + j % 32
     rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
