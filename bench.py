@@ -141,6 +141,7 @@ def bench_gemv(args, torch, pkg):
                               gbs=round(s["bytes"] / mean_us / 1e3, 1),
                               frac=round(s["bytes"] / mean_us / 1e3 / HBM_PEAK_GBS, 4),
                               copies=len(s["copies"]))
+    skinny = bench_skinny(args, torch, dev)
     step_bytes = sum(s["bytes"] for s in shapes)
     gu = per["gate_up"]
     return dict(
@@ -149,11 +150,67 @@ def bench_gemv(args, torch, pkg):
         dtype="int4 weights, bf16 x, fp32 accumulate",
         config={"workload": "int4 GEMV sweep M=1 act-order g128: qkv 4096x6144, o 4096x4096, "
                             "gate_up 4096x24576, down 12288x4096 (one step = one layer's 4 GEMVs)",
-                "per_kernel": per, "step_bytes": step_bytes},
+                "per_kernel": per, "step_bytes": step_bytes,
+                "skinny_gate_up": skinny},
         roofline={"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": gu["frac"], "traffic": None,
                   "kernel": "w4_gemm_kernel<1,16,GPTQ,perm> gate_up 4096x24576 M=1"},
     )
+
+
+def bench_skinny(args, torch, dev):
+    """Skinny-batch int4 GEMM on the gate_up shape (K 4096, N 24576, group 128, no
+    act-order) at M = 1, 2, 4, 8, 16 bf16 rows, one launch per call, weight copies rotated
+    past the Infinity Cache, mean us per launch: the full-K strip GEMM (no partials) and the
+    split-K GEMM (partials reduced by a second kernel)."""
+    from moss_tts_lite_amd import _native as N
+    from moss_tts_lite_amd import ops
+
+    k, n = 4096, 24576
+    per_copy = algo_bytes(1, k, n, GROUP, False)
+    copies = []
+    for c in range(max(2, math.ceil(640e6 / per_copy))):
+        qw, qz, sc, _ = make_gptq_weights(torch, dev, k, n, GROUP, seed=4321 + 13 * c, act_order=False)
+        copies.append((qw, ops.strip_weights(qw), qz, sc))
+    lib = N.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for kind in ("strip_rows", "split_k"):
+        res = {}
+        for m in (1, 2, 4, 8, 16):
+            x = torch.randn(m, k, device=dev, generator=torch.Generator(device=dev).manual_seed(m)).bfloat16()
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            ops.reserve_workspace(dev, ops.gemm_workspace_bytes(m, k, n, GROUP))
+
+            def launch(i):
+                qw, qs, qz, sc = copies[i % len(copies)]
+                if kind == "split_k":
+                    ops.w4_gemm(x, qw, N.META_GPTQ, sc, qz, None, n, GROUP, out=y)
+                else:
+                    N.check(lib.mtl_w4_gemm_strip_rows(x.data_ptr(), m, k, k, qs.data_ptr(),
+                                                       sc.data_ptr(), qz.data_ptr(), n, GROUP, 0,
+                                                       y.data_ptr(), n, N.OUT_BF16, stream),
+                            "strip rows")
+
+            for i in range(len(copies)):
+                launch(i)
+            reps = 4 * len(copies)
+            a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(2e8))
+            a_ev.record()
+            for i in range(reps):
+                launch(i)
+            b_ev.record()
+            torch.cuda.synchronize()
+            us = a_ev.elapsed_time(b_ev) * 1e3 / reps
+            byts = algo_bytes(m, k, n, GROUP, False)
+            res[f"M{m}"] = dict(us=round(us, 3), gbs=round(byts / us / 1e3, 1),
+                                frac=round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+                                tflops=round(2 * m * k * n / us / 1e6, 2))
+        out[kind] = res
+    del copies
+    return out
 
 
 def cpu_baseline_gemv(budget_s: float = 12.0):

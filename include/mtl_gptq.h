@@ -154,6 +154,26 @@ int64_t mtl_w4_strip_bytes(int64_t K, int64_t N);
 int mtl_w4_strip(const int32_t* qweight, int64_t K, int64_t N, int32_t* strip, int64_t strip_bytes,
                  void* stream);
 
+/*
+ * Skinny-batch int4 GEMM over the strip layout: y[M, N] = x[M, K] @ dequant(W), 1 <= M <= 16,
+ * fp32 accumulation, no workspace.  Replaces torch._weight_int4pack_mm at M > 1, which the
+ * reference's quantized prefill runs on every projection (moss_tts_lite/fast.py:218-270,
+ * via _linear at fast.py:107-121).  A workgroup owns whole columns over all of K, so no
+ * split-K partials are written; x of all M rows is staged once per workgroup.
+ *   x             bf16 [M, K], rows ldx elements apart (16-byte aligned, ldx % 8 == 0)
+ *   strip_weight  mtl_w4_strip output of qweight [K/8, N] (no act-order permutation: the
+ *                 caller orders x's channels as the weight's rows)
+ *   scales/qzeros as mtl_gptq_gemm; zero_offset as there
+ *   y             [M, N] bf16 or f32 (out_dtype), rows ldy elements apart
+ * K % 256 == 0, K <= 4096 (16 rows of x in LDS), N % 16 == 0; group_size 128 or 256
+ * (32 and 64 return MTL_ERR_UNSUPPORTED: the split-K mtl_gptq_gemm serves them).
+ */
+int mtl_w4_gemm_strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K,
+                           const int32_t* strip_weight, const void* scales,
+                           const int32_t* qzeros, int64_t N, int32_t group_size,
+                           int32_t zero_offset, void* y, int64_t ldy, int32_t out_dtype,
+                           void* stream);
+
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
                      void* stream);

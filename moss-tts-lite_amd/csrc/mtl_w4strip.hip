@@ -34,7 +34,7 @@ constexpr int strip_deep_ring(int gr, int nb) { return gr <= 2 || nb < 8 ? strip
 // VGPRs each); 12 (168 VGPRs) for the deep ring at NB = 16; 8 at g = 32 from NB = 8 on,
 // whose metadata needs more than 128 VGPRs.
 constexpr int strip_max_waves(int gr, int nb, int win) {
-  return gr == 1 && nb >= 8 ? 8 : nb >= 16 && win > 4 ? 12 : kStripMaxWaves;
+  return gr == 1 && nb >= 8 ? 8 : nb >= 16 ? 12 : kStripMaxWaves;
 }
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
 
@@ -218,8 +218,9 @@ w4_strip_kernel(StripArgs a) {
   float cur_s = 0.f, cur_z = 0.f;               // g = 256: the group of this block pair
   floatx4 acc;
   // Ring turns with the WIN ring slots unrolled inside, so ring indexes stay compile-time.
-  // Up to 8 blocks the turns are unrolled too (measured faster); at 16 they stay a loop,
-  // so a 16-block wave needs no more registers than a 4-block one.  The last turn is
+  // The turns are unrolled too (measured faster than a loop, whose ring registers need
+  // copies at the back edge), except at g = 32 from 6 blocks on, whose four groups per
+  // block would not fit in registers unrolled.  The last turn is
   // peeled: it issues no refills, so inside the loop every refill is unconditional and the
   // waits stay exact (a refill under a run-time branch makes the compiler wait for every
   // outstanding load).  Groups never straddle a turn: 4 * WIN row quads hold whole groups
@@ -261,7 +262,7 @@ w4_strip_kernel(StripArgs a) {
       }
     }
   };
-  constexpr int kTurnUnroll = NB <= 8 ? NB / WIN : 1;
+  constexpr int kTurnUnroll = GR == 1 && NB >= 6 ? 1 : NB / WIN;
 #pragma unroll kTurnUnroll
   for (int b0 = 0; b0 < NB - WIN; b0 += WIN) turn(b0, true);
   turn(NB - WIN, false);

@@ -205,6 +205,29 @@ def strip_weights(qweight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.Tensor,
+                    scales: torch.Tensor, n: int, group_size: int, zero_offset: int = 0,
+                    out: torch.Tensor | None = None,
+                    out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Skinny-batch GEMM over the strip layout (``mtl_w4_gemm_strip_rows``): ``x [M, K]``
+    bf16 with M <= 16 rows per launch (longer inputs run in 16-row chunks), ``K <= 4096``,
+    group 128 or 256; returns ``[M, n]``."""
+    x2 = _check_x(x, x.shape[-1])
+    m, k = x2.shape
+    if out is None:
+        out = torch.empty(m, n, dtype=out_dtype, device=x2.device)
+    odt = N.OUT_F32 if out.dtype == torch.float32 else N.OUT_BF16
+    lib = N.load()
+    stream = _stream(x2.device)
+    for r0 in range(0, m, _MAX_M):
+        r1 = min(m, r0 + _MAX_M)
+        N.check(lib.mtl_w4_gemm_strip_rows(
+            x2[r0:r1].data_ptr(), r1 - r0, k, k, strip_weight.data_ptr(), scales.data_ptr(),
+            qzeros.data_ptr(), n, group_size, zero_offset, out[r0:r1].data_ptr(), n, odt, stream),
+            "mtl_w4_gemm_strip_rows")
+    return out
+
+
 def unpack_codes(qweight: torch.Tensor) -> torch.Tensor:
     """``qweight [K/8, N]`` -> codes uint8 ``[K, N]``."""
     k = qweight.shape[0] * 8

@@ -183,6 +183,73 @@ def test_gate_up_skinny_batch(dev, m):
     assert err < TOL_F32
 
 
+def run_strip_rows(case, dev, out_dtype=torch.float32, zero_offset=0):
+    qw = ops.strip_weights(t_i32(case["qweight"], dev))
+    y = ops.strip_rows_gemm(t_bf16(case["x_bits"], dev), qw, t_i32(case["qzeros"], dev),
+                            t_f16(case["scales"], dev), case["n"], case["group"],
+                            zero_offset=zero_offset, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 8, 16, 21])
+def test_strip_rows_gate_up_skinny_batch(dev, m):
+    # the full-K strip GEMM on the 4096 x 24576 projection: every row against float64
+    # (M = 21 runs as a 16-row and a 5-row launch)
+    cols = np.arange(0, 24576, 48)
+    case = synth.gptq_case(k=4096, n=24576, m=m, group=128, act_order=False, seed=199 + m,
+                           ref_cols=cols)
+    y = run_strip_rows(case, dev)
+    err = rel_l2(y[:, cols], case["y_ref"])
+    print(f"strip rows gate_up M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32 and np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("group,k,n,m", [(128, 1024, 528, 5), (256, 4096, 6144, 16),
+                                         (128, 768, 4096, 7), (256, 512, 96, 2)])
+def test_strip_rows_shapes(dev, group, k, n, m):
+    case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=False, seed=group + k + n + m)
+    y = run_strip_rows(case, dev)
+    err = rel_l2(y, case["y_ref"])
+    print(f"strip rows g{group} {k}x{n} M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32
+    yb = run_strip_rows(case, dev, out_dtype=torch.bfloat16, zero_offset=0)
+    assert rel_l2(yb, case["y_ref"]) < TOL_BF16
+    # repeatable bit for bit, and row r of a batch equals the same row alone (rows do not
+    # interact: the same strips, slices and summation order)
+    assert np.array_equal(y, run_strip_rows(case, dev))
+    one = dict(case, m=1, x_bits=case["x_bits"][m - 1:m])
+    assert np.array_equal(run_strip_rows(one, dev)[0], y[m - 1])
+
+
+def test_strip_rows_matches_strip_gemv_at_m1(dev):
+    # at M = 1 the skinny kernel and the decode GEMV run different launch shapes; both
+    # agree with float64 and with each other within fp32 rounding
+    case = synth.gptq_case(k=4096, n=1024, m=1, group=128, seed=77)
+    y = run_strip_rows(case, dev)[0]
+    ys = _strip_partials(N.load(), case, dev, "bf16", x=t_bf16(case["x_bits"], dev)).cpu().numpy()
+    assert rel_l2(y, case["y_ref"][0]) < TOL_F32 and rel_l2(y, ys) < 1e-5
+
+
+def test_strip_rows_validation(dev):
+    lib = N.load()
+    st = torch.cuda.current_stream().cuda_stream
+    x = torch.zeros(16, 8192, dtype=torch.bfloat16, device=dev)
+    w = torch.zeros(8192 * 64 // 8, dtype=torch.int32, device=dev)
+    sc = torch.zeros(8192 // 32 * 64, dtype=torch.float16, device=dev)
+    qz = torch.zeros(8192 // 32 * 8, dtype=torch.int32, device=dev)
+    y = torch.zeros(16, 64, dtype=torch.float32, device=dev)
+    call = lambda m, k, g, n=64: lib.mtl_w4_gemm_strip_rows(  # noqa: E731
+        x.data_ptr(), m, 8192, k, w.data_ptr(), sc.data_ptr(), qz.data_ptr(), n, g, 0,
+        y.data_ptr(), 64, N.OUT_F32, st)
+    assert call(4, 4096, 32) == N.MTL_ERR_UNSUPPORTED
+    assert call(4, 4096, 48) == N.MTL_ERR_GROUP
+    assert call(4, 8192, 128) == N.MTL_ERR_SHAPE       # 16 rows of x would not fit in LDS
+    assert call(17, 4096, 128) == N.MTL_ERR_SHAPE
+    assert call(4, 4096, 128, n=72) == N.MTL_ERR_SHAPE
+    torch.cuda.synchronize()
+
+
 # ------------------------------------------------------------------ reference contract
 
 @pytest.mark.parametrize("n,k,m", [(512, 512, 8), (1024, 4096, 8), (4096, 4096, 1)])
