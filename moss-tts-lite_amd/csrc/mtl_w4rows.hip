@@ -9,8 +9,8 @@
 // partial ever leaves it: the split-K GEMM writes and re-reads splits * M * N * 4 bytes of
 // partials, which at M = 16 on the 4096 x 24576 projection is 12.6 MB per launch.
 //
-// x of all M rows over all of K is staged once per workgroup in LDS as [M][K/8] items in
-// pair order (up to 16 * K * 2 bytes: K <= 4096), plus one zero row that the A operands of
+// x of all M rows over all of K is staged once per workgroup in LDS as [M][K/8 + 1] items
+// in pair order (one item of padding per row against bank conflicts) (up to 16 * K * 2 bytes: K <= 4096), plus one zero row that the A operands of
 // rows >= M read, with its per-group sums as [group][16 rows]
 // (rows >= M zero), so every workgroup (one per CU) reads x once from L2 and a lane reads
 // the sums of its four result rows with one LDS load.
@@ -20,7 +20,7 @@ namespace mtl {
 
 constexpr int kStripCols = 16;         // output columns per strip
 constexpr int kRowsMax = 16;
-constexpr int kRowsMaxK = 4096;       // 16 rows of x and a zero row in LDS (136 KB)
+constexpr int kRowsMaxK = 4096;       // 16 rows of x and a zero row in LDS (140 KB)
 constexpr int kRowsMaxWaves = 16;
 // Waves per workgroup: 16 (128 VGPRs each), 12 (168 VGPRs) at 16 blocks per wave.
 constexpr int rows_max_waves(int nb) { return nb >= 16 ? 12 : kRowsMaxWaves; }
@@ -50,8 +50,11 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   const int kw = nw / CT;                      // K slices
   const int K8 = a.K >> 3;                     // x items per row
   const int ngrp = a.K / a.group;
-  u32x4* xa = smem;                                                   // [M + 1][K8]
-  float* xg = reinterpret_cast<float*>(smem + (size_t)(a.M + 1) * K8);  // [ngrp][16]
+  // rows XS = K8 + 1 items apart: the 16 rows an MFMA's A operand reads then start 16
+  // bytes apart in the LDS banks instead of all on the same banks
+  const int XS = K8 + 1;
+  u32x4* xa = smem;                                                   // [M + 1][XS]
+  float* xg = reinterpret_cast<float*>(smem + (size_t)(a.M + 1) * XS);  // [ngrp][16]
   float* ytile = xg + 16 * ngrp;                                      // [nw][16][16]
 
   const int wave = wave_id();
@@ -102,8 +105,9 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
     for (int z = threadIdx.x; z < ngrp * 16; z += nthr)        // group sums of rows >= M
       if ((z & 15) >= a.M) xg[z] = 0.f;
     for (int z = threadIdx.x; z < K8; z += nthr)               // row M: the zero A row
-      xa[a.M * K8 + z] = u32x4{0u, 0u, 0u, 0u};
-    constexpr int BATCH = 8;
+      xa[a.M * XS + z] = u32x4{0u, 0u, 0u, 0u};
+    // loads per thread in flight: 16 rows of K = 4096 in one batch (12 at 12 waves, 8 at 16)
+    constexpr int BATCH = rows_max_waves(NB) == 12 ? 12 : 8;
     for (int f0 = 0; f0 < total; f0 += BATCH * nthr) {
       u32x4 v[BATCH];
 #pragma unroll
@@ -123,8 +127,8 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
         for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
         if (f < total) {                                 // M * K8 need not fill the wave
-          xa[f] = pv;
           const int m = f / K8, i = f - m * K8;
+          xa[m * XS + i] = pv;
           if ((i & (GI - 1)) == 0) xg[(i / GI) * 16 + m] = sum;
         }
       }
@@ -137,7 +141,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   //    r = 0..3; per group y[m] += s * (A[m] - (128 + z) * X[m]).
   const uint32_t kMagic = vgpr_const(0x43004300u);
   const uint32_t kLo = vgpr_const(0x000F000Fu);
-  const u32x4* xrow = xa + (lj < a.M ? lj : a.M) * K8;       // rows >= M read the zero row
+  const u32x4* xrow = xa + (lj < a.M ? lj : a.M) * XS;       // rows >= M read the zero row
   float tot[4] = {0.f, 0.f, 0.f, 0.f};
   float cur_s = 0.f, cur_z = 0.f;
   floatx4 acc;
@@ -315,7 +319,7 @@ int mtl_w4_gemm_strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K,
   a.kblocks = (int)(K / 128);
   const int64_t G = N / (kStripCols * g.ct);
   a.xcd_order = G % 8 == 0;
-  const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)16 * (K / group_size) * 4 +
+  const size_t lds = (size_t)(M + 1) * (K / 8 + 1) * 16 + (size_t)16 * (K / group_size) * 4 +
                      (size_t)g.ct * g.kw * 256 * 4;
   hipStream_t st = (hipStream_t)stream;
   if (group_size == 128) rows_ct<4>(a, g, lds, st);
