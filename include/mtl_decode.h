@@ -150,6 +150,18 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
 int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,
                   int64_t pad_period, int64_t pad_index, void* stream);
 
+/*
+ * A linear kept in bf16 inside the decode step (the reference's F.linear on a kept
+ * projection, moss_tts_lite/gptq.py:689-693, e.g. v_proj in the shipped GPTQ presets,
+ * export.py:59-72): out[n] = bf16(sum_k x[k] W[n, k]) stored as fp32, where
+ * x = RMSNorm(h) = bf16(norm_w * bf16(h * rsqrt(sum(slots)/K + eps))) is formed while
+ * staging (slots: the sums of squares of h per 16 columns).  The fp32 values are bf16
+ * numbers, for consumers that read fp32 partials (one split).  W bf16 [N, K] row-major;
+ * K % 8 == 0, K <= 12288; h, norm_w, slots, W 16-byte aligned.
+ */
+int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, float eps,
+                       const void* w, int64_t N, int64_t K, float* out, void* stream);
+
 /* pos[0] += 1 on the device (ends a captured decode step). */
 int mtl_advance_position(int64_t* pos, void* stream);
 

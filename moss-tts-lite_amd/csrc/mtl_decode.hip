@@ -828,7 +828,8 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
                                                         const uint16_t* __restrict__ norm_w,
                                                         const float* __restrict__ slots,
                                                         float eps, int64_t pad_period,
-                                                        int64_t pad_index) {
+                                                        int64_t pad_index,
+                                                        float* __restrict__ out_f32) {
   __shared__ float sv[4];
   __shared__ long long si[4];
   const int wave = wave_id(), lane = threadIdx.x & 63;
@@ -901,6 +902,7 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
       uint32_t hb = f32_to_bf16(sum);
       if (pad_period > 0 && r % pad_period == pad_index) hb = 0xff80u;   // -inf
       if (logits && lane == 0) logits[r] = (uint16_t)hb;
+      if (out_f32 && lane == 0) out_f32[r] = bf16_to_f32(hb);   // the bf16 value, for fp32 readers
       const float lv = bf16_to_f32(hb);
       if (better(lv, r, best, bidx)) {   // rows in ascending order: first maximum kept
         best = lv;
@@ -927,15 +929,21 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
   }
 }
 
-// Launch the head GEMV with x held in ceil(K/512) items of 8 channels per lane.
+// Launch the head GEMV with x held in ceil(K/512) items of 8 channels per lane, on `wgs`
+// workgroups (kHeadWGs when an argmax reads the per-workgroup partials).
+template <typename... Args>
+static void launch_head_on(int wgs, int64_t K, hipStream_t s, Args... args) {
+  if (K <= 4096)
+    hipLaunchKernelGGL(head_gemv_kernel<8>, dim3(wgs), dim3(256), 0, s, args...);
+  else if (K <= 8192)
+    hipLaunchKernelGGL(head_gemv_kernel<16>, dim3(wgs), dim3(256), 0, s, args...);
+  else
+    hipLaunchKernelGGL(head_gemv_kernel<24>, dim3(wgs), dim3(256), 0, s, args...);
+}
+
 template <typename... Args>
 static void launch_head(int64_t K, hipStream_t s, Args... args) {
-  if (K <= 4096)
-    hipLaunchKernelGGL(head_gemv_kernel<8>, dim3(kHeadWGs), dim3(256), 0, s, args...);
-  else if (K <= 8192)
-    hipLaunchKernelGGL(head_gemv_kernel<16>, dim3(kHeadWGs), dim3(256), 0, s, args...);
-  else
-    hipLaunchKernelGGL(head_gemv_kernel<24>, dim3(kHeadWGs), dim3(256), 0, s, args...);
+  launch_head_on(kHeadWGs, K, s, args...);
 }
 
 __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restrict__ part_v,
@@ -1131,7 +1139,7 @@ int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, voi
   long long* pi = reinterpret_cast<long long*>(static_cast<char*>(workspace) + kHeadWGs * 4);
   launch_head(K, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), N, (int)K,
-                     static_cast<uint16_t*>(logits), pv, pi, nullptr, nullptr, 0.f, 0, 0);
+                     static_cast<uint16_t*>(logits), pv, pi, nullptr, nullptr, 0.f, 0, 0, nullptr);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
                        token_out);
@@ -1201,7 +1209,7 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
   launch_head(K, s,
                      static_cast<const uint16_t*>(h), static_cast<const uint16_t*>(w), N, (int)K,
                      static_cast<uint16_t*>(logits), pv, pi, static_cast<const uint16_t*>(norm_w),
-                     slots, eps, 0, 0);
+                     slots, eps, 0, 0, nullptr);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
                        token_out);
@@ -1218,7 +1226,22 @@ int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,
   launch_head(K, (hipStream_t)stream,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), N, (int)K,
                      static_cast<uint16_t*>(out), nullptr, nullptr, nullptr, nullptr, 0.f,
-                     pad_period, pad_index);
+                     pad_period, pad_index, nullptr);
+  return launch_status();
+}
+
+int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, float eps,
+                       const void* w, int64_t N, int64_t K, float* out, void* stream) {
+  if (!h || !norm_w || !slots || !w || !out) return MTL_ERR_INVALID_ARG;
+  if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
+  if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w) || !aligned16(slots))
+    return MTL_ERR_ALIGN;
+  // one row per wave where N allows: every wave stages the normalised x
+  const int64_t wgs = (N + 3) / 4 < kHeadWGs ? (N + 3) / 4 : kHeadWGs;
+  launch_head_on((int)wgs, K, (hipStream_t)stream, static_cast<const uint16_t*>(h),
+                 static_cast<const uint16_t*>(w), N, (int)K, static_cast<uint16_t*>(nullptr),
+                 static_cast<float*>(nullptr), static_cast<long long*>(nullptr),
+                 static_cast<const uint16_t*>(norm_w), slots, eps, (int64_t)0, (int64_t)0, out);
   return launch_status();
 }
 

@@ -81,6 +81,11 @@ class FastDecoder:
             raise ValueError("split_k names GEMVs of the strip plan: 'qkv', 'gate_up'")
         self.m = model
         self.plan = plan
+        # layers whose v_proj stays bf16: q|k on the int4 strip GEMV and v on the bf16
+        # GEMV, both into one fp32 "split" of the q|k|v partials the attention reads
+        self.v_keep = ["v_keep" in lyr for lyr in model.layers]
+        if any(self.v_keep) and plan != "strip":
+            raise ValueError("layers with a bf16-kept v_proj run in the strip plan")
         self.fused = plan != "unfused"
         self.strip = plan == "strip"
         # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
@@ -259,9 +264,23 @@ class FastDecoder:
             plan.append(("mtl_residual_add", (None, 0, self.h.data_ptr(), p(self.inv_perm_qkv[0]),
                                               self.x_qkv.data_ptr(), self.slots.data_ptr(),
                                               cfg.hidden)))
+        qkv_splits = self.splits["qkv"]
+        if self.v_keep[li]:
+            nqk = lyr["qkv"].out_features
+            plan += [
+                self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"], nqk, "qkv",
+                                    strip=True),
+                ("mtl_bf16_gemv_norm", (self.h.data_ptr(), lyr["input_layernorm"].data_ptr(),
+                                        self.slots.data_ptr(), eps, lyr["v_keep"].data_ptr(),
+                                        lyr["v_keep"].shape[0], cfg.hidden,
+                                        self.part["qkv"][nqk:].data_ptr())),
+            ]
+            qkv_splits = 1
+        else:
+            plan.append(self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"],
+                                            cfg.qkv_out, "qkv"))
         plan += [
-            self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"], cfg.qkv_out, "qkv"),
-            ("mtl_decode_attention_fused", (self.part["qkv"].data_ptr(), self.splits["qkv"],
+            ("mtl_decode_attention_fused", (self.part["qkv"].data_ptr(), qkv_splits,
                                             lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(),
                                             m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
                                             kc.data_ptr(), vc.data_ptr(), self.pos.data_ptr(),
@@ -309,9 +328,9 @@ class FastDecoder:
                  lin.zero_offset, layout, self.h.data_ptr(), p(scatter), p(h_ord),
                  self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel()))
 
-    def _norm_partials(self, h_ord, w_ord, lin, n, name):
+    def _norm_partials(self, h_ord, w_ord, lin, n, name, strip=None):
         _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip_gemv[name])
+        qw, layout = lin.stream_weight(self.strip_gemv[name] if strip is None else strip)
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
@@ -369,7 +388,7 @@ class FastDecoder:
                       "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
                       "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
                       "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual",
-                      "mtl_w4_gemm_norm_silu")}
+                      "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -418,6 +437,8 @@ class FastDecoder:
     def gemv_launch(self, li: int, name: str):
         """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
         shift = 1 if self.plan in ("fused", "strip") and li == 0 else 0   # layer 0: the stats
+        if self.v_keep[li] and name != "qkv":
+            shift += 1                                                     # the bf16 v launch
         return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:
@@ -529,7 +550,7 @@ class FastMossDecoder(FastDecoder):
     serves every cache length.
     """
 
-    def __init__(self, model: Int4Backbone, plan: str = "staged"):
+    def __init__(self, model: Int4Backbone, plan: str = "strip"):
         if model.cfg.n_vq < 1:
             raise ValueError("FastMossDecoder needs a MOSS-shaped backbone (cfg.n_vq > 0)")
         self.graphs: dict | None = None

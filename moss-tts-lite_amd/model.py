@@ -130,6 +130,18 @@ class Int4Backbone:
                 lin.post_init()
                 lin.drop_original()
                 lyr[k] = lin
+            # v_proj kept in bf16 (the shipped GPTQ presets, export.py:59-72): "qkv" then
+            # holds q|k only and "v" the bf16 weight [kv_heads * head_dim, hidden]
+            nv = cfg.n_kv_heads * cfg.head_dim
+            if "v" in lw:
+                v = lw["v"]
+                if v.dtype != torch.bfloat16 or tuple(v.shape) != (nv, cfg.hidden):
+                    raise ValueError(f"kept v must be bfloat16 [{nv}, {cfg.hidden}]")
+                lyr["v_keep"] = T(v)
+                if lyr["qkv"].out_features != cfg.qkv_out - nv:
+                    raise ValueError("with a kept v, qkv must hold q|k only")
+            elif lyr["qkv"].out_features != cfg.qkv_out:
+                raise ValueError("qkv must hold q|k|v")
             # gate|up emits its SiLU*up channels already in the down projection's
             # act-order input order, so the down GEMV reads them without a gather.
             perm_down = lyr["down"].kernel_args()[3]
@@ -166,8 +178,10 @@ def _random_gptq(gen, dev, k: int, n: int, g: int, perm: torch.Tensor | None) ->
     return GPTQLinear.from_buffers(qweight, qzeros, scales, g_idx, g)
 
 
-def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda") -> dict:
-    """Random-init weights of the configured shape, generated on the device."""
+def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda",
+                   v_keep: bool = False) -> dict:
+    """Random-init weights of the configured shape, generated on the device; with
+    ``v_keep`` each layer's v_proj stays bf16 (q|k int4), as in the shipped presets."""
     dev = torch.device(device)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -183,15 +197,19 @@ def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda") -> dict
         return torch.randperm(k, device=dev, generator=gen) if cfg.act_order else None
 
     layers = []
+    nv = cfg.n_kv_heads * cfg.head_dim
     for _ in range(cfg.n_layers):
-        layers.append({
+        lw = {
             "input_layernorm": norm_w(h), "post_attention_layernorm": norm_w(h),
             "q_norm": norm_w(cfg.head_dim), "k_norm": norm_w(cfg.head_dim),
-            "qkv": _random_gptq(gen, dev, h, cfg.qkv_out, g, perm(h)),
+            "qkv": _random_gptq(gen, dev, h, cfg.qkv_out - (nv if v_keep else 0), g, perm(h)),
             "o": _random_gptq(gen, dev, h, h, g, perm(h)),
             "gate_up": _random_gptq(gen, dev, h, 2 * cfg.intermediate, g, perm(h)),
             "down": _random_gptq(gen, dev, cfg.intermediate, h, g, perm(cfg.intermediate)),
-        })
+        }
+        if v_keep:
+            lw["v"] = normal(nv, h, std=0.02)
+        layers.append(lw)
     out = {"embed_tokens": normal(cfg.vocab, h, std=1.0), "final_norm": norm_w(h),
            "head": normal(cfg.vocab, h, std=0.02), "layers": layers}
     if cfg.n_vq:

@@ -46,29 +46,35 @@ def gate_up_columns(inter: int):
     return gate, gate + 32
 
 
-def build_case(cfg: BackboneConfig, seed: int, dev):
+def build_case(cfg: BackboneConfig, seed: int, dev, v_keep: bool = False):
+    """``v_keep``: each layer's v_proj stays a bf16 weight (q|k int4), as in the shipped
+    GPTQ presets."""
     r = synth.rng(seed)
     h, g, hd = cfg.hidden, cfg.group_size, cfg.head_dim
+    qn, kn = cfg.n_heads * hd, cfg.n_kv_heads * hd
     np_layers, dev_layers = [], []
     for _ in range(cfg.n_layers):
         norms = {k: _bf16_bits(r, n, std=0.05, mean=1.0) for k, n in
                  (("input_layernorm", h), ("post_attention_layernorm", h), ("q_norm", hd),
                   ("k_norm", hd))}
-        lin = {"qkv": _gptq_np(r, h, cfg.qkv_out, g, cfg.act_order),
+        lin = {"qkv": _gptq_np(r, h, cfg.qkv_out - (kn if v_keep else 0), g, cfg.act_order),
                "o": _gptq_np(r, h, h, g, cfg.act_order),
                "gate_up": _gptq_np(r, h, 2 * cfg.intermediate, g, cfg.act_order),
                "down": _gptq_np(r, cfg.intermediate, h, g, cfg.act_order)}
+        v_bits = _bf16_bits(r, (kn, h), std=0.05) if v_keep else None
         w_qkv = _dequant(lin["qkv"], g)
-        qn, kn = cfg.n_heads * hd, cfg.n_kv_heads * hd
         w_gu = _dequant(lin["gate_up"], g)
         gcol, ucol = gate_up_columns(cfg.intermediate)
         lw = {k: bf16_bits_to_f32(v) for k, v in norms.items()}
-        lw.update(q=w_qkv[:, :qn], k=w_qkv[:, qn:qn + kn], v=w_qkv[:, qn + kn:],
+        lw.update(q=w_qkv[:, :qn], k=w_qkv[:, qn:qn + kn],
+                  v=bf16_bits_to_f32(v_bits).T if v_keep else w_qkv[:, qn + kn:],
                   o=_dequant(lin["o"], g), gate=w_gu[:, gcol], up=w_gu[:, ucol],
                   down=_dequant(lin["down"], g))
         np_layers.append(lw)
         dl = {k: torch.from_numpy(v.view(np.int16)).view(torch.bfloat16) for k, v in norms.items()}
         dl.update({k: _to_linear(v, g, dev) for k, v in lin.items()})
+        if v_keep:
+            dl["v"] = torch.from_numpy(v_bits.view(np.int16)).view(torch.bfloat16).to(dev)
         dev_layers.append(dl)
     emb = _bf16_bits(r, (cfg.vocab, h), std=1.0)
     head = _bf16_bits(r, (cfg.vocab, h), std=0.02)

@@ -531,6 +531,75 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     assert int(tok.item()) == int(np.argmax(fb(logits)))
 
 
+def test_bf16_gemv_norm_kept_linear(dev, lib):
+    # a linear kept in bf16 with RMSNorm staging (the v_proj of the shipped presets):
+    # fp32 outputs holding bf16 values, equal bit for bit to the bf16 logits of the
+    # head kernel on the same input, and within the bf16 bar of float64
+    r = np.random.default_rng(52)
+    N_, K = 1024, 4096
+    h = round_bf16((2 * r.standard_normal(K)).astype(np.float32))
+    w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
+    W = round_bf16((r.standard_normal((N_, K)) * 0.05).astype(np.float32))
+    slots = torch.from_numpy(slots16(h)).to(dev)
+    tW, th, tw = tb(W, dev), tb(h, dev), tb(w, dev)
+    out = torch.full((N_,), float("nan"), dtype=torch.float32, device=dev)
+    N.check(lib.mtl_bf16_gemv_norm(th.data_ptr(), tw.data_ptr(), slots.data_ptr(),
+                                   ctypes.c_float(1e-6), tW.data_ptr(), N_, K, out.data_ptr(),
+                                   stream()), "bf16 gemv norm")
+    logits = torch.zeros(N_, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(int(lib.mtl_head_workspace_bytes(N_)), dtype=torch.uint8, device=dev)
+    N.check(lib.mtl_bf16_gemv_argmax_norm(th.data_ptr(), tw.data_ptr(), slots.data_ptr(),
+                                          ctypes.c_float(1e-6), tW.data_ptr(), N_, K,
+                                          logits.data_ptr(), None, ws.data_ptr(), ws.numel(),
+                                          stream()), "head norm")
+    torch.cuda.synchronize()
+    assert torch.equal(out, logits.float())
+    ref = round_bf16((W.astype(np.float64) @ D.rms_norm(h, w).astype(np.float64)).astype(np.float32))
+    err = rel_l2(out.cpu().numpy(), ref)
+    print(f"kept bf16 linear rel_l2={err:.2e}")
+    assert err < 1e-2
+    assert lib.mtl_bf16_gemv_norm(th.data_ptr(), tw.data_ptr(), slots.data_ptr(),
+                                  ctypes.c_float(1e-6), tW.data_ptr(), N_, 4100, out.data_ptr(),
+                                  stream()) == N.MTL_ERR_SHAPE
+
+
+def test_kept_v_proj_step_matches_oracle_and_graph(dev):
+    # v_proj kept bf16 (q|k int4): the strip plan runs q|k on the int4 strip GEMV and v on
+    # the bf16 GEMV into one fp32 split of the q|k|v partials; steps agree with the oracle
+    # and graph replays equal the eager steps bit for bit; other plans refuse the model
+    cfg = small_config()
+    model, ow = build_case(cfg, seed=13, dev=dev, v_keep=True)
+    with pytest.raises(ValueError):
+        FastDecoder(model, plan="staged")
+    dec = FastDecoder(model, plan="strip")
+    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    prompt = [5, 17, 999, 0, 42, 7]
+    okc, ovc = _oracle_caches(model)
+    o_logits = []
+    for p, t in enumerate(prompt):
+        lg, _, tok = D.decode_step(t, p, ow, okc, ovc, cos, sin, cfg.n_heads, cfg.n_kv_heads, 128)
+    tokens = []
+    for p in range(len(prompt), len(prompt) + 6):
+        tokens.append(tok)
+        lg, _, tok = D.decode_step(tok, p, ow, okc, ovc, cos, sin, cfg.n_heads, cfg.n_kv_heads, 128)
+        o_logits.append(lg)
+    dec.prefill(torch.tensor(prompt))
+    e_logits = []
+    for i in range(6):
+        dec.ids.fill_(tokens[i])                  # teacher-forced on the oracle's tokens
+        dec.run_step()
+        e_logits.append(dec.logits.clone())
+        err = rel_l2(fb(e_logits[i]), o_logits[i])
+        print(f"kept v step {i}: logits rel_l2={err:.2e}")
+        assert err < 1e-2
+    dec.prefill(torch.tensor(prompt))
+    dec.capture()
+    for i in range(6):
+        dec.ids.fill_(tokens[i])
+        dec.graph.replay()
+        assert torch.equal(dec.logits, e_logits[i]), f"replay {i} differs from eager"
+
+
 @pytest.mark.parametrize("plan", ["strip", "fused", "unfused"])
 def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
     # MOSS step: 33-way (here 1 + 4) embedding, layers, final norm, text + audio heads
