@@ -252,9 +252,9 @@ def bench_decode(args, torch):
     dev = torch.device("cuda:0")
     prompt_len = 256
     total = prompt_len + args.warmup + args.steps
-    cfg = BackboneConfig(max_seq=max(1536, ((total + 255) // 256) * 256))
+    cfg = BackboneConfig(max_seq=max(1536, ((total + 255) // 256) * 256), group_size=args.group)
     t0 = time.time()
-    model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev), dev)
+    model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev, v_keep=args.v_keep), dev)
     dec = FastDecoder(model, plan=args.plan)
     gen = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen)
@@ -297,9 +297,13 @@ def bench_decode(args, torch):
         gemv_us[name] = a_ev.elapsed_time(b_ev) * 1e3 / reps
     gu_us = gemv_us["gate_up"]
     gu_bytes = algo_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size, False)
+    nv = cfg.n_kv_heads * cfg.head_dim
     layer_bytes = sum(algo_bytes(1, k, n, cfg.group_size, True) for k, n in
-                      ((cfg.hidden, cfg.qkv_out), (cfg.hidden, cfg.hidden),
-                       (cfg.hidden, 2 * cfg.intermediate), (cfg.intermediate, cfg.hidden)))
+                      ((cfg.hidden, cfg.qkv_out - (nv if args.v_keep else 0)),
+                       (cfg.hidden, cfg.hidden), (cfg.hidden, 2 * cfg.intermediate),
+                       (cfg.intermediate, cfg.hidden)))
+    if args.v_keep:                       # the kept v_proj streams bf16 weights
+        layer_bytes += 2 * nv * cfg.hidden + 2 * cfg.hidden + 4 * nv
     avg_len = (prompt_len + args.warmup + 1 + final_pos) / 2
     kv_bytes = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim * 2 * avg_len
     step_bytes = cfg.n_layers * layer_bytes + 2 * cfg.vocab * cfg.hidden + kv_bytes
@@ -307,7 +311,8 @@ def bench_decode(args, torch):
     return dict(
         value=round(1000.0 / ms_step, 2), unit="steps/s", ms_per_step=ms_step, steps=args.steps,
         dtype="int4 GPTQ weights, bf16 activations, fp32 accumulate",
-        config={"workload": "36-layer Qwen3-8B-shaped int4 GPTQ backbone (act-order g128) + bf16 "
+        config={"workload": f"36-layer Qwen3-8B-shaped int4 GPTQ backbone (act-order g{cfg.group_size}"
+                            + (", v_proj kept bf16" if args.v_keep else "") + ") + bf16 "
                             "head 151936x4096, batch 1, prefill 256 random ids then hipGraph greedy "
                             f"decode, KV cache {prompt_len + args.warmup + 1}->{final_pos}",
                 "hidden": cfg.hidden, "layers": cfg.n_layers, "vocab": cfg.vocab,
@@ -324,7 +329,8 @@ def bench_decode(args, torch):
         roofline={"bound": "hbm", "achieved": round(gu_bytes / gu_us / 1e3, 1),
                   "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
-                  "traffic": profiled_traffic("gate_up", dec.plan),
+                  "traffic": (profiled_traffic("gate_up", dec.plan)
+                              if cfg.group_size == GROUP and not args.v_keep else None),
                   "kernel": GATE_UP_KERNEL.get(dec.plan, "gate_up 4096x24576 M=1")
                             + " (as launched in the decode step)",
                   "bytes_per_launch": gu_bytes},
@@ -446,6 +452,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--group", type=int, default=128, choices=[32, 64, 128, 256],
+                    help="int4 group size of every projection (decode workload)")
+    ap.add_argument("--v-keep", action="store_true",
+                    help="keep v_proj in bf16, as the shipped GPTQ presets do (decode workload)")
     ap.add_argument("--plan", default="strip",
                     choices=["strip", "fused", "staged", "partials", "unfused"],
                     help="decode launch plan (decode workload)")
