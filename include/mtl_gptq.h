@@ -56,7 +56,8 @@ enum {
   MTL_LAYOUT_ROWS = 0,    /* qweight int32 [K/8, N] as everywhere else                  */
   MTL_LAYOUT_TILED = 1,   /* mtl_w4_tile output (M = 1, N % 64 == 0, no perm)           */
   MTL_LAYOUT_STRIP = 2    /* mtl_w4_strip output (M = 1, N % 16 == 0, K % 256 == 0,
-                             K <= 16384, no perm): full-K strip GEMV, no split-K       */
+                             K <= 16384, no perm), with scales/qzeros in the strip order
+                             of mtl_w4_strip_meta: full-K strip GEMV, no split-K       */
 };
 
 /* Metadata format of mtl_w4_gemm_fused. */
@@ -153,6 +154,19 @@ int mtl_w4_tile(const int32_t* qweight, int64_t K, int64_t N, int32_t* tiled, in
 int64_t mtl_w4_strip_bytes(int64_t K, int64_t N);
 int mtl_w4_strip(const int32_t* qweight, int64_t K, int64_t N, int32_t* strip, int64_t strip_bytes,
                  void* stream);
+
+/*
+ * Strip-ordered copy of the group metadata for the strip GEMV (load time): for each
+ * 16-column strip and each 128-channel block (block pair at g = 256), the MB = 128/g
+ * scales of every column contiguously (fp16, MB = 1 at g = 256) and their zero nibbles
+ * (column c's MB nibbles at nibble c*MB of the record).  A permutation of scales
+ * [K/g, N] and of the qzeros nibbles: the outputs have the sizes of the inputs.  N % 16
+ * == 0, K % 256 == 0; outputs 16-byte aligned.  No reference counterpart (the reference's
+ * qsz tensor is torch's own layout).
+ */
+int mtl_w4_strip_meta(const void* scales, const int32_t* qzeros, int64_t K, int64_t N,
+                      int32_t group_size, void* strip_scales, int32_t* strip_zeros,
+                      void* stream);
 
 /*
  * Skinny-batch int4 GEMM over the strip layout: y[M, N] = x[M, K] @ dequant(W), 1 <= M <= 16,

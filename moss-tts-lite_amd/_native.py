@@ -90,6 +90,8 @@ _SIGNATURES = {
     "mtl_w4_tiled_bytes": (_i64, [_i64, _i64]),
     "mtl_w4_tile": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "mtl_w4_strip_bytes": (_i64, [_i64, _i64]),
+    "mtl_w4_strip_meta": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p,
+                                 _c_void_p]),
     "mtl_w4_strip": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "mtl_tune_set_reduce": (_i32, [_i32]),
     "mtl_tune_set_strip_nb": (_i32, [_i32]),

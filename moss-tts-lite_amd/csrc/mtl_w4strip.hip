@@ -135,28 +135,40 @@ w4_strip_kernel(StripArgs a) {
   //      Loads complete in issue order, so waiting for block b never waits for a later
   //      one, and the unpack and MFMA work overlaps the rest of the stream.
   constexpr int MB = GR <= 4 ? 4 / GR : 1;     // groups starting in one block
-  const int grp0 = item0 * 8 / a.group;
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / kStripCols) * a.kblocks * 1024),
       0x00020000);
   const int blk0 = s * a.kblocks + ks * NB;
-  // metadata through buffer loads too: a uniform (SGPR) row offset per group and one
-  // per-lane column offset, so no 64-bit address is held per group
+  // Metadata in the strip order of mtl_w4_strip_meta: record (s * KR + i) per block
+  // (per block pair at g = 256) holds the MB scales of each of the strip's 16 columns
+  // contiguously (fp16) and their zero nibbles, so a lane loads its column's metadata
+  // of a block with one scale load and one zero load (a uniform record offset and one
+  // per-lane offset).
   const int ngroups = a.K / a.group;
+  const int krec = GR == 8 ? a.kblocks >> 1 : a.kblocks;     // records per strip
+  const int rec0 = s * krec + (GR == 8 ? (ks * NB) >> 1 : ks * NB);
   const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.scales), (short)0, ngroups * N * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 3) * 4, 0x00020000);
+      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
   u32x4 wq[WIN];
-  uint32_t ms[WIN][MB], mz[WIN][MB];
+  uint32_t ms[WIN][MB == 4 ? 2 : 1], mz[WIN];
   // block b into ring slot r (r = b % WIN, a compile-time index at every call)
   auto issue = [&](int r, int b) {
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      if (GR <= 4 || (r & 1) == 0) {           // g = 256: one group per block pair (b, r alike in parity)
-        const int g = grp0 + (GR <= 4 ? b * MB + m : b >> 1);
-        ms[r][m] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, col * 2, g * N * 2, 0);
-        mz[r][m] = __builtin_amdgcn_raw_buffer_load_b32(zrsrc, (col >> 3) * 4, g * (N >> 3) * 4, 0);
+    if (GR <= 4 || (r & 1) == 0) {             // g = 256: one record per block pair (b, r alike in parity)
+      const int rec = rec0 + (GR == 8 ? b >> 1 : b);
+      if (MB == 4) {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                      srsrc, lj * 8, rec * 128, 0));
+        ms[r][0] = v.x;
+        ms[r][MB == 4 ? 1 : 0] = v.y;
+        mz[r] = __builtin_amdgcn_raw_buffer_load_b16(zrsrc, lj * 2, rec * 32, 0);
+      } else if (MB == 2) {
+        ms[r][0] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, lj * 4, rec * 64, 0);
+        mz[r] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj, rec * 16, 0);
+      } else {
+        ms[r][0] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, lj * 2, rec * 32, 0);
+        mz[r] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj >> 1, rec * 8, 0);
       }
     }
     wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -233,10 +245,11 @@ w4_strip_kernel(StripArgs a) {
       const int b = b0 + r;
       const u32x4 w4 = wq[r];
       float gs[MB], gz[MB];                     // scale and 128 + zero of the block's groups
+      const uint32_t zsh = MB == 1 ? (lj & 1) * 4 : 0;
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
-        gs[m] = f16_to_f32(ms[r][m] & 0xffffu);
-        gz[m] = (float)(128 + (int)((mz[r][m] >> ((col & 7) * 4)) & 0xfu) + a.zero_offset);
+        gs[m] = f16_to_f32((ms[r][m >> 1] >> (16 * (m & 1))) & 0xffffu);
+        gz[m] = (float)(128 + (int)((mz[r] >> (zsh + 4 * m)) & 0xfu) + a.zero_offset);
       }
       if (GR == 8 && (r & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
       // keep the compiler from hoisting later ring loads (and their registers) above here:
@@ -442,11 +455,65 @@ __global__ void strip_weights_kernel(const uint32_t* __restrict__ qw, int64_t K,
   }
 }
 
+// Strip metadata (see the strip GEMV): thread t handles record rec = t / 8 (block, or block
+// pair at g = 256, of strip s = rec / KR) and columns 2*(t%8), +1 of the strip.
+__global__ void strip_meta_kernel(const uint16_t* __restrict__ scales,
+                                  const uint32_t* __restrict__ qzeros, int64_t N, int64_t krec,
+                                  int64_t nrec, int mb, int pair, uint16_t* __restrict__ sc_out,
+                                  uint8_t* __restrict__ z_out) {
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < nrec * 8;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rec = t >> 3, cp = t & 7;
+    const int64_t s = rec / krec, i = rec % krec;
+    uint32_t zbits[2] = {0u, 0u};
+    for (int h = 0; h < 2; ++h) {
+      const int64_t c = 2 * cp + h, n = kStripCols * s + c;
+      for (int m = 0; m < mb; ++m) {
+        const int64_t g = pair ? i : i * mb + m;
+        sc_out[(rec * kStripCols + c) * mb + m] = scales[g * N + n];
+        const uint32_t z = (qzeros[g * (N >> 3) + (n >> 3)] >> (4 * (n & 7))) & 0xfu;
+        zbits[h] |= z << (4 * m);
+      }
+    }
+    if (mb == 4) {
+      reinterpret_cast<uint16_t*>(z_out)[rec * 16 + 2 * cp] = (uint16_t)zbits[0];
+      reinterpret_cast<uint16_t*>(z_out)[rec * 16 + 2 * cp + 1] = (uint16_t)zbits[1];
+    } else if (mb == 2) {
+      z_out[rec * 16 + 2 * cp] = (uint8_t)zbits[0];
+      z_out[rec * 16 + 2 * cp + 1] = (uint8_t)zbits[1];
+    } else {
+      z_out[rec * 8 + cp] = (uint8_t)(zbits[0] | (zbits[1] << 4));
+    }
+  }
+}
+
 }  // namespace mtl
 
 using namespace mtl;
 
 extern "C" {
+
+int mtl_w4_strip_meta(const void* scales, const int32_t* qzeros, int64_t K, int64_t N,
+                      int32_t group_size, void* strip_scales, int32_t* strip_zeros,
+                      void* stream) {
+  if (!scales || !qzeros || !strip_scales || !strip_zeros) return MTL_ERR_INVALID_ARG;
+  if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
+    return MTL_ERR_GROUP;
+  if (!mtl_w4_strip_bytes(K, N) || K % group_size != 0) return MTL_ERR_SHAPE;
+  if (!aligned16(strip_scales) || !aligned16(strip_zeros)) return MTL_ERR_ALIGN;
+  const int pair = group_size == 256;
+  const int mb = pair ? 1 : 128 / group_size;
+  const int64_t krec = pair ? K / 256 : K / 128;
+  const int64_t nrec = (N / kStripCols) * krec;
+  int blocks = (int)((nrec * 8 + 255) / 256);
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(strip_meta_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint16_t*>(scales),
+                     reinterpret_cast<const uint32_t*>(qzeros), N, krec, nrec, mb, pair,
+                     static_cast<uint16_t*>(strip_scales),
+                     reinterpret_cast<uint8_t*>(strip_zeros));
+  return launch_status();
+}
 
 int64_t mtl_w4_strip_bytes(int64_t K, int64_t N) {
   if (K <= 0 || N <= 0 || N % kStripCols != 0 || K % (2 * kStripBlockK) != 0) return 0;

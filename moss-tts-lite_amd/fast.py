@@ -169,6 +169,8 @@ class FastDecoder:
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
         _, qz, sc, _ = lin.kernel_args()
         qw, layout = lin.stream_weight(self.strip_gemv[name])
+        if layout == N.LAYOUT_STRIP:
+            sc, qz = lin.strip_meta()
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
@@ -310,6 +312,7 @@ class FastDecoder:
     def _norm_silu(self, h_ord, w_ord, lin):
         _, qz, sc, _ = lin.kernel_args()
         qw, layout = lin.stream_weight(True)
+        sc, qz = lin.strip_meta()
         return ("mtl_w4_gemm_norm_silu",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
@@ -319,6 +322,8 @@ class FastDecoder:
     def _residual(self, x, xpart_name, lin, scatter, h_ord):
         _, qz, sc, _ = lin.kernel_args()
         qw, layout = lin.stream_weight(self.strip)
+        if layout == N.LAYOUT_STRIP:
+            sc, qz = lin.strip_meta()
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         return ("mtl_w4_gemm_residual",
@@ -331,6 +336,8 @@ class FastDecoder:
     def _norm_partials(self, h_ord, w_ord, lin, n, name, strip=None):
         _, qz, sc, _ = lin.kernel_args()
         qw, layout = lin.stream_weight(self.strip_gemv[name] if strip is None else strip)
+        if layout == N.LAYOUT_STRIP:
+            sc, qz = lin.strip_meta()
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),

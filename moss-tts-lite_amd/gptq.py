@@ -52,6 +52,7 @@ class GPTQLinear(torch.nn.Module):
         self._perm: torch.Tensor | None = None
         self._tiled: torch.Tensor | None = None
         self._strip: torch.Tensor | None = None
+        self._strip_meta: tuple | None = None
 
     @classmethod
     def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
@@ -110,6 +111,12 @@ class GPTQLinear(torch.nn.Module):
             self._tiled = ops.tile_weights(qw)
         return self._tiled, N.LAYOUT_TILED
 
+    def strip_meta(self):
+        """``(scales, qzeros)`` in the strip order the strip GEMV reads (built once)."""
+        if self._strip_meta is None:
+            self._strip_meta = ops.strip_meta(self.scales, self.qzeros, self.group_size)
+        return self._strip_meta
+
     def drop_original(self) -> None:
         """Free the unsorted ``qweight`` once the sorted copy exists (load-time memory)."""
         if self._perm is not None:
@@ -127,7 +134,7 @@ class GPTQLinear(torch.nn.Module):
             raise ValueError("cols must list every output column once")
         if self._kernel_qweight is None:
             self.post_init()
-        self._tiled = self._strip = None
+        self._tiled = self._strip = self._strip_meta = None
         sorted_separately = self._kernel_qweight is not self.qweight
         self._kernel_qweight = self._kernel_qweight[:, cols].contiguous()
         if sorted_separately and self.qweight.numel():

@@ -205,6 +205,21 @@ def strip_weights(qweight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def strip_meta(scales: torch.Tensor, qzeros: torch.Tensor, group_size: int):
+    """Strip-ordered copies of ``scales [K/g, N]`` (fp16) and ``qzeros [K/g, N/8]`` for the
+    strip GEMV (``mtl_w4_strip_meta``); same sizes as the inputs."""
+    if scales.dtype != torch.float16 or qzeros.dtype != torch.int32:
+        raise RuntimeError("scales must be float16 and qzeros int32")
+    g, n = scales.shape
+    k = g * group_size
+    sc = torch.empty_like(scales)
+    qz = torch.empty_like(qzeros)
+    N.check(N.load().mtl_w4_strip_meta(scales.contiguous().data_ptr(), qzeros.contiguous().data_ptr(),
+                                       k, n, group_size, sc.data_ptr(), qz.data_ptr(),
+                                       _stream(scales.device)), "mtl_w4_strip_meta")
+    return sc, qz
+
+
 def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.Tensor,
                     scales: torch.Tensor, n: int, group_size: int, zero_offset: int = 0,
                     out: torch.Tensor | None = None,

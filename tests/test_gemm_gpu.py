@@ -470,12 +470,44 @@ def test_strip_layout_bit_exact(dev, k, n):
     assert np.array_equal(out, _strip_np(qw))
 
 
+def _strip_meta_np(scales_bits, qzeros, k, n, g):
+    """The strip order of the group metadata, restated: per strip and 128-channel block
+    (block pair at g = 256) the scales of each column contiguously, and the zero nibbles
+    of each column packed in column order."""
+    z = np.stack([(qzeros.view(np.uint32) >> (4 * j)) & 0xF for j in range(8)], -1)
+    z = z.reshape(k // g, n)
+    pair = g == 256
+    mb = 1 if pair else 128 // g
+    krec = k // 256 if pair else k // 128
+    sc_out, z_nib = [], []
+    for s_ in range(n // 16):
+        for i in range(krec):
+            grp = [i] if pair else [i * mb + m for m in range(mb)]
+            for c in range(16):
+                col = 16 * s_ + c
+                sc_out += [scales_bits[gg, col] for gg in grp]
+                z_nib += [z[gg, col] for gg in grp]
+    z_nib = np.array(z_nib, np.uint32)
+    packed = (z_nib[0::2] | (z_nib[1::2] << 4)).astype(np.uint8)
+    return np.array(sc_out, np.uint16), packed
+
+
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+def test_strip_meta_layout_bit_exact(dev, group):
+    k, n = 1024, 96
+    case = synth.gptq_case(k=k, n=n, m=1, group=group, seed=group, with_ref=False)
+    sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), group)
+    ref_sc, ref_z = _strip_meta_np(case["scales"].view(np.uint16), case["qzeros"], k, n, group)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16).reshape(-1), ref_sc)
+    assert np.array_equal(qz.cpu().numpy().view(np.uint8).reshape(-1), ref_z)
+
+
 def _strip_partials(lib, case, dev, src, x=None, xp=None, h=None, wn=None, slots=None):
     """One strip launch through the partials (or norm-partials) entry: fp32 [N]."""
     import ctypes
     k, n, g = case["k"], case["n"], case["group"]
     qw = ops.strip_weights(t_i32(case["qweight"], dev))
-    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), case["group"])
     y = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     if src == "norm":
@@ -569,7 +601,7 @@ def test_strip_residual_epilogue(dev, src):
     h0f = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(n).astype(np.float32)))
     scatter = torch.from_numpy(r.permutation(n).astype(np.int32)).to(dev)
     qw = ops.strip_weights(t_i32(case["qweight"], dev))
-    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), case["group"])
     st = torch.cuda.current_stream().cuda_stream
     for rep in range(2):
         h = t_bf16(f32_to_bf16_bits(h0f), dev)
@@ -658,7 +690,7 @@ def test_strip_norm_silu_epilogue(dev, n, ct, nb):
     h, wn = t_bf16(f32_to_bf16_bits(hf), dev), t_bf16(f32_to_bf16_bits(wf), dev)
     slots = torch.from_numpy(slots16(hf)).to(dev)
     qw = ops.strip_weights(t_i32(case["qweight"], dev))
-    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), case["group"])
     act = torch.zeros(n // 2, dtype=torch.bfloat16, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     assert lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
