@@ -188,6 +188,38 @@ int mtl_w4_gemm_strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K,
                            int32_t zero_offset, void* y, int64_t ldy, int32_t out_dtype,
                            void* stream);
 
+/*
+ * Prompt-length int4 GEMM over the strip layout: y[M, N] = x[M, K] @ dequant(W) for any
+ * M >= 1, fp32 accumulation on MFMA, no workspace.  The reference's quantized prefill
+ * runs every projection at M = prompt length through torch._weight_int4pack_mm
+ * (moss_tts_lite/fast.py:218-270, via _linear at fast.py:107-121); this entry serves
+ * those products.
+ *   x             bf16 [M, K], rows ldx elements apart (16-byte aligned, ldx % 8 == 0), in
+ *                 the weight's input (act-order sorted) channel order
+ *   strip_weight  mtl_w4_strip output; strip_scales/strip_zeros the mtl_w4_strip_meta
+ *                 outputs of the same linear; zero_offset as mtl_gptq_gemm
+ *   epilogue      MTL_EPI_NONE: y [M, N] bf16 or f32 (out_dtype);
+ *                 MTL_EPI_RESIDUAL: y is the bf16 residual stream [M, N], updated in place
+ *                 as y = bf16(bf16(acc) + y) (fast.py:243, 246-248);
+ *                 MTL_EPI_SILU_MUL: N columns interleaved gate|up in blocks of 32, y bf16
+ *                 [M, N/2] = bf16(silu(bf16 gate) * bf16 up) (fast.py:247)
+ *                 (the two epilogues need out_dtype MTL_OUT_BF16)
+ *   ldy           row pitch of y in elements (>= N, or N/2 for MTL_EPI_SILU_MUL)
+ *   workspace     NULL, or mtl_w4_gemm_prefill_workspace_bytes(M, K, N) bytes (16-byte
+ *                 aligned, no initialisation): when the grid alone would leave CUs idle, K
+ *                 is split over workgroups whose fp32 partial sums a second launch adds in
+ *                 split order before the epilogue (results then differ from the one-pass
+ *                 launch by fp32 rounding); a smaller or NULL workspace runs one pass.
+ *                 The workspace size query returns 0 when no split is needed.
+ * K % 256 == 0, N % 128 == 0, K % group_size == 0, group_size 32/64/128/256.
+ */
+int64_t mtl_w4_gemm_prefill_workspace_bytes(int64_t M, int64_t K, int64_t N);
+int mtl_w4_gemm_prefill(const void* x, int64_t M, int64_t ldx, int64_t K,
+                        const int32_t* strip_weight, const void* strip_scales,
+                        const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                        int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
+                        int64_t ldy, float* workspace, int64_t ws_bytes, void* stream);
+
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
                      void* stream);

@@ -84,6 +84,10 @@ _SIGNATURES = {
                                          _c_void_p, _i64, _c_void_p]),
     "mtl_w4_gemm_strip_rows": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _i64, _i32, _i32, _c_void_p, _i64, _i32, _c_void_p]),
+    "mtl_w4_gemm_prefill": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                   _i64, _i32, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p,
+                                   _i64, _c_void_p]),
+    "mtl_w4_gemm_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "mtl_w4_gemm_norm_silu": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                      _c_void_p, _c_void_p]),

@@ -60,6 +60,19 @@ __device__ __forceinline__ u32x4 pair_order(u32x4 v, float& sum) {
   return u32x4{e0 | (e4 << 16), e1 | (e5 << 16), e2 | (e6 << 16), e3 | (e7 << 16)};
 }
 
+// The same pair order with v_perm_b32 (one per output word) and the item's sum as a chain
+// of four v_dot2_f32_bf16 against (1, 1): cheaper, and the sum's rounding differs from
+// pair_order's fixed tree (a kernel uses one of the two throughout).
+__device__ __forceinline__ u32x4 pair_order_dot(u32x4 v, float& sum) {
+  const uint32_t ones = 0x3f803f80u;    // bf16 (1, 1)
+  sum = dot2_bf16(v.x, ones, 0.f);
+  sum = dot2_bf16(v.y, ones, sum);
+  sum = dot2_bf16(v.z, ones, sum);
+  sum = dot2_bf16(v.w, ones, sum);
+  return u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+               __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
 // x = bf16(w * bf16(h * r)) on 8 packed bf16 values (RMSNorm, model.py:34-40), two values
 // per v_cvt_pk_bf16_f32.  The result is an MFMA operand, so NaN bits are not normalised.
 __device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {

@@ -1,0 +1,452 @@
+// int4 GEMM over full-K column strips at prompt length for gfx950: y[M, N] = x[M, K] @ W
+// for any M (the prefill's projections, moss_tts_lite/fast.py:218-270, where every linear
+// runs at M = prompt length).
+//
+// Weights are the strip layout of the decode GEMV (mtl_w4strip.hip): 1 KB block
+// (s * K/128 + b) holds columns 16s..16s+15 over input channels 128b..128b+127, lane l's
+// 16 bytes being the B operands (codes as bf16 128 + q) of four v_mfma_f32_16x16x32_bf16
+// over the block's four 32-channel chunks.  Group metadata is in the strip order of
+// mtl_w4_strip_meta.  Per quantisation group the MFMA sums A = sum x * (128 + q) exactly in
+// fp32 and the group adds s * (A - (128 + z) * X) with X the group's sum of x, as in the
+// decode GEMV.
+//
+// A workgroup (4 waves) owns a tile of 64 x rows by 8 strips (128 columns); wave w serves
+// strips 2w and 2w+1 for all 64 rows (4 MFMA row tiles), so one unpacked B operand feeds 4
+// MFMAs and one A operand read from LDS feeds 2.  The K loop walks 128-channel blocks:
+// the x tile of block b + 1 (64 rows x 128 channels, in the pair order the code unpack
+// produces, with its per-group sums) is loaded while block b is multiplied and goes to
+// the other of two LDS buffers, one barrier per block; each wave keeps D blocks of its
+// two strips' weights and metadata in flight in a register ring.  The grid is (N / 128)
+// x (M / 64): with N / 128 a multiple of 8, the row tiles of one column tile run on one
+// XCD, so its weights are fetched into one L2.
+#include "mtl_w4core.h"
+
+namespace mtl {
+
+constexpr int kPfRows = 64;                      // x rows per workgroup
+constexpr int kPfWaves = 4;
+constexpr int kPfStrips = 2 * kPfWaves;          // 128 columns per workgroup
+constexpr int kPfCols = 16 * kPfStrips;
+constexpr int kPfPitch = 17;                     // LDS items per x row: 16 + 1 (banks)
+constexpr int kPfWavesPerEU = 3;                 // 168 VGPRs: 3 workgroups per CU
+constexpr int kPfRing = 2;                       // weight blocks in flight per wave
+constexpr int kPfMaxSplits = 8;
+
+struct PrefillArgs {
+  const uint16_t* x;          // bf16 [M, K], rows ldx apart, in the weight's input order
+  const u32x4* w;             // strip layout
+  const uint16_t* scales;     // strip-ordered fp16 scales
+  const uint32_t* qzeros;     // strip-ordered zero nibbles
+  void* y;                    // see the epilogues
+  float* part;                // splits > 1: fp32 partial sums [splits][M][N]
+  int64_t ldx, ldy;
+  int M, K, N, group, zero_offset, kblocks, out_f32;
+  int splits, kps;            // K splits (blockIdx.z) of kps blocks each
+};
+
+// Sum over aligned groups of G lanes (G = 4, 8 or 16) with DPP row permutations:
+// quad swaps, then the mirror within 8 and within 16 lanes.  Every lane of a group ends
+// with the group's sum (a + b and b + a round alike).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               CTRL, 0xf, 0xf, false));
+}
+
+template <int G>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
+  v += dpp_f32<0xB1>(v);                 // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);                 // quad_perm [2, 3, 0, 1]
+  if (G >= 8) v += dpp_f32<0x141>(v);    // row_half_mirror
+  if (G >= 16) v += dpp_f32<0x140>(v);   // row_mirror
+  return v;
+}
+
+template <int GR, int EPI>
+__global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEU)))
+w4_prefill_kernel(PrefillArgs a) {
+  constexpr int MB = GR <= 4 ? 4 / GR : 1;       // groups starting in one block
+  constexpr int GI = GR <= 4 ? 4 * GR : 16;      // x items per staged sum
+  constexpr int D = kPfRing;
+  static_assert(D % 2 == 0, "ring turns hold whole block pairs (g = 256)");
+  __shared__ u32x4 xa[2][kPfRows * kPfPitch];    // x tile: [row][item] in pair order
+  __shared__ float xs[2][MB][kPfRows];           // its group sums (g = 256: block sums)
+
+  const int t = threadIdx.x, lane = t & 63, wave = wave_id();
+  const int lg = lane >> 4, lj = lane & 15;
+  const int row0 = blockIdx.y * kPfRows;
+  const int kb = a.kblocks;
+  const int kb0 = blockIdx.z * a.kps, kb1 = kb0 + a.kps;   // this split's blocks (kps even)
+  const int N = a.N;
+  const int sA = blockIdx.x * kPfStrips + 2 * wave;   // this wave's strips sA, sA + 1
+
+  // x staging: thread t stages items t + 256 r (r = 0..3) of the tile: row (t >> 4) + 16 r,
+  // item t & 15 (channels 8 (t & 15) .. +7 of the block), through a bounds-checked buffer
+  // resource over the M rows, so rows at or past M stage zeros.
+  const int srow = t >> 4, sitem = t & 15;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x + (size_t)row0 * a.ldx), (short)0,
+      (int)(((int64_t)(a.M - row0) - 1) * a.ldx * 2 + (int64_t)a.K * 2), 0x00020000);
+  const int xoff = (int)(srow * a.ldx * 2) + 16 * sitem;
+  const int xrstep = (int)(16 * a.ldx * 2);      // 16 rows, a uniform offset
+  u32x4 xv[4];
+  auto x_load = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      xv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            xrsrc, xoff, r * xrstep + b * 256, 0));
+  };
+  auto x_store = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float sum;
+      const u32x4 pv = pair_order_dot(xv[r], sum);
+      sum = row_sum<GI>(sum);
+      xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
+      if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
+    }
+  };
+
+  // Weight ring: block b of both strips and the metadata records it starts go to slot
+  // b % D; a slot is refilled as soon as its block is unpacked.
+  const int ngroups = a.K / a.group;
+  const int krec = GR == 8 ? kb >> 1 : kb;       // metadata records per strip
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / 16) * kb * 1024), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.scales), (short)0, ngroups * N * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
+  u32x4 wq[D][2];
+  uint32_t ms[D][2][MB == 4 ? 2 : 1], mz[D][2];
+  auto issue = [&](int r, int b) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int strip = sA + s;
+      if (GR <= 4 || (r & 1) == 0) {
+        const int rec = strip * krec + (GR == 8 ? b >> 1 : b);
+        if (MB == 4) {
+          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                        srsrc, lj * 8, rec * 128, 0));
+          ms[r][s][0] = v.x;
+          ms[r][s][MB == 4 ? 1 : 0] = v.y;
+          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b16(zrsrc, lj * 2, rec * 32, 0);
+        } else if (MB == 2) {
+          ms[r][s][0] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, lj * 4, rec * 64, 0);
+          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj, rec * 16, 0);
+        } else {
+          ms[r][s][0] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, lj * 2, rec * 32, 0);
+          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj >> 1, rec * 8, 0);
+        }
+      }
+      wq[r][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               wrsrc, lane * 16, (strip * kb + b) * 1024, 0));
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < D; ++r) issue(r, kb0 + r);
+  x_load(kb0);
+  x_store(0);
+  x_load(kb0 + 1);
+  __syncthreads();
+
+  const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
+  const uint32_t kLo = vgpr_const(0x000F000Fu);
+  const floatx4 zero4{0.f, 0.f, 0.f, 0.f};
+  floatx4 tot[4][2];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) { tot[tt][0] = zero4; tot[tt][1] = zero4; }
+  // Chunks per correction: a group (g <= 128), or a block at g = 256, whose group's two
+  // blocks are folded one after the other with the pair's scale and zero.
+  constexpr int GC = GR <= 4 ? GR : 4;
+  float gs[2][MB], gz[2][MB];
+
+  for (int b0 = kb0; b0 < kb1; b0 += D) {
+#pragma unroll
+    for (int r = 0; r < D; ++r) {
+      const int b = b0 + r;
+      const int buf = r & 1;                     // b0 - kb0 and kb0 are even
+      if (GR <= 4 || (r & 1) == 0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const uint32_t zsh = MB == 1 ? (lj & 1) * 4 : 0;
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            gs[s][m] = f16_to_f32((ms[r][s][m >> 1] >> (16 * (m & 1))) & 0xffffu);
+            gz[s][m] = (float)(128 + (int)((mz[r][s] >> (zsh + 4 * m)) & 0xfu) + a.zero_offset);
+          }
+        }
+      }
+      bf16x8_t B[2][4];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 w = wq[r][s];
+        B[s][0] = unpack_codes8(w.x, kLo, kMagic);
+        B[s][1] = unpack_codes8(w.y, kLo, kMagic);
+        B[s][2] = unpack_codes8(w.z, kLo, kMagic);
+        B[s][3] = unpack_codes8(w.w, kLo, kMagic);
+      }
+      // keep the refill below the unpack (IR and machine scheduling)
+      asm volatile("" ::: "memory");
+      issue(r, b + D < kb1 ? b + D : kb1 - 1);   // unconditional refill (clamped)
+      __builtin_amdgcn_sched_barrier(0);
+      // Row tile by row tile, so one accumulator pair is live at a time.
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        floatx4 acc0, acc1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int q = j % GC;
+          const bf16x8_t A =
+              __builtin_bit_cast(bf16x8_t, xa[buf][(16 * tt + lj) * kPfPitch + 4 * j + lg]);
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[0][j], q == 0 ? zero4 : acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[1][j], q == 0 ? zero4 : acc1, 0, 0, 0);
+          if (q == GC - 1) {                     // fold the group into tot
+            const int m = GR <= 4 ? j / GR : 0;
+            const float4 X4 = *reinterpret_cast<const float4*>(&xs[buf][m][16 * tt + 4 * lg]);
+            const float X[4] = {X4.x, X4.y, X4.z, X4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              tot[tt][0][i] = fmaf(gs[0][m], fmaf(-gz[0][m], X[i], acc0[i]), tot[tt][0][i]);
+              tot[tt][1][i] = fmaf(gs[1][m], fmaf(-gz[1][m], X[i], acc1[i]), tot[tt][1][i]);
+            }
+          }
+        }
+        // pin the tile's corrections here: the next tile's LDS reads (and so its MFMAs)
+        // cannot move above a volatile asm that reads tot and clobbers memory
+        asm volatile("" ::"v"(tot[tt][0]), "v"(tot[tt][1]) : "memory");
+      }
+      // block b + 1 (loaded during block b - 1) into the other buffer, then block b + 2
+      // into registers (the last blocks reload the last block, unused)
+      __builtin_amdgcn_sched_barrier(0);
+      x_store(buf ^ 1);
+      x_load(b + 2 < kb1 ? b + 2 : kb1 - 1);
+      __syncthreads();
+    }
+  }
+
+  // Epilogue: tot[tt][s][i] is row row0 + 16 tt + 4 lg + i, column 16 (sA + s) + lj.
+  if (a.splits > 1) {                            // partial sums; prefill_reduce_kernel finishes
+    float* pz = a.part + (size_t)blockIdx.z * a.M * N;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 16 * tt + 4 * lg + i;
+          if (row < a.M) pz[(size_t)row * N + 16 * (sA + s) + lj] = tot[tt][s][i];
+        }
+    return;
+  }
+  if (EPI == MTL_EPI_SILU_MUL) {
+    // Strips 8c .. 8c+7 are two 64-column gate|up blocks (32 gate | 32 up columns each):
+    // waves 0 and 2 hold gate strips, waves 1 and 3 their up partners.  The up values
+    // meet the gate values in LDS (the x buffers, free after the last barrier).
+    float* ut = reinterpret_cast<float*>(&xa[0][0]);    // [2][2][4][4][64]
+    const int pair = wave >> 1;
+    if (wave & 1) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ut[(((pair * 2 + s) * 4 + tt) * 4 + i) * 64 + lane] = tot[tt][s][i];
+    }
+    __syncthreads();
+    if (wave & 1) return;
+    uint16_t* act = static_cast<uint16_t*>(a.y);
+    const int jb = 2 * blockIdx.x + pair;                // 32-column SwiGLU output block
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 16 * tt + 4 * lg + i;
+          const float u = ut[(((pair * 2 + s) * 4 + tt) * 4 + i) * 64 + lane];
+          if (row < a.M)
+            act[(size_t)row * a.ldy + 32 * jb + 16 * s + lj] = (uint16_t)silu_mul_bf16(tot[tt][s][i], u);
+        }
+    return;
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int col = 16 * (sA + s) + lj;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + 16 * tt + 4 * lg + i;
+        if (row >= a.M) continue;
+        const size_t o = (size_t)row * a.ldy + col;
+        const float v = tot[tt][s][i];
+        if (EPI == MTL_EPI_RESIDUAL) {
+          uint16_t* h = static_cast<uint16_t*>(a.y);
+          // h = bf16(bf16(acc) + h) (fast.py:168-171 on prompt rows)
+          h[o] = (uint16_t)f32_to_bf16(round_bf16(v) + bf16_to_f32(h[o]));
+        } else if (a.out_f32) {
+          static_cast<float*>(a.y)[o] = v;
+        } else {
+          static_cast<uint16_t*>(a.y)[o] = (uint16_t)f32_to_bf16(v);
+        }
+      }
+  }
+}
+
+// Sums the K-split partials in split order and applies the epilogue; thread t handles 4
+// consecutive output columns of one row (SiLU*up: 4 SwiGLU columns, from their gate and up
+// partials 32 columns apart).
+template <int EPI>
+__global__ void __launch_bounds__(256) prefill_reduce_kernel(PrefillArgs a) {
+  const int N = a.N;
+  const int ncols = EPI == MTL_EPI_SILU_MUL ? N / 2 : N;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = idx / (ncols / 4);
+  if (row >= a.M) return;
+  const int c = (int)(idx % (ncols / 4)) * 4;      // first output column
+  const size_t plane = (size_t)a.M * N;
+  const float* base = a.part + (size_t)row * N;
+  if (EPI == MTL_EPI_SILU_MUL) {
+    const int g = 64 * (c >> 5) + (c & 31);          // gate column; up is 32 to the right
+    float4 gs = *reinterpret_cast<const float4*>(base + g);
+    float4 us = *reinterpret_cast<const float4*>(base + g + 32);
+    for (int z = 1; z < a.splits; ++z) {
+      const float4 gv = *reinterpret_cast<const float4*>(base + z * plane + g);
+      const float4 uv = *reinterpret_cast<const float4*>(base + z * plane + g + 32);
+      gs.x += gv.x; gs.y += gv.y; gs.z += gv.z; gs.w += gv.w;
+      us.x += uv.x; us.y += uv.y; us.z += uv.z; us.w += uv.w;
+    }
+    uint16_t* act = static_cast<uint16_t*>(a.y) + (size_t)row * a.ldy + c;
+    act[0] = (uint16_t)silu_mul_bf16(gs.x, us.x);
+    act[1] = (uint16_t)silu_mul_bf16(gs.y, us.y);
+    act[2] = (uint16_t)silu_mul_bf16(gs.z, us.z);
+    act[3] = (uint16_t)silu_mul_bf16(gs.w, us.w);
+    return;
+  }
+  float4 v = *reinterpret_cast<const float4*>(base + c);
+  for (int z = 1; z < a.splits; ++z) {
+    const float4 p = *reinterpret_cast<const float4*>(base + z * plane + c);
+    v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+  }
+  const float y[4] = {v.x, v.y, v.z, v.w};
+  const size_t o = (size_t)row * a.ldy + c;
+  for (int e = 0; e < 4; ++e) {
+    if (EPI == MTL_EPI_RESIDUAL) {
+      uint16_t* h = static_cast<uint16_t*>(a.y);
+      h[o + e] = (uint16_t)f32_to_bf16(round_bf16(y[e]) + bf16_to_f32(h[o + e]));
+    } else if (a.out_f32) {
+      static_cast<float*>(a.y)[o + e] = y[e];
+    } else {
+      static_cast<uint16_t*>(a.y)[o + e] = (uint16_t)f32_to_bf16(y[e]);
+    }
+  }
+}
+
+// K splits for a launch of `tiles` workgroups over kb blocks: enough splits for about two
+// workgroups per CU, each split a whole number of ring turns (kPfRing blocks), at most
+// kPfMaxSplits.
+static int prefill_splits(int64_t tiles, int64_t kb, int cus) {
+  int s = 1;
+  while (s < kPfMaxSplits && tiles * s < 2 * cus) ++s;
+  while (s > 1 && kb % ((int64_t)s * kPfRing) != 0) --s;
+  return s;
+}
+
+static int g_pf_cus = 0;
+
+static int pf_device_cus() {
+  if (!g_pf_cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_pf_cus = n;
+  }
+  return g_pf_cus;
+}
+
+template <int GR, int EPI>
+static void prefill_launch(const PrefillArgs& a, hipStream_t st) {
+  const dim3 grid(a.N / kPfCols, (a.M + kPfRows - 1) / kPfRows, a.splits), block(64 * kPfWaves);
+  hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI>), grid, block, 0, st, a);
+  if (a.splits > 1) {
+    const int64_t ncols = EPI == MTL_EPI_SILU_MUL ? a.N / 2 : a.N;
+    const int64_t threads = (int64_t)a.M * (ncols / 4);
+    hipLaunchKernelGGL(prefill_reduce_kernel<EPI>, dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, st, a);
+  }
+}
+
+template <int GR>
+static void prefill_epi(const PrefillArgs& a, int epilogue, hipStream_t st) {
+  if (epilogue == MTL_EPI_RESIDUAL) prefill_launch<GR, MTL_EPI_RESIDUAL>(a, st);
+  else if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL>(a, st);
+  else prefill_launch<GR, MTL_EPI_NONE>(a, st);
+}
+
+}  // namespace mtl
+
+using namespace mtl;
+
+extern "C" {
+
+int64_t mtl_w4_gemm_prefill_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M < 1 || K < 256 || K % 256 != 0 || N < kPfCols || N % kPfCols != 0) return 0;
+  const int s = prefill_splits((N / kPfCols) * ((M + kPfRows - 1) / kPfRows), K / 128,
+                               pf_device_cus());
+  return s > 1 ? (int64_t)s * M * N * 4 : 0;
+}
+
+int mtl_w4_gemm_prefill(const void* x, int64_t M, int64_t ldx, int64_t K,
+                        const int32_t* strip_weight, const void* strip_scales,
+                        const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                        int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
+                        int64_t ldy, float* workspace, int64_t ws_bytes, void* stream) {
+  if (!x || !strip_weight || !strip_scales || !strip_zeros || !y) return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL)
+    return MTL_ERR_INVALID_ARG;
+  if (out_dtype != MTL_OUT_BF16 && out_dtype != MTL_OUT_F32) return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && out_dtype != MTL_OUT_BF16) return MTL_ERR_INVALID_ARG;
+  if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
+    return MTL_ERR_GROUP;
+  const int64_t ncols = epilogue == MTL_EPI_SILU_MUL ? N / 2 : N;
+  if (M < 1 || M > (int64_t)kPfRows * 65535 || K <= 0 || N <= 0 || K % 256 != 0 ||
+      K > 65536 || N % kPfCols != 0 || K % group_size != 0 || ldx < K || ldy < ncols ||
+      (N / 16) * (K / 128) * 1024 >= ((int64_t)1 << 31) || M * ldx * 2 >= ((int64_t)1 << 31) ||
+      (K / group_size) * N * 2 >= ((int64_t)1 << 31))
+    return MTL_ERR_SHAPE;
+  if (!aligned16(x) || ldx % 8 != 0 || !aligned16(strip_weight) || !aligned16(strip_scales) ||
+      !aligned16(strip_zeros) || (workspace && !aligned16(workspace)) ||
+      (reinterpret_cast<uintptr_t>(y) & (out_dtype == MTL_OUT_F32 ? 3u : 1u)))
+    return MTL_ERR_ALIGN;
+  PrefillArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = reinterpret_cast<const u32x4*>(strip_weight);
+  a.scales = static_cast<const uint16_t*>(strip_scales);
+  a.qzeros = reinterpret_cast<const uint32_t*>(strip_zeros);
+  a.y = y;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = (int)M; a.K = (int)K; a.N = (int)N;
+  a.group = group_size;
+  a.zero_offset = zero_offset;
+  a.kblocks = (int)(K / 128);
+  a.out_f32 = out_dtype == MTL_OUT_F32;
+  // K splits when the workspace holds their partial sums, else one pass
+  const int64_t need = mtl_w4_gemm_prefill_workspace_bytes(M, K, N);
+  a.splits = need > 0 && workspace && ws_bytes >= need ? (int)(need / (M * N * 4)) : 1;
+  a.kps = a.kblocks / a.splits;
+  a.part = workspace;
+  hipStream_t st = (hipStream_t)stream;
+  switch (group_size) {
+    case 32: prefill_epi<1>(a, epilogue, st); break;
+    case 64: prefill_epi<2>(a, epilogue, st); break;
+    case 128: prefill_epi<4>(a, epilogue, st); break;
+    default: prefill_epi<8>(a, epilogue, st); break;
+  }
+  return launch_status();
+}
+
+}  // extern "C"

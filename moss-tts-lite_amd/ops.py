@@ -57,6 +57,26 @@ def reserve_workspace(device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+_pf_ws_cache: dict = {}
+
+
+def prefill_workspace(device, m: int, k: int, n: int) -> torch.Tensor | None:
+    """The per-device K-split workspace of :func:`prefill_gemm` for an ``[m, k] x [k, n]``
+    product (grown on demand, outside graph capture); None when no split is needed."""
+    nbytes = int(N.load().mtl_w4_gemm_prefill_workspace_bytes(m, k, n))
+    if nbytes <= 0:
+        return None
+    device = torch.device(device)
+    key = _dev_index(device)
+    ws = _pf_ws_cache.get(key)
+    if ws is None or ws.numel() * 4 < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("prefill workspace must be reserved before graph capture")
+        ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+        _pf_ws_cache[key] = ws
+    return ws
+
+
 def gemm_workspace_bytes(m: int, k: int, n: int, group_size: int) -> int:
     return int(N.load().mtl_gemm_workspace_bytes(min(m, _MAX_M), k, n, group_size))
 
@@ -240,6 +260,42 @@ def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.T
             x2[r0:r1].data_ptr(), r1 - r0, k, k, strip_weight.data_ptr(), scales.data_ptr(),
             qzeros.data_ptr(), n, group_size, zero_offset, out[r0:r1].data_ptr(), n, odt, stream),
             "mtl_w4_gemm_strip_rows")
+    return out
+
+
+_PREFILL_EPI = {"none": 0, "residual": 1, "silu_mul": 2}
+
+
+def prefill_gemm(x: torch.Tensor, strip_weight: torch.Tensor, strip_scales: torch.Tensor,
+                 strip_zeros: torch.Tensor, n: int, group_size: int, zero_offset: int = 0,
+                 epilogue: str = "none", out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype = torch.bfloat16, split: bool = True) -> torch.Tensor:
+    """Prompt-length int4 GEMM over the strip layout (``mtl_w4_gemm_prefill``): ``x [M, K]``
+    bf16 (any M, channels in the weight's input order) times the strip copy of a linear
+    with its strip-ordered metadata.  ``epilogue``: ``"none"`` returns ``[M, n]``
+    (``out_dtype``); ``"residual"`` adds into ``out`` (bf16 ``[M, n]``, the residual
+    stream) in place; ``"silu_mul"`` returns bf16 ``[M, n/2]`` = SiLU(gate) * up of the
+    32-column gate|up interleave.  ``split``: let a small grid split K over workgroups
+    (per-device workspace); False runs one pass."""
+    if epilogue not in _PREFILL_EPI:
+        raise ValueError(f"epilogue must be one of {tuple(_PREFILL_EPI)}")
+    x2 = _check_x(x, x.shape[-1])
+    m, k = x2.shape
+    cols = n // 2 if epilogue == "silu_mul" else n
+    if out is None:
+        if epilogue == "residual":
+            raise RuntimeError("the residual epilogue updates `out` in place")
+        out = torch.empty(m, cols, dtype=out_dtype if epilogue == "none" else torch.bfloat16,
+                          device=x2.device)
+    if out.dim() != 2 or out.shape[0] != m or out.shape[1] < cols or out.stride(1) != 1:
+        raise RuntimeError(f"out must be [{m}, >= {cols}] with unit column stride")
+    odt = N.OUT_F32 if out.dtype == torch.float32 else N.OUT_BF16
+    ws = prefill_workspace(x2.device, m, k, n) if split else None
+    N.check(N.load().mtl_w4_gemm_prefill(
+        x2.data_ptr(), m, x2.stride(0), k, strip_weight.data_ptr(), strip_scales.data_ptr(),
+        strip_zeros.data_ptr(), n, group_size, zero_offset, _PREFILL_EPI[epilogue], odt,
+        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(),
+        0 if ws is None else ws.numel() * 4, _stream(x2.device)), "mtl_w4_gemm_prefill")
     return out
 
 

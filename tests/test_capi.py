@@ -148,6 +148,29 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG
 
 
+def test_prefill_gemm_validation(lib):
+    pf = lambda m, k, n, g=128, epi=0, odt=0, ldx=None, ldy=None, x=FAKE, y=FAKE: \
+        lib.mtl_w4_gemm_prefill(x, m, k if ldx is None else ldx, k, FAKE, FAKE, FAKE, n, g, 0,  # noqa: E731
+                                epi, odt, y, n if ldy is None else ldy, None, 0, None)
+    assert pf(0, 4096, 4096) == N.MTL_ERR_SHAPE
+    assert pf(256, 4224, 4096) == N.MTL_ERR_SHAPE          # K % 256
+    assert pf(256, 4096, 4112) == N.MTL_ERR_SHAPE          # N % 128
+    assert pf(256, 4096, 4096, ldx=4000) == N.MTL_ERR_SHAPE
+    assert pf(256, 4096, 4096, g=96) == N.MTL_ERR_GROUP
+    assert pf(256, 4096, 4096, epi=3) == N.MTL_ERR_INVALID_ARG
+    assert pf(256, 4096, 4096, epi=1, odt=1) == N.MTL_ERR_INVALID_ARG   # residual is bf16
+    assert pf(256, 4096, 4096, ldx=4100) == N.MTL_ERR_ALIGN              # 16-byte rows
+    assert pf(256, 4096, 4096, x=None) == N.MTL_ERR_INVALID_ARG
+    assert pf(256, 4096, 4096, y=ctypes.c_void_p(0x1001)) == N.MTL_ERR_ALIGN
+    # SiLU*up writes N/2 columns per row
+    assert pf(256, 4096, 4096, epi=2, ldy=2047) == N.MTL_ERR_SHAPE
+    # K splits only where the grid is small: 4096 x 24576 at 256 rows fills the CUs
+    assert lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4096, 24576) == 0
+    ws = lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4096, 4096)
+    assert ws > 0 and ws % (256 * 4096 * 4) == 0
+    assert lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4100, 4096) == 0
+
+
 def test_converter_validation(lib):
     assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE
