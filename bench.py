@@ -262,6 +262,19 @@ def bench_decode(args, torch):
     dec.capture()
     torch.cuda.synchronize()
     setup_s = time.time() - t0
+    # the prompt: every token per launch (fast.py:251-270); the set-up run built the strip
+    # copies, so this times the prefill itself (it leaves the same state: cache, pos, ids)
+    pf_gpu, pf_wall = [], []
+    for _ in range(3):
+        a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        a_ev.record()
+        dec.prefill(prompt)
+        b_ev.record()
+        torch.cuda.synchronize()
+        pf_wall.append((time.perf_counter() - w0) * 1e3)
+        pf_gpu.append(a_ev.elapsed_time(b_ev))
     for _ in range(args.warmup):
         dec.graph.replay()
     torch.cuda.synchronize()
@@ -320,6 +333,8 @@ def bench_decode(args, torch):
                 "step_hbm_gbs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
                 "host_enqueue_ms_per_step": round(host_s * 1e3 / args.steps, 4),
                 "setup_s": round(setup_s, 1), "plan": dec.plan,
+                "prefill_ms": {"tokens": prompt_len, "gpu": round(min(pf_gpu), 3),
+                               "wall": round(min(pf_wall), 3)},
                 "gemv_us": {k: round(v, 3) for k, v in gemv_us.items()},
                 "gemv_gbs": {k: round(algo_bytes(1, kk, nn, cfg.group_size, False) / gemv_us[k]
                                       / 1e3, 1) for k, kk, nn in

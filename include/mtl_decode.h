@@ -165,6 +165,51 @@ int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, fl
 /* pos[0] += 1 on the device (ends a captured decode step). */
 int mtl_advance_position(int64_t* pos, void* stream);
 
+/* ---- Prefill: every prompt row in one launch (moss_tts_lite/fast.py:210-270) ---- */
+
+/*
+ * Embedding sum of `rows` rows (fast.py:210-216): ids int64 [rows, n_tables] (device),
+ * tables/vocabs as mtl_embed_sum; out bf16 [rows, hidden].
+ */
+int mtl_embed_rows(const int64_t* ids, int64_t rows, int32_t n_tables, const void* const* tables,
+                   const int64_t* vocabs, int64_t hidden, void* out, void* stream);
+
+/*
+ * RMSNorm of each row (model.py:34-40, as mtl_rmsnorm) written in the act-order input
+ * order of the next int4 GEMM: out[r][j] = norm(x[r])[gather[j]] (gather NULL: no
+ * permutation).  x, w, out bf16; rows ldx / ldo elements apart (multiples of 8, 16-byte
+ * aligned); n % 8 == 0, n <= 16384.  In place only with ldx == ldo.
+ */
+int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t* gather,
+                       void* out, int64_t ldo, int64_t rows, int64_t n, float eps, void* stream);
+
+/*
+ * q/k RMSNorm, RoPE and KV-cache write for `rows` rows at positions pos0 .. pos0+rows-1
+ * (fast.py:226-237), the arithmetic of mtl_qk_norm_rope_kv per row.
+ *   qkv    bf16 [rows, ldq], each row q | k | v ((n_heads + 2 n_kv_heads) * 128)
+ *   q_out  bf16 [rows, n_heads * 128]
+ * head_dim must be 128; pos0 + rows <= max_seq.
+ */
+int mtl_qk_norm_rope_kv_rows(const void* qkv, int64_t ldq, int64_t rows, int64_t pos0,
+                             const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                             const void* sin_tab, void* q_out, void* k_cache, void* v_cache,
+                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                             int64_t max_seq, float eps, void* stream);
+
+/*
+ * Causal GQA attention of `rows` query rows at positions pos0 + r over cache positions
+ * [0, pos0 + r] (fast.py:238-242: SDPA, is_causal), scale as given (1/sqrt(head_dim) in
+ * the reference).  Scores and the value sum on MFMA (bf16 operands, fp32 accumulation),
+ * online softmax in fp32.
+ *   q    bf16 [rows, n_heads * 128] (normed, rotated: mtl_qk_norm_rope_kv_rows)
+ *   out  bf16 [rows, ldo]; value c of a row goes to column out_index[c] (NULL: c)
+ * head_dim 128, n_heads / n_kv_heads <= 8, pos0 + rows <= max_seq.
+ */
+int mtl_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t rows,
+                          int64_t pos0, void* out, int64_t ldo, const int32_t* out_index,
+                          int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                          float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

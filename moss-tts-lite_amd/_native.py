@@ -88,6 +88,16 @@ _SIGNATURES = {
                                    _i64, _i32, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p,
                                    _i64, _c_void_p]),
     "mtl_w4_gemm_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "mtl_embed_rows": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _c_void_p,
+                              _c_void_p]),
+    "mtl_rmsnorm_gather": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                                  _i64, ctypes.c_float, _c_void_p]),
+    "mtl_qk_norm_rope_kv_rows": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                        _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p]),
+    "mtl_prefill_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                                     _c_void_p, _i32, _i32, _i32, _i64, ctypes.c_float,
+                                     _c_void_p]),
     "mtl_w4_gemm_norm_silu": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                      _c_void_p, _c_void_p]),

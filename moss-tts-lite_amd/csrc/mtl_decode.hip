@@ -11,15 +11,6 @@ namespace mtl {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-
-__device__ __forceinline__ float lo_bf(uint32_t w) { return bf16_to_f32(w & 0xffffu); }
-__device__ __forceinline__ float hi_bf(uint32_t w) { return bf16_to_f32(w >> 16); }
-
 // ----------------------------------------------------------------------------------
 // RMSNorm (model.py:34-40): fp32 sum of squares, x * rsqrt(mean + eps) rounded to
 // bf16, then the bf16 weight product rounded to bf16.
@@ -332,21 +323,6 @@ __device__ __forceinline__ void head_sum(const float* __restrict__ part, int spl
   }
   x0 = round_bf16(a0);
   x1 = round_bf16(a1);
-}
-
-// RMSNorm over the 128 dims of one head (lane t holds dims t and t+64), then RoPE:
-// q*cos + rotate_half(q)*sin, each product and the sum rounded to bf16 as separate bf16
-// tensor ops (model.py:34-44, fast.py:141-144).
-__device__ __forceinline__ void norm_rope_pair(float x0, float x1, const uint16_t* w,
-                                               const uint16_t* cr, const uint16_t* sr, int t,
-                                               float eps, float& o0, float& o1) {
-  float ss = fmaf(x0, x0, x1 * x1);
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / 128.f + eps);
-  const float n0 = round_bf16(bf16_to_f32(w[t]) * round_bf16(x0 * r));
-  const float n1 = round_bf16(bf16_to_f32(w[t + 64]) * round_bf16(x1 * r));
-  o0 = round_bf16(round_bf16(n0 * bf16_to_f32(cr[t])) + round_bf16(-n1 * bf16_to_f32(sr[t])));
-  o1 = round_bf16(round_bf16(n1 * bf16_to_f32(cr[t + 64])) + round_bf16(n0 * bf16_to_f32(sr[t + 64])));
 }
 
 struct AttnArgs {

@@ -1,0 +1,380 @@
+// Prompt-length kernels of the prefill around the int4 GEMM (gfx950): the embedding sum,
+// RMSNorm with the act-order gather, q/k RMSNorm + RoPE + KV write, and causal GQA
+// attention, each over all prompt rows in one launch (moss_tts_lite/fast.py:210-270, the
+// quantized prefill that runs every layer at t = prompt length).
+//
+// Rounding follows the reference's bf16 tensor ops as in the decode-step kernels: the
+// norms and RoPE are bitwise the decode kernels' arithmetic on each row.  The attention
+// computes scores and the value sum on MFMA (bf16 operands, fp32 accumulation) with an
+// online softmax in fp32.
+#include "mtl_common.h"
+#include "mtl_decode.h"
+
+namespace mtl {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ----------------------------------------------------------------------------------
+// Embedding sum over rows (model.py:156-161, fast.py:210-216): row r of out is
+// bf16(...bf16(T0[ids[r][0]] + T1[ids[r][1]]) + ...).
+// ----------------------------------------------------------------------------------
+__global__ void embed_rows_kernel(const int64_t* __restrict__ ids, int n_tables,
+                                  const uint16_t* const* __restrict__ tables,
+                                  const int64_t* __restrict__ vocabs, int64_t hidden,
+                                  uint16_t* __restrict__ out) {
+  const int64_t r = blockIdx.y;
+  const int64_t* row_ids = ids + r * n_tables;
+  for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < hidden;
+       d += (int64_t)gridDim.x * blockDim.x) {
+    float h = 0.f;
+    for (int i = 0; i < n_tables; ++i) {
+      const int64_t id = row_ids[i];
+      const float v = (id >= 0 && id < vocabs[i]) ? bf16_to_f32(tables[i][id * hidden + d]) : 0.f;
+      h = (i == 0) ? v : round_bf16(h + v);
+    }
+    out[r * hidden + d] = (uint16_t)f32_to_bf16(h);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// RMSNorm of each row (model.py:34-40), summed in the order of mtl_rmsnorm, written as
+// out[r][j] = x_norm[r][gather[j]] (the act-order input order of the next int4 GEMM) or
+// unpermuted.  One 256-thread workgroup per row; the normalised row passes through LDS.
+// ----------------------------------------------------------------------------------
+constexpr int kRowNormMax = 16384;
+
+__global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
+    const uint16_t* x, int64_t ldx, const uint16_t* __restrict__ w,
+    const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n,
+    float eps) {
+  __shared__ uint16_t xs[kRowNormMax];
+  __shared__ float red[4];
+  const uint16_t* xr = x + (size_t)blockIdx.x * ldx;
+  uint16_t* orow = out + (size_t)blockIdx.x * ldo;
+  float ss = 0.f;
+  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + i);
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f0 = lo_bf(a[j]), f1 = hi_bf(a[j]);
+      ss = fmaf(f0, f0, ss);
+      ss = fmaf(f1, f1, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float r = rsqrtf(total / (float)n + eps);
+  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + i);
+    const u32x4 g = *reinterpret_cast<const u32x4*>(w + i);
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t b[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float y0 = round_bf16(lo_bf(b[j]) * round_bf16(lo_bf(a[j]) * r));
+      const float y1 = round_bf16(hi_bf(b[j]) * round_bf16(hi_bf(a[j]) * r));
+      o[j] = f32_to_bf16(y0) | (f32_to_bf16(y1) << 16);
+    }
+    if (gather) {
+      *reinterpret_cast<u32x4*>(xs + i) = u32x4{o[0], o[1], o[2], o[3]};
+    } else {
+      *reinterpret_cast<u32x4*>(orow + i) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  if (!gather) return;
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += 256) orow[j] = xs[gather[j]];
+}
+
+// ----------------------------------------------------------------------------------
+// q/k RMSNorm + RoPE + KV write for rows at positions pos0 + r (fast.py:226-237): one
+// 64-lane workgroup per (head, row), the decode kernel's arithmetic per row.
+// ----------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) qk_norm_rope_rows_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ldq, int64_t pos0,
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
+    const uint16_t* __restrict__ cos_tab, const uint16_t* __restrict__ sin_tab,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H,
+    int Hkv, int64_t max_seq, float eps) {
+  constexpr int D = 128;
+  const int b = blockIdx.x, t = threadIdx.x;
+  const int64_t r = blockIdx.y, pos = pos0 + r;
+  const uint16_t* src = qkv + r * ldq + (size_t)b * D;
+  const float x0 = bf16_to_f32(src[t]), x1 = bf16_to_f32(src[t + 64]);
+  if (b >= H + Hkv) {   // v head: copied unchanged
+    uint16_t* dst = vc + ((size_t)(b - H - Hkv) * max_seq + pos) * D;
+    dst[t] = (uint16_t)f32_to_bf16(x0);
+    dst[t + 64] = (uint16_t)f32_to_bf16(x1);
+    return;
+  }
+  float o0, o1;
+  norm_rope_pair(x0, x1, b < H ? qn : kn, cos_tab + pos * D, sin_tab + pos * D, t, eps, o0, o1);
+  uint16_t* dst = b < H ? q_out + r * (H * D) + (size_t)b * D
+                        : kc + ((size_t)(b - H) * max_seq + pos) * D;
+  dst[t] = (uint16_t)f32_to_bf16(o0);
+  dst[t + 64] = (uint16_t)f32_to_bf16(o1);
+}
+
+// ----------------------------------------------------------------------------------
+// Causal GQA attention over the prompt rows (fast.py:238-242, SDPA with is_causal: row r
+// at position pos0 + r attends to cache positions [0, pos0 + r]).
+//
+// Workgroup (kv head g, block of 16 rows); wave w serves q heads g * n_rep + w (+4).  Per
+// tile of 32 cache positions, staged once in LDS for the workgroup (K rows as they are,
+// V transposed to [dim][position]):
+//   S^T (positions x rows) = K Q^T: v_mfma_f32_16x16x32_bf16 with A = K rows, B = Q^T;
+//     lane (lg, lj) gets positions 16h + 4 lg + i of row lj, i = 0..3, h = 0, 1;
+//   online softmax per row (the lane's own column) in fp32;
+//   O^T (dims x rows) += V^T P^T: B = P^T is the lane's own 8 probabilities (bf16) with
+//     k index 8 lg + e standing for position 4 lg + e (e < 4) or 16 + 4 lg + e - 4, and A
+//     = V^T read from the transposed tile at the same positions.
+// So no operand crosses lanes.  O^T / l goes out as bf16, each value to
+// out[r][out_index[c]] (the act-order input order of the o projection) or column c.
+// ----------------------------------------------------------------------------------
+constexpr int kPaRows = 16;
+constexpr int kPaKeys = 32;
+constexpr int kPaVtPitch = kPaKeys + 4;   // bf16 per V^T row: 72 bytes apart, bank spread
+
+struct PrefillAttnArgs {
+  const uint16_t* q;        // bf16 [rows, H * 128]
+  const uint16_t* kc;       // bf16 [Hkv, max_seq, 128]
+  const uint16_t* vc;
+  uint16_t* out;            // bf16 [rows, ldo]
+  const int32_t* out_index;
+  int64_t ldo, pos0, max_seq;
+  int rows, H, Hkv;
+  float scale;
+};
+
+template <int HPW>   // q heads per wave: n_rep <= 4 * HPW
+__global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
+  constexpr int D = 128;
+  __shared__ u32x4 k_lds[kPaKeys][17];                 // 16 items + 1 pad per row
+  __shared__ uint16_t vt[D][kPaVtPitch];
+  const int kvh = blockIdx.x, rb = blockIdx.y;
+  const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
+  const int lg = lane >> 4, lj = lane & 15;
+  const int n_rep = a.H / a.Hkv;
+  const int r0 = rb * kPaRows;
+  const int my_row = r0 + lj;                          // this lane's query row
+  const bool row_ok = my_row < a.rows;
+  const int64_t my_pos = a.pos0 + (row_ok ? my_row : a.rows - 1);
+  const int last_row = (r0 + kPaRows < a.rows ? r0 + kPaRows : a.rows) - 1;
+  const int64_t last_pos = a.pos0 + last_row;          // the block's last position
+  const int ntiles = (int)(last_pos / kPaKeys) + 1;
+
+  // Q^T operands of this wave's heads: lane (lg, lj) holds dims 32 c + 8 lg .. +7 of row lj
+  u32x4 qb[HPW][4];
+  floatx4 o[HPW][8];
+  float m[HPW], l[HPW];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int hr = wave + 4 * hi;
+    const int hq = kvh * n_rep + (hr < n_rep ? hr : 0);
+    const uint16_t* qrow = a.q + (size_t)(row_ok ? my_row : 0) * (a.H * D) + (size_t)hq * D;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qrow + 32 * c + 8 * lg);
+      qb[hi][c] = row_ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[hi][d] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m[hi] = -INFINITY;
+    l[hi] = 0.f;
+  }
+
+  const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
+  const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    // stage the tile: items t and t + 256 are (position item / 16, dims 8 (item % 16) ..)
+    __syncthreads();                                   // the previous tile is consumed
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int item = t + 256 * j;
+      const int kr = item >> 4, c8 = item & 15;
+      const int64_t p = (int64_t)kt * kPaKeys + kr;
+      const bool ok = p <= last_pos;
+      const size_t off = (size_t)(ok ? p : 0) * D + 8 * c8;
+      u32x4 kv = *reinterpret_cast<const u32x4*>(kbase + off);
+      u32x4 vv = *reinterpret_cast<const u32x4*>(vbase + off);
+      if (!ok) { kv = u32x4{0u, 0u, 0u, 0u}; vv = kv; }
+      k_lds[kr][c8] = kv;
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[8 * c8 + 2 * e][kr] = (uint16_t)(vw[e] & 0xffffu);
+        vt[8 * c8 + 2 * e + 1][kr] = (uint16_t)(vw[e] >> 16);
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+      if (wave + 4 * hi >= n_rep) break;               // uniform over the wave
+      // S^T for positions kt*32 + [0, 16) and [16, 32)
+      floatx4 s[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        s[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bf16x8_t A = __builtin_bit_cast(bf16x8_t, k_lds[16 * h + lj][4 * c + lg]);
+          s[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8_t, qb[hi][c]),
+                                                         s[h], 0, 0, 0);
+        }
+      }
+      float mx = -INFINITY;
+      float sv[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t p = (int64_t)kt * kPaKeys + 16 * h + 4 * lg + i;
+          sv[h][i] = p <= my_pos ? s[h][i] * a.scale : -INFINITY;
+          mx = fmaxf(mx, sv[h][i]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m[hi], mx);            // finite: position 0 is in tile 0
+      const float alpha = expf(m[hi] - m_new);
+      float psum = 0.f;
+      float pv[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[h][i] = expf(sv[h][i] - m_new);
+          psum += pv[h][i];
+        }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      l[hi] = l[hi] * alpha + psum;
+      m[hi] = m_new;
+      const u32x4 pw{cvt_pk_bf16(pv[0][0], pv[0][1]), cvt_pk_bf16(pv[0][2], pv[0][3]),
+                     cvt_pk_bf16(pv[1][0], pv[1][1]), cvt_pk_bf16(pv[1][2], pv[1][3])};
+      const bf16x8_t P = __builtin_bit_cast(bf16x8_t, pw);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint16_t* vrow = &vt[16 * d + lj][0];
+        const u32x2 v0 = *reinterpret_cast<const u32x2*>(vrow + 4 * lg);
+        const u32x2 v1 = *reinterpret_cast<const u32x2*>(vrow + 16 + 4 * lg);
+        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, u32x4{v0.x, v0.y, v1.x, v1.y});
+        o[hi][d] = o[hi][d] * alpha;
+        o[hi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, P, o[hi][d], 0, 0, 0);
+      }
+    }
+  }
+
+  // out[row][hq * 128 + 16 d + 4 lg + i] = bf16(O / l)
+  if (!row_ok) return;
+  uint16_t* orow = a.out + (size_t)my_row * a.ldo;
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int hr = wave + 4 * hi;
+    if (hr >= n_rep) break;
+    const int hq = kvh * n_rep + hr;
+    const float inv = 1.f / l[hi];
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = hq * D + 16 * d + 4 * lg + i;
+        orow[a.out_index ? a.out_index[c] : c] = (uint16_t)f32_to_bf16(o[hi][d][i] * inv);
+      }
+  }
+}
+
+}  // namespace mtl
+
+using namespace mtl;
+
+extern "C" {
+
+int mtl_embed_rows(const int64_t* ids, int64_t rows, int32_t n_tables, const void* const* tables,
+                   const int64_t* vocabs, int64_t hidden, void* out, void* stream) {
+  if (!ids || !tables || !vocabs || !out) return MTL_ERR_INVALID_ARG;
+  if (rows < 1 || rows > 65535 || n_tables < 1 || hidden <= 0) return MTL_ERR_SHAPE;
+  const int blocks = (int)((hidden + 255) / 256);
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(blocks < 64 ? blocks : 64, (unsigned)rows), dim3(256),
+                     0, (hipStream_t)stream, ids, n_tables,
+                     reinterpret_cast<const uint16_t* const*>(tables), vocabs, hidden,
+                     static_cast<uint16_t*>(out));
+  return launch_status();
+}
+
+int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t* gather,
+                       void* out, int64_t ldo, int64_t rows, int64_t n, float eps, void* stream) {
+  if (!x || !w || !out) return MTL_ERR_INVALID_ARG;
+  if (rows < 1 || rows > (int64_t)1 << 30 || n <= 0 || n % 8 != 0 || n > kRowNormMax ||
+      ldx < n || ldo < n || ldx % 8 != 0 || ldo % 8 != 0)
+    return MTL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return MTL_ERR_ALIGN;
+  if (x == out && ldx != ldo) return MTL_ERR_INVALID_ARG;   // in place: the same row pitch
+  hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const uint16_t*>(x), ldx,
+                     static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out), ldo,
+                     (int)n, eps);
+  return launch_status();
+}
+
+int mtl_qk_norm_rope_kv_rows(const void* qkv, int64_t ldq, int64_t rows, int64_t pos0,
+                             const void* q_norm_w, const void* k_norm_w, const void* cos_tab,
+                             const void* sin_tab, void* q_out, void* k_cache, void* v_cache,
+                             int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                             int64_t max_seq, float eps, void* stream) {
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out || !k_cache || !v_cache)
+    return MTL_ERR_INVALID_ARG;
+  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
+  if (n_heads <= 0 || n_kv_heads <= 0 || rows < 1 || rows > 65535 || pos0 < 0 ||
+      pos0 + rows > max_seq || ldq < (int64_t)(n_heads + 2 * n_kv_heads) * 128)
+    return MTL_ERR_SHAPE;
+  hipLaunchKernelGGL(qk_norm_rope_rows_kernel, dim3(n_heads + 2 * n_kv_heads, (unsigned)rows),
+                     dim3(64), 0, (hipStream_t)stream, static_cast<const uint16_t*>(qkv), ldq,
+                     pos0, static_cast<const uint16_t*>(q_norm_w),
+                     static_cast<const uint16_t*>(k_norm_w), static_cast<const uint16_t*>(cos_tab),
+                     static_cast<const uint16_t*>(sin_tab), static_cast<uint16_t*>(q_out),
+                     static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), n_heads,
+                     n_kv_heads, max_seq, eps);
+  return launch_status();
+}
+
+int mtl_prefill_attention(const void* q, const void* k_cache, const void* v_cache, int64_t rows,
+                          int64_t pos0, void* out, int64_t ldo, const int32_t* out_index,
+                          int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                          float scale, void* stream) {
+  if (!q || !k_cache || !v_cache || !out) return MTL_ERR_INVALID_ARG;
+  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads / n_kv_heads > 8 ||
+      rows < 1 || pos0 < 0 || pos0 + rows > max_seq || (rows + kPaRows - 1) / kPaRows > 65535 ||
+      ldo < (int64_t)n_heads * 128)
+    return MTL_ERR_SHAPE;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return MTL_ERR_ALIGN;
+  PrefillAttnArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.kc = static_cast<const uint16_t*>(k_cache);
+  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.out = static_cast<uint16_t*>(out);
+  a.out_index = out_index;
+  a.ldo = ldo;
+  a.pos0 = pos0;
+  a.max_seq = max_seq;
+  a.rows = (int)rows;
+  a.H = n_heads;
+  a.Hkv = n_kv_heads;
+  a.scale = scale;
+  const dim3 grid(n_kv_heads, (unsigned)((rows + kPaRows - 1) / kPaRows));
+  if (n_heads / n_kv_heads <= 4)
+    hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -519,12 +519,121 @@ class FastDecoder:
         self.graph.replay()
         return self.ids
 
+    # -- prompt: every prompt row per launch ---------------------------------------------
+    def _prefill_io(self, rows: int) -> dict:
+        """Prompt-row buffers, grown on demand and kept for later prompts."""
+        pf = getattr(self, "_pf", None)
+        if pf is not None and pf["rows"] >= rows:
+            return pf
+        cfg, dev, bf = self.m.cfg, self.dev, torch.bfloat16
+        z = lambda n, dt=bf: torch.zeros(rows, n, dtype=dt, device=dev)  # noqa: E731
+        pf = {"rows": rows, "ids": z(self.table_ptrs.numel(), torch.int64), "h": z(cfg.hidden),
+              "x": z(cfg.hidden), "x_nat": z(cfg.hidden), "qkv": z(cfg.qkv_out),
+              "q": z(cfg.n_heads * cfg.head_dim), "attn": z(cfg.hidden),
+              "act": z(cfg.intermediate)}
+        self._pf = pf
+        return pf
+
+    def _prefill_gemm(self, x, rows: int, lin, epilogue: int, y, ldy: int, stream) -> None:
+        """One prompt-length int4 GEMM on the strip copy of ``lin`` (mtl_w4_gemm_prefill)."""
+        qw, _ = lin.stream_weight(True)
+        sc, qz = lin.strip_meta()
+        ws = ops.prefill_workspace(self.dev, rows, lin.in_features, lin.out_features)
+        N.check(N.load().mtl_w4_gemm_prefill(
+            x.data_ptr(), rows, x.stride(0), lin.in_features, qw.data_ptr(), sc.data_ptr(),
+            qz.data_ptr(), lin.out_features, lin.group_size, lin.zero_offset, epilogue,
+            N.OUT_BF16, y.data_ptr(), ldy, None if ws is None else ws.data_ptr(),
+            0 if ws is None else ws.numel() * 4, stream), "mtl_w4_gemm_prefill")
+
+    def prefill_rows(self, ids: torch.Tensor, pos0: int = 0) -> torch.Tensor:
+        """Every layer over the prompt rows ``ids`` (int64 ``[L, n_tables]``: one id per
+        embedding table) at positions ``pos0 .. pos0 + L - 1``, writing their K/V into the
+        cache: the reference's quantized prefill (moss_tts_lite/fast.py:210-270), each
+        launch covering all L rows.  Returns the residual stream after the last layer,
+        bf16 ``[L, hidden]`` (a view of an internal buffer)."""
+        m, cfg = self.m, self.m.cfg
+        ids = ids.to(device=self.dev, dtype=torch.int64).reshape(-1, self.table_ptrs.numel())
+        rows = ids.shape[0]
+        if rows < 1 or pos0 < 0 or pos0 + rows > cfg.max_seq:
+            raise ValueError("prompt rows do not fit the KV cache")
+        pf = self._prefill_io(rows)
+        pf["ids"][:rows].copy_(ids)
+        lib = N.load()
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        eps = ctypes.c_float(cfg.eps)
+        scale = ctypes.c_float(attention_scale(cfg))
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        h, x, qkv, q, attn, act = (pf[k] for k in ("h", "x", "qkv", "q", "attn", "act"))
+        H, Hkv, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        N.check(lib.mtl_embed_rows(pf["ids"].data_ptr(), rows, self.table_ptrs.numel(),
+                                   self.table_ptrs.data_ptr(), self.vocabs.data_ptr(), cfg.hidden,
+                                   h.data_ptr(), st), "mtl_embed_rows")
+        for li, lyr in enumerate(m.layers):
+            lq = lyr["qkv"]
+            N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
+                                           lyr["input_layernorm"].data_ptr(),
+                                           p(lq.kernel_args()[3]), x.data_ptr(), cfg.hidden, rows,
+                                           cfg.hidden, eps, st), "mtl_rmsnorm_gather")
+            self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
+            if self.v_keep[li]:
+                # the bf16-kept v_proj (gptq.py:689-693) reads x in its natural order
+                N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
+                                               lyr["input_layernorm"].data_ptr(), None,
+                                               pf["x_nat"].data_ptr(), cfg.hidden, rows,
+                                               cfg.hidden, eps, st), "mtl_rmsnorm_gather")
+                qkv[:rows, lq.out_features:] = torch.nn.functional.linear(
+                    pf["x_nat"][:rows], lyr["v_keep"])
+            N.check(lib.mtl_qk_norm_rope_kv_rows(
+                qkv.data_ptr(), cfg.qkv_out, rows, pos0, lyr["q_norm"].data_ptr(),
+                lyr["k_norm"].data_ptr(), m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
+                q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), H, Hkv, D,
+                cfg.max_seq, eps, st), "mtl_qk_norm_rope_kv_rows")
+            N.check(lib.mtl_prefill_attention(
+                q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), rows, pos0,
+                attn.data_ptr(), cfg.hidden, p(self.inv_perm_o[li]), H, Hkv, D, cfg.max_seq,
+                scale, st), "mtl_prefill_attention")
+            self._prefill_gemm(attn, rows, lyr["o"], N.EPI_RESIDUAL, h, cfg.hidden, st)
+            N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
+                                           lyr["post_attention_layernorm"].data_ptr(),
+                                           p(lyr["gate_up"].kernel_args()[3]), x.data_ptr(),
+                                           cfg.hidden, rows, cfg.hidden, eps, st),
+                    "mtl_rmsnorm_gather")
+            self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_SILU_MUL, act, cfg.intermediate, st)
+            self._prefill_gemm(act, rows, lyr["down"], N.EPI_RESIDUAL, h, cfg.hidden, st)
+        return h[:rows]
+
+    def _final_norm_row(self, h_row: torch.Tensor) -> None:
+        """``h_final = RMSNorm(h_row)`` (fast.py:268)."""
+        cfg = self.m.cfg
+        N.check(N.load().mtl_rmsnorm(h_row.data_ptr(), self.m.final_norm.data_ptr(),
+                                     self.h_final.data_ptr(), 1, cfg.hidden,
+                                     ctypes.c_float(cfg.eps),
+                                     torch.cuda.current_stream(self.dev).cuda_stream),
+                "mtl_rmsnorm")
+
     # -- prompt + greedy loop ---------------------------------------------------------
     def prefill(self, token_ids: torch.Tensor) -> None:
-        """Fill the KV cache with a prompt, one decode step per token (eager).
+        """Fill the KV cache with a prompt, all prompt tokens per launch
+        (:meth:`prefill_rows`), then the final norm, head and greedy token of the last one.
 
-        Leaves ``ids`` = greedy next token and ``pos`` = prompt length.
+        Leaves ``ids`` = greedy next token, ``logits`` its logits and ``pos`` = prompt length.
         """
+        toks = token_ids.to(device=self.dev, dtype=torch.int64).reshape(-1)
+        cfg = self.m.cfg
+        if toks.numel() > cfg.max_seq:
+            raise ValueError("prompt longer than the KV cache")
+        self.m.reset_cache()
+        h = self.prefill_rows(toks.reshape(-1, 1))
+        self._final_norm_row(h[-1])
+        st = torch.cuda.current_stream(self.dev).cuda_stream
+        N.check(N.load().mtl_bf16_gemv_argmax(
+            self.h_final.data_ptr(), self.m.head.data_ptr(), cfg.vocab, cfg.hidden,
+            self.logits.data_ptr(), ctypes.c_void_p(self.ids.data_ptr()), self.head_ws.data_ptr(),
+            self.head_ws.numel(), st), "mtl_bf16_gemv_argmax")
+        self.pos.fill_(toks.numel())
+
+    def prefill_stepwise(self, token_ids: torch.Tensor) -> None:
+        """The same prompt as one decode step per token (eager); same end state."""
         toks = token_ids.to(device=self.dev, dtype=torch.int64).reshape(-1)
         if toks.numel() > self.m.cfg.max_seq:
             raise ValueError("prompt longer than the KV cache")
@@ -641,8 +750,22 @@ class FastMossDecoder(FastDecoder):
         return self.lt, self.la, self.h_final, self.two
 
     def prefill(self, rows: torch.Tensor) -> torch.Tensor:
-        """Fill the KV cache with a prompt of ``rows`` ([L, 1 + n_vq] ids), one eager
-        step per row; returns ``h_final`` of the last row (the prompt's hidden state)."""
+        """Fill the KV cache with a prompt of ``rows`` ([L, 1 + n_vq] ids), every row per
+        launch (:meth:`prefill_rows`, moss_tts_lite/fast.py:251-270); returns ``h_final``,
+        the final-normed hidden state of the last row.  Leaves ``pos`` = L, the first free
+        cache position (the warm-up steps of :meth:`capture` write there, and the first
+        real step overwrites it)."""
+        rows = rows.to(device=self.dev, dtype=torch.int64).reshape(-1, 1 + self.m.cfg.n_vq)
+        if rows.shape[0] > self.m.cfg.max_seq:
+            raise ValueError("prompt longer than the KV cache")
+        self.m.reset_cache()
+        h = self.prefill_rows(rows)
+        self._final_norm_row(h[-1])
+        self.pos.fill_(rows.shape[0])
+        return self.h_final
+
+    def prefill_stepwise(self, rows: torch.Tensor) -> torch.Tensor:
+        """The same prompt as one eager step per row; returns ``h_final`` of the last row."""
         rows = rows.to(device=self.dev, dtype=torch.int64).reshape(-1, 1 + self.m.cfg.n_vq)
         if rows.shape[0] > self.m.cfg.max_seq:
             raise ValueError("prompt longer than the KV cache")
@@ -654,6 +777,7 @@ class FastMossDecoder(FastDecoder):
             for plan in self._layers:
                 self._run(plan)
         self._run(self._final_norm_plan())
+        self.pos.fill_(rows.shape[0])
         return self.h_final
 
     def generate(self, n_steps: int, use_graph: bool = True) -> torch.Tensor:

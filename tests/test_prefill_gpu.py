@@ -129,3 +129,225 @@ def test_prefill_silu_mul_epilogue(dev, split):
     got = act.view(torch.int16).cpu().numpy().view(np.uint16)
     ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
     assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99
+
+
+# ---------------------------------------------------------------- prompt-row kernels
+import ctypes  # noqa: E402
+
+from moss_tts_lite_amd import _native as N  # noqa: E402
+from oracle import decode_ref as D  # noqa: E402
+from oracle.bf16 import round_bf16  # noqa: E402
+
+
+def tb(a, dev):
+    return torch.from_numpy(f32_to_bf16_bits(np.asarray(a, np.float32)).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def fb(t):
+    return t.float().cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return N.load()
+
+
+def test_rmsnorm_gather_rows_match_rmsnorm(dev, lib):
+    # each row bit for bit the single-row RMSNorm kernel's result, gathered by the perm
+    r = np.random.default_rng(20)
+    rows, n = 5, 4096
+    x = round_bf16((3 * r.standard_normal((rows, n))).astype(np.float32))
+    w = round_bf16((1 + 0.1 * r.standard_normal(n)).astype(np.float32))
+    perm = r.permutation(n).astype(np.int32)
+    tx, tw = tb(x, dev), tb(w, dev)
+    ref = torch.empty_like(tx)
+    N.check(lib.mtl_rmsnorm(tx.data_ptr(), tw.data_ptr(), ref.data_ptr(), rows, n,
+                            ctypes.c_float(1e-6), stream()), "rmsnorm")
+    tp = torch.from_numpy(perm).to(dev)
+    out = torch.zeros(rows, n + 64, dtype=torch.bfloat16, device=dev)
+    N.check(lib.mtl_rmsnorm_gather(tx.data_ptr(), n, tw.data_ptr(), tp.data_ptr(), out.data_ptr(),
+                                   n + 64, rows, n, ctypes.c_float(1e-6), stream()), "gather")
+    assert torch.equal(out[:, :n], ref[:, tp.long()]) and not out[:, n:].any()
+    plain = torch.empty_like(tx)
+    N.check(lib.mtl_rmsnorm_gather(tx.data_ptr(), n, tw.data_ptr(), None, plain.data_ptr(), n,
+                                   rows, n, ctypes.c_float(1e-6), stream()), "plain")
+    assert torch.equal(plain, ref)
+
+
+def test_embed_rows_match_embed_sum(dev, lib):
+    r = np.random.default_rng(21)
+    tabs = [round_bf16(r.standard_normal((v, 256)).astype(np.float32)) for v in (50, 7, 9)]
+    tt = [tb(t, dev) for t in tabs]
+    ptrs = torch.tensor([t.data_ptr() for t in tt], dtype=torch.int64, device=dev)
+    vocabs = torch.tensor([50, 7, 9], dtype=torch.int64, device=dev)
+    ids = torch.tensor([[3, 6, 0], [49, 2, 99], [0, 0, 8], [7, -1, 1]], dtype=torch.int64, device=dev)
+    out = torch.empty(4, 256, dtype=torch.bfloat16, device=dev)
+    N.check(lib.mtl_embed_rows(ids.data_ptr(), 4, 3, ptrs.data_ptr(), vocabs.data_ptr(), 256,
+                               out.data_ptr(), stream()), "embed rows")
+    for i in range(4):
+        one = torch.empty(256, dtype=torch.bfloat16, device=dev)
+        N.check(lib.mtl_embed_sum(ids[i].data_ptr(), 3, ptrs.data_ptr(), vocabs.data_ptr(), 256,
+                                  one.data_ptr(), stream()), "embed")
+        assert torch.equal(out[i], one)
+
+
+def test_qk_norm_rope_rows_match_decode_kernel(dev, lib):
+    # rows at positions pos0 .. pos0 + L - 1: q out, K/V cache rows bit for bit the
+    # single-position kernel's
+    from moss_tts_lite_amd.model import rope_tables
+    r = np.random.default_rng(22)
+    H, Hkv, S, L, pos0 = 8, 2, 96, 21, 30
+    ld = (H + 2 * Hkv) * 128
+    qkv = round_bf16((2 * r.standard_normal((L, ld))).astype(np.float32))
+    qn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
+    kn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
+    cos, sin = rope_tables(S, 128, 1e6, dev)
+    tq, tqn, tkn = tb(qkv, dev), tb(qn, dev), tb(kn, dev)
+    kc = torch.zeros(Hkv, S, 128, dtype=torch.bfloat16, device=dev)
+    vc, kc1, vc1 = torch.zeros_like(kc), torch.zeros_like(kc), torch.zeros_like(kc)
+    q_out = torch.zeros(L, H * 128, dtype=torch.bfloat16, device=dev)
+    eps = ctypes.c_float(1e-6)
+    N.check(lib.mtl_qk_norm_rope_kv_rows(tq.data_ptr(), ld, L, pos0, tqn.data_ptr(), tkn.data_ptr(),
+                                         cos.data_ptr(), sin.data_ptr(), q_out.data_ptr(),
+                                         kc.data_ptr(), vc.data_ptr(), H, Hkv, 128, S, eps,
+                                         stream()), "rows")
+    q1 = torch.zeros(H * 128, dtype=torch.bfloat16, device=dev)
+    for i in range(L):
+        tpos = torch.tensor([pos0 + i], dtype=torch.int64, device=dev)
+        N.check(lib.mtl_qk_norm_rope_kv(tq[i].data_ptr(), tqn.data_ptr(), tkn.data_ptr(),
+                                        cos.data_ptr(), sin.data_ptr(), tpos.data_ptr(),
+                                        q1.data_ptr(), kc1.data_ptr(), vc1.data_ptr(), H, Hkv, 128,
+                                        S, eps, stream()), "one")
+        assert torch.equal(q_out[i], q1)
+    assert torch.equal(kc, kc1) and torch.equal(vc, vc1)
+    assert lib.mtl_qk_norm_rope_kv_rows(tq.data_ptr(), ld, L, S - L + 1, tqn.data_ptr(),
+                                        tkn.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                        q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), H, Hkv,
+                                        128, S, eps, stream()) == N.MTL_ERR_SHAPE
+
+
+@pytest.mark.parametrize("H,Hkv,L,pos0", [(32, 8, 70, 0), (4, 2, 33, 0), (16, 2, 17, 5),
+                                          (8, 8, 1, 0), (32, 8, 200, 40)])
+def test_prefill_attention_matches_oracle(dev, lib, H, Hkv, L, pos0):
+    # causal GQA attention of every row against float64 softmax attention over [0, pos]
+    r = np.random.default_rng(H + L + pos0)
+    S = pos0 + L + 8
+    kc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
+    vc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
+    q = round_bf16((0.5 * r.standard_normal((L, H, 128))).astype(np.float32))
+    perm = r.permutation(H * 128).astype(np.int32)
+    tk, tv, tq = tb(kc, dev), tb(vc, dev), tb(q.reshape(L, H * 128), dev)
+    tidx = torch.from_numpy(perm).to(dev)
+    out = torch.zeros(L, H * 128, dtype=torch.bfloat16, device=dev)
+    scale = 1 / np.sqrt(128)
+    N.check(lib.mtl_prefill_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), L, pos0,
+                                      out.data_ptr(), H * 128, tidx.data_ptr(), H, Hkv, 128, S,
+                                      ctypes.c_float(scale), stream()), "prefill attention")
+    got = fb(out)[:, perm].reshape(L, H, 128)       # value c went to column perm[c]
+    errs = []
+    for i in range(L):
+        n = pos0 + i + 1
+        errs.append(rel_l2(got[i], D.attention(q[i], kc[:, :n], vc[:, :n], scale)))
+    print(f"prefill attention H={H} Hkv={Hkv} L={L} pos0={pos0} max rel_l2={max(errs):.2e}")
+    assert max(errs) < 1e-2
+
+
+def test_prefill_attention_agrees_with_decode_attention(dev, lib):
+    # row i equals the decode kernel at position pos0 + i to bf16 rounding
+    r = np.random.default_rng(23)
+    H, Hkv, S, L = 32, 8, 160, 40
+    kc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
+    vc = round_bf16(r.standard_normal((Hkv, S, 128)).astype(np.float32))
+    q = round_bf16(r.standard_normal((L, H * 128)).astype(np.float32))
+    tk, tv, tq = tb(kc, dev), tb(vc, dev), tb(q, dev)
+    out = torch.zeros(L, H * 128, dtype=torch.bfloat16, device=dev)
+    scale = ctypes.c_float(1 / np.sqrt(128))
+    N.check(lib.mtl_prefill_attention(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), L, 100,
+                                      out.data_ptr(), H * 128, None, H, Hkv, 128, S, scale,
+                                      stream()), "prefill attention")
+    ws = torch.zeros(int(lib.mtl_decode_attention_workspace_bytes(H, 128)), dtype=torch.uint8, device=dev)
+    one = torch.empty(H * 128, dtype=torch.bfloat16, device=dev)
+    for i in (0, 17, 39):
+        tpos = torch.tensor([100 + i], dtype=torch.int64, device=dev)
+        N.check(lib.mtl_decode_attention(tq[i].data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                                         tpos.data_ptr(), one.data_ptr(), None, H, Hkv, 128, S,
+                                         scale, ws.data_ptr(), ws.numel(), stream()), "decode")
+        assert rel_l2(fb(out[i]), fb(one)) < 1e-2
+
+
+# ------------------------------------------------------------------ the whole prefill
+def _oracle_prompt(ow, cfg, prompt, model):
+    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    okc = np.zeros((cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, 128), np.float32)
+    ovc = okc.copy()
+    for p, t in enumerate(prompt):
+        lg, hf, tok = D.decode_step(t, p, ow, okc, ovc, cos, sin, cfg.n_heads, cfg.n_kv_heads, 128)
+    return lg, hf, tok, okc, ovc
+
+
+@pytest.mark.parametrize("v_keep,L", [(False, 37), (False, 1), (True, 23)])
+def test_prefill_matches_oracle_and_stepwise(dev, v_keep, L):
+    # the batched prompt against the oracle's token-by-token decode of the same prompt:
+    # last-row logits, final hidden state and every K/V cache row within the bf16 bar;
+    # the device's own stepwise prefill lands on the same caches within that bar too
+    from moss_tts_lite_amd.fast import FastDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config()
+    model, ow = build_case(cfg, seed=41 + L, dev=dev, v_keep=v_keep)
+    dec = FastDecoder(model)
+    prompt = np.random.default_rng(L).integers(0, cfg.vocab, L)
+    lg, hf, tok, okc, ovc = _oracle_prompt(ow, cfg, prompt, model)
+    dec.prefill(torch.from_numpy(prompt))
+    torch.cuda.synchronize()
+    errs = {"logits": rel_l2(fb(dec.logits), lg), "h_final": rel_l2(fb(dec.h_final), hf),
+            "k": rel_l2(fb(model.k_cache)[:, :, :L], okc[:, :, :L]),
+            "v": rel_l2(fb(model.v_cache)[:, :, :L], ovc[:, :, :L])}
+    print(f"prefill L={L} v_keep={v_keep} " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) < 1e-2
+    assert int(dec.pos.item()) == L
+    srt = np.sort(lg)
+    if srt[-1] - srt[-2] > 0.05:
+        assert int(dec.ids.item()) == tok
+    assert not fb(model.k_cache)[:, :, L:].any()
+    kb, vb = model.k_cache.clone(), model.v_cache.clone()
+    dec.prefill_stepwise(torch.from_numpy(prompt))
+    assert rel_l2(fb(kb), fb(model.k_cache)) < 1e-2 and rel_l2(fb(vb), fb(model.v_cache)) < 1e-2
+
+
+def test_prefill_then_graph_decode(dev):
+    # decode steps after the batched prefill: graph replays equal eager steps bit for bit
+    # and the greedy trajectory follows the oracle's where its margin allows
+    from moss_tts_lite_amd.fast import FastDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config()
+    model, ow = build_case(cfg, seed=47, dev=dev)
+    dec = FastDecoder(model)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 29)
+    lg, hf, tok, okc, ovc = _oracle_prompt(ow, cfg, prompt, model)
+    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    dec.prefill(torch.from_numpy(prompt))
+    eager = []
+    for i in range(4):
+        assert int(dec.ids.item()) == tok or np.sort(lg)[-1] - np.sort(lg)[-2] <= 0.05
+        dec.ids.fill_(tok)                       # teacher-forced on the oracle's tokens
+        dec.run_step()
+        eager.append(dec.logits.clone())
+        lg, hf, tok = D.decode_step(tok, len(prompt) + i, ow, okc, ovc, cos, sin, cfg.n_heads,
+                                    cfg.n_kv_heads, 128)
+        assert rel_l2(fb(eager[-1]), lg) < 1e-2
+    toks = []
+    _, _, t0, okc2, ovc2 = _oracle_prompt(ow, cfg, prompt, model)
+    dec.prefill(torch.from_numpy(prompt))
+    dec.capture()
+    tok = t0
+    for i in range(4):
+        dec.ids.fill_(tok)
+        dec.graph.replay()
+        assert torch.equal(dec.logits, eager[i])
+        toks.append(tok)
+        _, _, tok = D.decode_step(tok, len(prompt) + i, ow, okc2, ovc2, cos, sin, cfg.n_heads,
+                                  cfg.n_kv_heads, 128)
