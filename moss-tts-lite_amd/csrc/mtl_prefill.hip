@@ -45,52 +45,72 @@ __global__ void embed_rows_kernel(const int64_t* __restrict__ ids, int n_tables,
 // unpermuted.  One 256-thread workgroup per row; the normalised row passes through LDS.
 // ----------------------------------------------------------------------------------
 constexpr int kRowNormMax = 16384;
+constexpr int kRowNormChunks = kRowNormMax / 2048;   // 8-element chunks per thread
 
 __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
     const uint16_t* x, int64_t ldx, const uint16_t* __restrict__ w,
-    const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n,
-    float eps) {
+    const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n, float eps) {
   __shared__ uint16_t xs[kRowNormMax];
   __shared__ float red[4];
   const uint16_t* xr = x + (size_t)blockIdx.x * ldx;
   uint16_t* orow = out + (size_t)blockIdx.x * ldo;
-  float ss = 0.f;
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + i);
-    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+  const int t = threadIdx.x;
+  const int nch = n / 2048 + (t * 8 < n % 2048 ? 1 : 0);   // this thread's chunks
+  // every load of the row first: x and w chunks (8 elements at 8 t + 2048 c) and the
+  // gather indices (j = t + 256 i)
+  u32x4 xv[kRowNormChunks], wv[kRowNormChunks];
+  int32_t gi[4 * kRowNormChunks];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float f0 = lo_bf(a[j]), f1 = hi_bf(a[j]);
-      ss = fmaf(f0, f0, ss);
-      ss = fmaf(f1, f1, ss);
+  for (int c = 0; c < kRowNormChunks; ++c) {
+    if (c < nch) {
+      xv[c] = *reinterpret_cast<const u32x4*>(xr + 8 * t + 2048 * c);
+      wv[c] = *reinterpret_cast<const u32x4*>(w + 8 * t + 2048 * c);
+    }
+  }
+  if (gather) {
+#pragma unroll
+    for (int i = 0; i < 4 * kRowNormChunks; ++i)
+      if (t + 256 * i < n) gi[i] = gather[t + 256 * i];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kRowNormChunks; ++c) {
+    if (c < nch) {
+      const uint32_t a[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float f0 = lo_bf(a[j]), f1 = hi_bf(a[j]);
+        ss = fmaf(f0, f0, ss);
+        ss = fmaf(f1, f1, ss);
+      }
     }
   }
   ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  if ((t & 63) == 0) red[t >> 6] = ss;
   __syncthreads();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float r = rsqrtf(total / (float)n + eps);
-  for (int i = threadIdx.x * 8; i < n; i += 256 * 8) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + i);
-    const u32x4 g = *reinterpret_cast<const u32x4*>(w + i);
-    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
-    const uint32_t b[4] = {g.x, g.y, g.z, g.w};
-    uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float y0 = round_bf16(lo_bf(b[j]) * round_bf16(lo_bf(a[j]) * r));
-      const float y1 = round_bf16(hi_bf(b[j]) * round_bf16(hi_bf(a[j]) * r));
-      o[j] = f32_to_bf16(y0) | (f32_to_bf16(y1) << 16);
-    }
-    if (gather) {
-      *reinterpret_cast<u32x4*>(xs + i) = u32x4{o[0], o[1], o[2], o[3]};
-    } else {
-      *reinterpret_cast<u32x4*>(orow + i) = u32x4{o[0], o[1], o[2], o[3]};
+  for (int c = 0; c < kRowNormChunks; ++c) {
+    if (c < nch) {
+      const uint32_t a[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+      const uint32_t b[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float y0 = round_bf16(lo_bf(b[j]) * round_bf16(lo_bf(a[j]) * r));
+        const float y1 = round_bf16(hi_bf(b[j]) * round_bf16(hi_bf(a[j]) * r));
+        o[j] = f32_to_bf16(y0) | (f32_to_bf16(y1) << 16);
+      }
+      uint16_t* dst = gather ? xs : orow;
+      *reinterpret_cast<u32x4*>(dst + 8 * t + 2048 * c) = u32x4{o[0], o[1], o[2], o[3]};
     }
   }
   if (!gather) return;
   __syncthreads();
-  for (int j = threadIdx.x; j < n; j += 256) orow[j] = xs[gather[j]];
+#pragma unroll
+  for (int i = 0; i < 4 * kRowNormChunks; ++i)
+    if (t + 256 * i < n) orow[t + 256 * i] = xs[gi[i]];
 }
 
 // ----------------------------------------------------------------------------------
@@ -192,21 +212,30 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
 
   const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
   const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
+  // tile loads: items t and t + 256 are (position item / 16, dims 8 (item % 16) ..); the
+  // next tile's loads are in flight while this tile is multiplied
+  u32x4 kv[2], vv[2];
+  auto tile_load = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int item = t + 256 * j;
+      const int64_t p = (int64_t)kt * kPaKeys + (item >> 4);
+      const bool ok = p <= last_pos;
+      const size_t off = (size_t)(ok ? p : 0) * D + 8 * (item & 15);
+      kv[j] = *reinterpret_cast<const u32x4*>(kbase + off);
+      vv[j] = *reinterpret_cast<const u32x4*>(vbase + off);
+      if (!ok) { kv[j] = u32x4{0u, 0u, 0u, 0u}; vv[j] = kv[j]; }
+    }
+  };
+  tile_load(0);
   for (int kt = 0; kt < ntiles; ++kt) {
-    // stage the tile: items t and t + 256 are (position item / 16, dims 8 (item % 16) ..)
     __syncthreads();                                   // the previous tile is consumed
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int item = t + 256 * j;
       const int kr = item >> 4, c8 = item & 15;
-      const int64_t p = (int64_t)kt * kPaKeys + kr;
-      const bool ok = p <= last_pos;
-      const size_t off = (size_t)(ok ? p : 0) * D + 8 * c8;
-      u32x4 kv = *reinterpret_cast<const u32x4*>(kbase + off);
-      u32x4 vv = *reinterpret_cast<const u32x4*>(vbase + off);
-      if (!ok) { kv = u32x4{0u, 0u, 0u, 0u}; vv = kv; }
-      k_lds[kr][c8] = kv;
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      k_lds[kr][c8] = kv[j];
+      const uint32_t vw[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vt[8 * c8 + 2 * e][kr] = (uint16_t)(vw[e] & 0xffffu);
@@ -214,6 +243,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
       }
     }
     __syncthreads();
+    if (kt + 1 < ntiles) tile_load(kt + 1);
 
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
