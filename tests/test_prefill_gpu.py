@@ -351,3 +351,66 @@ def test_prefill_then_graph_decode(dev):
         toks.append(tok)
         _, _, tok = D.decode_step(tok, len(prompt) + i, ow, okc2, ovc2, cos, sin, cfg.n_heads,
                                   cfg.n_kv_heads, 128)
+
+
+@pytest.mark.parametrize("group", [32, 256])
+def test_prefill_group_sizes_match_oracle(dev, group):
+    # the presets' g32 (and g256) linears through the whole prefill
+    from moss_tts_lite_amd.fast import FastDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config(group_size=group)
+    model, ow = build_case(cfg, seed=50 + group, dev=dev)
+    dec = FastDecoder(model)
+    prompt = np.random.default_rng(group).integers(0, cfg.vocab, 45)
+    lg, hf, tok, okc, ovc = _oracle_prompt(ow, cfg, prompt, model)
+    dec.prefill(torch.from_numpy(prompt))
+    torch.cuda.synchronize()
+    errs = [rel_l2(fb(dec.logits), lg), rel_l2(fb(model.k_cache)[:, :, :45], okc[:, :, :45]),
+            rel_l2(fb(model.v_cache)[:, :, :45], ovc[:, :, :45])]
+    print(f"prefill g{group}: " + " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) < 1e-2
+
+
+def test_prefill_in_chunks_continues_the_cache(dev):
+    # prefill_rows from pos0 > 0 continues a cache: two chunks land where one pass does
+    from moss_tts_lite_amd.fast import FastDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config()
+    model, ow = build_case(cfg, seed=60, dev=dev)
+    dec = FastDecoder(model)
+    prompt = torch.from_numpy(np.random.default_rng(60).integers(0, cfg.vocab, 50))
+    model.reset_cache()
+    h_one = dec.prefill_rows(prompt.reshape(-1, 1)).clone()
+    k_one, v_one = model.k_cache.clone(), model.v_cache.clone()
+    model.reset_cache()
+    h_a = dec.prefill_rows(prompt[:21].reshape(-1, 1)).clone()
+    h_b = dec.prefill_rows(prompt[21:].reshape(-1, 1), pos0=21).clone()
+    torch.cuda.synchronize()
+    # the first chunk's rows are the same computation; the second attends to the first's
+    # cache rows, written bit for bit alike
+    assert torch.equal(h_a, h_one[:21])
+    assert torch.equal(model.k_cache[:, :, :21], k_one[:, :, :21])
+    assert rel_l2(fb(h_b), fb(h_one[21:])) < 1e-2
+    assert rel_l2(fb(model.k_cache), fb(k_one)) < 1e-2 and rel_l2(fb(model.v_cache), fb(v_one)) < 1e-2
+    with pytest.raises(ValueError):
+        dec.prefill_rows(prompt.reshape(-1, 1), pos0=cfg.max_seq - 10)
+
+
+def test_moss_prefill_matches_stepwise(dev):
+    # MOSS rows (1 + n_vq embedding tables): the batched prompt and the step-per-row prompt
+    # give the same final hidden state and caches to the bf16 bar, and both leave pos = L
+    from moss_tts_lite_amd.fast import FastMossDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config(vocab=2000, n_vq=4, audio_vocab=1025, audio_pad_code=1024,
+                       two_way_ids=(1500, 1777))
+    model, ow = build_case(cfg, seed=61, dev=dev)
+    dec = FastMossDecoder(model)
+    r = np.random.default_rng(61)
+    rows = np.concatenate([r.integers(0, cfg.vocab, (19, 1)), r.integers(0, 1025, (19, cfg.n_vq))], 1)
+    hb = dec.prefill(torch.from_numpy(rows)).clone()
+    kb, vb = model.k_cache.clone(), model.v_cache.clone()
+    assert int(dec.pos.item()) == 19
+    hs = dec.prefill_stepwise(torch.from_numpy(rows)).clone()
+    assert int(dec.pos.item()) == 19
+    assert rel_l2(fb(hb), fb(hs)) < 1e-2
+    assert rel_l2(fb(kb), fb(model.k_cache)) < 1e-2 and rel_l2(fb(vb), fb(model.v_cache)) < 1e-2
