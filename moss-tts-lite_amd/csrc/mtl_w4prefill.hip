@@ -97,15 +97,16 @@ w4_prefill_kernel(PrefillArgs a) {
       xv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             xrsrc, xoff, r * xrstep + b * 256, 0));
   };
+  auto x_store_part = [&](int buf, int r) {     // item set r: rows srow + 16 r
+    float sum;
+    const u32x4 pv = pair_order_dot(xv[r], sum);
+    sum = row_sum<GI>(sum);
+    xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
+    if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
+  };
   auto x_store = [&](int buf) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float sum;
-      const u32x4 pv = pair_order_dot(xv[r], sum);
-      sum = row_sum<GI>(sum);
-      xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
-      if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
-    }
+    for (int r = 0; r < 4; ++r) x_store_part(buf, r);
   };
 
   // Weight ring: block b of both strips and the metadata records it starts go to slot
@@ -191,6 +192,44 @@ w4_prefill_kernel(PrefillArgs a) {
       asm volatile("" ::: "memory");
       issue(r, b + D < kb1 ? b + D : kb1 - 1);   // unconditional refill (clamped)
       __builtin_amdgcn_sched_barrier(0);
+      if (GR >= 4) {
+        // One group per block (or a block of a g = 256 pair): the row tiles run as a
+        // pipeline.  The MFMAs of tile tt are issued before the group correction of tile
+        // tt - 1 and a quarter of the next block's staging, so that VALU work overlaps the
+        // MFMAs in flight; two accumulator pairs are live.
+        floatx4 acc[2][2];
+        auto mm = [&](int tt) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bf16x8_t A =
+                __builtin_bit_cast(bf16x8_t, xa[buf][(16 * tt + lj) * kPfPitch + 4 * j + lg]);
+            acc[tt & 1][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[0][j], j == 0 ? zero4 : acc[tt & 1][0], 0, 0, 0);
+            acc[tt & 1][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B[1][j], j == 0 ? zero4 : acc[tt & 1][1], 0, 0, 0);
+          }
+        };
+        auto fold = [&](int tt) {
+          const float4 X4 = *reinterpret_cast<const float4*>(&xs[buf][0][16 * tt + 4 * lg]);
+          const float X[4] = {X4.x, X4.y, X4.z, X4.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            tot[tt][0][i] = fmaf(gs[0][0], fmaf(-gz[0][0], X[i], acc[tt & 1][0][i]), tot[tt][0][i]);
+            tot[tt][1][i] = fmaf(gs[1][0], fmaf(-gz[1][0], X[i], acc[tt & 1][1][i]), tot[tt][1][i]);
+          }
+          x_store_part(buf ^ 1, tt);             // block b + 1, loaded during block b - 1
+          asm volatile("" ::"v"(tot[tt][0]), "v"(tot[tt][1]) : "memory");
+        };
+        mm(0);
+#pragma unroll
+        for (int tt = 1; tt < 4; ++tt) {
+          mm(tt);
+          fold(tt - 1);
+        }
+        fold(3);
+        __builtin_amdgcn_sched_barrier(0);
+        x_load(b + 2 < kb1 ? b + 2 : kb1 - 1);
+        __syncthreads();
+        continue;
+      }
       // Row tile by row tile, so one accumulator pair is live at a time.
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
