@@ -401,6 +401,51 @@ def bench_kernels(args, torch):
                       "gemv_launches_each": args.steps}))
 
 
+def bench_prefill(args, torch):
+    """Prompt-length int4 GEMMs (mtl_w4_gemm_prefill) on the decode shapes at M =
+    --prefill-rows, random strip-layout weights, --steps launches each between one event
+    pair; the whole prefill is timed by the decode workload (config.prefill_ms)."""
+    from moss_tts_lite_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    m = args.prefill_rows
+    shapes = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576),
+              "down": (12288, 4096)}
+    names = list(shapes) if args.prefill_shape == "all" else [args.prefill_shape]
+    out = {}
+    for name in names:
+        k, n = shapes[name]
+        qw = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 8, n), dtype=torch.int32, device=dev,
+                           generator=gen)
+        sc = (torch.rand(k // 128, n, device=dev, generator=gen) * 0.01 + 0.002).half()
+        qz = torch.randint(-2 ** 31, 2 ** 31 - 1, (k // 128, n // 8), dtype=torch.int32,
+                           device=dev, generator=gen)
+        st = ops.strip_weights(qw)
+        ssc, sqz = ops.strip_meta(sc, qz, 128)
+        x = torch.randn(m, k, device=dev, generator=gen).bfloat16()
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        res = {}
+        for split in ((True, False) if args.prefill_split == "auto" else (False,)):
+            for _ in range(3):
+                ops.prefill_gemm(x, st, ssc, sqz, n, 128, out=y, split=split)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            for _ in range(args.steps):
+                ops.prefill_gemm(x, st, ssc, sqz, n, 128, out=y, split=split)
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / args.steps
+            res["us" if split else "one_pass_us"] = round(us, 2)
+            if split:
+                res["tflops"] = round(2.0 * m * n * k / us / 1e6, 1)
+        out[name] = res
+    print(json.dumps({"workload": "prefill", "rows": m, "launches_each": args.steps,
+                      "dtype": "int4 GPTQ weights, bf16 activations, fp32 accumulate",
+                      "gemm": out}))
+
+
 def cpu_baseline_decode(budget_s: float = 20.0):
     """The oracle's restatement of the reference CPU path (dequantise each layer's
     weights, float64 products, the step's bf16 rounding) on one full-size layer plus the
@@ -465,7 +510,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "kernels"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "gemv", "kernels", "prefill"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--group", type=int, default=128, choices=[32, 64, 128, 256],
                     help="int4 group size of every projection (decode workload)")
@@ -474,6 +520,11 @@ def main():
     ap.add_argument("--plan", default="strip",
                     choices=["strip", "fused", "staged", "partials", "unfused"],
                     help="decode launch plan (decode workload)")
+    ap.add_argument("--prefill-rows", type=int, default=256, help="M (prefill workload)")
+    ap.add_argument("--prefill-shape", default="all",
+                    choices=["all", "qkv", "o", "gate_up", "down"], help="(prefill workload)")
+    ap.add_argument("--prefill-split", default="auto", choices=["auto", "off"],
+                    help="K split of small grids, or one pass only (prefill workload)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -487,6 +538,10 @@ def main():
     if args.workload == "kernels":
         args.steps = 72 if args.steps is None else args.steps
         bench_kernels(args, torch)
+        return
+    if args.workload == "prefill":
+        args.steps = 20 if args.steps is None else args.steps
+        bench_prefill(args, torch)
         return
     if args.workload == "decode":
         args.warmup = 16 if args.warmup is None else args.warmup
