@@ -171,6 +171,44 @@ def test_prefill_gemm_validation(lib):
     assert lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4100, 4096) == 0
 
 
+def test_prefill_row_entry_validation(lib):
+    eps = ctypes.c_float(1e-6)
+    sc = ctypes.c_float(0.088)
+    # embedding rows
+    assert lib.mtl_embed_rows(None, 4, 1, FAKE, FAKE, 4096, FAKE, None) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_embed_rows(FAKE, 0, 1, FAKE, FAKE, 4096, FAKE, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_embed_rows(FAKE, 4, 0, FAKE, FAKE, 4096, FAKE, None) == N.MTL_ERR_SHAPE
+    # RMSNorm + gather: n % 8, n <= 16384, row pitches, alignment, in place only with one pitch
+    ng = lambda x, ldx, out, ldo, rows, n: lib.mtl_rmsnorm_gather(  # noqa: E731
+        x, ldx, FAKE, None, out, ldo, rows, n, eps, None)
+    assert ng(FAKE, 4100, FAKE, 4100, 4, 4100) == N.MTL_ERR_SHAPE
+    assert ng(FAKE, 32768, FAKE, 32768, 4, 32768) == N.MTL_ERR_SHAPE
+    assert ng(FAKE, 4000, FAKE, 4096, 4, 4096) == N.MTL_ERR_SHAPE
+    assert ng(FAKE, 4096, FAKE, 4096, 0, 4096) == N.MTL_ERR_SHAPE
+    assert ng(ctypes.c_void_p(0x1008), 4096, FAKE, 4096, 4, 4096) == N.MTL_ERR_ALIGN
+    assert ng(FAKE, 4096, FAKE, 4104, 4, 4096) == N.MTL_ERR_INVALID_ARG
+    assert ng(None, 4096, FAKE, 4096, 4, 4096) == N.MTL_ERR_INVALID_ARG
+    # q/k norm + RoPE rows: head_dim 128, rows inside the cache, the q|k|v row pitch
+    qk = lambda ldq, rows, pos0, hd=128, S=2048: lib.mtl_qk_norm_rope_kv_rows(  # noqa: E731
+        FAKE, ldq, rows, pos0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8, hd, S, eps, None)
+    assert qk(6144, 16, 0, hd=64) == N.MTL_ERR_UNSUPPORTED
+    assert qk(6144, 16, 2040) == N.MTL_ERR_SHAPE
+    assert qk(6000, 16, 0) == N.MTL_ERR_SHAPE
+    assert qk(6144, 16, -1) == N.MTL_ERR_SHAPE
+    # causal attention: GQA ratio <= 8, rows inside the cache, out pitch
+    at = lambda rows, pos0, H=32, Hkv=8, ldo=4096, S=2048: lib.mtl_prefill_attention(  # noqa: E731
+        FAKE, FAKE, FAKE, rows, pos0, FAKE, ldo, None, H, Hkv, 128, S, sc, None)
+    assert at(16, 0, H=32, Hkv=2) == N.MTL_ERR_SHAPE
+    assert at(16, 0, H=32, Hkv=6) == N.MTL_ERR_SHAPE
+    assert at(16, 2040) == N.MTL_ERR_SHAPE
+    assert at(0, 0) == N.MTL_ERR_SHAPE
+    assert at(16, 0, ldo=4000) == N.MTL_ERR_SHAPE
+    assert lib.mtl_prefill_attention(FAKE, FAKE, FAKE, 16, 0, FAKE, 4096, None, 32, 8, 64, 2048,
+                                     sc, None) == N.MTL_ERR_UNSUPPORTED
+    assert lib.mtl_prefill_attention(ctypes.c_void_p(0x1008), FAKE, FAKE, 16, 0, FAKE, 4096, None,
+                                     32, 8, 128, 2048, sc, None) == N.MTL_ERR_ALIGN
+
+
 def test_converter_validation(lib):
     assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE
