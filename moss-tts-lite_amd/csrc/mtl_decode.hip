@@ -356,6 +356,10 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
   for (int hr = wave; hr < n_rep; hr += 4) {
     const int h = kvh * n_rep + hr;
     const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
+    // the output columns of dims 2*lane, +1, loaded with the partials (not at the store)
+    const int i0 = h * D + 2 * lane;
+    int2 oi = make_int2(i0, i0 + 1);
+    if (a.out_index) oi = *reinterpret_cast<const int2*>(a.out_index + i0);
     // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1 as 64-bit
     // agent-scope loads, all issued before any use
     typedef unsigned long long u64;
@@ -393,10 +397,9 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
         }
     }
     const float Ls = lc;
-    const int i0 = h * D + 2 * lane;
     const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
-    a.out[a.out_index ? a.out_index[i0] : i0] = (uint16_t)f32_to_bf16(r0);
-    a.out[a.out_index ? a.out_index[i0 + 1] : i0 + 1] = (uint16_t)f32_to_bf16(r1);
+    a.out[oi.x] = (uint16_t)f32_to_bf16(r0);
+    a.out[oi.y] = (uint16_t)f32_to_bf16(r1);
   }
 }
 
@@ -617,6 +620,11 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   HeadPart hq, hkv;
   if (FROM_PART && wave < n_rep)
     head_issue(a.qkv_part, a.splits, ncols, kvh * n_rep + wave, lane, hq);
+  // k (wave 0) and v (wave 1) of this kv head at position pos, loaded by every workgroup
+  // before pos is known: only the one holding pos uses them, but its prologue then needs
+  // no second round trip after the position arrives
+  if (FROM_PART && wave < 2)
+    head_issue(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv);
   const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
   const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
   const int last_row = (int)a.max_seq - 1;
@@ -639,8 +647,6 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   const int p0 = c * P;
   const int p1 = p0 + P < L ? p0 + P : L;
   const bool has_pos = pos >= p0 && pos < p1;
-  if (FROM_PART && has_pos && wave < 2)   // k (wave 0) or v (wave 1) of position pos
-    head_issue(a.qkv_part, a.splits, ncols, (wave == 0 ? a.H : a.H + a.Hkv) + kvh, lane, hkv);
 
   // 1. Prologue: q heads into LDS; k/v of position pos into the cache and the LDS tile.
   const size_t prow = (size_t)(pos >= 0 && pos < a.max_seq ? pos : 0) * D;
