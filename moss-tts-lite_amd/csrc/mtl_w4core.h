@@ -90,6 +90,49 @@ __device__ __forceinline__ u32x4 rmsnorm8(u32x4 h, u32x4 w, float r) {
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// Strip-ordered group metadata (mtl_w4_strip_meta): record rec (a strip's 128-channel
+// block, or block pair at g = 256) holds the MB = max(1, 128/g) fp16 scales of each of the
+// strip's 16 columns contiguously and their zero nibbles (MB = 4: 16 bits per column,
+// MB = 2: 8 bits, MB = 1: a nibble, two columns a byte).  Lane column lj loads its
+// column's metadata of a record with one scale load and one zero load.
+template <int MB>
+struct StripMeta {
+  uint32_t s[MB == 4 ? 2 : 1];   // MB packed fp16 scales
+  uint32_t z;                    // MB zero nibbles (MB = 1: the record byte)
+};
+
+template <int MB>
+__device__ __forceinline__ void strip_meta_load(__amdgpu_buffer_rsrc_t srsrc,
+                                                __amdgpu_buffer_rsrc_t zrsrc, int lj, int rec,
+                                                StripMeta<MB>& m) {
+  if (MB == 4) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                  srsrc, lj * 8, rec * 128, 0));
+    m.s[0] = v.x;
+    m.s[MB == 4 ? 1 : 0] = v.y;
+    m.z = __builtin_amdgcn_raw_buffer_load_b16(zrsrc, lj * 2, rec * 32, 0);
+  } else if (MB == 2) {
+    m.s[0] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, lj * 4, rec * 64, 0);
+    m.z = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj, rec * 16, 0);
+  } else {
+    m.s[0] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, lj * 2, rec * 32, 0);
+    m.z = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj >> 1, rec * 8, 0);
+  }
+}
+
+// Scale and 128 + zero + zero_offset of the record's MB groups for column lj.
+template <int MB>
+__device__ __forceinline__ void strip_meta_decode(const StripMeta<MB>& m, int lj,
+                                                  int zero_offset, float (&gs)[MB],
+                                                  float (&gz)[MB]) {
+  const uint32_t zsh = MB == 1 ? (lj & 1) * 4 : 0;
+#pragma unroll
+  for (int g = 0; g < MB; ++g) {
+    gs[g] = f16_to_f32((m.s[g >> 1] >> (16 * (g & 1))) & 0xffffu);
+    gz[g] = (float)(128 + (int)((m.z >> (zsh + 4 * g)) & 0xfu) + zero_offset);
+  }
+}
+
 // Arguments of the full-K strip GEMV (mtl_w4strip.hip), M = 1, AutoGPTQ meta.  The source
 // of x is xpart (SiLU*up), else hn (RMSNorm), else x; the epilogue is SiLU*up into act
 // when act is set (RMSNorm source only), the residual add when h is set, else an fp32

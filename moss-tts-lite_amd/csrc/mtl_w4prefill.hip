@@ -120,27 +120,13 @@ w4_prefill_kernel(PrefillArgs a) {
   const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
   u32x4 wq[D][2];
-  uint32_t ms[D][2][MB == 4 ? 2 : 1], mz[D][2];
+  StripMeta<MB> mt[D][2];
   auto issue = [&](int r, int b) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int strip = sA + s;
-      if (GR <= 4 || (r & 1) == 0) {
-        const int rec = strip * krec + (GR == 8 ? b >> 1 : b);
-        if (MB == 4) {
-          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                        srsrc, lj * 8, rec * 128, 0));
-          ms[r][s][0] = v.x;
-          ms[r][s][MB == 4 ? 1 : 0] = v.y;
-          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b16(zrsrc, lj * 2, rec * 32, 0);
-        } else if (MB == 2) {
-          ms[r][s][0] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, lj * 4, rec * 64, 0);
-          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj, rec * 16, 0);
-        } else {
-          ms[r][s][0] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, lj * 2, rec * 32, 0);
-          mz[r][s] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj >> 1, rec * 8, 0);
-        }
-      }
+      if (GR <= 4 || (r & 1) == 0)
+        strip_meta_load<MB>(srsrc, zrsrc, lj, strip * krec + (GR == 8 ? b >> 1 : b), mt[r][s]);
       wq[r][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                wrsrc, lane * 16, (strip * kb + b) * 1024, 0));
     }
@@ -170,14 +156,7 @@ w4_prefill_kernel(PrefillArgs a) {
       const int buf = r & 1;                     // b0 - kb0 and kb0 are even
       if (GR <= 4 || (r & 1) == 0) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const uint32_t zsh = MB == 1 ? (lj & 1) * 4 : 0;
-#pragma unroll
-          for (int m = 0; m < MB; ++m) {
-            gs[s][m] = f16_to_f32((ms[r][s][m >> 1] >> (16 * (m & 1))) & 0xffffu);
-            gz[s][m] = (float)(128 + (int)((mz[r][s] >> (zsh + 4 * m)) & 0xfu) + a.zero_offset);
-          }
-        }
+        for (int s = 0; s < 2; ++s) strip_meta_decode<MB>(mt[r][s], lj, a.zero_offset, gs[s], gz[s]);
       }
       bf16x8_t B[2][4];
 #pragma unroll

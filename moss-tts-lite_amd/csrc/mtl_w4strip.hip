@@ -152,25 +152,11 @@ w4_strip_kernel(StripArgs a) {
   const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
   u32x4 wq[WIN];
-  uint32_t ms[WIN][MB == 4 ? 2 : 1], mz[WIN];
+  StripMeta<MB> mt[WIN];
   // block b into ring slot r (r = b % WIN, a compile-time index at every call)
   auto issue = [&](int r, int b) {
-    if (GR <= 4 || (r & 1) == 0) {             // g = 256: one record per block pair (b, r alike in parity)
-      const int rec = rec0 + (GR == 8 ? b >> 1 : b);
-      if (MB == 4) {
-        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                      srsrc, lj * 8, rec * 128, 0));
-        ms[r][0] = v.x;
-        ms[r][MB == 4 ? 1 : 0] = v.y;
-        mz[r] = __builtin_amdgcn_raw_buffer_load_b16(zrsrc, lj * 2, rec * 32, 0);
-      } else if (MB == 2) {
-        ms[r][0] = __builtin_amdgcn_raw_buffer_load_b32(srsrc, lj * 4, rec * 64, 0);
-        mz[r] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj, rec * 16, 0);
-      } else {
-        ms[r][0] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, lj * 2, rec * 32, 0);
-        mz[r] = __builtin_amdgcn_raw_buffer_load_b8(zrsrc, lj >> 1, rec * 8, 0);
-      }
-    }
+    if (GR <= 4 || (r & 1) == 0)               // g = 256: one record per block pair (b, r alike in parity)
+      strip_meta_load<MB>(srsrc, zrsrc, lj, rec0 + (GR == 8 ? b >> 1 : b), mt[r]);
     wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                           wrsrc, lane * 16, (blk0 + b) * 1024, kStripAux));
   };
@@ -245,12 +231,7 @@ w4_strip_kernel(StripArgs a) {
       const int b = b0 + r;
       const u32x4 w4 = wq[r];
       float gs[MB], gz[MB];                     // scale and 128 + zero of the block's groups
-      const uint32_t zsh = MB == 1 ? (lj & 1) * 4 : 0;
-#pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        gs[m] = f16_to_f32((ms[r][m >> 1] >> (16 * (m & 1))) & 0xffffu);
-        gz[m] = (float)(128 + (int)((mz[r] >> (zsh + 4 * m)) & 0xfu) + a.zero_offset);
-      }
+      strip_meta_decode<MB>(mt[r], lj, a.zero_offset, gs, gz);
       if (GR == 8 && (r & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
       // keep the compiler from hoisting later ring loads (and their registers) above here:
       // an empty asm with a memory clobber orders the loads at the IR level, the
