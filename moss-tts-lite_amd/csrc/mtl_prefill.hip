@@ -174,13 +174,20 @@ struct PrefillAttnArgs {
 };
 
 template <int HPW>   // q heads per wave: n_rep <= 4 * HPW
-__global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
+__global__ void __launch_bounds__(512) prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int D = 128;
-  __shared__ u32x4 k_lds[kPaKeys][17];                 // 16 items + 1 pad per row
-  __shared__ uint16_t vt[D][kPaVtPitch];
+  // Two wave groups of 4 take alternate tiles (group g2: tiles 2 it + g2), each with its
+  // own LDS tile; their (m, l, O) meet in LDS at the end.  The raw buffer holds the two
+  // K tiles ([32][16 items + 1 pad] u32x4 each), then the two V^T tiles, and after the
+  // loop the merge exchange.
+  constexpr int kKItems = 2 * kPaKeys * 17;
+  __shared__ u32x4 lds_raw[kKItems + (2 * D * kPaVtPitch * 2) / 16];
   const int kvh = blockIdx.x, rb = blockIdx.y;
   const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
+  const int g2 = wave >> 2, hw = wave & 3, tg = t & 255;
   const int lg = lane >> 4, lj = lane & 15;
+  u32x4* k_lds = lds_raw + g2 * kPaKeys * 17;                       // [32][17]
+  uint16_t* vt = reinterpret_cast<uint16_t*>(lds_raw + kKItems) + g2 * D * kPaVtPitch;
   const int n_rep = a.H / a.Hkv;
   const int r0 = rb * kPaRows;
   const int my_row = r0 + lj;                          // this lane's query row
@@ -189,6 +196,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
   const int last_row = (r0 + kPaRows < a.rows ? r0 + kPaRows : a.rows) - 1;
   const int64_t last_pos = a.pos0 + last_row;          // the block's last position
   const int ntiles = (int)(last_pos / kPaKeys) + 1;
+  const int nit = (ntiles + 1) / 2;
 
   // Q^T operands of this wave's heads: lane (lg, lj) holds dims 32 c + 8 lg .. +7 of row lj
   u32x4 qb[HPW][4];
@@ -196,7 +204,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
   float m[HPW], l[HPW];
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
-    const int hr = wave + 4 * hi;
+    const int hr = hw + 4 * hi;
     const int hq = kvh * n_rep + (hr < n_rep ? hr : 0);
     const uint16_t* qrow = a.q + (size_t)(row_ok ? my_row : 0) * (a.H * D) + (size_t)hq * D;
 #pragma unroll
@@ -212,13 +220,13 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
 
   const uint16_t* kbase = a.kc + (size_t)kvh * a.max_seq * D;
   const uint16_t* vbase = a.vc + (size_t)kvh * a.max_seq * D;
-  // tile loads: items t and t + 256 are (position item / 16, dims 8 (item % 16) ..); the
-  // next tile's loads are in flight while this tile is multiplied
+  // tile loads: the group's items tg and tg + 256 are (position item / 16, dims
+  // 8 (item % 16) ..); the group's next tile is in flight while this one is multiplied
   u32x4 kv[2], vv[2];
   auto tile_load = [&](int kt) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int item = t + 256 * j;
+      const int item = tg + 256 * j;
       const int64_t p = (int64_t)kt * kPaKeys + (item >> 4);
       const bool ok = p <= last_pos;
       const size_t off = (size_t)(ok ? p : 0) * D + 8 * (item & 15);
@@ -227,27 +235,29 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
       if (!ok) { kv[j] = u32x4{0u, 0u, 0u, 0u}; vv[j] = kv[j]; }
     }
   };
-  tile_load(0);
-  for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();                                   // the previous tile is consumed
+  tile_load(g2);
+  for (int it = 0; it < nit; ++it) {
+    const int kt = 2 * it + g2;                        // past the last tile: all zero, skipped
+    __syncthreads();                                   // the previous tiles are consumed
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int item = t + 256 * j;
+      const int item = tg + 256 * j;
       const int kr = item >> 4, c8 = item & 15;
-      k_lds[kr][c8] = kv[j];
+      k_lds[kr * 17 + c8] = kv[j];
       const uint32_t vw[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        vt[8 * c8 + 2 * e][kr] = (uint16_t)(vw[e] & 0xffffu);
-        vt[8 * c8 + 2 * e + 1][kr] = (uint16_t)(vw[e] >> 16);
+        vt[(8 * c8 + 2 * e) * kPaVtPitch + kr] = (uint16_t)(vw[e] & 0xffffu);
+        vt[(8 * c8 + 2 * e + 1) * kPaVtPitch + kr] = (uint16_t)(vw[e] >> 16);
       }
     }
     __syncthreads();
-    if (kt + 1 < ntiles) tile_load(kt + 1);
+    if (kt + 2 < ntiles) tile_load(kt + 2);
+    if (kt >= ntiles) continue;                        // uniform over the wave
 
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
-      if (wave + 4 * hi >= n_rep) break;               // uniform over the wave
+      if (hw + 4 * hi >= n_rep) break;                 // uniform over the wave
       // S^T for positions kt*32 + [0, 16) and [16, 32)
       floatx4 s[2];
 #pragma unroll
@@ -255,7 +265,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
         s[h] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const bf16x8_t A = __builtin_bit_cast(bf16x8_t, k_lds[16 * h + lj][4 * c + lg]);
+          const bf16x8_t A = __builtin_bit_cast(bf16x8_t, k_lds[(16 * h + lj) * 17 + 4 * c + lg]);
           s[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8_t, qb[hi][c]),
                                                          s[h], 0, 0, 0);
         }
@@ -272,15 +282,17 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
         }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m[hi], mx);            // finite: position 0 is in tile 0
-      const float alpha = expf(m[hi] - m_new);
+      // a row may have no position yet in the odd group's tiles: m stays -inf, l 0, O 0
+      const float m_new = fmaxf(m[hi], mx);
+      const bool none = m_new == -INFINITY;
+      const float alpha = none ? 1.f : expf(m[hi] - m_new);
       float psum = 0.f;
       float pv[2][4];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pv[h][i] = expf(sv[h][i] - m_new);
+          pv[h][i] = none ? 0.f : expf(sv[h][i] - m_new);
           psum += pv[h][i];
         }
       psum += __shfl_xor(psum, 16);
@@ -292,7 +304,7 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
       const bf16x8_t P = __builtin_bit_cast(bf16x8_t, pw);
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
-        const uint16_t* vrow = &vt[16 * d + lj][0];
+        const uint16_t* vrow = vt + (16 * d + lj) * kPaVtPitch;
         const u32x2 v0 = *reinterpret_cast<const u32x2*>(vrow + 4 * lg);
         const u32x2 v1 = *reinterpret_cast<const u32x2*>(vrow + 16 + 4 * lg);
         const bf16x8_t A = __builtin_bit_cast(bf16x8_t, u32x4{v0.x, v0.y, v1.x, v1.y});
@@ -302,21 +314,38 @@ __global__ void __launch_bounds__(256) prefill_attn_kernel(PrefillAttnArgs a) {
     }
   }
 
-  // out[row][hq * 128 + 16 d + 4 lg + i] = bf16(O / l)
-  if (!row_ok) return;
-  uint16_t* orow = a.out + (size_t)my_row * a.ldo;
+  // The odd group hands (m, l, O) to the even group through LDS, head by head; the even
+  // group combines (its m is finite: position 0 is in tile 0) and writes
+  // out[row][hq * 128 + 16 d + 4 lg + i] = bf16(O / l).
+  float* mo = reinterpret_cast<float*>(lds_raw);        // [4 waves][32 values][64 lanes]
+  float* ml = mo + 4 * 32 * 64;                         // [4 waves][2][64 lanes]
+  uint16_t* orow = a.out + (size_t)(row_ok ? my_row : 0) * a.ldo;
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
-    const int hr = wave + 4 * hi;
-    if (hr >= n_rep) break;
+    const int hr = hw + 4 * hi;
+    __syncthreads();                                   // LDS free (tiles or previous head)
+    if (g2 == 1 && hr < n_rep) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mo[(hw * 32 + 4 * d + i) * 64 + lane] = o[hi][d][i];
+      ml[(hw * 2) * 64 + lane] = m[hi];
+      ml[(hw * 2 + 1) * 64 + lane] = l[hi];
+    }
+    __syncthreads();
+    if (g2 == 1 || hr >= n_rep || !row_ok) continue;
+    const float m1 = ml[(hw * 2) * 64 + lane], l1 = ml[(hw * 2 + 1) * 64 + lane];
+    const float mt = fmaxf(m[hi], m1);
+    const float a0 = expf(m[hi] - mt), a1 = m1 == -INFINITY ? 0.f : expf(m1 - mt);
+    const float inv = 1.f / (l[hi] * a0 + l1 * a1);
     const int hq = kvh * n_rep + hr;
-    const float inv = 1.f / l[hi];
 #pragma unroll
     for (int d = 0; d < 8; ++d)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const float v = o[hi][d][i] * a0 + mo[(hw * 32 + 4 * d + i) * 64 + lane] * a1;
         const int c = hq * D + 16 * d + 4 * lg + i;
-        orow[a.out_index ? a.out_index[c] : c] = (uint16_t)f32_to_bf16(o[hi][d][i] * inv);
+        orow[a.out_index ? a.out_index[c] : c] = (uint16_t)f32_to_bf16(v * inv);
       }
   }
 }
@@ -401,9 +430,9 @@ int mtl_prefill_attention(const void* q, const void* k_cache, const void* v_cach
   a.scale = scale;
   const dim3 grid(n_kv_heads, (unsigned)((rows + kPaRows - 1) / kPaRows));
   if (n_heads / n_kv_heads <= 4)
-    hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(prefill_attn_kernel<1>, grid, dim3(512), 0, (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(prefill_attn_kernel<2>, grid, dim3(512), 0, (hipStream_t)stream, a);
   return launch_status();
 }
 
