@@ -133,6 +133,19 @@ int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K,
                          int32_t inner_k_tiles, int32_t* packed, void* stream);
 
 /*
+ * torch's tiled int4 tensor -> packed int32 [K/8, N] (the mtl_int4pack_convert layout).
+ * Ingests the `.q` records of the reference's standalone export
+ * (moss_tts_lite/export.py:324-334, read back at export.py:691-734 and handed to
+ * torch._weight_int4pack_mm): the int32 [N/8, K/(16*T), 32, T/2] tensor that
+ * torch.ops.aten._convert_weight_to_int4pack(pre, T) returns on a ROCm GPU.
+ *   tiles          int32, N*K/8 words, 4-byte aligned
+ *   inner_k_tiles  T in {2, 4, 8} (the export writes 8)
+ *   N % 16 == 0, K % 256 == 0
+ */
+int mtl_int4pack_from_torch_tiles(const int32_t* tiles, int64_t N, int64_t K,
+                                  int32_t inner_k_tiles, int32_t* packed, void* stream);
+
+/*
  * Wave-contiguous copy of a qweight [K/8, N] for the decode-step GEMVs (load time):
  * 16-byte word l of 1 KB block ((s * N/64 + cg) * 16 + q) holds row 64s + 4q + l/16,
  * columns 64cg + 4(l%16) .. +3; rows past K/8 are zero.  Each GEMV wave then streams

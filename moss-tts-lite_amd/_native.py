@@ -33,6 +33,7 @@ _SIGNATURES = {
     "mtl_int4pack_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64,
                                _c_void_p, _c_void_p, _i64, _c_void_p]),
     "mtl_int4pack_convert": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+    "mtl_int4pack_from_torch_tiles": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
     "mtl_unpack_codes": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
     "mtl_gptq_dequant": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _i32,
                                 _c_void_p, _c_void_p]),

@@ -26,6 +26,40 @@ __global__ void int4pack_convert_kernel(const uint8_t* __restrict__ pre, int64_t
   }
 }
 
+// torch's tiled int4 tensor (ROCm layout of aten._convert_weight_to_int4pack, inner_k_tiles
+// T, half = T/2) -> qweight int32 [K/8, N].  torch stores 512-word blocks, one per
+// (16 columns, 256 channels), the channel block the faster index.  Within a block, code
+// (n, k) with r = k % 32, chunk j = (k % 256) / 32 and bits r4..r0 of r sits in word
+// (b * 32 + c) * half + d, nibble e, where b = 2 * (j / half) + r3, d = j % half,
+// c = 16 * r2 + n % 16 and e = r1 | r4 << 1 | r0 << 2.  Output word (q8, n) holds channels
+// 8q8 .. 8q8+7: r3 and r4 come from q8, r2 splits them between two torch words
+// (c = n % 16 for the first four, +16 for the last four).
+__global__ void int4pack_from_torch_kernel(const uint32_t* __restrict__ tiles, int64_t N,
+                                           int64_t K, int half, uint32_t* __restrict__ out) {
+  const int64_t rows = K / 8;
+  const int64_t total = rows * N;
+  const int64_t kb = K / 256;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q8 = t / N;
+    const int64_t n = t - q8 * N;
+    const int j = (int)(q8 >> 2) & 7;
+    const int r3 = (int)q8 & 1, r4 = (int)(q8 >> 1) & 1;
+    const int b = 2 * (j / half) + r3, d = j % half;
+    const int64_t base = ((n >> 4) * kb + (q8 >> 5)) * 512;
+    const uint32_t wa = tiles[base + (int64_t)(b * 32 + (int)(n & 15)) * half + d];
+    const uint32_t wb = tiles[base + (int64_t)(b * 32 + 16 + (int)(n & 15)) * half + d];
+    uint32_t w = 0;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t src = jj < 4 ? wa : wb;
+      const int e = ((jj >> 1) & 1) | (r4 << 1) | ((jj & 1) << 2);
+      w |= ((src >> (4 * e)) & 0xfu) << (4 * jj);
+    }
+    out[t] = w;
+  }
+}
+
 __global__ void unpack_codes_kernel(const uint32_t* __restrict__ qw, int64_t K, int64_t N,
                                     uint8_t* __restrict__ codes) {
   const int64_t total = (K / 8) * N;
@@ -158,6 +192,20 @@ int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K, int32_t
   const int64_t total = (K / 8) * N;
   hipLaunchKernelGGL(int4pack_convert_kernel, dim3(grid_for(total)), dim3(256), 0,
                      (hipStream_t)stream, prepacked, N, K, reinterpret_cast<uint32_t*>(packed));
+  return launch_status();
+}
+
+int mtl_int4pack_from_torch_tiles(const int32_t* tiles, int64_t N, int64_t K,
+                                  int32_t inner_k_tiles, int32_t* packed, void* stream) {
+  if (!tiles || !packed) return MTL_ERR_INVALID_ARG;
+  if (inner_k_tiles != 2 && inner_k_tiles != 4 && inner_k_tiles != 8) return MTL_ERR_INVALID_ARG;
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % 256 != 0) return MTL_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(tiles) & 3u) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+    return MTL_ERR_ALIGN;
+  const int64_t total = (K / 8) * N;
+  hipLaunchKernelGGL(int4pack_from_torch_kernel, dim3(grid_for(total)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(tiles), N, K,
+                     inner_k_tiles / 2, reinterpret_cast<uint32_t*>(packed));
   return launch_status();
 }
 

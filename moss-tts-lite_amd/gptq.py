@@ -298,10 +298,16 @@ class W4Dispatch:
     holds its group size, and linears listed in ``bf16_keep`` (a layer index keeps the
     whole layer, an ``(li, name)`` pair one linear) stay bf16 and run
     :func:`bf16_linear`.  A layer with nothing quantised has ``qlayers[li] = None``.
+
+    ``state`` records hold either the GPTQ state's unpacked codes (``{"q", "qsz"}``,
+    :func:`load_gptq_state`) or the standalone export's torch tiles (``{"packed",
+    "qsz"}``, :func:`moss_tts_lite_amd.export.read_standalone`); a record's linear need not
+    be in ``layers`` (it is placed on ``device`` then).
     """
 
     def __init__(self, layers: list, w4_group_size: int = 128, bf16_keep=(),
-                 group_size_map: dict | None = None, state: dict | None = None):
+                 group_size_map: dict | None = None, state: dict | None = None,
+                 device="cuda"):
         if w4_group_size not in (32, 64, 128, 256):
             raise ValueError("w4_group_size must be 32/64/128/256")
         self.layers = layers                       # per layer: name -> bf16 weight [N, K]
@@ -323,20 +329,23 @@ class W4Dispatch:
                 continue
             qd = {}
             for name in LIN_NAMES:
-                if (li, name) in self._keep_linears or name not in lyr:
+                rec = None if state is None else state.get(li, {}).get(name)
+                if (li, name) in self._keep_linears or (name not in lyr and rec is None):
                     continue
                 g = self.group_size_map[li][name]
-                rec = None if state is None else state[li][name]
+                dev = lyr[name].device if name in lyr else torch.device(device)
                 if rec is None:            # round-to-nearest from the bf16 weight (fast.py:86-101)
                     q, sc, mn = rtn_quantize(lyr[name], g)
                     qd[name] = pack_fast(q, sc, mn)
-                else:                      # calibrated codes + qsz (gptq.py:504-509, 664-687)
-                    dev = lyr[name].device
+                elif "q" in rec:           # calibrated codes + qsz (gptq.py:504-509, 664-687)
                     q = rec["q"].to(device=dev, dtype=torch.uint8)
                     pre = (q[:, 1::2] | (q[:, 0::2] << 4)).contiguous()
                     qd[name] = (ops.convert_weight_to_int4pack(pre, 8),
                                 rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous())
-                lyr.pop(name)
+                else:                      # standalone export: torch's tiles + qsz (export.py:712-734)
+                    qd[name] = (ops.int4pack_from_torch_tiles(rec["packed"].to(dev)),
+                                rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous())
+                lyr.pop(name, None)
             self.qlayers.append(qd if qd else None)
 
     def _linear(self, x: torch.Tensor, li: int, name: str) -> torch.Tensor:

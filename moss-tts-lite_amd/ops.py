@@ -191,6 +191,31 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
     return out
 
 
+def int4pack_from_torch_tiles(tiles: torch.Tensor) -> torch.Tensor:
+    """torch's tiled int4 tensor -> this build's int32 ``[K/8, N]`` (mtl_int4pack_from_torch_tiles).
+
+    ``tiles`` is int32 ``[N/8, K/(16T), 32, T/2]`` as ``aten._convert_weight_to_int4pack(pre,
+    T)`` returns it on a ROCm GPU: the ``.q`` records of the reference's standalone export
+    (moss_tts_lite/export.py:324-334).  N must be a multiple of 16 and K of 256.
+    """
+    if tiles.dtype != torch.int32 or tiles.dim() != 4 or tiles.shape[2] != 32:
+        raise RuntimeError("expected torch's int32 [N/8, K/(16*T), 32, T/2] int4 tiles")
+    t = 2 * tiles.shape[3]
+    n, k = tiles.shape[0] * 8, tiles.shape[1] * 16 * t
+    if t not in (2, 4, 8):
+        raise RuntimeError("innerKTiles must be 2, 4 or 8")
+    if n % 16 or k % 256:
+        raise RuntimeError(f"N={n} must be a multiple of 16 and K={k} a multiple of 256")
+    if tiles.device.type != "cuda":
+        raise RuntimeError("int4 tiles must be on the GPU")
+    src = tiles.contiguous()
+    out = torch.empty(k // 8, n, dtype=torch.int32, device=src.device)
+    N.check(N.load().mtl_int4pack_from_torch_tiles(src.data_ptr(), n, k, t, out.data_ptr(),
+                                                   _stream(src.device)),
+            "mtl_int4pack_from_torch_tiles")
+    return out
+
+
 def tile_weights(qweight: torch.Tensor) -> torch.Tensor:
     """Wave-contiguous copy of ``qweight [K/8, N]`` for the decode-step GEMVs
     (``mtl_w4_tile``); N must be a multiple of 64."""

@@ -254,6 +254,51 @@ def int4pack_from_prepacked(p_u8: np.ndarray) -> np.ndarray:
     return qweight_from_reference_codes(unprepack_u8(p_u8))
 
 
+def torch_tile_locate(n, k, K: int, inner_k_tiles: int):
+    """(word, nibble) of code ``(n, k)`` in torch's tiled int4 tensor on ROCm.
+
+    The tensor is what ``torch.ops.aten._convert_weight_to_int4pack(pre, T)`` returns on
+    a ROCm GPU (int32 ``[N/8, K/(16T), 32, T/2]``), the ``.q`` record of the reference's
+    standalone export (moss_tts_lite/export.py:324-334).  Words form 512-word blocks,
+    one per (16 columns, 256 channels), the channel block the faster index.  Within a
+    block, with ``r = k % 32`` (bits r4..r0) and ``j = (k % 256) // 32``: word
+    ``(b * 32 + c) * T/2 + d`` with ``b = 2 * (j // (T/2)) + r3``, ``d = j % (T/2)``,
+    ``c = 16 * r2 + n % 16``; nibble ``r1 | r4 << 1 | r0 << 2``.  Pinned against torch
+    2.10+rocm7.0's packer on gfx950 (every nibble of separable code patterns, and the
+    random-code fixtures in tests/golden).
+    """
+    n = np.asarray(n, np.int64)
+    k = np.asarray(k, np.int64)
+    half = inner_k_tiles // 2
+    r = k % 32
+    j = (k % 256) // 32
+    b = 2 * (j // half) + ((r >> 3) & 1)
+    c = 16 * ((r >> 2) & 1) + n % 16
+    word = (n // 16 * (K // 256) + k // 256) * 512 + (b * 32 + c) * half + j % half
+    nib = ((r >> 1) & 1) | (((r >> 4) & 1) << 1) | ((r & 1) << 2)
+    return word, nib
+
+
+def torch_tiles_pack(q_nk: np.ndarray, inner_k_tiles: int) -> np.ndarray:
+    """Codes ``uint8 [N, K]`` -> torch's tiled int32 ``[N/8, K/(16T), 32, T/2]`` (ROCm)."""
+    q = np.asarray(q_nk, np.uint8)
+    n_, k_ = q.shape
+    nn, kk = np.meshgrid(np.arange(n_), np.arange(k_), indexing="ij")
+    word, nib = torch_tile_locate(nn.ravel(), kk.ravel(), k_, inner_k_tiles)
+    out = np.zeros(n_ * k_ // 8, np.uint32)
+    np.bitwise_or.at(out, word, q.ravel().astype(np.uint32) << (4 * nib).astype(np.uint32))
+    t = inner_k_tiles
+    return out.view(np.int32).reshape(n_ // 8, k_ // (16 * t), 32, t // 2)
+
+
+def torch_tiles_unpack(tiles: np.ndarray, n_: int, k_: int, inner_k_tiles: int) -> np.ndarray:
+    """torch's tiled int32 tensor (ROCm) -> codes ``uint8 [N, K]``."""
+    w = np.asarray(tiles).reshape(-1).view(np.uint32)
+    nn, kk = np.meshgrid(np.arange(n_), np.arange(k_), indexing="ij")
+    word, nib = torch_tile_locate(nn, kk, k_, inner_k_tiles)
+    return ((w[word] >> (4 * nib).astype(np.uint32)) & 0xF).astype(np.uint8)
+
+
 def qsz_as_gptq_meta(qsz: np.ndarray):
     """Split reference ``qsz`` bits into float32 ``(scale [G, N], zero [G, N])``."""
     return bf16_bits_to_f32(qsz[:, :, 0]), bf16_bits_to_f32(qsz[:, :, 1])

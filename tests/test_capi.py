@@ -212,6 +212,12 @@ def test_prefill_row_entry_validation(lib):
 def test_converter_validation(lib):
     assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE
+    tt = lib.mtl_int4pack_from_torch_tiles
+    assert tt(None, 64, 512, 8, FAKE, None) == N.MTL_ERR_INVALID_ARG
+    assert tt(FAKE, 64, 512, 6, FAKE, None) == N.MTL_ERR_INVALID_ARG
+    assert tt(FAKE, 56, 512, 8, FAKE, None) == N.MTL_ERR_SHAPE      # N % 16
+    assert tt(FAKE, 64, 384, 8, FAKE, None) == N.MTL_ERR_SHAPE      # K % 256
+    assert tt(ctypes.c_void_p(0x1002), 64, 512, 8, FAKE, None) == N.MTL_ERR_ALIGN
 
 
 def test_load_gptq_state_safe_loader(tmp_path):

@@ -5,6 +5,8 @@ on tiny inputs, known-answer words, torch's independent CPU int4 kernel, and the
 exact special cases of the closed forms.  Nothing here retypes a formula as its
 own check.
 """
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -191,3 +193,59 @@ def test_gptq_gemm_against_float64_brute_force():
                 gg = case["g_idx"][k]
                 acc += x[m, k] * (int(codes[k, n]) - int(z[gg, n])) * s[gg, n]
             assert abs(acc - case["y_ref"][m, n]) <= 1e-9 * max(1.0, abs(acc))
+
+
+# -- torch's tiled int4 tensor (the standalone export's `.q`, export.py:324-334) ---------
+
+_TILE_FIXTURES = Path(__file__).parent / "golden" / "int4pack_fixtures.npz"
+
+
+def _tile_cases():
+    z = np.load(_TILE_FIXTURES, allow_pickle=False)
+    for key in sorted(z.files):
+        if key.startswith("pre_"):
+            tag = key[4:]
+            n, k = map(int, tag.split("_t")[0].split("x"))
+            yield tag, n, k, int(tag.split("_t")[1]), G.unprepack_u8(z[key]), z["packed_" + tag]
+
+
+def test_torch_tiles_fixture_provenance():
+    z = np.load(_TILE_FIXTURES, allow_pickle=False)
+    assert "rocm" in str(z["torch_version"])
+    assert {t for t, *_ in _tile_cases()} == {"64x512_t2", "64x512_t4", "64x512_t8", "48x256_t8"}
+
+
+@pytest.mark.parametrize("case", list(_tile_cases()), ids=lambda c: c[0])
+def test_torch_tiles_match_torch_rocm_packer(case):
+    # torch's own packer output (tests/golden) decodes to the codes it was given, and the
+    # restatement re-packs them to the same words
+    tag, n, k, t, codes, packed = case
+    assert packed.shape == (n // 8, k // (16 * t), 32, t // 2) and packed.dtype == np.int32
+    np.testing.assert_array_equal(G.torch_tiles_unpack(packed, n, k, t), codes)
+    np.testing.assert_array_equal(G.torch_tiles_pack(codes, t), packed)
+
+
+def test_torch_tile_locate_is_a_bijection():
+    for n, k, t in ((64, 512, 2), (32, 1024, 4), (48, 768, 8)):
+        nn, kk = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+        word, nib = G.torch_tile_locate(nn.ravel(), kk.ravel(), k, t)
+        slots = np.sort(word * 8 + nib)
+        np.testing.assert_array_equal(slots, np.arange(n * k))
+
+
+def test_torch_int4pack_mm_fixture_matches_closed_form():
+    # y from torch._weight_int4pack_mm on ROCm (tests/golden) == x @ effective_weight^T:
+    # pins the qsz contract (q - 8) * scale + zero together with the tile layout
+    z = np.load(_TILE_FIXTURES, allow_pickle=False)
+    m, n, k, g, t = (int(v) for v in z["mm_meta"])
+    codes = G.unprepack_u8(z["mm_pre"])
+    qsz = z["mm_qsz_bits"].view(np.uint16)
+    x = bf16_bits_to_f32(z["mm_x_bits"].view(np.uint16))
+    y_torch = bf16_bits_to_f32(z["mm_y_bits"].view(np.uint16)).astype(np.float64)
+    w = G.effective_weight(codes, qsz, g)
+    y = G.gemm_f64(x, w.T)
+    rel = np.linalg.norm(y - y_torch) / np.linalg.norm(y)
+    assert rel < 1e-2, rel
+    # a transposed group order of the metadata does not pass
+    w_bad = G.effective_weight(codes, qsz[::-1].copy(), g)
+    assert np.linalg.norm(G.gemm_f64(x, w_bad.T) - y_torch) / np.linalg.norm(y) > 5e-2
