@@ -1,4 +1,5 @@
-"""GPU parity of the standalone-export ingestion (moss_tts_lite/export.py:324-334, 691-769).
+"""GPU parity of the standalone-export ingestion (moss_tts_lite/export.py:324-334, 691-769)
+and of the drop-in int4 operators against torch's own ROCm packer and int4 GEMM.
 
 The export's ``.q`` records are torch's tiled int4 tensors.  Bars: the converted
 ``[K/8, N]`` words bit-exact against this build's packer of the same codes (torch's tiles
@@ -106,3 +107,25 @@ def test_ingested_export_matches_torch_int4pack_mm(dev, tmp_path):
         y_ref = G.gemm_f64(xb, G.effective_weight(codes, qsz.view(torch.int16).numpy().view(np.uint16), g).T)
         assert rel_l2(y, y_torch) < 1e-2, (name, rel_l2(y, y_torch))
         assert rel_l2(y, y_ref) < 1e-2, (name, rel_l2(y, y_ref))
+
+
+@pytest.mark.parametrize("m,k,n,g", [(1, 4096, 4096, 128), (1, 4096, 24576, 128),
+                                     (1, 12288, 4096, 128), (16, 4096, 6144, 128),
+                                     (3, 4096, 4096, 32), (5, 2048, 1024, 64),
+                                     (2, 4096, 2048, 256)])
+def test_drop_in_matches_torch_int4_operators(dev, m, k, n, g):
+    # the reference's two operators on ROCm (fast.py:97-99, 118): torch's packer + int4 GEMM,
+    # against this build's drop-ins on the same pre-pack bytes, qsz and x
+    print("shape", m, k, n, g, flush=True)
+    gen = torch.Generator().manual_seed(m * 131 + k + n + g)
+    codes = torch.randint(0, 16, (n, k), generator=gen, dtype=torch.int32)
+    pre = _prepack(codes).to(dev)
+    sc = torch.rand(k // g, n, generator=gen) * 0.02 + 0.002
+    zr = torch.rand(k // g, n, generator=gen) * 0.2 - 0.1
+    qsz = torch.stack([sc, zr], 2).to(torch.bfloat16).to(dev).contiguous()
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(dev)
+    y_torch = torch._weight_int4pack_mm(x, torch.ops.aten._convert_weight_to_int4pack(pre, 8), g, qsz)
+    y = ops.weight_int4pack_mm(x, ops.convert_weight_to_int4pack(pre, 8), g, qsz)
+    assert y.dtype == y_torch.dtype == torch.bfloat16 and y.shape == y_torch.shape
+    r = rel_l2(y.float().cpu().numpy(), y_torch.float().cpu().numpy())
+    assert r < 1e-2, r
