@@ -505,13 +505,72 @@ def cpu_baseline_decode(budget_s: float = 20.0):
                       f"151936x4096 head ({t_head:.2f} s scaled), scaled to 36 layers"}
 
 
+def bench_int4_op(args, torch):
+    """The reference's decode operator beside this build's kernels, same GPU, graph-captured:
+    ``torch._weight_int4pack_mm`` on torch's own packed weights (moss_tts_lite/fast.py:118,
+    the reference's int4 linear) and the ``mtl_int4pack_mm`` drop-in, M = 1, g = 128, on
+    the four decode-step projections.  Each timing replays a graph of ``steps`` launches
+    rotating over enough weight copies (>= 400 MB) that no launch reads from the 256 MB
+    Infinity Cache."""
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+    __graft_entry__.import_package()
+    from moss_tts_lite_amd import ops
+    dev = torch.device("cuda:0")
+    steps = args.steps or 96
+    shapes = {"qkv": (4096, 6144), "o": (4096, 4096), "gate_up": (4096, 24576), "down": (12288, 4096)}
+    gen = torch.Generator(device="cpu").manual_seed(11)
+    out = {}
+    for name, (k, n) in shapes.items():
+        copies = int(400e6 // (k * n // 2)) + 1
+        ws = []
+        for _ in range(copies):
+            c = torch.randint(0, 16, (n, k), generator=gen, dtype=torch.int32).to(dev)
+            pre = (c[:, 1::2] | (c[:, 0::2] << 4)).to(torch.uint8).contiguous()
+            qsz = torch.stack([torch.rand(k // 128, n, generator=gen) * 0.02 + 0.002,
+                               torch.rand(k // 128, n, generator=gen) * 0.2 - 0.1],
+                              2).to(torch.bfloat16).to(dev).contiguous()
+            ws.append((torch.ops.aten._convert_weight_to_int4pack(pre, 8),
+                       ops.convert_weight_to_int4pack(pre, 8), qsz))
+            del c, pre
+        x = torch.randn(1, k, generator=gen).to(torch.bfloat16).to(dev)
+        res = {}
+        for label, fn in (("torch_weight_int4pack_mm", lambda w: torch._weight_int4pack_mm(x, w[0], 128, w[2])),
+                          ("mtl_int4pack_mm", lambda w: ops.weight_int4pack_mm(x, w[1], 128, w[2]))):
+            for w in ws:
+                fn(w)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(steps):
+                    fn(ws[i % copies])
+            g.replay()
+            torch.cuda.synchronize()
+            best = 1e9
+            for _ in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                g.replay()
+                b.record()
+                torch.cuda.synchronize()
+                best = min(best, a.elapsed_time(b) * 1e3 / steps)
+            res[label] = round(best, 3)
+            del g
+        res["weight_mb"] = round(k * n / 2 / 1e6, 2)
+        out[name] = res
+        print(f"{name}: {res}", file=sys.stderr, flush=True)
+        del ws
+    print(json.dumps({"workload": "int4_op", "m": 1, "group": 128, "launches_each": steps,
+                      "us_per_launch": out}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "kernels", "prefill"])
+                    choices=["decode", "gemv", "kernels", "prefill", "int4-op"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--group", type=int, default=128, choices=[32, 64, 128, 256],
                     help="int4 group size of every projection (decode workload)")
@@ -539,6 +598,8 @@ def main():
         args.steps = 72 if args.steps is None else args.steps
         bench_kernels(args, torch)
         return
+    if args.workload == "int4-op":
+        return bench_int4_op(args, torch)
     if args.workload == "prefill":
         args.steps = 20 if args.steps is None else args.steps
         bench_prefill(args, torch)
