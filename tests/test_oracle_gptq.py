@@ -249,3 +249,31 @@ def test_torch_int4pack_mm_fixture_matches_closed_form():
     # a transposed group order of the metadata does not pass
     w_bad = G.effective_weight(codes, qsz[::-1].copy(), g)
     assert np.linalg.norm(G.gemm_f64(x, w_bad.T) - y_torch) / np.linalg.norm(y) > 5e-2
+
+
+def test_torch_tile_fixtures_reject_plausible_mistakes():
+    # each variant of the tile formula with one plausible slip (nibble bits swapped, the
+    # column half-select dropped, the channel-block order transposed) misreads torch's tiles
+    tag, n, k, t, codes, packed = next(c for c in _tile_cases() if c[0] == "64x512_t8")
+    w = packed.reshape(-1).view(np.uint32)
+    nn, kk = np.meshgrid(np.arange(n), np.arange(k), indexing="ij")
+    half = t // 2
+
+    def read(word, nib):
+        return ((w[word] >> (4 * nib).astype(np.uint32)) & 0xF).astype(np.uint8)
+
+    r, j = kk % 32, (kk % 256) // 32
+    b = 2 * (j // half) + ((r >> 3) & 1)
+    c = 16 * ((r >> 2) & 1) + nn % 16
+    good_nib = ((r >> 1) & 1) | (((r >> 4) & 1) << 1) | ((r & 1) << 2)
+    block = nn // 16 * (k // 256) + kk // 256
+    word = block * 512 + (b * 32 + c) * half + j % half
+    np.testing.assert_array_equal(read(word, good_nib), codes)
+    slips = {
+        "nibble bits r0/r1 swapped": (word, (r & 1) | (((r >> 4) & 1) << 1) | (((r >> 1) & 1) << 2)),
+        "column half-select dropped": (block * 512 + (b * 32 + nn % 16) * half + j % half, good_nib),
+        "block order transposed": ((kk // 256 * (n // 16) + nn // 16) * 512
+                                   + (b * 32 + c) * half + j % half, good_nib),
+    }
+    for name, (wd, nb) in slips.items():
+        assert (read(wd, nb) != codes).mean() > 0.25, name      # and fails exact equality
