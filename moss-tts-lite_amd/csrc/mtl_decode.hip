@@ -537,7 +537,9 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] *= corr;
       m = mn;
-      e_lds[wave][(lane & 3) * 16 + (lane >> 2)] = e;   // position ps+4i at ps*16+i
+      // the value sum takes e rounded to bf16, the sum l the unrounded e: the form of
+      // torch's fused SDPA on bf16 tensors (moss_tts_lite/model.py:183-189)
+      e_lds[wave][(lane & 3) * 16 + (lane >> 2)] = round_bf16(e);   // position ps+4i at ps*16+i
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -721,7 +723,8 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const float e = expf(sv[r] - M);                  // 0 for masked positions
-    if (hd < n_rep) e_lds[hd][16 * wave + 4 * g + r] = e;
+    // value sum over bf16(e), sum over e: torch's fused SDPA form (model.py:183-189)
+    if (hd < n_rep) e_lds[hd][16 * wave + 4 * g + r] = round_bf16(e);
     lsum += e;
   }
   lsum += __shfl_xor(lsum, 16);

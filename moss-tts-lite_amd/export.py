@@ -1,15 +1,24 @@
-"""Reader of the reference's standalone GPTQ export (moss_tts_lite/export.py:639-734).
+"""Reads the reference's standalone GPTQ export directories (moss_tts_lite/export.py).
 
-A standalone directory holds ``meta.json`` (``"format": "moss_tts_lite.standalone-gptq"``)
-and one safetensors file whose int4 linears are ``layers.{i}.{proj}.q`` (int32: torch's
-tiled int4 tensor, ``aten._convert_weight_to_int4pack(pre, 8)``) and
-``layers.{i}.{proj}.qsz`` (bf16 ``[K/g, N, 2]``); every other tensor is a bf16 weight.
-:func:`read_standalone` returns what the reference's does, the ``(meta, weights, state,
-group_size_map, bf16_keep)`` tuple, with ``state[li][proj] = {"packed", "qsz"}`` as read
-from the file.  :class:`moss_tts_lite_amd.gptq.W4Dispatch` takes that state and converts
-each ``packed`` into this build's layout on the GPU (``ops.int4pack_from_torch_tiles``).
+What a directory holds (the on-disk format, moss_tts_lite/export.py:29-32, 55, 424-438):
+- ``meta.json`` with ``"format": "moss_tts_lite.standalone-gptq"``, the preset name, the
+  weight file's name, per-preset group sizes and bf16 keeps, and ``tool.torch``, the
+  torch build that wrote the file;
+- one safetensors file (``quantized.safetensors`` unless ``weight_file.name`` says
+  otherwise). Its tensors named ``layers.{i}.{linear}.q`` are int4 weights in torch's tiled
+  int4 layout (``aten._convert_weight_to_int4pack(pre, 8)``), ``layers.{i}.{linear}.qsz``
+  their bf16 ``[K/g, N, 2]`` scales and zeros, and every other tensor is a plain weight.
 
-Files are read with safetensors and json only: nothing in them is executed.
+:func:`read_standalone` returns the reference reader's tuple ``(meta, weights, state,
+group_size_map, bf16_keep)``. There ``state[layer][linear] = {"packed", "qsz"}`` holds the
+tensors as stored. :class:`moss_tts_lite_amd.gptq.W4Dispatch` turns each ``packed`` into
+this build's layout on the GPU (``ops.int4pack_from_torch_tiles``).
+
+torch's tiled layout is not the same on every backend, and this build reads the ROCm one
+only. A directory whose ``tool.torch`` does not name a ROCm build is refused with
+``ValueError`` rather than decoded into wrong weights.
+
+Only json and safetensors touch the files, so nothing in them is executed.
 """
 from __future__ import annotations
 
@@ -22,89 +31,111 @@ import torch
 from .gptq import LIN_NAMES
 
 __all__ = ["FORMAT_TAG", "META_FILE", "Q_FILE", "is_standalone_dir", "standalone_presets",
-           "read_standalone"]
+           "read_standalone", "tiles_backend"]
 
-# names of the reference's format (export.py:29-32) and its record keys (export.py:55)
 FORMAT_TAG = "moss_tts_lite.standalone-gptq"
 Q_FILE = "quantized.safetensors"
 META_FILE = "meta.json"
-_Q_KEY = re.compile(r"^layers\.(\d+)\.(" + "|".join(LIN_NAMES) + r")\.(q|qsz)$")
-_RECORD = {"q": "packed", "qsz": "qsz"}
+
+# "layers.<i>.<linear>.<q|qsz>"
+_INT4_NAME = re.compile(r"layers\.(?P<layer>\d+)\.(?P<linear>%s)\.(?P<part>qsz|q)"
+                        % "|".join(LIN_NAMES))
+_PART_FIELD = {"q": "packed", "qsz": "qsz"}
 
 
-def _meta(path: str) -> dict:
-    with open(os.path.join(path, META_FILE), encoding="utf-8") as f:
-        return json.load(f)
+def _load_meta(model_dir: str) -> dict:
+    with open(os.path.join(model_dir, META_FILE), encoding="utf-8") as fh:
+        return json.load(fh)
 
 
 def is_standalone_dir(path: str) -> bool:
-    """True if ``path`` holds a standalone export's ``meta.json`` (export.py:639-649)."""
-    if not os.path.isfile(os.path.join(path, META_FILE)):
-        return False
+    """Whether ``path`` holds a readable ``meta.json`` carrying the standalone format tag
+    (the reference's test, export.py:639-649)."""
     try:
-        meta = _meta(path)
-    except (OSError, json.JSONDecodeError):
+        return _load_meta(path).get("format") == FORMAT_TAG
+    except (OSError, ValueError):
         return False
-    return meta.get("format") == FORMAT_TAG
 
 
 def standalone_presets(path: str) -> list[str]:
-    """Preset names a standalone directory offers (export.py:651-657)."""
-    meta = _meta(path)
-    names = list(meta.get("presets") or {})
-    if not names and meta.get("preset_name"):
-        names = [meta["preset_name"]]
-    return names
+    """The presets a directory offers (export.py:651-657): the keys of ``presets``, or
+    the lone ``preset_name`` of a directory without that table."""
+    meta = _load_meta(path)
+    table = meta.get("presets") or {}
+    if table:
+        return list(table)
+    return [meta["preset_name"]] if meta.get("preset_name") else []
 
 
-def _read_safetensors(path: str) -> dict[str, torch.Tensor]:
-    from safetensors import safe_open
-    out = {}
-    with safe_open(path, framework="pt", device="cpu") as f:
-        for key in f.keys():
-            out[key] = f.get_tensor(key)
-    return out
+def tiles_backend(meta: dict) -> str:
+    """``"rocm"`` when ``meta.tool.torch`` names a ROCm build of torch, else the version
+    string found (``""`` when the export does not say)."""
+    version = str(((meta.get("tool") or {}).get("torch")) or "")
+    return "rocm" if "+rocm" in version else version
+
+
+def _pair(key: str) -> tuple[int, str]:
+    layer, _, linear = key.partition(":")
+    return int(layer), linear
+
+
+def _preset_tables(meta: dict) -> tuple[dict, list]:
+    preset = (meta.get("presets") or {}).get(meta.get("preset_name"), {})
+    gmap = {_pair(k): int(g) for k, g in (preset.get("group_size_map") or {}).items()}
+    keep: list = [_pair(k) for k in (preset.get("bf16_linears") or [])]
+    keep.extend(int(layer) for layer in (preset.get("bf16_layers") or []))
+    return gmap, keep
+
+
+def _weight_path(model_dir: str, meta: dict) -> str:
+    entry = meta.get("weight_file")
+    name = entry.get("name", Q_FILE) if isinstance(entry, dict) else Q_FILE
+    return os.path.join(model_dir, name)
 
 
 def read_standalone(model_dir: str, expected_preset: str | None = None):
-    """Read a standalone directory (export.py:691-734): ``(meta, weights, state, gmap, keep)``.
+    """``(meta, weights, state, group_size_map, bf16_keep)`` of a standalone directory,
+    with the reference reader's meaning (export.py:691-734).
 
-    ``state[li][proj]`` is ``{"packed": int32 torch tiles, "qsz": bf16 [K/g, N, 2]}``,
-    ``gmap[(li, proj)]`` the per-linear group size of the preset, ``keep`` the bf16-kept
-    linears ``(li, proj)`` and layers ``li``.  Raises ``ValueError`` for a directory of
-    another format or a record missing its ``q`` or ``qsz``, ``SystemExit`` when
-    ``expected_preset`` is not the directory's preset, ``FileNotFoundError`` for a missing
-    weight file.
+    Raises:
+    - ``ValueError``: the directory is of another format; an int4 record lacks its ``q``
+      or ``qsz``; or its tiles were written by a torch build other than ROCm's.
+    - ``SystemExit``: ``expected_preset`` is not the directory's preset (the reference
+      stops there too).
+    - ``FileNotFoundError``: the weight file is missing.
     """
-    meta = _meta(model_dir)
+    meta = _load_meta(model_dir)
     if meta.get("format") != FORMAT_TAG:
-        raise ValueError(f"{os.path.join(model_dir, META_FILE)} is not a {FORMAT_TAG} directory")
+        raise ValueError(f"{model_dir}: meta.json has format {meta.get('format')!r}, "
+                         f"expected {FORMAT_TAG!r}")
     preset = meta.get("preset_name")
     if expected_preset and expected_preset != preset:
-        raise SystemExit(f"[export] {model_dir} provides preset {preset!r} only, but "
-                         f"{expected_preset!r} was requested. Available: "
-                         f"{standalone_presets(model_dir)}")
-    wf = meta.get("weight_file")
-    qfile = os.path.join(model_dir, wf["name"] if isinstance(wf, dict) else Q_FILE)
-    if not os.path.isfile(qfile):
-        raise FileNotFoundError(f"{qfile} not found in {model_dir}")
+        raise SystemExit(f"{model_dir} holds preset {preset!r}, not {expected_preset!r} "
+                         f"(presets offered: {standalone_presets(model_dir)})")
+    path = _weight_path(model_dir, meta)
+    if not os.path.isfile(path):
+        raise FileNotFoundError(f"weight file {path} is missing")
+    from safetensors import safe_open
+
     weights: dict[str, torch.Tensor] = {}
     state: dict[int, dict[str, dict[str, torch.Tensor]]] = {}
-    for key, t in _read_safetensors(qfile).items():
-        m = _Q_KEY.match(key)
-        if m:
-            state.setdefault(int(m.group(1)), {}).setdefault(m.group(2), {})[_RECORD[m.group(3)]] = t
-        else:
-            weights[key] = t
-    for li, projs in state.items():
-        for proj, rec in projs.items():
-            if set(rec) != {"packed", "qsz"}:
-                raise ValueError(f"incomplete record for layer {li} {proj}: {sorted(rec)}")
-    pmeta = (meta.get("presets") or {}).get(preset, {})
-    gmap = {}
-    for key, val in (pmeta.get("group_size_map") or {}).items():
-        a, b = key.split(":")
-        gmap[(int(a), b)] = int(val)
-    keep: list = [(int(x.split(":")[0]), x.split(":")[1]) for x in (pmeta.get("bf16_linears") or [])]
-    keep += [int(x) for x in (pmeta.get("bf16_layers") or [])]
+    with safe_open(path, framework="pt", device="cpu") as fh:
+        for name in fh.keys():
+            hit = _INT4_NAME.fullmatch(name)
+            if hit is None:
+                weights[name] = fh.get_tensor(name)
+                continue
+            rec = state.setdefault(int(hit["layer"]), {}).setdefault(hit["linear"], {})
+            rec[_PART_FIELD[hit["part"]]] = fh.get_tensor(name)
+    for layer in sorted(state):
+        for linear, rec in state[layer].items():
+            missing = {"packed", "qsz"} - set(rec)
+            if missing:
+                raise ValueError(f"{model_dir}: layer {layer} {linear} has an incomplete "
+                                 f"int4 record (no {', '.join(sorted(missing))})")
+    if state and tiles_backend(meta) != "rocm":
+        raise ValueError(f"{model_dir}: its int4 tiles were written by torch "
+                         f"{tiles_backend(meta) or '(version not recorded)'}; only the "
+                         "tile layout of ROCm builds is read here")
+    gmap, keep = _preset_tables(meta)
     return meta, weights, state, gmap, keep

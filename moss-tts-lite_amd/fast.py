@@ -67,6 +67,26 @@ def _gather(w: torch.Tensor, perm: torch.Tensor | None) -> torch.Tensor:
     return w if perm is None else w[perm.long()].contiguous()
 
 
+def _check_ids(ids, limits) -> None:
+    """``ValueError`` unless every id of each column lies inside its embedding table
+    (``limits[c]`` rows for column c), as the reference's embedding lookups require
+    (model.py:156-161). ``ids`` is ``[rows, columns]`` (host or device)."""
+    t = torch.as_tensor(ids).reshape(-1, len(limits)).to("cpu", torch.int64)
+    lim = torch.tensor(limits, dtype=torch.int64)
+    bad = (t < 0) | (t >= lim)
+    if bool(bad.any()):
+        r, c = (int(v) for v in bad.nonzero()[0])
+        raise ValueError(f"id {int(t[r, c])} in column {c} is outside its embedding table "
+                         f"of {int(lim[c])} rows")
+
+
+def _check_pos(pos: int, max_seq: int) -> int:
+    pos = int(pos)
+    if not 0 <= pos < max_seq:
+        raise ValueError(f"position {pos} is outside the KV cache of {max_seq} positions")
+    return pos
+
+
 class FastDecoder:
     """One decode step over an :class:`Int4Backbone` (eager or hipGraph replay)."""
 
@@ -152,7 +172,8 @@ class FastDecoder:
         self.logits = torch.zeros(cfg.vocab, dtype=torch.bfloat16, device=dev)
         self.table_ptrs = torch.tensor([self.m.embed_tokens.data_ptr()], dtype=torch.int64,
                                        device=dev)
-        self.vocabs = torch.tensor([cfg.vocab], dtype=torch.int64, device=dev)
+        self.id_limits = [cfg.text_embed_rows]
+        self.vocabs = torch.tensor(self.id_limits, dtype=torch.int64, device=dev)
 
     # -- launch plan ------------------------------------------------------------------
     def _gemm(self, x, lin, n, epilogue, resid, y, no_perm=False):
@@ -509,13 +530,16 @@ class FastDecoder:
         self.graph = g
 
     def step(self, token: int | None = None, pos: int | None = None) -> torch.Tensor:
-        """One replayed step; returns the (device) next-token buffer."""
+        """One replayed step; returns the (device) next-token buffer. ``token`` and ``pos``
+        (host ints) replace the device-side ones; ``ValueError`` for a token outside the
+        embedding or a position outside the KV cache."""
         if self.graph is None:
             raise RuntimeError("call capture() first")
         if token is not None:
+            _check_ids([int(token)], self.id_limits)
             self.ids.fill_(int(token))
         if pos is not None:
-            self.pos.fill_(int(pos))
+            self.pos.fill_(_check_pos(pos, self.m.cfg.max_seq))
         self.graph.replay()
         return self.ids
 
@@ -552,6 +576,7 @@ class FastDecoder:
         launch covering all L rows.  Returns the residual stream after the last layer,
         bf16 ``[L, hidden]`` (a view of an internal buffer)."""
         m, cfg = self.m, self.m.cfg
+        _check_ids(ids, self.id_limits)
         ids = ids.to(device=self.dev, dtype=torch.int64).reshape(-1, self.table_ptrs.numel())
         rows = ids.shape[0]
         if rows < 1 or pos0 < 0 or pos0 + rows > cfg.max_seq:
@@ -634,6 +659,7 @@ class FastDecoder:
 
     def prefill_stepwise(self, token_ids: torch.Tensor) -> None:
         """The same prompt as one decode step per token (eager); same end state."""
+        _check_ids(token_ids, self.id_limits)
         toks = token_ids.to(device=self.dev, dtype=torch.int64).reshape(-1)
         if toks.numel() > self.m.cfg.max_seq:
             raise ValueError("prompt longer than the KV cache")
@@ -679,8 +705,8 @@ class FastMossDecoder(FastDecoder):
         self.table_ptrs = torch.tensor([m.embed_tokens.data_ptr()] +
                                        [t.data_ptr() for t in m.emb_ext], dtype=torch.int64,
                                        device=dev)
-        self.vocabs = torch.tensor([cfg.vocab] + [cfg.audio_vocab] * cfg.n_vq, dtype=torch.int64,
-                                   device=dev)
+        self.id_limits = [cfg.text_embed_rows] + [cfg.audio_vocab] * cfg.n_vq
+        self.vocabs = torch.tensor(self.id_limits, dtype=torch.int64, device=dev)
         self.lt = torch.zeros(cfg.vocab, dtype=bf, device=dev)
         self.la = torch.zeros(cfg.n_vq, cfg.audio_vocab, dtype=bf, device=dev)
         self.two = torch.zeros(2, dtype=bf, device=dev)
@@ -735,17 +761,24 @@ class FastMossDecoder(FastDecoder):
     def step(self, row: torch.Tensor | None, pos: int, audio2: bool = False):
         """Replay one decode step for ``row`` ([1 + n_vq] ids) at cache position ``pos``.
 
+        ``ValueError`` for a position outside the KV cache or, for a host ``row``, an id
+        outside its table. A row already on the device is used as is: an id outside its
+        table there sums a zero row into the embedding.
+
         Returns ``(lt, la, h_final, two)`` like ``FastMossTTS.step``: the text logits
         (stale in the audio2 variant), audio logits ``[n_vq, audio_vocab]``, the normed
         final hidden state and the 2-way logits (stale in the text variant).
         """
         if self.graphs is None:
             raise RuntimeError("call capture() first")
+        pos = _check_pos(pos, self.m.cfg.max_seq)
         if row is not None:
-            src = row.reshape(-1)
+            src = torch.as_tensor(row).reshape(-1)
+            if src.device.type == "cpu":      # host rows are checked; device rows are not
+                _check_ids(src, self.id_limits)  # read back (a sync per step)
             if src.data_ptr() != self.ids.data_ptr():
                 self.ids.copy_(src)
-        self.pos.fill_(int(pos))
+        self.pos.fill_(pos)
         self.graphs[bool(audio2)].replay()
         return self.lt, self.la, self.h_final, self.two
 
@@ -766,6 +799,7 @@ class FastMossDecoder(FastDecoder):
 
     def prefill_stepwise(self, rows: torch.Tensor) -> torch.Tensor:
         """The same prompt as one eager step per row; returns ``h_final`` of the last row."""
+        _check_ids(rows, self.id_limits)
         rows = rows.to(device=self.dev, dtype=torch.int64).reshape(-1, 1 + self.m.cfg.n_vq)
         if rows.shape[0] > self.m.cfg.max_seq:
             raise ValueError("prompt longer than the KV cache")

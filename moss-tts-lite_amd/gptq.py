@@ -288,65 +288,102 @@ def bf16_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return out.reshape(*shp[:-1], n)
 
 
+_GROUP_SIZES = (32, 64, 128, 256)
+
+
+def _layer_linear(key: str) -> tuple[int, str]:
+    """``"3:down"`` -> ``(3, "down")``: how the reference's metadata names one linear."""
+    layer, _, linear = key.partition(":")
+    return int(layer), linear
+
+
+def split_keeps(bf16_keep) -> tuple[set, set]:
+    """The reference's bf16-keep list (gptq.py:645-650) as two sets: whole layers (plain
+    layer indices) and single linears (``(layer, name)`` pairs)."""
+    layers, linears = set(), set()
+    for item in bf16_keep:
+        if isinstance(item, (tuple, list)):
+            linears.add((int(item[0]), str(item[1])))
+        else:
+            layers.add(int(item))
+    return layers, linears
+
+
 class W4Dispatch:
     """The reference's per-linear int4 dispatch on this build's kernels.
 
     Mirrors ``FastMossTTS._quantize/_linear`` (moss_tts_lite/fast.py:73-121) and
-    ``GptqMossTTS._quantize/_linear`` (gptq.py:641-697): ``qlayers[li]`` maps each
-    quantised linear name to ``(packed, qsz)`` (``packed`` in this build's ``[K/8, N]``
-    layout from :func:`ops.convert_weight_to_int4pack`), ``group_size_map[li][name]``
-    holds its group size, and linears listed in ``bf16_keep`` (a layer index keeps the
-    whole layer, an ``(li, name)`` pair one linear) stay bf16 and run
-    :func:`bf16_linear`.  A layer with nothing quantised has ``qlayers[li] = None``.
+    ``GptqMossTTS._quantize/_linear`` (gptq.py:641-697):
+    - ``qlayers[li]`` maps each quantised linear name to ``(packed, qsz)``, with ``packed``
+      in this build's ``[K/8, N]`` layout (:func:`ops.convert_weight_to_int4pack`);
+      ``qlayers[li]`` is None for a layer with nothing quantised;
+    - ``group_size_map[li][name]`` holds each linear's group size (``w4_group_size``
+      unless ``group_size_map`` overrides it);
+    - linears in ``bf16_keep`` stay bf16 and run :func:`bf16_linear`: a layer index keeps
+      the whole layer, a ``(li, name)`` pair one linear.
 
-    ``state`` records hold either the GPTQ state's unpacked codes (``{"q", "qsz"}``,
-    :func:`load_gptq_state`) or the standalone export's torch tiles (``{"packed",
-    "qsz"}``, :func:`moss_tts_lite_amd.export.read_standalone`); a record's linear need not
-    be in ``layers`` (it is placed on ``device`` then).
+    Without ``state``, every other linear of ``layers`` is quantised round-to-nearest
+    (fast.py:86-101). With ``state``, every linear that is not kept must have a record in
+    it, or ``KeyError`` is raised, as the reference's ``state[li][name]`` lookup does. A
+    record holds either the GPTQ state's unpacked codes (``{"q", "qsz"}``,
+    :func:`load_gptq_state`) or the standalone export's torch tiles (``{"packed", "qsz"}``,
+    :func:`moss_tts_lite_amd.export.read_standalone`). A record's linear need not be in
+    ``layers``; it is placed on ``device`` then. Quantised bf16 weights are dropped from
+    ``layers``.
     """
 
     def __init__(self, layers: list, w4_group_size: int = 128, bf16_keep=(),
                  group_size_map: dict | None = None, state: dict | None = None,
                  device="cuda"):
-        if w4_group_size not in (32, 64, 128, 256):
-            raise ValueError("w4_group_size must be 32/64/128/256")
-        self.layers = layers                       # per layer: name -> bf16 weight [N, K]
+        overrides = {(int(li), str(name)): int(g) for (li, name), g in (group_size_map or {}).items()}
+        for where, g in [("w4_group_size", w4_group_size)] + list(overrides.items()):
+            if g not in _GROUP_SIZES:
+                raise ValueError(f"group size {g} ({where}) is not one of {_GROUP_SIZES}")
+        self.layers = layers
         self.w4_group_size = w4_group_size
-        keep = set(bf16_keep)
-        self._keep_layers = {int(x) for x in keep if isinstance(x, int)}
-        self._keep_linears = {(int(a), b) for a, b in (x for x in keep if not isinstance(x, int))}
-        gmap = {(int(a), b): int(g) for (a, b), g in (group_size_map or {}).items()}
-        self.group_size_map = {li: {name: gmap.get((li, name), w4_group_size) for name in LIN_NAMES}
-                               for li in range(len(layers))}
-        for li, gm in self.group_size_map.items():
-            for name, g in gm.items():
-                if g not in (32, 64, 128, 256):
-                    raise ValueError(f"group size {g} of layer {li} {name} not in 32/64/128/256")
-        self.qlayers = []
-        for li, lyr in enumerate(layers):
-            if li in self._keep_layers:
-                self.qlayers.append(None)
+        self._keep_layers, self._keep_linears = split_keeps(bf16_keep)
+        self.group_size_map = {li: {name: overrides.get((li, name), w4_group_size)
+                                    for name in LIN_NAMES} for li in range(len(layers))}
+        self._device = torch.device(device)
+        self.qlayers = [self._install(li, state) for li in range(len(layers))]
+
+    def is_kept(self, li: int, name: str) -> bool:
+        return li in self._keep_layers or (li, name) in self._keep_linears
+
+    def _install(self, li: int, state: dict | None):
+        if li in self._keep_layers:
+            return None
+        weights = self.layers[li]
+        installed = {}
+        for name in LIN_NAMES:
+            if (li, name) in self._keep_linears:
                 continue
-            qd = {}
-            for name in LIN_NAMES:
-                rec = None if state is None else state.get(li, {}).get(name)
-                if (li, name) in self._keep_linears or (name not in lyr and rec is None):
+            g = self.group_size_map[li][name]
+            if state is None:
+                if name not in weights:
                     continue
-                g = self.group_size_map[li][name]
-                dev = lyr[name].device if name in lyr else torch.device(device)
-                if rec is None:            # round-to-nearest from the bf16 weight (fast.py:86-101)
-                    q, sc, mn = rtn_quantize(lyr[name], g)
-                    qd[name] = pack_fast(q, sc, mn)
-                elif "q" in rec:           # calibrated codes + qsz (gptq.py:504-509, 664-687)
-                    q = rec["q"].to(device=dev, dtype=torch.uint8)
-                    pre = (q[:, 1::2] | (q[:, 0::2] << 4)).contiguous()
-                    qd[name] = (ops.convert_weight_to_int4pack(pre, 8),
-                                rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous())
-                else:                      # standalone export: torch's tiles + qsz (export.py:712-734)
-                    qd[name] = (ops.int4pack_from_torch_tiles(rec["packed"].to(dev)),
-                                rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous())
-                lyr.pop(name, None)
-            self.qlayers.append(qd if qd else None)
+                codes, s, mn = rtn_quantize(weights[name], g)
+                installed[name] = pack_fast(codes, s, mn)
+            else:
+                try:
+                    rec = state[li][name]
+                except KeyError:
+                    raise KeyError(f"the GPTQ state has no record for layer {li} {name}, "
+                                   "which is not kept in bf16") from None
+                dev = weights[name].device if name in weights else self._device
+                installed[name] = self._from_record(rec, dev)
+            weights.pop(name, None)
+        return installed or None
+
+    @staticmethod
+    def _from_record(rec: dict, dev) -> tuple:
+        qsz = rec["qsz"].to(device=dev, dtype=torch.bfloat16).contiguous()
+        if "q" in rec:        # calibrated codes [N, K] (gptq.py:504-509)
+            codes = rec["q"].to(device=dev, dtype=torch.uint8)
+            prepacked = (codes[:, 1::2] | (codes[:, 0::2] << 4)).contiguous()
+            return ops.convert_weight_to_int4pack(prepacked, 8), qsz
+        # torch's int4 tiles as stored by the export (export.py:712-734)
+        return ops.int4pack_from_torch_tiles(rec["packed"].to(dev)), qsz
 
     def _linear(self, x: torch.Tensor, li: int, name: str) -> torch.Tensor:
         """``F.linear``-shaped projection ``x[..., K] -> [..., N]`` in the active mode."""
@@ -358,22 +395,24 @@ class W4Dispatch:
 
 
 def load_gptq_state(path: str):
-    """Read an offline GPTQ state and its ``.meta.json`` (gptq.py:608-626) with loaders
-    that execute nothing from the file: returns ``(state, group_size_map, bf16_keep)``."""
+    """``(state, group_size_map, bf16_keep)`` of an offline GPTQ state file and the
+    ``<path>.meta.json`` beside it (the format of gptq.py:608-626).
+
+    The weights load with ``torch.load(weights_only=True)`` and the metadata with json, so
+    nothing in either file runs. The metadata is required: a state's group sizes and bf16
+    keeps cannot be recovered from its tensors (``FileNotFoundError`` without it).
+    """
     import json
     import os
-    state = torch.load(path, map_location="cpu", weights_only=True)
-    meta_path = path + ".meta.json"
-    if not os.path.isfile(meta_path):
-        raise FileNotFoundError(f"{meta_path} not found: per-linear group sizes and bf16 keeps "
-                                "cannot be inferred from the weights alone")
-    with open(meta_path) as f:
-        meta = json.load(f)
-    gmap = {}
-    for key, val in meta.get("group_size_map", {}).items():
-        layer, name = key.split(":")
-        gmap[(int(layer), name)] = int(val)
-    keep = [(int(x.split(":")[0]), x.split(":")[1]) for x in meta.get("bf16_linears", [])]
-    keep += [int(x) for x in meta.get("bf16_layers", [])]
-    return state, gmap, keep
 
+    meta_path = f"{path}.meta.json"
+    if not os.path.isfile(meta_path):
+        raise FileNotFoundError(f"{meta_path} is missing; it records the state's per-linear "
+                                "group sizes and bf16 keeps")
+    state = torch.load(path, map_location="cpu", weights_only=True)
+    with open(meta_path, encoding="utf-8") as fh:
+        meta = json.load(fh)
+    gmap = {_layer_linear(k): int(g) for k, g in (meta.get("group_size_map") or {}).items()}
+    keep: list = [_layer_linear(k) for k in (meta.get("bf16_linears") or [])]
+    keep.extend(int(layer) for layer in (meta.get("bf16_layers") or []))
+    return state, gmap, keep

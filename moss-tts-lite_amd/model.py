@@ -41,6 +41,13 @@ class BackboneConfig:
     audio_vocab: int = 1025
     audio_pad_code: int = 1024
     two_way_ids: tuple = (151656, 151662)
+    # rows of the text embedding when they differ from the head's (the reference reads
+    # the two from separate tensors, model.py:60-97); None: the same as ``vocab``
+    embed_vocab: int | None = None
+
+    @property
+    def text_embed_rows(self) -> int:
+        return self.vocab if self.embed_vocab is None else self.embed_vocab
 
     @property
     def qkv_out(self) -> int:
@@ -87,12 +94,16 @@ def gate_up_columns_for(order: torch.Tensor, block: int = 32) -> torch.Tensor:
 
 
 def rope_tables(n: int, head_dim: int, theta: float, device, dtype=torch.bfloat16):
-    """cos/sin ``[n, head_dim]``: the reference's fp32 chain (model.py:115-124)."""
-    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
-    pos = torch.arange(n, dtype=torch.float32)
+    """cos/sin ``[n, head_dim]``: the reference's fp32 chain (model.py:115-124), computed on
+    ``device`` as the reference computes it on its own device. The chain fixes the rounding:
+    fp32 inverse frequencies, fp32 angles ``pos * inv`` duplicated, fp32 cos/sin, then one
+    rounding to ``dtype``."""
+    dev = torch.device(device)
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=dev) / head_dim))
+    pos = torch.arange(n, dtype=torch.float32, device=dev)
     freqs = torch.outer(pos, inv)
     emb = torch.cat((freqs, freqs), dim=-1)
-    return emb.cos().to(dtype).to(device), emb.sin().to(dtype).to(device)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
 class Int4Backbone:
@@ -110,6 +121,10 @@ class Int4Backbone:
         self.embed_tokens = T(weights["embed_tokens"])
         self.final_norm = T(weights["final_norm"])
         self.head = T(weights["head"])
+        if tuple(self.embed_tokens.shape) != (cfg.text_embed_rows, cfg.hidden):
+            raise ValueError(f"embed_tokens must be [{cfg.text_embed_rows}, {cfg.hidden}]")
+        if tuple(self.head.shape) != (cfg.vocab, cfg.hidden):
+            raise ValueError(f"head must be [{cfg.vocab}, {cfg.hidden}]")
         self.emb_ext, self.head_audio, self.head_2way = [], None, None
         if cfg.n_vq:
             self.emb_ext = [T(t) for t in weights["emb_ext"]]
@@ -210,7 +225,7 @@ def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda",
         if v_keep:
             lw["v"] = normal(nv, h, std=0.02)
         layers.append(lw)
-    out = {"embed_tokens": normal(cfg.vocab, h, std=1.0), "final_norm": norm_w(h),
+    out = {"embed_tokens": normal(cfg.text_embed_rows, h, std=1.0), "final_norm": norm_w(h),
            "head": normal(cfg.vocab, h, std=0.02), "layers": layers}
     if cfg.n_vq:
         out["emb_ext"] = [normal(cfg.audio_vocab, h, std=1.0) for _ in range(cfg.n_vq)]

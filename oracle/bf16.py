@@ -15,9 +15,15 @@ import numpy as np
 def f32_to_bf16_bits(a) -> np.ndarray:
     """float32 array -> uint16 bf16 bit patterns, round-to-nearest-even."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    lsb = (u >> np.uint64(16)) & np.uint64(1)
-    r = ((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)).astype(np.uint16)
+    u = a.view(np.uint32)
+    # u + 0x7FFF + lsb stays below 2**32 for every non-NaN pattern (at most 0xFF807FFF);
+    # NaNs, which may wrap, are overwritten below
+    t = u >> np.uint32(16)
+    t &= np.uint32(1)
+    t += u
+    t += np.uint32(0x7FFF)
+    t >>= np.uint32(16)
+    r = t.astype(np.uint16)
     nan = np.isnan(a)
     if nan.any():
         r[nan] = np.uint16(0x7FC0)

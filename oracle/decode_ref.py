@@ -54,17 +54,29 @@ def linear(x: np.ndarray, w_kn: np.ndarray) -> np.ndarray:
     return round_bf16((np.asarray(x, np.float64) @ np.asarray(w_kn, np.float64)).astype(np.float32))
 
 
-def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
-    """GQA decode attention: q ``[H, D]``, k/v ``[Hkv, L, D]`` -> bf16 ``[H, D]``."""
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+              p_bf16: bool = True) -> np.ndarray:
+    """GQA decode attention: q ``[H, D]``, k/v ``[Hkv, L, D]`` -> bf16 ``[H, D]``.
+
+    The reference calls ``F.scaled_dot_product_attention`` on bf16 tensors (model.py:183-189,
+    fast.py:149-162). torch's fused kernels for that case compute fp32 scores
+    ``s = (q . k) * scale``, ``e = exp(s - max s)``, round ``e`` to bf16 for the
+    probability-value product and divide by the fp32 sum of the unrounded ``e``. That is
+    the default form here. ``p_bf16=False`` gives the exact softmax (no rounding of ``e``).
+
+    Pinned by torch's CPU SDPA on bf16 inputs (equal for single-block lengths), by float64
+    brute force with ``p_bf16=False``, and by the special cases of a single position and
+    equal scores."""
     h, d = q.shape
     hkv = k.shape[0]
     rep = h // hkv
     out = np.empty((h, d), np.float64)
     for i in range(h):
         kk = k[i // rep].astype(np.float64)
-        s = kk @ q[i].astype(np.float64) * scale
-        p = np.exp(s - s.max())
-        out[i] = (p / p.sum()) @ v[i // rep].astype(np.float64)
+        s = ((kk @ q[i].astype(np.float64)).astype(np.float32) * np.float32(scale)).astype(np.float32)
+        e = np.exp((s - s.max()).astype(np.float64)).astype(np.float32)
+        p = round_bf16(e) if p_bf16 else e
+        out[i] = (p.astype(np.float64) @ v[i // rep].astype(np.float64)) / e.astype(np.float64).sum()
     return round_bf16(out.astype(np.float32))
 
 
@@ -109,9 +121,14 @@ def embed_sum(ids, tables) -> np.ndarray:
     return h
 
 
-def bf16_linear_rows(hf: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """``F.linear(hf, W)`` for a bf16 weight ``[N, K]``: float64 products, bf16 out."""
-    return round_bf16((np.asarray(w, np.float64) @ hf.astype(np.float64)).astype(np.float32))
+def bf16_linear_rows(hf: np.ndarray, w: np.ndarray, chunk: int = 8192) -> np.ndarray:
+    """``F.linear(hf, W)`` for a bf16 weight ``[N, K]``: float64 products, bf16 out
+    (rows taken ``chunk`` at a time, so a long head needs no float64 copy of itself)."""
+    x = np.asarray(hf, np.float64)
+    out = np.empty(w.shape[0], np.float32)
+    for r0 in range(0, w.shape[0], chunk):
+        out[r0:r0 + chunk] = (np.asarray(w[r0:r0 + chunk], np.float64) @ x).astype(np.float32)
+    return round_bf16(out)
 
 
 def moss_heads(hf: np.ndarray, head_text, head_audio, head_2way, pad_code: int,
@@ -151,5 +168,5 @@ def decode_step(token: int, pos: int, weights: dict, k_cache, v_cache, cos, sin,
         h = decoder_layer(h, lw, k_cache[li], v_cache[li], pos, cos, sin, n_heads, n_kv,
                           head_dim, eps)
     hf = rms_norm(h, weights["final_norm"], eps)
-    logits = round_bf16((np.asarray(weights["head"], np.float64) @ hf.astype(np.float64)).astype(np.float32))
+    logits = bf16_linear_rows(hf, weights["head"])
     return logits, hf, int(np.argmax(logits))

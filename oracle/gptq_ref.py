@@ -29,14 +29,26 @@ from .bf16 import bf16_bits_to_f32, f16_bits_to_f32, f32_to_bf16_bits
 # ----------------------------------------------------------------------------
 
 
-def group_scales_from_weight(w2d: np.ndarray, group_size: int = 128):
+_FIFTEENTH = np.float32(1.0) / np.float32(15.0)
+
+
+def group_scales_from_weight(w2d: np.ndarray, group_size: int = 128, divide: str = "device"):
     """Asymmetric per-(row, group) min/max statistics.
 
     Follows moss_tts_lite/gptq.py:35-45 (also fast.py:88-90): ``s =
-    clamp((max - min) / 15, min=1e-6)`` in float32.  Returns ``(s, mn)``, each
-    float32 ``[N, K/g]``.  Pinned by brute force (tests: every group's extreme
-    elements reproduce min/max, and the clamp floor).
+    clamp((max - min) / 15.0, min=1e-6)`` in float32. Returns ``(s, mn)``, each
+    float32 ``[N, K/g]``.
+
+    torch divides a tensor by a host scalar differently per device. Its GPU kernel
+    multiplies by the float32 reciprocal, ``(max - min) * fp32(1/15)``; its CPU kernel
+    divides exactly. The reference quantises on the GPU (``--quant`` requires CUDA,
+    cli.py:469-471), so ``divide="device"`` is the default; ``divide="cpu"`` gives torch's
+    CPU result. Pinned: the CPU form against torch on the CPU; the device form against the
+    reference's chain run by torch on the GPU (tests/test_gemm_gpu.py); both by brute force
+    (every group's extreme elements reproduce min/max) and the clamp floor.
     """
+    if divide not in ("device", "cpu"):
+        raise ValueError("divide must be 'device' or 'cpu'")
     w = np.asarray(w2d, dtype=np.float32)
     n, k = w.shape
     if k % group_size:
@@ -44,23 +56,27 @@ def group_scales_from_weight(w2d: np.ndarray, group_size: int = 128):
     wg = w.reshape(n, k // group_size, group_size)
     mx = wg.max(-1)
     mn = wg.min(-1)
-    s = np.maximum((mx - mn) / np.float32(15.0), np.float32(1e-6)).astype(np.float32)
+    span = (mx - mn).astype(np.float32)
+    s = (span * _FIFTEENTH) if divide == "device" else (span / np.float32(15.0))
+    s = np.maximum(s.astype(np.float32), np.float32(1e-6)).astype(np.float32)
     return s, mn.astype(np.float32)
 
 
-def rtn_quantize(w2d: np.ndarray, group_size: int = 128):
+def rtn_quantize(w2d: np.ndarray, group_size: int = 128, divide: str = "device"):
     """Round-to-nearest int4 group quantisation.
 
     Follows moss_tts_lite/gptq.py:54-64 (= FastMossTTS._quantize, fast.py:86-92):
     ``q = clamp(round_half_even((w - mn) / s), 0, 15)`` with float32 subtract
-    and divide.  Returns ``(q uint8 [N, K], s, mn)``.  Pinned by brute force:
-    each code is the nearest grid point of ``mn + q*s`` measured in the same
-    float32 quotient (tests/test_oracle_gptq.py).
+    and an exact float32 divide (a tensor by a tensor). ``divide`` picks how ``s`` is
+    formed (:func:`group_scales_from_weight`). Returns ``(q uint8 [N, K], s, mn)``.
+    Pinned by brute force: each code is the nearest grid point of ``mn + q*s`` measured
+    in the same float32 quotient (tests/test_oracle_gptq.py); and against torch on both
+    devices.
     """
     w = np.asarray(w2d, dtype=np.float32)
     n, k = w.shape
     g = group_size
-    s, mn = group_scales_from_weight(w, g)
+    s, mn = group_scales_from_weight(w, g, divide)
     wg = w.reshape(n, k // g, g)
     t = (wg - mn[..., None]) / s[..., None]
     q = np.clip(np.rint(t), 0, 15).astype(np.uint8).reshape(n, k)

@@ -236,3 +236,34 @@ def test_load_gptq_state_safe_loader(tmp_path):
     st, gmap, keep = load_gptq_state(str(p))
     assert gmap == {(0, "q"): 32} and keep == [(1, "down"), 3]
     assert torch.equal(st[0]["q"]["q"], state[0]["q"]["q"])
+
+
+def test_w4_dispatch_incomplete_state_raises():
+    # with a GPTQ state, a linear that is neither kept in bf16 nor recorded is an error
+    # (the reference indexes state[li][name], gptq.py:675), not a silent round-to-nearest
+    import torch
+    from moss_tts_lite_amd.gptq import W4Dispatch
+    layers = [{"q": torch.zeros(8, 256, dtype=torch.bfloat16)}]
+    with pytest.raises(KeyError, match="layer 0 q"):
+        W4Dispatch(layers, state={0: {}}, device="cpu")
+    with pytest.raises(KeyError, match="layer 0 q"):
+        W4Dispatch(layers, state={}, device="cpu")
+    # a kept layer needs no record and installs nothing
+    assert W4Dispatch(layers, bf16_keep=[0], state={}, device="cpu").qlayers == [None]
+    with pytest.raises(ValueError):
+        W4Dispatch(layers, w4_group_size=16)
+
+
+def test_step_position_and_id_checks():
+    # the decoders' host checks (moss_tts_lite/model.py:_check_ids raises for ids and
+    # lengths that do not fit)
+    import torch
+    from moss_tts_lite_amd.fast import _check_ids, _check_pos
+    _check_ids(torch.tensor([[0, 1024], [8191, 0]]), [8192, 1025])
+    for bad in ([[8192, 0]], [[0, 1025]], [[-1, 0]]):
+        with pytest.raises(ValueError, match="outside its embedding table"):
+            _check_ids(torch.tensor(bad), [8192, 1025])
+    assert _check_pos(63, 64) == 63
+    for bad in (64, -1):
+        with pytest.raises(ValueError, match="outside the KV cache"):
+            _check_pos(bad, 64)

@@ -83,14 +83,19 @@ def test_embed_sum_kernel(dev, lib):
         assert np.array_equal(fb(out), h)
 
 
+def oracle_tables(n, dev):
+    """The oracle's RoPE tables as device bf16 tensors (kernel inputs)."""
+    cos, sin = D.rope_tables(n, 128)
+    return tb(cos, dev), tb(sin, dev)
+
+
 def test_qk_norm_rope_kv_kernel(dev, lib):
-    from moss_tts_lite_amd.model import rope_tables
     r = np.random.default_rng(2)
     H, Hkv, S, pos = 32, 8, 64, 37
     qkv = round_bf16((2 * r.standard_normal((H + 2 * Hkv) * 128)).astype(np.float32))
     qn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
     kn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
-    cos, sin = rope_tables(S, 128, 1e6, dev)
+    cos, sin = oracle_tables(S, dev)
     kc = torch.zeros(Hkv, S, 128, dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
     q_out = torch.zeros(H * 128, dtype=torch.bfloat16, device=dev)
@@ -101,7 +106,7 @@ def test_qk_norm_rope_kv_kernel(dev, lib):
                                     sin.data_ptr(), tpos.data_ptr(), q_out.data_ptr(), kc.data_ptr(),
                                     vc.data_ptr(), H, Hkv, 128, S, ctypes.c_float(1e-6), stream()),
             "qk_rope")
-    c, s = fb(cos)[pos], fb(sin)[pos]
+    c, s = (t[pos] for t in D.rope_tables(S, 128))
     q = D.apply_rope(D.rms_norm(qkv[:H * 128].reshape(H, 128), qn), c, s)
     k = D.apply_rope(D.rms_norm(qkv[H * 128:(H + Hkv) * 128].reshape(Hkv, 128), kn), c, s)
     v = qkv[(H + Hkv) * 128:].reshape(Hkv, 128)
@@ -185,7 +190,7 @@ def test_mini_model_steps_match_oracle_and_graph_is_bitwise(dev, plan):
     cfg = small_config()
     model, ow = build_case(cfg, seed=11, dev=dev)
     dec = FastDecoder(model, plan=plan)
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     prompt = [5, 17, 999, 0, 42, 7]
     # oracle: prompt then greedy decode
     okc, ovc = _oracle_caches(model)
@@ -293,7 +298,7 @@ def test_full_size_layer_config3(dev):
     dec.run_layer(0)
     dec.flush_residual()
     torch.cuda.synchronize()
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     h1 = D.decoder_layer(h0, ow["layers"][0], kc[0], vc[0], 2048, cos, sin, 32, 8, 128)
     err = rel_l2(fb(dec.h), h1)
     kerr = rel_l2(fb(model.k_cache)[0, :, 2048], kc[0, :, 2048])
@@ -356,7 +361,6 @@ def test_down_reads_silu_mul_from_gate_up_partials(dev, lib):
 
 
 def test_qk_rope_from_partials_matches_bf16_input(dev, lib):
-    from moss_tts_lite_amd.model import rope_tables
     r = np.random.default_rng(8)
     H, Hkv, S_, pos, splits = 32, 8, 64, 11, 8
     ncols = (H + 2 * Hkv) * 128
@@ -364,7 +368,7 @@ def test_qk_rope_from_partials_matches_bf16_input(dev, lib):
     qkv = round_bf16(_seq_sum(parts))
     qn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
     kn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
-    cos, sin = rope_tables(S_, 128, 1e6, dev)
+    cos, sin = oracle_tables(S_, dev)
     tpos = torch.tensor([pos], dtype=torch.int64, device=dev)
     res = []
     for use_part in (False, True):
@@ -469,14 +473,13 @@ def test_gemm_norm_partials_match_oracle(dev, lib):
 
 @pytest.mark.parametrize("pos,max_seq", [(11, 64), (700, 1024), (0, 64), (1023, 1024)])
 def test_attention_fused_matches_two_kernel_path(dev, lib, pos, max_seq):
-    from moss_tts_lite_amd.model import rope_tables
     r = np.random.default_rng(40 + pos)
     H, Hkv, splits = 32, 8, 8
     ncols = (H + 2 * Hkv) * 128
     parts = torch.from_numpy((r.standard_normal((splits, ncols)) * 0.5).astype(np.float32)).to(dev)
     qn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
     kn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
-    cos, sin = rope_tables(max_seq, 128, 1e6, dev)
+    cos, sin = oracle_tables(max_seq, dev)
     tpos = torch.tensor([pos], dtype=torch.int64, device=dev)
     cache = tb(r.standard_normal((2, Hkv, max_seq, 128)).astype(np.float32), dev)
     ws = torch.zeros(int(lib.mtl_decode_attention_workspace_bytes(H, 128)), dtype=torch.uint8,
@@ -572,7 +575,7 @@ def test_kept_v_proj_step_matches_oracle_and_graph(dev):
     with pytest.raises(ValueError):
         FastDecoder(model, plan="staged")
     dec = FastDecoder(model, plan="strip")
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     prompt = [5, 17, 999, 0, 42, 7]
     okc, ovc = _oracle_caches(model)
     o_logits = []
@@ -611,7 +614,7 @@ def test_moss_step_heads_match_oracle_and_graphs(dev, plan):
     dec = FastMossDecoder(model, plan=plan)
     r = np.random.default_rng(3)
     rows = np.concatenate([r.integers(0, cfg.vocab, (7, 1)), r.integers(0, 1025, (7, cfg.n_vq))], 1)
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     okc, ovc = _oracle_caches(model)
     # prompt rows 0..4 through the oracle, then steps at positions 5, 6 (text, audio2)
     for p in range(5):
@@ -688,3 +691,27 @@ def test_residual_gemv_matches_partials_plus_residual_add(dev, lib, src):
                                          ws.data_ptr(), ws.numel(), stream()), "residual gemv")
         assert torch.equal(h_a, h_b) and torch.equal(ord_a, ord_b)
         assert torch.equal(slots_a[:n // 16], slots_b[:n // 16])
+
+
+def test_rope_tables_on_device_match_oracle_and_reference(dev):
+    # the product builds its tables on the device with the reference's fp32 chain
+    # (model.py:115-124); the oracle rounds float64 trigonometry of the same fp32 angles and
+    # the reference's CPU chain (tests/golden/moss_step_fixtures.npz) uses torch's CPU
+    # cos/sin. All three agree to one bf16 ulp (2.5e-4 where a value near zero has a finer
+    # ulp than the fp32 error of a large angle), and differ in a small share of entries.
+    from moss_tts_lite_amd.model import rope_tables
+    from tests.test_oracle_step_fixture import FIX, reference_rope_bits
+    fix = dict(np.load(FIX))
+    ocos, osin = D.rope_tables(2048, 128)
+    dcos, dsin = rope_tables(2048, 128, 1e6, dev)
+    assert dcos.device.type == "cuda" and dcos.dtype == torch.bfloat16
+    for name, dt, ot in (("cos", dcos, ocos), ("sin", dsin, osin)):
+        ref = bf16_bits_to_f32(reference_rope_bits(fix, name)).reshape(2048, 128)
+        ours = fb(dt)
+        for other, label in ((ot, "oracle"), (ref, "reference CPU")):
+            d = np.abs(ours - other)
+            n_diff = int((d > 0).sum())
+            print(f"device {name} vs {label}: {n_diff} of {d.size} entries differ, "
+                  f"{int((d[:128] > 0).sum())} below position 128")
+            assert (d <= np.maximum(np.abs(other) * 2.0 ** -7, 2.5e-4)).all(), label
+            assert n_diff < d.size // 100, label

@@ -16,7 +16,8 @@ def _write_dir(path, records, meta_over=None, preset="w4-mixed"):
             "presets": {preset: {"group_size_default": 128,
                                  "group_size_map": {"0:o": 32, "1:down": 256},
                                  "bf16_linears": ["0:v"], "bf16_layers": [2]}},
-            "quantization": {"method": "gptq", "inner_k_tiles": 8}}
+            "quantization": {"method": "gptq", "inner_k_tiles": 8},
+            "tool": {"name": "moss_tts_lite.export.export_standalone", "torch": "2.10.0+rocm7.0"}}
     meta.update(meta_over or {})
     (path / E.META_FILE).write_text(json.dumps(meta))
 
@@ -54,7 +55,7 @@ def test_read_standalone_errors(tmp_path):
     b = tmp_path / "b"; b.mkdir()
     recs = _records(); recs.pop("layers.0.o.qsz")
     _write_dir(b, recs)
-    with pytest.raises(ValueError, match="incomplete record"):
+    with pytest.raises(ValueError, match="incomplete int4 record"):
         E.read_standalone(str(b))
     c = tmp_path / "c"; c.mkdir()
     _write_dir(c, _records(), meta_over={"format": "something-else"})
@@ -66,3 +67,23 @@ def test_read_standalone_errors(tmp_path):
     with pytest.raises(FileNotFoundError):
         E.read_standalone(str(d))
     assert not E.is_standalone_dir(str(tmp_path / "nowhere"))
+
+
+@pytest.mark.parametrize("torch_version", ["2.9.1+cu128", "2.9.1", None])
+def test_read_standalone_refuses_tiles_of_other_torch_builds(tmp_path, torch_version):
+    # a CUDA build of torch tiles the same [N/8, K/(16T), 32, T/2] shape differently: an
+    # export it wrote (the reference's own, "CUDA required", export.py:438) is refused,
+    # as is one that does not record its torch
+    tool = {"name": "x"} if torch_version is None else {"name": "x", "torch": torch_version}
+    _write_dir(tmp_path, _records(), meta_over={"tool": tool})
+    assert E.tiles_backend(json.loads((tmp_path / E.META_FILE).read_text())) != "rocm"
+    with pytest.raises(ValueError, match="ROCm"):
+        E.read_standalone(str(tmp_path))
+
+
+def test_read_standalone_without_int4_records_needs_no_backend(tmp_path):
+    # a directory of plain weights only has no tiles to misread
+    recs = {k: v for k, v in _records().items() if not k.endswith((".q", ".qsz"))}
+    _write_dir(tmp_path, recs, meta_over={"tool": {"torch": "2.9.1+cu128"}})
+    _, weights, state, _, _ = E.read_standalone(str(tmp_path))
+    assert state == {} and len(weights) == 2

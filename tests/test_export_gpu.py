@@ -93,8 +93,14 @@ def test_ingested_export_matches_torch_int4pack_mm(dev, tmp_path):
     (tmp_path / E.META_FILE).write_text(json.dumps({
         "format": E.FORMAT_TAG, "preset_name": "p", "weight_file": {"name": E.Q_FILE},
         "presets": {"p": {"group_size_map": {"0:o": 128, "0:down": 32}, "bf16_linears": []}},
-        "quantization": {"method": "gptq", "inner_k_tiles": 8}}))
+        "quantization": {"method": "gptq", "inner_k_tiles": 8},
+        "tool": {"torch": torch.__version__}}))     # the tiles come from this ROCm torch
     meta, weights, state, gmap, keep = E.read_standalone(str(tmp_path))
+    # the linears without a record must be kept in bf16 (else the state is incomplete)
+    with pytest.raises(KeyError):
+        W4Dispatch([{}], w4_group_size=128, bf16_keep=keep, group_size_map=gmap, state=state,
+                   device=dev)
+    keep = keep + [(0, n) for n in ("q", "k", "v", "gate", "up")]
     disp = W4Dispatch([{}], w4_group_size=128, bf16_keep=keep, group_size_map=gmap,
                       state=state, device=dev)
     for name, (codes, qsz, tiles, g) in ref.items():

@@ -361,8 +361,10 @@ def test_deterministic_and_graph_replay(dev):
 
 def test_w4_dispatch_modes(dev):
     # FastMossTTS/GptqMossTTS-style dispatch (fast.py:107-121, gptq.py:689-697): RTN int4
-    # at the default group, a per-linear group override, bf16-kept linears and layers
-    from moss_tts_lite_amd.gptq import W4Dispatch, effective_weight, LIN_NAMES
+    # at the default group, a per-linear group override, bf16-kept linears and layers.
+    # Every reference value comes from the oracle: its RTN codes and qsz of the same bf16
+    # weights, the packed words of its restatement of the layout, its dequant.
+    from moss_tts_lite_amd.gptq import LIN_NAMES, W4Dispatch
     r = np.random.default_rng(0)
     shapes = {"q": (512, 256), "k": (128, 256), "v": (128, 256), "o": (256, 512),
               "gate": (384, 256), "up": (384, 256), "down": (256, 384)}
@@ -385,14 +387,50 @@ def test_w4_dispatch_modes(dev):
             if disp.qlayers[li] is None or name not in disp.qlayers[li]:
                 ref = xf @ orig[li][name].astype(np.float64).T          # bf16 kept
             else:
-                packed, qsz = disp.qlayers[li][name]
                 g = disp.group_size_map[li][name]
-                assert qsz.shape == (k // g, shapes[name][0], 2)
-                codes = ops.unpack_codes(packed).t()                    # [N, K]
-                w = effective_weight(codes, qsz, g).double().cpu().numpy()
-                ref = xf @ w.T
+                codes, sc, mn = G.rtn_quantize(orig[li][name], g)
+                qsz_o = G.pack_qsz(sc, mn)
+                packed, qsz = disp.qlayers[li][name]
+                np.testing.assert_array_equal(qsz.view(torch.int16).cpu().numpy().view(np.uint16),
+                                              qsz_o)
+                np.testing.assert_array_equal(packed.cpu().numpy(),
+                                              G.int4pack_from_prepacked(G.prepack_u8(codes)))
+                ref = xf @ G.effective_weight(codes, qsz_o, g).astype(np.float64).T
             err = rel_l2(got, ref)
             assert err < TOL_BF16, (li, name, err)
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_product_rtn_and_qsz_match_oracle(dev, group):
+    # gptq.rtn_quantize / pack_qsz_only on the device == the oracle's (gptq.py:35-85) bit for
+    # bit: codes, fp32 scale and min, bf16 qsz. The weights include a constant group (the
+    # 1e-6 scale floor), a group whose values sit on exact half-steps of the grid (ties to
+    # even) and a wide-range group.
+    from moss_tts_lite_amd.gptq import pack_qsz_only, rtn_quantize
+    r = np.random.default_rng(group)
+    n, k = 96, 1024
+    w = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    w[0, :group] = 0.125                                   # constant group
+    # min 0, max 15/16: scale exactly 1/16, and the values k/32 land on exact half-steps
+    # for odd k (bf16 holds them exactly), so the rounding of ties decides those codes
+    w[1, :group] = (np.arange(group) % 31) * 2.0 ** -5
+    w[2, :group] *= 100.0                                  # wide range
+    wb = torch.from_numpy(w).to(dev).bfloat16()
+    w32 = wb.float().cpu().numpy()
+    q, sc, mn = rtn_quantize(wb, group)
+    qo, so, mno = G.rtn_quantize(w32, group)          # the device form of the span / 15
+    # the reference's chain in torch ops on this device (gptq.py:35-64) pins that form
+    from tests.test_oracle_gptq import _torch_rtn
+    tq, ts, tm = _torch_rtn(wb, group)
+    np.testing.assert_array_equal(ts.cpu().numpy(), so)
+    np.testing.assert_array_equal(tq.cpu().numpy(), qo)
+    np.testing.assert_array_equal(sc.cpu().numpy(), so)
+    np.testing.assert_array_equal(mn.cpu().numpy(), mno)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    assert float(so[0, 0]) == np.float32(1e-6)
+    qsz = pack_qsz_only(sc, mn, group)
+    np.testing.assert_array_equal(qsz.view(torch.int16).cpu().numpy().view(np.uint16),
+                                  G.pack_qsz(so, mno))
 
 
 # ------------------------------------------------------------------ tiled weight stream

@@ -73,12 +73,33 @@ def test_attention_matches_torch_sdpa():
     q = _bf(r, (8, 128))
     k = _bf(r, (2, 37, 128))
     v = _bf(r, (2, 37, 128))
+    tq = torch.from_numpy(q).view(1, 8, 1, 128)
+    tk = torch.from_numpy(k).repeat_interleave(4, 0).view(1, 8, 37, 128)
+    tv = torch.from_numpy(v).repeat_interleave(4, 0).view(1, 8, 37, 128)
+    # the flash form: torch's CPU SDPA on the bf16 tensors, up to rare flips of one
+    # probability's bf16 rounding (fp32 score sums in another order); the exact softmax
+    # is three times further away
     ours = D.attention(q, k, v, 1 / np.sqrt(128))
-    tq = torch.from_numpy(q).double().view(1, 8, 1, 128)
-    tk = torch.from_numpy(k).double().repeat_interleave(4, 0).view(1, 8, 37, 128)
-    tv = torch.from_numpy(v).double().repeat_interleave(4, 0).view(1, 8, 37, 128)
-    ref = F.scaled_dot_product_attention(tq, tk, tv).view(8, 128).float().numpy()
-    assert np.all(np.abs(ours - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+    got = F.scaled_dot_product_attention(tq.bfloat16(), tk.bfloat16(), tv.bfloat16())
+    got = got.view(8, 128).float().numpy()
+    flash_err = np.linalg.norm(ours - got) / np.linalg.norm(got)
+    exact_err = np.linalg.norm(D.attention(q, k, v, 1 / np.sqrt(128), p_bf16=False) - got) \
+        / np.linalg.norm(got)
+    assert flash_err < 1.5e-3 and exact_err > 2 * flash_err, (flash_err, exact_err)
+    # single kv head, 4 query heads (the reference's ratio): equal bit for bit
+    q4, k1, v1 = q[:4], k[:1, :6], v[:1, :6]
+    got4 = F.scaled_dot_product_attention(
+        torch.from_numpy(q4).bfloat16().view(1, 4, 1, 128),
+        torch.from_numpy(k1).bfloat16().repeat_interleave(4, 0).view(1, 4, 6, 128),
+        torch.from_numpy(v1).bfloat16().repeat_interleave(4, 0).view(1, 4, 6, 128))
+    np.testing.assert_array_equal(D.attention(q4, k1, v1, 1 / np.sqrt(128)),
+                                  got4.view(4, 128).float().numpy())
+    # the exact form: float64 SDPA, to the final bf16 rounding
+    exact = D.attention(q, k, v, 1 / np.sqrt(128), p_bf16=False)
+    ref = F.scaled_dot_product_attention(tq.double(), tk.double(), tv.double()).view(8, 128).float().numpy()
+    assert np.all(np.abs(exact - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6)
+    # the two forms differ by the bf16 rounding of the probabilities only
+    assert 2e-4 < np.linalg.norm(ours - exact) / np.linalg.norm(exact) < 5e-3
 
 
 def test_attention_special_cases():

@@ -78,6 +78,41 @@ def test_rtn_brute_force_nearest_grid_point():
             assert q[n, g * 32 + int(np.argmax(wg[n, g]))] == 15
 
 
+def _torch_rtn(w: torch.Tensor, g: int):
+    """The reference's RTN chain (gptq.py:35-64) in torch ops, on ``w``'s device."""
+    n, k = w.shape
+    wg = w.float().reshape(n, k // g, g)
+    mx, mn = wg.amax(-1), wg.amin(-1)
+    s = ((mx - mn) / 15.0).clamp(min=1e-6)
+    q = ((wg - mn.unsqueeze(-1)) / s.unsqueeze(-1)).round().clamp(0, 15).to(torch.uint8)
+    return q.reshape(n, k), s, mn
+
+
+def test_rtn_cpu_form_matches_torch_on_cpu():
+    # torch's CPU kernel divides the span by 15 exactly: the oracle's "cpu" form, bit for bit
+    r = np.random.default_rng(12)
+    w = bf16_bits_to_f32(f32_to_bf16_bits((r.standard_normal((64, 512)) * 0.05).astype(np.float32)))
+    q, s, mn = G.rtn_quantize(w, 128, divide="cpu")
+    tq, ts, tm = _torch_rtn(torch.from_numpy(w), 128)
+    assert np.array_equal(s, ts.numpy()) and np.array_equal(mn, tm.numpy())
+    assert np.array_equal(q, tq.numpy())
+
+
+def test_rtn_device_form_is_the_reciprocal_product():
+    # the device form (the default): span * fp32(1/15), which differs from the exact
+    # quotient by one float32 ulp in many groups (so the two forms are distinguishable)
+    r = np.random.default_rng(13)
+    w = (r.standard_normal((64, 512)) * 0.05).astype(np.float32)
+    s_dev, mn = G.group_scales_from_weight(w, 128)
+    s_cpu, _ = G.group_scales_from_weight(w, 128, divide="cpu")
+    wg = w.reshape(64, 4, 128)
+    span = (wg.max(-1) - wg.min(-1)).astype(np.float32)
+    assert np.array_equal(s_dev, (span * (np.float32(1.0) / np.float32(15.0))).astype(np.float32))
+    assert np.array_equal(s_cpu, (span / np.float32(15.0)).astype(np.float32))
+    ulps = np.abs(s_dev.view(np.int32).astype(np.int64) - s_cpu.view(np.int32))
+    assert ulps.max() == 1 and 0.2 < (ulps == 1).mean() < 0.9
+
+
 def test_rtn_scale_floor():
     w = np.zeros((2, 64), dtype=np.float32)
     q, s, mn = G.rtn_quantize(w, 32)

@@ -198,14 +198,14 @@ def test_embed_rows_match_embed_sum(dev, lib):
 def test_qk_norm_rope_rows_match_decode_kernel(dev, lib):
     # rows at positions pos0 .. pos0 + L - 1: q out, K/V cache rows bit for bit the
     # single-position kernel's
-    from moss_tts_lite_amd.model import rope_tables
     r = np.random.default_rng(22)
     H, Hkv, S, L, pos0 = 8, 2, 96, 21, 30
     ld = (H + 2 * Hkv) * 128
     qkv = round_bf16((2 * r.standard_normal((L, ld))).astype(np.float32))
     qn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
     kn = round_bf16((1 + 0.1 * r.standard_normal(128)).astype(np.float32))
-    cos, sin = rope_tables(S, 128, 1e6, dev)
+    ocos, osin = D.rope_tables(S, 128)
+    cos, sin = tb(ocos, dev), tb(osin, dev)
     tq, tqn, tkn = tb(qkv, dev), tb(qn, dev), tb(kn, dev)
     kc = torch.zeros(Hkv, S, 128, dtype=torch.bfloat16, device=dev)
     vc, kc1, vc1 = torch.zeros_like(kc), torch.zeros_like(kc), torch.zeros_like(kc)
@@ -281,7 +281,7 @@ def test_prefill_attention_agrees_with_decode_attention(dev, lib):
 
 # ------------------------------------------------------------------ the whole prefill
 def _oracle_prompt(ow, cfg, prompt, model):
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     okc = np.zeros((cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, 128), np.float32)
     ovc = okc.copy()
     for p, t in enumerate(prompt):
@@ -328,7 +328,7 @@ def test_prefill_then_graph_decode(dev):
     dec = FastDecoder(model)
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 29)
     lg, hf, tok, okc, ovc = _oracle_prompt(ow, cfg, prompt, model)
-    cos, sin = fb(model.rope_cos), fb(model.rope_sin)
+    cos, sin = D.rope_tables(cfg.max_seq, 128)
     dec.prefill(torch.from_numpy(prompt))
     eager = []
     for i in range(4):
