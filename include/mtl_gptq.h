@@ -96,6 +96,24 @@ int mtl_gptq_gemm(const void* x, int64_t M, int64_t K,
                   void* workspace, int64_t ws_bytes, void* stream);
 
 /*
+ * mtl_gptq_gemm without a workspace argument, and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops).  The split-K workspace is a
+ * library-owned static device array of MTL_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends; the first call on a device looks up its address and zero-fills it on
+ * `stream`.  Every call on one GPU shares that array: calls that overlap on one GPU race
+ * and must be ordered by the caller.  Arguments and results as mtl_gptq_gemm;
+ * MTL_ERR_WORKSPACE when mtl_gemm_workspace_bytes(M, K, N, group_size) exceeds the
+ * array (16 MiB: the decode shapes q|k|v 4096x6144, o 4096x4096, gate|up 4096x24576 and
+ * down 12288x4096 fit at every M <= 16; gate|up at M = 16 needs 12 MiB).
+ */
+#define MTL_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int mtl_gptq_gemm_noalloc(const void* x, int64_t M, int64_t K,
+                          const int32_t* qweight, const int32_t* qzeros, const void* scales,
+                          const int32_t* perm, int64_t N, int32_t group_size,
+                          int32_t zero_offset, void* y, int32_t out_dtype, void* stream);
+
+/*
  * Act-order preparation: from an AutoGPTQ qweight whose input channels are
  * grouped by an arbitrary g_idx (desc_act=True checkpoints), write the
  * group-contiguous copy qweight_sorted[K/8, N] and the gather index perm[K]

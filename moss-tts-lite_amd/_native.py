@@ -27,6 +27,8 @@ _SIGNATURES = {
     "mtl_workspace_init": (_i32, [_c_void_p, _i64, _c_void_p]),
     "mtl_gptq_gemm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                              _i64, _i32, _i32, _c_void_p, _i32, _c_void_p, _i64, _c_void_p]),
+    "mtl_gptq_gemm_noalloc": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_void_p, _i64, _i32, _i32, _c_void_p, _i32, _c_void_p]),
     "mtl_actorder_scratch_bytes": (_i64, [_i64]),
     "mtl_gptq_actorder_prepare": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p,
                                          _c_void_p, _c_void_p, _i64, _c_void_p]),
@@ -116,6 +118,7 @@ _SIGNATURES = {
     "mtl_tune_set_attn_fixed": (_i32, [_i32]),
 }
 
+NOALLOC_SCRATCH_BYTES = 16 << 20      # MTL_NOALLOC_SCRATCH_BYTES
 MTL_OK = 0
 MTL_ERR_INVALID_ARG = -1
 MTL_ERR_SHAPE = -2
