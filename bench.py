@@ -27,6 +27,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode steps/s at bs=1; int4 GEMV HBM GB/s as % of ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
+# decode positions of the benchmark workload: prefill 256, then 1024 steps (KV 257 -> 1280)
+CONFIG4_POSITIONS = (256, 1279)
 GEMV_SHAPES = (("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576),
                ("down", 12288, 4096))
 GROUP = 128
@@ -213,34 +215,89 @@ def bench_skinny(args, torch, dev):
     return out
 
 
-def cpu_baseline_gemv(budget_s: float = 12.0):
-    """The oracle's port of the reference CPU path on the gate_up shape: dequantise
-    (effective weight) then an fp32 x @ W, timed on this host's cores."""
-    import numpy as np
-
-    from oracle import synth
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
-    k, n = 4096, 24576
-    case = synth.gptq_case(k=k, n=n, m=1, group=GROUP, act_order=True, seed=1234, with_ref=False)
-    x = case["x_bits"].astype(np.uint32) << 16
-    x = x.view(np.float32)
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """All threads of this process's CPU share: OMP_NUM_THREADS when set, else the
+    affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
+def _median_s(fn, budget_s: float, max_runs: int = 20) -> tuple[float, int]:
+    """Median wall time of ``fn`` over up to ``max_runs`` runs (at least 3) after warm-up
+    runs (3, or 1 when one run exceeds a fifth of the budget), stopping at ``budget_s``."""
+    t = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t
+    for _ in range(0 if first > budget_s / 5 else 2):
+        fn()
     times = []
-    t_end = time.time() + budget_s
-    while time.time() < t_end or not times:
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (len(times) < max_runs and time.perf_counter() < t_end):
         t = time.perf_counter()
-        synth.chunked_gptq_gemm(x, case["qweight"], case["qzeros"], case["scales"], case["g_idx"],
-                                GROUP, chunk=4096)
+        fn()
         times.append(time.perf_counter() - t)
-    best = sorted(times)[len(times) // 2]
-    gbs = algo_bytes(1, k, n, GROUP, True) / best / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"gate_up 4096x24576 M=1 act-order, {len(times)} calls, median "
-                      f"{best * 1e3:.0f} ms/call (numpy dequant + BLAS matmul)"}
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_linear_datapoints(torch, shapes, budget_s: float = 1.2) -> dict:
+    """The reference's CPU int4 linear (oracle/cpu_path.py: effective_weight dequant then an
+    fp32 x @ W.T, tests/test_quant.py:104-107) and torch's CPU int4 GEMM
+    (_weight_int4pack_mm_for_cpu) on each (name, K, N) shape at M = 1, g = 128, seeded
+    codes and qsz, at 1 thread and at all of this process's threads: median microseconds
+    (BASELINE: >= 20 runs or the per-datapoint budget, at least 3)."""
+    from oracle import cpu_path as C
+
+    n_all = _cpu_threads()
+    saved = torch.get_num_threads()
+    gen = torch.Generator().manual_seed(1234)
+    out = {}
+    for name, k, n in shapes:
+        q = torch.randint(0, 16, (n, k), dtype=torch.int32, generator=gen)
+        qsz = torch.stack([torch.rand(k // GROUP, n, generator=gen) * 0.018 + 0.002,
+                           torch.rand(k // GROUP, n, generator=gen) * 0.2 - 0.1], 2).bfloat16()
+        x = torch.randn(1, k, generator=gen).bfloat16()
+        packed = C.pack_for_cpu(q)
+        res = {}
+        for threads in (1, n_all):
+            torch.set_num_threads(threads)
+            for label, fn in (("fp32", lambda: C.linear_fp32(x, q, qsz, GROUP)),
+                              ("int4_cpu", lambda: C.int4pack_mm_cpu(x, packed, GROUP, qsz))):
+                sec, runs = _median_s(fn, budget_s)
+                res[f"{label}_{threads}t_us"] = round(sec * 1e6, 1)
+                res[f"{label}_{threads}t_runs"] = runs
+        res["bytes"] = algo_bytes(1, k, n, GROUP, False)
+        out[name] = res
+        del q, packed
+    torch.set_num_threads(saved)
+    return out
+
+
+def cpu_baseline_gemv(torch, gpu_us: dict):
+    """The reference's CPU path on the four decode-step shapes at M = 1 (value: GB/s of
+    the fp32 path on gate_up at all threads), with torch's CPU int4 GEMM beside it."""
+    n_all = _cpu_threads()
+    per = cpu_linear_datapoints(torch, GEMV_SHAPES)
+    for name, d in per.items():
+        if name in gpu_us:
+            d["gpu_speedup_vs_fp32_all"] = round(d[f"fp32_{n_all}t_us"] / gpu_us[name], 1)
+    gu = per["gate_up"]
+    return {"value": round(gu["bytes"] / gu[f"fp32_{n_all}t_us"] / 1e3, 3), "unit": "GB/s",
+            "cores": n_all, "kind": "port", "cpu_model": _cpu_model(),
+            "sample": f"gate_up 4096x24576 M=1 g128: effective_weight dequant + fp32 x @ W.T "
+                      f"in torch on {n_all} threads (median of up to 20 calls)",
+            "per_shape": per}
 
 
 def bench_decode(args, torch):
@@ -253,6 +310,7 @@ def bench_decode(args, torch):
     prompt_len = 256
     total = prompt_len + args.warmup + args.steps
     cfg = BackboneConfig(max_seq=max(1536, ((total + 255) // 256) * 256), group_size=args.group)
+    del total
     t0 = time.time()
     model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev, v_keep=args.v_keep), dev)
     dec = FastDecoder(model, plan=args.plan)
@@ -277,10 +335,18 @@ def bench_decode(args, torch):
         pf_gpu.append(a_ev.elapsed_time(b_ev))
     for _ in range(args.warmup):
         dec.graph.replay()
+    # The workload decodes at positions 256 .. 1279 (KV length 257 -> 1280). The timed
+    # steps sit in the middle of that range, so their mean cost is the range's: untimed
+    # greedy steps advance the cache there first.
+    pos_now = int(dec.pos.item())
+    start = max(pos_now, (CONFIG4_POSITIONS[0] + CONFIG4_POSITIONS[1] + 1) // 2 - args.steps // 2)
+    start = min(start, max(pos_now, CONFIG4_POSITIONS[1] + 1 - args.steps))
+    for _ in range(start - pos_now):
+        dec.graph.replay()
     torch.cuda.synchronize()
+    first_pos = int(dec.pos.item())
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    toks = torch.empty(args.steps, dtype=torch.int64, device=dev)
     h0 = time.perf_counter()
     e0.record()
     for i in range(args.steps):
@@ -289,8 +355,19 @@ def bench_decode(args, torch):
     host_s = time.perf_counter() - h0
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
-    del toks
     final_pos = int(dec.pos.item())
+
+    # The whole range once more, every step timed (a second prompt, same state).
+    dec.prefill(prompt)
+    n_range = CONFIG4_POSITIONS[1] + 1 - int(dec.pos.item())
+    torch.cuda.synchronize()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    for _ in range(n_range):
+        dec.graph.replay()
+    r1.record()
+    torch.cuda.synchronize()
+    range_ms = r0.elapsed_time(r1) / n_range
 
     # Dominant kernel, live: each int4 GEMV launch of the step exactly as the captured plan
     # issues it, over the model's own 36 layers (1.9 GB of distinct gate_up weights, so no
@@ -317,7 +394,7 @@ def bench_decode(args, torch):
                        (cfg.intermediate, cfg.hidden)))
     if args.v_keep:                       # the kept v_proj streams bf16 weights
         layer_bytes += 2 * nv * cfg.hidden + 2 * cfg.hidden + 4 * nv
-    avg_len = (prompt_len + args.warmup + 1 + final_pos) / 2
+    avg_len = (first_pos + 1 + final_pos) / 2
     kv_bytes = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim * 2 * avg_len
     step_bytes = cfg.n_layers * layer_bytes + 2 * cfg.vocab * cfg.hidden + kv_bytes
     del np
@@ -327,7 +404,11 @@ def bench_decode(args, torch):
         config={"workload": f"36-layer Qwen3-8B-shaped int4 GPTQ backbone (act-order g{cfg.group_size}"
                             + (", v_proj kept bf16" if args.v_keep else "") + ") + bf16 "
                             "head 151936x4096, batch 1, prefill 256 random ids then hipGraph greedy "
-                            f"decode, KV cache {prompt_len + args.warmup + 1}->{final_pos}",
+                            f"decode at positions 256..1279 (KV 257->1280); the timed steps run at "
+                            f"KV {first_pos + 1}->{final_pos}, the middle of that range",
+                "config4_full_range": {"positions": f"256..{CONFIG4_POSITIONS[1]}",
+                                       "steps": n_range, "ms_per_step": round(range_ms, 4),
+                                       "steps_per_s": round(1000.0 / range_ms, 2)},
                 "hidden": cfg.hidden, "layers": cfg.n_layers, "vocab": cfg.vocab,
                 "step_bytes_avg": int(step_bytes),
                 "step_hbm_gbs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
@@ -446,63 +527,37 @@ def bench_prefill(args, torch):
                       "gemm": out}))
 
 
-def cpu_baseline_decode(budget_s: float = 20.0):
-    """The oracle's restatement of the reference CPU path (dequantise each layer's
-    weights, float64 products, the step's bf16 rounding) on one full-size layer plus the
-    head, scaled to a 36-layer step."""
-    import numpy as np
-
-    from oracle import decode_ref as D
-    from oracle import gptq_ref as G
-    from oracle import synth
-    from oracle.bf16 import bf16_bits_to_f32
-
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
-    r = synth.rng(1234)
-    h, inter, g = 4096, 12288, 128
-
-    def lin(k, n):
-        return dict(qweight=synth.random_qweight(r, k, n), qzeros=synth.random_qzeros(r, k // g, n),
-                    scales=synth.random_scales(r, k // g, n),
-                    g_idx=G.actorder_g_idx(r.permutation(k), g))
-
-    raw = {"qkv": lin(h, 6144), "o": lin(h, h), "gate_up": lin(h, 2 * inter), "down": lin(inter, h)}
-    norm = np.ones(h, np.float32)
-    kc = np.zeros((8, 1280, 128), np.float32)
-    vc = np.zeros_like(kc)
-    kc[:, :767] = bf16_bits_to_f32(synth.random_x_bits(r, 8 * 767, 128)).reshape(8, 767, 128)
-    vc[:, :767] = kc[:, :767][:, ::-1]
-    cos, sin = D.rope_tables(1280, 128)
-    x0 = bf16_bits_to_f32(synth.random_x_bits(r, 1, h))[0]
-    layers_timed, t_layer = 0, 0.0
-    t_end = time.time() + budget_s
-    while layers_timed == 0 or time.time() < t_end:
-        t = time.perf_counter()
-        w = {k: G.gptq_dequant(v["qweight"], v["qzeros"], v["scales"], v["g_idx"], g)
-             for k, v in raw.items()}
-        lw = {"input_layernorm": norm, "post_attention_layernorm": norm,
-              "q_norm": np.ones(128, np.float32), "k_norm": np.ones(128, np.float32),
-              "q": w["qkv"][:, :4096], "k": w["qkv"][:, 4096:5120], "v": w["qkv"][:, 5120:],
-              "o": w["o"], "gate": w["gate_up"][:, 0::2], "up": w["gate_up"][:, 1::2],
-              "down": w["down"]}
-        D.decoder_layer(x0, lw, kc, vc, 767, cos, sin, 32, 8, 128)
-        t_layer += time.perf_counter() - t
-        layers_timed += 1
-    t_layer /= layers_timed
-    rows = 16384
-    head = bf16_bits_to_f32(synth.random_x_bits(r, rows, h))
-    t = time.perf_counter()
-    head @ x0.astype(np.float32)
-    t_head = (time.perf_counter() - t) * 151936 / rows
-    step_s = 36 * t_layer + t_head
-    return {"value": round(1.0 / step_s, 5), "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"{layers_timed} full-size decoder layers at KV length 768 (dequantise + "
-                      f"float64 products, {t_layer:.2f} s/layer) + a 16384-row slice of the "
-                      f"151936x4096 head ({t_head:.2f} s scaled), scaled to 36 layers"}
+def cpu_baseline_decode(torch, gpu_us: dict):
+    """The reference's CPU path for one decode step of the 36-layer model, timed per
+    linear: each layer's four int4 linears at M = 1 through effective_weight + fp32 x @ W.T
+    (oracle/cpu_path.py, tests/test_quant.py:104-107), plus a 16384-row slice of the bf16
+    head (F.linear) scaled to 151936 rows. The step is 36 layers' linears and the head
+    (norms, RoPE and attention are under 1 % of it). Also given: the same step with torch's
+    CPU int4 GEMM, and every datapoint at 1 thread."""
+    n_all = _cpu_threads()
+    per = cpu_linear_datapoints(torch, GEMV_SHAPES)
+    head = torch.randn(16384, 4096, generator=torch.Generator().manual_seed(5)).bfloat16() * 0.02
+    hf = torch.randn(4096, generator=torch.Generator().manual_seed(6)).bfloat16()
+    saved = torch.get_num_threads()
+    steps = {}
+    for threads in (1, n_all):
+        torch.set_num_threads(threads)
+        t_head = _median_s(lambda: torch.nn.functional.linear(hf, head), 1.0)[0] * 151936 / 16384
+        for label in ("fp32", "int4_cpu"):
+            t_layers = sum(d[f"{label}_{threads}t_us"] for d in per.values()) * 1e-6
+            steps[f"{label}_{threads}t"] = round(1.0 / (36 * t_layers + t_head), 4)
+    torch.set_num_threads(saved)
+    for name, d in per.items():
+        if name in gpu_us:
+            d["gpu_speedup_vs_fp32_all"] = round(d[f"fp32_{n_all}t_us"] / gpu_us[name], 1)
+            d["gpu_speedup_vs_int4_cpu_all"] = round(d[f"int4_cpu_{n_all}t_us"] / gpu_us[name], 1)
+    return {"value": steps[f"fp32_{n_all}t"], "unit": "steps/s", "cores": n_all, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": "one decode step of the 36-layer model from per-linear timings: the four "
+                      "decode-step linears at M=1 (effective_weight dequant + fp32 x @ W.T in "
+                      f"torch, median of up to 20 calls each) x 36 + the bf16 head, on {n_all} "
+                      "threads",
+            "steps_per_s": steps, "per_shape": per}
 
 
 def bench_int4_op(args, torch):
@@ -608,12 +663,14 @@ def main():
         args.warmup = 16 if args.warmup is None else args.warmup
         args.steps = 1024 - args.warmup if args.steps is None else args.steps
         res = bench_decode(args, torch)
-        cpu = None if args.no_cpu_baseline else cpu_baseline_decode()
+        cpu = None if args.no_cpu_baseline else cpu_baseline_decode(torch,
+                                                                    res["config"]["gemv_us"])
     else:
         args.warmup = 20 if args.warmup is None else args.warmup
         args.steps = 200 if args.steps is None else args.steps
         res = bench_gemv(args, torch, pkg)
-        cpu = None if args.no_cpu_baseline else cpu_baseline_gemv()
+        cpu = None if args.no_cpu_baseline else cpu_baseline_gemv(
+            torch, {k: v["us"] for k, v in res["config"]["per_kernel"].items()})
     line = {
         "metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1,
         "steps": res["steps"], "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 6),
