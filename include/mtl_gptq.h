@@ -15,9 +15,14 @@
  *   - Entry points are stateless and reentrant.  A workspace belongs to one
  *     stream at a time: two launches that share a workspace must be ordered.
  *
- * Weight layout (both contracts): `qweight` int32 [K/8, N]; the 4-bit code of
- * input channel k = 8*i + j of output column n is bits [4j, 4j+4) of
- * qweight[i*N + n] (AutoGPTQ order, low nibble first).
+ * Weight layouts.  AutoGPTQ: `qweight` int32 [K/8, N]; the 4-bit code of input channel
+ * k = 8*i + j of output column n is bits [4j, 4j+4) of qweight[i*N + n] (low nibble
+ * first).  The reference's contract (mtl_int4pack_*): the strip layout of that qweight
+ * (mtl_w4_strip): 1 KB block (s * K/128 + b) holds columns 16s .. 16s+15 over input
+ * channels 128b .. 128b+127, word j of its 16-byte word l the qweight word (row
+ * 16b + 4j + l/16, column 16s + l%16).  A column strip is one contiguous K*8-byte run, so
+ * the N*K/8 words, shaped as torch's [N/8, K/(16*T), 32, T/2], concatenate along dim 0
+ * exactly as a concatenation of the weights along N.
  */
 #ifndef MTL_GPTQ_H
 #define MTL_GPTQ_H
@@ -55,9 +60,13 @@ enum {
 enum {
   MTL_LAYOUT_ROWS = 0,    /* qweight int32 [K/8, N] as everywhere else                  */
   MTL_LAYOUT_TILED = 1,   /* mtl_w4_tile output (M = 1, N % 64 == 0, no perm)           */
-  MTL_LAYOUT_STRIP = 2    /* mtl_w4_strip output (M = 1, N % 16 == 0, K % 256 == 0,
+  MTL_LAYOUT_STRIP = 2,   /* mtl_w4_strip output (M = 1, N % 16 == 0, K % 256 == 0,
                              K <= 16384, no perm), with scales/qzeros in the strip order
                              of mtl_w4_strip_meta: full-K strip GEMV, no split-K       */
+  MTL_LAYOUT_STRIP_QSZ = 3 /* the same strip-layout weights (mtl_w4_strip, or the output of
+                             mtl_int4pack_convert / mtl_int4pack_from_torch_tiles) with the
+                             reference's metadata: `scales` is qsz bf16 [K/g, N, 2]
+                             (w = (q - 8) * scale + zero), `qzeros` and zero_offset unused */
 };
 
 /* Metadata format of mtl_w4_gemm_fused. */
@@ -129,13 +138,21 @@ int mtl_gptq_actorder_prepare(const int32_t* qweight, const int32_t* g_idx,
 
 /*
  * Reference-contract GEMM: y[M,N] = x[M,K] @ W^T with
- * W[n,k] = (q-8)*qsz[k/g,n,0] + qsz[k/g,n,1] (bf16 pair widened to fp32).
+ * W[n,k] = (q-8)*qsz[k/g,n,0] + qsz[k/g,n,1] (bf16 pair widened to fp32), fp32 sums.
  * Replaces torch._weight_int4pack_mm(x, packed, g, qsz) at
  * moss_tts_lite/fast.py:118, gptq.py:582, fast_native.py:169.
- *   packed  int32 [K/8, N] from mtl_int4pack_convert (NOT torch's tiled bytes)
- *   qsz     bf16 [K/g, N, 2]
- *   y       bf16 [M, N]
+ *   x       bf16 [M, K], any M >= 1
+ *   packed  strip layout from mtl_int4pack_convert or mtl_int4pack_from_torch_tiles
+ *           (N*K/8 words; NOT torch's tiled bytes)
+ *   qsz     bf16 [K/g, N, 2], read in place
+ *   y       bf16 [M, N], 8-byte aligned
+ *   workspace  NULL, or mtl_int4pack_mm_workspace_bytes(M, K, N) bytes: lets a launch
+ *           with M > 1 split K over workgroups (results then differ by fp32 rounding)
+ * M = 1 runs the full-K strip GEMV; M > 1 the prompt-length GEMM (N % 128 == 0), else
+ * one strip GEMV per row.  K % 256 == 0, K % g == 0, N % 16 == 0 (torch asks N % 8 only);
+ * the strip GEMV serves K <= 16384.
  */
+int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
                     int32_t group_size, const void* qsz, int64_t N, void* y,
                     void* workspace, int64_t ws_bytes, void* stream);
@@ -143,15 +160,16 @@ int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
 /*
  * Reference-contract packer: the reference's nibble pre-pack uint8 [N, K/2]
  * (byte = q[n,2i]<<4 | q[n,2i+1], moss_tts_lite/fast.py:98, gptq.py:76) ->
- * packed int32 [K/8, N].  Replaces torch.ops.aten._convert_weight_to_int4pack
- * (fast.py:97, gptq.py:75); inner_k_tiles is accepted for signature parity and
- * must be 2, 4 or 8 (it does not change this layout).
+ * packed: the strip layout, N*K/8 int32 words.  Replaces
+ * torch.ops.aten._convert_weight_to_int4pack (fast.py:97, gptq.py:75); inner_k_tiles is
+ * accepted for signature parity and must be 2, 4 or 8 (it does not change this layout).
+ * K % 256 == 0, N % 16 == 0.
  */
 int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K,
                          int32_t inner_k_tiles, int32_t* packed, void* stream);
 
 /*
- * torch's tiled int4 tensor -> packed int32 [K/8, N] (the mtl_int4pack_convert layout).
+ * torch's tiled int4 tensor -> packed, the strip layout of mtl_int4pack_convert.
  * Ingests the `.q` records of the reference's standalone export
  * (moss_tts_lite/export.py:324-334, read back at export.py:691-734 and handed to
  * torch._weight_int4pack_mm): the int32 [N/8, K/(16*T), 32, T/2] tensor that
@@ -250,6 +268,13 @@ int mtl_w4_gemm_prefill(const void* x, int64_t M, int64_t ldx, int64_t K,
                         const int32_t* strip_zeros, int64_t N, int32_t group_size,
                         int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
                         int64_t ldy, float* workspace, int64_t ws_bytes, void* stream);
+/* The same GEMM with the reference's metadata: qsz bf16 [K/g, N, 2] read in place,
+ * W[n,k] = (q-8)*scale + zero (moss_tts_lite/gptq.py:87-97; the quantized prefill of
+ * fast.py:218-270 runs its projections through torch._weight_int4pack_mm on such weights). */
+int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,
+                            const int32_t* strip_weight, const void* qsz, int64_t N,
+                            int32_t group_size, int32_t epilogue, int32_t out_dtype, void* y,
+                            int64_t ldy, float* workspace, int64_t ws_bytes, void* stream);
 
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
@@ -260,8 +285,9 @@ int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* code
 int mtl_gptq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales,
                      int64_t K, int64_t N, int32_t group_size, int32_t zero_offset,
                      float* w_out, void* stream);
-/* Same for the reference contract: fp32 W[K, N] = effective_weight(q, qsz).T
- * (moss_tts_lite/gptq.py:87-97). */
+/* Same for the reference contract, from the strip layout of mtl_int4pack_convert:
+ * fp32 W[K, N] = effective_weight(q, qsz).T (moss_tts_lite/gptq.py:87-97).
+ * K % 256 == 0, N % 16 == 0. */
 int mtl_qsz_dequant(const int32_t* packed, const void* qsz, int64_t K, int64_t N,
                     int32_t group_size, float* w_out, void* stream);
 

@@ -91,6 +91,10 @@ _SIGNATURES = {
                                    _i64, _i32, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p,
                                    _i64, _c_void_p]),
     "mtl_w4_gemm_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "mtl_w4_gemm_prefill_qsz": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64,
+                                       _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _i64,
+                                       _c_void_p]),
+    "mtl_int4pack_mm_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "mtl_embed_rows": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _i64, _c_void_p,
                               _c_void_p]),
     "mtl_rmsnorm_gather": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
@@ -129,7 +133,7 @@ MTL_ERR_LAUNCH = -6
 MTL_ERR_UNSUPPORTED = -7
 
 OUT_BF16, OUT_F32 = 0, 1
-LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_STRIP = 0, 1, 2
+LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_STRIP, LAYOUT_STRIP_QSZ = 0, 1, 2, 3
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 META_GPTQ, META_QSZ = 0, 1
 

@@ -133,14 +133,40 @@ __device__ __forceinline__ void strip_meta_decode(const StripMeta<MB>& m, int lj
   }
 }
 
-// Arguments of the full-K strip GEMV (mtl_w4strip.hip), M = 1, AutoGPTQ meta.  The source
-// of x is xpart (SiLU*up), else hn (RMSNorm), else x; the epilogue is SiLU*up into act
-// when act is set (RMSNorm source only), the residual add when h is set, else an fp32
-// store to y.
+// Group metadata of the strip-layout kernels.
+enum : int {
+  STRIP_META_GPTQ = 0,  // fp16 scales and zero nibbles in the strip order of mtl_w4_strip_meta:
+                        // w = (q - z - zero_offset) * s
+  STRIP_META_QSZ = 1    // the reference's qsz bf16 [K/g, N, 2] (scale, zero) pairs, in place:
+                        // w = (q - 8) * scale + zero (moss_tts_lite/gptq.py:87-97)
+};
+
+// One (scale, zero) pair of the reference's qsz for group gidx of column col: 4 bytes at
+// (gidx * N + col) * 4 (a per-lane column offset and a uniform group offset).
+__device__ __forceinline__ uint32_t qsz_load(__amdgpu_buffer_rsrc_t qrsrc, int col, int gidx,
+                                             int N) {
+  return __builtin_amdgcn_raw_buffer_load_b32(qrsrc, col * 4, gidx * N * 4, 0);
+}
+
+// The group correction of both contracts.  The MFMA accumulates A = sum (128 + q) * x over
+// the group exactly in fp32 products; with X the group's sum of x, the group adds
+// s * (A - c * X) + d * X: (s, 128 + z + zero_offset, 0) for GPTQ metadata, and
+// (scale, 136, zero) for the reference's qsz (136 = 128 + 8).
+__device__ __forceinline__ void qsz_decode(uint32_t sz, float& s, float& c, float& d) {
+  s = __uint_as_float(sz << 16);
+  c = 136.0f;
+  d = __uint_as_float(sz & 0xffff0000u);
+}
+
+// Arguments of the full-K strip GEMV (mtl_w4strip.hip), M = 1.  The source of x is xpart
+// (SiLU*up), else hn (RMSNorm), else x; the epilogue is SiLU*up into act when act is set
+// (RMSNorm source only), the residual add when h is set, else a store to y (fp32) or y16
+// (bf16).  fmt is the group metadata (STRIP_META_*): with STRIP_META_QSZ, scales points at
+// the reference's qsz and qzeros is unused.
 struct StripArgs {
   const u32x4* w;             // strip layout of mtl_w4_strip
-  const uint16_t* scales;     // fp16 [G, N]
-  const uint32_t* qzeros;     // int32 [G, N/8]
+  const uint16_t* scales;     // strip-ordered fp16 scales, or the qsz pairs
+  const uint32_t* qzeros;     // strip-ordered zero nibbles (GPTQ metadata)
   const uint16_t* x;          // bf16 [K] in the weight's input order
   const float* xpart;         // gate|up partials [xsplits, xpart_ld]
   int xsplits, xpart_ld;
@@ -149,12 +175,13 @@ struct StripArgs {
   const float* slots;
   float eps;
   float* y;                   // fp32 [N]
+  uint16_t* y16;              // bf16 [N] (store epilogue, when set instead of y)
   uint16_t* h;                // bf16 [N], updated in place
   const int32_t* scatter;     // h_ord[scatter[n]] = h[n] (NULL: identity)
   uint16_t* h_ord;            // may be NULL
   float* slots_out;           // one sum of squares per 16 columns
   uint16_t* act;              // bf16 [N/2]: silu(gate) * up, 32-column gate|up interleave
-  int K, N, group, zero_offset, kblocks, xcd_order;
+  int K, N, group, zero_offset, kblocks, xcd_order, fmt;
 };
 
 enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };

@@ -715,12 +715,16 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
 // Partials-only launch for fused consumers: writes fp32 [splits, M, N] into `partials`
 // (splits = w4_splits(K)); x comes from `x` (bf16, optionally through `perm`) or, when
 // `xpart` is set, from the gate|up partials of the previous GEMV (SiLU*up, M = 1).
+static bool is_strip(int layout) {
+  return layout == MTL_LAYOUT_STRIP || layout == MTL_LAYOUT_STRIP_QSZ;
+}
+
 static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32_t* perm,
                         int group) {
-  if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED && layout != MTL_LAYOUT_STRIP)
+  if (layout != MTL_LAYOUT_ROWS && layout != MTL_LAYOUT_TILED && !is_strip(layout))
     return MTL_ERR_INVALID_ARG;
   if (layout == MTL_LAYOUT_TILED && (N % kWaveN != 0 || M != 1 || perm)) return MTL_ERR_SHAPE;
-  if (layout == MTL_LAYOUT_STRIP &&
+  if (is_strip(layout) &&
       (M != 1 || perm || N <= 0 || N % 16 != 0 || K > 16384 ||
        !strip_blocks_per_wave(K, 1, group) ||
        N * K / 2 >= ((int64_t)1 << 31)))
@@ -728,15 +732,25 @@ static int check_layout(int layout, int64_t M, int64_t K, int64_t N, const int32
   return MTL_OK;
 }
 
-// The strip GEMV reads 16 scales (32 B) and 16 zero nibbles (8 B) of a strip at a time.
-static bool strip_meta_aligned(const void* scales, const int32_t* qzeros) {
+// The strip GEMV reads 16 scales (32 B) and 16 zero nibbles (8 B) of a strip at a time
+// (GPTQ metadata), or one 4-byte (scale, zero) pair per lane (the reference's qsz).
+static bool strip_meta_aligned(int layout, const void* scales, const int32_t* qzeros) {
+  if (layout == MTL_LAYOUT_STRIP_QSZ) return (reinterpret_cast<uintptr_t>(scales) & 3u) == 0;
   return aligned16(scales) && (reinterpret_cast<uintptr_t>(qzeros) & 7u) == 0;
+}
+
+// The metadata pointers a layout needs: qzeros is unused with the reference's qsz.
+static bool meta_given(int layout, const void* meta0, const int32_t* qzeros) {
+  return meta0 && (qzeros || layout == MTL_LAYOUT_STRIP_QSZ);
 }
 
 // The strip GEMV's arguments common to every entry point.
 static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
-                            const int32_t* qzeros, int64_t N, int group, int zero_offset) {
+                            const int32_t* qzeros, int64_t N, int group, int zero_offset,
+                            int layout = MTL_LAYOUT_STRIP) {
   StripArgs a;
+  a.fmt = layout == MTL_LAYOUT_STRIP_QSZ ? STRIP_META_QSZ : STRIP_META_GPTQ;
+  a.y16 = nullptr;
   a.w = reinterpret_cast<const u32x4*>(w);
   a.scales = static_cast<const uint16_t*>(scales);
   a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
@@ -766,7 +780,8 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
                             int zero_offset, int layout, float* partials, int64_t partials_bytes,
                             hipStream_t stream) {
   if (const int st = check_layout(layout, M, K, N, perm, group)) return st;
-  if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !partials)
+  if ((!x && !xpart) || (x && xpart) || !qweight || !meta_given(layout, meta0, qzeros) ||
+      !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (M < 1 || M > kMaxM || K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0)
@@ -782,11 +797,10 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
   }
   if (!aligned16(qweight) || !aligned16(partials) || (perm && !aligned16(perm)))
     return MTL_ERR_ALIGN;
-  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
-  if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
+  if (is_strip(layout)) {   // full-K strips: the final sums, as one split
     if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
-    if (!strip_meta_aligned(meta0, qzeros)) return MTL_ERR_ALIGN;
-    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    if (!strip_meta_aligned(layout, meta0, qzeros)) return MTL_ERR_ALIGN;
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
     sa.x = static_cast<const uint16_t*>(x);
     sa.xpart = xpart;
     sa.xsplits = xsplits;
@@ -794,6 +808,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
     sa.y = partials;
     return strip_launch(sa, stream);
   }
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   const Plan p = plan_for(K, N, M, group);
   if (partials_bytes < (int64_t)p.splits * M * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
@@ -824,7 +839,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
                                  int zero_offset, int layout, float* partials,
                                  int64_t partials_bytes, hipStream_t stream) {
   if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
-  if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !partials)
+  if (!h_ord || !w_ord || !slots || !qweight || !meta_given(layout, meta0, qzeros) || !partials)
     return MTL_ERR_INVALID_ARG;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
@@ -832,11 +847,10 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (!weight_fits(K, N) || K > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
   if (!aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) || !aligned16(partials))
     return MTL_ERR_ALIGN;
-  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
-  if (layout == MTL_LAYOUT_STRIP) {   // full-K strips: the final sums, as one split
+  if (is_strip(layout)) {   // full-K strips: the final sums, as one split
     if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
-    if (!strip_meta_aligned(meta0, qzeros)) return MTL_ERR_ALIGN;
-    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    if (!strip_meta_aligned(layout, meta0, qzeros)) return MTL_ERR_ALIGN;
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
     sa.hn = static_cast<const uint16_t*>(h_ord);
     sa.wn = static_cast<const uint16_t*>(w_ord);
     sa.slots = slots;
@@ -844,6 +858,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
     sa.y = partials;
     return strip_launch(sa, stream);
   }
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   const Plan p = plan_for(K, N, 1, group);
   if (partials_bytes < (int64_t)p.splits * N * 4) return MTL_ERR_WORKSPACE;
   W4Args a = blank_args();
@@ -876,7 +891,8 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
                             int layout, void* h, const int32_t* scatter, void* h_ord,
                             float* slots, void* workspace, int64_t ws_bytes,
                             hipStream_t stream) {
-  if ((!x && !xpart) || (x && xpart) || !qweight || !meta0 || !qzeros || !h || !slots)
+  if ((!x && !xpart) || (x && xpart) || !qweight || !meta_given(layout, meta0, qzeros) || !h ||
+      !slots)
     return MTL_ERR_INVALID_ARG;
   if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
@@ -890,11 +906,11 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
     return MTL_ERR_ALIGN;
   }
   if (!aligned16(qweight) || (reinterpret_cast<uintptr_t>(h) & 7u)) return MTL_ERR_ALIGN;
-  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
-  if (layout == MTL_LAYOUT_STRIP) {
-    if (!aligned16(slots) || (scatter && !aligned16(scatter)) || !strip_meta_aligned(meta0, qzeros))
+  if (is_strip(layout)) {
+    if (!aligned16(slots) || (scatter && !aligned16(scatter)) ||
+        !strip_meta_aligned(layout, meta0, qzeros))
       return MTL_ERR_ALIGN;
-    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
     sa.x = static_cast<const uint16_t*>(x);
     sa.xpart = xpart;
     sa.xsplits = xsplits;
@@ -905,6 +921,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
     sa.slots_out = slots;
     return strip_launch(sa, stream);
   }
+  if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
   const Plan p = plan_for(K, N, 1, group);
   W4Args a = blank_args();
   if (p.splits > 1) {
@@ -943,18 +960,18 @@ static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* 
                              int64_t K, const int32_t* qweight, const void* meta0,
                              const int32_t* qzeros, int64_t N, int group, int zero_offset,
                              int layout, void* act, hipStream_t stream) {
-  if (!h_ord || !w_ord || !slots || !qweight || !meta0 || !qzeros || !act)
+  if (!h_ord || !w_ord || !slots || !qweight || !meta_given(layout, meta0, qzeros) || !act)
     return MTL_ERR_INVALID_ARG;
-  if (layout != MTL_LAYOUT_STRIP) return MTL_ERR_UNSUPPORTED;
+  if (!is_strip(layout)) return MTL_ERR_UNSUPPORTED;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 64 != 0 || K > 16384 ||
       !strip_blocks_per_wave(K, 2, group) ||
       N * K / 2 >= ((int64_t)1 << 31) || K > (int64_t)kSlotCols * kMaxSlots)
     return MTL_ERR_SHAPE;
   if (!aligned16(slots) || !aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) ||
-      (reinterpret_cast<uintptr_t>(act) & 7u) || !strip_meta_aligned(meta0, qzeros))
+      (reinterpret_cast<uintptr_t>(act) & 7u) || !strip_meta_aligned(layout, meta0, qzeros))
     return MTL_ERR_ALIGN;
-  StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset);
+  StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
   sa.hn = static_cast<const uint16_t*>(h_ord);
   sa.wn = static_cast<const uint16_t*>(w_ord);
   sa.slots = slots;
@@ -1057,14 +1074,6 @@ int mtl_gptq_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight,
                   void* workspace, int64_t ws_bytes, void* stream) {
   return w4_gemm(x, M, K, qweight, MTL_META_GPTQ, scales, qzeros, perm, N, group_size,
                  zero_offset, MTL_EPI_NONE, nullptr, y, out_dtype, workspace, ws_bytes,
-                 (hipStream_t)stream);
-}
-
-int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
-                    int32_t group_size, const void* qsz, int64_t N, void* y, void* workspace,
-                    int64_t ws_bytes, void* stream) {
-  return w4_gemm(x, M, K, packed, MTL_META_QSZ, qsz, nullptr, nullptr, N, group_size, 0,
-                 MTL_EPI_NONE, nullptr, y, MTL_OUT_BF16, workspace, ws_bytes,
                  (hipStream_t)stream);
 }
 

@@ -4,16 +4,31 @@
 
 namespace mtl {
 
-// prepacked uint8 [N, K/2] (byte i of row n = q[n,2i] << 4 | q[n,2i+1]) ->
-// qweight int32 [K/8, N] (code of k = 8r + j in bits [4j, 4j+4) of word (r, n)).
+// The strip layout (mtl_w4strip.hip) as 32-bit words: word (r, n) of a qweight [K/8, N]
+// (channels 8r .. 8r+7 of column n) is word j = (r / 4) % 4 of 16-byte word
+// l = 16 (r % 4) + n % 16 of 1 KB block (n / 16) * K/128 + r / 16.  Output index t of the
+// layout maps back to (r, n) here.
+__device__ __forceinline__ void strip_word_rn(int64_t t, int64_t kb, int64_t& r, int64_t& n) {
+  const int64_t j = t & 3, l = (t >> 2) & 63, blk = t >> 8;
+  const int64_t b = blk % kb, s = blk / kb;
+  n = 16 * s + (l & 15);
+  r = 16 * b + (l >> 4) + 4 * j;
+}
+
+__device__ __forceinline__ int64_t strip_word_index(int64_t r, int64_t n, int64_t kb) {
+  return (((n >> 4) * kb + (r >> 4)) * 64 + 16 * (r & 3) + (n & 15)) * 4 + ((r >> 2) & 3);
+}
+
+// prepacked uint8 [N, K/2] (byte i of row n = q[n,2i] << 4 | q[n,2i+1]) -> the strip
+// layout, whose word (r, n) holds the code of k = 8r + j in bits [4j, 4j+4).
 __global__ void int4pack_convert_kernel(const uint8_t* __restrict__ pre, int64_t N, int64_t K,
                                         uint32_t* __restrict__ out) {
-  const int64_t rows = K / 8;
-  const int64_t total = rows * N;
+  const int64_t total = (K / 8) * N;
+  const int64_t kb = K / 128;
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = t / N;
-    const int64_t n = t - r * N;
+    int64_t r, n;
+    strip_word_rn(t, kb, r, n);
     const uint32_t b4 = *reinterpret_cast<const uint32_t*>(pre + n * (K / 2) + r * 4);
     uint32_t w = 0;
 #pragma unroll
@@ -33,7 +48,7 @@ __global__ void int4pack_convert_kernel(const uint8_t* __restrict__ pre, int64_t
 // (b * 32 + c) * half + d, nibble e, where b = 2 * (j / half) + r3, d = j % half,
 // c = 16 * r2 + n % 16 and e = r1 | r4 << 1 | r0 << 2.  Output word (q8, n) holds channels
 // 8q8 .. 8q8+7: r3 and r4 come from q8, r2 splits them between two torch words
-// (c = n % 16 for the first four, +16 for the last four).
+// (c = n % 16 for the first four, +16 for the last four).  Written in the strip layout.
 __global__ void int4pack_from_torch_kernel(const uint32_t* __restrict__ tiles, int64_t N,
                                            int64_t K, int half, uint32_t* __restrict__ out) {
   const int64_t rows = K / 8;
@@ -41,8 +56,8 @@ __global__ void int4pack_from_torch_kernel(const uint32_t* __restrict__ tiles, i
   const int64_t kb = K / 256;
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t q8 = t / N;
-    const int64_t n = t - q8 * N;
+    int64_t q8, n;
+    strip_word_rn(t, K / 128, q8, n);
     const int j = (int)(q8 >> 2) & 7;
     const int r3 = (int)q8 & 1, r4 = (int)(q8 >> 1) & 1;
     const int b = 2 * (j / half) + r3, d = j % half;
@@ -91,7 +106,8 @@ __global__ void tile_weights_kernel(const uint4* __restrict__ qw, int64_t rows, 
   }
 }
 
-// fp32 W[K, N]; fmt GPTQ: (q - (z + zero_offset)) * s ; QSZ: (q - 8) * scale + zero.
+// fp32 W[K, N]; fmt GPTQ: (q - (z + zero_offset)) * s over a qweight [K/8, N];
+// QSZ: (q - 8) * scale + zero over the strip layout of mtl_int4pack_convert.
 template <int FMT>
 __global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* __restrict__ meta0,
                                const uint32_t* __restrict__ qzeros, int64_t K, int64_t N,
@@ -101,7 +117,7 @@ __global__ void dequant_kernel(const uint32_t* __restrict__ qw, const uint16_t* 
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = t / N;
     const int64_t n = t - r * N;
-    const uint32_t w = qw[t];
+    const uint32_t w = FMT == MTL_META_QSZ ? qw[strip_word_index(r, n, K / 128)] : qw[t];
     const int64_t grp = (r * 8) / group;
     float s, c, d;
     if (FMT == MTL_META_QSZ) {
@@ -187,8 +203,9 @@ int mtl_int4pack_convert(const uint8_t* prepacked, int64_t N, int64_t K, int32_t
                          int32_t* packed, void* stream) {
   if (!prepacked || !packed) return MTL_ERR_INVALID_ARG;
   if (inner_k_tiles != 2 && inner_k_tiles != 4 && inner_k_tiles != 8) return MTL_ERR_INVALID_ARG;
-  if (N <= 0 || K <= 0 || K % 8 != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
-  if (reinterpret_cast<uintptr_t>(prepacked) & 3u) return MTL_ERR_ALIGN;
+  if (N <= 0 || K <= 0 || K % 256 != 0 || N % 16 != 0) return MTL_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(prepacked) & 3u) || (reinterpret_cast<uintptr_t>(packed) & 3u))
+    return MTL_ERR_ALIGN;
   const int64_t total = (K / 8) * N;
   hipLaunchKernelGGL(int4pack_convert_kernel, dim3(grid_for(total)), dim3(256), 0,
                      (hipStream_t)stream, prepacked, N, K, reinterpret_cast<uint32_t*>(packed));
@@ -256,7 +273,8 @@ int mtl_qsz_dequant(const int32_t* packed, const void* qsz, int64_t K, int64_t N
                     float* w_out, void* stream) {
   if (!packed || !qsz || !w_out) return MTL_ERR_INVALID_ARG;
   if (!valid_group(group_size)) return MTL_ERR_GROUP;
-  if (N <= 0 || K <= 0 || K % group_size != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
+  if (N <= 0 || K <= 0 || K % group_size != 0 || K % 256 != 0 || N % 16 != 0)
+    return MTL_ERR_SHAPE;
   const int64_t total = (K / 8) * N;
   hipLaunchKernelGGL((dequant_kernel<MTL_META_QSZ>), dim3(grid_for(total)), dim3(256), 0,
                      (hipStream_t)stream, reinterpret_cast<const uint32_t*>(packed),

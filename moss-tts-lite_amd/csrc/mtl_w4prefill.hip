@@ -35,8 +35,8 @@ constexpr int kPfMaxSplits = 8;
 struct PrefillArgs {
   const uint16_t* x;          // bf16 [M, K], rows ldx apart, in the weight's input order
   const u32x4* w;             // strip layout
-  const uint16_t* scales;     // strip-ordered fp16 scales
-  const uint32_t* qzeros;     // strip-ordered zero nibbles
+  const uint16_t* scales;     // strip-ordered fp16 scales, or the reference's qsz pairs
+  const uint32_t* qzeros;     // strip-ordered zero nibbles (GPTQ metadata)
   void* y;                    // see the epilogues
   float* part;                // splits > 1: fp32 partial sums [splits][M][N]
   int64_t ldx, ldy;
@@ -63,7 +63,7 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
-template <int GR, int EPI>
+template <int GR, int EPI, int FMT>
 __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEU)))
 w4_prefill_kernel(PrefillArgs a) {
   constexpr int MB = GR <= 4 ? 4 / GR : 1;       // groups starting in one block
@@ -116,17 +116,27 @@ w4_prefill_kernel(PrefillArgs a) {
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / 16) * kb * 1024), 0x00020000);
   const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.scales), (short)0, ngroups * N * 2, 0x00020000);
+      const_cast<uint16_t*>(a.scales), (short)0,
+      FMT == STRIP_META_QSZ ? ngroups * N * 4 : ngroups * N * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
+      const_cast<uint32_t*>(a.qzeros), (short)0,
+      FMT == STRIP_META_QSZ ? 0 : ngroups * (N >> 1), 0x00020000);
   u32x4 wq[D][2];
-  StripMeta<MB> mt[D][2];
+  StripMeta<MB> mt[FMT == STRIP_META_GPTQ ? D : 1][2];
+  uint32_t mq[FMT == STRIP_META_QSZ ? D : 1][2][MB];   // the reference's (scale, zero) pairs
   auto issue = [&](int r, int b) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int strip = sA + s;
-      if (GR <= 4 || (r & 1) == 0)
-        strip_meta_load<MB>(srsrc, zrsrc, lj, strip * krec + (GR == 8 ? b >> 1 : b), mt[r][s]);
+      if (GR <= 4 || (r & 1) == 0) {
+        if constexpr (FMT == STRIP_META_GPTQ) {
+          strip_meta_load<MB>(srsrc, zrsrc, lj, strip * krec + (GR == 8 ? b >> 1 : b), mt[r][s]);
+        } else {
+#pragma unroll
+          for (int m = 0; m < MB; ++m)
+            mq[r][s][m] = qsz_load(srsrc, 16 * strip + lj, GR == 8 ? b >> 1 : b * MB + m, N);
+        }
+      }
       wq[r][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                wrsrc, lane * 16, (strip * kb + b) * 1024, 0));
     }
@@ -147,7 +157,7 @@ w4_prefill_kernel(PrefillArgs a) {
   // Chunks per correction: a group (g <= 128), or a block at g = 256, whose group's two
   // blocks are folded one after the other with the pair's scale and zero.
   constexpr int GC = GR <= 4 ? GR : 4;
-  float gs[2][MB], gz[2][MB];
+  float gs[2][MB], gz[2][MB], gd[2][MB];
 
   for (int b0 = kb0; b0 < kb1; b0 += D) {
 #pragma unroll
@@ -156,7 +166,14 @@ w4_prefill_kernel(PrefillArgs a) {
       const int buf = r & 1;                     // b0 - kb0 and kb0 are even
       if (GR <= 4 || (r & 1) == 0) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) strip_meta_decode<MB>(mt[r][s], lj, a.zero_offset, gs[s], gz[s]);
+        for (int s = 0; s < 2; ++s) {
+          if constexpr (FMT == STRIP_META_GPTQ) {
+            strip_meta_decode<MB>(mt[r][s], lj, a.zero_offset, gs[s], gz[s]);
+          } else {
+#pragma unroll
+            for (int m = 0; m < MB; ++m) qsz_decode(mq[r][s][m], gs[s][m], gz[s][m], gd[s][m]);
+          }
+        }
       }
       bf16x8_t B[2][4];
 #pragma unroll
@@ -193,6 +210,10 @@ w4_prefill_kernel(PrefillArgs a) {
           for (int i = 0; i < 4; ++i) {
             tot[tt][0][i] = fmaf(gs[0][0], fmaf(-gz[0][0], X[i], acc[tt & 1][0][i]), tot[tt][0][i]);
             tot[tt][1][i] = fmaf(gs[1][0], fmaf(-gz[1][0], X[i], acc[tt & 1][1][i]), tot[tt][1][i]);
+            if constexpr (FMT == STRIP_META_QSZ) {
+              tot[tt][0][i] = fmaf(gd[0][0], X[i], tot[tt][0][i]);
+              tot[tt][1][i] = fmaf(gd[1][0], X[i], tot[tt][1][i]);
+            }
           }
           x_store_part(buf ^ 1, tt);             // block b + 1, loaded during block b - 1
           asm volatile("" ::"v"(tot[tt][0]), "v"(tot[tt][1]) : "memory");
@@ -228,6 +249,10 @@ w4_prefill_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
               tot[tt][0][i] = fmaf(gs[0][m], fmaf(-gz[0][m], X[i], acc0[i]), tot[tt][0][i]);
               tot[tt][1][i] = fmaf(gs[1][m], fmaf(-gz[1][m], X[i], acc1[i]), tot[tt][1][i]);
+              if constexpr (FMT == STRIP_META_QSZ) {
+                tot[tt][0][i] = fmaf(gd[0][m], X[i], tot[tt][0][i]);
+                tot[tt][1][i] = fmaf(gd[1][m], X[i], tot[tt][1][i]);
+              }
             }
           }
         }
@@ -385,10 +410,10 @@ static int pf_device_cus() {
   return g_pf_cus;
 }
 
-template <int GR, int EPI>
+template <int GR, int EPI, int FMT>
 static void prefill_launch(const PrefillArgs& a, hipStream_t st) {
   const dim3 grid(a.N / kPfCols, (a.M + kPfRows - 1) / kPfRows, a.splits), block(64 * kPfWaves);
-  hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI, FMT>), grid, block, 0, st, a);
   if (a.splits > 1) {
     const int64_t ncols = EPI == MTL_EPI_SILU_MUL ? a.N / 2 : a.N;
     const int64_t threads = (int64_t)a.M * (ncols / 4);
@@ -397,11 +422,78 @@ static void prefill_launch(const PrefillArgs& a, hipStream_t st) {
   }
 }
 
-template <int GR>
+template <int GR, int FMT>
 static void prefill_epi(const PrefillArgs& a, int epilogue, hipStream_t st) {
-  if (epilogue == MTL_EPI_RESIDUAL) prefill_launch<GR, MTL_EPI_RESIDUAL>(a, st);
-  else if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL>(a, st);
-  else prefill_launch<GR, MTL_EPI_NONE>(a, st);
+  if (epilogue == MTL_EPI_RESIDUAL) prefill_launch<GR, MTL_EPI_RESIDUAL, FMT>(a, st);
+  else if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL, FMT>(a, st);
+  else prefill_launch<GR, MTL_EPI_NONE, FMT>(a, st);
+}
+
+template <int FMT>
+static void prefill_group(const PrefillArgs& a, int epilogue, hipStream_t st) {
+  switch (a.group) {
+    case 32: prefill_epi<1, FMT>(a, epilogue, st); break;
+    case 64: prefill_epi<2, FMT>(a, epilogue, st); break;
+    case 128: prefill_epi<4, FMT>(a, epilogue, st); break;
+    default: prefill_epi<8, FMT>(a, epilogue, st); break;
+  }
+}
+
+// Both metadata contracts (fmt: STRIP_META_*); with STRIP_META_QSZ, scales is the
+// reference's qsz bf16 [K/g, N, 2] and zeros is unused.
+static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
+                        const int32_t* strip_weight, const void* scales, const int32_t* zeros,
+                        int64_t N, int32_t group_size, int32_t zero_offset, int32_t epilogue,
+                        int32_t out_dtype, void* y, int64_t ldy, float* workspace,
+                        int64_t ws_bytes, int fmt, hipStream_t st);
+
+static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
+                             const int32_t* strip_weight, const void* scales,
+                             const int32_t* zeros, int64_t N, int32_t group_size,
+                             int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
+                             int64_t ldy, float* workspace, int64_t ws_bytes, int fmt,
+                             hipStream_t st) {
+  if (!x || !strip_weight || !scales || !y) return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL)
+    return MTL_ERR_INVALID_ARG;
+  if (out_dtype != MTL_OUT_BF16 && out_dtype != MTL_OUT_F32) return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && out_dtype != MTL_OUT_BF16) return MTL_ERR_INVALID_ARG;
+  if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
+    return MTL_ERR_GROUP;
+  const int64_t ncols = epilogue == MTL_EPI_SILU_MUL ? N / 2 : N;
+  const int64_t meta_bytes = fmt == STRIP_META_QSZ ? 4 : 2;
+  if (M < 1 || M > (int64_t)kPfRows * 65535 || K <= 0 || N <= 0 || K % 256 != 0 ||
+      K > 65536 || N % kPfCols != 0 || K % group_size != 0 || ldx < K || ldy < ncols ||
+      (N / 16) * (K / 128) * 1024 >= ((int64_t)1 << 31) || M * ldx * 2 >= ((int64_t)1 << 31) ||
+      (K / group_size) * N * meta_bytes >= ((int64_t)1 << 31))
+    return MTL_ERR_SHAPE;
+  const bool meta_ok = fmt == STRIP_META_QSZ ? (reinterpret_cast<uintptr_t>(scales) & 3u) == 0
+                                             : aligned16(scales);
+  if (!aligned16(x) || ldx % 8 != 0 || !aligned16(strip_weight) || !meta_ok ||
+      (workspace && !aligned16(workspace)) ||
+      (reinterpret_cast<uintptr_t>(y) & (out_dtype == MTL_OUT_F32 ? 3u : 1u)))
+    return MTL_ERR_ALIGN;
+  PrefillArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = reinterpret_cast<const u32x4*>(strip_weight);
+  a.scales = static_cast<const uint16_t*>(scales);
+  a.qzeros = reinterpret_cast<const uint32_t*>(zeros);
+  a.y = y;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = (int)M; a.K = (int)K; a.N = (int)N;
+  a.group = group_size;
+  a.zero_offset = zero_offset;
+  a.kblocks = (int)(K / 128);
+  a.out_f32 = out_dtype == MTL_OUT_F32;
+  // K splits when the workspace holds their partial sums, else one pass
+  const int64_t need = mtl_w4_gemm_prefill_workspace_bytes(M, K, N);
+  a.splits = need > 0 && workspace && ws_bytes >= need ? (int)(need / (M * N * 4)) : 1;
+  a.kps = a.kblocks / a.splits;
+  a.part = workspace;
+  if (fmt == STRIP_META_QSZ) prefill_group<STRIP_META_QSZ>(a, epilogue, st);
+  else prefill_group<STRIP_META_GPTQ>(a, epilogue, st);
+  return launch_status();
 }
 
 }  // namespace mtl
@@ -422,49 +514,66 @@ int mtl_w4_gemm_prefill(const void* x, int64_t M, int64_t ldx, int64_t K,
                         const int32_t* strip_zeros, int64_t N, int32_t group_size,
                         int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
                         int64_t ldy, float* workspace, int64_t ws_bytes, void* stream) {
-  if (!x || !strip_weight || !strip_scales || !strip_zeros || !y) return MTL_ERR_INVALID_ARG;
-  if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL)
-    return MTL_ERR_INVALID_ARG;
-  if (out_dtype != MTL_OUT_BF16 && out_dtype != MTL_OUT_F32) return MTL_ERR_INVALID_ARG;
-  if (epilogue != MTL_EPI_NONE && out_dtype != MTL_OUT_BF16) return MTL_ERR_INVALID_ARG;
+  if (!strip_zeros) return MTL_ERR_INVALID_ARG;
+  if (!aligned16(strip_zeros)) return MTL_ERR_ALIGN;
+  return prefill_gemm(x, M, ldx, K, strip_weight, strip_scales, strip_zeros, N, group_size,
+                      zero_offset, epilogue, out_dtype, y, ldy, workspace, ws_bytes,
+                      STRIP_META_GPTQ, (hipStream_t)stream);
+}
+
+int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,
+                            const int32_t* strip_weight, const void* qsz, int64_t N,
+                            int32_t group_size, int32_t epilogue, int32_t out_dtype, void* y,
+                            int64_t ldy, float* workspace, int64_t ws_bytes, void* stream) {
+  return prefill_gemm(x, M, ldx, K, strip_weight, qsz, nullptr, N, group_size, 0, epilogue,
+                      out_dtype, y, ldy, workspace, ws_bytes, STRIP_META_QSZ,
+                      (hipStream_t)stream);
+}
+
+int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+  return M > 1 ? mtl_w4_gemm_prefill_workspace_bytes(M, K, N) : 0;
+}
+
+// The drop-in for torch._weight_int4pack_mm: M = 1 on the full-K strip GEMV, more rows on
+// the prompt-length GEMM (or, when N is not a multiple of 128, one strip GEMV per row).
+int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
+                    int32_t group_size, const void* qsz, int64_t N, void* y, void* workspace,
+                    int64_t ws_bytes, void* stream) {
+  if (!x || !packed || !qsz || !y) return MTL_ERR_INVALID_ARG;
   if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
     return MTL_ERR_GROUP;
-  const int64_t ncols = epilogue == MTL_EPI_SILU_MUL ? N / 2 : N;
-  if (M < 1 || M > (int64_t)kPfRows * 65535 || K <= 0 || N <= 0 || K % 256 != 0 ||
-      K > 65536 || N % kPfCols != 0 || K % group_size != 0 || ldx < K || ldy < ncols ||
-      (N / 16) * (K / 128) * 1024 >= ((int64_t)1 << 31) || M * ldx * 2 >= ((int64_t)1 << 31) ||
-      (K / group_size) * N * 2 >= ((int64_t)1 << 31))
+  if (M < 1 || K <= 0 || N <= 0 || K % 256 != 0 || N % 16 != 0 || K % group_size != 0 ||
+      (N / 16) * (K / 128) * 1024 >= ((int64_t)1 << 31) || M * K >= ((int64_t)1 << 31) ||
+      (K / group_size) * N * 4 >= ((int64_t)1 << 31))
     return MTL_ERR_SHAPE;
-  if (!aligned16(x) || ldx % 8 != 0 || !aligned16(strip_weight) || !aligned16(strip_scales) ||
-      !aligned16(strip_zeros) || (workspace && !aligned16(workspace)) ||
-      (reinterpret_cast<uintptr_t>(y) & (out_dtype == MTL_OUT_F32 ? 3u : 1u)))
+  if (!aligned16(x) || !aligned16(packed) || (reinterpret_cast<uintptr_t>(qsz) & 3u) ||
+      (reinterpret_cast<uintptr_t>(y) & 7u))
     return MTL_ERR_ALIGN;
-  PrefillArgs a;
-  a.x = static_cast<const uint16_t*>(x);
-  a.w = reinterpret_cast<const u32x4*>(strip_weight);
-  a.scales = static_cast<const uint16_t*>(strip_scales);
-  a.qzeros = reinterpret_cast<const uint32_t*>(strip_zeros);
-  a.y = y;
-  a.ldx = ldx;
-  a.ldy = ldy;
-  a.M = (int)M; a.K = (int)K; a.N = (int)N;
-  a.group = group_size;
-  a.zero_offset = zero_offset;
-  a.kblocks = (int)(K / 128);
-  a.out_f32 = out_dtype == MTL_OUT_F32;
-  // K splits when the workspace holds their partial sums, else one pass
-  const int64_t need = mtl_w4_gemm_prefill_workspace_bytes(M, K, N);
-  a.splits = need > 0 && workspace && ws_bytes >= need ? (int)(need / (M * N * 4)) : 1;
-  a.kps = a.kblocks / a.splits;
-  a.part = workspace;
   hipStream_t st = (hipStream_t)stream;
-  switch (group_size) {
-    case 32: prefill_epi<1>(a, epilogue, st); break;
-    case 64: prefill_epi<2>(a, epilogue, st); break;
-    case 128: prefill_epi<4>(a, epilogue, st); break;
-    default: prefill_epi<8>(a, epilogue, st); break;
+  const bool strip_ok = K <= 16384 && strip_blocks_per_wave(K, 1, group_size) > 0;
+  StripArgs sa = {};
+  sa.w = reinterpret_cast<const u32x4*>(packed);
+  sa.scales = static_cast<const uint16_t*>(qsz);
+  sa.K = (int)K;
+  sa.N = (int)N;
+  sa.group = group_size;
+  sa.fmt = STRIP_META_QSZ;
+  if (M == 1 && strip_ok) {
+    sa.x = static_cast<const uint16_t*>(x);
+    sa.y16 = static_cast<uint16_t*>(y);
+    return strip_launch(sa, st);
   }
-  return launch_status();
+  if (N % kPfCols == 0)
+    return prefill_gemm(x, M, K, K, packed, qsz, nullptr, N, group_size, 0, MTL_EPI_NONE,
+                        MTL_OUT_BF16, y, N, static_cast<float*>(workspace), ws_bytes,
+                        STRIP_META_QSZ, st);
+  if (!strip_ok) return MTL_ERR_UNSUPPORTED;
+  for (int64_t r = 0; r < M; ++r) {
+    sa.x = static_cast<const uint16_t*>(x) + r * K;
+    sa.y16 = static_cast<uint16_t*>(y) + r * N;
+    if (const int status = strip_launch(sa, st)) return status;
+  }
+  return MTL_OK;
 }
 
 }  // extern "C"

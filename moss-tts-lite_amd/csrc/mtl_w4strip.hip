@@ -43,7 +43,7 @@ static int g_strip_ct = 0;            // tuning override of strips per workgroup
 static int g_strip_xcd = 1;           // 1: XCD-contiguous strip order (see the kernel)
 static int g_strip_full = -1;         // tuning override: 1 all blocks in flight, 0 ring, -1 auto
 
-template <int GR, int XSRC, int EPI, int NB, int CT, int WIN>
+template <int GR, int XSRC, int EPI, int NB, int CT, int WIN, int FMT>
 __global__ void __launch_bounds__(64 * strip_max_waves(GR, NB, WIN), 1)
 w4_strip_kernel(StripArgs a) {
   constexpr int ITEMS = 16 * NB;               // x items (8 channels) per K slice
@@ -144,19 +144,32 @@ w4_strip_kernel(StripArgs a) {
   // contiguously (fp16) and their zero nibbles, so a lane loads its column's metadata
   // of a block with one scale load and one zero load (a uniform record offset and one
   // per-lane offset).
+  // The reference's qsz (STRIP_META_QSZ) instead: one (scale, zero) pair per group and
+  // column, read in place at (group * N + column) * 4.
   const int ngroups = a.K / a.group;
   const int krec = GR == 8 ? a.kblocks >> 1 : a.kblocks;     // records per strip
   const int rec0 = s * krec + (GR == 8 ? (ks * NB) >> 1 : ks * NB);
   const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.scales), (short)0, ngroups * N * 2, 0x00020000);
+      const_cast<uint16_t*>(a.scales), (short)0,
+      FMT == STRIP_META_QSZ ? ngroups * N * 4 : ngroups * N * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(a.qzeros), (short)0, ngroups * (N >> 1), 0x00020000);
+      const_cast<uint32_t*>(a.qzeros), (short)0,
+      FMT == STRIP_META_QSZ ? 0 : ngroups * (N >> 1), 0x00020000);
   u32x4 wq[WIN];
-  StripMeta<MB> mt[WIN];
+  StripMeta<MB> mt[FMT == STRIP_META_GPTQ ? WIN : 1];
+  uint32_t mq[FMT == STRIP_META_QSZ ? WIN : 1][MB];
+  const int kbs = ks * NB;                     // the slice's first block within K
   // block b into ring slot r (r = b % WIN, a compile-time index at every call)
   auto issue = [&](int r, int b) {
-    if (GR <= 4 || (r & 1) == 0)               // g = 256: one record per block pair (b, r alike in parity)
-      strip_meta_load<MB>(srsrc, zrsrc, lj, rec0 + (GR == 8 ? b >> 1 : b), mt[r]);
+    if (GR <= 4 || (r & 1) == 0) {             // g = 256: one record per block pair (b, r alike in parity)
+      if constexpr (FMT == STRIP_META_GPTQ) {
+        strip_meta_load<MB>(srsrc, zrsrc, lj, rec0 + (GR == 8 ? b >> 1 : b), mt[r]);
+      } else {
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+          mq[r][m] = qsz_load(srsrc, col, GR == 8 ? (kbs + b) >> 1 : (kbs + b) * MB + m, N);
+      }
+    }
     wq[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                           wrsrc, lane * 16, (blk0 + b) * 1024, kStripAux));
   };
@@ -213,7 +226,7 @@ w4_strip_kernel(StripArgs a) {
   const uint32_t kMagic = vgpr_const(0x43004300u);   // bf16 (128, 128)
   const uint32_t kLo = vgpr_const(0x000F000Fu);
   float tot = 0.f;
-  float cur_s = 0.f, cur_z = 0.f;               // g = 256: the group of this block pair
+  float cur_s = 0.f, cur_z = 0.f, cur_d = 0.f;  // g = 256: the group of this block pair
   floatx4 acc;
   // Ring turns with the WIN ring slots unrolled inside, so ring indexes stay compile-time.
   // The turns are unrolled too (measured faster than a loop, whose ring registers need
@@ -230,9 +243,18 @@ w4_strip_kernel(StripArgs a) {
     for (int r = 0; r < WIN; ++r) {
       const int b = b0 + r;
       const u32x4 w4 = wq[r];
-      float gs[MB], gz[MB];                     // scale and 128 + zero of the block's groups
-      strip_meta_decode<MB>(mt[r], lj, a.zero_offset, gs, gz);
-      if (GR == 8 && (r & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; }
+      float gs[MB], gz[MB], gd[MB];             // (s, c, d) of the block's groups (qsz_decode)
+      if (GR <= 4 || (r & 1) == 0) {
+        if constexpr (FMT == STRIP_META_GPTQ) {
+          strip_meta_decode<MB>(mt[r], lj, a.zero_offset, gs, gz);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) gd[m] = 0.f;
+        } else {
+#pragma unroll
+          for (int m = 0; m < MB; ++m) qsz_decode(mq[r][m], gs[m], gz[m], gd[m]);
+        }
+      }
+      if (GR == 8 && (r & 1) == 0) { cur_s = gs[0]; cur_z = gz[0]; cur_d = gd[0]; }
       // keep the compiler from hoisting later ring loads (and their registers) above here:
       // an empty asm with a memory clobber orders the loads at the IR level, the
       // scheduling barrier in the machine scheduler
@@ -251,7 +273,9 @@ w4_strip_kernel(StripArgs a) {
           const float Asum = acc[0];
           const float sc = GR == 8 ? cur_s : gs[j / GR];
           const float cz = GR == 8 ? cur_z : gz[j / GR];
-          tot = fmaf(sc, fmaf(-cz, xg[ks][rq / GR], Asum), tot);
+          const float X = xg[ks][rq / GR];
+          tot = fmaf(sc, fmaf(-cz, X, Asum), tot);
+          if constexpr (FMT == STRIP_META_QSZ) tot = fmaf(GR == 8 ? cur_d : gd[j / GR], X, tot);
         }
       }
     }
@@ -276,7 +300,14 @@ w4_strip_kernel(StripArgs a) {
   const int c0 = s0 * kStripCols + 4 * q4;
   const bool owner = lane < 4 * CT;
   if (EPI == STRIP_EPI_STORE) {
-    if (owner) *reinterpret_cast<float4*>(a.y + c0) = make_float4(y[0], y[1], y[2], y[3]);
+    if (owner) {
+      if (a.y16)
+        *reinterpret_cast<u32x2*>(a.y16 + c0) =
+            u32x2{f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16),
+                  f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
+      else
+        *reinterpret_cast<float4*>(a.y + c0) = make_float4(y[0], y[1], y[2], y[3]);
+    }
     return;
   }
   if (EPI == STRIP_EPI_SILU) {
@@ -364,59 +395,72 @@ static StripGeom strip_geometry(const StripArgs& a) {
   return g;
 }
 
-template <int GR, int XSRC, int EPI, int CT>
+template <int GR, int XSRC, int EPI, int CT, int FMT>
 static void strip_nb(const StripArgs& a, const StripGeom& g, hipStream_t st) {
   const dim3 grid(a.N / (kStripCols * CT));
   const dim3 block(64 * CT * (a.kblocks / g.nb));
   const size_t lds = (size_t)(a.kblocks / g.nb) * 16 * g.nb * sizeof(u32x4);
+  // the deep ring is a tuning geometry of the GPTQ metadata only
+  const bool full = FMT == STRIP_META_GPTQ && g.full;
 #define MTL_STRIP_LAUNCH(NB_, WIN_) \
-  hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, NB_, CT, WIN_>), grid, block, lds, st, a)
+  hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, NB_, CT, WIN_, FMT>), grid, block, lds, st, a)
   switch (g.nb) {
     case 2: MTL_STRIP_LAUNCH(2, 2); break;
     case 4: MTL_STRIP_LAUNCH(4, 4); break;
     case 6: MTL_STRIP_LAUNCH(6, strip_ring(GR, 6)); break;
     case 8:
-      if (g.full) MTL_STRIP_LAUNCH(8, strip_deep_ring(GR, 8)); else MTL_STRIP_LAUNCH(8, 4);
+      if (full) MTL_STRIP_LAUNCH(8, strip_deep_ring(GR, 8)); else MTL_STRIP_LAUNCH(8, 4);
       break;
     default:
-      if (g.full) MTL_STRIP_LAUNCH(16, strip_deep_ring(GR, 16)); else MTL_STRIP_LAUNCH(16, 4);
+      if (full) MTL_STRIP_LAUNCH(16, strip_deep_ring(GR, 16)); else MTL_STRIP_LAUNCH(16, 4);
       break;
   }
 #undef MTL_STRIP_LAUNCH
 }
 
-template <int GR>
+template <int GR, int FMT>
 static void strip_variant(const StripArgs& a, const StripGeom& g, hipStream_t st) {
   if (a.act) {
-    if (g.ct == 6) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 6>(a, g, st);
-    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 2>(a, g, st);
+    if (FMT == STRIP_META_GPTQ && g.ct == 6) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 6, FMT>(a, g, st);
+    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_SILU, 2, FMT>(a, g, st);
   } else if (a.h) {
-    if (a.xpart) strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_RESID, 1>(a, g, st);
-    else strip_nb<GR, XSRC_BF16, STRIP_EPI_RESID, 1>(a, g, st);
+    if (a.xpart) strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_RESID, 1, FMT>(a, g, st);
+    else strip_nb<GR, XSRC_BF16, STRIP_EPI_RESID, 1, FMT>(a, g, st);
   } else if (a.hn) {
-    if (g.ct == 4) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 4>(a, g, st);
-    else if (g.ct == 2) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 2>(a, g, st);
-    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1>(a, g, st);
+    if (FMT == STRIP_META_GPTQ && g.ct == 4) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 4, FMT>(a, g, st);
+    else if (FMT == STRIP_META_GPTQ && g.ct == 2) strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 2, FMT>(a, g, st);
+    else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1, FMT>(a, g, st);
   } else if (a.xpart) {
-    strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1>(a, g, st);
+    strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1, FMT>(a, g, st);
   } else {
-    strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1>(a, g, st);
+    strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1, FMT>(a, g, st);
+  }
+}
+
+template <int FMT>
+static void strip_group(const StripArgs& a, const StripGeom& g, hipStream_t st) {
+  switch (a.group) {
+    case 32: strip_variant<1, FMT>(a, g, st); break;
+    case 64: strip_variant<2, FMT>(a, g, st); break;
+    case 128: strip_variant<4, FMT>(a, g, st); break;
+    default: strip_variant<8, FMT>(a, g, st); break;
   }
 }
 
 // Shapes, pointers and alignment are checked by the entry points.
 int strip_launch(const StripArgs& args, hipStream_t st) {
   StripArgs a = args;
-  const StripGeom g = strip_geometry(a);
+  StripGeom g = strip_geometry(a);
+  if (a.fmt == STRIP_META_QSZ) {         // the reference's metadata: automatic geometry only
+    g.ct = a.act ? 2 : 1;
+    g.full = 0;
+    g.nb = blocks_per_wave(a.K, g.ct, 0, a.group);
+  }
   if (!g.nb || a.N % (kStripCols * g.ct) != 0) return MTL_ERR_SHAPE;
   a.kblocks = a.K / kStripBlockK;
   a.xcd_order = g_strip_xcd && (a.N / (kStripCols * g.ct)) % 8 == 0;
-  switch (a.group) {
-    case 32: strip_variant<1>(a, g, st); break;
-    case 64: strip_variant<2>(a, g, st); break;
-    case 128: strip_variant<4>(a, g, st); break;
-    default: strip_variant<8>(a, g, st); break;
-  }
+  if (a.fmt == STRIP_META_QSZ) strip_group<STRIP_META_QSZ>(a, g, st);
+  else strip_group<STRIP_META_GPTQ>(a, g, st);
   return launch_status();
 }
 

@@ -146,35 +146,67 @@ def gptq_gemm(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor, scal
     return y.reshape(*x.shape[:-1], n)
 
 
+def _int4pack_shape(n: int, k: int, inner_k_tiles: int) -> tuple:
+    """torch's shape of a packed int4 weight, ``[N/8, K/(16 T), 32, T/2]``."""
+    return (n // 8, k // (16 * inner_k_tiles), 32, inner_k_tiles // 2)
+
+
+_pack_ws_cache: dict = {}
+
+
 def weight_int4pack_mm(x: torch.Tensor, packed: torch.Tensor, q_group_size: int,
                        q_scale_and_zeros: torch.Tensor) -> torch.Tensor:
     """Drop-in for ``torch._weight_int4pack_mm(x, packed, qGroupSize, qScaleAndZeros)``.
 
-    ``x`` bf16 ``[M, K]``; ``packed`` from :func:`convert_weight_to_int4pack`;
+    ``x`` bf16 ``[M, K]`` (any M); ``packed`` from :func:`convert_weight_to_int4pack` or
+    :func:`int4pack_from_torch_tiles` (torch's 4-D shape, this build's strip layout inside:
+    a concatenation along dim 0 is a concatenation along N, as with torch's tiles);
     ``qScaleAndZeros`` bf16 ``[K/g, N, 2]`` = (scale, zero) with
     ``w = (q - 8) * scale + zero`` (moss_tts_lite/gptq.py:87-97).  Returns bf16 ``[M, N]``.
+    M = 1 runs the full-K strip GEMV, more rows the prompt-length GEMM.
     """
     if x.dim() != 2:
         raise RuntimeError(f"x must be 2-D [M, K], got {tuple(x.shape)}")
-    k = packed.shape[0] * 8
-    n = packed.shape[1]
-    _check_group(q_group_size, k)
-    x2 = _check_x(x, k)
     qsz = q_scale_and_zeros
-    if qsz.dtype != torch.bfloat16 or tuple(qsz.shape) != (k // q_group_size, n, 2):
-        raise RuntimeError(f"qScaleAndZeros must be bfloat16 [{k // q_group_size}, {n}, 2]")
-    if packed.dtype != torch.int32:
-        raise RuntimeError("packed weight must be int32")
-    return w4_gemm(x2, packed.contiguous(), N.META_QSZ, qsz.contiguous(), None, None, n,
-                   q_group_size)
+    if qsz.dtype != torch.bfloat16 or qsz.dim() != 3 or qsz.shape[2] != 2:
+        raise RuntimeError("qScaleAndZeros must be bfloat16 [K/g, N, 2]")
+    _check_group(q_group_size, qsz.shape[0] * q_group_size)
+    k, n = qsz.shape[0] * q_group_size, qsz.shape[1]
+    if packed.dtype != torch.int32 or packed.dim() != 4 or packed.shape[0] * 8 != n or \
+            packed.numel() * 8 != n * k:
+        raise RuntimeError(f"packed weight must be int32 [N/8, K/(16*T), 32, T/2] for "
+                           f"N={n}, K={k}")
+    x2 = _check_x(x, k)
+    m = x2.shape[0]
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=x2.device)
+    lib = N.load()
+    ws, nbytes = None, int(lib.mtl_int4pack_mm_workspace_bytes(m, k, n))
+    if nbytes > 0:
+        key = _dev_index(x2.device)
+        ws = _pack_ws_cache.get(key)
+        if ws is None or ws.numel() * 4 < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                ws = None                  # no growth under capture: one pass instead
+            else:
+                ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=x2.device)
+                _pack_ws_cache[key] = ws
+    N.check(lib.mtl_int4pack_mm(x2.data_ptr(), m, k, packed.data_ptr(), q_group_size,
+                                qsz.contiguous().data_ptr(), n, y.data_ptr(),
+                                None if ws is None else ws.data_ptr(),
+                                0 if ws is None else ws.numel() * 4, _stream(x2.device)),
+            "mtl_int4pack_mm")
+    return y
 
 
 def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) -> torch.Tensor:
     """Drop-in for ``aten._convert_weight_to_int4pack(uint8[N, K/2], innerKTiles)``.
 
     Input is the reference's nibble pre-pack (even k in the high nibble,
-    moss_tts_lite/fast.py:98).  Output is this build's int32 ``[K/8, N]`` layout,
-    not torch's tiled bytes.
+    moss_tts_lite/fast.py:98).  Output has torch's shape ``[N/8, K/(16 T), 32, T/2]`` int32
+    and holds this build's strip layout, not torch's tiled bytes: 16-column strips over all
+    of K, each one contiguous, so ``torch.cat(..., dim=0)`` of two packed weights is the
+    packed concatenation of the weights along N (moss_tts_lite/fast_native.py:158-159).
+    K % 256 == 0 and N % 16 == 0.
     """
     if prepacked.dtype != torch.uint8 or prepacked.dim() != 2:
         raise RuntimeError("expected a uint8 [N, K/2] tensor")
@@ -182,17 +214,18 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
         raise RuntimeError("innerKTiles must be 2, 4 or 8")
     n, kh = prepacked.shape
     k = kh * 2
-    if k % 8 or n % 8:
-        raise RuntimeError(f"K={k} must be a multiple of 8 and N={n} a multiple of 8")
+    if k % 256 or n % 16:
+        raise RuntimeError(f"K={k} must be a multiple of 256 and N={n} a multiple of 16")
     src = prepacked.contiguous()
-    out = torch.empty(k // 8, n, dtype=torch.int32, device=src.device)
+    out = torch.empty(_int4pack_shape(n, k, inner_k_tiles), dtype=torch.int32, device=src.device)
     N.check(N.load().mtl_int4pack_convert(src.data_ptr(), n, k, inner_k_tiles, out.data_ptr(),
                                           _stream(src.device)), "mtl_int4pack_convert")
     return out
 
 
 def int4pack_from_torch_tiles(tiles: torch.Tensor) -> torch.Tensor:
-    """torch's tiled int4 tensor -> this build's int32 ``[K/8, N]`` (mtl_int4pack_from_torch_tiles).
+    """torch's tiled int4 tensor -> this build's packed weight (mtl_int4pack_from_torch_tiles),
+    in the same ``[N/8, K/(16T), 32, T/2]`` shape.
 
     ``tiles`` is int32 ``[N/8, K/(16T), 32, T/2]`` as ``aten._convert_weight_to_int4pack(pre,
     T)`` returns it on a ROCm GPU: the ``.q`` records of the reference's standalone export
@@ -209,7 +242,7 @@ def int4pack_from_torch_tiles(tiles: torch.Tensor) -> torch.Tensor:
     if tiles.device.type != "cuda":
         raise RuntimeError("int4 tiles must be on the GPU")
     src = tiles.contiguous()
-    out = torch.empty(k // 8, n, dtype=torch.int32, device=src.device)
+    out = torch.empty_like(src)
     N.check(N.load().mtl_int4pack_from_torch_tiles(src.data_ptr(), n, k, t, out.data_ptr(),
                                                    _stream(src.device)),
             "mtl_int4pack_from_torch_tiles")
@@ -324,6 +357,37 @@ def prefill_gemm(x: torch.Tensor, strip_weight: torch.Tensor, strip_scales: torc
     return out
 
 
+def prefill_gemm_qsz(x: torch.Tensor, packed: torch.Tensor, qsz: torch.Tensor, group_size: int,
+                     epilogue: str = "none", out: torch.Tensor | None = None,
+                     out_dtype: torch.dtype = torch.bfloat16, split: bool = True) -> torch.Tensor:
+    """:func:`prefill_gemm` on the reference's own contract (``mtl_w4_gemm_prefill_qsz``):
+    ``packed`` from :func:`convert_weight_to_int4pack` / :func:`int4pack_from_torch_tiles`,
+    ``qsz`` bf16 ``[K/g, N, 2]`` read in place (``w = (q - 8) * scale + zero``)."""
+    if epilogue not in _PREFILL_EPI:
+        raise ValueError(f"epilogue must be one of {tuple(_PREFILL_EPI)}")
+    if qsz.dtype != torch.bfloat16 or qsz.dim() != 3 or qsz.shape[2] != 2:
+        raise RuntimeError("qsz must be bfloat16 [K/g, N, 2]")
+    k, n = qsz.shape[0] * group_size, qsz.shape[1]
+    x2 = _check_x(x, k)
+    m = x2.shape[0]
+    cols = n // 2 if epilogue == "silu_mul" else n
+    if out is None:
+        if epilogue == "residual":
+            raise RuntimeError("the residual epilogue updates `out` in place")
+        out = torch.empty(m, cols, dtype=out_dtype if epilogue == "none" else torch.bfloat16,
+                          device=x2.device)
+    if out.dim() != 2 or out.shape[0] != m or out.shape[1] < cols or out.stride(1) != 1:
+        raise RuntimeError(f"out must be [{m}, >= {cols}] with unit column stride")
+    odt = N.OUT_F32 if out.dtype == torch.float32 else N.OUT_BF16
+    ws = prefill_workspace(x2.device, m, k, n) if split else None
+    N.check(N.load().mtl_w4_gemm_prefill_qsz(
+        x2.data_ptr(), m, x2.stride(0), k, packed.data_ptr(), qsz.contiguous().data_ptr(), n,
+        group_size, _PREFILL_EPI[epilogue], odt, out.data_ptr(), out.stride(0),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel() * 4,
+        _stream(x2.device)), "mtl_w4_gemm_prefill_qsz")
+    return out
+
+
 def unpack_codes(qweight: torch.Tensor) -> torch.Tensor:
     """``qweight [K/8, N]`` -> codes uint8 ``[K, N]``."""
     k = qweight.shape[0] * 8
@@ -346,9 +410,9 @@ def gptq_dequant(qweight, qzeros, scales, group_size: int, zero_offset: int = 0)
 
 
 def qsz_dequant(packed, qsz, group_size: int) -> torch.Tensor:
-    """Exact fp32 ``W[K, N]`` of the reference contract (``effective_weight(q, qsz).T``)."""
-    k = packed.shape[0] * 8
-    n = packed.shape[1]
+    """Exact fp32 ``W[K, N]`` of the reference contract (``effective_weight(q, qsz).T``)
+    from a packed weight of :func:`convert_weight_to_int4pack`."""
+    k, n = qsz.shape[0] * group_size, qsz.shape[1]
     out = torch.empty(k, n, dtype=torch.float32, device=packed.device)
     N.check(N.load().mtl_qsz_dequant(packed.contiguous().data_ptr(), qsz.contiguous().data_ptr(),
                                      k, n, group_size, out.data_ptr(), _stream(packed.device)),

@@ -261,13 +261,32 @@ def qweight_from_reference_codes(q_nk: np.ndarray) -> np.ndarray:
     return pack_qweight(np.ascontiguousarray(np.asarray(q_nk, np.uint8).T))
 
 
-def int4pack_from_prepacked(p_u8: np.ndarray) -> np.ndarray:
-    """The reference's pre-packed ``uint8 [N, K/2]`` (even k high) -> ``qweight [K/8, N]``.
+def strip_layout(qweight: np.ndarray) -> np.ndarray:
+    """``qweight [K/8, N]`` words in the build's strip order, flat uint32 ``[N*K/8]``.
 
-    This is what the build's replacement of ``_convert_weight_to_int4pack``
-    (called at moss_tts_lite/fast.py:97, gptq.py:75) produces.
+    16-byte word l of 1 KB block ``(s * K/128 + b)`` holds, as its 32-bit words j = 0..3,
+    the qweight words (row ``16b + 4j + l/16``, column ``16s + l%16``): column strips of 16
+    over all of K, one strip a contiguous run.  K % 128 == 0, N % 16 == 0.  Pinned by a
+    per-word brute force (tests/test_oracle_gptq.py).
     """
-    return qweight_from_reference_codes(unprepack_u8(p_u8))
+    rows, n = qweight.shape
+    w = np.ascontiguousarray(qweight).view(np.uint32).reshape(rows // 16, 4, 4, n // 16, 16)
+    return np.ascontiguousarray(w.transpose(3, 0, 2, 4, 1)).reshape(-1)   # s, b, l/16, l%16, j
+
+
+def strip_layout_inverse(words: np.ndarray, k: int, n: int) -> np.ndarray:
+    """Inverse of :func:`strip_layout`: ``qweight [K/8, N]`` (uint32 -> int32)."""
+    w = np.ascontiguousarray(words).view(np.uint32).reshape(n // 16, k // 128, 4, 16, 4)
+    return np.ascontiguousarray(w.transpose(1, 4, 2, 0, 3)).reshape(k // 8, n).view(np.int32)
+
+
+def int4pack_from_prepacked(p_u8: np.ndarray) -> np.ndarray:
+    """The reference's pre-packed ``uint8 [N, K/2]`` (even k high) -> the packed words the
+    build's replacement of ``_convert_weight_to_int4pack`` (called at
+    moss_tts_lite/fast.py:97, gptq.py:75) produces: the strip layout of the codes' qweight,
+    flat uint32 ``[N*K/8]``.
+    """
+    return strip_layout(qweight_from_reference_codes(unprepack_u8(p_u8)))
 
 
 def torch_tile_locate(n, k, K: int, inner_k_tiles: int):

@@ -122,7 +122,7 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4104,
                                     128, 0, 1, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
     assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
-                                    128, 0, 3, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
+                                    128, 0, 4, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_w4_tiled_bytes(4096, 24576) == 8 * 384 * 16 * 1024
     assert lib.mtl_w4_tiled_bytes(4096, 24600) == 0
     # the strip layout needs N % 16 == 0, K % 256 == 0 (K <= 16384), M = 1, no gather index
@@ -134,6 +134,16 @@ def test_decode_entry_validation(lib):
     assert part(1, 32768, 4096) == N.MTL_ERR_SHAPE
     assert part(2, 4096, 4096) == N.MTL_ERR_SHAPE
     assert part(1, 4096, 4096, FAKE) == N.MTL_ERR_SHAPE
+    # the same shapes with the reference's qsz (layout STRIP_QSZ, qzeros unused)
+    qpart = lambda m, k, n: lib.mtl_w4_gemm_partials(  # noqa: E731
+        FAKE, None, 0, 0, m, k, FAKE, FAKE, None, None, n, 128, 0, N.LAYOUT_STRIP_QSZ, FAKE,
+        1 << 30, None)
+    assert qpart(1, 4096, 4104) == N.MTL_ERR_SHAPE
+    assert qpart(1, 4224, 4096) == N.MTL_ERR_SHAPE
+    assert qpart(2, 4096, 4096) == N.MTL_ERR_SHAPE
+    # GPTQ strip metadata still needs its zeros
+    assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, None, None, 4096, 128,
+                                    0, strip, FAKE, 1 << 30, None) == N.MTL_ERR_INVALID_ARG
     assert lib.mtl_w4_gemm_partials(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096, 128,
                                     0, strip, FAKE, 4096 * 4 - 4, None) == N.MTL_ERR_WORKSPACE
     assert lib.mtl_w4_strip_bytes(4096, 24576) == 4096 * 24576 // 2
@@ -211,7 +221,17 @@ def test_prefill_row_entry_validation(lib):
 
 def test_converter_validation(lib):
     assert lib.mtl_int4pack_convert(FAKE, 64, 64, 3, FAKE, None) == N.MTL_ERR_INVALID_ARG
-    assert lib.mtl_int4pack_convert(FAKE, 60, 64, 8, FAKE, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_int4pack_convert(FAKE, 56, 512, 8, FAKE, None) == N.MTL_ERR_SHAPE   # N % 16
+    assert lib.mtl_int4pack_convert(FAKE, 64, 384, 8, FAKE, None) == N.MTL_ERR_SHAPE   # K % 256
+    mm = lib.mtl_int4pack_mm
+    assert mm(None, 1, 512, FAKE, 128, FAKE, 64, FAKE, None, 0, None) == N.MTL_ERR_INVALID_ARG
+    assert mm(FAKE, 1, 512, FAKE, 16, FAKE, 64, FAKE, None, 0, None) == N.MTL_ERR_GROUP
+    assert mm(FAKE, 1, 384, FAKE, 128, FAKE, 64, FAKE, None, 0, None) == N.MTL_ERR_SHAPE
+    assert mm(FAKE, 1, 512, FAKE, 128, FAKE, 56, FAKE, None, 0, None) == N.MTL_ERR_SHAPE
+    assert mm(FAKE, 0, 512, FAKE, 128, FAKE, 64, FAKE, None, 0, None) == N.MTL_ERR_SHAPE
+    assert mm(FAKE, 1, 512, FAKE, 128, FAKE, 64, ctypes.c_void_p(0x1004), None, 0,
+              None) == N.MTL_ERR_ALIGN
+    assert lib.mtl_int4pack_mm_workspace_bytes(1, 4096, 4096) == 0
     tt = lib.mtl_int4pack_from_torch_tiles
     assert tt(None, 64, 512, 8, FAKE, None) == N.MTL_ERR_INVALID_ARG
     assert tt(FAKE, 64, 512, 6, FAKE, None) == N.MTL_ERR_INVALID_ARG

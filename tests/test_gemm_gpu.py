@@ -75,7 +75,7 @@ def test_gptq_dequant_bit_exact(dev, group, zero_offset):
 @pytest.mark.parametrize("group", [32, 128])
 def test_qsz_dequant_bit_exact(dev, group):
     case = synth.qsz_case(k=512, n=96, group=group, seed=group)
-    packed = t_i32(G.qweight_from_reference_codes(case["q"]), dev)
+    packed = t_i32(G.int4pack_from_prepacked(G.prepack_u8(case["q"])).view(np.int32), dev)
     got = ops.qsz_dequant(packed, t_bf16(case["qsz"], dev), group).cpu().numpy()
     ref = G.effective_weight(case["q"], case["qsz"], group).T
     assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(ref).view(np.uint32))
@@ -83,11 +83,20 @@ def test_qsz_dequant_bit_exact(dev, group):
 
 def test_int4pack_convert_bit_exact(dev):
     r = np.random.default_rng(2)
-    q = r.integers(0, 16, size=(200, 384)).astype(np.uint8)      # [N, K]
+    q = r.integers(0, 16, size=(208, 512)).astype(np.uint8)      # [N, K]
     pre = G.prepack_u8(q)
-    got = ops.convert_weight_to_int4pack(torch.from_numpy(pre).to(dev), 8).cpu().numpy()
-    assert np.array_equal(got, G.int4pack_from_prepacked(pre))
-    assert np.array_equal(G.unpack_qweight(got), q.T)
+    got = ops.convert_weight_to_int4pack(torch.from_numpy(pre).to(dev), 8)
+    assert tuple(got.shape) == (208 // 8, 512 // 128, 32, 4) and got.dtype == torch.int32
+    words = got.cpu().numpy().reshape(-1).view(np.uint32)
+    assert np.array_equal(words, G.int4pack_from_prepacked(pre))
+    assert np.array_equal(G.unpack_qweight(G.strip_layout_inverse(words, 512, 208)), q.T)
+    # torch's shape for other inner_k_tiles, the same words inside
+    for t in (2, 4):
+        other = ops.convert_weight_to_int4pack(torch.from_numpy(pre).to(dev), t)
+        assert tuple(other.shape) == (26, 512 // (16 * t), 32, t // 2)
+        assert torch.equal(other.reshape(-1), got.reshape(-1))
+    with pytest.raises(RuntimeError):
+        ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q[:200])).to(dev), 8)
 
 
 def test_actorder_prepare_bit_exact(dev):
@@ -265,6 +274,114 @@ def test_int4pack_mm_matches_effective_weight(dev, n, k, m):
     assert err < 5e-3
 
 
+def _qsz_weights(r, n, k, g):
+    """Reference-contract operands: codes [N, K], qsz bits [K/g, N, 2] (scale, zero)."""
+    q = r.integers(0, 16, (n, k), dtype=np.uint8)
+    qsz = f32_to_bf16_bits(np.stack([r.uniform(0.002, 0.02, (k // g, n)),
+                                     r.uniform(-0.1, 0.1, (k // g, n))], -1).astype(np.float32))
+    return q, qsz
+
+
+@pytest.mark.parametrize("m,k,n,g", [(1, 4096, 24576, 128), (1, 12288, 4096, 32),
+                                     (1, 4096, 6144, 64), (1, 2048, 1024, 256),
+                                     (1, 16384, 512, 128), (5, 4096, 4096, 128),
+                                     (64, 2048, 1024, 32), (3, 1024, 208, 128),
+                                     (300, 1024, 256, 256)])
+def test_int4pack_mm_paths_match_oracle(dev, m, k, n, g):
+    # the drop-in's three paths on the reference's own metadata (qsz read in place): M = 1
+    # strip GEMV, M > 1 prompt-length GEMM, and per-row strip GEMVs when N % 128 != 0;
+    # against the float64 closed form x @ effective_weight(q, qsz).T on sampled columns
+    print("int4pack_mm path", m, k, n, g, flush=True)
+    r = np.random.default_rng(m * 7 + k + n + g)
+    q, qsz = _qsz_weights(r, n, k, g)
+    xb = f32_to_bf16_bits(r.standard_normal((m, k)).astype(np.float32))
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+    y = ops.weight_int4pack_mm(t_bf16(xb, dev), packed, g, t_bf16(qsz, dev))
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (m, n)
+    cols = np.sort(r.choice(n, min(n, 1024), replace=False))
+    ref = G.int4pack_mm(bf16_bits_to_f32(xb), q[cols], np.ascontiguousarray(qsz[:, cols]), g)
+    err = rel_l2(y.float().cpu().numpy()[:, cols], ref)
+    print(f"  rel_l2={err:.2e}")
+    assert err < TOL_BF16
+
+
+def test_int4pack_dim0_concat_is_concat_along_n(dev):
+    # moss_tts_lite/fast_native.py:146-161 fuses linears with torch.cat(packed, dim=0) and
+    # torch.cat(qsz, dim=1): the concatenated packed words are the packing of the
+    # concatenated weights, and the M = 1 GEMM on them is the separate GEMMs side by side
+    r = np.random.default_rng(77)
+    k, g = 4096, 128
+    parts = [_qsz_weights(r, n, k, g) for n in (4096, 1024)]
+    packed = [ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+              for q, _ in parts]
+    fused_q = np.concatenate([q for q, _ in parts], 0)
+    fused = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(fused_q)).to(dev), 8)
+    cat = torch.cat(packed, dim=0)
+    assert torch.equal(cat, fused)
+    qszs = [t_bf16(z, dev) for _, z in parts]
+    x = t_bf16(f32_to_bf16_bits(r.standard_normal((1, k)).astype(np.float32)), dev)
+    y_fused = ops.weight_int4pack_mm(x, cat, g, torch.cat(qszs, dim=1))
+    y_parts = torch.cat([ops.weight_int4pack_mm(x, p, g, z) for p, z in zip(packed, qszs)], 1)
+    assert torch.equal(y_fused, y_parts)
+
+
+def test_int4pack_mm_graph_replay(dev):
+    # the drop-in under capture, M = 1 and M = 8, replayed with eager work in between
+    r = np.random.default_rng(5)
+    k, n, g = 4096, 6144, 128
+    q, qsz = _qsz_weights(r, n, k, g)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+    tq = t_bf16(qsz, dev)
+    xs = [t_bf16(f32_to_bf16_bits(r.standard_normal((m, k)).astype(np.float32)), dev)
+          for m in (1, 8)]
+    eager = [ops.weight_int4pack_mm(x, packed, g, tq) for x in xs]   # workspace grows here
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [ops.weight_int4pack_mm(x, packed, g, tq) for x in xs]
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a, b)
+        ops.weight_int4pack_mm(xs[1], packed, g, tq)                 # eager work between
+
+
+@pytest.mark.parametrize("epilogue", ["none", "residual", "silu_mul"])
+@pytest.mark.parametrize("g", [32, 128, 256])
+def test_prefill_gemm_qsz_epilogues(dev, epilogue, g):
+    # the prompt-length GEMM on the reference's metadata with each epilogue, vs the oracle:
+    # residual h = bf16(bf16(acc) + h); silu_mul over 32-column gate|up blocks
+    r = np.random.default_rng(g + len(epilogue))
+    m, k, n = 37, 2048, 1024
+    q, qsz = _qsz_weights(r, n, k, g)
+    xb = f32_to_bf16_bits(r.standard_normal((m, k)).astype(np.float32))
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+    acc = G.int4pack_mm(bf16_bits_to_f32(xb), q, qsz, g).astype(np.float32)
+    x = t_bf16(xb, dev)
+    if epilogue == "none":
+        got = ops.prefill_gemm_qsz(x, packed, t_bf16(qsz, dev), g).float().cpu().numpy()
+        ref = bf16_bits_to_f32(f32_to_bf16_bits(acc))
+    elif epilogue == "residual":
+        hb = f32_to_bf16_bits(r.standard_normal((m, n)).astype(np.float32))
+        h = t_bf16(hb, dev)
+        ops.prefill_gemm_qsz(x, packed, t_bf16(qsz, dev), g, epilogue="residual", out=h)
+        got = h.float().cpu().numpy()
+        ref = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(f32_to_bf16_bits(acc))
+                                                + bf16_bits_to_f32(hb)))
+    else:
+        got = ops.prefill_gemm_qsz(x, packed, t_bf16(qsz, dev), g,
+                                   epilogue="silu_mul").float().cpu().numpy()
+        j = np.arange(n // 2)
+        gate = bf16_bits_to_f32(f32_to_bf16_bits(acc[:, (j // 32) * 64 + j % 32]))
+        up = bf16_bits_to_f32(f32_to_bf16_bits(acc[:, (j // 32) * 64 + j % 32 + 32]))
+        sg = bf16_bits_to_f32(f32_to_bf16_bits(gate / (1.0 + np.exp(-gate))))
+        ref = bf16_bits_to_f32(f32_to_bf16_bits(sg * up))
+    err = rel_l2(got, ref)
+    print(f"prefill qsz {epilogue} g={g}: rel_l2={err:.2e}")
+    assert err < TOL_BF16
+
+
 def test_int4pack_group_sizes_like_g9(dev):
     # reference G9 (tests/test_quant.py:427-457): 32..256 accepted, 16 rejected
     case = synth.qsz_case(k=4096, n=256, m=4, group=128, seed=1)
@@ -287,7 +404,7 @@ def test_int4pack_group_sizes_like_g9(dev):
 
 def test_residual_epilogue(dev):
     case = synth.qsz_case(k=1024, n=512, m=1, group=128, seed=5)
-    packed = ops.convert_weight_to_int4pack(torch.from_numpy(case["prepacked"]).to(dev), 8)
+    packed = t_i32(G.qweight_from_reference_codes(case["q"]), dev)      # [K/8, N] rows
     x = t_bf16(case["x_bits"], dev).reshape(1, -1)
     resid_bits = f32_to_bf16_bits(np.random.default_rng(6).standard_normal((1, 512)).astype(np.float32))
     resid = t_bf16(resid_bits, dev)
@@ -367,7 +484,7 @@ def test_w4_dispatch_modes(dev):
     from moss_tts_lite_amd.gptq import LIN_NAMES, W4Dispatch
     r = np.random.default_rng(0)
     shapes = {"q": (512, 256), "k": (128, 256), "v": (128, 256), "o": (256, 512),
-              "gate": (384, 256), "up": (384, 256), "down": (256, 384)}
+              "gate": (512, 256), "up": (512, 256), "down": (256, 512)}
     def layer():
         return {n: torch.from_numpy((r.standard_normal(s) * 0.05).astype(np.float32))
                 .to(dev).bfloat16() for n, s in shapes.items()}
@@ -393,7 +510,7 @@ def test_w4_dispatch_modes(dev):
                 packed, qsz = disp.qlayers[li][name]
                 np.testing.assert_array_equal(qsz.view(torch.int16).cpu().numpy().view(np.uint16),
                                               qsz_o)
-                np.testing.assert_array_equal(packed.cpu().numpy(),
+                np.testing.assert_array_equal(packed.cpu().numpy().reshape(-1).view(np.uint32),
                                               G.int4pack_from_prepacked(G.prepack_u8(codes)))
                 ref = xf @ G.effective_weight(codes, qsz_o, g).astype(np.float64).T
             err = rel_l2(got, ref)

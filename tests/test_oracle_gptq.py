@@ -35,7 +35,7 @@ def test_reference_prepack_even_k_high_nibble():
     assert G.prepack_u8(q).tolist() == [[0xA3, 0x1F]]
 
 
-@pytest.mark.parametrize("k,n", [(8, 8), (64, 24), (256, 40)])
+@pytest.mark.parametrize("k,n", [(8, 8), (64, 24), (256, 40), (512, 48)])
 def test_pack_round_trips(k, n):
     r = np.random.default_rng(k + n)
     codes = r.integers(0, 16, size=(k, n)).astype(np.uint8)
@@ -44,8 +44,26 @@ def test_pack_round_trips(k, n):
     assert np.array_equal(G.unpack_qzeros(G.pack_qzeros(z)), z)
     qn = codes.T.copy()
     assert np.array_equal(G.unprepack_u8(G.prepack_u8(qn)), qn)
-    # reference pre-pack -> device layout keeps every (n, k) code
-    assert np.array_equal(G.unpack_qweight(G.int4pack_from_prepacked(G.prepack_u8(qn))), codes)
+    # reference pre-pack -> the drop-in's strip layout keeps every (n, k) code
+    if k % 128 == 0 and n % 16 == 0:
+        words = G.int4pack_from_prepacked(G.prepack_u8(qn))
+        assert np.array_equal(G.unpack_qweight(G.strip_layout_inverse(words, k, n)), codes)
+
+
+def test_strip_layout_brute_force():
+    # every 32-bit word lands where the layout's formula puts it
+    k, n = 256, 48
+    qw = np.arange(k // 8 * n, dtype=np.uint32).reshape(k // 8, n).view(np.int32)
+    words = G.strip_layout(qw)
+    kb = k // 128
+    for r in range(k // 8):
+        for c in range(n):
+            s_, b, rr = c // 16, r // 16, r % 16
+            lane, j = 16 * (rr % 4) + c % 16, rr // 4
+            assert words[((s_ * kb + b) * 64 + lane) * 4 + j] == qw[r, c].view(np.uint32)
+    assert np.array_equal(G.strip_layout_inverse(words, k, n), qw)
+    # a strip is one contiguous run: column 0..15 over all of K come first
+    assert set(words[:k // 8 * 16].tolist()) == set(qw[:, :16].view(np.uint32).reshape(-1).tolist())
 
 
 def test_pack_brute_force_bits():
