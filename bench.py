@@ -619,13 +619,135 @@ def bench_int4_op(args, torch):
                       "us_per_launch": out}))
 
 
+# bf16 keeps of the reference's two shipped GPTQ presets (moss_tts_lite/export.py:59-72):
+# w1 keeps every v_proj, w2 also up_proj of layers 6, 7, 9 and 35; both use group 32
+MOSS_PRESETS = {"w1": [(li, "v") for li in range(36)],
+                "w2": [(li, "v") for li in range(36)] + [(li, "up") for li in (6, 7, 9, 35)]}
+
+
+def moss_records(torch, cfg, dev, keep, group, seed=1234):
+    """Random-init weights of the MOSS backbone in the reference's record form: per linear
+    ``{"packed": torch's int4 tiles [N/8, K/128, 32, 4], "qsz": bf16 [K/g, N, 2]}`` (the
+    standalone export's records, moss_tts_lite/export.py:324-334), and the dense bf16
+    weight of each kept linear. Codes uniform 0..15, scales U(0.002, 0.02), zero points
+    (8 - z) * scale with z uniform 6..9, kept weights N(0, 0.02)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    h, d = cfg.hidden, cfg.head_dim
+    shapes = {"q": (cfg.n_heads * d, h), "k": (cfg.n_kv_heads * d, h), "v": (cfg.n_kv_heads * d, h),
+              "o": (h, cfg.n_heads * d), "gate": (cfg.intermediate, h), "up": (cfg.intermediate, h),
+              "down": (h, cfg.intermediate)}
+    keep = set(keep)
+    layers, state = [], {}
+    for li in range(cfg.n_layers):
+        lw, rec = {}, {}
+        for name, (n, k) in shapes.items():
+            if (li, name) in keep:
+                lw[name] = (torch.randn(n, k, device=dev, generator=gen) * 0.02).bfloat16()
+                continue
+            tiles = torch.randint(-2**31, 2**31 - 1, (n // 8, k // 128, 32, 4), dtype=torch.int32,
+                                  device=dev, generator=gen)
+            sc = torch.rand(k // group, n, device=dev, generator=gen) * 0.018 + 0.002
+            z = torch.randint(6, 10, (k // group, n), device=dev, generator=gen)
+            rec[name] = {"packed": tiles, "qsz": torch.stack([sc, (8 - z) * sc], -1).bfloat16()}
+        layers.append(lw)
+        state[li] = rec
+    return layers, state
+
+
+def bench_moss(args, torch):
+    """The MOSS-TTS decode step at the reference's shape (moss_tts_lite/model.py:9-24: Qwen3-8B
+    backbone, text vocabulary 155648, 32 audio codebooks of 1025) on the reference's own
+    weight records: a shipped preset's group size and bf16 keeps, (packed, qsz) records
+    through W4Dispatch and layers_from_dispatch, qsz read in place by the strip kernels.
+    Prefill 256 random id rows, then graph replays of the text-head variant at host-given
+    positions (FastMossDecoder.step, the reference's FastMossTTS.step contract), timed in
+    the middle of positions 256..1279."""
+    from moss_tts_lite_amd.fast import FastMossDecoder
+    from moss_tts_lite_amd.gptq import W4Dispatch
+    from moss_tts_lite_amd.model import Int4Backbone, layers_from_dispatch, moss_config
+
+    dev = torch.device("cuda:0")
+    group = 32
+    keep = MOSS_PRESETS[args.preset]
+    cfg = moss_config(group_size=group, act_order=False, max_seq=1536)
+    t0 = time.time()
+    layers, state = moss_records(torch, cfg, dev, keep, group)
+    disp = W4Dispatch(layers, w4_group_size=group, bf16_keep=keep, state=state, device=dev)
+    del state
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    h = cfg.hidden
+
+    def normal(*shape, std):
+        return (torch.randn(*shape, device=dev, generator=gen) * std).bfloat16()
+
+    def norm_w(n):
+        return (1.0 + torch.randn(n, device=dev, generator=gen) * 0.05).bfloat16()
+
+    norms = [{"input_layernorm": norm_w(h), "post_attention_layernorm": norm_w(h),
+              "q_norm": norm_w(cfg.head_dim), "k_norm": norm_w(cfg.head_dim)}
+             for _ in range(cfg.n_layers)]
+    w = {"embed_tokens": normal(cfg.text_embed_rows, h, std=1.0), "final_norm": norm_w(h),
+         "head": normal(cfg.vocab, h, std=0.02), "layers": layers_from_dispatch(disp, norms),
+         "emb_ext": [normal(cfg.audio_vocab, h, std=1.0) for _ in range(cfg.n_vq)],
+         "head_audio": normal(cfg.n_vq, cfg.audio_vocab, h, std=0.02)}
+    del disp, layers
+    model = Int4Backbone(cfg, w, dev)
+    del w
+    dec = FastMossDecoder(model)
+    g = torch.Generator().manual_seed(1234)
+    prompt_len = 256
+    rows = torch.cat([torch.randint(0, cfg.vocab, (prompt_len, 1), generator=g),
+                      torch.randint(0, cfg.audio_vocab - 1, (prompt_len, cfg.n_vq), generator=g)], 1)
+    dec.prefill(rows)
+    dec.capture()
+    torch.cuda.synchronize()
+    setup_s = time.time() - t0
+    row = rows[-1].to(dev)
+    mid = (CONFIG4_POSITIONS[0] + CONFIG4_POSITIONS[1] + 1) // 2
+    start = max(prompt_len, min(mid - args.steps // 2, CONFIG4_POSITIONS[1] + 1 - args.steps))
+    for p in range(prompt_len, start):             # untimed steps fill the cache up to there
+        dec.step(row, p)
+    for i in range(args.warmup):
+        dec.step(row, start + i % max(1, args.steps))
+    res = {}
+    for audio2 in (False, True):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            dec.step(row, start + i, audio2)
+        e1.record()
+        torch.cuda.synchronize()
+        res[audio2] = e0.elapsed_time(e1) / args.steps
+    ms_step = res[False]
+    launches = sum(len(p) for p in dec._layers) + len(dec._embed) + len(dec._final_variant(False))
+    return dict(
+        value=round(1000.0 / ms_step, 2), unit="steps/s", ms_per_step=ms_step, steps=args.steps,
+        dtype="int4 (packed, qsz) weights, bf16 activations, fp32 accumulate",
+        config={"workload": f"MOSS-TTS decode step, preset {args.preset} (group {group}, bf16 "
+                            f"keeps: {len(keep)} linears): 36-layer Qwen3-8B backbone on the "
+                            "reference's (packed, qsz) records, 33-way summed embedding, text "
+                            "head 155648x4096 + 32 audio heads of 1025; prefill 256 rows, then "
+                            f"graph replays at host-given positions {start}..{start + args.steps - 1}",
+                "ms_per_step_audio2": round(res[True], 4),
+                "steps_per_s_audio2": round(1000.0 / res[True], 2),
+                "launches_per_step": launches, "setup_s": round(setup_s, 1),
+                "reference_a10g_steps_per_s": {"w1": 81.5, "w2": 78.6}[args.preset]},
+        roofline=None,
+    )
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "kernels", "prefill", "int4-op"])
+                    choices=["decode", "gemv", "kernels", "prefill", "int4-op", "moss"])
+    ap.add_argument("--preset", default="w2", choices=sorted(MOSS_PRESETS),
+                    help="the reference's GPTQ preset: group size and bf16 keeps (moss workload)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--group", type=int, default=128, choices=[32, 64, 128, 256],
                     help="int4 group size of every projection (decode workload)")
@@ -658,6 +780,17 @@ def main():
     if args.workload == "prefill":
         args.steps = 20 if args.steps is None else args.steps
         bench_prefill(args, torch)
+        return
+    if args.workload == "moss":
+        args.warmup = 16 if args.warmup is None else args.warmup
+        args.steps = 256 if args.steps is None else args.steps
+        res = bench_moss(args, torch)
+        print(json.dumps({"metric": "MOSS-TTS decode steps/s at bs=1", "value": res["value"],
+                          "unit": res["unit"], "n_gpus": 1, "steps": res["steps"],
+                          "warmup": args.warmup, "ms_per_step": round(res["ms_per_step"], 6),
+                          "higher_is_better": True, "dtype": res["dtype"],
+                          "data": "synthetic: random-init records and weights, random id rows",
+                          "config": res["config"]}))
         return
     if args.workload == "decode":
         args.warmup = 16 if args.warmup is None else args.warmup

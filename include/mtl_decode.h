@@ -165,6 +165,14 @@ int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, fl
 /* pos[0] += 1 on the device (ends a captured decode step). */
 int mtl_advance_position(int64_t* pos, void* stream);
 
+/*
+ * SwiGLU of a layer whose up_proj stays bf16 (the w2 preset keeps it on some layers,
+ * moss_tts_lite/export.py:66-70) while gate_proj is int4:
+ * act[i] = bf16(silu(bf16 gate[i]) * bf16 up[i]) (moss_tts_lite/fast.py:170-171), from the
+ * two projections' fp32 outputs.  n elements (any rows x columns, contiguous).
+ */
+int mtl_silu_mul_f32(const float* gate, const float* up, void* act, int64_t n, void* stream);
+
 /* ---- Prefill: every prompt row in one launch (moss_tts_lite/fast.py:210-270) ---- */
 
 /*

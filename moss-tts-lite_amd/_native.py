@@ -62,6 +62,7 @@ _SIGNATURES = {
     "mtl_bf16_gemv_argmax": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                                     _c_void_p, _i64, _c_void_p]),
     "mtl_advance_position": (_i32, [_c_void_p, _c_void_p]),
+    "mtl_silu_mul_f32": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "mtl_bf16_gemv_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _i64,
                                   _i64, _c_void_p, _c_void_p]),
     "mtl_bf16_gemv": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p]),

@@ -41,6 +41,13 @@ __device__ __forceinline__ void round_bf16x2(float lo, float hi, float& rlo, flo
   rhi = __uint_as_float(p & 0xffff0000u);
 }
 
+// bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
+__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
+  g = round_bf16(g);
+  const float sg = round_bf16(g / (1.0f + expf(-g)));
+  return f32_to_bf16(sg * round_bf16(u));
+}
+
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
 }

@@ -961,6 +961,16 @@ __global__ void advance_position_kernel(int64_t* pos) {
   if (threadIdx.x == 0 && blockIdx.x == 0) pos[0] += 1;
 }
 
+// act[i] = bf16(silu(bf16 gate_i) * bf16 up_i) from fp32 projections (fast.py:170-171): the
+// SwiGLU of a layer whose up_proj stays bf16 while gate_proj is int4, so the two come from
+// separate GEMVs.
+__global__ void silu_mul_f32_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                    uint16_t* __restrict__ act, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    act[i] = (uint16_t)silu_mul_bf16(gate[i], up[i]);
+}
+
 }  // namespace mtl
 
 using namespace mtl;
@@ -1241,6 +1251,16 @@ int mtl_tune_set_attn_fixed(int32_t on) {
 int mtl_advance_position(int64_t* pos, void* stream) {
   if (!pos) return MTL_ERR_INVALID_ARG;
   hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, pos);
+  return launch_status();
+}
+
+int mtl_silu_mul_f32(const float* gate, const float* up, void* act, int64_t n, void* stream) {
+  if (!gate || !up || !act) return MTL_ERR_INVALID_ARG;
+  if (n < 1 || n >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+  int blocks = (int)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(silu_mul_f32_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, gate,
+                     up, static_cast<uint16_t*>(act), n);
   return launch_status();
 }
 

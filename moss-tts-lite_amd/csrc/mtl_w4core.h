@@ -16,13 +16,6 @@ __device__ __forceinline__ float4 ld_f4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 
-// bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
-__device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
-  g = round_bf16(g);
-  const float sg = round_bf16(g / (1.0f + expf(-g)));
-  return f32_to_bf16(sg * round_bf16(u));
-}
-
 // Where a GEMV kernel reads its activation row from.
 enum : int {
   XSRC_BF16 = 0,      // x bf16 [M, K]

@@ -51,6 +51,7 @@ import torch
 
 from . import _native as N
 from . import ops
+from .gptq import QszLinear
 from .model import Int4Backbone, attention_scale
 
 
@@ -95,17 +96,25 @@ class FastDecoder:
     def __init__(self, model: Int4Backbone, plan: str = "strip", split_k: tuple | None = None):
         if plan not in self.PLANS:
             raise ValueError(f"plan must be one of {self.PLANS}")
+        # the reference's (packed, qsz) records exist in the strip layout only
+        qsz = any(isinstance(lyr[k], QszLinear) for lyr in model.layers
+                  for k in ("qkv", "o", "gate_up", "down"))
         if split_k is None:   # measured fastest: q|k|v keeps split-K (the attention sums it)
-            split_k = ("qkv",) if plan == "strip" else ()
+            split_k = ("qkv",) if plan == "strip" and not qsz else ()
         if not set(split_k) <= {"qkv", "gate_up"} or (split_k and plan != "strip"):
             raise ValueError("split_k names GEMVs of the strip plan: 'qkv', 'gate_up'")
+        if qsz and (plan != "strip" or split_k):
+            raise ValueError("(packed, qsz) linears run in the strip plan with split_k=()")
         self.m = model
         self.plan = plan
         # layers whose v_proj stays bf16: q|k on the int4 strip GEMV and v on the bf16
         # GEMV, both into one fp32 "split" of the q|k|v partials the attention reads
         self.v_keep = ["v_keep" in lyr for lyr in model.layers]
-        if any(self.v_keep) and plan != "strip":
-            raise ValueError("layers with a bf16-kept v_proj run in the strip plan")
+        # layers whose up_proj stays bf16: the int4 gate and the bf16 up write fp32 halves
+        # of the gate|up partials, an elementwise pass forms SiLU(gate) * up
+        self.up_keep = ["up_keep" in lyr for lyr in model.layers]
+        if (any(self.v_keep) or any(self.up_keep)) and plan != "strip":
+            raise ValueError("layers with a bf16-kept v_proj or up_proj run in the strip plan")
         self.fused = plan != "unfused"
         self.strip = plan == "strip"
         # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
@@ -186,19 +195,26 @@ class FastDecoder:
                  qz.data_ptr(), p(perm), n, lin.group_size, lin.zero_offset, epilogue, p(resid),
                  y.data_ptr(), N.OUT_BF16, self.ws.data_ptr(), self.ws.numel()))
 
+    @staticmethod
+    def _weight(lin, strip: bool):
+        """``(weight, layout, metadata, zeros)`` of one int4 GEMV launch: the strip copy
+        with its strip-ordered metadata (or the qsz read in place), else the split-K form."""
+        _, qz, sc, _ = lin.kernel_args()
+        qw, layout = lin.stream_weight(strip)
+        if layout in (N.LAYOUT_STRIP, N.LAYOUT_STRIP_QSZ):
+            sc, qz = lin.strip_meta()
+        return qw, layout, sc, qz
+
     def _partials(self, x, xpart_name, lin, n, name):
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
-        _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip_gemv[name])
-        if layout == N.LAYOUT_STRIP:
-            sc, qz = lin.strip_meta()
+        qw, layout, sc, qz = self._weight(lin, self.strip_gemv[name])
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
         out = self.part[name]
         return ("mtl_w4_gemm_partials",
                 (p(x), p(xpart), xs, 2 * lin.in_features if xpart_name else 0, 1,
-                 lin.in_features, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(),
+                 lin.in_features, qw.data_ptr(), sc.data_ptr(), p(qz),
                  None, n, lin.group_size,
                  lin.zero_offset, layout, out.data_ptr(), out.numel() * 4))
 
@@ -313,7 +329,22 @@ class FastDecoder:
                                             self.attn_ws.numel())),
             self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu),
         ]
-        if self.strip_gemv["gate_up"]:   # SiLU*up in the epilogue; down reads the product
+        if self.up_keep[li]:   # int4 gate and bf16 up into fp32 halves, then SiLU*up
+            inter = cfg.intermediate
+            gu = self.part["gate_up"]
+            plan += [
+                self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"], inter,
+                                    "gate_up", strip=True),
+                ("mtl_bf16_gemv_norm", (self.h.data_ptr(), lyr["post_attention_layernorm"].data_ptr(),
+                                        self.slots.data_ptr(), eps, lyr["up_keep"].data_ptr(),
+                                        inter, cfg.hidden, gu[inter:].data_ptr())),
+                ("mtl_silu_mul_f32", (gu.data_ptr(), gu[inter:].data_ptr(), self.act.data_ptr(),
+                                      inter)),
+                self._residual(self.act, None, lyr["down"],
+                               None if last else self.inv_perm_qkv[li + 1],
+                               None if last else self.x_qkv),
+            ]
+        elif self.strip_gemv["gate_up"]:   # SiLU*up in the epilogue; down reads the product
             plan += [
                 self._norm_silu(self.x_gu, self.norm_gu[li], lyr["gate_up"]),
                 self._residual(self.act, None, lyr["down"],
@@ -331,39 +362,33 @@ class FastDecoder:
         return plan
 
     def _norm_silu(self, h_ord, w_ord, lin):
-        _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(True)
-        sc, qz = lin.strip_meta()
+        qw, layout, sc, qz = self._weight(lin, True)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         return ("mtl_w4_gemm_norm_silu",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
-                 qz.data_ptr(), lin.out_features, lin.group_size, lin.zero_offset, layout,
+                 p(qz), lin.out_features, lin.group_size, lin.zero_offset, layout,
                  self.act.data_ptr()))
 
     def _residual(self, x, xpart_name, lin, scatter, h_ord):
-        _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip)
-        if layout == N.LAYOUT_STRIP:
-            sc, qz = lin.strip_meta()
+        qw, layout, sc, qz = self._weight(lin, self.strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
         return ("mtl_w4_gemm_residual",
                 (p(x), p(xpart), self.splits[xpart_name] if xpart_name else 0,
                  2 * lin.in_features if xpart_name else 0, lin.in_features, qw.data_ptr(),
-                 sc.data_ptr(), qz.data_ptr(), lin.out_features, lin.group_size,
+                 sc.data_ptr(), p(qz), lin.out_features, lin.group_size,
                  lin.zero_offset, layout, self.h.data_ptr(), p(scatter), p(h_ord),
                  self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel()))
 
     def _norm_partials(self, h_ord, w_ord, lin, n, name, strip=None):
-        _, qz, sc, _ = lin.kernel_args()
-        qw, layout = lin.stream_weight(self.strip_gemv[name] if strip is None else strip)
-        if layout == N.LAYOUT_STRIP:
-            sc, qz = lin.strip_meta()
+        qw, layout, sc, qz = self._weight(lin, self.strip_gemv[name] if strip is None else strip)
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         out = self.part[name]
         return ("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
-                 qz.data_ptr(), n, lin.group_size, lin.zero_offset, layout, out.data_ptr(),
+                 p(qz), n, lin.group_size, lin.zero_offset, layout, out.data_ptr(),
                  out.numel() * 4))
 
     def _layer_plan(self, li: int) -> list:
@@ -416,7 +441,7 @@ class FastDecoder:
                       "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
                       "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
                       "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual",
-                      "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm")}
+                      "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -467,6 +492,8 @@ class FastDecoder:
         shift = 1 if self.plan in ("fused", "strip") and li == 0 else 0   # layer 0: the stats
         if self.v_keep[li] and name != "qkv":
             shift += 1                                                     # the bf16 v launch
+        if self.up_keep[li] and name == "down":
+            shift += 2                                                     # bf16 up, SiLU*up
         return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:
@@ -554,15 +581,24 @@ class FastDecoder:
         pf = {"rows": rows, "ids": z(self.table_ptrs.numel(), torch.int64), "h": z(cfg.hidden),
               "x": z(cfg.hidden), "x_nat": z(cfg.hidden), "qkv": z(cfg.qkv_out),
               "q": z(cfg.n_heads * cfg.head_dim), "attn": z(cfg.hidden),
-              "act": z(cfg.intermediate)}
+              "act": z(cfg.intermediate),
+              "gate": z(cfg.intermediate) if any(self.up_keep) else None}
         self._pf = pf
         return pf
 
     def _prefill_gemm(self, x, rows: int, lin, epilogue: int, y, ldy: int, stream) -> None:
-        """One prompt-length int4 GEMM on the strip copy of ``lin`` (mtl_w4_gemm_prefill)."""
-        qw, _ = lin.stream_weight(True)
+        """One prompt-length int4 GEMM on the strip copy of ``lin`` (mtl_w4_gemm_prefill,
+        or mtl_w4_gemm_prefill_qsz for the reference's records)."""
+        qw, layout = lin.stream_weight(True)
         sc, qz = lin.strip_meta()
         ws = ops.prefill_workspace(self.dev, rows, lin.in_features, lin.out_features)
+        if layout == N.LAYOUT_STRIP_QSZ:
+            N.check(N.load().mtl_w4_gemm_prefill_qsz(
+                x.data_ptr(), rows, x.stride(0), lin.in_features, qw.data_ptr(), sc.data_ptr(),
+                lin.out_features, lin.group_size, epilogue, N.OUT_BF16, y.data_ptr(), ldy,
+                None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel() * 4,
+                stream), "mtl_w4_gemm_prefill_qsz")
+            return
         N.check(N.load().mtl_w4_gemm_prefill(
             x.data_ptr(), rows, x.stride(0), lin.in_features, qw.data_ptr(), sc.data_ptr(),
             qz.data_ptr(), lin.out_features, lin.group_size, lin.zero_offset, epilogue,
@@ -623,7 +659,23 @@ class FastDecoder:
                                            p(lyr["gate_up"].kernel_args()[3]), x.data_ptr(),
                                            cfg.hidden, rows, cfg.hidden, eps, st),
                     "mtl_rmsnorm_gather")
-            self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_SILU_MUL, act, cfg.intermediate, st)
+            if self.up_keep[li]:
+                # int4 gate and the bf16-kept up_proj (gptq.py:689-693), then SiLU(gate) * up
+                # in bf16 as the reference's MLP forms it (model.py:40-44)
+                gate = pf["gate"]
+                self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_NONE, gate, cfg.intermediate, st)
+                x_up = x
+                if lyr["gate_up"].kernel_args()[3] is not None:   # up reads natural order
+                    x_up = pf["x_nat"]
+                    N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
+                                                   lyr["post_attention_layernorm"].data_ptr(),
+                                                   None, x_up.data_ptr(), cfg.hidden, rows,
+                                                   cfg.hidden, eps, st), "mtl_rmsnorm_gather")
+                up = torch.nn.functional.linear(x_up[:rows], lyr["up_keep"])
+                torch.mul(torch.nn.functional.silu(gate[:rows]), up, out=act[:rows])
+            else:
+                self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_SILU_MUL, act,
+                                   cfg.intermediate, st)
             self._prefill_gemm(act, rows, lyr["down"], N.EPI_RESIDUAL, h, cfg.hidden, st)
         return h[:rows]
 

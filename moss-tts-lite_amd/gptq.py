@@ -16,7 +16,8 @@ import torch
 from . import _native as N
 from . import ops
 
-__all__ = ["GPTQLinear", "fuse_gptq_linears", "group_scales_from_weight", "rtn_quantize",
+__all__ = ["GPTQLinear", "QszLinear", "fuse_gptq_linears", "fuse_qsz_linears",
+           "interleave_qsz_gate_up", "group_scales_from_weight", "rtn_quantize",
            "pack_fast", "pack_qsz_only", "effective_weight", "kernel_linear",
            "interleave_gate_up", "bf16_linear", "W4Dispatch", "load_gptq_state", "LIN_NAMES"]
 
@@ -159,6 +160,93 @@ class GPTQLinear(torch.nn.Module):
         out = torch.empty_like(w)
         out[perm.long()] = w
         return out
+
+
+class QszLinear:
+    """An int4 linear in the reference's own contract (moss_tts_lite/gptq.py:66-97):
+    ``packed`` from :func:`ops.convert_weight_to_int4pack` or
+    :func:`ops.int4pack_from_torch_tiles` (the strip layout in torch's 4-D shape) and
+    ``qsz`` bf16 ``[K/g, N, 2]`` = (scale, zero), ``w = (q - 8) * scale + zero``.  Its
+    groups are contiguous runs of K (no act-order).  The decode step and the prefill run it
+    on the strip kernels with the qsz read in place (``MTL_LAYOUT_STRIP_QSZ``).
+    """
+
+    zero_offset = 0
+
+    def __init__(self, packed: torch.Tensor, qsz: torch.Tensor, group_size: int):
+        if group_size not in (32, 64, 128, 256):
+            raise ValueError("group_size must be 32/64/128/256")
+        if qsz.dtype != torch.bfloat16 or qsz.dim() != 3 or qsz.shape[2] != 2:
+            raise ValueError("qsz must be bfloat16 [K/g, N, 2]")
+        self.group_size = group_size
+        self.in_features = qsz.shape[0] * group_size
+        self.out_features = qsz.shape[1]
+        k, n = self.in_features, self.out_features
+        if packed.dtype != torch.int32 or packed.numel() * 8 != n * k or packed.shape[0] * 8 != n:
+            raise ValueError(f"packed must be the int32 [N/8, ...] packing of N={n}, K={k}")
+        if k % 256 or n % 16:
+            raise ValueError("the strip kernels need K % 256 == 0 and N % 16 == 0")
+        self.packed = packed.contiguous()
+        self.qsz = qsz.contiguous()
+
+    def kernel_args(self):
+        """``(weight, qzeros, metadata, perm)`` as GPTQLinear's: no zeros, no gather."""
+        return self.packed, None, self.qsz, None
+
+    def supports_strip(self) -> bool:
+        return self.in_features <= 16384
+
+    def stream_weight(self, strip: bool = True):
+        """The packed weight is the strip layout already (``MTL_LAYOUT_STRIP_QSZ``)."""
+        return self.packed, N.LAYOUT_STRIP_QSZ
+
+    def strip_meta(self):
+        """``(metadata, zeros)`` in the strip kernels' argument order: qsz, none."""
+        return self.qsz, None
+
+    def post_init(self) -> "QszLinear":
+        return self
+
+    def drop_original(self) -> None:
+        pass
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shp = x.shape
+        y = ops.weight_int4pack_mm(x.reshape(-1, shp[-1]), self.packed, self.group_size, self.qsz)
+        return y.reshape(*shp[:-1], self.out_features)
+
+    __call__ = forward
+
+    def dequantize(self) -> torch.Tensor:
+        """Exact fp32 ``W[K, N]``."""
+        return ops.qsz_dequant(self.packed, self.qsz, self.group_size)
+
+
+def fuse_qsz_linears(parts: list[QszLinear]) -> QszLinear:
+    """Concatenate reference-contract linears along N, as fast_native.py:146-161 does
+    (``torch.cat(packed, 0)``, ``torch.cat(qsz, 1)``): bitwise neutral per column."""
+    g, k = parts[0].group_size, parts[0].in_features
+    if any(p.group_size != g or p.in_features != k for p in parts[1:]):
+        raise ValueError("fused linears need the same K and group size")
+    return QszLinear(torch.cat([p.packed for p in parts], 0), torch.cat([p.qsz for p in parts], 1), g)
+
+
+def interleave_qsz_gate_up(gate: QszLinear, up: QszLinear, block: int = 32) -> QszLinear:
+    """gate and up fused with columns in alternating 32-wide blocks ``[gate 0:32 | up 0:32 |
+    gate 32:64 | ...]`` (the layout of the SiLU*up epilogue): whole 16-column strips of the
+    packed weights and the matching qsz columns are reordered."""
+    n = gate.out_features
+    if up.out_features != n or n % block or up.in_features != gate.in_features or \
+            up.group_size != gate.group_size:
+        raise ValueError("gate and up need the same K, group and N (a multiple of 32)")
+    per = block // 16                                   # strips per block
+    gp = gate.packed.reshape(n // block, per, -1)
+    uq = up.packed.reshape(n // block, per, -1)
+    packed = torch.stack([gp, uq], 1).reshape(2 * n // 8, *gate.packed.shape[1:])
+    gs = gate.qsz.reshape(gate.qsz.shape[0], n // block, block, 2)
+    us = up.qsz.reshape(up.qsz.shape[0], n // block, block, 2)
+    qsz = torch.stack([gs, us], 2).reshape(gate.qsz.shape[0], 2 * n, 2)
+    return QszLinear(packed, qsz, gate.group_size)
 
 
 def fuse_gptq_linears(parts: list[GPTQLinear]) -> GPTQLinear:

@@ -14,10 +14,12 @@ import math
 
 import torch
 
-from .gptq import GPTQLinear
+from .gptq import (GPTQLinear, QszLinear, W4Dispatch, fuse_qsz_linears,
+                   interleave_qsz_gate_up)
 
 ROPE_THETA = 1_000_000.0
 RMS_EPS = 1e-6
+_NORMS = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm")
 
 
 @dataclasses.dataclass
@@ -107,7 +109,15 @@ def rope_tables(n: int, head_dim: int, theta: float, device, dtype=torch.bfloat1
 
 
 class Int4Backbone:
-    """Weights, caches and tables of the decoder on one device."""
+    """Weights, caches and tables of the decoder on one device.
+
+    Each layer's int4 projections are :class:`GPTQLinear` (AutoGPTQ buffers) or
+    :class:`QszLinear` (the reference's ``(packed, qsz)`` records, see
+    :func:`layers_from_dispatch`).  Two projections may stay bf16 as in the reference's
+    presets (gptq.py:645-650): ``"v"`` (then ``"qkv"`` holds q|k) and ``"up"`` (then the
+    layer holds ``"gate"``, an int4 linear of ``intermediate`` columns, instead of the
+    interleaved ``"gate_up"``).
+    """
 
     def __init__(self, cfg: BackboneConfig, weights: dict, device="cuda"):
         cfg.validate()
@@ -136,15 +146,15 @@ class Int4Backbone:
             self.head_2way = self.head[list(cfg.two_way_ids)].contiguous()
         self.layers = []
         for lw in weights["layers"]:
-            lyr = {k: T(lw[k]) for k in ("input_layernorm", "post_attention_layernorm",
-                                         "q_norm", "k_norm")}
-            for k in ("qkv", "o", "gate_up", "down"):
+            lyr = {k: T(lw[k]) for k in _NORMS}
+            up_keep = "up" in lw
+            for k in ("qkv", "o", "gate" if up_keep else "gate_up", "down"):
                 lin = lw[k]
-                if not isinstance(lin, GPTQLinear):
-                    raise TypeError(f"layer weight {k} must be a GPTQLinear")
+                if not isinstance(lin, (GPTQLinear, QszLinear)):
+                    raise TypeError(f"layer weight {k} must be a GPTQLinear or QszLinear")
                 lin.post_init()
                 lin.drop_original()
-                lyr[k] = lin
+                lyr["gate_up" if k == "gate" else k] = lin
             # v_proj kept in bf16 (the shipped GPTQ presets, export.py:59-72): "qkv" then
             # holds q|k only and "v" the bf16 weight [kv_heads * head_dim, hidden]
             nv = cfg.n_kv_heads * cfg.head_dim
@@ -157,9 +167,22 @@ class Int4Backbone:
                     raise ValueError("with a kept v, qkv must hold q|k only")
             elif lyr["qkv"].out_features != cfg.qkv_out:
                 raise ValueError("qkv must hold q|k|v")
+            perm_down = lyr["down"].kernel_args()[3]
+            if up_keep:
+                # up_proj kept in bf16: "gate_up" holds the int4 gate alone; SiLU*up is a
+                # separate elementwise pass, so down must read its input in natural order
+                up = lw["up"]
+                if up.dtype != torch.bfloat16 or tuple(up.shape) != (cfg.intermediate, cfg.hidden):
+                    raise ValueError(f"kept up must be bfloat16 [{cfg.intermediate}, {cfg.hidden}]")
+                if lyr["gate_up"].out_features != cfg.intermediate:
+                    raise ValueError("with a kept up, gate must have intermediate columns")
+                if perm_down is not None:
+                    raise ValueError("a kept up needs a down projection without act-order")
+                lyr["up_keep"] = T(up)
+            elif lyr["gate_up"].out_features != 2 * cfg.intermediate:
+                raise ValueError("gate_up must hold 2 * intermediate columns")
             # gate|up emits its SiLU*up channels already in the down projection's
             # act-order input order, so the down GEMV reads them without a gather.
-            perm_down = lyr["down"].kernel_args()[3]
             lyr["act_in_down_order"] = perm_down is not None
             if perm_down is not None:
                 lyr["gate_up"].reorder_output_columns(gate_up_columns_for(perm_down))
@@ -172,6 +195,44 @@ class Int4Backbone:
     def reset_cache(self) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()
+
+
+def layers_from_dispatch(disp: W4Dispatch, norms: list[dict]) -> list[dict]:
+    """Backbone layer weights from the reference's per-linear records: the
+    ``(packed, qsz)`` pairs a :class:`W4Dispatch` installed (fast.py:73-121,
+    gptq.py:641-697) and the bf16 weights it kept.
+
+    q|k|v are concatenated along N, as fast_native.py:146-161 concatenates them
+    (``torch.cat`` of the packed tensors on dim 0 and of the qsz on dim 1); gate and up
+    are interleaved in whole 16-column strips for the SiLU*up epilogue.  v_proj and
+    up_proj may be kept bf16; every other projection must be int4.  ``norms[li]`` holds
+    the layer's four norm weights."""
+    out = []
+    for li, lw in enumerate(disp.layers):
+        qd = disp.qlayers[li] or {}
+        missing = [n for n in ("q", "k", "o", "gate", "down") if n not in qd]
+        if missing:
+            raise ValueError(f"layer {li}: {missing} must be int4 for the decode step")
+
+        def lin(name):
+            packed, qsz = qd[name]
+            return QszLinear(packed, qsz, disp.group_size_map[li][name])
+
+        layer = {k: norms[li][k] for k in _NORMS}
+        if "v" in qd:
+            layer["qkv"] = fuse_qsz_linears([lin("q"), lin("k"), lin("v")])
+        else:
+            layer["qkv"] = fuse_qsz_linears([lin("q"), lin("k")])
+            layer["v"] = lw["v"]
+        layer["o"] = lin("o")
+        if "up" in qd:
+            layer["gate_up"] = interleave_qsz_gate_up(lin("gate"), lin("up"))
+        else:
+            layer["gate"] = lin("gate")
+            layer["up"] = lw["up"]
+        layer["down"] = lin("down")
+        out.append(layer)
+    return out
 
 
 def _random_gptq(gen, dev, k: int, n: int, g: int, perm: torch.Tensor | None) -> GPTQLinear:

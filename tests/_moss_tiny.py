@@ -199,3 +199,33 @@ def device_backbone(m: dict, dev, max_seq: int = 64):
          "head": bf(m["head"]), "layers": layers,
          "emb_ext": [bf(e) for e in m["emb_ext"]], "head_audio": bf(m["head_audio"])}
     return Int4Backbone(backbone_config(max_seq, m["act_order"]), w, dev)
+
+
+def dispatch_backbone(m: dict, dev, max_seq: int = 64, keep=()):
+    """The same model through the reference's own per-linear records: a ``W4Dispatch``
+    over the layers' dense bf16 weights with a state of ``(codes, qsz)`` records
+    (:func:`qsz_record`) for every linear not in ``keep`` (the reference's bf16-keep list,
+    gptq.py:645-650), assembled by ``layers_from_dispatch``. Contiguous groups only."""
+    import torch
+
+    from moss_tts_lite_amd.gptq import W4Dispatch
+    from moss_tts_lite_amd.model import Int4Backbone, layers_from_dispatch
+
+    def bf(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(dev)
+
+    dense = [{name: bf(_bf16(dense_nk(lyr[name]))) for name in LINEARS} for lyr in m["layers"]]
+    state = {}
+    for li, lyr in enumerate(m["layers"]):
+        state[li] = {}
+        for name in LINEARS:
+            rec = qsz_record(lyr[name])
+            state[li][name] = {"q": torch.from_numpy(rec["q"]),
+                               "qsz": torch.from_numpy(rec["qsz"].view(np.int16)).view(torch.bfloat16)}
+    disp = W4Dispatch(dense, w4_group_size=GROUP, bf16_keep=keep, state=state, device=dev)
+    norms = [{k: bf(lyr[k]) for k in ("input_layernorm", "post_attention_layernorm", "q_norm",
+                                      "k_norm")} for lyr in m["layers"]]
+    w = {"embed_tokens": bf(m["embed_tokens"]), "final_norm": bf(m["final_norm"]),
+         "head": bf(m["head"]), "layers": layers_from_dispatch(disp, norms),
+         "emb_ext": [bf(e) for e in m["emb_ext"]], "head_audio": bf(m["head_audio"])}
+    return Int4Backbone(backbone_config(max_seq, False), w, dev)

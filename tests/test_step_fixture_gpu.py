@@ -40,14 +40,35 @@ def fb(t):
 def test_moss_decoder_matches_reference_model(dev, tag, plan):
     from moss_tts_lite_amd.fast import FastMossDecoder
 
+    model = T.device_backbone(T.generate(T.SEED, tag == "ao"), dev, max_seq=64)
+    _check_decoder(FastMossDecoder(model, plan=plan), tag, plan)
+
+
+# bf16-keep lists in the reference's form (gptq.py:645-650): every v_proj kept, and
+# up_proj of layer 0 as in the shipped presets' layers that keep it
+KEEPS = {"int4": (), "keep_v_up": [(0, "v"), (1, "v"), (0, "up")]}
+
+
+@pytest.mark.parametrize("keep", list(KEEPS))
+def test_moss_decoder_on_reference_records(dev, keep):
+    """The reference's own ``(codes, qsz)`` records through ``W4Dispatch`` and
+    ``layers_from_dispatch``: the qsz read in place by the strip kernels, v/up kept bf16."""
+    from moss_tts_lite_amd.fast import FastMossDecoder
+
+    model = T.dispatch_backbone(T.generate(T.SEED, False), dev, max_seq=64, keep=KEEPS[keep])
+    dec = FastMossDecoder(model)
+    assert dec.up_keep == [keep != "int4", False]
+    assert dec.v_keep == [keep != "int4"] * 2
+    _check_decoder(dec, "ct", keep)
+
+
+def _check_decoder(dec, tag, label):
     fix = dict(np.load(FIX))
     f = bf16_bits_to_f32
-    model = T.device_backbone(T.generate(T.SEED, tag == "ao"), dev, max_seq=64)
-    dec = FastMossDecoder(model, plan=plan)
     rows, n_prompt = fix["rows"], int(fix["prompt_rows"])
     hf0 = fb(dec.prefill(torch.from_numpy(rows[:n_prompt])))
     err = rel_l2(hf0, f(fix[f"{tag}_hf"][0]))
-    print(f"{tag}/{plan} prefill: hf rel_l2={err:.2e}")
+    print(f"{tag}/{label} prefill: hf rel_l2={err:.2e}")
     assert err < BAR
     dec.capture()
     idx = fix[f"{tag}_lt_idx"]
@@ -63,7 +84,7 @@ def test_moss_decoder_matches_reference_model(dev, tag, plan):
                 "lt": rel_l2(fb(lt)[idx], f(fix[f"{tag}_lt"][i])),
                 "la": rel_l2(fb(la)[:, keep], f(fix[f"{tag}_la"][i])[:, keep]),
                 "two": rel_l2(fb(two), f(fix[f"{tag}_two"][i]))}
-        print(f"{tag}/{plan} pos {p}: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+        print(f"{tag}/{label} pos {p}: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
         assert max(errs.values()) < BAR, (p, errs)
     # positions outside the cache and host ids outside a table are refused before replay
     with pytest.raises(ValueError):
