@@ -10,6 +10,10 @@ exact result the fp32 kernels approximate), then round.
 Pinning: ``rms_norm`` against torch's own bf16 chain and closed-form properties;
 ``rope_tables`` against float64 trigonometry (<= 1 bf16 ulp); ``attention`` against a
 float64 brute-force softmax and torch's CPU SDPA; see tests/test_oracle_decode.py.
+The composition (``decoder_layer``, ``decode_step``, ``moss_decode_step``, ``moss_heads``)
+and every piece on the reference's own operands are pinned to the reference's eager
+``MossTTSModel`` run on the CPU (tests/golden/moss_step_fixtures.npz,
+tests/test_oracle_step_fixture.py), with planted composition slips as negative controls.
 """
 from __future__ import annotations
 
