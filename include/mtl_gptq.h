@@ -368,6 +368,57 @@ int mtl_w4_gemm_norm_silu(const void* h, const void* w, const float* slots, floa
                           int64_t N, int32_t group_size, int32_t zero_offset, int32_t layout,
                           void* act, void* stream);
 
+/*
+ * Launch geometry of the full-K strip GEMV (MTL_LAYOUT_STRIP, MTL_LAYOUT_STRIP_QSZ).  No
+ * counterpart in the reference: the entries below are the four strip-layout GEMV entries
+ * above with the launch shape given explicitly instead of chosen by the library, for
+ * callers that sweep or pin launch shapes (benchmarks, tests).  Every field 0 (or a NULL
+ * geometry) means automatic, which is what the entries without _geom use.  The arithmetic
+ * per column is the same in every geometry up to the number of K slices whose sums are
+ * added (strips_per_wg and blocks_per_wave fix it); the ring depth changes only when loads
+ * are issued, so outputs equal the automatic ring's bit for bit.
+ *   strips_per_wg    CT, 16-column strips per workgroup: 1, 2 or 4 for the RMSNorm-staged
+ *                    store, 2 or 6 for the SiLU*up epilogue (gate|up strip pairs), 1 for
+ *                    the others; qsz metadata (MTL_LAYOUT_STRIP_QSZ): automatic only
+ *   blocks_per_wave  NB, 128-channel blocks per wave: 2, 4, 6, 8 or 16 with K/128 % NB == 0
+ *                    and (K/128/NB) * CT waves per workgroup within the kernel's limit
+ *   ring             blocks in flight per wave: 2 (NB = 2 or 8), 4 (NB = 4, 8 or 16),
+ *                    8 (NB = 8 or 16, g >= 64), 16 (NB = 16, g >= 64), or NB = 6's own
+ *   xcd_order        1: each XCD runs a contiguous range of strips (when the workgroup
+ *                    count is a multiple of 8); -1: workgroup id order; 0: automatic (1)
+ * A geometry that does not fit returns MTL_ERR_SHAPE (NB, CT) or MTL_ERR_UNSUPPORTED.
+ */
+typedef struct mtl_strip_geometry {
+  int32_t strips_per_wg;
+  int32_t blocks_per_wave;
+  int32_t ring;
+  int32_t xcd_order;
+} mtl_strip_geometry;
+
+int mtl_w4_gemm_partials_geom(const void* x, const float* xpart, int32_t xsplits,
+                              int64_t xpart_ld, int64_t M, int64_t K, const int32_t* qweight,
+                              const void* scales, const int32_t* qzeros, const int32_t* perm,
+                              int64_t N, int32_t group_size, int32_t zero_offset, int32_t layout,
+                              float* partials, int64_t partials_bytes,
+                              const mtl_strip_geometry* geom, void* stream);
+int mtl_w4_gemm_norm_partials_geom(const void* h, const void* w, const float* slots, float eps,
+                                   int64_t K, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, int64_t N, int32_t group_size,
+                                   int32_t zero_offset, int32_t layout, float* partials,
+                                   int64_t partials_bytes, const mtl_strip_geometry* geom,
+                                   void* stream);
+int mtl_w4_gemm_residual_geom(const void* x, const float* xpart, int32_t xsplits,
+                              int64_t xpart_ld, int64_t K, const int32_t* qweight,
+                              const void* scales, const int32_t* qzeros, int64_t N,
+                              int32_t group_size, int32_t zero_offset, int32_t layout, void* h,
+                              const int32_t* scatter, void* h_ord, float* slots, void* workspace,
+                              int64_t ws_bytes, const mtl_strip_geometry* geom, void* stream);
+int mtl_w4_gemm_norm_silu_geom(const void* h, const void* w, const float* slots, float eps,
+                               int64_t K, const int32_t* qweight, const void* scales,
+                               const int32_t* qzeros, int64_t N, int32_t group_size,
+                               int32_t zero_offset, int32_t layout, void* act,
+                               const mtl_strip_geometry* geom, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

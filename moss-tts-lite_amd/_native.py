@@ -109,19 +109,37 @@ _SIGNATURES = {
     "mtl_w4_gemm_norm_silu": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                      _c_void_p, _c_void_p]),
+    "mtl_w4_gemm_partials_geom": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _c_void_p,
+                                         _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                         _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "mtl_w4_gemm_norm_partials_geom": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
+                                              _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
+                                              _i32, _i32, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "mtl_w4_gemm_residual_geom": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p,
+                                         _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _c_void_p,
+                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                         _c_void_p, _c_void_p]),
+    "mtl_w4_gemm_norm_silu_geom": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
+                                          _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                          _c_void_p, _c_void_p, _c_void_p]),
     "mtl_w4_tiled_bytes": (_i64, [_i64, _i64]),
     "mtl_w4_tile": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
     "mtl_w4_strip_bytes": (_i64, [_i64, _i64]),
     "mtl_w4_strip_meta": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                  _c_void_p]),
     "mtl_w4_strip": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p]),
-    "mtl_tune_set_reduce": (_i32, [_i32]),
-    "mtl_tune_set_strip_nb": (_i32, [_i32]),
-    "mtl_tune_set_strip_xcd": (_i32, [_i32]),
-    "mtl_tune_set_strip_ct": (_i32, [_i32]),
-    "mtl_tune_set_strip_full": (_i32, [_i32]),
-    "mtl_tune_set_attn_fixed": (_i32, [_i32]),
 }
+
+class StripGeometry(ctypes.Structure):
+    """``mtl_strip_geometry``: the strip GEMV's launch shape (0 = automatic per field)."""
+    _fields_ = [("strips_per_wg", ctypes.c_int32), ("blocks_per_wave", ctypes.c_int32),
+                ("ring", ctypes.c_int32), ("xcd_order", ctypes.c_int32)]
+
+
+def strip_geometry(ct: int = 0, nb: int = 0, ring: int = 0, xcd_order: int = 0):
+    """A ``mtl_strip_geometry`` passed by reference to the ``*_geom`` entries."""
+    return ctypes.byref(StripGeometry(ct, nb, ring, xcd_order))
+
 
 NOALLOC_SCRATCH_BYTES = 16 << 20      # MTL_NOALLOC_SCRATCH_BYTES
 MTL_OK = 0

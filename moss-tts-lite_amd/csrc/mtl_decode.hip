@@ -346,7 +346,6 @@ struct AttnArgs {
   int fixed_chunks;           // chunks are the fixed blocks [64c, 64c + 64)
 };
 
-static int g_attn_fixed = 1;  // tuning knob: fixed 64-position chunks where max_seq allows
 
 // The merge of one kv head's chunk partials (m, l, o[128]) per q head, in chunk order,
 // by the last workgroup of that kv head to finish; out[h*128 + d] (through out_index).
@@ -1079,7 +1078,7 @@ static int attn_check(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int
 static void attn_launch(AttnArgs& a, void* workspace, bool from_part, hipStream_t s) {
   a.counters = static_cast<uint32_t*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kAttnCounterBytes);
-  a.fixed_chunks = g_attn_fixed && a.max_seq <= kAttnBlock * kAttnMaxChunks;
+  a.fixed_chunks = a.max_seq <= kAttnBlock * kAttnMaxChunks;   // the tile kernel where it fits
   int64_t ch = (a.max_seq + kAttnBlock - 1) / kAttnBlock;
   if (ch > kAttnMaxChunks) ch = kAttnMaxChunks;
   const dim3 grid(a.Hkv, (unsigned)ch);
@@ -1238,14 +1237,6 @@ int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, fl
                  static_cast<float*>(nullptr), static_cast<long long*>(nullptr),
                  static_cast<const uint16_t*>(norm_w), slots, eps, (int64_t)0, (int64_t)0, out);
   return launch_status();
-}
-
-// Tuning knob (process-wide): 1 = the tile attention kernel (fixed 64-position chunks,
-// MFMA scores) when max_seq <= 4096, 0 = the chunked kernel with length-sized chunks.
-int mtl_tune_set_attn_fixed(int32_t on) {
-  if (on != 0 && on != 1) return MTL_ERR_INVALID_ARG;
-  g_attn_fixed = on;
-  return MTL_OK;
 }
 
 int mtl_advance_position(int64_t* pos, void* stream) {

@@ -175,6 +175,7 @@ struct StripArgs {
   float* slots_out;           // one sum of squares per 16 columns
   uint16_t* act;              // bf16 [N/2]: silu(gate) * up, 32-column gate|up interleave
   int K, N, group, zero_offset, kblocks, xcd_order, fmt;
+  mtl_strip_geometry geom;    // requested launch shape (all 0: automatic)
 };
 
 enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };

@@ -580,7 +580,6 @@ static Plan plan_for(int64_t K, int64_t N, int64_t M = 1, int group = 128) {
 // Workspace = a fixed tile-counter region (so partial tiles of one shape never land on
 // another shape's counters) followed by the fp32 partial tiles [splits, M, N].
 constexpr int64_t kCounterBytes = 16384;   // 4096 column tiles: N <= 1M
-static int g_inkernel_reduce = 1;
 
 template <int MR, int GR, int KW>
 static void launch_fmt(const W4Args& a, int fmt, dim3 grid, hipStream_t s) {
@@ -696,7 +695,7 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   a.splits = p.splits;
   a.epilogue = epilogue;
   a.out_f32 = out_dtype == MTL_OUT_F32;
-  a.inkernel_reduce = g_inkernel_reduce;
+  a.inkernel_reduce = 1;   // split-K tiles reduced by their last workgroup
   if (p.splits > 1) {
     const int64_t need = kCounterBytes + (int64_t)p.splits * M * N * 4;
     if (!workspace || ws_bytes < need) return MTL_ERR_WORKSPACE;
@@ -771,6 +770,7 @@ static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
   a.group = group; a.zero_offset = zero_offset;
   a.kblocks = 0;
   a.xcd_order = 0;
+  a.geom = mtl_strip_geometry{0, 0, 0, 0};
   return a;
 }
 
@@ -778,7 +778,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
                             int64_t M, int64_t K, const int32_t* qweight, const void* meta0,
                             const int32_t* qzeros, const int32_t* perm, int64_t N, int group,
                             int zero_offset, int layout, float* partials, int64_t partials_bytes,
-                            hipStream_t stream) {
+                            hipStream_t stream, const mtl_strip_geometry* geom = nullptr) {
   if (const int st = check_layout(layout, M, K, N, perm, group)) return st;
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta_given(layout, meta0, qzeros) ||
       !partials)
@@ -806,6 +806,7 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
     sa.xsplits = xsplits;
     sa.xpart_ld = (int)xpart_ld;
     sa.y = partials;
+    if (geom) sa.geom = *geom;
     return strip_launch(sa, stream);
   }
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
@@ -837,7 +838,8 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
                                  float eps, int64_t K, const int32_t* qweight,
                                  const void* meta0, const int32_t* qzeros, int64_t N, int group,
                                  int zero_offset, int layout, float* partials,
-                                 int64_t partials_bytes, hipStream_t stream) {
+                                 int64_t partials_bytes, hipStream_t stream,
+                                 const mtl_strip_geometry* geom = nullptr) {
   if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (!h_ord || !w_ord || !slots || !qweight || !meta_given(layout, meta0, qzeros) || !partials)
     return MTL_ERR_INVALID_ARG;
@@ -856,6 +858,7 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
     sa.slots = slots;
     sa.eps = eps;
     sa.y = partials;
+    if (geom) sa.geom = *geom;
     return strip_launch(sa, stream);
   }
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
@@ -890,7 +893,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
                             const int32_t* qzeros, int64_t N, int group, int zero_offset,
                             int layout, void* h, const int32_t* scatter, void* h_ord,
                             float* slots, void* workspace, int64_t ws_bytes,
-                            hipStream_t stream) {
+                            hipStream_t stream, const mtl_strip_geometry* geom = nullptr) {
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta_given(layout, meta0, qzeros) || !h ||
       !slots)
     return MTL_ERR_INVALID_ARG;
@@ -919,6 +922,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
     sa.scatter = scatter;
     sa.h_ord = static_cast<uint16_t*>(h_ord);
     sa.slots_out = slots;
+    if (geom) sa.geom = *geom;
     return strip_launch(sa, stream);
   }
   if (reinterpret_cast<uintptr_t>(meta0) & 7u) return MTL_ERR_ALIGN;
@@ -959,13 +963,14 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
 static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* slots, float eps,
                              int64_t K, const int32_t* qweight, const void* meta0,
                              const int32_t* qzeros, int64_t N, int group, int zero_offset,
-                             int layout, void* act, hipStream_t stream) {
+                             int layout, void* act, hipStream_t stream,
+                             const mtl_strip_geometry* geom = nullptr) {
   if (!h_ord || !w_ord || !slots || !qweight || !meta_given(layout, meta0, qzeros) || !act)
     return MTL_ERR_INVALID_ARG;
   if (!is_strip(layout)) return MTL_ERR_UNSUPPORTED;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 64 != 0 || K > 16384 ||
-      !strip_blocks_per_wave(K, 2, group) ||
+      (!geom && !strip_blocks_per_wave(K, 2, group)) ||
       N * K / 2 >= ((int64_t)1 << 31) || K > (int64_t)kSlotCols * kMaxSlots)
     return MTL_ERR_SHAPE;
   if (!aligned16(slots) || !aligned16(h_ord) || !aligned16(w_ord) || !aligned16(qweight) ||
@@ -977,6 +982,7 @@ static int w4_gemm_norm_silu(const void* h_ord, const void* w_ord, const float* 
   sa.slots = slots;
   sa.eps = eps;
   sa.act = static_cast<uint16_t*>(act);
+  if (geom) sa.geom = *geom;
   return strip_launch(sa, stream);
 }
 
@@ -1087,12 +1093,49 @@ int mtl_w4_gemm_fused(const void* x, int64_t M, int64_t K, const int32_t* qweigh
                  (hipStream_t)stream);
 }
 
-// Tuning knobs for launch-shape sweeps; process-wide, not for concurrent use.
-// Split-K reduction: 1 = in-kernel (last workgroup of a tile), 0 = separate kernel.
-int mtl_tune_set_reduce(int32_t inkernel) {
-  if (inkernel != 0 && inkernel != 1) return MTL_ERR_INVALID_ARG;
-  g_inkernel_reduce = inkernel;
-  return MTL_OK;
+int mtl_w4_gemm_partials_geom(const void* x, const float* xpart, int32_t xsplits,
+                              int64_t xpart_ld, int64_t M, int64_t K, const int32_t* qweight,
+                              const void* scales, const int32_t* qzeros, const int32_t* perm,
+                              int64_t N, int32_t group_size, int32_t zero_offset, int32_t layout,
+                              float* partials, int64_t partials_bytes,
+                              const mtl_strip_geometry* geom, void* stream) {
+  if (geom && !is_strip(layout)) return MTL_ERR_UNSUPPORTED;
+  return w4_gemm_partials(x, xpart, xsplits, xpart_ld, M, K, qweight, scales, qzeros, perm, N,
+                          group_size, zero_offset, layout, partials, partials_bytes,
+                          (hipStream_t)stream, geom);
+}
+
+int mtl_w4_gemm_norm_partials_geom(const void* h, const void* w, const float* slots, float eps,
+                                   int64_t K, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, int64_t N, int32_t group_size,
+                                   int32_t zero_offset, int32_t layout, float* partials,
+                                   int64_t partials_bytes, const mtl_strip_geometry* geom,
+                                   void* stream) {
+  if (geom && !is_strip(layout)) return MTL_ERR_UNSUPPORTED;
+  return w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N, group_size,
+                               zero_offset, layout, partials, partials_bytes,
+                               (hipStream_t)stream, geom);
+}
+
+int mtl_w4_gemm_residual_geom(const void* x, const float* xpart, int32_t xsplits,
+                              int64_t xpart_ld, int64_t K, const int32_t* qweight,
+                              const void* scales, const int32_t* qzeros, int64_t N,
+                              int32_t group_size, int32_t zero_offset, int32_t layout, void* h,
+                              const int32_t* scatter, void* h_ord, float* slots, void* workspace,
+                              int64_t ws_bytes, const mtl_strip_geometry* geom, void* stream) {
+  if (geom && !is_strip(layout)) return MTL_ERR_UNSUPPORTED;
+  return w4_gemm_residual(x, xpart, xsplits, xpart_ld, K, qweight, scales, qzeros, N, group_size,
+                          zero_offset, layout, h, scatter, h_ord, slots, workspace, ws_bytes,
+                          (hipStream_t)stream, geom);
+}
+
+int mtl_w4_gemm_norm_silu_geom(const void* h, const void* w, const float* slots, float eps,
+                               int64_t K, const int32_t* qweight, const void* scales,
+                               const int32_t* qzeros, int64_t N, int32_t group_size,
+                               int32_t zero_offset, int32_t layout, void* act,
+                               const mtl_strip_geometry* geom, void* stream) {
+  return w4_gemm_norm_silu(h, w, slots, eps, K, qweight, scales, qzeros, N, group_size,
+                           zero_offset, layout, act, (hipStream_t)stream, geom);
 }
 
 

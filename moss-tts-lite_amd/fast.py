@@ -93,7 +93,11 @@ class FastDecoder:
 
     PLANS = ("strip", "fused", "staged", "partials", "unfused")
 
-    def __init__(self, model: Int4Backbone, plan: str = "strip", split_k: tuple | None = None):
+    def __init__(self, model: Int4Backbone, plan: str = "strip", split_k: tuple | None = None,
+                 strip_geometry: dict | None = None):
+        """``strip_geometry`` maps a GEMV name ("qkv", "o", "gate_up", "down") to the launch
+        shape of its strip launch, ``dict(ct=, nb=, ring=, xcd_order=)`` with 0 for automatic
+        (``mtl_strip_geometry``); the default is the library's automatic choice."""
         if plan not in self.PLANS:
             raise ValueError(f"plan must be one of {self.PLANS}")
         # the reference's (packed, qsz) records exist in the strip layout only
@@ -107,6 +111,12 @@ class FastDecoder:
             raise ValueError("(packed, qsz) linears run in the strip plan with split_k=()")
         self.m = model
         self.plan = plan
+        geo = dict(strip_geometry or {})
+        if not set(geo) <= {"qkv", "o", "gate_up", "down"}:
+            raise ValueError("strip_geometry names GEMVs: 'qkv', 'o', 'gate_up', 'down'")
+        self._geom = {k: N.StripGeometry(int(v.get("ct", 0)), int(v.get("nb", 0)),
+                                         int(v.get("ring", 0)), int(v.get("xcd_order", 0)))
+                      for k, v in geo.items()}
         # layers whose v_proj stays bf16: q|k on the int4 strip GEMV and v on the bf16
         # GEMV, both into one fp32 "split" of the q|k|v partials the attention reads
         self.v_keep = ["v_keep" in lyr for lyr in model.layers]
@@ -205,6 +215,15 @@ class FastDecoder:
             sc, qz = lin.strip_meta()
         return qw, layout, sc, qz
 
+    def _with_geometry(self, launch, name):
+        """The launch through its ``_geom`` entry when a strip geometry is set for ``name``."""
+        fn, args = launch
+        layout = {"mtl_w4_gemm_partials": 13, "mtl_w4_gemm_norm_partials": 11,
+                  "mtl_w4_gemm_residual": 11, "mtl_w4_gemm_norm_silu": 11}[fn]
+        if name not in self._geom or args[layout] not in (N.LAYOUT_STRIP, N.LAYOUT_STRIP_QSZ):
+            return launch
+        return fn + "_geom", args + (ctypes.byref(self._geom[name]),)
+
     def _partials(self, x, xpart_name, lin, n, name):
         """Partials-only GEMV; its input is already in the weight's act-order row order."""
         qw, layout, sc, qz = self._weight(lin, self.strip_gemv[name])
@@ -212,11 +231,11 @@ class FastDecoder:
         xpart = self.part[xpart_name] if xpart_name else None
         xs = self.splits[xpart_name] if xpart_name else 0
         out = self.part[name]
-        return ("mtl_w4_gemm_partials",
+        return self._with_geometry(("mtl_w4_gemm_partials",
                 (p(x), p(xpart), xs, 2 * lin.in_features if xpart_name else 0, 1,
                  lin.in_features, qw.data_ptr(), sc.data_ptr(), p(qz),
                  None, n, lin.group_size,
-                 lin.zero_offset, layout, out.data_ptr(), out.numel() * 4))
+                 lin.zero_offset, layout, out.data_ptr(), out.numel() * 4)), name)
 
     def _layer_plan_fused(self, li: int) -> list:
         m, cfg = self.m, self.m.cfg
@@ -327,7 +346,7 @@ class FastDecoder:
                                             cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
                                             cfg.max_seq, scale, eps, self.attn_ws.data_ptr(),
                                             self.attn_ws.numel())),
-            self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu),
+            self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu, "o"),
         ]
         if self.up_keep[li]:   # int4 gate and bf16 up into fp32 halves, then SiLU*up
             inter = cfg.intermediate
@@ -364,32 +383,32 @@ class FastDecoder:
     def _norm_silu(self, h_ord, w_ord, lin):
         qw, layout, sc, qz = self._weight(lin, True)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        return ("mtl_w4_gemm_norm_silu",
+        return self._with_geometry(("mtl_w4_gemm_norm_silu",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
                  p(qz), lin.out_features, lin.group_size, lin.zero_offset, layout,
-                 self.act.data_ptr()))
+                 self.act.data_ptr())), "gate_up")
 
-    def _residual(self, x, xpart_name, lin, scatter, h_ord):
+    def _residual(self, x, xpart_name, lin, scatter, h_ord, name="down"):
         qw, layout, sc, qz = self._weight(lin, self.strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
-        return ("mtl_w4_gemm_residual",
+        return self._with_geometry(("mtl_w4_gemm_residual",
                 (p(x), p(xpart), self.splits[xpart_name] if xpart_name else 0,
                  2 * lin.in_features if xpart_name else 0, lin.in_features, qw.data_ptr(),
                  sc.data_ptr(), p(qz), lin.out_features, lin.group_size,
                  lin.zero_offset, layout, self.h.data_ptr(), p(scatter), p(h_ord),
-                 self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel()))
+                 self.slots.data_ptr(), self.res_ws.data_ptr(), self.res_ws.numel())), name)
 
     def _norm_partials(self, h_ord, w_ord, lin, n, name, strip=None):
         qw, layout, sc, qz = self._weight(lin, self.strip_gemv[name] if strip is None else strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         out = self.part[name]
-        return ("mtl_w4_gemm_norm_partials",
+        return self._with_geometry(("mtl_w4_gemm_norm_partials",
                 (h_ord.data_ptr(), w_ord.data_ptr(), self.slots.data_ptr(),
                  ctypes.c_float(self.m.cfg.eps), lin.in_features, qw.data_ptr(), sc.data_ptr(),
                  p(qz), n, lin.group_size, lin.zero_offset, layout, out.data_ptr(),
-                 out.numel() * 4))
+                 out.numel() * 4)), name)
 
     def _layer_plan(self, li: int) -> list:
         m, cfg = self.m, self.m.cfg
@@ -441,7 +460,9 @@ class FastDecoder:
                       "mtl_qk_norm_rope_kv_partials", "mtl_residual_rmsnorm", "mtl_residual_add",
                       "mtl_w4_gemm_norm_partials", "mtl_decode_attention_fused",
                       "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual",
-                      "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32")}
+                      "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32",
+                      "mtl_w4_gemm_partials_geom", "mtl_w4_gemm_norm_partials_geom",
+                      "mtl_w4_gemm_residual_geom", "mtl_w4_gemm_norm_silu_geom")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -744,11 +765,12 @@ class FastMossDecoder(FastDecoder):
     serves every cache length.
     """
 
-    def __init__(self, model: Int4Backbone, plan: str = "strip"):
+    def __init__(self, model: Int4Backbone, plan: str = "strip",
+                 strip_geometry: dict | None = None):
         if model.cfg.n_vq < 1:
             raise ValueError("FastMossDecoder needs a MOSS-shaped backbone (cfg.n_vq > 0)")
         self.graphs: dict | None = None
-        super().__init__(model, plan)
+        super().__init__(model, plan, strip_geometry=strip_geometry)
 
     def _alloc_io(self) -> None:
         m, cfg, dev = self.m, self.m.cfg, self.m.device

@@ -27,12 +27,15 @@ def test_every_header_symbol_has_a_signature():
 
 def test_every_bound_symbol_is_declared():
     declared = set(N.header_symbols())
-    undeclared = [n for n in N._SIGNATURES if n not in declared and not n.startswith("mtl_tune_")]
+    undeclared = [n for n in N._SIGNATURES if n not in declared]
     assert not undeclared, undeclared
 
 
-def test_tune_knobs_validate(lib):
-    assert lib.mtl_tune_set_reduce(2) == N.MTL_ERR_INVALID_ARG
+def test_no_process_wide_tuning_state(lib):
+    # launch shapes travel as arguments (mtl_strip_geometry), never as library state
+    names = set(N.header_symbols()) | set(N._SIGNATURES)
+    assert not [n for n in names if n.startswith("mtl_tune_")]
+    assert not hasattr(lib, "mtl_tune_set_strip_nb")
 
 
 def test_status_strings(lib):
@@ -150,9 +153,24 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_w4_strip_bytes(4096, 24584) == 0 and lib.mtl_w4_strip_bytes(4224, 4096) == 0
     assert lib.mtl_w4_strip(FAKE, 4096, 24584, FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
     assert lib.mtl_w4_strip(FAKE, 4096, 4096, FAKE, 100, None) == N.MTL_ERR_WORKSPACE
-    assert lib.mtl_tune_set_strip_nb(3) == N.MTL_ERR_INVALID_ARG
-    assert lib.mtl_tune_set_strip_ct(3) == N.MTL_ERR_INVALID_ARG
-    assert lib.mtl_tune_set_strip_full(2) == N.MTL_ERR_INVALID_ARG
+    # explicit launch geometries are validated before any launch
+    geo = lambda **kw: lib.mtl_w4_gemm_partials_geom(  # noqa: E731
+        FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096, 128, 0, strip, FAKE, 1 << 30,
+        N.strip_geometry(**kw), None)
+    assert geo(nb=3) == N.MTL_ERR_SHAPE             # 32 blocks do not split into 3s
+    assert geo(ct=2) == N.MTL_ERR_UNSUPPORTED       # the plain store serves one strip
+    assert geo(nb=4, ring=2) == N.MTL_ERR_UNSUPPORTED
+    assert geo(nb=2, ring=4) == N.MTL_ERR_UNSUPPORTED
+    assert geo(xcd_order=2) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_w4_gemm_partials_geom(FAKE, None, 0, 0, 1, 4096, FAKE, FAKE, FAKE, None, 4096,
+                                         128, 0, N.LAYOUT_ROWS, FAKE, 1 << 30,
+                                         N.strip_geometry(nb=8), None) == N.MTL_ERR_UNSUPPORTED
+    silu = lambda **kw: lib.mtl_w4_gemm_norm_silu_geom(  # noqa: E731
+        FAKE, FAKE, FAKE, ctypes.c_float(1e-6), 4096, FAKE, FAKE, FAKE, 24576, 128, 0, strip,
+        FAKE, N.strip_geometry(**kw), None)
+    assert silu(ct=4) == N.MTL_ERR_UNSUPPORTED     # gate|up pairs: 2 or 6 strips
+    assert silu(ct=6, nb=8) == N.MTL_ERR_SHAPE      # 4 slices x 6 strips: 24 waves
+    assert silu(ct=2, nb=8, ring=16) == N.MTL_ERR_UNSUPPORTED
     assert lib.mtl_bf16_gemv_argmax(FAKE, FAKE, 100, 4100, None, None, FAKE, 1 << 20,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_advance_position(None, None) == N.MTL_ERR_INVALID_ARG

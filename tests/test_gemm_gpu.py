@@ -657,25 +657,27 @@ def test_strip_meta_layout_bit_exact(dev, group):
     assert np.array_equal(qz.cpu().numpy().view(np.uint8).reshape(-1), ref_z)
 
 
-def _strip_partials(lib, case, dev, src, x=None, xp=None, h=None, wn=None, slots=None):
-    """One strip launch through the partials (or norm-partials) entry: fp32 [N]."""
+def _strip_partials(lib, case, dev, src, x=None, xp=None, h=None, wn=None, slots=None, geom=None):
+    """One strip launch through the partials (or norm-partials) entry: fp32 [N]; with
+    ``geom`` (a dict of mtl_strip_geometry fields) through its ``_geom`` twin."""
     import ctypes
     k, n, g = case["k"], case["n"], case["group"]
     qw = ops.strip_weights(t_i32(case["qweight"], dev))
     sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), case["group"])
     y = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
     st = torch.cuda.current_stream().cuda_stream
+    extra = () if geom is None else (N.strip_geometry(**geom),)
     if src == "norm":
-        N.check(lib.mtl_w4_gemm_norm_partials(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
-                                              ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
-                                              qz.data_ptr(), n, g, 0, N.LAYOUT_STRIP, y.data_ptr(),
-                                              y.numel() * 4, st), "strip norm")
+        fn = lib.mtl_w4_gemm_norm_partials if geom is None else lib.mtl_w4_gemm_norm_partials_geom
+        N.check(fn(h.data_ptr(), wn.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), k,
+                   qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), n, g, 0, N.LAYOUT_STRIP,
+                   y.data_ptr(), y.numel() * 4, *extra, st), "strip norm")
     else:
-        N.check(lib.mtl_w4_gemm_partials(None if x is None else x.data_ptr(),
-                                         None if xp is None else xp.data_ptr(),
-                                         0 if xp is None else xp.shape[0], 0 if xp is None else 2 * k,
-                                         1, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), None, n,
-                                         g, 0, N.LAYOUT_STRIP, y.data_ptr(), y.numel() * 4, st),
+        fn = lib.mtl_w4_gemm_partials if geom is None else lib.mtl_w4_gemm_partials_geom
+        N.check(fn(None if x is None else x.data_ptr(), None if xp is None else xp.data_ptr(),
+                   0 if xp is None else xp.shape[0], 0 if xp is None else 2 * k,
+                   1, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), None, n,
+                   g, 0, N.LAYOUT_STRIP, y.data_ptr(), y.numel() * 4, *extra, st),
                 "strip partials")
     torch.cuda.synchronize()
     return y
@@ -789,38 +791,30 @@ def test_strip_residual_epilogue(dev, src):
     assert torch.equal(h2, h) and torch.equal(o2, h_ord) and torch.equal(s2, slots)
 
 
-@pytest.mark.parametrize("k,n,nb", [(4096, 1024, 8), (4096, 1024, 16), (12288, 512, 8)])
-def test_strip_ring_depth_is_bitwise_neutral(dev, k, n, nb):
-    # the deep load ring (8 blocks in flight) changes when loads are issued, not the
-    # arithmetic: outputs equal the default 4-block ring's bit for bit
+@pytest.mark.parametrize("k,n,nb,rings", [(4096, 1024, 8, (2, 4, 8)), (4096, 1024, 16, (4, 8, 16)),
+                                           (12288, 512, 8, (2, 4, 8))])
+def test_strip_ring_depth_is_bitwise_neutral(dev, k, n, nb, rings):
+    # the load ring (blocks in flight per wave) changes when loads are issued, not the
+    # arithmetic: every ring gives the automatic ring's outputs bit for bit
     lib = N.load()
     case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=k + n + nb)
     x = t_bf16(case["x_bits"], dev)
-    outs = []
-    try:
-        assert lib.mtl_tune_set_strip_nb(nb) == 0
-        for full in (0, 1):
-            assert lib.mtl_tune_set_strip_full(full) == 0
-            outs.append(_strip_partials(lib, case, dev, "bf16", x=x))
-    finally:
-        lib.mtl_tune_set_strip_nb(0)
-        lib.mtl_tune_set_strip_full(-1)
+    outs = [_strip_partials(lib, case, dev, "bf16", x=x, geom=dict(nb=nb, ring=r)) for r in rings]
     assert rel_l2(outs[0].cpu().numpy(), case["y_ref"][0]) < TOL_F32
-    assert torch.equal(outs[0], outs[1])
+    for o in outs[1:]:
+        assert torch.equal(outs[0], o)
+    if nb == 8:        # the automatic geometry is one of them
+        assert torch.equal(outs[0], _strip_partials(lib, case, dev, "bf16", x=x))
 
 
-def test_strip_blocks_per_wave_knob(dev):
+def test_strip_blocks_per_wave_geometry(dev):
     # every launch shape of the strip GEMV computes the same product (rounding aside)
     lib = N.load()
     case = synth.gptq_case(k=4096, n=1024, m=1, group=128, seed=3)
     x = t_bf16(case["x_bits"], dev)
-    outs = {}
-    try:
-        for nb in (0, 2, 4, 8):
-            assert lib.mtl_tune_set_strip_nb(nb) == 0
-            outs[nb] = _strip_partials(lib, case, dev, "bf16", x=x).cpu().numpy()
-    finally:
-        lib.mtl_tune_set_strip_nb(0)
+    outs = {nb: _strip_partials(lib, case, dev, "bf16", x=x,
+                                geom=None if nb == 0 else dict(nb=nb)).cpu().numpy()
+            for nb in (0, 2, 4, 8)}
     for nb, y in outs.items():
         assert rel_l2(y, case["y_ref"][0]) < TOL_F32, nb
     assert np.array_equal(outs[0], outs[8])     # automatic choice for K = 4096
@@ -852,18 +846,12 @@ def test_strip_norm_silu_epilogue(dev, n, ct, nb):
                                      ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
                                      qz.data_ptr(), n, 128, 0, N.LAYOUT_ROWS, act.data_ptr(),
                                      st) == N.MTL_ERR_UNSUPPORTED
-    try:
-        assert lib.mtl_tune_set_strip_ct(ct) == 0
-        N.check(lib.mtl_w4_gemm_norm_silu(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
-                                          ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
-                                          qz.data_ptr(), n, 128, 0, N.LAYOUT_STRIP, act.data_ptr(),
-                                          st), "norm silu")
-        assert lib.mtl_tune_set_strip_ct(0) == 0
-        assert lib.mtl_tune_set_strip_nb(nb) == 0
-        y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots).cpu().numpy()
-    finally:
-        lib.mtl_tune_set_strip_ct(0)
-        lib.mtl_tune_set_strip_nb(0)
+    N.check(lib.mtl_w4_gemm_norm_silu_geom(h.data_ptr(), wn.data_ptr(), slots.data_ptr(),
+                                           ctypes.c_float(1e-6), k, qw.data_ptr(), sc.data_ptr(),
+                                           qz.data_ptr(), n, 128, 0, N.LAYOUT_STRIP, act.data_ptr(),
+                                           N.strip_geometry(ct=ct, nb=nb), st), "norm silu")
+    y = _strip_partials(lib, case, dev, "norm", h=h, wn=wn, slots=slots,
+                        geom=dict(nb=nb)).cpu().numpy()
     j = np.arange(n // 2)
     gcol = (j // 32) * 64 + j % 32
     rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
