@@ -42,9 +42,16 @@ __device__ __forceinline__ void round_bf16x2(float lo, float hi, float& rlo, flo
 }
 
 // bf16(silu(bf16 g) * bf16 u): F.silu on a bf16 tensor then a bf16 product (fast.py:170-171).
+// silu(g) = g / (1 + e^-g) in fp32 from the hardware exp2 and reciprocal (v_exp_f32 of
+// -g * log2(e), v_rcp_f32, each about 1 ulp): within a few fp32 ulps of the correctly
+// rounded quotient, so the bf16 result differs from it only where the quotient lies within
+// those ulps of a bf16 rounding boundary (a few in 10^5).  Every kernel uses this one form.
+// It sits on the tail of the SiLU*up GEMV launches, where the libm exp and the IEEE
+// division cost 0.3 us.  g -> -inf gives -0 (e = inf, rcp = 0), g -> +inf gives g.
 __device__ __forceinline__ uint32_t silu_mul_bf16(float g, float u) {
   g = round_bf16(g);
-  const float sg = round_bf16(g / (1.0f + expf(-g)));
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  const float sg = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + e));
   return f32_to_bf16(sg * round_bf16(u));
 }
 

@@ -578,11 +578,17 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   }
 
   // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order.
+  // The count is a release (every partial store of the workgroup happens before it, through
+  // the barrier) and the workgroup that makes it complete takes an acquire fence before any
+  // thread reads the partials: the hand-off is ordered by the memory model, not only by the
+  // store acknowledgements.
   __builtin_amdgcn_s_waitcnt(0);      // every partial store acknowledged before the count
   __syncthreads();
-  if (threadIdx.x == 0)
-    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELAXED,
+  if (threadIdx.x == 0) {
+    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nch - 1);
+    if (last_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
   if (!last_flag) return;
   if (threadIdx.x == 0)
@@ -771,12 +777,15 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
     }
   }
 
-  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order.
+  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order
+  //    (release count, acquire fence of the completing workgroup, as in attn_decode_kernel).
   __builtin_amdgcn_s_waitcnt(0);      // every partial store acknowledged before the count
   __syncthreads();
-  if (t == 0)
-    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELAXED,
+  if (t == 0) {
+    last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nch - 1);
+    if (last_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
   if (!last_flag) return;
   if (t == 0)

@@ -374,12 +374,15 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
                            __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    // release count / acquire fence of the completing workgroup (as in the decode attention)
     __builtin_amdgcn_s_waitcnt(0);   // every partial store acknowledged before the count
     __syncthreads();
     __shared__ int last_flag;
-    if (t == 0)
-      last_flag = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED,
+    if (t == 0) {
+      last_flag = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELEASE,
                                          __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(a.splits - 1);
+      if (last_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     __syncthreads();
     if (!last_flag) return;
     if (t == 0)

@@ -287,6 +287,27 @@ w4_strip_kernel(StripArgs a) {
   if (wave != 0) return;
   const int q4 = lane % (4 * CT);                // CT need not be a power of two
   const int ec = q4 >> 2;                        // strip of these columns
+  if (EPI == STRIP_EPI_SILU) {
+    // lanes 0..4P-1 sum the gate columns 4*(lane%4)..+3 of pair P*wg + lane/4 and their up
+    // partners (strip ec + P) straight from LDS, both in slice order: no cross-lane step
+    // between the sums and SiLU on the launch's tail.  Column i of pair p's gate strip is
+    // SwiGLU output 16*p + i (64-column blocks of 32 gate | 32 up), so lane l writes
+    // 16*P*wg + 4*l .. +3.
+    if (lane >= 4 * P) return;
+    float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < kw; ++k) {
+      const float4 g4 = *reinterpret_cast<const float4*>(&ytile[k * CT + ec][4 * (q4 & 3)]);
+      const float4 u4 = *reinterpret_cast<const float4*>(&ytile[k * CT + ec + P][4 * (q4 & 3)]);
+      g[0] += g4.x; g[1] += g4.y; g[2] += g4.z; g[3] += g4.w;
+      u[0] += u4.x; u[1] += u4.y; u[2] += u4.z; u[3] += u4.w;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = silu_mul_bf16(g[e], u[e]);
+    *reinterpret_cast<u32x2*>(a.act + (size_t)wg * 16 * P + 4 * lane) =
+        u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    return;
+  }
   float y[4] = {0.f, 0.f, 0.f, 0.f};
   for (int k = 0; k < kw; ++k) {
     const float4 t4 = *reinterpret_cast<const float4*>(&ytile[k * CT + ec][4 * (q4 & 3)]);
@@ -302,22 +323,6 @@ w4_strip_kernel(StripArgs a) {
                   f32_to_bf16(y[2]) | (f32_to_bf16(y[3]) << 16)};
       else
         *reinterpret_cast<float4*>(a.y + c0) = make_float4(y[0], y[1], y[2], y[3]);
-    }
-    return;
-  }
-  if (EPI == STRIP_EPI_SILU) {
-    // lanes 0..4P-1 hold gate columns 4*(lane%4)..+3 of pair P*wg + lane/4 and take their
-    // up partners from lanes 4P..8P-1; column i of pair p's gate strip is SwiGLU output
-    // 16*p + i (64-column blocks of 32 gate | 32 up), so lane l writes 16*P*wg + 4*l ..
-    float u[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) u[e] = __shfl_down(y[e], 4 * P);
-    if (lane < 4 * P) {
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = silu_mul_bf16(y[e], u[e]);
-      *reinterpret_cast<u32x2*>(a.act + (size_t)wg * 16 * P + 4 * lane) =
-          u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
     }
     return;
   }

@@ -107,3 +107,23 @@ def slots16(h) -> np.ndarray:
     for j in range(4):
         c = (c + sq[:, :, j]).astype(np.float32)
     return ((c[:, 0] + c[:, 1]) + (c[:, 2] + c[:, 3])).astype(np.float32)
+
+
+def silu_mul_check(got_bits, g, u):
+    """Compare SwiGLU outputs ``bf16(silu(bf16 g) * bf16 u)`` (uint16 bits) with numpy's
+    correctly rounded form.  The kernels take silu from the hardware exp2 and reciprocal, so
+    silu(g) may round to the other bf16 neighbour of the exact quotient where that quotient
+    lies within a few fp32 ulps of a rounding boundary; the product then differs by up to
+    2 bf16 ulps.  Returns (share of outputs equal bit for bit, every output equal to the
+    product with silu rounded to the exact bf16 value or one of its two neighbours)."""
+    rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
+    g = rb(g)
+    ub = rb(u)
+    sg_bits = f32_to_bf16_bits((g / (np.float32(1) + np.exp(-g))).astype(np.float32)).astype(np.int64)
+    got = np.asarray(got_bits).astype(np.int64)
+    exact = f32_to_bf16_bits((bf16_bits_to_f32(sg_bits.astype(np.uint16)) * ub).astype(np.float32))
+    ok = got == exact
+    for d in (1, -1):
+        nb = ((sg_bits + d) & 0xFFFF).astype(np.uint16)
+        ok |= got == f32_to_bf16_bits((bf16_bits_to_f32(nb) * ub).astype(np.float32))
+    return float(np.mean(got == exact)), bool(ok.all())

@@ -825,11 +825,11 @@ def test_strip_norm_silu_epilogue(dev, n, ct, nb):
     # gate|up with RMSNorm staging and the SiLU*up epilogue (one gate|up strip pair per
     # workgroup by default, three with ct = 6): act equals bf16(silu(bf16 g) * bf16 u) of
     # the strip sums taken with the same K slicing (8 blocks per wave for K = 4096 by
-    # default, 16 with three pairs), to float32 libm rounding, and the float64 oracle
-    # within the bf16 bar
+    # default, 16 with three pairs), up to the hardware SiLU's rare bf16 neighbour
+    # (tests/_decode_case.silu_mul_check), and the float64 oracle within the bf16 bar
     import ctypes
     from oracle import decode_ref as D
-    from tests._decode_case import slots16
+    from tests._decode_case import silu_mul_check, slots16
     lib = N.load()
     k = 4096
     case = synth.gptq_case(k=k, n=n, m=1, group=128, seed=123, with_ref=False)
@@ -854,13 +854,9 @@ def test_strip_norm_silu_epilogue(dev, n, ct, nb):
                         geom=dict(nb=nb)).cpu().numpy()
     j = np.arange(n // 2)
     gcol = (j // 32) * 64 + j % 32
-    rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
-    g = rb(y[gcol])
-    sg = rb(g / (np.float32(1) + np.exp(-g)))
-    ref_bits = f32_to_bf16_bits((sg * rb(y[gcol + 32])).astype(np.float32))
     got_bits = act.view(torch.int16).cpu().numpy().view(np.uint16)
-    ulps = np.abs(got_bits.astype(np.int32) - ref_bits.astype(np.int32))
-    assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99
+    same, near = silu_mul_check(got_bits, y[gcol], y[gcol + 32])
+    assert near and same > 0.99, same
     x = D.rms_norm(hf, wf)
     y64 = G.gptq_gemm(x[None], case["qweight"], case["qzeros"], case["scales"], case["g_idx"], 128)[0]
     g64, u64 = y64[gcol], y64[gcol + 32]

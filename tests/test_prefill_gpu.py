@@ -122,13 +122,10 @@ def test_prefill_silu_mul_epilogue(dev, split):
     assert act.shape == (50, 256)
     j = np.arange(256)
     gcol = (j // 32) * 64 + j % 32
-    rb = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))  # noqa: E731
-    g = rb(y[:, gcol])
-    sg = rb(g / (np.float32(1) + np.exp(-g)))
-    ref = f32_to_bf16_bits((sg * rb(y[:, gcol + 32])).astype(np.float32))
+    from tests._decode_case import silu_mul_check
     got = act.view(torch.int16).cpu().numpy().view(np.uint16)
-    ulps = np.abs(got.astype(np.int32) - ref.astype(np.int32))
-    assert ulps.max() <= 1 and np.mean(ulps == 0) > 0.99
+    same, near = silu_mul_check(got, y[:, gcol], y[:, gcol + 32])
+    assert near and same > 0.99, same
 
 
 # ---------------------------------------------------------------- prompt-row kernels
