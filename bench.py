@@ -655,6 +655,49 @@ def moss_records(torch, cfg, dev, keep, group, seed=1234):
     return layers, state
 
 
+def moss_generation_rates(torch, dec, prompt_rows, steps: int) -> dict:
+    """Whole generation steps per second (step + sampling + state machine) from an audio
+    continuation prompt (the last text id AUDIO_START): the device generator
+    (moss_tts_lite_amd.generate.generate_fast: sampling on the device, one host read per step
+    behind the next step's backbone), and the reference's read pattern (generate_fast,
+    moss_tts_lite/fast.py:487-539: every sampled token read to the host with int(), the next
+    id row copied back) over the same decoder and the same device sampling ops."""
+    from moss_tts_lite_amd import generate as G
+
+    rows = prompt_rows.clone()
+    rows[-1, 0] = G.AUDIO_START_TOKEN_ID
+    prompt = {"input_ids": rows[None]}
+    kw = dict(max_new_tokens=steps, seed=1234, watchdog=False)
+    G.generate_fast(dec, prompt, **dict(kw, max_new_tokens=8))          # warm-up
+    st = {}
+    res = G.generate_fast(dec, prompt, stats=st, **kw)
+    out = {"steps": res.n_steps, "device_sampling_steps_per_s": round(res.n_steps / st["wall_s"], 1),
+           "host_wait_ms_per_step": round(st["host_wait_s"] * 1e3 / res.n_steps, 3)}
+    # the reference's pattern: the same step and sampling ops, then a host read of every token
+    dev = dec.dev
+    n_vq = dec.m.cfg.n_vq
+    dec.prefill(rows)
+    torch.cuda.synchronize()
+    pos, al = rows.shape[0], 1
+    t0 = time.perf_counter()
+    for t in range(steps):
+        if t:
+            dec.step(None, pos, audio2=True)
+            pos += 1
+        two = dec.two / 1.5
+        text = G.sample_rows(two.view(1, -1), top_k=50, top_p=1.0)[0]
+        nxt = [G.AUDIO_GEN_SLOT_TOKEN_ID if int(text) == 0 else G.AUDIO_DELAY_SLOT_TOKEN_ID]
+        la = dec.la / 1.7
+        act = min(al, n_vq)
+        toks = G.sample_rows(la[:act].clone(), top_k=25, top_p=0.8)
+        nxt += [int(toks[j]) for j in range(act)] + [G.AUDIO_PAD_CODE] * (n_vq - act)
+        dec.ids.copy_(torch.tensor(nxt, dtype=torch.int64).to(dev))
+        al += 1
+    torch.cuda.synchronize()
+    out["host_reads_steps_per_s"] = round(steps / (time.perf_counter() - t0), 1)
+    return out
+
+
 def bench_moss(args, torch):
     """The MOSS-TTS decode step at the reference's shape (moss_tts_lite/model.py:9-24: Qwen3-8B
     backbone, text vocabulary 155648, 32 audio codebooks of 1025) on the reference's own
@@ -723,6 +766,7 @@ def bench_moss(args, torch):
         res[audio2] = e0.elapsed_time(e1) / args.steps
     ms_step = res[False]
     launches = sum(len(p) for p in dec._layers) + len(dec._embed) + len(dec._final_variant(False))
+    gen_rates = moss_generation_rates(torch, dec, rows, steps=128)
     return dict(
         value=round(1000.0 / ms_step, 2), unit="steps/s", ms_per_step=ms_step, steps=args.steps,
         dtype="int4 (packed, qsz) weights, bf16 activations, fp32 accumulate",
@@ -734,7 +778,8 @@ def bench_moss(args, torch):
                 "ms_per_step_audio2": round(res[True], 4),
                 "steps_per_s_audio2": round(1000.0 / res[True], 2),
                 "launches_per_step": launches, "setup_s": round(setup_s, 1),
-                "reference_a10g_steps_per_s": {"w1": 81.5, "w2": 78.6}[args.preset]},
+                "reference_a10g_steps_per_s": {"w1": 81.5, "w2": 78.6}[args.preset],
+                "generation": gen_rates},
         roofline=None,
     )
 

@@ -770,6 +770,7 @@ class FastMossDecoder(FastDecoder):
         if model.cfg.n_vq < 1:
             raise ValueError("FastMossDecoder needs a MOSS-shaped backbone (cfg.n_vq > 0)")
         self.graphs: dict | None = None
+        self.part_graphs: dict | None = None
         super().__init__(model, plan, strip_geometry=strip_geometry)
 
     def _alloc_io(self) -> None:
@@ -789,7 +790,8 @@ class FastMossDecoder(FastDecoder):
     def _final_plan(self) -> list:
         return self._final_variant(audio2=False)
 
-    def _final_variant(self, audio2: bool) -> list:
+    def _heads_variant(self, audio2: bool) -> list:
+        """The output heads on ``h_final``: text (or 2-way) logits and the audio logits."""
         m, cfg = self.m, self.m.cfg
         hf = self.h_final.data_ptr()
         audio = ("mtl_bf16_gemv", (hf, m.head_audio.data_ptr(), cfg.n_vq * cfg.audio_vocab,
@@ -801,7 +803,10 @@ class FastMossDecoder(FastDecoder):
         else:
             first = ("mtl_bf16_gemv", (hf, m.head.data_ptr(), cfg.vocab, cfg.hidden,
                                        self.lt.data_ptr(), 0, 0))
-        return self._final_norm_plan() + [first, audio]
+        return [first, audio]
+
+    def _final_variant(self, audio2: bool) -> list:
+        return self._final_norm_plan() + self._heads_variant(audio2)
 
     def run_step(self, audio2: bool = False) -> None:
         """One whole step, eager, at the position in ``pos`` (not advanced)."""
@@ -831,6 +836,36 @@ class FastMossDecoder(FastDecoder):
         torch.cuda.synchronize(self.dev)
         self.ids.copy_(saved_ids)
         self.pos.copy_(saved_pos)
+
+    def capture_parts(self) -> None:
+        """Capture the step in two parts, for callers that decide the head variant after
+        the backbone has started: the backbone (embedding, layers, final norm into
+        ``h_final``) and one graph per head variant on ``h_final``."""
+        if getattr(self, "part_graphs", None) is not None:
+            return
+        self.capture()
+        saved_ids, saved_pos = self.ids.clone(), self.pos.clone()
+        self.part_graphs = {}
+        backbone = self._embed + [op for plan in self._layers for op in plan] + \
+            self._final_norm_plan()
+        for key, plan in (("backbone", backbone), (False, self._heads_variant(False)),
+                          (True, self._heads_variant(True))):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._run(plan)
+            self.part_graphs[key] = g
+        torch.cuda.synchronize(self.dev)
+        self.ids.copy_(saved_ids)
+        self.pos.copy_(saved_pos)
+
+    def replay_backbone(self, pos: int) -> None:
+        """The backbone of one step for the ids row already in ``ids``, at ``pos``."""
+        self.pos.fill_(_check_pos(pos, self.m.cfg.max_seq))
+        self.part_graphs["backbone"].replay()
+
+    def replay_heads(self, audio2: bool = False) -> None:
+        """The output heads on ``h_final`` (text + audio, or 2-way + audio)."""
+        self.part_graphs[bool(audio2)].replay()
 
     def step(self, row: torch.Tensor | None, pos: int, audio2: bool = False):
         """Replay one decode step for ``row`` ([1 + n_vq] ids) at cache position ``pos``.

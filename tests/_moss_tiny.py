@@ -158,18 +158,20 @@ def oracle_weights(m: dict) -> dict:
             "head_2way": head[list(TWO_WAY)], "layers": layers}
 
 
-def backbone_config(max_seq: int = 64, act_order: bool = True):
+def backbone_config(max_seq: int = 64, act_order: bool = True, embed_rows: int = EMBED_ROWS):
     from moss_tts_lite_amd.model import BackboneConfig
     return BackboneConfig(hidden=HIDDEN, n_heads=N_HEADS, n_kv_heads=N_KV, head_dim=HEAD_DIM,
                           intermediate=INTER, n_layers=N_LAYERS, vocab=TEXT_VOCAB,
                           group_size=GROUP, act_order=act_order, max_seq=max_seq, n_vq=N_VQ,
                           audio_vocab=AUDIO_VOCAB, audio_pad_code=AUDIO_PAD, two_way_ids=TWO_WAY,
-                          embed_vocab=EMBED_ROWS)
+                          embed_vocab=embed_rows)
 
 
-def device_backbone(m: dict, dev, max_seq: int = 64):
+def device_backbone(m: dict, dev, max_seq: int = 64, full_text_embedding: bool = False):
     """The int4 device backbone of the same model (AutoGPTQ buffers, act-order): q|k|v
-    fused along N, gate|up in the 32-column interleave."""
+    fused along N, gate|up in the 32-column interleave.  ``full_text_embedding``: a text
+    embedding of all TEXT_VOCAB rows (seeded on the device) instead of the model's 8192, so
+    that the special tokens (AUDIO_START and the slots) can be fed back as ids."""
     import torch
 
     from moss_tts_lite_amd.gptq import GPTQLinear, fuse_gptq_linears, interleave_gate_up
@@ -198,7 +200,12 @@ def device_backbone(m: dict, dev, max_seq: int = 64):
     w = {"embed_tokens": bf(m["embed_tokens"]), "final_norm": bf(m["final_norm"]),
          "head": bf(m["head"]), "layers": layers,
          "emb_ext": [bf(e) for e in m["emb_ext"]], "head_audio": bf(m["head_audio"])}
-    return Int4Backbone(backbone_config(max_seq, m["act_order"]), w, dev)
+    rows = EMBED_ROWS
+    if full_text_embedding:
+        g = torch.Generator(device=dev).manual_seed(SEED)
+        w["embed_tokens"] = torch.randn(TEXT_VOCAB, HIDDEN, generator=g, device=dev).bfloat16()
+        rows = TEXT_VOCAB
+    return Int4Backbone(backbone_config(max_seq, m["act_order"], rows), w, dev)
 
 
 def dispatch_backbone(m: dict, dev, max_seq: int = 64, keep=()):
