@@ -766,7 +766,7 @@ def bench_moss(args, torch):
         res[audio2] = e0.elapsed_time(e1) / args.steps
     ms_step = res[False]
     launches = sum(len(p) for p in dec._layers) + len(dec._embed) + len(dec._final_variant(False))
-    gen_rates = moss_generation_rates(torch, dec, rows, steps=128)
+    gen_rates = moss_generation_rates(torch, dec, rows, steps=384)
     return dict(
         value=round(1000.0 / ms_step, 2), unit="steps/s", ms_per_step=ms_step, steps=args.steps,
         dtype="int4 (packed, qsz) weights, bf16 activations, fp32 accumulate",

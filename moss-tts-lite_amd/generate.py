@@ -119,6 +119,12 @@ def sample_rows(logits: torch.Tensor, *, top_k=None, top_p=None, do_sample=True,
 
 
 # ---------------------------------------------------------------------------- generation
+def _set(x: torch.Tensor, col: int) -> None:
+    """``x[..., col] = -inf`` as a device fill (an indexed assignment of a Python number
+    stages the number on the host, which graph capture refuses)."""
+    x[..., col:col + 1].fill_(float("-inf"))
+
+
 @dataclasses.dataclass
 class _State:
     """The delay-pattern state machine of fast.py:423-450 (host integers)."""
@@ -134,7 +140,9 @@ class _State:
 
 
 class _Sampler:
-    """Device buffers and the per-step sampling stage."""
+    """Device buffers and the per-step sampling stage.  The ops are issued eagerly: the host
+    runs a step ahead of the GPU, so their launch cost is hidden (capturing each stage shape
+    as a graph measured no faster: 410 against 417 generated steps/s)."""
 
     def __init__(self, dec, max_steps: int, prompt: torch.Tensor, penalty: float):
         dev = dec.dev
@@ -161,31 +169,39 @@ class _Sampler:
               p: dict) -> None:
         """Queue step t's sampling: the next id row into ``dec.ids`` and ``rows[t]``, and the
         two numbers the host reads into the pinned buffer."""
+        self._ops(t, st, forced_text, sampling_text, smask, p)
+        self.rows[t].copy_(self.dec.ids)
+        self.host.copy_(self.decision, non_blocking=True)
+        self.done.record()
+
+    def _ops(self, t: int, st: _State, forced_text: int, sampling_text: bool, smask: list,
+             p: dict) -> None:
         dec = self.dec
         ids = dec.ids
         if sampling_text:
             if st.is_audio and not p["text_do_sample"]:
                 two = dec.two / p["text_temperature"]
                 if t == 0:
-                    two[1] = float("-inf")
+                    _set(two, 1)
                 pick = torch.argmax(two)
                 tok = torch.where(pick == 0, AUDIO_GEN_SLOT_TOKEN_ID, AUDIO_DELAY_SLOT_TOKEN_ID)
             elif st.is_audio:
                 buf = self.lt_buf
                 buf.fill_(float("-inf"))
-                buf[AUDIO_GEN_SLOT_TOKEN_ID] = dec.two[0] / p["text_temperature"]
-                buf[AUDIO_DELAY_SLOT_TOKEN_ID] = dec.two[1] / p["text_temperature"]
+                g, d = AUDIO_GEN_SLOT_TOKEN_ID, AUDIO_DELAY_SLOT_TOKEN_ID
+                buf[g:g + 1].copy_(dec.two[0:1] / p["text_temperature"])
+                buf[d:d + 1].copy_(dec.two[1:2] / p["text_temperature"])
                 if t == 0:
-                    buf[AUDIO_DELAY_SLOT_TOKEN_ID] = float("-inf")
+                    _set(buf, d)
                 tok = sample_rows(buf.view(1, -1), top_p=p["text_top_p"], top_k=p["text_top_k"],
                                   do_sample=True)[0]
             else:
                 lt = dec.lt / p["text_temperature"]
                 lt = lt.index_fill(0, self.pre_exclude0, float("-inf"))
                 if t == 0:
-                    lt[AUDIO_DELAY_SLOT_TOKEN_ID] = float("-inf")
+                    _set(lt, AUDIO_DELAY_SLOT_TOKEN_ID)
                 if t <= N_VQ:
-                    lt[IM_END_TOKEN_ID] = float("-inf")
+                    _set(lt, IM_END_TOKEN_ID)
                 tok = sample_rows(lt.view(1, -1), top_p=p["text_top_p"], top_k=p["text_top_k"],
                                   do_sample=p["text_do_sample"])[0]
             ids[0].copy_(tok)
@@ -198,22 +214,19 @@ class _Sampler:
                       do_sample=p["audio_do_sample"], penalty=self.penalty)
             if smask[0]:
                 ch0 = la[0].view(1, -1)
-                ch0[..., AUDIO_PAD_CODE] = float("-inf")
+                _set(ch0, AUDIO_PAD_CODE)
                 ids[1].copy_(sample_rows(ch0, seen=self.seen0, **kw)[0])
             rest = [j for j in range(1, N_VQ) if smask[j]]
             if rest:   # a contiguous run of channels (the delay pattern's window)
                 j0, j1 = rest[0], rest[-1] + 1
                 assert j1 - j0 == len(rest)
                 rl = la[j0:j1].clone()
-                rl[..., AUDIO_PAD_CODE] = float("-inf")
+                _set(rl, AUDIO_PAD_CODE)
                 ids[1 + j0:1 + j1].copy_(sample_rows(rl, seen=self.seen_rest, **kw))
-        if self.seen0 is not None:
-            self.seen0[ids[1:2]] = True
-            self.seen_rest[ids[2:]] = True
-        self.rows[t].copy_(ids)
+        if self.seen0 is not None:            # scatter: no host-side step, so capturable
+            self.seen0.scatter_(0, ids[1:2], True)
+            self.seen_rest.scatter_(0, ids[2:], True)
         self.decision.copy_(ids[0:2])
-        self.host.copy_(self.decision, non_blocking=True)
-        self.done.record()
 
     def read(self) -> tuple[int, int]:
         self.done.synchronize()
