@@ -45,6 +45,7 @@ Five launch plans produce the same step:
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -86,6 +87,17 @@ def _check_pos(pos: int, max_seq: int) -> int:
     if not 0 <= pos < max_seq:
         raise ValueError(f"position {pos} is outside the KV cache of {max_seq} positions")
     return pos
+
+
+@contextlib.contextmanager
+def _capturing(g: torch.cuda.CUDAGraph):
+    """``torch.cuda.graph(g)`` with inference mode off. A capture registers the default
+    CUDA generator's graph state, whose tensors torch creates on first use and updates in
+    place at every later capture: created under inference mode (generation runs there, as
+    the reference's does, fast.py:342), they would refuse a later capture outside it. The
+    captured work is library launches only, so the mode changes nothing in the graph."""
+    with torch.inference_mode(False), torch.cuda.graph(g):
+        yield
 
 
 class FastDecoder:
@@ -570,7 +582,7 @@ class FastDecoder:
         torch.cuda.current_stream(self.dev).wait_stream(s)
         torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with _capturing(g):
             self.run_step()
         torch.cuda.synchronize(self.dev)
         self.ids.copy_(saved_ids)
@@ -830,7 +842,7 @@ class FastMossDecoder(FastDecoder):
         self.graphs = {}
         for audio2 in (False, True):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with _capturing(g):
                 self.run_step(audio2)
             self.graphs[audio2] = g
         torch.cuda.synchronize(self.dev)
@@ -851,7 +863,7 @@ class FastMossDecoder(FastDecoder):
         for key, plan in (("backbone", backbone), (False, self._heads_variant(False)),
                           (True, self._heads_variant(True))):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            with _capturing(g):
                 self._run(plan)
             self.part_graphs[key] = g
         torch.cuda.synchronize(self.dev)

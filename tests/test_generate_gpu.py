@@ -97,3 +97,21 @@ def test_generate_fast_matches_reference_loop(dev, decoder, case, monkeypatch):
     assert res.n_steps == len(ref_text)
     if case == "watchdog":
         assert ref_reason == "silence" and res.watchdog_triggered
+
+
+def test_capture_outside_inference_mode_after_generation(dev):
+    # generation captures its graphs under inference mode; a decoder captured afterwards
+    # outside it must still capture and replay (the default generator's graph state is
+    # shared by every capture of the process)
+    from moss_tts_lite_amd.fast import FastMossDecoder
+    model = T.device_backbone(T.generate(T.SEED, True), dev, max_seq=64, full_text_embedding=True)
+    first = FastMossDecoder(model)
+    GEN.generate_fast(first, {"input_ids": _prompt("audio")}, max_new_tokens=4, seed=5)
+    second = FastMossDecoder(model)
+    assert not torch.is_inference_mode_enabled()
+    second.prefill(_prompt("audio")[0])
+    second.capture()
+    lt, la, _, _ = second.step(None, 8, audio2=True)
+    torch.cuda.synchronize()
+    pad = GEN.AUDIO_PAD_CODE                  # the heads' pad code is -inf by design
+    assert torch.isfinite(la[:, :pad].float()).all() and bool((la[:, pad] == float("-inf")).all())
