@@ -11,6 +11,10 @@ Workloads
           = the four GEMVs of one layer.  Weight copies are rotated so that more
           than 640 MB of distinct weights stream per cycle (MI355X's 256 MB
           Infinity Cache cannot serve repeats).
+  skinny  the skinny-batch int4 GEMM on gate_up 4096x24576 and down 12288x4096 (group 128,
+          no act-order) at M = 1, 2, 4, 8, 16 rows: the full-K strip GEMM and the split-K
+          GEMM, mean us per launch over rotated weight copies (gate_up is also part of the
+          gemv workload's line).
 Prints ONE JSON line (rank 0).
 """
 from __future__ import annotations
@@ -77,15 +81,22 @@ def bench_gemv(args, torch, pkg):
             qw, qz, sc, g_idx = make_gptq_weights(torch, dev, k, n, GROUP, seed=1234 + 97 * c + k + n)
             qws, perm = ops.actorder_prepare(qw, g_idx, GROUP)
             del qw
-            ws.append((qws, qz, sc, perm))
+            ws.append((qws, qz, sc, perm, ops.strip_weights(qws)))
         x = torch.randn(1, k, device=dev, generator=torch.Generator(device=dev).manual_seed(7)).bfloat16()
         y = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
         ops.reserve_workspace(dev, ops.gemm_workspace_bytes(1, k, n, GROUP))
         shapes.append(dict(name=name, k=k, n=n, copies=ws, x=x, y=y, bytes=per_copy))
     torch.cuda.synchronize()
 
+    # The GPTQ module's M = 1 route (GPTQLinear.forward): the skinny strip GEMM over the
+    # strip copy of the group-sorted weight, x gathered through the act-order index while
+    # staging; the split-K GEMM over the AutoGPTQ layout is timed beside it.
     def launch(s, i):
-        qws, qz, sc, perm = s["copies"][i % len(s["copies"])]
+        qws, qz, sc, perm, qss = s["copies"][i % len(s["copies"])]
+        ops.strip_rows_gemm(s["x"], qss, qz, sc, s["n"], GROUP, out=s["y"], perm=perm)
+
+    def launch_split_k(s, i):
+        qws, qz, sc, perm, qss = s["copies"][i % len(s["copies"])]
         ops.w4_gemm(s["x"], qws, N.META_GPTQ, sc, qz, perm, s["n"], GROUP, out=s["y"])
 
     for i in range(args.warmup):
@@ -125,8 +136,7 @@ def bench_gemv(args, torch, pkg):
 
     # Per-kernel durations: event pairs around single launches on the launch stream,
     # queued behind a GPU spin so the host never starves the queue.
-    per = {}
-    for s in shapes:
+    def event_us(s, fn):
         nrep = max(20, 4 * len(s["copies"]))
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(nrep)]
@@ -134,14 +144,20 @@ def bench_gemv(args, torch, pkg):
         torch.cuda._sleep(int(2e8))
         for i, (a, b) in enumerate(evs):
             a.record()
-            launch(s, i)
+            fn(s, i)
             b.record()
         torch.cuda.synchronize()
-        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+        return sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+
+    per = {}
+    for s in shapes:
+        us = event_us(s, launch)
+        sk = event_us(s, launch_split_k)
         mean_us = sum(us) / len(us)
         per[s["name"]] = dict(us=round(mean_us, 3), median_us=round(us[len(us) // 2], 3),
                               gbs=round(s["bytes"] / mean_us / 1e3, 1),
                               frac=round(s["bytes"] / mean_us / 1e3 / HBM_PEAK_GBS, 4),
+                              split_k_us=round(sum(sk) / len(sk), 3),
                               copies=len(s["copies"]))
     skinny = bench_skinny(args, torch, dev)
     step_bytes = sum(s["bytes"] for s in shapes)
@@ -151,24 +167,25 @@ def bench_gemv(args, torch, pkg):
         steps=steps,
         dtype="int4 weights, bf16 x, fp32 accumulate",
         config={"workload": "int4 GEMV sweep M=1 act-order g128: qkv 4096x6144, o 4096x4096, "
-                            "gate_up 4096x24576, down 12288x4096 (one step = one layer's 4 GEMVs)",
+                            "gate_up 4096x24576, down 12288x4096 (one step = one layer's 4 GEMVs) "
+                            "on the GPTQ module's M=1 route (skinny strip GEMM, act-order "
+                            "gather while staging; split_k_us: the split-K GEMM)",
                 "per_kernel": per, "step_bytes": step_bytes,
                 "skinny_gate_up": skinny},
         roofline={"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": gu["frac"], "traffic": None,
-                  "kernel": "w4_gemm_kernel<1,16,GPTQ,perm> gate_up 4096x24576 M=1"},
+                  "kernel": "w4_rows_kernel<g128, GPTQ> gate_up 4096x24576 M=1, act-order gather"},
     )
 
 
-def bench_skinny(args, torch, dev):
-    """Skinny-batch int4 GEMM on the gate_up shape (K 4096, N 24576, group 128, no
+def bench_skinny(args, torch, dev, k=4096, n=24576):
+    """Skinny-batch int4 GEMM on one shape (default gate_up: K 4096, N 24576; group 128, no
     act-order) at M = 1, 2, 4, 8, 16 bf16 rows, one launch per call, weight copies rotated
     past the Infinity Cache, mean us per launch: the full-K strip GEMM (no partials) and the
     split-K GEMM (partials reduced by a second kernel)."""
     from moss_tts_lite_amd import _native as N
     from moss_tts_lite_amd import ops
 
-    k, n = 4096, 24576
     per_copy = algo_bytes(1, k, n, GROUP, False)
     copies = []
     for c in range(max(2, math.ceil(640e6 / per_copy))):
@@ -790,7 +807,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "kernels", "prefill", "int4-op", "moss"])
+                    choices=["decode", "gemv", "skinny", "kernels", "prefill", "int4-op", "moss"])
     ap.add_argument("--preset", default="w2", choices=sorted(MOSS_PRESETS),
                     help="the reference's GPTQ preset: group size and bf16 keeps (moss workload)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -819,6 +836,12 @@ def main():
     if args.workload == "kernels":
         args.steps = 72 if args.steps is None else args.steps
         bench_kernels(args, torch)
+        return
+    if args.workload == "skinny":
+        dev = torch.device("cuda:0")
+        print(json.dumps({"workload": "skinny", "group": GROUP,
+                          "gate_up 4096x24576": bench_skinny(args, torch, dev),
+                          "down 12288x4096": bench_skinny(args, torch, dev, 12288, 4096)}))
         return
     if args.workload == "int4-op":
         return bench_int4_op(args, torch)

@@ -148,9 +148,10 @@ int mtl_gptq_actorder_prepare(const int32_t* qweight, const int32_t* g_idx,
  *   y       bf16 [M, N], 8-byte aligned
  *   workspace  NULL, or mtl_int4pack_mm_workspace_bytes(M, K, N) bytes: lets a launch
  *           with M > 1 split K over workgroups (results then differ by fp32 rounding)
- * M = 1 runs the full-K strip GEMV; M > 1 the prompt-length GEMM (N % 128 == 0), else
- * one strip GEMV per row.  K % 256 == 0, K % g == 0, N % 16 == 0 (torch asks N % 8 only);
- * the strip GEMV serves K <= 16384.
+ * M = 1 runs the full-K strip GEMV (K <= 16384); 2 <= M <= 16 the skinny strip GEMM
+ * (mtl_w4_gemm_strip_rows_ex) where M * 1024 <= 1.5 N, more rows the prompt-length GEMM
+ * (N % 128 == 0; otherwise the skinny GEMM 16 rows at a time).  K % 256 == 0, K % g == 0,
+ * N % 16 == 0 (torch asks N % 8 only).
  */
 int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
@@ -228,14 +229,34 @@ int mtl_w4_strip_meta(const void* scales, const int32_t* qzeros, int64_t K, int6
  *                 caller orders x's channels as the weight's rows)
  *   scales/qzeros as mtl_gptq_gemm; zero_offset as there
  *   y             [M, N] bf16 or f32 (out_dtype), rows ldy elements apart
- * K % 256 == 0, K <= 4096 (16 rows of x in LDS), N % 16 == 0; group_size 128 or 256
- * (32 and 64 return MTL_ERR_UNSUPPORTED: the split-K mtl_gptq_gemm serves them).
+ * K % 256 == 0, N % 16 == 0, N * K / 2 < 2^31; group_size 32, 64, 128 or 256.  x is staged
+ * in LDS in phases of K sized for 16 rows (all of K at once up to K = 4096), the same at
+ * every M, so a row's result does not depend on the rows launched with it.
  */
 int mtl_w4_gemm_strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K,
                            const int32_t* strip_weight, const void* scales,
                            const int32_t* qzeros, int64_t N, int32_t group_size,
                            int32_t zero_offset, void* y, int64_t ldy, int32_t out_dtype,
                            void* stream);
+
+/*
+ * mtl_w4_gemm_strip_rows for both metadata contracts and act-order inputs.  Replaces
+ * torch._weight_int4pack_mm at 2 <= M <= 16 on the reference's own (packed, qsz) records
+ * (moss_tts_lite/fast.py:107-121 at prompt rows, gptq.py:577-585), and serves the GPTQ
+ * module's forward at M <= 16 with its act-order gather.
+ *   perm         NULL, or int32 [K] (16-byte aligned): input row k of the weight multiplies
+ *                x channel perm[k] (the act-order index of mtl_actorder_prepare; GPTQ
+ *                metadata only)
+ *   meta_format  MTL_META_GPTQ (meta = scales fp16 [K/g, N], qzeros int32 [K/g, N/8]) or
+ *                MTL_META_QSZ (meta = qsz bf16 [K/g, N, 2], qzeros NULL, zero_offset 0)
+ *   other arguments as mtl_w4_gemm_strip_rows; no K limit beyond N * K / 2 < 2^31 (K
+ *   runs in phases whose x fits the LDS).
+ */
+int mtl_w4_gemm_strip_rows_ex(const void* x, int64_t M, int64_t ldx, int64_t K,
+                              const int32_t* perm, const int32_t* strip_weight, const void* meta,
+                              const int32_t* qzeros, int64_t N, int32_t group_size,
+                              int32_t zero_offset, int32_t meta_format, void* y, int64_t ldy,
+                              int32_t out_dtype, void* stream);
 
 /*
  * Prompt-length int4 GEMM over the strip layout: y[M, N] = x[M, K] @ dequant(W) for any

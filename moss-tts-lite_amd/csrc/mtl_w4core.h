@@ -186,6 +186,19 @@ int strip_blocks_per_wave(int64_t K, int ct, int group);
 // Launch the strip GEMV; shapes, pointers and alignment are checked by the caller.
 int strip_launch(const StripArgs& a, hipStream_t stream);
 
+// The skinny-batch strip GEMM (mtl_w4rows.hip) for 1 <= M <= 16 rows: fmt is STRIP_META_*,
+// perm (GPTQ metadata only) gathers x's channels; checks shapes and alignment itself.
+int strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K, const int32_t* perm,
+               const int32_t* strip_weight, const void* meta, const int32_t* qzeros, int64_t N,
+               int32_t group_size, int32_t zero_offset, int fmt, void* y, int64_t ldy,
+               int32_t out_dtype, void* stream);
+
+// Whether the skinny-batch strip GEMM pays at M rows over N columns: every workgroup (one
+// per CU) stages all M rows of x, 2 M K bytes against the N K / 512 bytes of weights a CU
+// streams, and measured on MI355X it stays ahead while M * 1024 <= 1.5 N (every M <= 16 on
+// a 24576-column projection, M <= 6 at 4096 columns).
+inline bool strip_rows_pays(int64_t M, int64_t N) { return M <= 16 && M * 1024 * 2 <= 3 * N; }
+
 // The residual add of the decode step (fast.py:168-171) on 4 consecutive columns:
 // h = bf16(bf16(acc) + h); returns their sum of squares (fixed fma order).
 __device__ __forceinline__ float residual4(const float acc[4], float hv[4]) {

@@ -340,11 +340,11 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   const bool active = (MR == 1 ? wave == 0 : true) && t < kTileN;
 
   // 7. Split-K.  Every workgroup publishes its fp32 partial tile.  With an in-kernel
-  //    reduction the partials travel as relaxed agent-scope atomics (coherent across
-  //    XCDs without a whole-L2 writeback), a per-tile counter names the last workgroup,
-  //    and that one sums all splits in split order (one column per thread, up to 32
-  //    loads in flight) and resets the counter.  Otherwise w4_reduce_kernel (or a
-  //    fused consumer) sums them.
+  //    reduction (the residual GEMV with published sums of squares, whose epilogue the
+  //    reduce kernel lacks) the partials travel as agent-scope atomic stores, a per-tile
+  //    release count names the last workgroup, which acquires and sums all splits in
+  //    split order (one column per thread, up to 32 loads in flight) and resets the
+  //    counter.  Otherwise w4_reduce_kernel (or a fused consumer) sums them.
   if (a.splits > 1 || a.partials_only) {
     float* pbase = a.partial + (size_t)split * M * N + ecol;
     if (!a.inkernel_reduce || a.partials_only) {
@@ -698,7 +698,11 @@ static int w4_gemm(const void* x, int64_t M, int64_t K, const int32_t* qweight, 
   a.splits = p.splits;
   a.epilogue = epilogue;
   a.out_f32 = out_dtype == MTL_OUT_F32;
-  a.inkernel_reduce = 1;   // split-K tiles reduced by their last workgroup
+  // Split-K partials are summed by w4_reduce_kernel, a second launch: the kernel boundary
+  // makes them visible without an agent-scope release (an L2 write-back) in each of the
+  // hundreds of workgroups, which made the last-workgroup reduction 2.4x slower at M = 1 on
+  // gate|up (34.6 against 14.4 us) and 2x at M = 16 (46.0 against 22.4 us).
+  a.inkernel_reduce = 0;
   if (p.splits > 1) {
     const int64_t need = kCounterBytes + (int64_t)p.splits * M * N * 4;
     if (!workspace || ws_bytes < need) return MTL_ERR_WORKSPACE;

@@ -530,12 +530,19 @@ int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,
                       (hipStream_t)stream);
 }
 
-int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-  return M > 1 ? mtl_w4_gemm_prefill_workspace_bytes(M, K, N) : 0;
+// Whether mtl_int4pack_mm runs M > 1 rows on the prompt-length GEMM (else on the skinny
+// strip GEMM, in 16-row launches when N is not a multiple of its 128-column tiles).
+static bool int4pack_prefill(int64_t M, int64_t N) {
+  return N % kPfCols == 0 && !strip_rows_pays(M, N);
 }
 
-// The drop-in for torch._weight_int4pack_mm: M = 1 on the full-K strip GEMV, more rows on
-// the prompt-length GEMM (or, when N is not a multiple of 128, one strip GEMV per row).
+int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+  return M > 1 && int4pack_prefill(M, N) ? mtl_w4_gemm_prefill_workspace_bytes(M, K, N) : 0;
+}
+
+// The drop-in for torch._weight_int4pack_mm: M = 1 on the full-K strip GEMV, 2 to 16 rows on
+// the skinny strip GEMM where it pays (strip_rows_pays), more on the prompt-length GEMM (or,
+// when N is not a multiple of 128, the skinny GEMM 16 rows at a time).
 int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
                     int32_t group_size, const void* qsz, int64_t N, void* y, void* workspace,
                     int64_t ws_bytes, void* stream) {
@@ -563,15 +570,17 @@ int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
     sa.y16 = static_cast<uint16_t*>(y);
     return strip_launch(sa, st);
   }
-  if (N % kPfCols == 0)
+  if (int4pack_prefill(M, N))
     return prefill_gemm(x, M, K, K, packed, qsz, nullptr, N, group_size, 0, MTL_EPI_NONE,
                         MTL_OUT_BF16, y, N, static_cast<float*>(workspace), ws_bytes,
                         STRIP_META_QSZ, st);
-  if (!strip_ok) return MTL_ERR_UNSUPPORTED;
-  for (int64_t r = 0; r < M; ++r) {
-    sa.x = static_cast<const uint16_t*>(x) + r * K;
-    sa.y16 = static_cast<uint16_t*>(y) + r * N;
-    if (const int status = strip_launch(sa, st)) return status;
+  for (int64_t r0 = 0; r0 < M; r0 += 16) {
+    const int64_t rows = M - r0 < 16 ? M - r0 : 16;
+    if (const int status = strip_rows(static_cast<const uint16_t*>(x) + r0 * K, rows, K, K,
+                                      nullptr, packed, qsz, nullptr, N, group_size, 0,
+                                      STRIP_META_QSZ, static_cast<uint16_t*>(y) + r0 * N, N,
+                                      MTL_OUT_BF16, stream))
+      return status;
   }
   return MTL_OK;
 }

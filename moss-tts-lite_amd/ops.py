@@ -298,13 +298,45 @@ def strip_meta(scales: torch.Tensor, qzeros: torch.Tensor, group_size: int):
     return sc, qz
 
 
+def strip_rows_pays(m: int, n: int, gathered: bool = False) -> bool:
+    """Whether the skinny strip GEMM beats the split-K GEMM at ``m`` rows over ``n``
+    columns on MI355X: each workgroup (one per CU) stages all m rows of x against the
+    N K / 512 weight bytes a CU streams, so it pays while m * 1024 <= 1.5 n (every m <= 16
+    on gate|up's 24576 columns, m <= 6 on down's 4096); with the act-order gather (two
+    bytes per load) while m * 1536 <= n.  The C drop-in mtl_int4pack_mm uses the first
+    rule."""
+    if m < 1 or m > _MAX_M:
+        return False
+    return m * 1536 <= n if gathered else 2 * m * 1024 <= 3 * n
+
+
 def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.Tensor,
                     scales: torch.Tensor, n: int, group_size: int, zero_offset: int = 0,
                     out: torch.Tensor | None = None,
-                    out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """Skinny-batch GEMM over the strip layout (``mtl_w4_gemm_strip_rows``): ``x [M, K]``
-    bf16 with M <= 16 rows per launch (longer inputs run in 16-row chunks), ``K <= 4096``,
-    group 128 or 256; returns ``[M, n]``."""
+                    out_dtype: torch.dtype = torch.bfloat16,
+                    perm: torch.Tensor | None = None) -> torch.Tensor:
+    """Skinny-batch GEMM over the strip layout (``mtl_w4_gemm_strip_rows_ex``): ``x [M, K]``
+    bf16 with M <= 16 rows per launch (longer inputs run in 16-row chunks), AutoGPTQ
+    ``scales``/``qzeros``, group 32, 64, 128 or 256; ``perm`` (int32 [K], the act-order
+    index of :func:`actorder_prepare`) gathers x's channels into the weight's row order.
+    Returns ``[M, n]``."""
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != x.shape[-1]):
+        raise RuntimeError("perm must be int32 [K]")
+    return _strip_rows(x, strip_weight, scales, qzeros, n, group_size, zero_offset,
+                       N.META_GPTQ, perm, out, out_dtype)
+
+
+def strip_rows_qsz(x: torch.Tensor, packed: torch.Tensor, qsz: torch.Tensor, group_size: int,
+                   out: torch.Tensor | None = None,
+                   out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The skinny-batch strip GEMM on the reference's own records: ``packed`` from
+    :func:`convert_weight_to_int4pack` and ``qsz`` bf16 ``[K/g, N, 2]``; ``x [M, K]``."""
+    return _strip_rows(x, packed, qsz, None, qsz.shape[1], group_size, 0, N.META_QSZ, None,
+                       out, out_dtype)
+
+
+def _strip_rows(x, strip_weight, meta, qzeros, n, group_size, zero_offset, meta_format, perm,
+                out, out_dtype):
     x2 = _check_x(x, x.shape[-1])
     m, k = x2.shape
     if out is None:
@@ -314,10 +346,11 @@ def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.T
     stream = _stream(x2.device)
     for r0 in range(0, m, _MAX_M):
         r1 = min(m, r0 + _MAX_M)
-        N.check(lib.mtl_w4_gemm_strip_rows(
-            x2[r0:r1].data_ptr(), r1 - r0, k, k, strip_weight.data_ptr(), scales.data_ptr(),
-            qzeros.data_ptr(), n, group_size, zero_offset, out[r0:r1].data_ptr(), n, odt, stream),
-            "mtl_w4_gemm_strip_rows")
+        N.check(lib.mtl_w4_gemm_strip_rows_ex(
+            x2[r0:r1].data_ptr(), r1 - r0, k, k, _ptr(perm), strip_weight.data_ptr(),
+            meta.data_ptr(), _ptr(qzeros), n, group_size, zero_offset, meta_format,
+            out[r0:r1].data_ptr(), n, odt, stream),
+            "mtl_w4_gemm_strip_rows_ex")
     return out
 
 

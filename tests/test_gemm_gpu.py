@@ -215,7 +215,9 @@ def test_strip_rows_gate_up_skinny_batch(dev, m):
 
 
 @pytest.mark.parametrize("group,k,n,m", [(128, 1024, 528, 5), (256, 4096, 6144, 16),
-                                         (128, 768, 4096, 7), (256, 512, 96, 2)])
+                                         (128, 768, 4096, 7), (256, 512, 96, 2),
+                                         (32, 1024, 528, 5), (64, 2048, 1536, 16),
+                                         (32, 256, 64, 1), (64, 768, 4096, 3)])
 def test_strip_rows_shapes(dev, group, k, n, m):
     case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=False, seed=group + k + n + m)
     y = run_strip_rows(case, dev)
@@ -229,6 +231,86 @@ def test_strip_rows_shapes(dev, group, k, n, m):
     assert np.array_equal(y, run_strip_rows(case, dev))
     one = dict(case, m=1, x_bits=case["x_bits"][m - 1:m])
     assert np.array_equal(run_strip_rows(one, dev)[0], y[m - 1])
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_strip_rows_gate_up_small_groups(dev, group):
+    # g 32 / 64 on the gate|up projection at 16 rows: 4 / 2 groups per 1 KB block, and at
+    # g 32 x, its group sums and the slice tiles fill the 160 KB of LDS
+    cols = np.arange(0, 24576, 96)
+    case = synth.gptq_case(k=4096, n=24576, m=16, group=group, act_order=False,
+                           seed=group + 5, ref_cols=cols)
+    y = run_strip_rows(case, dev)
+    err = rel_l2(y[:, cols], case["y_ref"])
+    print(f"strip rows gate_up g{group} M=16 rel_l2={err:.2e}")
+    assert err < TOL_F32 and np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("group,k,n,m", [(128, 12288, 4096, 16), (32, 12288, 4096, 16),
+                                         (256, 8192, 1024, 9), (64, 6144, 512, 2),
+                                         (128, 12288, 1024, 1)])
+def test_strip_rows_k_phases(dev, group, k, n, m):
+    # K beyond what one LDS tile of x holds runs in phases (the down projection's 12288 at
+    # 16 rows: three of 4096); every row against float64, and each row of the batch equals
+    # the same row run alone (phases keep the summation order per row)
+    cols = np.arange(0, n, 7)
+    case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=False, seed=group + k + m,
+                           ref_cols=cols)
+    y = run_strip_rows(case, dev)
+    err = rel_l2(y[:, cols], case["y_ref"])
+    print(f"strip rows phases g{group} {k}x{n} M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32 and np.isfinite(y).all()
+    one = dict(case, m=1, x_bits=case["x_bits"][m - 1:m])
+    assert np.array_equal(run_strip_rows(one, dev)[0], y[m - 1])
+
+
+@pytest.mark.parametrize("group,k,n,m", [(128, 4096, 6144, 8), (32, 2048, 1024, 3),
+                                         (128, 12288, 4096, 4), (256, 4096, 512, 16)])
+def test_strip_rows_act_order(dev, group, k, n, m):
+    # act-order weights: the group-sorted copy in the strip layout, x gathered through the
+    # act-order index while staging; against float64 on the original (unsorted) weight
+    cols = np.arange(0, n, 5)
+    case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=True, seed=3 * group + k + m,
+                           ref_cols=cols)
+    qws, perm = ops.actorder_prepare(t_i32(case["qweight"], dev), t_i32(case["g_idx"], dev), group)
+    y = ops.strip_rows_gemm(t_bf16(case["x_bits"], dev), ops.strip_weights(qws),
+                            t_i32(case["qzeros"], dev), t_f16(case["scales"], dev), n, group,
+                            out_dtype=torch.float32, perm=perm)
+    err = rel_l2(y.cpu().numpy()[:, cols], case["y_ref"])
+    print(f"strip rows act-order g{group} {k}x{n} M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("group,k,n,m", [(128, 4096, 1024, 16), (32, 4096, 512, 5),
+                                         (64, 12288, 256, 16), (256, 2048, 768, 2)])
+def test_strip_rows_qsz(dev, group, k, n, m):
+    # the reference's (packed, qsz) records: the group adds s * (A - 136 X) + zero * X
+    case = synth.qsz_case(k=k, n=n, m=m, group=group, seed=group + m)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(case["prepacked"]).to(dev), 8)
+    y = ops.strip_rows_qsz(t_bf16(case["x_bits"], dev), packed, t_bf16(case["qsz"], dev), group,
+                           out_dtype=torch.float32)
+    err = rel_l2(y.cpu().numpy(), case["y_ref"])
+    print(f"strip rows qsz g{group} {k}x{n} M={m} rel_l2={err:.2e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("act_order", [False, True])
+@pytest.mark.parametrize("k,n", [(4096, 6144), (2048, 2048)])
+def test_gptq_linear_forward_routes(dev, act_order, k, n):
+    # the module's forward over 1..21 rows crosses from the skinny strip GEMM to the split-K
+    # GEMM (ops.strip_rows_pays); every row count against float64 of the original weight
+    from moss_tts_lite_amd.gptq import GPTQLinear
+    case = synth.gptq_case(k=k, n=n, m=21, group=128, act_order=act_order, seed=k + n + act_order)
+    lin = GPTQLinear.from_buffers(t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev),
+                                  t_f16(case["scales"], dev),
+                                  t_i32(case["g_idx"], dev) if act_order else None, 128)
+    x = t_bf16(case["x_bits"], dev)
+    routes = []
+    for m in (1, 2, 3, 4, 8, 16, 21):
+        routes.append(ops.strip_rows_pays(m, n, act_order))
+        y = lin(x[:m], out_dtype=torch.float32).cpu().numpy()
+        assert rel_l2(y, case["y_ref"][:m]) < TOL_F32, m
+    assert any(routes) and not all(routes)
 
 
 def test_strip_rows_matches_strip_gemv_at_m1(dev):
@@ -251,11 +333,18 @@ def test_strip_rows_validation(dev):
     call = lambda m, k, g, n=64: lib.mtl_w4_gemm_strip_rows(  # noqa: E731
         x.data_ptr(), m, 8192, k, w.data_ptr(), sc.data_ptr(), qz.data_ptr(), n, g, 0,
         y.data_ptr(), 64, N.OUT_F32, st)
-    assert call(4, 4096, 32) == N.MTL_ERR_UNSUPPORTED
+    assert call(4, 4096, 32) == 0                      # g 32 and 64 run here too
+    assert call(4, 8192, 128) == 0                     # K in phases
     assert call(4, 4096, 48) == N.MTL_ERR_GROUP
-    assert call(4, 8192, 128) == N.MTL_ERR_SHAPE       # 16 rows of x would not fit in LDS
     assert call(17, 4096, 128) == N.MTL_ERR_SHAPE
     assert call(4, 4096, 128, n=72) == N.MTL_ERR_SHAPE
+    assert call(4, 4096, 128, n=1 << 20) == N.MTL_ERR_SHAPE   # N * K / 2 reaches 2^31
+    ex = lambda fmt, perm, zo: lib.mtl_w4_gemm_strip_rows_ex(  # noqa: E731
+        x.data_ptr(), 4, 8192, 4096, perm, w.data_ptr(), sc.data_ptr(), qz.data_ptr(), 64, 128,
+        zo, fmt, y.data_ptr(), 64, N.OUT_F32, st)
+    assert ex(2, None, 0) == N.MTL_ERR_INVALID_ARG            # no such metadata format
+    assert ex(N.META_QSZ, None, 1) == N.MTL_ERR_INVALID_ARG   # qsz has no zero offset
+    assert ex(N.META_QSZ, w.data_ptr(), 0) == N.MTL_ERR_INVALID_ARG   # nor an act-order index
     torch.cuda.synchronize()
 
 
