@@ -583,7 +583,8 @@ def bench_int4_op(args, torch):
     the reference's int4 linear) and the ``mtl_int4pack_mm`` drop-in, M = 1, g = 128, on
     the four decode-step projections.  Each timing replays a graph of ``steps`` launches
     rotating over enough weight copies (>= 400 MB) that no launch reads from the 256 MB
-    Infinity Cache."""
+    Infinity Cache; eager calls are timed too (host and wall time per call), as the
+    reference's non-captured paths issue them."""
     sys.path.insert(0, ROOT)
     import __graft_entry__
     __graft_entry__.import_package()
@@ -628,6 +629,17 @@ def bench_int4_op(args, torch):
                 best = min(best, a.elapsed_time(b) * 1e3 / steps)
             res[label] = round(best, 3)
             del g
+            # eager calls: host time per call (the loop is enqueue-bound when it exceeds
+            # the GPU time) and wall time per call with the final synchronize
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(200):
+                fn(ws[i % copies])
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            res[label + "_eager_host_us"] = round((t1 - t0) / 200 * 1e6, 2)
+            res[label + "_eager_wall_us"] = round((t2 - t0) / 200 * 1e6, 2)
         res["weight_mb"] = round(k * n / 2 / 1e6, 2)
         out[name] = res
         print(f"{name}: {res}", file=sys.stderr, flush=True)

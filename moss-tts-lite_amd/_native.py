@@ -174,6 +174,11 @@ def lib_path() -> str:
     return _build.LIB_PATH
 
 
+def torch_ops_path() -> str:
+    """The torch operator library built beside the C library (libmtl_torch_ops.so)."""
+    return _build.TORCH_OPS_PATH
+
+
 def header_symbols() -> list[str]:
     """Every function name declared in ``include/*.h``."""
     inc = os.path.join(_build.ROOT, "include")

@@ -53,9 +53,38 @@ def _run(cmd: list[str]) -> str:
     return err
 
 
+TORCH_OPS_SRC = os.path.join(PKG_DIR, "torch_ops", "mtl_torch_ops.cpp")
+TORCH_OPS_PATH = os.path.join(PKG_DIR, "libmtl_torch_ops.so")
+
+
+def torch_ops_command(out: str = TORCH_OPS_PATH) -> list[str]:
+    """g++ line of the torch dispatcher operators (host code over the C ABI), linked
+    against libmtl_hip.so beside it and torch's own libraries."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    tdir = os.path.dirname(torch.__file__)
+    incs = [p for p in ce.include_paths() if os.path.isdir(p)]
+    abi = int(torch.compiled_with_cxx11_abi())
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+            *[f"-I{p}" for p in incs], "-I/opt/rocm/include", f"-I{os.path.join(ROOT, 'include')}",
+            TORCH_OPS_SRC, f"-L{os.path.join(tdir, 'lib')}", f"-L{PKG_DIR}",
+            "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{os.path.join(tdir, 'lib')}",
+            "-lmtl_hip", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch", "-o", out]
+
+
+def build_torch_ops() -> str:
+    """Compile the torch operator library in-tree (after libmtl_hip.so) and return its path."""
+    tmp = TORCH_OPS_PATH + ".tmp"
+    _run(torch_ops_command(tmp))
+    os.replace(tmp, TORCH_OPS_PATH)
+    return TORCH_OPS_PATH
+
+
 def build(verbose: bool = False) -> str:
     """Compile the library in-tree (always recompiles; one hipcc per source, in
-    parallel) and return its path."""
+    parallel), then the torch operator library over it, and return the library's path."""
     from concurrent.futures import ThreadPoolExecutor
 
     with tempfile.TemporaryDirectory(prefix="mtl_build_") as tmpdir:
@@ -69,6 +98,7 @@ def build(verbose: bool = False) -> str:
     if verbose and err:
         print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
+    build_torch_ops()
     return LIB_PATH
 
 

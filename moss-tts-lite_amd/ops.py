@@ -11,6 +11,8 @@ Replaced reference calls (moss_tts_lite/...):
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _native as N
@@ -146,60 +148,44 @@ def gptq_gemm(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor, scal
     return y.reshape(*x.shape[:-1], n)
 
 
-def _int4pack_shape(n: int, k: int, inner_k_tiles: int) -> tuple:
-    """torch's shape of a packed int4 weight, ``[N/8, K/(16 T), 32, T/2]``."""
-    return (n // 8, k // (16 * inner_k_tiles), 32, inner_k_tiles // 2)
+def torch_ops():
+    """The torch dispatcher operators of ``libmtl_torch_ops.so`` (``torch.ops.mtl``), loaded
+    once after ``libmtl_hip.so``, which they call."""
+    global _torch_ops_loaded
+    if not _torch_ops_loaded:
+        N.load()
+        path = N.torch_ops_path()
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build the libraries first "
+                               "(python -c 'import __graft_entry__ as g; g.build()')")
+        torch.ops.load_library(path)
+        _torch_ops_loaded = True
+    return torch.ops.mtl
 
 
-_pack_ws_cache: dict = {}
+_torch_ops_loaded = False
 
 
 def weight_int4pack_mm(x: torch.Tensor, packed: torch.Tensor, q_group_size: int,
                        q_scale_and_zeros: torch.Tensor) -> torch.Tensor:
-    """Drop-in for ``torch._weight_int4pack_mm(x, packed, qGroupSize, qScaleAndZeros)``.
+    """Drop-in for ``torch._weight_int4pack_mm(x, packed, qGroupSize, qScaleAndZeros)``:
+    the ``torch.ops.mtl.weight_int4pack_mm`` operator over ``mtl_int4pack_mm``.
 
     ``x`` bf16 ``[M, K]`` (any M); ``packed`` from :func:`convert_weight_to_int4pack` or
     :func:`int4pack_from_torch_tiles` (torch's 4-D shape, this build's strip layout inside:
     a concatenation along dim 0 is a concatenation along N, as with torch's tiles);
     ``qScaleAndZeros`` bf16 ``[K/g, N, 2]`` = (scale, zero) with
     ``w = (q - 8) * scale + zero`` (moss_tts_lite/gptq.py:87-97).  Returns bf16 ``[M, N]``.
-    M = 1 runs the full-K strip GEMV, more rows the prompt-length GEMM.
+    M = 1 runs the full-K strip GEMV, 2 to 16 rows the skinny strip GEMM where it pays, more
+    rows the prompt-length GEMM.  ``RuntimeError`` for a wrong shape, dtype or group size,
+    as torch's operator raises.
     """
-    if x.dim() != 2:
-        raise RuntimeError(f"x must be 2-D [M, K], got {tuple(x.shape)}")
-    qsz = q_scale_and_zeros
-    if qsz.dtype != torch.bfloat16 or qsz.dim() != 3 or qsz.shape[2] != 2:
-        raise RuntimeError("qScaleAndZeros must be bfloat16 [K/g, N, 2]")
-    _check_group(q_group_size, qsz.shape[0] * q_group_size)
-    k, n = qsz.shape[0] * q_group_size, qsz.shape[1]
-    if packed.dtype != torch.int32 or packed.dim() != 4 or packed.shape[0] * 8 != n or \
-            packed.numel() * 8 != n * k:
-        raise RuntimeError(f"packed weight must be int32 [N/8, K/(16*T), 32, T/2] for "
-                           f"N={n}, K={k}")
-    x2 = _check_x(x, k)
-    m = x2.shape[0]
-    y = torch.empty(m, n, dtype=torch.bfloat16, device=x2.device)
-    lib = N.load()
-    ws, nbytes = None, int(lib.mtl_int4pack_mm_workspace_bytes(m, k, n))
-    if nbytes > 0:
-        key = _dev_index(x2.device)
-        ws = _pack_ws_cache.get(key)
-        if ws is None or ws.numel() * 4 < nbytes:
-            if torch.cuda.is_current_stream_capturing():
-                ws = None                  # no growth under capture: one pass instead
-            else:
-                ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=x2.device)
-                _pack_ws_cache[key] = ws
-    N.check(lib.mtl_int4pack_mm(x2.data_ptr(), m, k, packed.data_ptr(), q_group_size,
-                                qsz.contiguous().data_ptr(), n, y.data_ptr(),
-                                None if ws is None else ws.data_ptr(),
-                                0 if ws is None else ws.numel() * 4, _stream(x2.device)),
-            "mtl_int4pack_mm")
-    return y
+    return torch_ops().weight_int4pack_mm(x, packed, q_group_size, q_scale_and_zeros)
 
 
 def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) -> torch.Tensor:
-    """Drop-in for ``aten._convert_weight_to_int4pack(uint8[N, K/2], innerKTiles)``.
+    """Drop-in for ``aten._convert_weight_to_int4pack(uint8[N, K/2], innerKTiles)``: the
+    ``torch.ops.mtl.convert_weight_to_int4pack`` operator over ``mtl_int4pack_convert``.
 
     Input is the reference's nibble pre-pack (even k in the high nibble,
     moss_tts_lite/fast.py:98).  Output has torch's shape ``[N/8, K/(16 T), 32, T/2]`` int32
@@ -208,19 +194,7 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
     packed concatenation of the weights along N (moss_tts_lite/fast_native.py:158-159).
     K % 256 == 0 and N % 16 == 0.
     """
-    if prepacked.dtype != torch.uint8 or prepacked.dim() != 2:
-        raise RuntimeError("expected a uint8 [N, K/2] tensor")
-    if inner_k_tiles not in (2, 4, 8):
-        raise RuntimeError("innerKTiles must be 2, 4 or 8")
-    n, kh = prepacked.shape
-    k = kh * 2
-    if k % 256 or n % 16:
-        raise RuntimeError(f"K={k} must be a multiple of 256 and N={n} a multiple of 16")
-    src = prepacked.contiguous()
-    out = torch.empty(_int4pack_shape(n, k, inner_k_tiles), dtype=torch.int32, device=src.device)
-    N.check(N.load().mtl_int4pack_convert(src.data_ptr(), n, k, inner_k_tiles, out.data_ptr(),
-                                          _stream(src.device)), "mtl_int4pack_convert")
-    return out
+    return torch_ops().convert_weight_to_int4pack(prepacked, inner_k_tiles)
 
 
 def int4pack_from_torch_tiles(tiles: torch.Tensor) -> torch.Tensor:

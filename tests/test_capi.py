@@ -305,3 +305,26 @@ def test_step_position_and_id_checks():
     for bad in (64, -1):
         with pytest.raises(ValueError, match="outside the KV cache"):
             _check_pos(bad, 64)
+
+
+def test_torch_operators_registered():
+    # the dispatcher operators over the C ABI load on the CPU and report shapes through
+    # their meta kernels; bad arguments raise RuntimeError as torch's operators do
+    import torch
+    from moss_tts_lite_amd import ops
+    mtl = ops.torch_ops()
+    x = torch.empty(3, 4096, dtype=torch.bfloat16, device="meta")
+    packed = torch.empty(64, 32, 32, 4, dtype=torch.int32, device="meta")
+    qsz = torch.empty(32, 512, 2, dtype=torch.bfloat16, device="meta")
+    assert tuple(mtl.weight_int4pack_mm(x, packed, 128, qsz).shape) == (3, 512)
+    with pytest.raises(RuntimeError):
+        mtl.weight_int4pack_mm(x.float(), packed, 128, qsz)
+    with pytest.raises(RuntimeError):
+        mtl.weight_int4pack_mm(x, packed, 16, torch.empty(256, 512, 2, dtype=torch.bfloat16,
+                                                          device="meta"))
+    with pytest.raises(RuntimeError):
+        mtl.weight_int4pack_mm(x[:, :2048], packed, 128, qsz)
+    pre = torch.empty(512, 2048, dtype=torch.uint8, device="meta")
+    assert tuple(mtl.convert_weight_to_int4pack(pre, 8).shape) == (64, 32, 32, 4)
+    with pytest.raises(RuntimeError):
+        mtl.convert_weight_to_int4pack(pre, 3)

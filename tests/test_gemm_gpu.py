@@ -415,15 +415,17 @@ def test_int4pack_dim0_concat_is_concat_along_n(dev):
 
 
 def test_int4pack_mm_graph_replay(dev):
-    # the drop-in under capture, M = 1 and M = 8, replayed with eager work in between
+    # the drop-in operator under capture at M = 1 (strip GEMV), 8 (skinny strip GEMM) and 40
+    # (prompt-length GEMM, its K-split workspace allocated inside the capture), replayed
+    # with eager work in between
     r = np.random.default_rng(5)
     k, n, g = 4096, 6144, 128
     q, qsz = _qsz_weights(r, n, k, g)
     packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
     tq = t_bf16(qsz, dev)
     xs = [t_bf16(f32_to_bf16_bits(r.standard_normal((m, k)).astype(np.float32)), dev)
-          for m in (1, 8)]
-    eager = [ops.weight_int4pack_mm(x, packed, g, tq) for x in xs]   # workspace grows here
+          for m in (1, 8, 40)]
+    eager = [ops.weight_int4pack_mm(x, packed, g, tq) for x in xs]
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
