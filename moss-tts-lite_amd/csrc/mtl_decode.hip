@@ -939,6 +939,127 @@ static void launch_head(int64_t K, hipStream_t s, Args... args) {
   launch_head_on(kHeadWGs, K, s, args...);
 }
 
+// ----------------------------------------------------------------------------------
+// bf16 GEMV with RMSNorm staging for a kept projection (few rows per wave: v_proj is
+// 1024 x 4096).  The workgroup forms x = RMSNorm(h) once into LDS (each thread a share
+// of the 8-channel items) while its waves' first weight rows are already in flight; each
+// wave then holds x in registers in the head GEMV's lane layout (k = 512 i + 8 lane) and
+// streams rows wave, wave + 4, ... of the workgroup's band, two rows per pass.  Products,
+// their order and the roundings are the head GEMV's, so the results are the same bits;
+// the head GEMV forms x in every wave, which costs more than the row itself here.
+// ----------------------------------------------------------------------------------
+template <int kKit>
+__global__ void __launch_bounds__(256) bf16_rows_norm_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ norm_w,
+    const float* __restrict__ slots, float eps, const uint16_t* __restrict__ w, int64_t N,
+    int K, int rows_per_wg, float* __restrict__ out) {
+  __shared__ u32x4 xs[kKit * 64];               // x items: item j holds channels 8j .. 8j+7
+  const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
+  const int kit = (K + 511) / 512;
+  const int64_t b0 = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t b1 = b0 + rows_per_wg < N ? b0 + rows_per_wg : N;
+  // the first two rows of this wave (rows b0 + wave, b0 + wave + 4), before any x work
+  u32x4 ww[2][kKit];
+  auto issue = [&](int64_t r0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t r = r0 + 4 * j;
+      if (r >= b1) break;                       // wave-uniform: the band's last rows
+      const uint16_t* wr = w + r * K;
+#pragma unroll
+      for (int i = 0; i < kKit; ++i) {
+        const int k = 512 * i + 8 * lane;
+        if (i < kit && k < K)
+          ww[j][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + k));
+      }
+    }
+  };
+  if (b0 + wave < b1) issue(b0 + wave);
+  // x = bf16(norm_w * bf16(h * r)), r from h's sums of squares (every wave sums them)
+  SlotLoad sl;
+  slot_issue(slots, K, lane, sl);
+  const int items = K / 8;
+  constexpr int kStage = (kKit * 64 + 255) / 256;   // items staged per thread
+  u32x4 hv[kStage], gv[kStage];
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int j = t + 256 * u;
+    if (j < items) {
+      hv[u] = *reinterpret_cast<const u32x4*>(h + 8 * j);
+      gv[u] = *reinterpret_cast<const u32x4*>(norm_w + 8 * j);
+    }
+  }
+  const float r = rsqrtf(wave_sum(slot_finish(sl, K, lane)) / (float)K + eps);
+#pragma unroll
+  for (int u = 0; u < kStage; ++u) {
+    const int j = t + 256 * u;
+    if (j < items) {
+      const uint32_t hh[4] = {hv[u].x, hv[u].y, hv[u].z, hv[u].w};
+      const uint32_t gg[4] = {gv[u].x, gv[u].y, gv[u].z, gv[u].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = f32_to_bf16(round_bf16(lo_bf(gg[c]) * round_bf16(lo_bf(hh[c]) * r)));
+        const uint32_t hi = f32_to_bf16(round_bf16(hi_bf(gg[c]) * round_bf16(hi_bf(hh[c]) * r)));
+        o[c] = lo | (hi << 16);
+      }
+      xs[j] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+  __syncthreads();
+  u32x4 xv[kKit];
+#pragma unroll
+  for (int i = 0; i < kKit; ++i) {
+    const int j = 64 * i + lane;                 // channels 512 i + 8 lane
+    xv[i] = (i < kit && 8 * j < K) ? xs[j] : u32x4{0u, 0u, 0u, 0u};
+  }
+  for (int64_t rb = b0 + wave; rb < b1; rb += 8) {
+    float acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      acc[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < kKit; ++i) {
+        const int k = 512 * i + 8 * lane;
+        if (i < kit && k < K) {
+          acc[j] = dot2_bf16(ww[j][i].x, xv[i].x, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].y, xv[i].y, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].z, xv[i].z, acc[j]);
+          acc[j] = dot2_bf16(ww[j][i].w, xv[i].w, acc[j]);
+        }
+      }
+    }
+    if (rb + 8 < b1) issue(rb + 8);              // the next pass's rows go out first
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t row = rb + 4 * j;
+      const float sum = wave_sum(acc[j]);
+      if (row < b1 && lane == 0) out[row] = bf16_to_f32(f32_to_bf16(sum));
+    }
+  }
+}
+
+// Rows per workgroup of bf16_rows_norm_kernel: a band that spreads N over the CUs, 4 rows
+// at least (one per wave) and a multiple of 8 above that (two rows per wave and pass).
+static int bf16_rows_per_wg(int64_t N, int cus) {
+  int64_t r = (N + cus - 1) / cus;
+  r = r <= 4 ? 4 : (r + 7) / 8 * 8;
+  return (int)r;
+}
+
+static int g_dec_cus = 0;
+
+static int decode_device_cus() {
+  if (!g_dec_cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_dec_cus = n;
+  }
+  return g_dec_cus;
+}
+
 __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restrict__ part_v,
                                                            const long long* __restrict__ part_i,
                                                            int nparts, int64_t* token_out) {
@@ -1239,7 +1360,17 @@ int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, fl
   if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w) || !aligned16(slots))
     return MTL_ERR_ALIGN;
-  // one row per wave where N allows: every wave stages the normalised x
+  if (K <= 4096) {   // x formed once per workgroup into LDS
+    const int rpw = bf16_rows_per_wg(N, decode_device_cus());
+    const int64_t wgs = (N + rpw - 1) / rpw;
+    if (wgs >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+    hipLaunchKernelGGL(bf16_rows_norm_kernel<8>, dim3((unsigned)wgs), dim3(256), 0,
+                       (hipStream_t)stream, static_cast<const uint16_t*>(h),
+                       static_cast<const uint16_t*>(norm_w), slots, eps,
+                       static_cast<const uint16_t*>(w), N, (int)K, rpw, out);
+    return launch_status();
+  }
+  // longer rows: the head GEMV, one row per wave where N allows (every wave forms x)
   const int64_t wgs = (N + 3) / 4 < kHeadWGs ? (N + 3) / 4 : kHeadWGs;
   launch_head_on((int)wgs, K, (hipStream_t)stream, static_cast<const uint16_t*>(h),
                  static_cast<const uint16_t*>(w), N, (int)K, static_cast<uint16_t*>(nullptr),

@@ -534,12 +534,14 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     assert int(tok.item()) == int(np.argmax(fb(logits)))
 
 
-def test_bf16_gemv_norm_kept_linear(dev, lib):
-    # a linear kept in bf16 with RMSNorm staging (the v_proj of the shipped presets):
-    # fp32 outputs holding bf16 values, equal bit for bit to the bf16 logits of the
-    # head kernel on the same input, and within the bf16 bar of float64
-    r = np.random.default_rng(52)
-    N_, K = 1024, 4096
+@pytest.mark.parametrize("N_,K", [(1024, 4096), (12288, 4096), (37, 4096), (2000, 1024),
+                                  (300, 8192)])
+def test_bf16_gemv_norm_kept_linear(dev, lib, N_, K):
+    # a linear kept in bf16 with RMSNorm staging (the v_proj and up_proj of the shipped
+    # presets; K <= 4096 forms x once per workgroup, longer rows run on the head kernel):
+    # fp32 outputs holding bf16 values, equal bit for bit to the bf16 logits of the head
+    # kernel on the same input, and within the bf16 bar of float64
+    r = np.random.default_rng(52 + N_ + K)
     h = round_bf16((2 * r.standard_normal(K)).astype(np.float32))
     w = round_bf16((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
     W = round_bf16((r.standard_normal((N_, K)) * 0.05).astype(np.float32))
