@@ -28,7 +28,7 @@ int mtl_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int64_t n
 /*
  * Embedding lookup and sum (moss_tts_lite/model.py:156-161, fast.py:123-128):
  * out = bf16(...bf16(T0[ids[0]] + T1[ids[1]]) + ...), each table bf16 [vocab_i, hidden].
- *   ids     int64 [n_tables] (device)
+ *   ids     int64 [n_tables] (device), 1 <= n_tables <= 64
  *   tables  device array of n_tables table base pointers
  *   vocabs  device array of n_tables row counts (ids outside [0, vocab) read as 0)
  */

@@ -186,17 +186,35 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
 // ----------------------------------------------------------------------------------
 // Embedding sum (model.py:156-161): sequential bf16 adds of one row per table.
 // ----------------------------------------------------------------------------------
+constexpr int kEmbedMaxTables = 64;
+constexpr int kEmbedBatch = 8;       // table rows whose loads are in flight together
+
 __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
                                  const uint16_t* const* __restrict__ tables,
                                  const int64_t* __restrict__ vocabs, int64_t hidden,
                                  uint16_t* __restrict__ out) {
+  // each table's row (NULL for an id outside its table) once per workgroup, so the element
+  // loads of kEmbedBatch tables go out together instead of one table after another
+  __shared__ const uint16_t* rows[kEmbedMaxTables];
+  for (int i = threadIdx.x; i < n_tables; i += blockDim.x) {
+    const int64_t id = ids[i];
+    rows[i] = (id >= 0 && id < vocabs[i]) ? tables[i] + id * hidden : nullptr;
+  }
+  __syncthreads();
   for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < hidden;
        d += (int64_t)gridDim.x * blockDim.x) {
     float h = 0.f;
-    for (int i = 0; i < n_tables; ++i) {
-      const int64_t id = ids[i];
-      const float v = (id >= 0 && id < vocabs[i]) ? bf16_to_f32(tables[i][id * hidden + d]) : 0.f;
-      h = (i == 0) ? v : round_bf16(h + v);
+    for (int i0 = 0; i0 < n_tables; i0 += kEmbedBatch) {
+      float v[kEmbedBatch];
+#pragma unroll
+      for (int j = 0; j < kEmbedBatch; ++j) {
+        const int i = i0 + j;
+        const uint16_t* r = i < n_tables ? rows[i] : nullptr;
+        v[j] = r ? bf16_to_f32(r[d]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kEmbedBatch; ++j)   // summed in table order, rounded as before
+        if (i0 + j < n_tables) h = (i0 + j == 0) ? v[j] : round_bf16(h + v[j]);
     }
     out[d] = (uint16_t)f32_to_bf16(h);
   }
@@ -1120,7 +1138,7 @@ int mtl_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int64_t n
 int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* tables,
                   const int64_t* vocabs, int64_t hidden, void* out, void* stream) {
   if (!ids || !tables || !vocabs || !out) return MTL_ERR_INVALID_ARG;
-  if (n_tables < 1 || hidden < 1) return MTL_ERR_SHAPE;
+  if (n_tables < 1 || n_tables > kEmbedMaxTables || hidden < 1) return MTL_ERR_SHAPE;
   const int blocks = (int)((hidden + 255) / 256);
   hipLaunchKernelGGL(embed_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, ids,
                      n_tables, reinterpret_cast<const uint16_t* const*>(tables), vocabs, hidden,

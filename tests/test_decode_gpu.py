@@ -83,6 +83,29 @@ def test_embed_sum_kernel(dev, lib):
         assert np.array_equal(fb(out), h)
 
 
+def test_embed_sum_33_tables(dev, lib):
+    # the MOSS embedding: a text table and 32 audio tables summed in table order, loads
+    # batched 8 tables at a time (tables 0..32 end mid-batch); ids outside a table read 0,
+    # also in table 0 and in the middle of a batch; more than 64 tables are refused
+    r = np.random.default_rng(3)
+    hidden, vocabs_l = 4096, [300] + [17] * 32
+    tabs = [round_bf16(r.standard_normal((v, hidden)).astype(np.float32)) for v in vocabs_l]
+    tt = [tb(t, dev) for t in tabs]
+    ptrs = torch.tensor([t.data_ptr() for t in tt], dtype=torch.int64, device=dev)
+    vocabs = torch.tensor(vocabs_l, dtype=torch.int64, device=dev)
+    for ids in (list(r.integers(0, 17, 33)), [400] + [5] * 10 + [17] + [3] * 21):
+        tid = torch.tensor(ids, dtype=torch.int64, device=dev)
+        out = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+        N.check(lib.mtl_embed_sum(tid.data_ptr(), 33, ptrs.data_ptr(), vocabs.data_ptr(), hidden,
+                                  out.data_ptr(), stream()), "embed")
+        h = tabs[0][ids[0]] if ids[0] < vocabs_l[0] else np.zeros(hidden, np.float32)
+        for t, i in zip(tabs[1:], ids[1:]):
+            h = round_bf16(h + (t[i] if i < t.shape[0] else 0))
+        assert np.array_equal(fb(out), h)
+    assert lib.mtl_embed_sum(tid.data_ptr(), 65, ptrs.data_ptr(), vocabs.data_ptr(), hidden,
+                             out.data_ptr(), stream()) == N.MTL_ERR_SHAPE
+
+
 def oracle_tables(n, dev):
     """The oracle's RoPE tables as device bf16 tensors (kernel inputs)."""
     cos, sin = D.rope_tables(n, 128)
