@@ -187,7 +187,7 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
 // Embedding sum (model.py:156-161): sequential bf16 adds of one row per table.
 // ----------------------------------------------------------------------------------
 constexpr int kEmbedMaxTables = 64;
-constexpr int kEmbedBatch = 8;       // table rows whose loads are in flight together
+constexpr int kEmbedBatch = 17;      // table rows whose loads are in flight together (MOSS: 33 in two)
 
 __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
                                  const uint16_t* const* __restrict__ tables,

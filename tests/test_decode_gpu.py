@@ -84,9 +84,9 @@ def test_embed_sum_kernel(dev, lib):
 
 
 def test_embed_sum_33_tables(dev, lib):
-    # the MOSS embedding: a text table and 32 audio tables summed in table order, loads
-    # batched 8 tables at a time (tables 0..32 end mid-batch); ids outside a table read 0,
-    # also in table 0 and in the middle of a batch; more than 64 tables are refused
+    # the MOSS embedding: a text table and 32 audio tables summed in table order, their
+    # loads in flight together; ids outside a table read 0, also in table 0 and among the
+    # audio tables; more than 64 tables are refused
     r = np.random.default_rng(3)
     hidden, vocabs_l = 4096, [300] + [17] * 32
     tabs = [round_bf16(r.standard_normal((v, hidden)).astype(np.float32)) for v in vocabs_l]
