@@ -193,12 +193,16 @@ __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
                                  const uint16_t* const* __restrict__ tables,
                                  const int64_t* __restrict__ vocabs, int64_t hidden,
                                  uint16_t* __restrict__ out) {
-  // each table's row (NULL for an id outside its table) once per workgroup, so the element
-  // loads of kEmbedBatch tables go out together instead of one table after another
+  // each table's row once per workgroup: its address and its length in bytes, 0 for an id
+  // outside the table.  The element reads are buffer loads over that range, so an empty
+  // range reads 0 with no branch, and the loads of kEmbedBatch tables go out together.
   __shared__ const uint16_t* rows[kEmbedMaxTables];
+  __shared__ int row_bytes[kEmbedMaxTables];
   for (int i = threadIdx.x; i < n_tables; i += blockDim.x) {
     const int64_t id = ids[i];
-    rows[i] = (id >= 0 && id < vocabs[i]) ? tables[i] + id * hidden : nullptr;
+    const bool ok = id >= 0 && id < vocabs[i];
+    rows[i] = ok ? tables[i] + id * hidden : tables[i];
+    row_bytes[i] = ok ? (int)(hidden * 2) : 0;
   }
   __syncthreads();
   for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < hidden;
@@ -208,9 +212,15 @@ __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
       float v[kEmbedBatch];
 #pragma unroll
       for (int j = 0; j < kEmbedBatch; ++j) {
-        const int i = i0 + j;
-        const uint16_t* r = i < n_tables ? rows[i] : nullptr;
-        v[j] = r ? bf16_to_f32(r[d]) : 0.f;
+        const int i = i0 + j < n_tables ? i0 + j : 0;
+        // the same LDS word in every lane: wave-uniform, so the descriptor lives in SGPRs
+        const uint64_t ra = reinterpret_cast<uint64_t>(rows[i]);
+        const uint64_t ru = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ra >> 32)) << 32) |
+                            (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ra);
+        const int nb = __builtin_amdgcn_readfirstlane(i0 + j < n_tables ? row_bytes[i] : 0);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(ru), (short)0, nb, 0x00020000);
+        v[j] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(d * 2), 0, 0));
       }
 #pragma unroll
       for (int j = 0; j < kEmbedBatch; ++j)   // summed in table order, rounded as before
@@ -1138,7 +1148,8 @@ int mtl_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int64_t n
 int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* tables,
                   const int64_t* vocabs, int64_t hidden, void* out, void* stream) {
   if (!ids || !tables || !vocabs || !out) return MTL_ERR_INVALID_ARG;
-  if (n_tables < 1 || n_tables > kEmbedMaxTables || hidden < 1) return MTL_ERR_SHAPE;
+  if (n_tables < 1 || n_tables > kEmbedMaxTables || hidden < 1 || hidden * 2 >= ((int64_t)1 << 31))
+    return MTL_ERR_SHAPE;
   const int blocks = (int)((hidden + 255) / 256);
   hipLaunchKernelGGL(embed_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, ids,
                      n_tables, reinterpret_cast<const uint16_t* const*>(tables), vocabs, hidden,
