@@ -383,38 +383,32 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
   for (int hr = wave; hr < n_rep; hr += 4) {
     const int h = kvh * n_rep + hr;
     const float* ph = a.part + (size_t)h * kAttnMaxChunks * kAttnPart;
-    // the output columns of dims 2*lane, +1, loaded with the partials (not at the store)
-    const int i0 = h * D + 2 * lane;
-    int2 oi = make_int2(i0, i0 + 1);
-    if (a.out_index) oi = *reinterpret_cast<const int2*>(a.out_index + i0);
-    // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1 as 64-bit
-    // agent-scope loads, all issued before any use
+    // Every load of the merge is a bounds-checked buffer load issued before any use (the
+    // acquire fence of the completing workgroup already made the partials visible): the
+    // output columns of dims 2*lane, +1 (a missing out_index reads as 0, replaced below),
+    // (m, l) of chunk `lane` and the chunk outputs of dims 2*lane, +1, chunks at or past nch
+    // reading as 0.  No load sits under a branch, so none of them waits for another.
     typedef unsigned long long u64;
-    float mc = -INFINITY, lc = 0.f;
-    if (lane < nch) {
-      const u64 ml = __hip_atomic_load(reinterpret_cast<const u64*>(ph + (size_t)lane * kAttnPart),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      mc = __uint_as_float((uint32_t)ml);
-      lc = __uint_as_float((uint32_t)(ml >> 32));
-    }
-    float o0 = 0.f, o1 = 0.f;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-      u64 ov[16];
+    const int i0 = h * D + 2 * lane;
+    const __amdgpu_buffer_rsrc_t irs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(a.out_index), (short)0, a.out_index ? a.H * D * 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(ph), (short)0, nch * kAttnPart * 4, 0x00020000);
+    const u64 oiv = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(irs, i0 * 4, 0, 0));
+    const u64 ml = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(prs, lane * kAttnPart * 4, 0, 0));
+    float mc = __uint_as_float((uint32_t)ml);
+    float lc = __uint_as_float((uint32_t)(ml >> 32));   // 0 past nch: the chunk drops out
+    // chunk outputs 16 at a time; the first batch goes out with the loads above (peeled:
+    // a loop header there made the compiler wait for those first)
+    u64 ov[16];
+    auto load_batch = [&](int c0) {
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (c0 + j < nch)
-          ov[j] = __hip_atomic_load(
-              reinterpret_cast<const u64*>(ph + (size_t)(c0 + j) * kAttnPart + 4 + 2 * lane),
-              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (c0 == 0) {
-        const float M = wave_max(lc > 0.f ? mc : -INFINITY);
-        const float wc = lc > 0.f ? expf(mc - M) : 0.f;
-        w_lds[wave][lane] = wc;
-        lc = wave_sum(wc * lc);                        // Ls from here on
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
+        ov[j] = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(
+                                            prs, ((c0 + j) * kAttnPart + 4 + 2 * lane) * 4, 0, 0));
+    };
+    float o0 = 0.f, o1 = 0.f;
+    auto add_batch = [&](int c0) {
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (c0 + j < nch) {
@@ -422,9 +416,26 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
           o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
           o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
         }
+    };
+    load_batch(0);
+    {
+      const float M = wave_max(lc > 0.f ? mc : -INFINITY);
+      const float wc = lc > 0.f ? expf(mc - M) : 0.f;
+      w_lds[wave][lane] = wc;
+      lc = wave_sum(wc * lc);                          // Ls from here on
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    add_batch(0);
+    for (int c0 = 16; c0 < nch; c0 += 16) {
+      load_batch(c0);
+      add_batch(c0);
     }
     const float Ls = lc;
     const float r0 = Ls > 0.f ? o0 / Ls : 0.f, r1 = Ls > 0.f ? o1 / Ls : 0.f;
+    const int2 oi = a.out_index ? make_int2((int)(uint32_t)oiv, (int)(uint32_t)(oiv >> 32))
+                                : make_int2(i0, i0 + 1);
     a.out[oi.x] = (uint16_t)f32_to_bf16(r0);
     a.out[oi.y] = (uint16_t)f32_to_bf16(r1);
   }
