@@ -47,7 +47,7 @@ struct RowsArgs {
 
 // Wave w serves strip w % CT over K slice w / CT (KW slices of NB blocks per phase, CT =
 // a.ct); WIN blocks of the weight stream in flight per wave, as in the M = 1 strip GEMV.
-template <int GR, int NB, int FMT>
+template <int GR, int NB, int FMT, bool PERM>
 __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(RowsArgs a) {
   constexpr int WIN = rows_ring(GR, NB);
   constexpr int GI = 4 * GR;                   // x items per group
@@ -122,30 +122,54 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   for (int z = threadIdx.x; z < pgrp * 16; z += blockDim.x)
     if ((z & 15) >= a.M) xg[z] = 0.f;
   for (int z = threadIdx.x; z < K8; z += blockDim.x) xa[a.M * XS + z] = u32x4{0u, 0u, 0u, 0u};
-  // loads per thread in flight: 16 rows of K = 4096 in one batch (12 at 12 waves, 8 at 16)
-  constexpr int BATCH = rows_max_waves(NB) == 12 ? 12 : 8;
+  // items per thread in flight: 4 (more spill registers of the MFMA loop: 16 rows of K = 4096
+  // stage in three round trips)
+  constexpr int BATCH = 4;
+  // x through bounds-checked buffer resources over the M rows (and the act-order index):
+  // an item past the last row reads 0, so a batch's loads carry no branch and go out
+  // together (a branch per load made the compiler wait for each before the next)
+  const int xbytes = (int)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, xbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(a.perm), (short)0, PERM ? a.K * 4 : 0, 0x00020000);
   auto stage = [&](int p) {
     const int nthr = blockDim.x;
     const int total = a.M * K8;
     const int c0 = p * a.kp;                   // the phase's first input row
     for (int f0 = 0; f0 < total; f0 += BATCH * nthr) {
       u32x4 v[BATCH];
+      if constexpr (PERM) {                    // act-order: 8 channels through the index
+        constexpr int HB = 1;                  // items per index batch (register budget)
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int f = f0 + u * nthr + threadIdx.x;
-        const int m = f / K8, i = f - m * K8;
-        const uint16_t* xr = a.x + m * a.ldx;
-        if (f >= total) {
-          v[u] = u32x4{0u, 0u, 0u, 0u};
-        } else if (a.perm) {                    // act-order: 8 channels through the index
-          const int4 p0 = *reinterpret_cast<const int4*>(a.perm + c0 + 8 * i);
-          const int4 p1 = *reinterpret_cast<const int4*>(a.perm + c0 + 8 * i + 4);
-          v[u] = u32x4{(uint32_t)xr[p0.x] | ((uint32_t)xr[p0.y] << 16),
-                       (uint32_t)xr[p0.z] | ((uint32_t)xr[p0.w] << 16),
-                       (uint32_t)xr[p1.x] | ((uint32_t)xr[p1.y] << 16),
-                       (uint32_t)xr[p1.z] | ((uint32_t)xr[p1.w] << 16)};
-        } else {
-          v[u] = *reinterpret_cast<const u32x4*>(xr + c0 + (int64_t)i * 8);
+        for (int u0 = 0; u0 < BATCH; u0 += HB) {
+          int4 pi[HB][2];
+#pragma unroll
+          for (int u = 0; u < HB; ++u) {
+            const int f = f0 + (u0 + u) * nthr + threadIdx.x;
+            const int i = f - (f / K8) * K8;
+            const int po = f < total ? (c0 + 8 * i) * 4 : a.K * 4;   // past the end: 0
+            pi[u][0] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po, 0, 0));
+            pi[u][1] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po + 16, 0, 0));
+          }
+#pragma unroll
+          for (int u = 0; u < HB; ++u) {
+            const int f = f0 + (u0 + u) * nthr + threadIdx.x;
+            const int ro = (f < total ? (f / K8) * (int)a.ldx : xbytes) * 2;
+            auto e = [&](int c) {
+              return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(xrs, ro + 2 * c, 0, 0);
+            };
+            v[u0 + u] = u32x4{e(pi[u][0].x) | (e(pi[u][0].y) << 16), e(pi[u][0].z) | (e(pi[u][0].w) << 16),
+                              e(pi[u][1].x) | (e(pi[u][1].y) << 16), e(pi[u][1].z) | (e(pi[u][1].w) << 16)};
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          const int f = f0 + u * nthr + threadIdx.x;
+          const int m = f / K8, i = f - m * K8;
+          const int xo = f < total ? (m * (int)a.ldx + c0 + 8 * i) * 2 : xbytes;
+          v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
         }
       }
 #pragma unroll
@@ -320,25 +344,26 @@ static void rows_launch(Kern kern, dim3 grid, dim3 block, size_t lds, hipStream_
   hipLaunchKernelGGL(kern, grid, block, lds, st, a);
 }
 
-template <int GR, int FMT>
+template <int GR, int FMT, bool PERM>
 static void rows_nb(const RowsArgs& a, const RowsGeom& g, size_t lds, hipStream_t st) {
   const dim3 grid(a.N / (kStripCols * g.ct)), block(64 * g.ct * g.kw);
   static bool opted[4] = {false, false, false, false};
   switch (g.nb) {
-    case 2: rows_launch(w4_rows_kernel<GR, 2, FMT>, grid, block, lds, st, a, opted[0]); break;
-    case 4: rows_launch(w4_rows_kernel<GR, 4, FMT>, grid, block, lds, st, a, opted[1]); break;
-    case 8: rows_launch(w4_rows_kernel<GR, 8, FMT>, grid, block, lds, st, a, opted[2]); break;
-    default: rows_launch(w4_rows_kernel<GR, 16, FMT>, grid, block, lds, st, a, opted[3]); break;
+    case 2: rows_launch(w4_rows_kernel<GR, 2, FMT, PERM>, grid, block, lds, st, a, opted[0]); break;
+    case 4: rows_launch(w4_rows_kernel<GR, 4, FMT, PERM>, grid, block, lds, st, a, opted[1]); break;
+    case 8: rows_launch(w4_rows_kernel<GR, 8, FMT, PERM>, grid, block, lds, st, a, opted[2]); break;
+    default: rows_launch(w4_rows_kernel<GR, 16, FMT, PERM>, grid, block, lds, st, a, opted[3]); break;
   }
 }
 
-template <int FMT>
+// act-order inputs (GPTQ metadata only) run the PERM variants, whose staging gathers x
+template <int FMT, bool PERM>
 static void rows_group(const RowsArgs& a, const RowsGeom& g, size_t lds, hipStream_t st) {
   switch (a.group) {
-    case 32: rows_nb<1, FMT>(a, g, lds, st); break;
-    case 64: rows_nb<2, FMT>(a, g, lds, st); break;
-    case 128: rows_nb<4, FMT>(a, g, lds, st); break;
-    default: rows_nb<8, FMT>(a, g, lds, st); break;
+    case 32: rows_nb<1, FMT, PERM>(a, g, lds, st); break;
+    case 64: rows_nb<2, FMT, PERM>(a, g, lds, st); break;
+    case 128: rows_nb<4, FMT, PERM>(a, g, lds, st); break;
+    default: rows_nb<8, FMT, PERM>(a, g, lds, st); break;
   }
 }
 
@@ -367,7 +392,7 @@ int strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K, const int32_t* 
     return MTL_ERR_GROUP;
   if (M < 1 || M > kRowsMax || K <= 0 || N <= 0 || K % 256 != 0 || N % kStripCols != 0 ||
       K % group_size != 0 || ldx < K || ldy < N || N * K / 2 >= ((int64_t)1 << 31) ||
-      ldx * (M - 1) + K >= ((int64_t)1 << 31) || ldy * (M - 1) + N >= ((int64_t)1 << 31))
+      (ldx * (M - 1) + K) * 2 >= ((int64_t)1 << 31) || ldy * (M - 1) + N >= ((int64_t)1 << 31))
     return MTL_ERR_SHAPE;
   if (!aligned16(x) || ldx % 8 != 0 || !aligned16(strip_weight) || (perm && !aligned16(perm)) ||
       (reinterpret_cast<uintptr_t>(meta) & (fmt == STRIP_META_QSZ ? 3u : 1u)) ||
@@ -397,8 +422,9 @@ int strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K, const int32_t* 
   a.xcd_order = G % 8 == 0;
   const size_t lds = rows_lds(M, kp, group_size, g);
   hipStream_t st = (hipStream_t)stream;
-  if (fmt == STRIP_META_QSZ) rows_group<STRIP_META_QSZ>(a, g, lds, st);
-  else rows_group<STRIP_META_GPTQ>(a, g, lds, st);
+  if (fmt == STRIP_META_QSZ) rows_group<STRIP_META_QSZ, false>(a, g, lds, st);
+  else if (perm) rows_group<STRIP_META_GPTQ, true>(a, g, lds, st);
+  else rows_group<STRIP_META_GPTQ, false>(a, g, lds, st);
   return launch_status();
 }
 
