@@ -994,41 +994,65 @@ __global__ void __launch_bounds__(256) bf16_rows_norm_kernel(
     int K, int rows_per_wg, float* __restrict__ out) {
   __shared__ u32x4 xs[kKit * 64];               // x items: item j holds channels 8j .. 8j+7
   const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
-  const int kit = (K + 511) / 512;
   const int64_t b0 = (int64_t)blockIdx.x * rows_per_wg;
-  const int64_t b1 = b0 + rows_per_wg < N ? b0 + rows_per_wg : N;
-  // the first two rows of this wave (rows b0 + wave, b0 + wave + 4), before any x work
-  u32x4 ww[2][kKit];
-  auto issue = [&](int64_t r0) {
+  const int nrows = (int)((b0 + rows_per_wg < N ? b0 + rows_per_wg : N) - b0);
+  // Every load goes through a bounds-checked buffer resource (the band's rows, h, norm_w,
+  // the slots): a row past the band or a channel past K reads 0, so no load sits under a
+  // branch (a branch around a load made the compiler wait for all loads in flight), and a
+  // zero weight against a zero x item adds nothing (the sums cannot be -0).
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(w + b0 * K), (short)0, nrows * K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(h), (short)0, K * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(norm_w), (short)0, K * 2, 0x00020000);
+  const int ns = (K + kSlotCols - 1) / kSlotCols;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(slots), (short)0, ns * 4, 0x00020000);
+  const int wbytes = nrows * K * 2;
+  // x = bf16(norm_w * bf16(h * r)), r from h's sums of squares (every wave sums them).
+  // Its inputs (shared by every workgroup, so mostly L2 hits) are loaded before the weight
+  // rows: loads complete in issue order, so x is formed while the rows stream in.
+  float4 sv[kMaxSlots / 256];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t r = r0 + 4 * j;
-      if (r >= b1) break;                       // wave-uniform: the band's last rows
-      const uint16_t* wr = w + r * K;
-#pragma unroll
-      for (int i = 0; i < kKit; ++i) {
-        const int k = 512 * i + 8 * lane;
-        if (i < kit && k < K)
-          ww[j][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + k));
-      }
-    }
-  };
-  if (b0 + wave < b1) issue(b0 + wave);
-  // x = bf16(norm_w * bf16(h * r)), r from h's sums of squares (every wave sums them)
-  SlotLoad sl;
-  slot_issue(slots, K, lane, sl);
+  for (int it = 0; it < kMaxSlots / 256; ++it)
+    sv[it] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            srs, (4 * lane + 256 * it) * 4, 0, 0));
   const int items = K / 8;
   constexpr int kStage = (kKit * 64 + 255) / 256;   // items staged per thread
   u32x4 hv[kStage], gv[kStage];
 #pragma unroll
   for (int u = 0; u < kStage; ++u) {
     const int j = t + 256 * u;
-    if (j < items) {
-      hv[u] = *reinterpret_cast<const u32x4*>(h + 8 * j);
-      gv[u] = *reinterpret_cast<const u32x4*>(norm_w + 8 * j);
-    }
+    hv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(hrs, 16 * j, 0, 0));
+    gv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(grs, 16 * j, 0, 0));
   }
-  const float r = rsqrtf(wave_sum(slot_finish(sl, K, lane)) / (float)K + eps);
+  // rows rl and rl + 4 of the band (a wave's rows in one pass), non-temporal
+  u32x4 ww[2][kKit];
+  auto issue = [&](int rl) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = rl + 4 * j;
+#pragma unroll
+      for (int i = 0; i < kKit; ++i) {
+        const int k = 512 * i + 8 * lane;
+        const int off = r < nrows && k < K ? (r * K + k) * 2 : wbytes;
+        ww[j][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2));
+      }
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  issue(wave);
+  __builtin_amdgcn_sched_barrier(0);
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < kMaxSlots / 256; ++it) {
+    const int bs = 4 * lane + 256 * it;
+    const float4 v = sv[it];
+    ss += ((bs < ns ? v.x : 0.f) + (bs + 1 < ns ? v.y : 0.f)) +
+          ((bs + 2 < ns ? v.z : 0.f) + (bs + 3 < ns ? v.w : 0.f));
+  }
+  const float r = rsqrtf(wave_sum(ss) / (float)K + eps);
 #pragma unroll
   for (int u = 0; u < kStage; ++u) {
     const int j = t + 256 * u;
@@ -1050,30 +1074,27 @@ __global__ void __launch_bounds__(256) bf16_rows_norm_kernel(
 #pragma unroll
   for (int i = 0; i < kKit; ++i) {
     const int j = 64 * i + lane;                 // channels 512 i + 8 lane
-    xv[i] = (i < kit && 8 * j < K) ? xs[j] : u32x4{0u, 0u, 0u, 0u};
+    xv[i] = 8 * j < K ? xs[j] : u32x4{0u, 0u, 0u, 0u};
   }
-  for (int64_t rb = b0 + wave; rb < b1; rb += 8) {
+  for (int rb = wave; rb < nrows; rb += 8) {
     float acc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       acc[j] = 0.f;
 #pragma unroll
       for (int i = 0; i < kKit; ++i) {
-        const int k = 512 * i + 8 * lane;
-        if (i < kit && k < K) {
-          acc[j] = dot2_bf16(ww[j][i].x, xv[i].x, acc[j]);
-          acc[j] = dot2_bf16(ww[j][i].y, xv[i].y, acc[j]);
-          acc[j] = dot2_bf16(ww[j][i].z, xv[i].z, acc[j]);
-          acc[j] = dot2_bf16(ww[j][i].w, xv[i].w, acc[j]);
-        }
+        acc[j] = dot2_bf16(ww[j][i].x, xv[i].x, acc[j]);
+        acc[j] = dot2_bf16(ww[j][i].y, xv[i].y, acc[j]);
+        acc[j] = dot2_bf16(ww[j][i].z, xv[i].z, acc[j]);
+        acc[j] = dot2_bf16(ww[j][i].w, xv[i].w, acc[j]);
       }
     }
-    if (rb + 8 < b1) issue(rb + 8);              // the next pass's rows go out first
+    issue(rb + 8);                               // the next pass's rows (past the band: 0)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int64_t row = rb + 4 * j;
+      const int row = rb + 4 * j;
       const float sum = wave_sum(acc[j]);
-      if (row < b1 && lane == 0) out[row] = bf16_to_f32(f32_to_bf16(sum));
+      if (row < nrows && lane == 0) out[b0 + row] = bf16_to_f32(f32_to_bf16(sum));
     }
   }
 }
@@ -1403,7 +1424,8 @@ int mtl_bf16_gemv_norm(const void* h, const void* norm_w, const float* slots, fl
   if (K <= 4096) {   // x formed once per workgroup into LDS
     const int rpw = bf16_rows_per_wg(N, decode_device_cus());
     const int64_t wgs = (N + rpw - 1) / rpw;
-    if (wgs >= ((int64_t)1 << 31)) return MTL_ERR_SHAPE;
+    if (wgs >= ((int64_t)1 << 31) || (int64_t)rpw * K * 2 >= ((int64_t)1 << 31))
+      return MTL_ERR_SHAPE;                     // a band's bytes address one buffer resource
     hipLaunchKernelGGL(bf16_rows_norm_kernel<8>, dim3((unsigned)wgs), dim3(256), 0,
                        (hipStream_t)stream, static_cast<const uint16_t*>(h),
                        static_cast<const uint16_t*>(norm_w), slots, eps,

@@ -152,8 +152,8 @@ class GPTQLinear(torch.nn.Module):
         it), the others on the split-K GEMM over the AutoGPTQ layout."""
         qw, qz, sc, perm = self.kernel_args()
         m = x.numel() // self.in_features if self.in_features else 0
-        if m and self.supports_strip() and ops.strip_rows_pays(m, self.out_features,
-                                                               perm is not None):
+        if m and self.supports_strip() and ops.strip_rows_pays(m, self.in_features,
+                                                               self.out_features, perm is not None):
             strip = self.stream_weight(strip=True)[0]
             y = ops.strip_rows_gemm(x.reshape(m, self.in_features), strip, qz, sc,
                                     self.out_features, self.group_size, self.zero_offset,

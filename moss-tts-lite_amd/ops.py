@@ -272,16 +272,20 @@ def strip_meta(scales: torch.Tensor, qzeros: torch.Tensor, group_size: int):
     return sc, qz
 
 
-def strip_rows_pays(m: int, n: int, gathered: bool = False) -> bool:
-    """Whether the skinny strip GEMM beats the split-K GEMM at ``m`` rows over ``n``
-    columns on MI355X: each workgroup (one per CU) stages all m rows of x against the
-    N K / 512 weight bytes a CU streams, so it pays while m * 1024 <= 1.5 n (every m <= 16
-    on gate|up's 24576 columns, m <= 6 on down's 4096); with the act-order gather (two
-    bytes per load) while m * 1536 <= n.  The C drop-in mtl_int4pack_mm uses the first
-    rule."""
+def strip_rows_pays(m: int, k: int, n: int, gathered: bool = False) -> bool:
+    """Whether the skinny strip GEMM beats the split-K GEMM for ``m`` rows of a ``k x n``
+    product on MI355X.  Each workgroup (one per CU) stages all m rows of x against the
+    n k / 512 weight bytes a CU streams, so it pays while m * 1024 <= 1.5 n (every m <= 16
+    on gate|up's 24576 columns, m <= 6 on down's 4096).  With the act-order gather every
+    workgroup gathers all m * k channels of x two bytes per load, so it pays only for
+    k <= 4096 and while m * 1280 <= n (measured: m <= 4 on q|k|v's 6144 columns, m <= 3 on
+    o's 4096, every m <= 16 on gate|up; never on down, k = 12288).  The C drop-in
+    mtl_int4pack_mm uses the first rule."""
     if m < 1 or m > _MAX_M:
         return False
-    return m * 1536 <= n if gathered else 2 * m * 1024 <= 3 * n
+    if gathered:
+        return k <= 4096 and m * 1280 <= n
+    return 2 * m * 1024 <= 3 * n
 
 
 def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.Tensor,

@@ -307,7 +307,7 @@ def test_gptq_linear_forward_routes(dev, act_order, k, n):
     x = t_bf16(case["x_bits"], dev)
     routes = []
     for m in (1, 2, 3, 4, 8, 16, 21):
-        routes.append(ops.strip_rows_pays(m, n, act_order))
+        routes.append(ops.strip_rows_pays(m, k, n, act_order))
         y = lin(x[:m], out_dtype=torch.float32).cpu().numpy()
         assert rel_l2(y, case["y_ref"][:m]) < TOL_F32, m
     assert any(routes) and not all(routes)
