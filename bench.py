@@ -85,13 +85,18 @@ def bench_gemv(args, torch, pkg):
         x = torch.randn(1, k, device=dev, generator=torch.Generator(device=dev).manual_seed(7)).bfloat16()
         y = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
         ops.reserve_workspace(dev, ops.gemm_workspace_bytes(1, k, n, GROUP))
-        shapes.append(dict(name=name, k=k, n=n, copies=ws, x=x, y=y, bytes=per_copy))
+        shapes.append(dict(name=name, k=k, n=n, copies=ws, x=x, y=y, bytes=per_copy,
+                           rows=ops.strip_rows_pays(1, k, n, True)))
     torch.cuda.synchronize()
 
-    # The GPTQ module's M = 1 route (GPTQLinear.forward): the skinny strip GEMM over the
-    # strip copy of the group-sorted weight, x gathered through the act-order index while
-    # staging; the split-K GEMM over the AutoGPTQ layout is timed beside it.
+    # The GPTQ module's M = 1 route (GPTQLinear.forward, ops.strip_rows_pays): the skinny
+    # strip GEMM over the strip copy of the group-sorted weight with x gathered through the
+    # act-order index while staging, or the split-K GEMM over the AutoGPTQ layout, which is
+    # also timed on its own for every shape.
     def launch(s, i):
+        if not s["rows"]:
+            launch_split_k(s, i)
+            return
         qws, qz, sc, perm, qss = s["copies"][i % len(s["copies"])]
         ops.strip_rows_gemm(s["x"], qss, qz, sc, s["n"], GROUP, out=s["y"], perm=perm)
 
@@ -158,6 +163,7 @@ def bench_gemv(args, torch, pkg):
                               gbs=round(s["bytes"] / mean_us / 1e3, 1),
                               frac=round(s["bytes"] / mean_us / 1e3 / HBM_PEAK_GBS, 4),
                               split_k_us=round(sum(sk) / len(sk), 3),
+                              route="strip_rows" if s["rows"] else "split_k",
                               copies=len(s["copies"]))
     skinny = bench_skinny(args, torch, dev)
     step_bytes = sum(s["bytes"] for s in shapes)
@@ -168,8 +174,9 @@ def bench_gemv(args, torch, pkg):
         dtype="int4 weights, bf16 x, fp32 accumulate",
         config={"workload": "int4 GEMV sweep M=1 act-order g128: qkv 4096x6144, o 4096x4096, "
                             "gate_up 4096x24576, down 12288x4096 (one step = one layer's 4 GEMVs) "
-                            "on the GPTQ module's M=1 route (skinny strip GEMM, act-order "
-                            "gather while staging; split_k_us: the split-K GEMM)",
+                            "on the GPTQ module's M=1 route (per_kernel.route: the skinny "
+                            "strip GEMM with the act-order gather while staging, or the "
+                            "split-K GEMM; split_k_us: the split-K GEMM on every shape)",
                 "per_kernel": per, "step_bytes": step_bytes,
                 "skinny_gate_up": skinny},
         roofline={"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
