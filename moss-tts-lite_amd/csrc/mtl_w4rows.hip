@@ -43,6 +43,7 @@ struct RowsArgs {
   int M, K, N, group, zero_offset, out_f32, kblocks, xcd_order;
   int kp;                     // input channels per phase (a multiple of 256 dividing K)
   int ct;                     // strips per workgroup
+  int xraw;                   // act-order: x's M rows sit in LDS past the slice tiles
 };
 
 // Wave w serves strip w % CT over K slice w / CT (KW slices of NB blocks per phase, CT =
@@ -68,6 +69,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   u32x4* xa = smem;                                                   // [M + 1][XS]
   float* xg = reinterpret_cast<float*>(smem + (size_t)(a.M + 1) * XS);  // [pgrp][16]
   float* ytile = xg + 16 * pgrp;                                      // [nw][16][16]
+  uint16_t* xr = reinterpret_cast<uint16_t*>(ytile + nw * 256);       // xraw: [M][K]
 
   const int wave = wave_id();
   const int lane = threadIdx.x & 63;
@@ -81,7 +83,36 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   const int col = s * kStripCols + lj;
   const int rq0 = ks * 4 * NB;                 // the slice's first row quad (32 channels) in a phase
 
-  // 1. The weight ring and its group metadata go out first (they do not depend on x).
+  const int xbytes = (int)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, xbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(a.perm), (short)0, PERM ? a.K * 4 : 0, 0x00020000);
+  // Act-order with x resident (a.xraw): x's M rows go to LDS once, in 16-byte loads that
+  // a few cycles of the texture unit serve per wave instead of a cycle per gathered
+  // channel, and every phase gathers from there.  The first batch of those loads goes out
+  // ahead of the weight stream, so it does not queue behind it.
+  const int xr_items = PERM && a.xraw ? a.M * (a.K >> 3) : 0;
+  u32x4 rv[4];
+  auto raw_load = [&](int f0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int f = f0 + u * (int)blockDim.x + threadIdx.x;
+      const int m = f / (a.K >> 3), i = f - m * (a.K >> 3);
+      const int xo = f < xr_items ? (m * (int)a.ldx + 8 * i) * 2 : xbytes;
+      rv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+    }
+  };
+  auto raw_store = [&](int f0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int f = f0 + u * (int)blockDim.x + threadIdx.x;
+      if (f < xr_items) reinterpret_cast<u32x4*>(xr)[f] = rv[u];   // item m * K/8 + i
+    }
+  };
+  if (xr_items) raw_load(0);
+
+  // 1. The weight ring and its group metadata go out next (they do not depend on x).
   //    Block i of this wave's sequence (i = phase * NB + b) is K block phase * kbp + ks * NB + b.
   const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<u32x4*>(a.w), (short)0, (int)((int64_t)(N / kStripCols) * a.kblocks * 1024),
@@ -125,21 +156,29 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   // items per thread in flight: 4 (more spill registers of the MFMA loop: 16 rows of K = 4096
   // stage in three round trips)
   constexpr int BATCH = 4;
-  // x through bounds-checked buffer resources over the M rows (and the act-order index):
-  // an item past the last row reads 0, so a batch's loads carry no branch and go out
-  // together (a branch per load made the compiler wait for each before the next)
-  const int xbytes = (int)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2);
-  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.x), (short)0, xbytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int32_t*>(a.perm), (short)0, PERM ? a.K * 4 : 0, 0x00020000);
+  // x comes through bounds-checked buffer resources over the M rows (and the act-order
+  // index): an item past the last row reads 0, so a batch's loads carry no branch and go
+  // out together (a branch per load made the compiler wait for each before the next)
   auto stage = [&](int p) {
     const int nthr = blockDim.x;
     const int total = a.M * K8;
     const int c0 = p * a.kp;                   // the phase's first input row
     for (int f0 = 0; f0 < total; f0 += BATCH * nthr) {
       u32x4 v[BATCH];
-      if constexpr (PERM) {                    // act-order: 8 channels through the index
+      if (PERM && a.xraw) {                    // act-order, x resident in LDS
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+          const int f = f0 + u * nthr + threadIdx.x;
+          const int i = f - (f / K8) * K8;
+          const int po = f < total ? (c0 + 8 * i) * 4 : a.K * 4;   // past the end: 0
+          const int4 p0 = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po, 0, 0));
+          const int4 p1 = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po + 16, 0, 0));
+          const int mr = f / K8 < a.M ? f / K8 : a.M - 1;          // items past the end: unused
+          const uint16_t* xm = xr + mr * a.K;
+          v[u] = u32x4{xm[p0.x] | ((uint32_t)xm[p0.y] << 16), xm[p0.z] | ((uint32_t)xm[p0.w] << 16),
+                       xm[p1.x] | ((uint32_t)xm[p1.y] << 16), xm[p1.z] | ((uint32_t)xm[p1.w] << 16)};
+        }
+      } else if constexpr (PERM) {             // act-order: 8 channels through the index
         constexpr int HB = 1;                  // items per index batch (register budget)
 #pragma unroll
         for (int u0 = 0; u0 < BATCH; u0 += HB) {
@@ -189,6 +228,15 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
       }
     }
   };
+
+  if (xr_items) {
+    raw_store(0);
+    for (int f0 = 4 * (int)blockDim.x; f0 < xr_items; f0 += 4 * (int)blockDim.x) {
+      raw_load(f0);
+      raw_store(f0);
+    }
+    __syncthreads();
+  }
 
   // 3. MFMA over the slice's row quads as the ring delivers them.  Lane l supplies A row
   //    l%16 (x row m = l%16, the zero row when m >= M) and holds results D[4*(l/16) + r][l%16],
@@ -420,7 +468,10 @@ int strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K, const int32_t* 
   a.ct = g.ct;
   const int64_t G = N / (kStripCols * g.ct);
   a.xcd_order = G % 8 == 0;
-  const size_t lds = rows_lds(M, kp, group_size, g);
+  size_t lds = rows_lds(M, kp, group_size, g);
+  // act-order: x's rows resident in LDS when they fit beside the tile (M * K bf16)
+  a.xraw = perm && lds + (size_t)M * K * 2 <= kRowsMaxLds;
+  if (a.xraw) lds += (size_t)M * K * 2;
   hipStream_t st = (hipStream_t)stream;
   if (fmt == STRIP_META_QSZ) rows_group<STRIP_META_QSZ, false>(a, g, lds, st);
   else if (perm) rows_group<STRIP_META_GPTQ, true>(a, g, lds, st);

@@ -276,16 +276,15 @@ def strip_rows_pays(m: int, k: int, n: int, gathered: bool = False) -> bool:
     """Whether the skinny strip GEMM beats the split-K GEMM for ``m`` rows of a ``k x n``
     product on MI355X.  Each workgroup (one per CU) stages all m rows of x against the
     n k / 512 weight bytes a CU streams, so it pays while m * 1024 <= 1.5 n (every m <= 16
-    on gate|up's 24576 columns, m <= 6 on down's 4096).  With the act-order gather every
-    workgroup gathers all m * k channels of x two bytes per load, so it pays only for
-    k <= 4096 and while m * 1280 <= n (measured: m <= 4 on q|k|v's 6144 columns, m <= 3 on
-    o's 4096, every m <= 16 on gate|up; never on down, k = 12288).  The C drop-in
-    mtl_int4pack_mm uses the first rule."""
-    if m < 1 or m > _MAX_M:
+    on gate|up's 24576 columns, m <= 6 on down's 4096).  With the act-order gather, every
+    workgroup gathers all m * k channels: from x's rows held in LDS, which they fit at
+    m * k <= 32768, or else from memory, two bytes per load, which pays only on a wide
+    product (n >= 6 k: gate|up).  Measured: the gathered strip GEMM wins up to m = 8 on
+    q|k|v and o, m = 2 on down (to 4 with x resident), every m <= 16 on gate|up.  The C
+    drop-in mtl_int4pack_mm uses the first rule."""
+    if m < 1 or m > _MAX_M or 2 * m * 1024 > 3 * n:
         return False
-    if gathered:
-        return k <= 4096 and m * 1280 <= n
-    return 2 * m * 1024 <= 3 * n
+    return not gathered or m * k <= 32768 or n >= 6 * k
 
 
 def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.Tensor,

@@ -265,20 +265,28 @@ def test_strip_rows_k_phases(dev, group, k, n, m):
 
 
 @pytest.mark.parametrize("group,k,n,m", [(128, 4096, 6144, 8), (32, 2048, 1024, 3),
-                                         (128, 12288, 4096, 4), (256, 4096, 512, 16)])
+                                         (128, 12288, 4096, 4), (256, 4096, 512, 16),
+                                         (128, 12288, 4096, 1), (128, 4096, 24576, 16)])
 def test_strip_rows_act_order(dev, group, k, n, m):
     # act-order weights: the group-sorted copy in the strip layout, x gathered through the
-    # act-order index while staging; against float64 on the original (unsorted) weight
+    # act-order index while staging (from x's rows held in LDS where M * K fits beside the
+    # tile, else from memory); against float64 on the original (unsorted) weight
     cols = np.arange(0, n, 5)
     case = synth.gptq_case(k=k, n=n, m=m, group=group, act_order=True, seed=3 * group + k + m,
                            ref_cols=cols)
     qws, perm = ops.actorder_prepare(t_i32(case["qweight"], dev), t_i32(case["g_idx"], dev), group)
-    y = ops.strip_rows_gemm(t_bf16(case["x_bits"], dev), ops.strip_weights(qws),
-                            t_i32(case["qzeros"], dev), t_f16(case["scales"], dev), n, group,
-                            out_dtype=torch.float32, perm=perm)
-    err = rel_l2(y.cpu().numpy()[:, cols], case["y_ref"])
+    args = (ops.strip_weights(qws), t_i32(case["qzeros"], dev), t_f16(case["scales"], dev), n,
+            group)
+    y = ops.strip_rows_gemm(t_bf16(case["x_bits"], dev), *args, out_dtype=torch.float32,
+                            perm=perm).cpu().numpy()
+    err = rel_l2(y[:, cols], case["y_ref"])
     print(f"strip rows act-order g{group} {k}x{n} M={m} rel_l2={err:.2e}")
     assert err < TOL_F32
+    # the last row alone (x in LDS) is the same row of the batch bit for bit (at M = 16,
+    # gathered from memory): the same channels in the same order
+    one = ops.strip_rows_gemm(t_bf16(case["x_bits"][m - 1:m], dev), *args,
+                              out_dtype=torch.float32, perm=perm).cpu().numpy()
+    assert np.array_equal(one[0], y[m - 1])
 
 
 @pytest.mark.parametrize("group,k,n,m", [(128, 4096, 1024, 16), (32, 4096, 512, 5),
