@@ -111,6 +111,24 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
     }
   };
   if (xr_items) raw_load(0);
+  // x without the gather: the BATCH items per thread of phase items f0 + u * threads,
+  // through the bounds-checked resource (items past the M rows read 0)
+  constexpr int BATCH = 4;   // items per thread in flight (more spill the MFMA loop's registers)
+  auto x_batch = [&](int c0, int f0, u32x4 (&v)[BATCH]) {
+    const int nthr = blockDim.x;
+    const int total = a.M * K8;
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int f = f0 + u * nthr + threadIdx.x;
+      const int m = f / K8, i = f - m * K8;
+      const int xo = f < total ? (m * (int)a.ldx + c0 + 8 * i) * 2 : xbytes;
+      v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
+    }
+  };
+  // phase 0's first batch goes out ahead of the weight stream: loads return in issue order,
+  // so behind the ring it would wait for the ring's blocks
+  u32x4 xv0[BATCH];
+  if constexpr (!PERM) x_batch(0, 0, xv0);
 
   // 1. The weight ring and its group metadata go out next (they do not depend on x).
   //    Block i of this wave's sequence (i = phase * NB + b) is K block phase * kbp + ks * NB + b.
@@ -153,17 +171,36 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   for (int z = threadIdx.x; z < pgrp * 16; z += blockDim.x)
     if ((z & 15) >= a.M) xg[z] = 0.f;
   for (int z = threadIdx.x; z < K8; z += blockDim.x) xa[a.M * XS + z] = u32x4{0u, 0u, 0u, 0u};
-  // items per thread in flight: 4 (more spill registers of the MFMA loop: 16 rows of K = 4096
-  // stage in three round trips)
-  constexpr int BATCH = 4;
   // x comes through bounds-checked buffer resources over the M rows (and the act-order
   // index): an item past the last row reads 0, so a batch's loads carry no branch and go
   // out together (a branch per load made the compiler wait for each before the next)
-  auto stage = [&](int p) {
+  // a staged batch into LDS in pair order, with its per-group sums
+  auto put = [&](int f0, const u32x4 (&v)[BATCH]) {
+    const int nthr = blockDim.x;
+    const int total = a.M * K8;
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int fb = f0 + u * nthr + wave * 64;        // wave-uniform
+      if (fb >= total) break;
+      const int f = fb + lane;
+      float sum;
+      const u32x4 pv = pair_order(v[u], sum);
+#pragma unroll
+      for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
+      if (f < total) {                                 // M * K8 need not fill the wave
+        const int m = f / K8, i = f - m * K8;
+        xa[m * XS + i] = pv;
+        if ((i & (GI - 1)) == 0) xg[(i / GI) * 16 + m] = sum;
+      }
+    }
+  };
+  // phase p's items from item f_start on (phase 0 without the gather: its first batch went
+  // out ahead of the weight stream and is put before the first call)
+  auto stage = [&](int p, int f_start) {
     const int nthr = blockDim.x;
     const int total = a.M * K8;
     const int c0 = p * a.kp;                   // the phase's first input row
-    for (int f0 = 0; f0 < total; f0 += BATCH * nthr) {
+    for (int f0 = f_start; f0 < total; f0 += BATCH * nthr) {
       u32x4 v[BATCH];
       if (PERM && a.xraw) {                    // act-order, x resident in LDS
 #pragma unroll
@@ -203,29 +240,9 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
           }
         }
       } else {
-#pragma unroll
-        for (int u = 0; u < BATCH; ++u) {
-          const int f = f0 + u * nthr + threadIdx.x;
-          const int m = f / K8, i = f - m * K8;
-          const int xo = f < total ? (m * (int)a.ldx + c0 + 8 * i) * 2 : xbytes;
-          v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
-        }
+        x_batch(c0, f0, v);
       }
-#pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int fb = f0 + u * nthr + wave * 64;        // wave-uniform
-        if (fb >= total) break;
-        const int f = fb + lane;
-        float sum;
-        const u32x4 pv = pair_order(v[u], sum);
-#pragma unroll
-        for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
-        if (f < total) {                                 // M * K8 need not fill the wave
-          const int m = f / K8, i = f - m * K8;
-          xa[m * XS + i] = pv;
-          if ((i & (GI - 1)) == 0) xg[(i / GI) * 16 + m] = sum;
-        }
-      }
+      put(f0, v);
     }
   };
 
@@ -299,9 +316,11 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   // Every phase but the last refills in every turn (its last turn issues the next phase's
   // first blocks); the last phase peels its last turn, which issues nothing, so every
   // refill is unconditional inside a turn and the load waits stay exact.
+  if constexpr (!PERM) put(0, xv0);            // phase 0's first batch, loaded early
+  const int f_first = PERM ? 0 : BATCH * (int)blockDim.x;
   for (int p = 0; p < nphase - 1; ++p) {
     if (p > 0) __syncthreads();                // every wave is done with the last phase's x
-    stage(p);
+    stage(p, p == 0 ? f_first : 0);
     __syncthreads();
 #pragma unroll
     for (int b0 = 0; b0 < NB; b0 += WIN) turn(p, b0, true);
@@ -309,7 +328,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   {
     const int p = nphase - 1;
     if (p > 0) __syncthreads();
-    stage(p);
+    stage(p, p == 0 ? f_first : 0);
     __syncthreads();
 #pragma unroll
     for (int b0 = 0; b0 < NB - WIN; b0 += WIN) turn(p, b0, true);
