@@ -79,8 +79,11 @@ const char* mtl_status_string(int status);
 int mtl_abi_version(void);
 
 /* Bytes of workspace a GEMM of this shape needs: a 16 KB tile-counter region
- * followed by fp32 split-K partial tiles.  The counters must be zero before
- * first use (mtl_workspace_init zero-fills); every launch leaves them zero. */
+ * followed by fp32 split-K partial tiles.  mtl_gptq_gemm and mtl_w4_gemm_fused sum
+ * their partials in a second launch and read no counter, so their workspace needs no
+ * clearing; the entries that count workgroups (mtl_w4_gemm_residual and its _geom form)
+ * need the counters zero before first use (mtl_workspace_init zero-fills), and every launch
+ * leaves them zero. */
 int64_t mtl_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t group_size);
 int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream);
 

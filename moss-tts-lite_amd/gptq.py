@@ -149,16 +149,16 @@ class GPTQLinear(torch.nn.Module):
     def forward(self, x: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
         """``x[..., K] @ dequant(W)``.  Few rows run on the skinny strip GEMM where it pays
         (:func:`ops.strip_rows_pays`; it builds the strip copy of the weight once and keeps
-        it), the others on the split-K GEMM over the AutoGPTQ layout."""
+        it), the others on the split-K GEMM over the AutoGPTQ layout; both through the
+        ``torch.ops.mtl`` operators (one dispatcher call, torch's stream and allocator)."""
         qw, qz, sc, perm = self.kernel_args()
         m = x.numel() // self.in_features if self.in_features else 0
         if m and self.supports_strip() and ops.strip_rows_pays(m, self.in_features,
                                                                self.out_features, perm is not None):
             strip = self.stream_weight(strip=True)[0]
-            y = ops.strip_rows_gemm(x.reshape(m, self.in_features), strip, qz, sc,
-                                    self.out_features, self.group_size, self.zero_offset,
-                                    out_dtype=out_dtype, perm=perm)
-            return y.reshape(*x.shape[:-1], self.out_features)
+            return ops.torch_ops().strip_rows_gemm(x, strip, qz, sc, self.out_features,
+                                                   self.group_size, self.zero_offset, perm,
+                                                   out_dtype)
         return ops.gptq_gemm(x, qw, qz, sc, self.group_size, perm=perm,
                              zero_offset=self.zero_offset, out_dtype=out_dtype)
 

@@ -17,7 +17,6 @@ import torch
 
 from . import _native as N
 
-_GROUPS = (32, 64, 128, 256)
 _MAX_M = 16
 _ws_cache: dict = {}
 
@@ -93,13 +92,6 @@ def _check_x(x: torch.Tensor, k: int) -> torch.Tensor:
     return x.reshape(-1, k).contiguous()
 
 
-def _check_group(g: int, k: int) -> None:
-    if g not in _GROUPS:
-        raise RuntimeError(f"qGroupSize must be 32, 64, 128 or 256, got {g}")
-    if k % g:
-        raise RuntimeError(f"K={k} is not a multiple of group size {g}")
-
-
 def w4_gemm(x2: torch.Tensor, qweight: torch.Tensor, meta_format: int, meta0: torch.Tensor,
             qzeros, perm, n: int, group_size: int, zero_offset: int = 0,
             epilogue: int = N.EPI_NONE, resid=None, out: torch.Tensor | None = None,
@@ -130,22 +122,13 @@ def w4_gemm(x2: torch.Tensor, qweight: torch.Tensor, meta_format: int, meta0: to
 def gptq_gemm(x: torch.Tensor, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
               group_size: int, perm: torch.Tensor | None = None, zero_offset: int = 0,
               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """``x[..., K] @ dequant(W)[K, N]`` for the AutoGPTQ layout (fp32 accumulation)."""
-    k = qweight.shape[0] * 8
-    n = qweight.shape[1]
-    _check_group(group_size, k)
-    x2 = _check_x(x, k)
-    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
-        raise RuntimeError("qweight and qzeros must be int32")
-    if scales.dtype != torch.float16 or tuple(scales.shape) != (k // group_size, n):
-        raise RuntimeError(f"scales must be float16 [{k // group_size}, {n}]")
-    if tuple(qzeros.shape) != (k // group_size, n // 8):
-        raise RuntimeError(f"qzeros must be int32 [{k // group_size}, {n // 8}]")
-    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != k):
-        raise RuntimeError("perm must be int32 [K]")
-    y = w4_gemm(x2, qweight.contiguous(), N.META_GPTQ, scales.contiguous(), qzeros.contiguous(),
-                perm, n, group_size, zero_offset, out_dtype=out_dtype)
-    return y.reshape(*x.shape[:-1], n)
+    """``x[..., K] @ dequant(W)[K, N]`` for the AutoGPTQ layout (fp32 accumulation): the
+    ``torch.ops.mtl.gptq_gemm`` operator over ``mtl_gptq_gemm`` (split-K, 16 rows per launch,
+    the split partials in a workspace from torch's caching allocator).  ``perm`` is the
+    act-order index of :func:`actorder_prepare` for a group-sorted ``qweight``.
+    ``RuntimeError`` for a wrong shape, dtype or group size."""
+    return torch_ops().gptq_gemm(x, qweight, qzeros, scales, group_size, perm, zero_offset,
+                                 out_dtype)
 
 
 def torch_ops():

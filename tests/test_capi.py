@@ -328,3 +328,19 @@ def test_torch_operators_registered():
     assert tuple(mtl.convert_weight_to_int4pack(pre, 8).shape) == (64, 32, 32, 4)
     with pytest.raises(RuntimeError):
         mtl.convert_weight_to_int4pack(pre, 3)
+    # the GPTQ module's operators over the AutoGPTQ tensors: [..., K] in, [..., N] out
+    x3 = torch.empty(2, 3, 4096, dtype=torch.bfloat16, device="meta")
+    qw = torch.empty(512, 1024, dtype=torch.int32, device="meta")
+    qz = torch.empty(32, 128, dtype=torch.int32, device="meta")
+    sc = torch.empty(32, 1024, dtype=torch.float16, device="meta")
+    y = mtl.gptq_gemm(x3, qw, qz, sc, 128)
+    assert tuple(y.shape) == (2, 3, 1024) and y.dtype == torch.bfloat16
+    assert mtl.gptq_gemm(x3, qw, qz, sc, 128, out_dtype=torch.float32).dtype == torch.float32
+    with pytest.raises(RuntimeError):
+        mtl.gptq_gemm(x3, qw, qz, sc, 64)                     # scales of g128
+    with pytest.raises(RuntimeError):
+        mtl.gptq_gemm(x3, qw, qz, sc.float(), 128)
+    strip = torch.empty(4096 * 1024 // 8, dtype=torch.int32, device="meta")
+    assert tuple(mtl.strip_rows_gemm(x3, strip, qz, sc, 1024, 128).shape) == (2, 3, 1024)
+    with pytest.raises(RuntimeError):
+        mtl.strip_rows_gemm(x3, strip, qz, sc, 1024, 96)

@@ -573,6 +573,43 @@ def test_deterministic_and_graph_replay(dev):
         ops.gptq_gemm(x, qw, qz, sc, 128, perm=perm)   # eager work between replays
 
 
+def test_module_operators_match_c_entries(dev):
+    # torch.ops.mtl.gptq_gemm / strip_rows_gemm (the GPTQ module's eager path) run the C
+    # entries' kernels: the same bits, [..., K] in and [..., N] out, 16 rows per launch, and
+    # graph capture (the split partials then come from the graph's pool)
+    case = synth.gptq_case(k=4096, n=6144, m=21, group=128, act_order=True, seed=21,
+                           with_ref=False)
+    qws, perm = ops.actorder_prepare(t_i32(case["qweight"], dev),
+                                     torch.from_numpy(case["g_idx"]).to(dev), 128)
+    qz, sc = t_i32(case["qzeros"], dev), t_f16(case["scales"], dev)
+    x = t_bf16(case["x_bits"], dev)
+    mtl = ops.torch_ops()
+    y_op = mtl.gptq_gemm(x.view(3, 7, 4096), qws, qz, sc, 128, perm, 0, torch.float32)
+    y_c = ops.w4_gemm(x, qws, N.META_GPTQ, sc, qz, perm, 6144, 128, out_dtype=torch.float32)
+    assert tuple(y_op.shape) == (3, 7, 6144) and torch.equal(y_op.reshape(21, 6144), y_c)
+    strip = ops.strip_weights(qws)
+    s_op = mtl.strip_rows_gemm(x, strip, qz, sc, 6144, 128, 0, perm, torch.float32)
+    s_c = ops.strip_rows_gemm(x, strip, qz, sc, 6144, 128, perm=perm, out_dtype=torch.float32)
+    assert torch.equal(s_op, s_c)
+    x1 = x[:1]
+    eager = mtl.gptq_gemm(x1, qws, qz, sc, 128, perm)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mtl.gptq_gemm(x1, qws, qz, sc, 128, perm)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        out = mtl.gptq_gemm(x1, qws, qz, sc, 128, perm)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        mtl.gptq_gemm(x, qws, qz, sc, 128, perm)       # eager work between replays
+
+
 # ------------------------------------------------------------------ per-linear dispatch
 
 def test_w4_dispatch_modes(dev):
