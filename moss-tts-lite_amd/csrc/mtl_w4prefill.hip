@@ -8,7 +8,8 @@
 // over the block's four 32-channel chunks.  Group metadata is in the strip order of
 // mtl_w4_strip_meta.  Per quantisation group the MFMA sums A = sum x * (128 + q) exactly in
 // fp32 and the group adds s * (A - (128 + z) * X) with X the group's sum of x, as in the
-// decode GEMV.
+// decode GEMV; on the reference's qsz records, s * A + (d - 136 s) * X, two FMAs per output
+// with d - 136 s formed once per group and column (g = 32 folds every 32 channels).
 //
 // A workgroup (4 waves) owns a tile of 64 x rows by 8 strips (128 columns); wave w serves
 // strips 2w and 2w+1 for all 64 rows (4 MFMA row tiles), so one unpacked B operand feeds 4
@@ -171,7 +172,10 @@ w4_prefill_kernel(PrefillArgs a) {
             strip_meta_decode<MB>(mt[r][s], lj, a.zero_offset, gs[s], gz[s]);
           } else {
 #pragma unroll
-            for (int m = 0; m < MB; ++m) qsz_decode(mq[r][s][m], gs[s][m], gz[s][m], gd[s][m]);
+            for (int m = 0; m < MB; ++m) {
+              qsz_decode(mq[r][s][m], gs[s][m], gz[s][m], gd[s][m]);
+              gd[s][m] = fmaf(-gs[s][m], gz[s][m], gd[s][m]);   // d - s * c
+            }
           }
         }
       }
@@ -208,11 +212,12 @@ w4_prefill_kernel(PrefillArgs a) {
           const float X[4] = {X4.x, X4.y, X4.z, X4.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            tot[tt][0][i] = fmaf(gs[0][0], fmaf(-gz[0][0], X[i], acc[tt & 1][0][i]), tot[tt][0][i]);
-            tot[tt][1][i] = fmaf(gs[1][0], fmaf(-gz[1][0], X[i], acc[tt & 1][1][i]), tot[tt][1][i]);
-            if constexpr (FMT == STRIP_META_QSZ) {
-              tot[tt][0][i] = fmaf(gd[0][0], X[i], tot[tt][0][i]);
-              tot[tt][1][i] = fmaf(gd[1][0], X[i], tot[tt][1][i]);
+            if constexpr (FMT == STRIP_META_QSZ) {   // s * acc + (d - s * c) * X: two FMAs
+              tot[tt][0][i] = fmaf(gd[0][0], X[i], fmaf(gs[0][0], acc[tt & 1][0][i], tot[tt][0][i]));
+              tot[tt][1][i] = fmaf(gd[1][0], X[i], fmaf(gs[1][0], acc[tt & 1][1][i], tot[tt][1][i]));
+            } else {
+              tot[tt][0][i] = fmaf(gs[0][0], fmaf(-gz[0][0], X[i], acc[tt & 1][0][i]), tot[tt][0][i]);
+              tot[tt][1][i] = fmaf(gs[1][0], fmaf(-gz[1][0], X[i], acc[tt & 1][1][i]), tot[tt][1][i]);
             }
           }
           x_store_part(buf ^ 1, tt);             // block b + 1, loaded during block b - 1
@@ -247,11 +252,12 @@ w4_prefill_kernel(PrefillArgs a) {
             const float X[4] = {X4.x, X4.y, X4.z, X4.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              tot[tt][0][i] = fmaf(gs[0][m], fmaf(-gz[0][m], X[i], acc0[i]), tot[tt][0][i]);
-              tot[tt][1][i] = fmaf(gs[1][m], fmaf(-gz[1][m], X[i], acc1[i]), tot[tt][1][i]);
-              if constexpr (FMT == STRIP_META_QSZ) {
-                tot[tt][0][i] = fmaf(gd[0][m], X[i], tot[tt][0][i]);
-                tot[tt][1][i] = fmaf(gd[1][m], X[i], tot[tt][1][i]);
+              if constexpr (FMT == STRIP_META_QSZ) { // s * acc + (d - s * c) * X: two FMAs
+                tot[tt][0][i] = fmaf(gd[0][m], X[i], fmaf(gs[0][m], acc0[i], tot[tt][0][i]));
+                tot[tt][1][i] = fmaf(gd[1][m], X[i], fmaf(gs[1][m], acc1[i], tot[tt][1][i]));
+              } else {
+                tot[tt][0][i] = fmaf(gs[0][m], fmaf(-gz[0][m], X[i], acc0[i]), tot[tt][0][i]);
+                tot[tt][1][i] = fmaf(gs[1][m], fmaf(-gz[1][m], X[i], acc1[i]), tot[tt][1][i]);
               }
             }
           }
