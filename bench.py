@@ -280,7 +280,7 @@ def cpu_linear_datapoints(torch, shapes, budget_s: float = 1.2) -> dict:
     fp32 x @ W.T, tests/test_quant.py:104-107) and torch's CPU int4 GEMM
     (_weight_int4pack_mm_for_cpu) on each (name, K, N) shape at M = 1, g = 128, seeded
     codes and qsz, at 1 thread and at all of this process's threads: median microseconds
-    (BASELINE: >= 20 runs or the per-datapoint budget, at least 3)."""
+    (20 runs, or fewer within the per-datapoint time budget, at least 3)."""
     from oracle import cpu_path as C
 
     n_all = _cpu_threads()
@@ -585,7 +585,7 @@ def cpu_baseline_decode(torch, gpu_us: dict):
 
 
 def bench_int4_op(args, torch):
-    """The reference's decode operator beside this build's kernels, same GPU, graph-captured:
+    """The reference's decode operator beside the mtl kernels, same GPU, graph-captured:
     ``torch._weight_int4pack_mm`` on torch's own packed weights (moss_tts_lite/fast.py:118,
     the reference's int4 linear) and the ``mtl_int4pack_mm`` drop-in, M = 1, g = 128, on
     the four decode-step projections.  Each timing replays a graph of ``steps`` launches
@@ -856,7 +856,7 @@ def main():
                     help="K split of small grids, or one pass only (prefill workload)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the package has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     import torch

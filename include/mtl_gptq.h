@@ -41,7 +41,7 @@ enum {
   MTL_ERR_ALIGN = -4,         /* pointer not 16-byte aligned              */
   MTL_ERR_WORKSPACE = -5,     /* workspace missing or too small           */
   MTL_ERR_LAUNCH = -6,        /* HIP launch error                         */
-  MTL_ERR_UNSUPPORTED = -7    /* valid request this build does not serve  */
+  MTL_ERR_UNSUPPORTED = -7    /* valid request the library does not serve */
 };
 
 /* Output element type of the GEMM entry points. */

@@ -12,9 +12,9 @@ What a directory holds (the on-disk format, moss_tts_lite/export.py:29-32, 55, 4
 :func:`read_standalone` returns the reference reader's tuple ``(meta, weights, state,
 group_size_map, bf16_keep)``. There ``state[layer][linear] = {"packed", "qsz"}`` holds the
 tensors as stored. :class:`moss_tts_lite_amd.gptq.W4Dispatch` turns each ``packed`` into
-this build's layout on the GPU (``ops.int4pack_from_torch_tiles``).
+the strip layout on the GPU (``ops.int4pack_from_torch_tiles``).
 
-torch's tiled layout is not the same on every backend, and this build reads the ROCm one
+torch's tiled layout is not the same on every backend, and the package reads the ROCm one
 only. A directory whose ``tool.torch`` does not name a ROCm build is refused with
 ``ValueError`` rather than decoded into wrong weights.
 

@@ -7,7 +7,7 @@ copy an act-order checkpoint needs and forward runs the gfx950 int4 GEMV.
 
 The helpers mirror moss_tts_lite/gptq.py:35-97 on torch tensors
 (``rtn_quantize``, ``pack_fast``, ``pack_qsz_only``, ``effective_weight``) and
-``kernel_linear`` mirrors gptq.py:577-585 on this build's op.
+``kernel_linear`` mirrors gptq.py:577-585 on the mtl operator.
 """
 from __future__ import annotations
 
@@ -340,7 +340,7 @@ def pack_qsz_only(s: torch.Tensor, mn: torch.Tensor, group_size: int = 128) -> t
 
 def pack_fast(q: torch.Tensor, s: torch.Tensor, mn: torch.Tensor, inner_k_tiles: int = 8):
     """``(packed, qsz)`` for :func:`ops.weight_int4pack_mm` (gptq.py:66-77): the same
-    nibble pre-pack as the reference, converted to this build's layout."""
+    nibble pre-pack as the reference, converted to the strip layout."""
     q = q.to(torch.uint8).contiguous()
     qsz = pack_qsz_only(s, mn)
     pre = (q[:, 1::2] | (q[:, 0::2] << 4)).contiguous()
@@ -409,12 +409,12 @@ def split_keeps(bf16_keep) -> tuple[set, set]:
 
 
 class W4Dispatch:
-    """The reference's per-linear int4 dispatch on this build's kernels.
+    """The reference's per-linear int4 dispatch on the mtl kernels.
 
     Mirrors ``FastMossTTS._quantize/_linear`` (moss_tts_lite/fast.py:73-121) and
     ``GptqMossTTS._quantize/_linear`` (gptq.py:641-697):
     - ``qlayers[li]`` maps each quantised linear name to ``(packed, qsz)``, with ``packed``
-      in this build's ``[K/8, N]`` layout (:func:`ops.convert_weight_to_int4pack`);
+      in the strip ``[K/8, N]`` layout (:func:`ops.convert_weight_to_int4pack`);
       ``qlayers[li]`` is None for a layer with nothing quantised;
     - ``group_size_map[li][name]`` holds each linear's group size (``w4_group_size``
       unless ``group_size_map`` overrides it);

@@ -155,7 +155,7 @@ def weight_int4pack_mm(x: torch.Tensor, packed: torch.Tensor, q_group_size: int,
     the ``torch.ops.mtl.weight_int4pack_mm`` operator over ``mtl_int4pack_mm``.
 
     ``x`` bf16 ``[M, K]`` (any M); ``packed`` from :func:`convert_weight_to_int4pack` or
-    :func:`int4pack_from_torch_tiles` (torch's 4-D shape, this build's strip layout inside:
+    :func:`int4pack_from_torch_tiles` (torch's 4-D shape, the strip layout inside:
     a concatenation along dim 0 is a concatenation along N, as with torch's tiles);
     ``qScaleAndZeros`` bf16 ``[K/g, N, 2]`` = (scale, zero) with
     ``w = (q - 8) * scale + zero`` (moss_tts_lite/gptq.py:87-97).  Returns bf16 ``[M, N]``.
@@ -172,7 +172,7 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
 
     Input is the reference's nibble pre-pack (even k in the high nibble,
     moss_tts_lite/fast.py:98).  Output has torch's shape ``[N/8, K/(16 T), 32, T/2]`` int32
-    and holds this build's strip layout, not torch's tiled bytes: 16-column strips over all
+    and holds the strip layout, not torch's tiled bytes: 16-column strips over all
     of K, each one contiguous, so ``torch.cat(..., dim=0)`` of two packed weights is the
     packed concatenation of the weights along N (moss_tts_lite/fast_native.py:158-159).
     K % 256 == 0 and N % 16 == 0.
@@ -181,7 +181,7 @@ def convert_weight_to_int4pack(prepacked: torch.Tensor, inner_k_tiles: int = 8) 
 
 
 def int4pack_from_torch_tiles(tiles: torch.Tensor) -> torch.Tensor:
-    """torch's tiled int4 tensor -> this build's packed weight (mtl_int4pack_from_torch_tiles),
+    """torch's tiled int4 tensor -> the strip-layout packed weight (mtl_int4pack_from_torch_tiles),
     in the same ``[N/8, K/(16T), 32, T/2]`` shape.
 
     ``tiles`` is int32 ``[N/8, K/(16T), 32, T/2]`` as ``aten._convert_weight_to_int4pack(pre,

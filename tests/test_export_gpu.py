@@ -2,7 +2,7 @@
 and of the drop-in int4 operators against torch's own ROCm packer and int4 GEMM.
 
 The export's ``.q`` records are torch's tiled int4 tensors.  Bars: the converted
-``[K/8, N]`` words bit-exact against this build's packer of the same codes (torch's tiles
+``[K/8, N]`` words bit-exact against the mtl packer of the same codes (torch's tiles
 from the committed fixtures and from torch's packer run live at the model's shapes); the
 int4 GEMM on an ingested export within rel-L2 1e-2 of ``torch._weight_int4pack_mm`` on
 the export's own tiles (the reference's kernel) and of the oracle's float64 product.
@@ -122,7 +122,7 @@ def test_ingested_export_matches_torch_int4pack_mm(dev, tmp_path):
                                      (2, 4096, 2048, 256)])
 def test_drop_in_matches_torch_int4_operators(dev, m, k, n, g):
     # the reference's two operators on ROCm (fast.py:97-99, 118): torch's packer + int4 GEMM,
-    # against this build's drop-ins on the same pre-pack bytes, qsz and x
+    # against the mtl drop-ins on the same pre-pack bytes, qsz and x
     print("shape", m, k, n, g, flush=True)
     gen = torch.Generator().manual_seed(m * 131 + k + n + g)
     codes = torch.randint(0, 16, (n, k), generator=gen, dtype=torch.int32)
