@@ -363,6 +363,23 @@ int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, 
                               int64_t partials_bytes, void* stream);
 
 /*
+ * mtl_w4_gemm_norm_partials and mtl_bf16_gemv_norm(bh, bnorm_w, slots, eps, bweight, bn,
+ * K, bout) over the same slots (the RMS of h) in one launch: the decode step's int4 q|k
+ * GEMV beside its bf16-kept v_proj (the w2 preset keeps v_proj in bf16, gptq.py:689-697;
+ * moss_tts_lite/model.py:169-173 forms q, k and v from the same normed h), or the int4
+ * gate beside a kept up_proj.  With the strip layout, one strip per workgroup of 4 waves
+ * and K <= 4096 the first N/16 workgroups run the GEMV and the rest the bf16 rows;
+ * otherwise the two launches are issued.  Either way the results are the two entries'
+ * bits.  bh, bnorm_w, bweight 16-byte aligned; bweight bf16 [bn, K]; bout fp32 [bn].
+ */
+int mtl_w4_gemm_norm_partials_bf16(const void* h, const void* w, const float* slots, float eps,
+                                   int64_t K, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, int64_t N, int32_t group_size,
+                                   int32_t zero_offset, int32_t layout, float* partials,
+                                   int64_t partials_bytes, const void* bh, const void* bnorm_w,
+                                   const void* bweight, int64_t bn, float* bout, void* stream);
+
+/*
  * M = 1 GEMV whose epilogue is the decode step's residual add (moss_tts_lite/fast.py:
  * 168-171): h[n] = bf16(bf16((x @ W)[n]) + h[n]) in place, h scattered into the next
  * RMSNorm-staged GEMV's act-order input order (h_ord[scatter[n]] = h[n]; scatter NULL:

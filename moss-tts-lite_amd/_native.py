@@ -86,6 +86,10 @@ _SIGNATURES = {
     "mtl_w4_gemm_norm_partials": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _i64,
                                          _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                          _c_void_p, _i64, _c_void_p]),
+    "mtl_w4_gemm_norm_partials_bf16": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
+                                              _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i32,
+                                              _i32, _i32, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                              _c_void_p, _i64, _c_void_p, _c_void_p]),
     "mtl_w4_gemm_strip_rows": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _i64, _i32, _i32, _c_void_p, _i64, _i32, _c_void_p]),
     "mtl_w4_gemm_strip_rows_ex": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,

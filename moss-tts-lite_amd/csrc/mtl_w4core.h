@@ -185,6 +185,10 @@ enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };
 int strip_blocks_per_wave(int64_t K, int ct, int group);
 // Launch the strip GEMV; shapes, pointers and alignment are checked by the caller.
 int strip_launch(const StripArgs& a, hipStream_t stream);
+struct Bf16RowsArgs;
+// The RMSNorm-staged strip GEMV and a bf16 kept projection (gb workgroups of its rows) in
+// one launch; MTL_ERR_UNSUPPORTED where that launch shape does not apply.
+int strip_launch_bf16(const StripArgs& a, const Bf16RowsArgs& b, int gb, hipStream_t stream);
 
 // The skinny-batch strip GEMM (mtl_w4rows.hip) for 1 <= M <= 16 rows: fmt is STRIP_META_*,
 // perm (GPTQ metadata only) gathers x's channels; checks shapes and alignment itself.

@@ -28,8 +28,23 @@
 // accumulated sum A = sum x*(128+q) and X = sum x give
 //     sum x*w = s * (A - (128 + c) * X) + d * X.
 #include "mtl_w4core.h"
+#include "mtl_bf16rows.h"
+#include "mtl_decode.h"
 
 namespace mtl {
+
+static int g_gemm_cus = 0;
+
+static int gemm_device_cus() {
+  if (!g_gemm_cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_gemm_cus = n;
+  }
+  return g_gemm_cus;
+}
 
 constexpr int kTileN = 256;        // output columns per workgroup (4 waves)
 constexpr int kWaveN = 64;         // output columns per wave (16 lanes x 4)
@@ -841,12 +856,12 @@ static int w4_gemm_partials(const void* x, const float* xpart, int xsplits, int6
 }
 
 // Partials-only launch whose input is RMSNorm(h) computed while staging (M = 1).
-static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const float* slots,
-                                 float eps, int64_t K, const int32_t* qweight,
-                                 const void* meta0, const int32_t* qzeros, int64_t N, int group,
-                                 int zero_offset, int layout, float* partials,
-                                 int64_t partials_bytes, hipStream_t stream,
-                                 const mtl_strip_geometry* geom = nullptr) {
+// Arguments of the RMSNorm-staged GEMV; for the strip layout also its launch arguments.
+static int norm_partials_check(const void* h_ord, const void* w_ord, const float* slots,
+                               float eps, int64_t K, const int32_t* qweight, const void* meta0,
+                               const int32_t* qzeros, int64_t N, int group, int zero_offset,
+                               int layout, float* partials, int64_t partials_bytes,
+                               StripArgs* sa) {
   if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (!h_ord || !w_ord || !slots || !qweight || !meta_given(layout, meta0, qzeros) || !partials)
     return MTL_ERR_INVALID_ARG;
@@ -859,12 +874,28 @@ static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const flo
   if (is_strip(layout)) {   // full-K strips: the final sums, as one split
     if (partials_bytes < N * 4) return MTL_ERR_WORKSPACE;
     if (!strip_meta_aligned(layout, meta0, qzeros)) return MTL_ERR_ALIGN;
-    StripArgs sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
-    sa.hn = static_cast<const uint16_t*>(h_ord);
-    sa.wn = static_cast<const uint16_t*>(w_ord);
-    sa.slots = slots;
-    sa.eps = eps;
-    sa.y = partials;
+    *sa = strip_args(K, qweight, meta0, qzeros, N, group, zero_offset, layout);
+    sa->hn = static_cast<const uint16_t*>(h_ord);
+    sa->wn = static_cast<const uint16_t*>(w_ord);
+    sa->slots = slots;
+    sa->eps = eps;
+    sa->y = partials;
+  }
+  return MTL_OK;
+}
+
+static int w4_gemm_norm_partials(const void* h_ord, const void* w_ord, const float* slots,
+                                 float eps, int64_t K, const int32_t* qweight,
+                                 const void* meta0, const int32_t* qzeros, int64_t N, int group,
+                                 int zero_offset, int layout, float* partials,
+                                 int64_t partials_bytes, hipStream_t stream,
+                                 const mtl_strip_geometry* geom = nullptr) {
+  StripArgs sa;
+  if (const int st = norm_partials_check(h_ord, w_ord, slots, eps, K, qweight, meta0, qzeros, N,
+                                         group, zero_offset, layout, partials, partials_bytes,
+                                         &sa))
+    return st;
+  if (is_strip(layout)) {
     if (geom) sa.geom = *geom;
     return strip_launch(sa, stream);
   }
@@ -1061,6 +1092,38 @@ int mtl_w4_gemm_norm_partials(const void* h, const void* w, const float* slots, 
   return w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N,
                                group_size, zero_offset, layout, partials, partials_bytes,
                                (hipStream_t)stream);
+}
+
+int mtl_w4_gemm_norm_partials_bf16(const void* h, const void* w, const float* slots, float eps,
+                                   int64_t K, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, int64_t N, int32_t group_size,
+                                   int32_t zero_offset, int32_t layout, float* partials,
+                                   int64_t partials_bytes, const void* bh, const void* bnorm_w,
+                                   const void* bweight, int64_t bn, float* bout, void* stream) {
+  if (!bh || !bnorm_w || !bweight || !bout) return MTL_ERR_INVALID_ARG;
+  if (bn < 1 || K % 8 != 0) return MTL_ERR_SHAPE;
+  if (!aligned16(bh) || !aligned16(bnorm_w) || !aligned16(bweight)) return MTL_ERR_ALIGN;
+  StripArgs sa;
+  if (const int st = norm_partials_check(h, w, slots, eps, K, qweight, scales, qzeros, N,
+                                         group_size, zero_offset, layout, partials,
+                                         partials_bytes, &sa))
+    return st;
+  if (is_strip(layout) && K <= 4096) {   // one launch where its shape applies
+    const int rpw = bf16_rows_per_wg(bn, gemm_device_cus());
+    const int64_t gb = (bn + rpw - 1) / rpw;
+    if (gb + N / 16 < ((int64_t)1 << 31) && (int64_t)rpw * K * 2 < ((int64_t)1 << 31)) {
+      const Bf16RowsArgs b{static_cast<const uint16_t*>(bh), static_cast<const uint16_t*>(bnorm_w),
+                           slots, eps, static_cast<const uint16_t*>(bweight), bn, (int)K, rpw,
+                           bout};
+      const int st = strip_launch_bf16(sa, b, (int)gb, (hipStream_t)stream);
+      if (st != MTL_ERR_UNSUPPORTED) return st;
+    }
+  }
+  if (const int st = w4_gemm_norm_partials(h, w, slots, eps, K, qweight, scales, qzeros, N,
+                                           group_size, zero_offset, layout, partials,
+                                           partials_bytes, (hipStream_t)stream))
+    return st;
+  return mtl_bf16_gemv_norm(bh, bnorm_w, slots, eps, bweight, bn, K, bout, stream);
 }
 
 int mtl_w4_gemm_residual(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,

@@ -19,6 +19,7 @@
 // column sums of a strip meet in LDS and are added in slice order, so results are
 // bitwise repeatable.
 #include "mtl_w4core.h"
+#include "mtl_bf16rows.h"
 
 namespace mtl {
 
@@ -38,9 +39,10 @@ constexpr int strip_max_waves(int gr, int nb, int win) {
 }
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
 
+// The body of one workgroup: `bid` of a launch of G strip workgroups (the kernel's own
+// grid, or the first G workgroups of the combined launch below).
 template <int GR, int XSRC, int EPI, int NB, int CT, int WIN, int FMT>
-__global__ void __launch_bounds__(64 * strip_max_waves(GR, NB, WIN), 1)
-w4_strip_kernel(StripArgs a) {
+__device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, const int G) {
   constexpr int ITEMS = 16 * NB;               // x items (8 channels) per K slice
   constexpr int STAGERS = 64 * CT;             // threads that stage one slice
   constexpr int ROUNDS = (ITEMS + STAGERS - 1) / STAGERS;
@@ -62,8 +64,7 @@ w4_strip_kernel(StripArgs a) {
   // Workgroups go to the 8 XCDs round robin; with xcd_order, XCD x runs the contiguous
   // workgroups x*G/8 .. (x+1)*G/8 - 1, so the cache lines of scales and zeros that
   // neighbouring strips share are fetched into one L2 only.
-  const int G = gridDim.x;
-  const int wg = a.xcd_order ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int wg = a.xcd_order ? (bid & 7) * (G >> 3) + (bid >> 3) : bid;
   // SiLU*up: the workgroup holds P = CT/2 (gate, up) strip pairs; pair p is the gate strip
   // 4*(p/2) + p%2 and its up partner two strips (32 columns) to the right, in the gate|up
   // interleave of 32-column blocks.  Waves cs < P serve the gate strips of pairs
@@ -397,6 +398,25 @@ static bool ring_built(int gr, int nb, int win, int fmt) {
   }
 }
 
+template <int GR, int XSRC, int EPI, int NB, int CT, int WIN, int FMT>
+__global__ void __launch_bounds__(64 * strip_max_waves(GR, NB, WIN), 1)
+w4_strip_kernel(StripArgs a) {
+  strip_body<GR, XSRC, EPI, NB, CT, WIN, FMT>(a, blockIdx.x, gridDim.x);
+}
+
+// The RMSNorm-staged GEMV (one strip per workgroup, 4 waves) and a bf16 kept projection
+// over the same h in one launch: workgroups below ga run the strip GEMV, the others the
+// bf16 rows (mtl_bf16rows.h).  Two dependent launches become one, and the two products
+// stream at once (the kept v_proj beside the int4 q|k of the MOSS step).
+template <int GR, int NB, int WIN, int FMT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+w4_strip_bf16_kernel(StripArgs a, Bf16RowsArgs b, int ga) {
+  if ((int)blockIdx.x < ga)
+    strip_body<GR, XSRC_RMSNORM, STRIP_EPI_STORE, NB, 1, WIN, FMT>(a, blockIdx.x, ga);
+  else
+    bf16_rows_norm_body<8>(b, (int)blockIdx.x - ga);
+}
+
 // Resolve the launch shape of a: the requested geometry, automatic where a field is 0.
 // Strips per workgroup: SiLU*up 2 (one gate|up pair) or 6 (three pairs); the RMSNorm-staged
 // store 1, 2 or 4; the others 1.  The reference's qsz metadata takes the automatic CT.
@@ -497,6 +517,47 @@ int strip_launch(const StripArgs& args, hipStream_t st) {
   if (a.fmt == STRIP_META_QSZ) strip_group<STRIP_META_QSZ>(a, g, st);
   else strip_group<STRIP_META_GPTQ>(a, g, st);
   return launch_status();
+}
+
+// The combined launch of an RMSNorm-staged strip GEMV (XSRC_RMSNORM, store epilogue) and
+// a bf16 kept projection; MTL_ERR_UNSUPPORTED where its shape does not apply (the caller
+// then issues the two launches): one strip per workgroup in 4 waves, K <= 4096.
+template <int GR, int FMT>
+static int strip_bf16_group(const StripArgs& a, const StripGeom& g, const Bf16RowsArgs& b,
+                            int gb, hipStream_t st) {
+  const int ga = a.N / kStripCols;
+  const dim3 grid(ga + gb), block(256);
+  const size_t lds = (size_t)(a.kblocks / g.nb) * 16 * g.nb * sizeof(u32x4);
+#define MTL_STRIP_BF16(NB_, WIN_) \
+  hipLaunchKernelGGL((w4_strip_bf16_kernel<GR, NB_, WIN_, FMT>), grid, block, lds, st, a, b, ga)
+  if (g.nb == 8 && g.win == 4) MTL_STRIP_BF16(8, 4);
+  else if (g.nb == 8 && g.win == 2) MTL_STRIP_BF16(8, 2);
+  else return MTL_ERR_UNSUPPORTED;
+#undef MTL_STRIP_BF16
+  return MTL_OK;
+}
+
+int strip_launch_bf16(const StripArgs& args, const Bf16RowsArgs& b, int gb, hipStream_t st) {
+  StripArgs a = args;
+  StripGeom g;
+  if (!a.hn || a.h || a.act || a.xpart) return MTL_ERR_UNSUPPORTED;
+  if (const int status = strip_geometry(a, g)) return status;
+  a.kblocks = a.K / kStripBlockK;
+  if (g.ct != 1 || 64 * (a.kblocks / g.nb) != 256 || a.K > 4096 || b.K != a.K)
+    return MTL_ERR_UNSUPPORTED;
+  a.xcd_order = a.geom.xcd_order != -1 && (a.N / kStripCols) % 8 == 0;
+  int st_code = MTL_ERR_UNSUPPORTED;
+  switch (a.group) {
+    case 32: st_code = a.fmt == STRIP_META_QSZ ? strip_bf16_group<1, STRIP_META_QSZ>(a, g, b, gb, st)
+                                               : strip_bf16_group<1, STRIP_META_GPTQ>(a, g, b, gb, st); break;
+    case 64: st_code = a.fmt == STRIP_META_QSZ ? strip_bf16_group<2, STRIP_META_QSZ>(a, g, b, gb, st)
+                                               : strip_bf16_group<2, STRIP_META_GPTQ>(a, g, b, gb, st); break;
+    case 128: st_code = a.fmt == STRIP_META_QSZ ? strip_bf16_group<4, STRIP_META_QSZ>(a, g, b, gb, st)
+                                                : strip_bf16_group<4, STRIP_META_GPTQ>(a, g, b, gb, st); break;
+    default: st_code = a.fmt == STRIP_META_QSZ ? strip_bf16_group<8, STRIP_META_QSZ>(a, g, b, gb, st)
+                                               : strip_bf16_group<8, STRIP_META_GPTQ>(a, g, b, gb, st); break;
+  }
+  return st_code ? st_code : launch_status();
 }
 
 // Strip layout (see the top of this file); rows past K/8 never occur (K % 256 == 0).

@@ -335,16 +335,14 @@ class FastDecoder:
                                               self.x_qkv.data_ptr(), self.slots.data_ptr(),
                                               cfg.hidden)))
         qkv_splits = self.splits["qkv"]
-        if self.v_keep[li]:
+        if self.v_keep[li]:   # the int4 q|k GEMV and the bf16 v_proj in one launch
             nqk = lyr["qkv"].out_features
-            plan += [
+            launches = self._with_bf16(
                 self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"], nqk, "qkv",
                                     strip=True),
-                ("mtl_bf16_gemv_norm", (self.h.data_ptr(), lyr["input_layernorm"].data_ptr(),
-                                        self.slots.data_ptr(), eps, lyr["v_keep"].data_ptr(),
-                                        lyr["v_keep"].shape[0], cfg.hidden,
-                                        self.part["qkv"][nqk:].data_ptr())),
-            ]
+                lyr["input_layernorm"], lyr["v_keep"], self.part["qkv"][nqk:])
+            self._keep_launches[(li, "v")] = len(launches)
+            plan += launches
             qkv_splits = 1
         else:
             plan.append(self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"],
@@ -363,12 +361,12 @@ class FastDecoder:
         if self.up_keep[li]:   # int4 gate and bf16 up into fp32 halves, then SiLU*up
             inter = cfg.intermediate
             gu = self.part["gate_up"]
-            plan += [
+            launches = self._with_bf16(
                 self._norm_partials(self.x_gu, self.norm_gu[li], lyr["gate_up"], inter,
                                     "gate_up", strip=True),
-                ("mtl_bf16_gemv_norm", (self.h.data_ptr(), lyr["post_attention_layernorm"].data_ptr(),
-                                        self.slots.data_ptr(), eps, lyr["up_keep"].data_ptr(),
-                                        inter, cfg.hidden, gu[inter:].data_ptr())),
+                lyr["post_attention_layernorm"], lyr["up_keep"], gu[inter:])
+            self._keep_launches[(li, "up")] = len(launches)
+            plan += launches + [
                 ("mtl_silu_mul_f32", (gu.data_ptr(), gu[inter:].data_ptr(), self.act.data_ptr(),
                                       inter)),
                 self._residual(self.act, None, lyr["down"],
@@ -391,6 +389,21 @@ class FastDecoder:
                                None if last else self.x_qkv),
             ]
         return plan
+
+    def _with_bf16(self, gemv, norm_w, keep, out):
+        """An RMSNorm-staged int4 GEMV launch joined by the bf16-kept projection of the same
+        normed h (``mtl_w4_gemm_norm_partials_bf16``: one launch where its shape applies,
+        the same bits as the two); with an explicit launch geometry, the two launches."""
+        eps = ctypes.c_float(self.m.cfg.eps)
+        rows = ("mtl_bf16_gemv_norm", (self.h.data_ptr(), norm_w.data_ptr(), self.slots.data_ptr(),
+                                       eps, keep.data_ptr(), keep.shape[0], self.m.cfg.hidden,
+                                       out.data_ptr()))
+        name, args = gemv
+        if name != "mtl_w4_gemm_norm_partials":
+            return [gemv, rows]
+        return [("mtl_w4_gemm_norm_partials_bf16",
+                 args + (self.h.data_ptr(), norm_w.data_ptr(), keep.data_ptr(), keep.shape[0],
+                         out.data_ptr()))]
 
     def _norm_silu(self, h_ord, w_ord, lin):
         qw, layout, sc, qz = self._weight(lin, True)
@@ -457,6 +470,7 @@ class FastDecoder:
                                           self.table_ptrs.data_ptr(), self.vocabs.data_ptr(),
                                           cfg.hidden, self.h.data_ptr()))]
         if self.plan in ("fused", "strip"):
+            self._keep_launches = {}
             self._layers = [self._layer_plan_resid(li) for li in range(cfg.n_layers)]
         elif self.plan == "staged":
             self._layers = [self._layer_plan_staged(li) for li in range(cfg.n_layers)]
@@ -474,7 +488,8 @@ class FastDecoder:
                       "mtl_bf16_gemv_argmax_norm", "mtl_bf16_gemv", "mtl_w4_gemm_residual",
                       "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32",
                       "mtl_w4_gemm_partials_geom", "mtl_w4_gemm_norm_partials_geom",
-                      "mtl_w4_gemm_residual_geom", "mtl_w4_gemm_norm_silu_geom")}
+                      "mtl_w4_gemm_residual_geom", "mtl_w4_gemm_norm_silu_geom",
+                      "mtl_w4_gemm_norm_partials_bf16")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -524,9 +539,9 @@ class FastDecoder:
         """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
         shift = 1 if self.plan in ("fused", "strip") and li == 0 else 0   # layer 0: the stats
         if self.v_keep[li] and name != "qkv":
-            shift += 1                                                     # the bf16 v launch
+            shift += self._keep_launches[(li, "v")] - 1                    # a separate bf16 v
         if self.up_keep[li] and name == "down":
-            shift += 2                                                     # bf16 up, SiLU*up
+            shift += self._keep_launches[(li, "up")]                       # bf16 up?, SiLU*up
         return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:

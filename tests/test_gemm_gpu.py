@@ -851,6 +851,58 @@ def test_strip_norm_staging_matches_oracle(dev):
     assert err < TOL_F32
 
 
+@pytest.mark.parametrize("fmt,group,n,bn", [("gptq", 128, 6144, 1024), ("gptq", 32, 5120, 1024),
+                                            ("qsz", 32, 5120, 1024), ("qsz", 32, 12288, 12288),
+                                            ("rows", 128, 4096, 37)])
+def test_norm_partials_bf16_one_launch(dev, fmt, group, n, bn):
+    # the RMSNorm-staged int4 GEMV and a bf16-kept projection of the same h in one entry
+    # (the MOSS step's q|k + v_proj, gate + up_proj): the same bits as the two entries,
+    # whether it runs as one launch (strip layouts) or as the two (the split-K layout)
+    import ctypes
+    from tests._decode_case import slots16
+    lib = N.load()
+    k = 4096
+    r = np.random.default_rng(group + n + bn)
+    hf = bf16_bits_to_f32(f32_to_bf16_bits(r.standard_normal(k).astype(np.float32)))
+    wf = bf16_bits_to_f32(f32_to_bf16_bits((1 + 0.1 * r.standard_normal(k)).astype(np.float32)))
+    h, wn = t_bf16(f32_to_bf16_bits(hf), dev), t_bf16(f32_to_bf16_bits(wf), dev)
+    w2 = t_bf16(f32_to_bf16_bits((1 + 0.1 * r.standard_normal(k)).astype(np.float32)), dev)
+    slots = torch.from_numpy(slots16(hf)).to(dev)
+    bw = t_bf16(f32_to_bf16_bits((r.standard_normal((bn, k)) * 0.05).astype(np.float32)), dev)
+    if fmt == "qsz":
+        q, qsz = _qsz_weights(r, n, k, group)
+        qw = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+        meta, qz, layout = t_bf16(qsz, dev), None, N.LAYOUT_STRIP_QSZ
+    else:
+        case = synth.gptq_case(k=k, n=n, m=1, group=group, seed=n + bn, with_ref=False)
+        qw, qz = t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev)
+        meta, layout = t_f16(case["scales"], dev), N.LAYOUT_ROWS
+        if fmt == "gptq":
+            qw = ops.strip_weights(qw)
+            meta, qz = ops.strip_meta(meta, qz, group)
+            layout = N.LAYOUT_STRIP
+    ws = int(lib.mtl_w4_gemm_splits(k, n)) * n if layout == N.LAYOUT_ROWS else n
+    st = torch.cuda.current_stream().cuda_stream
+    eps = ctypes.c_float(1e-6)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    y1 = torch.full((ws,), float("nan"), dtype=torch.float32, device=dev)
+    b1 = torch.full((bn,), float("nan"), dtype=torch.float32, device=dev)
+    N.check(lib.mtl_w4_gemm_norm_partials(h.data_ptr(), wn.data_ptr(), slots.data_ptr(), eps, k,
+                                          qw.data_ptr(), meta.data_ptr(), p(qz), n, group, 0,
+                                          layout, y1.data_ptr(), ws * 4, st), "norm partials")
+    N.check(lib.mtl_bf16_gemv_norm(h.data_ptr(), w2.data_ptr(), slots.data_ptr(), eps,
+                                   bw.data_ptr(), bn, k, b1.data_ptr(), st), "bf16 rows")
+    y2, b2 = torch.full_like(y1, float("nan")), torch.full_like(b1, float("nan"))
+    N.check(lib.mtl_w4_gemm_norm_partials_bf16(h.data_ptr(), wn.data_ptr(), slots.data_ptr(), eps,
+                                               k, qw.data_ptr(), meta.data_ptr(), p(qz), n, group,
+                                               0, layout, y2.data_ptr(), ws * 4, h.data_ptr(),
+                                               w2.data_ptr(), bw.data_ptr(), bn, b2.data_ptr(),
+                                               st), "one launch")
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(b1, b2)
+    assert torch.isfinite(y2).all() and torch.isfinite(b2).all()
+
+
 @pytest.mark.parametrize("xsplits", [1, 8])
 def test_strip_silu_staging_matches_split_k(dev, xsplits):
     # same SiLU*up staging (bitwise equal x) as the split-K GEMV; only the fp32 summation
