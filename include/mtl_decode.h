@@ -36,6 +36,18 @@ int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* table
                   const int64_t* vocabs, int64_t hidden, void* out, void* stream);
 
 /*
+ * mtl_embed_sum that also prepares the first decoder layer's RMSNorm-staged GEMV
+ * (the input RMSNorm of moss_tts_lite/model.py:169 on the summed embedding): the same out, plus
+ *   slots   float [hidden / 16]: sum of squares of out's columns 16b .. 16b+15, bit for bit
+ *           as mtl_residual_add forms it with part = NULL
+ *   h_ord   bf16 [hidden] or NULL: h_ord[scatter[d]] = out[d] (scatter NULL: h_ord[d])
+ * hidden % 256 == 0 and hidden <= 16384, else MTL_ERR_SHAPE.
+ */
+int mtl_embed_sum_stats(const int64_t* ids, int32_t n_tables, const void* const* tables,
+                        const int64_t* vocabs, int64_t hidden, void* out,
+                        const int32_t* scatter, void* h_ord, float* slots, void* stream);
+
+/*
  * Per-head q/k RMSNorm, RoPE and KV-cache write for one decode position
  * (moss_tts_lite/fast.py:134-147, model.py:175-185).
  *   qkv      bf16 [(n_heads + 2*n_kv_heads) * head_dim] = q | k | v projections

@@ -46,6 +46,8 @@ _SIGNATURES = {
     # mtl_decode.h
     "mtl_rmsnorm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, ctypes.c_float, _c_void_p]),
     "mtl_embed_sum": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "mtl_embed_sum_stats": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i64, _c_void_p,
+                                   _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "mtl_qk_norm_rope_kv": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64,
                                    ctypes.c_float, _c_void_p]),

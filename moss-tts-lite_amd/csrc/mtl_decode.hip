@@ -190,10 +190,18 @@ __global__ void __launch_bounds__(64) residual_add_kernel(
 constexpr int kEmbedMaxTables = 64;
 constexpr int kEmbedBatch = 17;      // table rows whose loads are in flight together (MOSS: 33 in two)
 
+// STATS: also the first RMSNorm's statistics of the sum and its copy in the first GEMV's
+// input order, as residual_add_kernel forms them after a residual add: slots[b] = the sum
+// of squares of columns 16b .. 16b+15 (each 4 consecutive columns by a chain of FMAs, the
+// four chains joined as slot_combine joins them, so the bits are the same) and
+// h_ord[scatter[d]] = out[d] (scatter NULL: h_ord[d]; h_ord NULL: no copy).  Every lane of
+// a wave holds a column (hidden % 64 == 0).
+template <bool STATS>
 __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
                                  const uint16_t* const* __restrict__ tables,
                                  const int64_t* __restrict__ vocabs, int64_t hidden,
-                                 uint16_t* __restrict__ out) {
+                                 uint16_t* __restrict__ out, const int32_t* __restrict__ scatter,
+                                 uint16_t* __restrict__ h_ord, float* __restrict__ slots) {
   // each table's row once per workgroup: its address and its length in bytes, 0 for an id
   // outside the table.  The element reads are buffer loads over that range, so an empty
   // range reads 0 with no branch, and the loads of kEmbedBatch tables go out together.
@@ -227,7 +235,21 @@ __global__ void embed_sum_kernel(const int64_t* __restrict__ ids, int n_tables,
       for (int j = 0; j < kEmbedBatch; ++j)   // summed in table order, rounded as before
         if (i0 + j < n_tables) h = (i0 + j == 0) ? v[j] : round_bf16(h + v[j]);
     }
-    out[d] = (uint16_t)f32_to_bf16(h);
+    const uint32_t hb = f32_to_bf16(h);
+    out[d] = (uint16_t)hb;
+    if constexpr (STATS) {
+      const float hv = bf16_to_f32(hb);
+      if (h_ord) h_ord[scatter ? scatter[d] : d] = (uint16_t)hb;
+      const int lane = threadIdx.x & 63;
+      const float h1 = __shfl(hv, lane + 1), h2 = __shfl(hv, lane + 2), h3 = __shfl(hv, lane + 3);
+      float ss = fmaf(hv, hv, 0.f);              // lane 4q: columns 4q .. 4q+3 in order
+      ss = fmaf(h1, h1, ss);
+      ss = fmaf(h2, h2, ss);
+      ss = fmaf(h3, h3, ss);
+      ss += __shfl_xor(ss, 4);                   // slot_combine over the 4 column quads
+      ss += __shfl_xor(ss, 8);
+      if ((lane & 15) == 0) slots[d / kSlotCols] = ss;
+    }
   }
 }
 
@@ -1060,9 +1082,24 @@ int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* table
   if (n_tables < 1 || n_tables > kEmbedMaxTables || hidden < 1 || hidden * 2 >= ((int64_t)1 << 31))
     return MTL_ERR_SHAPE;
   const int blocks = (int)((hidden + 255) / 256);
-  hipLaunchKernelGGL(embed_sum_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, ids,
-                     n_tables, reinterpret_cast<const uint16_t* const*>(tables), vocabs, hidden,
-                     static_cast<uint16_t*>(out));
+  hipLaunchKernelGGL(embed_sum_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     ids, n_tables, reinterpret_cast<const uint16_t* const*>(tables), vocabs,
+                     hidden, static_cast<uint16_t*>(out), nullptr, nullptr, nullptr);
+  return launch_status();
+}
+
+int mtl_embed_sum_stats(const int64_t* ids, int32_t n_tables, const void* const* tables,
+                        const int64_t* vocabs, int64_t hidden, void* out, const int32_t* scatter,
+                        void* h_ord, float* slots, void* stream) {
+  if (!ids || !tables || !vocabs || !out || !slots) return MTL_ERR_INVALID_ARG;
+  if (n_tables < 1 || n_tables > kEmbedMaxTables || hidden < 1 || hidden * 2 >= ((int64_t)1 << 31))
+    return MTL_ERR_SHAPE;
+  if (hidden % kResidCols != 0 || hidden > (int64_t)kSlotCols * kMaxSlots) return MTL_ERR_SHAPE;
+  const int blocks = (int)(hidden / 256);
+  hipLaunchKernelGGL(embed_sum_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     ids, n_tables, reinterpret_cast<const uint16_t* const*>(tables), vocabs,
+                     hidden, static_cast<uint16_t*>(out), scatter, static_cast<uint16_t*>(h_ord),
+                     slots);
   return launch_status();
 }
 

@@ -330,10 +330,6 @@ class FastDecoder:
             raise RuntimeError("fused plan needs gate|up columns in the down input order")
         last = li + 1 == cfg.n_layers
         plan = []
-        if li == 0:   # statistics and act-order copy of the embedding output
-            plan.append(("mtl_residual_add", (None, 0, self.h.data_ptr(), p(self.inv_perm_qkv[0]),
-                                              self.x_qkv.data_ptr(), self.slots.data_ptr(),
-                                              cfg.hidden)))
         qkv_splits = self.splits["qkv"]
         if self.v_keep[li]:   # the int4 q|k GEMV and the bf16 v_proj in one launch
             nqk = lyr["qkv"].out_features
@@ -466,10 +462,18 @@ class FastDecoder:
     def _build_plan(self) -> None:
         cfg = self.m.cfg
         lib = N.load()
-        self._embed = [("mtl_embed_sum", (self.ids.data_ptr(), self.table_ptrs.numel(),
-                                          self.table_ptrs.data_ptr(), self.vocabs.data_ptr(),
-                                          cfg.hidden, self.h.data_ptr()))]
+        embed = (self.ids.data_ptr(), self.table_ptrs.numel(), self.table_ptrs.data_ptr(),
+                 self.vocabs.data_ptr(), cfg.hidden, self.h.data_ptr())
+        self._embed = [("mtl_embed_sum", embed)]
+        self._layer0_in = []
         if self.plan in ("fused", "strip"):
+            # layer 0's RMSNorm statistics and act-order copy of h: formed by the embedding
+            # sum in the step, by a residual add without partials when layer 0 runs alone
+            p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+            into = (p(self.inv_perm_qkv[0]), self.x_qkv.data_ptr(), self.slots.data_ptr())
+            self._embed = [("mtl_embed_sum_stats", embed + into)]
+            self._layer0_in = [("mtl_residual_add", (None, 0, self.h.data_ptr()) + into +
+                                (cfg.hidden,))]
             self._keep_launches = {}
             self._layers = [self._layer_plan_resid(li) for li in range(cfg.n_layers)]
         elif self.plan == "staged":
@@ -489,7 +493,7 @@ class FastDecoder:
                       "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32",
                       "mtl_w4_gemm_partials_geom", "mtl_w4_gemm_norm_partials_geom",
                       "mtl_w4_gemm_residual_geom", "mtl_w4_gemm_norm_silu_geom",
-                      "mtl_w4_gemm_norm_partials_bf16")}
+                      "mtl_w4_gemm_norm_partials_bf16", "mtl_embed_sum_stats")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -537,7 +541,7 @@ class FastDecoder:
 
     def gemv_launch(self, li: int, name: str):
         """The (C function name, args) of one layer's int4 GEMV exactly as the step issues it."""
-        shift = 1 if self.plan in ("fused", "strip") and li == 0 else 0   # layer 0: the stats
+        shift = 0
         if self.v_keep[li] and name != "qkv":
             shift += self._keep_launches[(li, "v")] - 1                    # a separate bf16 v
         if self.up_keep[li] and name == "down":
@@ -560,7 +564,7 @@ class FastDecoder:
         In the partials plans the layer's residual add of the down projection happens at the
         start of the next layer (or the final norm); :meth:`flush_residual` applies it.
         """
-        self._run(self._layers[li])
+        self._run((self._layer0_in if li == 0 else []) + self._layers[li])
 
     def flush_residual(self) -> None:
         """Partials plans: fold the pending down-projection partials into ``self.h``

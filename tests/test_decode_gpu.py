@@ -106,6 +106,54 @@ def test_embed_sum_33_tables(dev, lib):
                              out.data_ptr(), stream()) == N.MTL_ERR_SHAPE
 
 
+@pytest.mark.parametrize("hidden,vocabs_l", [(4096, [300] + [17] * 32), (256, [50, 7, 9]),
+                                             (2560, [40])])
+def test_embed_sum_stats_matches_two_entries(dev, lib, hidden, vocabs_l):
+    # mtl_embed_sum_stats == mtl_embed_sum followed by mtl_residual_add without partials,
+    # bit for bit: the sum, the slot statistics in their documented order and the
+    # act-order copy (scattered, plain, or none)
+    r = np.random.default_rng(hidden + len(vocabs_l))
+    nt = len(vocabs_l)
+    tabs = [round_bf16(r.standard_normal((v, hidden)).astype(np.float32)) for v in vocabs_l]
+    tt = [tb(t, dev) for t in tabs]
+    ptrs = torch.tensor([t.data_ptr() for t in tt], dtype=torch.int64, device=dev)
+    vocabs = torch.tensor(vocabs_l, dtype=torch.int64, device=dev)
+    ns = hidden // 16
+    scatter = torch.from_numpy(r.permutation(hidden).astype(np.int32)).to(dev)
+    for ids in ([int(r.integers(0, v)) for v in vocabs_l], [v + 3 for v in vocabs_l[:1]] +
+                [int(r.integers(0, v)) for v in vocabs_l[1:]]):
+        tid = torch.tensor(ids, dtype=torch.int64, device=dev)
+        ref = torch.empty(hidden, dtype=torch.bfloat16, device=dev)
+        N.check(lib.mtl_embed_sum(tid.data_ptr(), nt, ptrs.data_ptr(), vocabs.data_ptr(), hidden,
+                                  ref.data_ptr(), stream()), "embed")
+        for sc in (scatter, None):
+            ref_ord = torch.zeros(hidden, dtype=torch.bfloat16, device=dev)
+            ref_slots = torch.zeros(ns, dtype=torch.float32, device=dev)
+            N.check(lib.mtl_residual_add(None, 0, ref.data_ptr(), None if sc is None else
+                                         sc.data_ptr(), ref_ord.data_ptr(), ref_slots.data_ptr(),
+                                         hidden, stream()), "residual_add")
+            out = torch.full((hidden,), 7.0, dtype=torch.bfloat16, device=dev)
+            h_ord = torch.zeros(hidden, dtype=torch.bfloat16, device=dev)
+            slots = torch.full((ns,), -1.0, dtype=torch.float32, device=dev)
+            N.check(lib.mtl_embed_sum_stats(tid.data_ptr(), nt, ptrs.data_ptr(),
+                                            vocabs.data_ptr(), hidden, out.data_ptr(),
+                                            None if sc is None else sc.data_ptr(),
+                                            h_ord.data_ptr(), slots.data_ptr(), stream()),
+                    "embed_stats")
+            assert torch.equal(out, ref)
+            assert torch.equal(h_ord, ref_ord)
+            assert torch.equal(slots, ref_slots)
+            assert np.array_equal(slots.cpu().numpy(), slots16(fb(ref)))
+        slots.fill_(-1.0)
+        N.check(lib.mtl_embed_sum_stats(tid.data_ptr(), nt, ptrs.data_ptr(), vocabs.data_ptr(),
+                                        hidden, out.data_ptr(), None, None, slots.data_ptr(),
+                                        stream()), "embed_stats, no copy")
+        assert torch.equal(out, ref) and torch.equal(slots, ref_slots)
+    assert lib.mtl_embed_sum_stats(tid.data_ptr(), nt, ptrs.data_ptr(), vocabs.data_ptr(),
+                                   hidden - 64, out.data_ptr(), None, None, slots.data_ptr(),
+                                   stream()) == N.MTL_ERR_SHAPE
+
+
 def oracle_tables(n, dev):
     """The oracle's RoPE tables as device bf16 tensors (kernel inputs)."""
     cos, sin = D.rope_tables(n, 128)
