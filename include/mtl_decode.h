@@ -36,8 +36,8 @@ int mtl_embed_sum(const int64_t* ids, int32_t n_tables, const void* const* table
                   const int64_t* vocabs, int64_t hidden, void* out, void* stream);
 
 /*
- * mtl_embed_sum that also prepares the first decoder layer's RMSNorm-staged GEMV
- * (the input RMSNorm of moss_tts_lite/model.py:169 on the summed embedding): the same out, plus
+ * mtl_embed_sum that also prepares the first decoder layer's RMSNorm-staged GEMV (the
+ * input RMSNorm of moss_tts_lite/model.py:169 on the summed embedding): the same out, plus
  *   slots   float [hidden / 16]: sum of squares of out's columns 16b .. 16b+15, bit for bit
  *           as mtl_residual_add forms it with part = NULL
  *   h_ord   bf16 [hidden] or NULL: h_ord[scatter[d]] = out[d] (scatter NULL: h_ord[d])
@@ -151,6 +151,17 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
                               const void* w, int64_t N, int64_t K, void* logits,
                               int64_t* token_out, void* workspace, int64_t ws_bytes,
                               void* stream);
+
+/*
+ * mtl_bf16_gemv_argmax_norm followed by mtl_advance_position, the end of a captured
+ * greedy decode step (moss_tts_lite/fast.py:179-180 and the next position), with the
+ * position advanced by the argmax's own last launch: one launch fewer.  token_out and
+ * pos are required (else MTL_ERR_INVALID_ARG).
+ */
+int mtl_bf16_gemv_argmax_norm_advance(const void* h, const void* norm_w, const float* slots,
+                                      float eps, const void* w, int64_t N, int64_t K,
+                                      void* logits, int64_t* token_out, int64_t* pos,
+                                      void* workspace, int64_t ws_bytes, void* stream);
 
 /*
  * bf16 GEMV without selection: out[n] = bf16(sum_k W[n,k] x[k]) for W bf16 [N, K]

@@ -77,6 +77,10 @@ _SIGNATURES = {
     "mtl_bf16_gemv_argmax_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float,
                                          _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                          _i64, _c_void_p]),
+    "mtl_bf16_gemv_argmax_norm_advance": (_i32, [_c_void_p, _c_void_p, _c_void_p,
+                                                 ctypes.c_float, _c_void_p, _i64, _i64,
+                                                 _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                                 _i64, _c_void_p]),
     # tuning knobs (not part of the headers)
     "mtl_w4_gemm_splits": (_i32, [_i64, _i64]),
     "mtl_w4_gemm_partials": (_i32, [_c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _c_void_p,

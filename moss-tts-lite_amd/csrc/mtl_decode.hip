@@ -1021,7 +1021,8 @@ static int decode_device_cus() {
 
 __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restrict__ part_v,
                                                            const long long* __restrict__ part_i,
-                                                           int nparts, int64_t* token_out) {
+                                                           int nparts, int64_t* token_out,
+                                                           int64_t* pos) {
   __shared__ float sv[256];
   __shared__ long long si[256];
   float b = 0.f;
@@ -1042,7 +1043,10 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const float* __restri
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) token_out[0] = si[0] < 0 ? 0 : (int64_t)si[0];
+  if (threadIdx.x == 0) {
+    token_out[0] = si[0] < 0 ? 0 : (int64_t)si[0];
+    if (pos) pos[0] += 1;   // the step's last launch also advances the position
+  }
 }
 
 __global__ void advance_position_kernel(int64_t* pos) {
@@ -1241,7 +1245,7 @@ int mtl_bf16_gemv_argmax(const void* x, const void* w, int64_t N, int64_t K, voi
                      static_cast<uint16_t*>(logits), pv, pi, nullptr, nullptr, 0.f, 0, 0, nullptr);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
-                       token_out);
+                       token_out, nullptr);
   return launch_status();
 }
 
@@ -1292,10 +1296,9 @@ int mtl_decode_attention_fused(const float* qkv_partials, int32_t splits, const 
   return launch_status();
 }
 
-int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
-                              const void* w, int64_t N, int64_t K, void* logits,
-                              int64_t* token_out, void* workspace, int64_t ws_bytes,
-                              void* stream) {
+static int argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
+                       const void* w, int64_t N, int64_t K, void* logits, int64_t* token_out,
+                       int64_t* pos, void* workspace, int64_t ws_bytes, void* stream) {
   if (!h || !norm_w || !slots || !w) return MTL_ERR_INVALID_ARG;
   if (N < 1 || K < 8 || K % 8 != 0 || K > 512 * kHeadKitMax) return MTL_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w) || !aligned16(norm_w) || !aligned16(slots))
@@ -1311,8 +1314,25 @@ int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* sl
                      slots, eps, 0, 0, nullptr);
   if (token_out)
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, pv, pi, kHeadWGs,
-                       token_out);
+                       token_out, pos);
   return launch_status();
+}
+
+int mtl_bf16_gemv_argmax_norm(const void* h, const void* norm_w, const float* slots, float eps,
+                              const void* w, int64_t N, int64_t K, void* logits,
+                              int64_t* token_out, void* workspace, int64_t ws_bytes,
+                              void* stream) {
+  return argmax_norm(h, norm_w, slots, eps, w, N, K, logits, token_out, nullptr, workspace,
+                     ws_bytes, stream);
+}
+
+int mtl_bf16_gemv_argmax_norm_advance(const void* h, const void* norm_w, const float* slots,
+                                      float eps, const void* w, int64_t N, int64_t K,
+                                      void* logits, int64_t* token_out, int64_t* pos,
+                                      void* workspace, int64_t ws_bytes, void* stream) {
+  if (!token_out || !pos) return MTL_ERR_INVALID_ARG;
+  return argmax_norm(h, norm_w, slots, eps, w, N, K, logits, token_out, pos, workspace,
+                     ws_bytes, stream);
 }
 
 int mtl_bf16_gemv(const void* x, const void* w, int64_t N, int64_t K, void* out,

@@ -493,7 +493,8 @@ class FastDecoder:
                       "mtl_w4_gemm_norm_silu", "mtl_bf16_gemv_norm", "mtl_silu_mul_f32",
                       "mtl_w4_gemm_partials_geom", "mtl_w4_gemm_norm_partials_geom",
                       "mtl_w4_gemm_residual_geom", "mtl_w4_gemm_norm_silu_geom",
-                      "mtl_w4_gemm_norm_partials_bf16", "mtl_embed_sum_stats")}
+                      "mtl_w4_gemm_norm_partials_bf16", "mtl_embed_sum_stats",
+                      "mtl_bf16_gemv_argmax_norm_advance")}
 
     def _final_norm_plan(self) -> list:
         """Fold the last layer's pending residual and write ``h_final = RMSNorm(h)``."""
@@ -512,13 +513,13 @@ class FastDecoder:
         m, cfg = self.m, self.m.cfg
         eps = ctypes.c_float(cfg.eps)
         if self.plan in ("staged", "fused", "strip"):   # the head applies the final norm
+            # the argmax's last launch also advances the position
             final = [] if self.plan != "staged" else [self._flush_staged()]
-            final += [("mtl_bf16_gemv_argmax_norm", (self.h.data_ptr(), m.final_norm.data_ptr(),
-                                                    self.slots.data_ptr(), eps, m.head.data_ptr(),
-                                                    cfg.vocab, cfg.hidden, self.logits.data_ptr(),
-                                                    ctypes.c_void_p(self.ids.data_ptr()),
-                                                    self.head_ws.data_ptr(),
-                                                    self.head_ws.numel()))]
+            return final + [("mtl_bf16_gemv_argmax_norm_advance", (
+                self.h.data_ptr(), m.final_norm.data_ptr(), self.slots.data_ptr(), eps,
+                m.head.data_ptr(), cfg.vocab, cfg.hidden, self.logits.data_ptr(),
+                ctypes.c_void_p(self.ids.data_ptr()), ctypes.c_void_p(self.pos.data_ptr()),
+                self.head_ws.data_ptr(), self.head_ws.numel()))]
         else:
             final = self._final_norm_plan() + [
                 ("mtl_bf16_gemv_argmax", (self.h_final.data_ptr(), m.head.data_ptr(), cfg.vocab,

@@ -603,6 +603,24 @@ def test_head_norm_argmax_matches_oracle(dev, lib):
     if srt[-1] - srt[-2] > 0.05:
         assert int(tok.item()) == int(np.argmax(ref))
     assert int(tok.item()) == int(np.argmax(fb(logits)))
+    # the step-ending variant: the same logits and token, and the position one further,
+    # twice in a row; both outputs are required
+    pos = torch.full((1,), 41, dtype=torch.int64, device=dev)
+    for i in range(2):
+        logits2 = torch.zeros(V, dtype=torch.bfloat16, device=dev)
+        tok2 = torch.full((1,), -5, dtype=torch.int64, device=dev)
+        N.check(lib.mtl_bf16_gemv_argmax_norm_advance(
+            th.data_ptr(), tw.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), tW.data_ptr(),
+            V, K, logits2.data_ptr(), tok2.data_ptr(), pos.data_ptr(), ws.data_ptr(), ws.numel(),
+            stream()), "head norm advance")
+        assert torch.equal(logits2, logits) and torch.equal(tok2, tok)
+        assert int(pos.item()) == 42 + i
+    for t, p in ((None, pos), (tok2, None)):
+        assert lib.mtl_bf16_gemv_argmax_norm_advance(
+            th.data_ptr(), tw.data_ptr(), slots.data_ptr(), ctypes.c_float(1e-6), tW.data_ptr(),
+            V, K, logits2.data_ptr(), None if t is None else t.data_ptr(),
+            None if p is None else p.data_ptr(), ws.data_ptr(), ws.numel(),
+            stream()) == N.MTL_ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("N_,K", [(1024, 4096), (12288, 4096), (37, 4096), (2000, 1024),
