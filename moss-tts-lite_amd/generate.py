@@ -360,7 +360,8 @@ def generate_fast(dec, prompt: dict, max_new_tokens=4096, seed=1234, greedy=Fals
         n_steps += 1
         if st.is_stopping or (st.wd_stop and next_text == AUDIO_END_TOKEN_ID):
             break
-        dec.replay_heads(st.is_audio)       # step t + 1's heads, on the backbone just run
+        if t + 1 < max_new_tokens:          # step t + 1's heads, on the backbone just run
+            dec.replay_heads(st.is_audio)
         pos += 1
     torch.cuda.synchronize(dec.dev)
     if stats is not None:

@@ -1,17 +1,23 @@
-"""The device-side sampler against the reference's sampling ops, on the CPU.
+"""The device-side sampler against the reference's own sampler, on the CPU.
 
 moss_tts_lite_amd.generate.sample_rows replaces ``torch.multinomial`` by the draw it makes
 internally (``q = exponential_(1)`` over the probabilities' shape, ``argmax(p / q)``) and
-``torch.unique`` by presence masks; the tokens and the generator's state afterwards must
-equal the reference's ``sample_token`` (restated in tests/_generate_ref.py from
-moss_tts_lite/sampling.py) for every argument combination the reference's own tests use
-(tests/test_core.py:230-246).
+``torch.unique`` by presence masks.  ``tests/golden/generate_fixtures.npz`` holds what the
+reference's ``sample_token`` (moss_tts_lite/sampling.py:70-99, run on the CPU by
+``tests/golden/make_generate_fixtures.py``) returned for the argument combinations the
+reference's own tests use (tests/test_core.py:230-246), and the generator state it left; the
+device sampler must give the same tokens and leave the same state.
 """
+import os
+
+import numpy as np
 import pytest
 import torch
 
 from moss_tts_lite_amd import generate as GEN
-from tests import _generate_ref as R
+from tests.golden.make_generate_fixtures import SAMPLE_GRID, sample_grid_logits
+
+FIXTURES = os.path.join(os.path.dirname(__file__), "golden", "generate_fixtures.npz")
 
 
 def _history_masks(prev, v):
@@ -20,24 +26,22 @@ def _history_masks(prev, v):
     return seen
 
 
-@pytest.mark.parametrize("tk,tp", [(None, None), (25, 0.8), (50, 1.0), (None, 0.95), (5, None)])
-@pytest.mark.parametrize("rep", [1.0, 1.2])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_sample_rows_matches_sample_token(tk, tp, rep, dtype):
-    g = torch.Generator().manual_seed(3)
-    for rows, v in ((1, 50), (31, 1025)):
-        lg = (torch.randn(rows, v, generator=g) * 2).to(dtype)
-        prev = torch.randint(0, v, (1, 9, 3), generator=g)
-        torch.manual_seed(42)
-        a = R.sample_token(lg.clone(), prev_tokens=prev, repetition_penalty=rep, top_p=tp,
-                           top_k=tk, do_sample=True)
-        after_a = torch.rand(3)
-        torch.manual_seed(42)
-        b = GEN.sample_rows(lg.clone(), seen=_history_masks(prev, v), penalty=rep, top_p=tp,
-                            top_k=tk, do_sample=True)
-        after_b = torch.rand(3)
-        assert torch.equal(a, b), (tk, tp, rep, rows)
-        assert torch.equal(after_a, after_b)       # the generator advanced alike
+@pytest.fixture(scope="module")
+def fixtures():
+    return np.load(FIXTURES)
+
+
+@pytest.mark.parametrize("i", range(len(SAMPLE_GRID)))
+def test_sample_rows_matches_reference_sample_token(fixtures, i):
+    tk, tp, rep, dt, shape = SAMPLE_GRID[i]
+    lg, prev = sample_grid_logits(i, shape, dt)
+    torch.manual_seed(42)
+    got = GEN.sample_rows(lg.clone(), seen=_history_masks(prev, shape[1]), penalty=rep, top_p=tp,
+                          top_k=tk, do_sample=True)
+    after = torch.rand(3)
+    want = fixtures["sample_tokens"][i][:shape[0]]
+    assert got.tolist() == want.tolist(), (tk, tp, rep, dt, shape)
+    assert torch.equal(after, torch.from_numpy(fixtures["sample_after"][i]))   # same generator state
 
 
 def test_sample_rows_greedy_and_penalty_values():

@@ -1,21 +1,30 @@
-"""Device-side MOSS generation against the reference's host loop, on the GPU.
+"""Device-side MOSS generation against the reference's own generation loop, on the GPU.
 
-moss_tts_lite_amd.generate.generate_fast (sampling on the device, one overlapped host read
-per step) and the reference's generate_fast restated in tests/_generate_ref.py (every
-decision read back to the host, torch.multinomial, torch.unique) drive the same
-FastMossDecoder over the seeded tiny MOSS model from the same seed; the text tokens, the
-audio frames and the stop reason must be identical.  Also: on this GPU
-``torch.multinomial(p, 1)`` equals ``argmax(p / exponential_(1))`` drawn from the same
+``tests/golden/generate_fixtures.npz`` holds the decisions of the reference's
+``generate_fast`` (moss_tts_lite/fast.py:343-610), run on the CPU by
+``tests/golden/make_generate_fixtures.py`` over the scripted head outputs of
+``tests/_generate_script.py``.  Here moss_tts_lite_amd.generate.generate_fast (sampling on the
+device, one overlapped host read per step) drives a FastMossDecoder over the seeded tiny MOSS
+model whose head outputs are overwritten with the same scripted logits after every head
+pass; the text tokens, the audio frames, the stop fields, the (position, audio2) of every
+step and the shapes of the random draws, in order, must be the reference's.  Also: on this
+GPU ``torch.multinomial(p, 1)`` equals ``argmax(p / exponential_(1))`` drawn from the same
 generator, in the dtypes and shapes generation uses.
 """
+import json
+import os
+
+import numpy as np
 import pytest
 import torch
 
 from moss_tts_lite_amd import generate as GEN
-from tests import _generate_ref as R
+from tests import _generate_script as S
 from tests import _moss_tiny as T
 
 pytestmark = pytest.mark.gpu
+
+FIXTURES = os.path.join(os.path.dirname(__file__), "golden", "generate_fixtures.npz")
 
 
 @pytest.mark.parametrize("rows,v", [(1, 1025), (31, 1025), (1, 151664), (7, 2)])
@@ -36,67 +45,70 @@ def test_multinomial_is_the_exponential_argmax(dev, rows, v, dtype):
 @pytest.fixture(scope="module")
 def decoder(dev):
     from moss_tts_lite_amd.fast import FastMossDecoder
-    model = T.device_backbone(T.generate(T.SEED, True), dev, max_seq=192, full_text_embedding=True)
+    model = T.device_backbone(T.generate(T.SEED, True), dev, max_seq=320, full_text_embedding=True)
     return FastMossDecoder(model)
 
 
-def _prompt(kind):
-    g = torch.Generator().manual_seed(11)
-    rows = torch.full((8, 33), GEN.AUDIO_PAD_CODE, dtype=torch.long)
-    rows[:, 0] = torch.randint(100, 8000, (8,), generator=g)
-    if kind == "audio":                       # a continuation: audio already started
-        rows[-1, 0] = GEN.AUDIO_START_TOKEN_ID
-        rows[3, 1:] = torch.randint(0, 1024, (32,), generator=g)
-    return rows[None]
+@pytest.fixture(scope="module")
+def fixtures():
+    return np.load(FIXTURES)
 
 
-CASES = {
-    "audio_sampled": dict(prompt="audio"),
-    "audio_greedy": dict(prompt="audio", greedy=True),
-    "audio_penalty": dict(prompt="audio", audio_repetition_penalty=1.3, audio_top_k=40),
-    "audio_text_sampled_2way": dict(prompt="audio", text_temperature=1.0, text_top_k=2),
-    "text_first": dict(prompt="text", text_top_p=0.9),
-    # channel 0 pinned to a low-energy code (see the test): three such frames in a row
-    # stop the segment
-    "watchdog": dict(prompt="audio", watchdog_silence_frames=3),
-}
+@pytest.mark.parametrize("case", sorted(S.CASES))
+def test_generate_fast_matches_reference_fixture(dev, decoder, fixtures, case, monkeypatch):
+    spec = S.CASES[case]
+    p = case + "/"
+    script = S.Script(case, vocab=decoder.lt.numel())
+    assert decoder.lt.numel() == S.TEXT_VOCAB
+    assert script.checksum(6) == float(fixtures[p + "checksum"])    # the same scripted logits
+    prompt = S.prompt(spec["prompt"])
+    assert np.array_equal(prompt.numpy(), fixtures[p + "prompt"])
 
+    heads, backbone = decoder.replay_heads, decoder.replay_backbone
+    flags, positions, draws = [], [], []
 
-@pytest.mark.parametrize("case", list(CASES))
-def test_generate_fast_matches_reference_loop(dev, decoder, case, monkeypatch):
-    kw = dict(CASES[case])
-    prompt = _prompt(kw.pop("prompt"))
-    n = kw.pop("n", 90)
-    if case == "watchdog":      # channel 0's logits after every head pass: only code 9 finite
-        heads, step = decoder.replay_heads, decoder.step
+    def scripted_heads(audio2=False):
+        heads(audio2)
+        k = len(flags)
+        lt, la, two = script.heads(k)
+        if k == 0 or not audio2:                 # what this pass of the heads refreshes
+            decoder.lt.copy_(lt)
+        if k == 0 or audio2:
+            decoder.two.copy_(two)
+        decoder.la.copy_(la)
+        flags.append(bool(audio2))
 
-        def pin():
-            decoder.la[0].fill_(float("-inf"))
-            decoder.la[0, 9] = 1.0
+    def recorded_backbone(pos):
+        positions.append(int(pos))
+        backbone(pos)
 
-        def pinned_heads(audio2=False):
-            heads(audio2)
-            pin()
+    real_exponential = torch.Tensor.exponential_
 
-        def pinned_step(row, pos, audio2=False):
-            out = step(row, pos, audio2)
-            pin()
-            return out
+    def recorded_exponential(self, *a, **k):
+        draws.append(list(self.shape))
+        return real_exponential(self, *a, **k)
 
-        monkeypatch.setattr(decoder, "replay_heads", pinned_heads)
-        monkeypatch.setattr(decoder, "step", pinned_step)
-    ref_text, ref_audio, ref_reason = R.generate(decoder, prompt, max_new_tokens=n, seed=5, **kw)
-    stats = {}
-    res = GEN.generate_fast(decoder, {"input_ids": prompt}, max_new_tokens=n, seed=5, stats=stats,
-                            **kw)
-    print(f"{case}: {res.n_steps} steps, text {sorted(set(res.text_ids.tolist()))[:6]}, "
-          f"reason {res.watchdog_reason!r}, host wait {stats['host_wait_s'] * 1e3:.1f} ms")
-    assert res.text_ids.tolist() == ref_text
-    assert torch.equal(res.audio_frames, ref_audio)
-    assert res.watchdog_reason == ref_reason
-    assert res.n_steps == len(ref_text)
-    if case == "watchdog":
-        assert ref_reason == "silence" and res.watchdog_triggered
+    monkeypatch.setattr(decoder, "replay_heads", scripted_heads)
+    monkeypatch.setattr(decoder, "replay_backbone", recorded_backbone)
+    monkeypatch.setattr(torch.Tensor, "exponential_", recorded_exponential)
+    res = GEN.generate_fast(decoder, {"input_ids": prompt}, max_new_tokens=spec["n"], seed=5,
+                            **spec["kwargs"])
+    monkeypatch.undo()
+    want = json.loads(str(fixtures[p + "result"]))
+    print(f"{case}: {res.n_steps} steps, reason {res.watchdog_reason!r}, "
+          f"{len(draws)} draws (reference {len(fixtures[p + 'draws'])})")
+    assert res.text_ids.tolist() == fixtures[p + "text_ids"].tolist()
+    assert np.array_equal(res.audio_frames.numpy(), fixtures[p + "audio_frames"])
+    assert (res.finished, res.n_steps) == (want["finished"], want["n_steps"])
+    assert (res.watchdog_triggered, res.watchdog_reason) == (want["watchdog_triggered"],
+                                                              want["watchdog_reason"])
+    assert res.watchdog_stats == want["watchdog_stats"]
+    calls = fixtures[p + "calls"]                # the reference's step(pos, audio2), steps 1..
+    assert flags[1:] == [bool(a) for a in calls[:, 1]]
+    # the backbone of the step after the last one is queued before the host's decision
+    assert positions[:len(calls)] == calls[:, 0].tolist()
+    assert len(positions) - len(calls) in (0, 1)
+    assert draws == fixtures[p + "draws"].tolist()
 
 
 def test_capture_outside_inference_mode_after_generation(dev):
@@ -106,10 +118,10 @@ def test_capture_outside_inference_mode_after_generation(dev):
     from moss_tts_lite_amd.fast import FastMossDecoder
     model = T.device_backbone(T.generate(T.SEED, True), dev, max_seq=64, full_text_embedding=True)
     first = FastMossDecoder(model)
-    GEN.generate_fast(first, {"input_ids": _prompt("audio")}, max_new_tokens=4, seed=5)
+    GEN.generate_fast(first, {"input_ids": S.prompt("audio")}, max_new_tokens=4, seed=5)
     second = FastMossDecoder(model)
     assert not torch.is_inference_mode_enabled()
-    second.prefill(_prompt("audio")[0])
+    second.prefill(S.prompt("audio")[0])
     second.capture()
     lt, la, _, _ = second.step(None, 8, audio2=True)
     torch.cuda.synchronize()
