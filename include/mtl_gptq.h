@@ -12,7 +12,8 @@
  *   - `stream` is a hipStream_t (NULL = the null stream).  Launch paths do not
  *     allocate, synchronise or read device memory from the host, so every
  *     launch is capturable into a hipGraph.
- *   - Entry points are stateless and reentrant.  A workspace belongs to one
+ *   - Entry points are stateless and reentrant, except mtl_gptq_gemm_noalloc, whose
+ *     calls on one GPU share a library-owned array.  A workspace belongs to one
  *     stream at a time: two launches that share a workspace must be ordered.
  *
  * Weight layouts.  AutoGPTQ: `qweight` int32 [K/8, N]; the 4-bit code of input channel
@@ -112,9 +113,11 @@ int mtl_gptq_gemm(const void* x, int64_t M, int64_t K,
  * No counterpart in the reference: it is for callers that cannot allocate device
  * memory (code under graph capture, tight serving loops).  The split-K workspace is a
  * library-owned static device array of MTL_NOALLOC_SCRATCH_BYTES per GPU, held until the
- * process ends; the first call on a device looks up its address and zero-fills it on
- * `stream`.  Every call on one GPU shares that array: calls that overlap on one GPU race
- * and must be ordered by the caller.  Arguments and results as mtl_gptq_gemm;
+ * process ends; the first call on a device looks up its address (no stream operation, so
+ * a first call under graph capture records only the GEMM's own launches).  Nothing in the
+ * array needs clearing: the GEMM reads only partials the same call wrote.  Every call on
+ * one GPU shares that array: calls that overlap on one GPU race and must be ordered by the
+ * caller.  Arguments and results as mtl_gptq_gemm;
  * MTL_ERR_WORKSPACE when mtl_gemm_workspace_bytes(M, K, N, group_size) exceeds the
  * array (16 MiB: the decode shapes q|k|v 4096x6144, o 4096x4096, gate|up 4096x24576 and
  * down 12288x4096 fit at every M <= 16; gate|up at M = 16 needs 12 MiB).
