@@ -136,3 +136,50 @@ def test_drop_in_matches_torch_int4_operators(dev, m, k, n, g):
     assert y.dtype == y_torch.dtype == torch.bfloat16 and y.shape == y_torch.shape
     r = rel_l2(y.float().cpu().numpy(), y_torch.float().cpu().numpy())
     assert r < 1e-2, r
+
+
+def test_reference_gptq_state_file(dev, tmp_path):
+    # A GPTQ state as the reference's calibration writes it (gptq.py:504-509): per linear the
+    # torch-packed tiles of pack_fast (gptq.py:66-77, here torch's ROCm packer), qsz, the
+    # codes q [N, K] and the scale/zero; saved with torch.save beside its .meta.json
+    # (gptq.py:608-626).  Loading it must rebuild the mtl layout from q: the record's
+    # "packed" holds torch's tiles, which the mtl kernels do not read.
+    from moss_tts_lite_amd.gptq import load_gptq_state
+    rng = np.random.default_rng(11)
+    shapes = {"q": (512, 1024, 128), "down": (256, 2048, 32)}     # name: (N, K, g)
+    state, ref = {0: {}}, {}
+    for name, (n, k, g) in shapes.items():
+        codes = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
+        sc = rng.uniform(0.002, 0.02, size=(n, k // g)).astype(np.float32)
+        mn = rng.uniform(-0.1, 0.0, size=(n, k // g)).astype(np.float32)
+        qsz = torch.stack([torch.from_numpy(sc), torch.from_numpy(mn + 8 * sc)], -1)
+        qsz = qsz.to(torch.bfloat16).transpose(0, 1).contiguous()           # [K/g, N, 2]
+        tiles = torch.ops.aten._convert_weight_to_int4pack(
+            _prepack(torch.from_numpy(codes).to(dev)), 8).cpu()
+        state[0][name] = {"packed": tiles, "qsz": qsz, "q": torch.from_numpy(codes),
+                          "scale": torch.from_numpy(sc), "zero": torch.from_numpy(mn),
+                          "shape": (n, k)}
+        ref[name] = (codes, qsz, tiles, g)
+    path = tmp_path / "w4.pt"
+    torch.save(state, str(path))
+    keep = [f"0:{n}" for n in ("k", "v", "o", "gate", "up")]
+    (tmp_path / "w4.pt.meta.json").write_text(json.dumps(
+        {"group_size_map": {"0:q": 128, "0:down": 32}, "bf16_linears": keep}))
+    st, gmap, kept = load_gptq_state(str(path))
+    disp = W4Dispatch([{}], w4_group_size=128, bf16_keep=kept, group_size_map=gmap, state=st,
+                      device=dev)
+    for name, (codes, qsz, tiles, g) in ref.items():
+        n, k, _ = shapes[name]
+        print("linear", name, n, k, g, flush=True)
+        packed, _ = disp.qlayers[0][name]
+        assert tuple(packed.shape) == tuple(tiles.shape)
+        assert not torch.equal(packed.cpu(), tiles)       # rebuilt from q, not torch's tiles
+        assert torch.equal(packed, ops.convert_weight_to_int4pack(
+            _prepack(torch.from_numpy(codes).to(dev)), 8))
+        x = torch.randn(3, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16).to(dev)
+        y = disp._linear(x, 0, name).float().cpu().numpy()
+        y_torch = torch._weight_int4pack_mm(x, tiles.to(dev), g, qsz.to(dev)).float().cpu().numpy()
+        xb = bf16_bits_to_f32(x.view(torch.int16).cpu().numpy().view(np.uint16))
+        y_ref = G.gemm_f64(xb, G.effective_weight(codes, qsz.view(torch.int16).numpy().view(np.uint16), g).T)
+        assert rel_l2(y, y_ref) < 1e-2, (name, rel_l2(y, y_ref))
+        assert rel_l2(y, y_torch) < 1e-2, (name, rel_l2(y, y_torch))
