@@ -131,28 +131,112 @@ __device__ __forceinline__ float slot_total(const float* slots, int n, int lane)
   return wave_sum(slot_finish(sl, n, lane));
 }
 
+__device__ __forceinline__ float lo_bf(uint32_t w) { return bf16_to_f32(w & 0xffffu); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return bf16_to_f32(w >> 16); }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   return v;
 }
 
-__device__ __forceinline__ float lo_bf(uint32_t w) { return bf16_to_f32(w & 0xffffu); }
-__device__ __forceinline__ float hi_bf(uint32_t w) { return bf16_to_f32(w >> 16); }
+// The same cross-lane steps on the VALU, for code where all 64 lanes are active: a
+// __shfl_xor is a ds_bpermute, an LDS round trip of about 85 cycles that the next step
+// waits for; these are a few cycles each.  xor 32 and xor 16 come from v_permlane32_swap /
+// v_permlane16_swap (after the swap of two copies of x, the two registers hold x[i] and
+// x[i ^ 16] in some order, and addition and max are commutative); xor 8 and xor 4 are DPP
+// row rotations, which equal them once the values depend only on the lane modulo 16 and 8
+// (true after the larger steps of a butterfly that goes 32, 16, 8, 4, 2, 1); xor 2 and 1
+// are DPP quad permutations.  So wave_sum_valu / wave_max_valu give the bits of wave_sum /
+// wave_max.  The swaps are inline asm with both registers in and out (the compiler's
+// builtin loses the second result when both inputs are the same value), with the wait
+// states around them explicit.
+__device__ __forceinline__ void permlane_swap16(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+__device__ __forceinline__ void permlane_swap32(uint32_t& a, uint32_t& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+__device__ __forceinline__ float xor16_add(float v) {
+  uint32_t a = __float_as_uint(v), b = a;
+  permlane_swap16(a, b);
+  return __uint_as_float(a) + __uint_as_float(b);
+}
+
+__device__ __forceinline__ float xor32_add(float v) {
+  uint32_t a = __float_as_uint(v), b = a;
+  permlane_swap32(a, b);
+  return __uint_as_float(a) + __uint_as_float(b);
+}
+
+__device__ __forceinline__ float xor16_max(float v) {
+  uint32_t a = __float_as_uint(v), b = a;
+  permlane_swap16(a, b);
+  return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+
+__device__ __forceinline__ float xor32_max(float v) {
+  uint32_t a = __float_as_uint(v), b = a;
+  permlane_swap32(a, b);
+  return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124;          // row_ror:8, row_ror:4
+constexpr int kDppXor2 = 0x4E, kDppXor1 = 0xB1;            // quad_perm [2,3,0,1], [1,0,3,2]
+
+__device__ __forceinline__ float wave_sum_valu(float v) {
+  v = xor32_add(v);
+  v = xor16_add(v);
+  v += dpp_f32<kDppRor8>(v);
+  v += dpp_f32<kDppRor4>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppXor1>(v);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_valu(float v) {
+  v = xor32_max(v);
+  v = xor16_max(v);
+  v = fmaxf(v, dpp_f32<kDppRor8>(v));
+  v = fmaxf(v, dpp_f32<kDppRor4>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  return v;
+}
 
 // RMSNorm over the 128 dims of one head (lane t holds dims t and t+64), then RoPE:
 // q*cos + rotate_half(q)*sin, each product and the sum rounded to bf16 as separate bf16
 // tensor ops (model.py:34-44, fast.py:141-144).
+// The same with the lane's operands already loaded: norm weights w0 = w[t], w1 = w[t+64],
+// cos c0 = cr[t], c1 = cr[t+64], sin s0 = sr[t], s1 = sr[t+64] (bf16 values in fp32).
+// VALU: the sum of squares with wave_sum_valu (all 64 lanes active; the same bits).
+template <bool VALU = false>
+__device__ __forceinline__ void norm_rope_vals(float x0, float x1, float w0, float w1, float c0,
+                                               float c1, float s0, float s1, float eps,
+                                               float& o0, float& o1) {
+  float ss = fmaf(x0, x0, x1 * x1);
+  ss = VALU ? wave_sum_valu(ss) : wave_sum(ss);
+  const float r = rsqrtf(ss / 128.f + eps);
+  const float n0 = round_bf16(w0 * round_bf16(x0 * r));
+  const float n1 = round_bf16(w1 * round_bf16(x1 * r));
+  o0 = round_bf16(round_bf16(n0 * c0) + round_bf16(-n1 * s0));
+  o1 = round_bf16(round_bf16(n1 * c1) + round_bf16(n0 * s1));
+}
+
 __device__ __forceinline__ void norm_rope_pair(float x0, float x1, const uint16_t* w,
                                                const uint16_t* cr, const uint16_t* sr, int t,
                                                float eps, float& o0, float& o1) {
-  float ss = fmaf(x0, x0, x1 * x1);
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / 128.f + eps);
-  const float n0 = round_bf16(bf16_to_f32(w[t]) * round_bf16(x0 * r));
-  const float n1 = round_bf16(bf16_to_f32(w[t + 64]) * round_bf16(x1 * r));
-  o0 = round_bf16(round_bf16(n0 * bf16_to_f32(cr[t])) + round_bf16(-n1 * bf16_to_f32(sr[t])));
-  o1 = round_bf16(round_bf16(n1 * bf16_to_f32(cr[t + 64])) + round_bf16(n0 * bf16_to_f32(sr[t + 64])));
+  norm_rope_vals(x0, x1, bf16_to_f32(w[t]), bf16_to_f32(w[t + 64]), bf16_to_f32(cr[t]),
+                 bf16_to_f32(cr[t + 64]), bf16_to_f32(sr[t]), bf16_to_f32(sr[t + 64]), eps, o0,
+                 o1);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -45,14 +45,9 @@ struct PrefillArgs {
   int splits, kps;            // K splits (blockIdx.z) of kps blocks each
 };
 
-// Sum over aligned groups of G lanes (G = 4, 8 or 16) with DPP row permutations:
-// quad swaps, then the mirror within 8 and within 16 lanes.  Every lane of a group ends
-// with the group's sum (a + b and b + a round alike).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
-                                                               CTRL, 0xf, 0xf, false));
-}
+// Sum over aligned groups of G lanes (G = 4, 8 or 16) with DPP row permutations
+// (dpp_f32, mtl_common.h): quad swaps, then the mirror within 8 and within 16 lanes.  Every
+// lane of a group ends with the group's sum (a + b and b + a round alike).
 
 template <int G>
 __device__ __forceinline__ float row_sum(float v) {
