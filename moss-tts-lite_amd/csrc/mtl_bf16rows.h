@@ -98,7 +98,7 @@ __device__ __forceinline__ void bf16_rows_norm_body(const Bf16RowsArgs& p, int b
     ss += ((bs < ns ? v.x : 0.f) + (bs + 1 < ns ? v.y : 0.f)) +
           ((bs + 2 < ns ? v.z : 0.f) + (bs + 3 < ns ? v.w : 0.f));
   }
-  const float r = rsqrtf(wave_sum(ss) / (float)K + eps);
+  const float r = rsqrtf(wave_sum_valu(ss) / (float)K + eps);
 #pragma unroll
   for (int u = 0; u < kStage; ++u) {
     const int j = t + 256 * u;
@@ -139,7 +139,7 @@ __device__ __forceinline__ void bf16_rows_norm_body(const Bf16RowsArgs& p, int b
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int row = rb + 4 * j;
-      const float sum = wave_sum(acc[j]);
+      const float sum = wave_sum_valu(acc[j]);
       if (row < nrows && lane == 0) out[b0 + row] = bf16_to_f32(f32_to_bf16(sum));
     }
   }

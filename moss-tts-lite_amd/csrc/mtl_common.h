@@ -202,6 +202,35 @@ __device__ __forceinline__ float wave_sum_valu(float v) {
   return v;
 }
 
+// Sum over aligned groups of G lanes (G = 2, 4, ..., 64), every lane ending with its group's
+// sum: the butterfly xor 1, 2, 4, ... in that order on the VALU (quad permutations; the
+// mirrors within 8 and within 16 lanes, which equal xor 4 and xor 8 once each quad and each 8
+// lanes hold one value; then the permlane swaps), so the bits of
+// `for (o = 1; o < G; o <<= 1) v += __shfl_xor(v, o)`.  All 64 lanes active.
+constexpr int kDppHalfMirror = 0x141, kDppMirror = 0x140;  // row_half_mirror, row_mirror
+
+template <int G>
+__device__ __forceinline__ float group_sum_valu(float v) {
+  static_assert(G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "power of two");
+  v += dpp_f32<kDppXor1>(v);
+  if (G >= 4) v += dpp_f32<kDppXor2>(v);
+  if (G >= 8) v += dpp_f32<kDppHalfMirror>(v);
+  if (G >= 16) v += dpp_f32<kDppMirror>(v);
+  if (G >= 32) v = xor16_add(v);
+  if (G >= 64) v = xor32_add(v);
+  return v;
+}
+
+// slot_combine on the VALU (the same bits; all lanes active).
+__device__ __forceinline__ float slot_combine_valu(float ss) { return group_sum_valu<4>(ss); }
+
+// slot_total on the VALU (the same bits; all lanes active).
+__device__ __forceinline__ float slot_total_valu(const float* slots, int n, int lane) {
+  SlotLoad sl;
+  slot_issue(slots, n, lane, sl);
+  return wave_sum_valu(slot_finish(sl, n, lane));
+}
+
 __device__ __forceinline__ float wave_max_valu(float v) {
   v = xor32_max(v);
   v = xor16_max(v);

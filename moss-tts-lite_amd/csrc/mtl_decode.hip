@@ -907,7 +907,7 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
     xv[i] = (i < kit && k < K) ? *reinterpret_cast<const u32x4*>(x + k) : u32x4{0u, 0u, 0u, 0u};
   }
   if (norm_w) {   // x is the residual stream: apply the final RMSNorm here (model.py:34-40)
-    const float r = rsqrtf(slot_total(slots, K, lane) / (float)K + eps);
+    const float r = rsqrtf(slot_total_valu(slots, K, lane) / (float)K + eps);
 #pragma unroll
     for (int i = 0; i < kHeadKit; ++i) {
       const int k = 512 * i + 8 * lane;
@@ -961,7 +961,7 @@ __global__ void __launch_bounds__(256) head_gemv_kernel(const uint16_t* __restri
     for (int j = 0; j < RB; ++j) {
       const int64_t r = rb + j;
       if (r >= r1) break;
-      const float sum = wave_sum(acc[j]);
+      const float sum = wave_sum_valu(acc[j]);   // cross-lane steps on the VALU
       uint32_t hb = f32_to_bf16(sum);
       if (pad_period > 0 && r % pad_period == pad_index) hb = 0xff80u;   // -inf
       if (logits && lane == 0) logits[r] = (uint16_t)hb;

@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
   if (stager) {
     float norm_r = 0.f;
     if (XSRC == XSRC_RMSNORM)     // rsqrt(mean(h^2) + eps) from the slots (one wave)
-      norm_r = rsqrtf(wave_sum(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
+      norm_r = rsqrtf(wave_sum_valu(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
       const int m = MR == 1 ? 0 : (t >> 6) + 4 * j;
@@ -259,8 +259,7 @@ __global__ void __launch_bounds__(256 * KW) w4_gemm_kernel(W4Args a) {
       if (!xok[j]) v = u32x4{0u, 0u, 0u, 0u};
       float s;
       xa[m][i] = pair_order(v, s);
-#pragma unroll
-      for (int o = 1; o < GI; o <<= 1) s += __shfl_xor(s, o);
+      s = group_sum_valu<GI>(s);                // every lane of the staging waves active here
       if ((i & (GI - 1)) == 0) xg[m][i / GI] = s;
     }
   }

@@ -45,19 +45,7 @@ struct PrefillArgs {
   int splits, kps;            // K splits (blockIdx.z) of kps blocks each
 };
 
-// Sum over aligned groups of G lanes (G = 4, 8 or 16) with DPP row permutations
-// (dpp_f32, mtl_common.h): quad swaps, then the mirror within 8 and within 16 lanes.  Every
-// lane of a group ends with the group's sum (a + b and b + a round alike).
-
-template <int G>
-__device__ __forceinline__ float row_sum(float v) {
-  static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
-  v += dpp_f32<0xB1>(v);                 // quad_perm [1, 0, 3, 2]
-  v += dpp_f32<0x4E>(v);                 // quad_perm [2, 3, 0, 1]
-  if (G >= 8) v += dpp_f32<0x141>(v);    // row_half_mirror
-  if (G >= 16) v += dpp_f32<0x140>(v);   // row_mirror
-  return v;
-}
+// Sums over aligned groups of 4, 8 or 16 lanes: group_sum_valu (mtl_common.h).
 
 template <int GR, int EPI, int FMT>
 __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEU)))
@@ -96,7 +84,7 @@ w4_prefill_kernel(PrefillArgs a) {
   auto x_store_part = [&](int buf, int r) {     // item set r: rows srow + 16 r
     float sum;
     const u32x4 pv = pair_order_dot(xv[r], sum);
-    sum = row_sum<GI>(sum);
+    sum = group_sum_valu<GI>(sum);
     xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
     if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
   };

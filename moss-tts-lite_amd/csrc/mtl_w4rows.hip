@@ -185,8 +185,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
       const int f = fb + lane;
       float sum;
       const u32x4 pv = pair_order(v[u], sum);
-#pragma unroll
-      for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
+      sum = group_sum_valu<GI>(sum);           // every lane of the wave active here
       if (f < total) {                                 // M * K8 need not fill the wave
         const int m = f / K8, i = f - m * K8;
         xa[m * XS + i] = pv;

@@ -177,7 +177,7 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
   if (stages) {
     float norm_r = 0.f;
     if (XSRC == XSRC_RMSNORM)
-      norm_r = rsqrtf(wave_sum(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
+      norm_r = rsqrtf(wave_sum_valu(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
       u32x4 v = xv[r];
@@ -203,8 +203,7 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
       }
       float sum;
       const u32x4 pv = pair_order(v, sum);
-#pragma unroll
-      for (int o = 1; o < GI; o <<= 1) sum += __shfl_xor(sum, o);
+      sum = group_sum_valu<GI>(sum);            // every lane of the wave active here
       const int i = r * STAGERS + tt;
       if (iok[r]) {
         xa[i] = pv;
@@ -333,7 +332,7 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
   float hv[4] = {bf16_to_f32(rr.x & 0xffffu), bf16_to_f32(rr.x >> 16),
                  bf16_to_f32(rr.y & 0xffffu), bf16_to_f32(rr.y >> 16)};
   float ss = residual4(y, hv);
-  ss = slot_combine(ss);
+  ss = slot_combine_valu(ss);
   if (owner) {
     *reinterpret_cast<u32x2*>(a.h + c0) =
         u32x2{f32_to_bf16(hv[0]) | (f32_to_bf16(hv[1]) << 16),
