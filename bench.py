@@ -337,6 +337,8 @@ def bench_decode(args, torch):
     del total
     t0 = time.time()
     model = Int4Backbone(cfg, random_weights(cfg, seed=1234, device=dev, v_keep=args.v_keep), dev)
+    if args.plan == "strip":        # one resident int4 copy per linear: the strip copy
+        model.keep_strip_copies_only()
     dec = FastDecoder(model, plan=args.plan)
     gen = torch.Generator().manual_seed(1234)
     prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen)
@@ -344,6 +346,12 @@ def bench_decode(args, torch):
     dec.capture()
     torch.cuda.synchronize()
     setup_s = time.time() - t0
+    gib = 1 << 30
+    memory = {"int4_weight_gib": round(model.int4_weight_bytes() / gib, 3),
+              "allocated_gib": round(torch.cuda.memory_allocated(dev) / gib, 3),
+              "max_allocated_gib": round(torch.cuda.max_memory_allocated(dev) / gib, 3),
+              "note": "torch allocator bytes on the device after set-up and at their peak "
+                      "(random-init weights built on the device, prefill, graph capture)"}
     # the prompt: every token per launch (fast.py:251-270); the set-up run built the strip
     # copies, so this times the prefill itself (it leaves the same state: cache, pos, ids)
     pf_gpu, pf_wall = [], []
@@ -437,7 +445,7 @@ def bench_decode(args, torch):
                 "step_bytes_avg": int(step_bytes),
                 "step_hbm_gbs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
                 "host_enqueue_ms_per_step": round(host_s * 1e3 / args.steps, 4),
-                "setup_s": round(setup_s, 1), "plan": dec.plan,
+                "setup_s": round(setup_s, 1), "plan": dec.plan, "memory": memory,
                 "prefill_ms": {"tokens": prompt_len, "gpu": round(min(pf_gpu), 3),
                                "wall": round(min(pf_wall), 3)},
                 "gemv_us": {k: round(v, 3) for k, v in gemv_us.items()},

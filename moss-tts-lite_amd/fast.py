@@ -22,9 +22,11 @@ Five launch plans produce the same step:
   16-column strips over all of K): gate|up applies SiLU*up in its epilogue and down reads
   that bf16 product, and o and down apply the residual add in their epilogue (publishing
   the sums of squares and the scattered copy of ``h`` the next RMSNorm-staged GEMV reads).
-  q|k|v keeps the split-K GEMV (``split_k=("qkv",)``), whose partials the attention sums
-  anyway; ``split_k=()`` runs it as a strip too (one "split").  Its GEMV sums run in a
-  different order than the split-K plans', so it agrees with them to rounding, not bitwise.
+  q|k|v runs as a strip GEMV too (two strips per workgroup for GPTQ linears), handing the
+  attention one "split"; ``split_k=("qkv",)`` keeps it on the split-K GEMV over the tiled
+  copy instead.  The strip GEMVs sum in another order than the split-K plans', so this
+  plan agrees with them to rounding, not bitwise.  It reads only the strip copies of the
+  weights, so it runs on a model after ``Int4Backbone.keep_strip_copies_only()``.
 
 * ``"staged"``: each int4 GEMV publishes only its split-K partials and the
   consumer folds the reduction in.  A 16-workgroup residual add sums the o/down
@@ -115,8 +117,8 @@ class FastDecoder:
         # the reference's (packed, qsz) records exist in the strip layout only
         qsz = any(isinstance(lyr[k], QszLinear) for lyr in model.layers
                   for k in ("qkv", "o", "gate_up", "down"))
-        if split_k is None:   # measured fastest: q|k|v keeps split-K (the attention sums it)
-            split_k = ("qkv",) if plan == "strip" and not qsz else ()
+        if split_k is None:
+            split_k = ()
         if not set(split_k) <= {"qkv", "gate_up"} or (split_k and plan != "strip"):
             raise ValueError("split_k names GEMVs of the strip plan: 'qkv', 'gate_up'")
         if qsz and (plan != "strip" or split_k):
@@ -129,6 +131,13 @@ class FastDecoder:
         self._geom = {k: N.StripGeometry(int(v.get("ct", 0)), int(v.get("nb", 0)),
                                          int(v.get("ring", 0)), int(v.get("xcd_order", 0)))
                       for k, v in geo.items()}
+        # q|k|v of GPTQ linears on the strip GEMV: two strips per workgroup unless a geometry
+        # is given (measured: 1485.6 us per step against 1503.4 with one strip and 1487.8
+        # on the split-K GEMV, whose tiled copy of the weight it no longer needs)
+        self._qkv_geom = None
+        if plan == "strip" and not qsz and "qkv" not in split_k and "qkv" not in geo and \
+                all(lyr["qkv"].out_features % 32 == 0 for lyr in model.layers):
+            self._qkv_geom = N.StripGeometry(2, 0, 0, 0)
         # layers whose v_proj stays bf16: q|k on the int4 strip GEMV and v on the bf16
         # GEMV, both into one fp32 "split" of the q|k|v partials the attention reads
         self.v_keep = ["v_keep" in lyr for lyr in model.layers]
@@ -187,8 +196,8 @@ class FastDecoder:
         self.inv_perm_o, self.inv_perm_qkv, self.inv_perm_gu = [], [], []
         self.norm_qkv, self.norm_gu = [], []      # norm weights gathered by the GEMV's perm
         for lyr in model.layers:
-            self.inv_perm_o.append(_inverse(lyr["o"].kernel_args()[3]))
-            pq, pg = lyr["qkv"].kernel_args()[3], lyr["gate_up"].kernel_args()[3]
+            self.inv_perm_o.append(_inverse(lyr["o"].perm))
+            pq, pg = lyr["qkv"].perm, lyr["gate_up"].perm
             self.inv_perm_qkv.append(_inverse(pq))
             self.inv_perm_gu.append(_inverse(pg))
             self.norm_qkv.append(_gather(lyr["input_layernorm"], pq))
@@ -221,10 +230,11 @@ class FastDecoder:
     def _weight(lin, strip: bool):
         """``(weight, layout, metadata, zeros)`` of one int4 GEMV launch: the strip copy
         with its strip-ordered metadata (or the qsz read in place), else the split-K form."""
-        _, qz, sc, _ = lin.kernel_args()
         qw, layout = lin.stream_weight(strip)
         if layout in (N.LAYOUT_STRIP, N.LAYOUT_STRIP_QSZ):
             sc, qz = lin.strip_meta()
+        else:
+            _, qz, sc, _ = lin.kernel_args()
         return qw, layout, sc, qz
 
     def _with_geometry(self, launch, name):
@@ -257,9 +267,9 @@ class FastDecoder:
         eps = ctypes.c_float(cfg.eps)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         prev = self.part["down"] if li > 0 else None
-        perm_qkv = lyr["qkv"].kernel_args()[3]
-        perm_gu = lyr["gate_up"].kernel_args()[3]
-        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+        perm_qkv = lyr["qkv"].perm
+        perm_gu = lyr["gate_up"].perm
+        if not lyr["act_in_down_order"] and lyr["down"].perm is not None:
             raise RuntimeError("fused plan needs gate|up columns in the down input order")
         return [
             ("mtl_residual_rmsnorm", (p(prev), self.splits["down"], self.h.data_ptr(),
@@ -293,7 +303,7 @@ class FastDecoder:
         eps = ctypes.c_float(cfg.eps)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         prev = self.part["down"] if li > 0 else None
-        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+        if not lyr["act_in_down_order"] and lyr["down"].perm is not None:
             raise RuntimeError("staged plan needs gate|up columns in the down input order")
         return [
             ("mtl_residual_add", (p(prev), self.splits["down"], self.h.data_ptr(),
@@ -326,7 +336,7 @@ class FastDecoder:
         scale = ctypes.c_float(attention_scale(cfg))
         eps = ctypes.c_float(cfg.eps)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        if not lyr["act_in_down_order"] and lyr["down"].kernel_args()[3] is not None:
+        if not lyr["act_in_down_order"] and lyr["down"].perm is not None:
             raise RuntimeError("fused plan needs gate|up columns in the down input order")
         last = li + 1 == cfg.n_layers
         plan = []
@@ -341,8 +351,11 @@ class FastDecoder:
             plan += launches
             qkv_splits = 1
         else:
-            plan.append(self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"],
-                                            cfg.qkv_out, "qkv"))
+            launch = self._norm_partials(self.x_qkv, self.norm_qkv[li], lyr["qkv"],
+                                         cfg.qkv_out, "qkv")
+            if self._qkv_geom is not None and launch[0] == "mtl_w4_gemm_norm_partials":
+                launch = (launch[0] + "_geom", launch[1] + (ctypes.byref(self._qkv_geom),))
+            plan.append(launch)
         plan += [
             ("mtl_decode_attention_fused", (self.part["qkv"].data_ptr(), qkv_splits,
                                             lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(),
@@ -686,7 +699,7 @@ class FastDecoder:
             lq = lyr["qkv"]
             N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
                                            lyr["input_layernorm"].data_ptr(),
-                                           p(lq.kernel_args()[3]), x.data_ptr(), cfg.hidden, rows,
+                                           p(lq.perm), x.data_ptr(), cfg.hidden, rows,
                                            cfg.hidden, eps, st), "mtl_rmsnorm_gather")
             self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
             if self.v_keep[li]:
@@ -709,7 +722,7 @@ class FastDecoder:
             self._prefill_gemm(attn, rows, lyr["o"], N.EPI_RESIDUAL, h, cfg.hidden, st)
             N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
                                            lyr["post_attention_layernorm"].data_ptr(),
-                                           p(lyr["gate_up"].kernel_args()[3]), x.data_ptr(),
+                                           p(lyr["gate_up"].perm), x.data_ptr(),
                                            cfg.hidden, rows, cfg.hidden, eps, st),
                     "mtl_rmsnorm_gather")
             if self.up_keep[li]:
@@ -718,7 +731,7 @@ class FastDecoder:
                 gate = pf["gate"]
                 self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_NONE, gate, cfg.intermediate, st)
                 x_up = x
-                if lyr["gate_up"].kernel_args()[3] is not None:   # up reads natural order
+                if lyr["gate_up"].perm is not None:   # up reads natural order
                     x_up = pf["x_nat"]
                     N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
                                                    lyr["post_attention_layernorm"].data_ptr(),

@@ -54,6 +54,7 @@ class GPTQLinear(torch.nn.Module):
         self._tiled: torch.Tensor | None = None
         self._strip: torch.Tensor | None = None
         self._strip_meta: tuple | None = None
+        self._strip_only = False
 
     @classmethod
     def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
@@ -76,6 +77,8 @@ class GPTQLinear(torch.nn.Module):
     @torch.no_grad()
     def post_init(self) -> "GPTQLinear":
         """Build the kernel-side weight: for act-order, the group-sorted copy and gather index."""
+        if self._strip_only:
+            return self
         if self.is_act_order():
             self._kernel_qweight, self._perm = ops.actorder_prepare(self.qweight, self.g_idx,
                                                                     self.group_size)
@@ -84,9 +87,39 @@ class GPTQLinear(torch.nn.Module):
         return self
 
     def kernel_args(self):
+        """``(qweight, qzeros, scales, perm)`` of the AutoGPTQ-layout kernels (the weight
+        group-sorted for act-order).  ``RuntimeError`` after :meth:`keep_strip_only`."""
+        if self._strip_only:
+            raise RuntimeError("this linear keeps only its strip copy (keep_strip_only): "
+                               "the AutoGPTQ-layout kernels have no weight to read")
         if self._kernel_qweight is None:
             self.post_init()
         return self._kernel_qweight, self.qzeros, self.scales, self._perm
+
+    @property
+    def perm(self) -> torch.Tensor | None:
+        """The act-order gather index (int32 ``[K]``: sorted row i is input channel
+        ``perm[i]``), or None when the groups are contiguous."""
+        if self._kernel_qweight is None and not self._strip_only:
+            self.post_init()
+        return self._perm
+
+    @torch.no_grad()
+    def keep_strip_only(self) -> "GPTQLinear":
+        """Keep one resident int4 copy: build the strip copy and its strip-ordered
+        metadata, then free the AutoGPTQ ``qweight``, its group-sorted copy and the split-K
+        tiled copy.  The linear then serves the strip kernels only (the decode step's strip
+        GEMVs, the prompt-length GEMM, :meth:`forward`); ``kernel_args``, ``dequantize``
+        and ``reorder_output_columns`` raise ``RuntimeError``."""
+        if self._strip_only:
+            return self
+        self.stream_weight(strip=True)
+        self.strip_meta()
+        self._kernel_qweight = None
+        self._tiled = None
+        self.qweight = torch.empty(0, dtype=torch.int32, device=self.scales.device)
+        self._strip_only = True
+        return self
 
     def supports_strip(self) -> bool:
         return self.out_features % 16 == 0 and self.in_features % 256 == 0 \
@@ -98,13 +131,14 @@ class GPTQLinear(torch.nn.Module):
         ``strip=False``: the wave-contiguous tiled copy of the kernel weight (split-K
         GEMV) when N % 64 == 0, else the kernel weight in row layout.  ``strip=True``:
         the column-strip copy for the full-K strip GEMV.  Copies are built once."""
+        if strip and self._strip is not None:
+            return self._strip, N.LAYOUT_STRIP
         qw = self.kernel_args()[0]
         if strip:
             if not self.supports_strip():
                 raise RuntimeError(f"no strip layout for K={self.in_features}, "
                                    f"N={self.out_features}")
-            if self._strip is None:
-                self._strip = ops.strip_weights(qw)
+            self._strip = ops.strip_weights(qw)
             return self._strip, N.LAYOUT_STRIP
         if self.out_features % 64:
             return qw, N.LAYOUT_ROWS
@@ -130,6 +164,9 @@ class GPTQLinear(torch.nn.Module):
         Used at load time so a producer writes its output directly in the act-order
         input order of its consumer (bitwise neutral per column).
         """
+        if self._strip_only:
+            raise RuntimeError("reorder_output_columns needs the AutoGPTQ weight "
+                               "(freed by keep_strip_only)")
         cols = cols.to(device=self.scales.device, dtype=torch.long)
         if cols.numel() != self.out_features:
             raise ValueError("cols must list every output column once")
@@ -151,14 +188,26 @@ class GPTQLinear(torch.nn.Module):
         (:func:`ops.strip_rows_pays`; it builds the strip copy of the weight once and keeps
         it), the others on the split-K GEMM over the AutoGPTQ layout; both through the
         ``torch.ops.mtl`` operators (one dispatcher call, torch's stream and allocator)."""
-        qw, qz, sc, perm = self.kernel_args()
         m = x.numel() // self.in_features if self.in_features else 0
-        if m and self.supports_strip() and ops.strip_rows_pays(m, self.in_features,
-                                                               self.out_features, perm is not None):
+        perm = self.perm
+        if m and self.supports_strip() and (
+                (self._strip_only and m <= 16) or
+                ops.strip_rows_pays(m, self.in_features, self.out_features, perm is not None)):
             strip = self.stream_weight(strip=True)[0]
-            return ops.torch_ops().strip_rows_gemm(x, strip, qz, sc, self.out_features,
-                                                   self.group_size, self.zero_offset, perm,
-                                                   out_dtype)
+            return ops.torch_ops().strip_rows_gemm(x, strip, self.qzeros, self.scales,
+                                                   self.out_features, self.group_size,
+                                                   self.zero_offset, perm, out_dtype)
+        if self._strip_only:
+            # the prompt-length GEMM over the strip copy, x's channels taken into the
+            # weight's (group-sorted) row order first
+            x2 = x.reshape(-1, self.in_features)
+            if perm is not None:
+                x2 = x2.index_select(1, perm.long())
+            sc, qz = self.strip_meta()
+            y = ops.prefill_gemm(x2.contiguous(), self._strip, sc, qz, self.out_features,
+                                 self.group_size, self.zero_offset, out_dtype=out_dtype)
+            return y.reshape(*x.shape[:-1], self.out_features)
+        qw, qz, sc, perm = self.kernel_args()
         return ops.gptq_gemm(x, qw, qz, sc, self.group_size, perm=perm,
                              zero_offset=self.zero_offset, out_dtype=out_dtype)
 
@@ -215,11 +264,17 @@ class QszLinear:
         """``(metadata, zeros)`` in the strip kernels' argument order: qsz, none."""
         return self.qsz, None
 
+    perm = None          # contiguous groups: no act-order gather
+
     def post_init(self) -> "QszLinear":
         return self
 
     def drop_original(self) -> None:
         pass
+
+    def keep_strip_only(self) -> "QszLinear":
+        """The packed weight is the only copy already."""
+        return self
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shp = x.shape

@@ -167,7 +167,7 @@ class Int4Backbone:
                     raise ValueError("with a kept v, qkv must hold q|k only")
             elif lyr["qkv"].out_features != cfg.qkv_out:
                 raise ValueError("qkv must hold q|k|v")
-            perm_down = lyr["down"].kernel_args()[3]
+            perm_down = lyr["down"].perm
             if up_keep:
                 # up_proj kept in bf16: "gate_up" holds the int4 gate alone; SiLU*up is a
                 # separate elementwise pass, so down must read its input in natural order
@@ -195,6 +195,31 @@ class Int4Backbone:
     def reset_cache(self) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()
+
+    def keep_strip_copies_only(self) -> "Int4Backbone":
+        """One resident int4 copy per linear: each GPTQ linear keeps its strip copy (with
+        strip-ordered metadata) and frees its AutoGPTQ and split-K copies, one linear at a
+        time.  Afterwards the model runs the decode step's strip plan and the prompt-length
+        GEMMs, which read only the strip copies; the other launch plans need the freed
+        copies and raise ``RuntimeError`` at construction."""
+        for lyr in self.layers:
+            for k in ("qkv", "o", "gate_up", "down"):
+                lyr[k].keep_strip_only()
+        return self
+
+    def int4_weight_bytes(self) -> int:
+        """Device bytes of every resident int4 weight copy (codes, not metadata)."""
+        seen, total = set(), 0
+        for lyr in self.layers:
+            for k in ("qkv", "o", "gate_up", "down"):
+                lin = lyr[k]
+                copies = ((lin.packed,) if isinstance(lin, QszLinear) else
+                          (lin.qweight, lin._kernel_qweight, lin._tiled, lin._strip))
+                for t in copies:
+                    if t is not None and t.numel() and t.data_ptr() not in seen:
+                        seen.add(t.data_ptr())
+                        total += t.numel() * t.element_size()
+        return total
 
 
 def layers_from_dispatch(disp: W4Dispatch, norms: list[dict]) -> list[dict]:
@@ -263,8 +288,14 @@ def random_weights(cfg: BackboneConfig, seed: int = 1234, device="cuda",
     gen.manual_seed(seed)
     h, g = cfg.hidden, cfg.group_size
 
-    def normal(*shape, std):
-        return (torch.randn(*shape, device=dev, generator=gen) * std).bfloat16()
+    def normal(*shape, std, rows: int = 8192):
+        # drawn a block of leading rows at a time: no float32 copy of a whole table
+        out = torch.empty(*shape, dtype=torch.bfloat16, device=dev)
+        flat = out.view(shape[0], -1)
+        for r0 in range(0, shape[0], rows):
+            blk = flat[r0:r0 + rows]
+            blk.copy_(torch.randn(blk.shape, device=dev, generator=gen) * std)
+        return out
 
     def norm_w(n):
         return (1.0 + torch.randn(n, device=dev, generator=gen) * 0.05).bfloat16()

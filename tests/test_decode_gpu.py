@@ -330,7 +330,7 @@ def test_launch_plans_agree(dev):
         assert np.array_equal(out["fused"][1][i], out["staged"][1][i]), f"step {i}"
 
 
-@pytest.mark.parametrize("plan,split_k", [("strip", None), ("strip", ()), ("fused", None),
+@pytest.mark.parametrize("plan,split_k", [("strip", None), ("strip", ("qkv",)), ("fused", None),
                                           ("staged", None), ("partials", None)])
 def test_plan_graph_replay_is_bitwise(dev, plan, split_k):
     cfg = small_config()
@@ -348,6 +348,36 @@ def test_plan_graph_replay_is_bitwise(dev, plan, split_k):
         dec.graph.replay()
         assert int(dec.ids.item()) == eager[i][0]
         assert torch.equal(dec.logits, eager[i][1]), f"{plan}: replay {i} differs from eager"
+
+
+def test_keep_strip_copies_only(dev):
+    # One resident int4 copy per linear: after keep_strip_copies_only the strip plan (and
+    # the prompt-length GEMMs) run on the strip copies alone, bit for bit as before, the
+    # int4 bytes fall to one copy, and a plan that needs the freed copies refuses to build
+    cfg = small_config()
+    model, _ = build_case(cfg, seed=31, dev=dev)
+    prompt = torch.tensor([8, 6, 7, 5, 3, 0, 9])
+
+    def run():
+        dec = FastDecoder(model)
+        dec.prefill(prompt)
+        out = []
+        for _ in range(4):
+            dec.run_step()
+            out.append((int(dec.ids.item()), dec.logits.clone()))
+        return out
+
+    before = run()
+    both = model.int4_weight_bytes()
+    model.keep_strip_copies_only()
+    one = sum(lyr[k].in_features * lyr[k].out_features // 2 for lyr in model.layers
+              for k in ("qkv", "o", "gate_up", "down"))
+    assert model.int4_weight_bytes() == one < both
+    after = run()
+    for i, ((t0, l0), (t1, l1)) in enumerate(zip(before, after)):
+        assert t0 == t1 and torch.equal(l0, l1), i
+    with pytest.raises(RuntimeError, match="strip copy"):
+        FastDecoder(model, plan="unfused")
 
 
 def test_full_size_layer_config3(dev):

@@ -321,6 +321,31 @@ def test_gptq_linear_forward_routes(dev, act_order, k, n):
     assert any(routes) and not all(routes)
 
 
+@pytest.mark.parametrize("act_order", [False, True])
+def test_gptq_linear_strip_only_forward(dev, act_order):
+    # keep_strip_only frees the AutoGPTQ copies: up to 16 rows run on the skinny strip GEMM
+    # (the same launches as before, bit for bit), more rows on the prompt-length GEMM over
+    # the strip copy (x gathered into the sorted row order); every row count against float64
+    from moss_tts_lite_amd.gptq import GPTQLinear
+    k, n = 2048, 1024
+    case = synth.gptq_case(k=k, n=n, m=40, group=128, act_order=act_order, seed=k + act_order)
+    lin = GPTQLinear.from_buffers(t_i32(case["qweight"], dev), t_i32(case["qzeros"], dev),
+                                  t_f16(case["scales"], dev),
+                                  t_i32(case["g_idx"], dev) if act_order else None, 128)
+    x = t_bf16(case["x_bits"], dev)
+    rows = (1, 5, 16, 40)
+    ref = {m: lin(x[:m], out_dtype=torch.float32) for m in rows}
+    lin.keep_strip_only()
+    assert lin.qweight.numel() == 0 and lin._kernel_qweight is None and lin._tiled is None
+    for m in rows:
+        y = lin(x[:m], out_dtype=torch.float32)
+        assert rel_l2(y.cpu().numpy(), case["y_ref"][:m]) < TOL_F32, m
+        if ops.strip_rows_pays(m, k, n, act_order):
+            assert torch.equal(y, ref[m]), m
+    with pytest.raises(RuntimeError, match="strip copy"):
+        lin.kernel_args()
+
+
 def test_strip_rows_matches_strip_gemv_at_m1(dev):
     # at M = 1 the skinny kernel and the decode GEMV run different launch shapes; both
     # agree with float64 and with each other within fp32 rounding
