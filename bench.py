@@ -67,51 +67,49 @@ def make_gptq_weights(torch, dev, k, n, g, seed, act_order=True):
     return qweight, qzeros, scales, g_idx
 
 
-def bench_gemv(args, torch, pkg):
+def module_gemv_sweep(torch, dev, steps: int, warmup: int, with_split_k: bool = False) -> dict:
+    """The GPTQ module at one row (GPTQLinear.forward, M = 1, act-order g128) on the four
+    decode shapes, weight copies rotated so no launch finds its weights in the caches:
+    the full-K strip GEMV over the strip copy with x gathered through the act-order index
+    while staging.  The sweep (one layer's four GEMVs per step) replays a hipGraph of
+    module calls, so host overhead is out of the timed region; per-shape durations replay
+    a hipGraph of that shape's calls alone, back to back over its weight copies (as the
+    decode workload times its GEMVs).  ``with_split_k`` also times the split-K GEMM over
+    the AutoGPTQ layout on every shape (event pairs around single launches)."""
     from moss_tts_lite_amd import _native as N
     from moss_tts_lite_amd import ops
+    from moss_tts_lite_amd.gptq import GPTQLinear
 
-    dev = torch.device("cuda:0")
     shapes = []
     for name, k, n in GEMV_SHAPES:
         per_copy = algo_bytes(1, k, n, GROUP, True)
         copies = max(2, math.ceil(640e6 / per_copy))
-        ws = []
+        mods = []
         for c in range(copies):
             qw, qz, sc, g_idx = make_gptq_weights(torch, dev, k, n, GROUP, seed=1234 + 97 * c + k + n)
-            qws, perm = ops.actorder_prepare(qw, g_idx, GROUP)
-            del qw
-            ws.append((qws, qz, sc, perm, ops.strip_weights(qws)))
+            lin = GPTQLinear.from_buffers(qw, qz, sc, g_idx, GROUP).post_init()
+            if with_split_k:
+                lin.drop_original()
+            else:
+                lin.keep_strip_only()
+            mods.append(lin)
         x = torch.randn(1, k, device=dev, generator=torch.Generator(device=dev).manual_seed(7)).bfloat16()
-        y = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
         ops.reserve_workspace(dev, ops.gemm_workspace_bytes(1, k, n, GROUP))
-        shapes.append(dict(name=name, k=k, n=n, copies=ws, x=x, y=y, bytes=per_copy,
-                           rows=ops.strip_rows_pays(1, k, n, True)))
+        shapes.append(dict(name=name, k=k, n=n, mods=mods, x=x, bytes=per_copy))
     torch.cuda.synchronize()
 
-    # The GPTQ module's M = 1 route (GPTQLinear.forward, ops.strip_rows_pays): the skinny
-    # strip GEMM over the strip copy of the group-sorted weight with x gathered through the
-    # act-order index while staging, or the split-K GEMM over the AutoGPTQ layout, which is
-    # also timed on its own for every shape.
     def launch(s, i):
-        if not s["rows"]:
-            launch_split_k(s, i)
-            return
-        qws, qz, sc, perm, qss = s["copies"][i % len(s["copies"])]
-        ops.strip_rows_gemm(s["x"], qss, qz, sc, s["n"], GROUP, out=s["y"], perm=perm)
+        s["mods"][i % len(s["mods"])](s["x"])
 
     def launch_split_k(s, i):
-        qws, qz, sc, perm, qss = s["copies"][i % len(s["copies"])]
-        ops.w4_gemm(s["x"], qws, N.META_GPTQ, sc, qz, perm, s["n"], GROUP, out=s["y"])
+        qws, qz, sc, perm = s["mods"][i % len(s["mods"])].kernel_args()
+        ops.w4_gemm(s["x"], qws, N.META_GPTQ, sc, qz, perm, s["n"], GROUP)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         for s in shapes:
             launch(s, i)
     torch.cuda.synchronize()
-
-    # The step loop replays a hipGraph of `cycle` steps (one per weight copy of the
-    # deepest rotation), so host launch overhead is out of the timed region.
-    cycle = max(len(s["copies"]) for s in shapes)
+    cycle = max(len(s["mods"]) for s in shapes)
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -127,8 +125,7 @@ def bench_gemv(args, torch, pkg):
                 launch(s, i)
     graph.replay()
     torch.cuda.synchronize()
-    reps = max(1, math.ceil(args.steps / cycle))
-    steps = reps * cycle
+    reps = max(1, math.ceil(steps / cycle))
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -137,12 +134,10 @@ def bench_gemv(args, torch, pkg):
         graph.replay()
     t1.record()
     torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / steps
+    sweep_us = t0.elapsed_time(t1) * 1e3 / (reps * cycle)
 
-    # Per-kernel durations: event pairs around single launches on the launch stream,
-    # queued behind a GPU spin so the host never starves the queue.
     def event_us(s, fn):
-        nrep = max(20, 4 * len(s["copies"]))
+        nrep = max(20, 4 * len(s["mods"]))
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in range(nrep)]
         torch.cuda.synchronize()
@@ -154,34 +149,56 @@ def bench_gemv(args, torch, pkg):
         torch.cuda.synchronize()
         return sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
 
+    def back_to_back_us(s):
+        calls = len(s["mods"]) * max(1, math.ceil(64 / len(s["mods"])))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(calls):
+                launch(s, i)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(4):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (4 * calls)
+
     per = {}
     for s in shapes:
-        us = event_us(s, launch)
-        sk = event_us(s, launch_split_k)
-        mean_us = sum(us) / len(us)
-        per[s["name"]] = dict(us=round(mean_us, 3), median_us=round(us[len(us) // 2], 3),
-                              gbs=round(s["bytes"] / mean_us / 1e3, 1),
-                              frac=round(s["bytes"] / mean_us / 1e3 / HBM_PEAK_GBS, 4),
-                              split_k_us=round(sum(sk) / len(sk), 3),
-                              route="strip_rows" if s["rows"] else "split_k",
-                              copies=len(s["copies"]))
-    skinny = bench_skinny(args, torch, dev)
+        us = back_to_back_us(s)
+        per[s["name"]] = dict(us=round(us, 3), gbs=round(s["bytes"] / us / 1e3, 1),
+                              frac=round(s["bytes"] / us / 1e3 / HBM_PEAK_GBS, 4),
+                              copies=len(s["mods"]))
+        if with_split_k:
+            sk = event_us(s, launch_split_k)
+            per[s["name"]]["split_k_us"] = round(sum(sk) / len(sk), 3)
     step_bytes = sum(s["bytes"] for s in shapes)
-    gu = per["gate_up"]
+    return {"workload": "GPTQ module forward at one row (GPTQLinear, act-order g128): qkv "
+                        "4096x6144, o 4096x4096, gate_up 4096x24576, down 12288x4096 on the "
+                        "full-K strip GEMV with the act-order gather while staging",
+            "sweep_us": round(sweep_us, 3), "sweep_gbs": round(step_bytes / sweep_us / 1e3, 1),
+            "per_shape": per, "step_bytes": step_bytes}
+
+
+def bench_gemv(args, torch, pkg):
+    dev = torch.device("cuda:0")
+    sweep = module_gemv_sweep(torch, dev, args.steps, args.warmup, with_split_k=True)
+    skinny = bench_skinny(args, torch, dev)
+    gu = sweep["per_shape"]["gate_up"]
+    ms_step = sweep["sweep_us"] / 1e3
     return dict(
-        value=round(step_bytes / (ms_step * 1e-3) / 1e9, 1), unit="GB/s", ms_per_step=ms_step,
-        steps=steps,
+        value=sweep["sweep_gbs"], unit="GB/s", ms_per_step=ms_step, steps=args.steps,
         dtype="int4 weights, bf16 x, fp32 accumulate",
-        config={"workload": "int4 GEMV sweep M=1 act-order g128: qkv 4096x6144, o 4096x4096, "
-                            "gate_up 4096x24576, down 12288x4096 (one step = one layer's 4 GEMVs) "
-                            "on the GPTQ module's M=1 route (per_kernel.route: the skinny "
-                            "strip GEMM with the act-order gather while staging, or the "
-                            "split-K GEMM; split_k_us: the split-K GEMM on every shape)",
-                "per_kernel": per, "step_bytes": step_bytes,
+        config={"workload": sweep["workload"] + " (one step = one layer's 4 GEMVs; "
+                            "split_k_us: the split-K GEMM on every shape)",
+                "per_kernel": sweep["per_shape"], "step_bytes": sweep["step_bytes"],
                 "skinny_gate_up": skinny},
         roofline={"bound": "hbm", "achieved": gu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                   "frac": gu["frac"], "traffic": None,
-                  "kernel": "w4_rows_kernel<g128, GPTQ> gate_up 4096x24576 M=1, act-order gather"},
+                  "kernel": "w4_strip_kernel<g128, PERM, STORE> gate_up 4096x24576 M=1, "
+                            "act-order gather (event-timed single calls)"},
     )
 
 
@@ -426,6 +443,8 @@ def bench_decode(args, torch):
                        (cfg.intermediate, cfg.hidden)))
     if args.v_keep:                       # the kept v_proj streams bf16 weights
         layer_bytes += 2 * nv * cfg.hidden + 2 * cfg.hidden + 4 * nv
+    # config 1: the GPTQ module's own one-row forward on the same four shapes
+    module_gemv = module_gemv_sweep(torch, dev, steps=200, warmup=3)
     avg_len = (first_pos + 1 + final_pos) / 2
     kv_bytes = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim * 2 * avg_len
     step_bytes = cfg.n_layers * layer_bytes + 2 * cfg.vocab * cfg.hidden + kv_bytes
@@ -449,6 +468,7 @@ def bench_decode(args, torch):
                 "prefill_ms": {"tokens": prompt_len, "gpu": round(min(pf_gpu), 3),
                                "wall": round(min(pf_wall), 3)},
                 "gemv_us": {k: round(v, 3) for k, v in gemv_us.items()},
+                "module_gemv": module_gemv,
                 "gemv_gbs": {k: round(algo_bytes(1, kk, nn, cfg.group_size, False) / gemv_us[k]
                                       / 1e3, 1) for k, kk, nn in
                              (("gate_up", cfg.hidden, 2 * cfg.intermediate),
@@ -459,8 +479,14 @@ def bench_decode(args, torch):
                   "frac": round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
                   "traffic": (profiled_traffic("gate_up", dec.plan)
                               if cfg.group_size == GROUP and not args.v_keep else None),
-                  "kernel": GATE_UP_KERNEL.get(dec.plan, "gate_up 4096x24576 M=1")
-                            + " (as launched in the decode step)",
+                  "kernel": GATE_UP_KERNEL.get(dec.plan, "gate_up 4096x24576 M=1"),
+                  "timing": "achieved and frac: the step's own gate|up launch, 144 launches "
+                            "back to back over the 36 layers' weights between one HIP event "
+                            "pair on the launch stream; in_step_trace: the same kernel's "
+                            "average duration inside the graph-replayed step, from the "
+                            "committed rocprofv3 kernel trace of this workload",
+                  "in_step_trace": profiled_in_step("gate_up", dec.plan, gu_bytes)
+                                   if cfg.group_size == GROUP and not args.v_keep else None,
                   "bytes_per_launch": gu_bytes},
     )
 
@@ -483,6 +509,24 @@ def profiled_traffic(name: str, plan: str):
             for line in f:
                 if line.startswith(f"traffic_bytes {plan} {name}:"):
                     return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def profiled_in_step(name: str, plan: str, nbytes: int):
+    """Average duration of one decode-step GEMV of that plan inside the graph-replayed step,
+    from the committed rocprofv3 kernel trace (a line ``in_step_us <plan> <name>: <us>``),
+    with the rate and roofline fraction it gives; None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "decode_step_36layer_kernel_trace.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"in_step_us {plan} {name}:"):
+                    us = float(line.split(":")[1])
+                    return {"us": us, "achieved": round(nbytes / us / 1e3, 1),
+                            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
     except OSError:
         pass
     return None

@@ -265,6 +265,28 @@ int mtl_w4_gemm_strip_rows_ex(const void* x, int64_t M, int64_t ldx, int64_t K,
                               int32_t out_dtype, void* stream);
 
 /*
+ * One row on the full-K strip GEMV: y[N] = x[K] @ dequant(W) over a GPTQ linear's strip copy
+ * (mtl_w4_strip of its group-sorted qweight, mtl_w4_strip_meta of its scales and zeros),
+ * x in the checkpoint's channel order.  Serves the GPTQ module's forward at M = 1, the
+ * product the reference's kernel_linear hands to torch._weight_int4pack_mm
+ * (moss_tts_lite/gptq.py:577-585, 149-160); the reference's own (packed, qsz) records take
+ * the same kernel through mtl_int4pack_mm.
+ *   x             bf16 [K], 16-byte aligned
+ *   perm          NULL, or uint16 [K] (16-byte aligned): a permutation of 0..K-1, row k of
+ *                 the sorted weight multiplies x[perm[k]] (mtl_gptq_actorder_prepare's
+ *                 index, narrowed); the launch copies x into LDS and gathers from there
+ *                 while staging
+ *   strip_weight, strip_scales, strip_zeros   as mtl_w4_gemm_partials with MTL_LAYOUT_STRIP
+ *   y             [N] bf16 or f32 (out_dtype), 8- or 16-byte aligned
+ * K % 256 == 0, K <= 16384 (K <= 12288 with perm), N % 16 == 0, N * K / 2 < 2^31; group
+ * size 32, 64, 128 or 256.  The sums are the decode step's strip GEMV's (same launch shape).
+ */
+int mtl_w4_gemv_strip(const void* x, int64_t K, const uint16_t* perm,
+                      const int32_t* strip_weight, const void* strip_scales,
+                      const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                      int32_t zero_offset, int32_t out_dtype, void* y, void* stream);
+
+/*
  * Prompt-length int4 GEMM over the strip layout: y[M, N] = x[M, K] @ dequant(W) for any
  * M >= 1, fp32 accumulation on MFMA, no workspace.  The reference's quantized prefill
  * runs every projection at M = prompt length through torch._weight_int4pack_mm

@@ -101,6 +101,8 @@ _SIGNATURES = {
     "mtl_w4_gemm_strip_rows_ex": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
                                          _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
                                          _c_void_p, _i64, _i32, _c_void_p]),
+    "mtl_w4_gemv_strip": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _i64, _i32, _i32, _i32, _c_void_p, _c_void_p]),
     "mtl_w4_gemm_prefill": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i32, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p,
                                    _i64, _c_void_p]),

@@ -152,7 +152,8 @@ __device__ __forceinline__ void qsz_decode(uint32_t sz, float& s, float& c, floa
 }
 
 // Arguments of the full-K strip GEMV (mtl_w4strip.hip), M = 1.  The source of x is xpart
-// (SiLU*up), else hn (RMSNorm), else x; the epilogue is SiLU*up into act when act is set
+// (SiLU*up), else hn (RMSNorm), else x (gathered through perm when set, GPTQ metadata and
+// the store epilogue only); the epilogue is SiLU*up into act when act is set
 // (RMSNorm source only), the residual add when h is set, else a store to y (fp32) or y16
 // (bf16).  fmt is the group metadata (STRIP_META_*): with STRIP_META_QSZ, scales points at
 // the reference's qsz and qzeros is unused.
@@ -160,13 +161,12 @@ struct StripArgs {
   const u32x4* w;             // strip layout of mtl_w4_strip
   const uint16_t* scales;     // strip-ordered fp16 scales, or the qsz pairs
   const uint32_t* qzeros;     // strip-ordered zero nibbles (GPTQ metadata)
-  const uint16_t* x;          // bf16 [K] in the weight's input order
+  const uint16_t* x;          // bf16 [K] in the weight's input order, or (perm set) in
+  const uint16_t* perm;       //   the checkpoint's order: row k of the weight is x[perm[k]]
   const float* xpart;         // gate|up partials [xsplits, xpart_ld]
-  int xsplits, xpart_ld;
   const uint16_t* hn;         // residual stream h [K] (input order), norm weight [K],
   const uint16_t* wn;         //   sums of squares of h per 16 columns
   const float* slots;
-  float eps;
   float* y;                   // fp32 [N]
   uint16_t* y16;              // bf16 [N] (store epilogue, when set instead of y)
   uint16_t* h;                // bf16 [N], updated in place
@@ -174,9 +174,16 @@ struct StripArgs {
   uint16_t* h_ord;            // may be NULL
   float* slots_out;           // one sum of squares per 16 columns
   uint16_t* act;              // bf16 [N/2]: silu(gate) * up, 32-column gate|up interleave
-  int K, N, group, zero_offset, kblocks, xcd_order, fmt;
+  int xsplits, xpart_ld;
+  float eps;
+  int K, N, group, zero_offset, kblocks;
+  int16_t xcd_order, fmt;
   mtl_strip_geometry geom;    // requested launch shape (all 0: automatic)
 };
+// The launch passes StripArgs by value: its 184 bytes put the kernel's arguments at 440
+// bytes with the hidden ones; at 448 (8 bytes more) every strip launch measured about
+// 0.25 us slower.
+static_assert(sizeof(StripArgs) == 184, "StripArgs size");
 
 enum : int { STRIP_EPI_STORE = 0, STRIP_EPI_RESID = 1, STRIP_EPI_SILU = 2 };
 

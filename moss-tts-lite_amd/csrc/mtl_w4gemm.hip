@@ -775,6 +775,7 @@ static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
   a.scales = static_cast<const uint16_t*>(scales);
   a.qzeros = reinterpret_cast<const uint32_t*>(qzeros);
   a.x = nullptr;
+  a.perm = nullptr;
   a.xpart = nullptr;
   a.xsplits = 0;
   a.xpart_ld = 0;
@@ -1071,6 +1072,31 @@ int mtl_workspace_init(void* workspace, int64_t ws_bytes, void* stream) {
 int32_t mtl_w4_gemm_splits(int64_t K, int64_t N) {
   if (K <= 0 || N <= 0 || K % 8 != 0) return 0;
   return plan_for(K, N).splits;
+}
+
+int mtl_w4_gemv_strip(const void* x, int64_t K, const uint16_t* perm,
+                      const int32_t* strip_weight, const void* strip_scales,
+                      const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                      int32_t zero_offset, int32_t out_dtype, void* y, void* stream) {
+  if (!x || !strip_weight || !strip_scales || !strip_zeros || !y) return MTL_ERR_INVALID_ARG;
+  if (out_dtype != MTL_OUT_BF16 && out_dtype != MTL_OUT_F32) return MTL_ERR_INVALID_ARG;
+  if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
+    return MTL_ERR_GROUP;
+  if (K <= 0 || N <= 0 || K % 256 != 0 || N % 16 != 0 || K % group_size != 0 ||
+      K > (perm ? 12288 : 16384) || N * K / 2 >= ((int64_t)1 << 31) ||
+      !strip_blocks_per_wave(K, 1, group_size))
+    return MTL_ERR_SHAPE;
+  if (!aligned16(x) || (perm && !aligned16(perm)) || !aligned16(strip_weight) ||
+      !strip_meta_aligned(MTL_LAYOUT_STRIP, strip_scales, strip_zeros) ||
+      (reinterpret_cast<uintptr_t>(y) & (out_dtype == MTL_OUT_F32 ? 15u : 7u)))
+    return MTL_ERR_ALIGN;
+  StripArgs sa = strip_args(K, strip_weight, strip_scales, strip_zeros, N, group_size,
+                            zero_offset);
+  sa.x = static_cast<const uint16_t*>(x);
+  sa.perm = perm;
+  if (out_dtype == MTL_OUT_F32) sa.y = static_cast<float*>(y);
+  else sa.y16 = static_cast<uint16_t*>(y);
+  return strip_launch(sa, (hipStream_t)stream);
 }
 
 int mtl_w4_gemm_partials(const void* x, const float* xpart, int32_t xsplits, int64_t xpart_ld,

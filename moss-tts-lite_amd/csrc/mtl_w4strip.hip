@@ -38,6 +38,14 @@ constexpr int strip_max_waves(int gr, int nb, int win) {
   return gr == 1 && nb >= 8 ? 8 : nb >= 16 ? 12 : kStripMaxWaves;
 }
 constexpr int kStripAux = 2;          // weight stream: non-temporal (read once per step)
+// Strips per workgroup of the act-order gather (x copied into LDS and gathered there): the
+// whole of x is staged per workgroup, so fewer, wider workgroups stage less, as long as
+// they stay about as many as the CUs.  Two strips where that leaves at least 192
+// workgroups (measured, GPTQ module at one row: q|k|v 6144 columns 4.99 -> 4.6 us, gate|up
+// 24576 columns 11.7 -> 10.3 us; o and down, 4096 columns, are slower with 128 workgroups:
+// 4.04 -> 4.4 and 7.95 -> 9.4 us; four strips are slower on every shape).
+constexpr int kGatherCT = 2;
+constexpr int kGatherMinWGs = 192;
 
 // The body of one workgroup: `bid` of a launch of G strip workgroups (the kernel's own
 // grid, or the first G workgroups of the combined launch below).
@@ -84,6 +92,20 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
   // 1. Activation loads of this thread's items of the slice (raw; transformed once the
   //    weights are in flight).  Every item index is below K/8: K = 128 * KW * NB.
   const int tt = cs * 64 + lane;               // thread index among the slice's stagers
+  // XSRC_PERM: the workgroup copies all of x (K/8 items, XR per thread) into LDS behind
+  // the slices' tile, and each stager gathers its items' 8 channels from there through
+  // perm (loaded with x, so the gather costs one round trip, like the other sources)
+  constexpr int XR = XSRC == XSRC_PERM ? (NB + 4 * CT - 1) / (4 * CT) : 1;
+  u32x4 xr[XR];
+  u32x4 pv[XSRC == XSRC_PERM ? ROUNDS : 1];    // the items' 8 gather indices (uint16)
+  if (XSRC == XSRC_PERM) {
+    const int nitems = a.K >> 3;
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int i = r * (int)blockDim.x + (int)threadIdx.x;
+      xr[r] = *reinterpret_cast<const u32x4*>(a.x + (size_t)(i < nitems ? i : 0) * 8);
+    }
+  }
   u32x4 xv[ROUNDS], wv[XSRC == XSRC_RMSNORM ? ROUNDS : 1];
   float4 sg[XSRC == XSRC_SILU_PART ? ROUNDS : 1][2], su[XSRC == XSRC_SILU_PART ? ROUNDS : 1][2];
   const float* sbase[XSRC == XSRC_SILU_PART ? ROUNDS : 1];
@@ -95,6 +117,9 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
     const int it = item0 + (iok[r] ? i : 0);
     if (XSRC == XSRC_BF16) {
       xv[r] = *reinterpret_cast<const u32x4*>(a.x + (size_t)it * 8);
+    } else if (XSRC == XSRC_PERM) {
+      xv[r] = u32x4{0u, 0u, 0u, 0u};
+      pv[r] = *reinterpret_cast<const u32x4*>(a.perm + (size_t)it * 8);
     } else if (XSRC == XSRC_RMSNORM) {
       xv[r] = *reinterpret_cast<const u32x4*>(a.hn + (size_t)it * 8);
       wv[r] = *reinterpret_cast<const u32x4*>(a.wn + (size_t)it * 8);
@@ -174,6 +199,30 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
   __builtin_amdgcn_sched_barrier(0);
 
   // 4. x into LDS in pair order, with per-group sums (fixed butterfly order).
+  if (XSRC == XSRC_PERM) {
+    u32x4* xs = xa_all + kw * ITEMS;           // x in the checkpoint's order
+    const int nitems = a.K >> 3;
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int i = r * (int)blockDim.x + (int)threadIdx.x;
+      if (i < nitems) xs[i] = xr[r];
+    }
+    __syncthreads();
+    if (stages) {
+      const uint16_t* xs16 = reinterpret_cast<const uint16_t*>(xs);
+#pragma unroll
+      for (int r = 0; r < ROUNDS; ++r) {
+        const uint32_t p[8] = {pv[r].x & 0xffffu, pv[r].x >> 16, pv[r].y & 0xffffu,
+                               pv[r].y >> 16, pv[r].z & 0xffffu, pv[r].z >> 16,
+                               pv[r].w & 0xffffu, pv[r].w >> 16};
+        uint32_t e[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = xs16[p[c]];
+        xv[r] = u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                      e[6] | (e[7] << 16)};
+      }
+    }
+  }
   if (stages) {
     float norm_r = 0.f;
     if (XSRC == XSRC_RMSNORM)
@@ -422,11 +471,15 @@ w4_strip_bf16_kernel(StripArgs a, Bf16RowsArgs b, int ga) {
 static int strip_geometry(const StripArgs& a, StripGeom& g) {
   const int gr = a.group / 32;
   const mtl_strip_geometry& r = a.geom;
-  const int auto_ct = a.act ? 2 : 1;
+  const bool gather = a.perm && !a.h && !a.xpart && !a.hn;
+  const int auto_ct = a.act ? 2
+                     : gather && a.N % (kStripCols * kGatherCT) == 0 &&
+                               a.N / (kStripCols * kGatherCT) >= kGatherMinWGs &&
+                               blocks_per_wave(a.K, kGatherCT, a.group) ? kGatherCT : 1;
   g.ct = r.strips_per_wg ? r.strips_per_wg : auto_ct;
   if (a.act) {
     if (g.ct != 2 && g.ct != 6) return MTL_ERR_UNSUPPORTED;
-  } else if (a.hn && !a.h) {
+  } else if ((a.hn && !a.h) || gather) {
     if (g.ct != 1 && g.ct != 2 && g.ct != 4) return MTL_ERR_UNSUPPORTED;
   } else if (g.ct != 1) {
     return MTL_ERR_UNSUPPORTED;
@@ -447,7 +500,9 @@ template <int GR, int XSRC, int EPI, int CT, int FMT>
 static void strip_nb(const StripArgs& a, const StripGeom& g, hipStream_t st) {
   const dim3 grid(a.N / (kStripCols * CT));
   const dim3 block(64 * CT * (a.kblocks / g.nb));
-  const size_t lds = (size_t)(a.kblocks / g.nb) * 16 * g.nb * sizeof(u32x4);
+  // the slices' x tile, and for the act-order gather all of x behind it
+  const size_t lds = (size_t)(a.kblocks / g.nb) * 16 * g.nb * sizeof(u32x4) +
+                     (XSRC == XSRC_PERM ? (size_t)a.K * 2 : 0);
   constexpr bool kDeep = GR >= 4 && FMT == STRIP_META_GPTQ;
 #define MTL_STRIP_LAUNCH(NB_, WIN_) \
   hipLaunchKernelGGL((w4_strip_kernel<GR, XSRC, EPI, NB_, CT, WIN_, FMT>), grid, block, lds, st, a)
@@ -491,6 +546,10 @@ static void strip_variant(const StripArgs& a, const StripGeom& g, hipStream_t st
     else strip_nb<GR, XSRC_RMSNORM, STRIP_EPI_STORE, 1, FMT>(a, g, st);
   } else if (a.xpart) {
     strip_nb<GR, XSRC_SILU_PART, STRIP_EPI_STORE, 1, FMT>(a, g, st);
+  } else if (FMT == STRIP_META_GPTQ && a.perm) {
+    if (g.ct == 4) strip_nb<GR, XSRC_PERM, STRIP_EPI_STORE, 4, FMT>(a, g, st);
+    else if (g.ct == 2) strip_nb<GR, XSRC_PERM, STRIP_EPI_STORE, 2, FMT>(a, g, st);
+    else strip_nb<GR, XSRC_PERM, STRIP_EPI_STORE, 1, FMT>(a, g, st);
   } else {
     strip_nb<GR, XSRC_BF16, STRIP_EPI_STORE, 1, FMT>(a, g, st);
   }

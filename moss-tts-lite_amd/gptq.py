@@ -55,6 +55,7 @@ class GPTQLinear(torch.nn.Module):
         self._strip: torch.Tensor | None = None
         self._strip_meta: tuple | None = None
         self._strip_only = False
+        self._perm16: torch.Tensor | None = None     # the act-order index as int16 (K <= 12288)
 
     @classmethod
     def from_buffers(cls, qweight, qzeros, scales, g_idx=None, group_size: int = 128,
@@ -172,7 +173,7 @@ class GPTQLinear(torch.nn.Module):
             raise ValueError("cols must list every output column once")
         if self._kernel_qweight is None:
             self.post_init()
-        self._tiled = self._strip = self._strip_meta = None
+        self._tiled = self._strip = self._strip_meta = self._perm16 = None
         sorted_separately = self._kernel_qweight is not self.qweight
         self._kernel_qweight = self._kernel_qweight[:, cols].contiguous()
         if sorted_separately and self.qweight.numel():
@@ -184,12 +185,22 @@ class GPTQLinear(torch.nn.Module):
         return self
 
     def forward(self, x: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-        """``x[..., K] @ dequant(W)``.  Few rows run on the skinny strip GEMM where it pays
-        (:func:`ops.strip_rows_pays`; it builds the strip copy of the weight once and keeps
-        it), the others on the split-K GEMM over the AutoGPTQ layout; both through the
-        ``torch.ops.mtl`` operators (one dispatcher call, torch's stream and allocator)."""
+        """``x[..., K] @ dequant(W)``.  One row runs on the full-K strip GEMV (x gathered
+        through the act-order index while staging), few rows on the skinny strip GEMM where
+        it pays (:func:`ops.strip_rows_pays`); both read the strip copy of the weight, built
+        once and kept.  The others run on the split-K GEMM over the AutoGPTQ layout (or,
+        after :meth:`keep_strip_only`, the prompt-length GEMM over the strip copy).  Calls
+        go through the ``torch.ops.mtl`` operators (one dispatcher call, torch's stream and
+        allocator)."""
         m = x.numel() // self.in_features if self.in_features else 0
         perm = self.perm
+        if m == 1 and self.supports_strip() and (perm is None or self.in_features <= 12288):
+            strip = self.stream_weight(strip=True)[0]
+            sc, qz = self.strip_meta()
+            if perm is not None and self._perm16 is None:
+                self._perm16 = perm.to(torch.int16)
+            return ops.strip_gemv(x, strip, sc, qz, self.out_features, self.group_size,
+                                  self.zero_offset, self._perm16, out_dtype)
         if m and self.supports_strip() and (
                 (self._strip_only and m <= 16) or
                 ops.strip_rows_pays(m, self.in_features, self.out_features, perm is not None)):

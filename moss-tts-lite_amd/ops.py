@@ -286,6 +286,19 @@ def strip_rows_gemm(x: torch.Tensor, strip_weight: torch.Tensor, qzeros: torch.T
                        N.META_GPTQ, perm, out, out_dtype)
 
 
+def strip_gemv(x: torch.Tensor, strip_weight: torch.Tensor, strip_scales: torch.Tensor,
+               strip_zeros: torch.Tensor, n: int, group_size: int, zero_offset: int = 0,
+               perm: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """One row on the full-K strip GEMV (``mtl_w4_gemv_strip``, through the ``mtl::strip_gemv``
+    operator): ``x [..., K]`` with one row, the strip copy of a GPTQ linear and its
+    strip-ordered metadata (:func:`strip_weights`, :func:`strip_meta`), x gathered through
+    ``perm`` (int16 [K]: :func:`actorder_prepare`'s index narrowed, K <= 12288) while
+    staging.  Returns ``[..., n]``."""
+    return torch_ops().strip_gemv(x, strip_weight, strip_scales, strip_zeros, n, group_size,
+                                  zero_offset, perm, out_dtype)
+
+
 def strip_rows_qsz(x: torch.Tensor, packed: torch.Tensor, qsz: torch.Tensor, group_size: int,
                    out: torch.Tensor | None = None,
                    out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:

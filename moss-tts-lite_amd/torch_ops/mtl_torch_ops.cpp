@@ -2,9 +2,10 @@
 // mtl::convert_weight_to_int4pack, the drop-ins for torch._weight_int4pack_mm and
 // torch.ops.aten._convert_weight_to_int4pack that the reference calls eagerly
 // (moss_tts_lite/fast.py:97-99, 118; gptq.py:75-76, 582; fast_native.py:169), and
-// mtl::gptq_gemm / mtl::strip_rows_gemm, the int4 products of the GPTQ linear module's
-// forward over its AutoGPTQ tensors (the layer the reference's kernel_linear serves,
-// gptq.py:577-585), so an eager module call costs one dispatcher call per launch group.
+// mtl::gptq_gemm / mtl::strip_rows_gemm / mtl::strip_gemv, the int4 products of the GPTQ
+// linear module's forward over its AutoGPTQ tensors and their strip copy (the layer the
+// reference's kernel_linear serves, gptq.py:577-585), so an eager module call costs one
+// dispatcher call per launch group.
 //
 // Host code only: each operator checks its tensors, allocates the output (and the split-K
 // workspace) from torch's caching allocator, and calls the C entry on torch's current
@@ -225,6 +226,51 @@ at::Tensor strip_rows_gemm(const at::Tensor& x, const at::Tensor& strip_weight,
   return y.view(out_shape(x, n));
 }
 
+// One row on the full-K strip GEMV (mtl_w4_gemv_strip) over the strip copy of an AutoGPTQ
+// linear and its strip-ordered metadata, x gathered through perm (int16, the act-order index
+// narrowed) for an act-order linear.
+at::Tensor strip_gemv(const at::Tensor& x, const at::Tensor& strip_weight,
+                      const at::Tensor& strip_scales, const at::Tensor& strip_zeros, int64_t n,
+                      int64_t group_size, int64_t zero_offset,
+                      const c10::optional<at::Tensor>& perm, at::ScalarType out_dtype) {
+  const int64_t K = x.size(-1);
+  TORCH_CHECK(x.numel() == K, "strip_gemv takes one row of x, got ", x.sizes());
+  TORCH_CHECK(strip_weight.scalar_type() == at::kInt && strip_weight.numel() * 8 == n * K,
+              "strip_weight must be the int32 strip copy of a [", K, ", ", n, "] weight");
+  TORCH_CHECK(strip_scales.scalar_type() == at::kHalf && strip_scales.numel() == n * K / group_size,
+              "strip_scales must be the fp16 strip-ordered scales (mtl_w4_strip_meta)");
+  TORCH_CHECK(strip_zeros.scalar_type() == at::kInt, "strip_zeros must be int32");
+  const at::Tensor x2 = rows_of(x, K);
+  TORCH_CHECK(x2.is_cuda() && strip_weight.device() == x2.device() &&
+                  strip_scales.device() == x2.device() && strip_zeros.device() == x2.device(),
+              "x and the strip tensors must be on one HIP device");
+  const c10::DeviceGuard guard(x2.device());
+  at::Tensor pk;
+  const uint16_t* pp = nullptr;
+  if (perm.has_value()) {
+    TORCH_CHECK(perm->scalar_type() == at::kShort && perm->numel() == K,
+                "perm must be int16 [", K, "] (the act-order index, narrowed)");
+    pk = perm->contiguous();
+    pp = reinterpret_cast<const uint16_t*>(pk.data_ptr());
+  }
+  const at::Tensor w = strip_weight.contiguous(), sc = strip_scales.contiguous(),
+                   z = strip_zeros.contiguous();
+  at::Tensor y = at::empty({1, n}, x2.options().dtype(out_dtype));
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(x2.device().index()).stream();
+  check_status(mtl_w4_gemv_strip(x2.data_ptr(), K, pp, w.data_ptr<int32_t>(), sc.data_ptr(),
+                                 z.data_ptr<int32_t>(), n, (int32_t)group_size,
+                                 (int32_t)zero_offset, out_code(out_dtype), y.data_ptr(), stream),
+               "mtl_w4_gemv_strip");
+  return y.view(out_shape(x, n));
+}
+
+at::Tensor strip_gemv_meta(const at::Tensor& x, const at::Tensor& strip_weight,
+                           const at::Tensor& strip_scales, const at::Tensor& strip_zeros,
+                           int64_t n, int64_t group_size, int64_t zero_offset,
+                           const c10::optional<at::Tensor>& perm, at::ScalarType out_dtype) {
+  return at::empty(out_shape(x, n), x.options().dtype(out_dtype));
+}
+
 at::Tensor strip_rows_gemm_meta(const at::Tensor& x, const at::Tensor& strip_weight,
                                 const at::Tensor& qzeros, const at::Tensor& scales, int64_t n,
                                 int64_t group_size, int64_t zero_offset,
@@ -244,6 +290,9 @@ TORCH_LIBRARY(mtl, m) {
   m.def("strip_rows_gemm(Tensor x, Tensor strip_weight, Tensor qzeros, Tensor scales, int n, "
         "int group_size, int zero_offset=0, Tensor? perm=None, "
         "ScalarType out_dtype=bfloat16) -> Tensor");
+  m.def("strip_gemv(Tensor x, Tensor strip_weight, Tensor strip_scales, Tensor strip_zeros, "
+        "int n, int group_size, int zero_offset=0, Tensor? perm=None, "
+        "ScalarType out_dtype=bfloat16) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(mtl, CUDA, m) {
@@ -251,6 +300,7 @@ TORCH_LIBRARY_IMPL(mtl, CUDA, m) {
   m.impl("convert_weight_to_int4pack", &convert_weight_to_int4pack);
   m.impl("gptq_gemm", &gptq_gemm);
   m.impl("strip_rows_gemm", &strip_rows_gemm);
+  m.impl("strip_gemv", &strip_gemv);
 }
 
 TORCH_LIBRARY_IMPL(mtl, Meta, m) {
@@ -258,4 +308,5 @@ TORCH_LIBRARY_IMPL(mtl, Meta, m) {
   m.impl("convert_weight_to_int4pack", &convert_weight_to_int4pack_meta);
   m.impl("gptq_gemm", &gptq_gemm_meta);
   m.impl("strip_rows_gemm", &strip_rows_gemm_meta);
+  m.impl("strip_gemv", &strip_gemv_meta);
 }

@@ -199,6 +199,22 @@ def test_prefill_gemm_validation(lib):
     assert lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4100, 4096) == 0
 
 
+def test_gemv_strip_validation(lib):
+    gv = lambda k, n, g=128, perm=None, odt=0, x=FAKE, y=FAKE, w=FAKE: lib.mtl_w4_gemv_strip(  # noqa: E731
+        x, k, perm, w, FAKE, FAKE, n, g, 0, odt, y, None)
+    assert gv(4096, 4096, x=None) == N.MTL_ERR_INVALID_ARG
+    assert gv(4096, 4096, w=None) == N.MTL_ERR_INVALID_ARG
+    assert gv(4096, 4096, odt=2) == N.MTL_ERR_INVALID_ARG
+    assert gv(4096, 4096, g=96) == N.MTL_ERR_GROUP
+    assert gv(4224, 4096) == N.MTL_ERR_SHAPE             # K % 256
+    assert gv(4096, 4104) == N.MTL_ERR_SHAPE             # N % 16
+    assert gv(32768, 512) == N.MTL_ERR_SHAPE             # K <= 16384
+    assert gv(16384, 512, perm=FAKE) == N.MTL_ERR_SHAPE  # the gather keeps x in LDS: K <= 12288
+    assert gv(4096, 4096, perm=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
+    assert gv(4096, 4096, x=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
+    assert gv(4096, 4096, odt=1, y=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN   # fp32: 16 B
+
+
 def test_prefill_row_entry_validation(lib):
     eps = ctypes.c_float(1e-6)
     sc = ctypes.c_float(0.088)
@@ -326,6 +342,10 @@ def test_torch_operators_registered():
         mtl.weight_int4pack_mm(x[:, :2048], packed, 128, qsz)
     pre = torch.empty(512, 2048, dtype=torch.uint8, device="meta")
     assert tuple(mtl.convert_weight_to_int4pack(pre, 8).shape) == (64, 32, 32, 4)
+    sw = torch.empty(4096 * 512 // 8, dtype=torch.int32, device="meta")
+    ssc = torch.empty(32, 512, dtype=torch.float16, device="meta")
+    szr = torch.empty(32, 64, dtype=torch.int32, device="meta")
+    assert tuple(mtl.strip_gemv(x[:1], sw, ssc, szr, 512, 128).shape) == (1, 512)
     with pytest.raises(RuntimeError):
         mtl.convert_weight_to_int4pack(pre, 3)
     # the GPTQ module's operators over the AutoGPTQ tensors: [..., K] in, [..., N] out

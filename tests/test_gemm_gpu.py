@@ -340,10 +340,50 @@ def test_gptq_linear_strip_only_forward(dev, act_order):
     for m in rows:
         y = lin(x[:m], out_dtype=torch.float32)
         assert rel_l2(y.cpu().numpy(), case["y_ref"][:m]) < TOL_F32, m
-        if ops.strip_rows_pays(m, k, n, act_order):
+        if m == 1 or ops.strip_rows_pays(m, k, n, act_order):
             assert torch.equal(y, ref[m]), m
     with pytest.raises(RuntimeError, match="strip copy"):
         lin.kernel_args()
+
+
+@pytest.mark.parametrize("group,k,n", [(128, 4096, 24576), (128, 12288, 4096), (32, 4096, 1024),
+                                       (64, 2048, 768), (256, 4096, 512), (128, 4096, 6144)])
+def test_gemv_strip_act_order_gather(dev, group, k, n):
+    # mtl_w4_gemv_strip: x in the checkpoint's channel order, gathered through perm from the
+    # LDS copy while staging, gives the same bits as x taken into the sorted row order
+    # beforehand and gathered through the identity (the same launch, the same sums), in
+    # bf16 and fp32, and the float64 product of the original weight; so does the launch
+    # without perm on the sorted x (its own launch shape: within fp32 rounding)
+    lib = N.load()
+    case = synth.gptq_case(k=k, n=n, m=1, group=group, act_order=True, seed=group + k + n)
+    qws, perm = ops.actorder_prepare(t_i32(case["qweight"], dev), t_i32(case["g_idx"], dev), group)
+    strip = ops.strip_weights(qws)
+    sc, qz = ops.strip_meta(t_f16(case["scales"], dev), t_i32(case["qzeros"], dev), group)
+    x = t_bf16(case["x_bits"], dev)[0].contiguous()
+    xs = x[perm.long()].contiguous()
+    perm16 = perm.to(torch.int16)
+    ident16 = torch.arange(k, dtype=torch.int16, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    for odt, dt in ((N.OUT_F32, torch.float32), (N.OUT_BF16, torch.bfloat16)):
+        y = torch.full((n,), float("nan"), dtype=dt, device=dev)
+        ys = torch.full((n,), float("nan"), dtype=dt, device=dev)
+        N.check(lib.mtl_w4_gemv_strip(x.data_ptr(), k, perm16.data_ptr(), strip.data_ptr(),
+                                      sc.data_ptr(), qz.data_ptr(), n, group, 0, odt,
+                                      y.data_ptr(), st), "gather")
+        yn = torch.full((n,), float("nan"), dtype=dt, device=dev)
+        N.check(lib.mtl_w4_gemv_strip(xs.data_ptr(), k, ident16.data_ptr(), strip.data_ptr(),
+                                      sc.data_ptr(), qz.data_ptr(), n, group, 0, odt,
+                                      ys.data_ptr(), st), "sorted x, identity")
+        N.check(lib.mtl_w4_gemv_strip(xs.data_ptr(), k, None, strip.data_ptr(), sc.data_ptr(),
+                                      qz.data_ptr(), n, group, 0, odt, yn.data_ptr(), st),
+                "sorted x, no gather")
+        torch.cuda.synchronize()
+        assert torch.equal(y, ys), dt
+        tol = TOL_F32 if dt == torch.float32 else TOL_BF16
+        for out in (y, yn):
+            err = rel_l2(out.float().cpu().numpy(), case["y_ref"][0])
+            print(f"gemv strip g{group} {k}x{n} {dt} rel_l2={err:.2e}")
+            assert err < tol
 
 
 def test_strip_rows_matches_strip_gemv_at_m1(dev):
