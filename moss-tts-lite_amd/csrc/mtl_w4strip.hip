@@ -137,7 +137,9 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
   }
   const bool stages = cs * 64 < ITEMS;         // wave-uniform: this wave stages items
   SlotLoad slot_l;
-  if (XSRC == XSRC_RMSNORM && stages) slot_issue(a.slots, a.K, lane, slot_l);
+  // RMSNorm: wave 0 alone loads the sums-of-squares slots and shares r through LDS (every
+  // staging wave loading all of them cost 1 KB per wave: q|k|v 4.72 -> 4.56 us)
+  if (XSRC == XSRC_RMSNORM && wave == 0) slot_issue(a.slots, a.K, lane, slot_l);
   // residual epilogue inputs of wave 0's column owners, read ahead of everything else
   u32x2 h_pre{0u, 0u};
   int32_t sc_pre[4] = {0, 0, 0, 0};
@@ -223,10 +225,17 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
       }
     }
   }
+  __shared__ float norm_sh;
+  if (XSRC == XSRC_RMSNORM) {
+    if (wave == 0) {
+      const float t = rsqrtf(wave_sum_valu(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
+      if (lane == 0) norm_sh = t;
+    }
+    __syncthreads();
+  }
   if (stages) {
     float norm_r = 0.f;
-    if (XSRC == XSRC_RMSNORM)
-      norm_r = rsqrtf(wave_sum_valu(slot_finish(slot_l, a.K, lane)) / (float)a.K + a.eps);
+    if (XSRC == XSRC_RMSNORM) norm_r = norm_sh;
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
       u32x4 v = xv[r];
