@@ -145,12 +145,13 @@ __device__ __forceinline__ void bf16_rows_norm_body(const Bf16RowsArgs& p, int b
   }
 }
 
-// Rows per workgroup of bf16_rows_norm_kernel: a band that spreads N over the CUs, 4 rows
-// at least (one per wave) and a multiple of 8 above that (two rows per wave and pass).
+// Rows per workgroup of bf16_rows_norm_kernel and of the bf16 half of the combined launch:
+// 8 (two rows per wave and pass), or 16 where that still leaves 3 workgroups per CU.
+// Measured on the MOSS step's kept linears (v_proj 1024 rows, up_proj 12288 rows beside
+// their int4 partners): 526 -> 541 steps/s against a band spreading the rows over the CUs
+// (4 and 48 rows); 16 rows for v_proj or 8 / 12 for up_proj measured the same or slower.
 inline int bf16_rows_per_wg(int64_t N, int cus) {
-  int64_t r = (N + cus - 1) / cus;
-  r = r <= 4 ? 4 : (r + 7) / 8 * 8;
-  return (int)r;
+  return N / 16 >= 3 * (int64_t)cus ? 16 : 8;
 }
 
 
