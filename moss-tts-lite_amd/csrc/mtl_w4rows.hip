@@ -63,6 +63,14 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
   const int pgrp = a.kp / a.group;             // groups per phase (LDS sums)
   const int kbp = a.kp >> 7;                   // blocks per phase
   const int nphase = a.K / a.kp;
+  // x item f of a phase is row f / K8, item f % K8: a shift and a mask where K8 is a power
+  // of two (every phase of the decode shapes), instead of the integer division's ~40 VALU
+  const bool k8p2 = (K8 & (K8 - 1)) == 0;
+  const int k8s = 31 - __builtin_clz(K8);
+  auto row_of = [&](int f) { return k8p2 ? f >> k8s : f / K8; };
+  const int kr8 = a.K >> 3;                    // x items per row over all of K
+  const bool kr8p2 = (kr8 & (kr8 - 1)) == 0;
+  const int kr8s = 31 - __builtin_clz(kr8);
   // rows XS = K8 + 1 items apart: the 16 rows an MFMA's A operand reads then start 16
   // bytes apart in the LDS banks instead of all on the same banks
   const int XS = K8 + 1;
@@ -98,7 +106,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int f = f0 + u * (int)blockDim.x + threadIdx.x;
-      const int m = f / (a.K >> 3), i = f - m * (a.K >> 3);
+      const int m = kr8p2 ? f >> kr8s : f / kr8, i = f - m * kr8;
       const int xo = f < xr_items ? (m * (int)a.ldx + 8 * i) * 2 : xbytes;
       rv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
     }
@@ -120,7 +128,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       const int f = f0 + u * nthr + threadIdx.x;
-      const int m = f / K8, i = f - m * K8;
+      const int m = row_of(f), i = f - m * K8;
       const int xo = f < total ? (m * (int)a.ldx + c0 + 8 * i) * 2 : xbytes;
       v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0));
     }
@@ -184,10 +192,14 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
       if (fb >= total) break;
       const int f = fb + lane;
       float sum;
-      const u32x4 pv = pair_order(v[u], sum);
+      // v_perm and a v_dot2 chain: about 8 VALU per item against pair_order's 20 (the sums
+      // round in another order than the M = 1 strip GEMV's tree: within fp32 rounding);
+      // with the index arithmetic above, gate|up at M = 16 went from 15.8 to 14.6 us and
+      // down from 21.0 to 15.4
+      const u32x4 pv = pair_order_dot(v[u], sum);
       sum = group_sum_valu<GI>(sum);           // every lane of the wave active here
       if (f < total) {                                 // M * K8 need not fill the wave
-        const int m = f / K8, i = f - m * K8;
+        const int m = row_of(f), i = f - m * K8;
         xa[m * XS + i] = pv;
         if ((i & (GI - 1)) == 0) xg[(i / GI) * 16 + m] = sum;
       }
@@ -205,11 +217,11 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
           const int f = f0 + u * nthr + threadIdx.x;
-          const int i = f - (f / K8) * K8;
+          const int i = f - row_of(f) * K8;
           const int po = f < total ? (c0 + 8 * i) * 4 : a.K * 4;   // past the end: 0
           const int4 p0 = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po, 0, 0));
           const int4 p1 = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po + 16, 0, 0));
-          const int mr = f / K8 < a.M ? f / K8 : a.M - 1;          // items past the end: unused
+          const int mr = row_of(f) < a.M ? row_of(f) : a.M - 1;          // items past the end: unused
           const uint16_t* xm = xr + mr * a.K;
           v[u] = u32x4{xm[p0.x] | ((uint32_t)xm[p0.y] << 16), xm[p0.z] | ((uint32_t)xm[p0.w] << 16),
                        xm[p1.x] | ((uint32_t)xm[p1.y] << 16), xm[p1.z] | ((uint32_t)xm[p1.w] << 16)};
@@ -222,7 +234,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
           for (int u = 0; u < HB; ++u) {
             const int f = f0 + (u0 + u) * nthr + threadIdx.x;
-            const int i = f - (f / K8) * K8;
+            const int i = f - row_of(f) * K8;
             const int po = f < total ? (c0 + 8 * i) * 4 : a.K * 4;   // past the end: 0
             pi[u][0] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po, 0, 0));
             pi[u][1] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(prs, po + 16, 0, 0));
@@ -230,7 +242,7 @@ __global__ void __launch_bounds__(64 * rows_max_waves(NB), 1) w4_rows_kernel(Row
 #pragma unroll
           for (int u = 0; u < HB; ++u) {
             const int f = f0 + (u0 + u) * nthr + threadIdx.x;
-            const int ro = (f < total ? (f / K8) * (int)a.ldx : xbytes) * 2;
+            const int ro = (f < total ? row_of(f) * (int)a.ldx : xbytes) * 2;
             auto e = [&](int c) {
               return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(xrs, ro + 2 * c, 0, 0);
             };
