@@ -155,8 +155,8 @@ int mtl_gptq_actorder_prepare(const int32_t* qweight, const int32_t* g_idx,
  *   workspace  NULL, or mtl_int4pack_mm_workspace_bytes(M, K, N) bytes: lets a launch
  *           with M > 1 split K over workgroups (results then differ by fp32 rounding)
  * M = 1 runs the full-K strip GEMV (K <= 16384); 2 <= M <= 16 the skinny strip GEMM
- * (mtl_w4_gemm_strip_rows_ex) where M * 1024 <= 1.5 N, more rows the prompt-length GEMM
- * (N % 128 == 0; otherwise the skinny GEMM 16 rows at a time).  K % 256 == 0, K % g == 0,
+ * (mtl_w4_gemm_strip_rows_ex), more rows the prompt-length GEMM (N % 128 == 0; otherwise
+ * the skinny GEMM 16 rows at a time).  K % 256 == 0, K % g == 0,
  * N % 16 == 0 (torch asks N % 8 only).
  */
 int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N);

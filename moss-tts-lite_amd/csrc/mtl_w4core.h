@@ -204,11 +204,11 @@ int strip_rows(const void* x, int64_t M, int64_t ldx, int64_t K, const int32_t* 
                int32_t group_size, int32_t zero_offset, int fmt, void* y, int64_t ldy,
                int32_t out_dtype, void* stream);
 
-// Whether the skinny-batch strip GEMM pays at M rows over N columns: every workgroup (one
-// per CU) stages all M rows of x, 2 M K bytes against the N K / 512 bytes of weights a CU
-// streams, and measured on MI355X it stays ahead while M * 1024 <= 1.5 N (every M <= 16 on
-// a 24576-column projection, M <= 6 at 4096 columns).
-inline bool strip_rows_pays(int64_t M, int64_t N) { return M <= 16 && M * 1024 * 2 <= 3 * N; }
+// Whether the skinny-batch strip GEMM pays at M rows over N columns (without an act-order
+// gather): measured on MI355X it is ahead of the prompt-length GEMM at every M <= 16 on the
+// four decode shapes, g32 and g128 (q|k|v 6.5-9.1 against 14.2-17.7 us, down 9.8-21.9
+// against 19.9-25.6 us, weights rotated past the Infinity Cache).
+inline bool strip_rows_pays(int64_t M, int64_t /*N*/) { return M <= 16; }
 
 // The residual add of the decode step (fast.py:168-171) on 4 consecutive columns:
 // h = bf16(bf16(acc) + h); returns their sum of squares (fixed fma order).

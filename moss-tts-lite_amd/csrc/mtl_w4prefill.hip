@@ -530,8 +530,8 @@ int64_t mtl_int4pack_mm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
 }
 
 // The drop-in for torch._weight_int4pack_mm: M = 1 on the full-K strip GEMV, 2 to 16 rows on
-// the skinny strip GEMM where it pays (strip_rows_pays), more on the prompt-length GEMM (or,
-// when N is not a multiple of 128, the skinny GEMM 16 rows at a time).
+// the skinny strip GEMM (strip_rows_pays), more on the prompt-length GEMM (or, when N is not
+// a multiple of 128, the skinny GEMM 16 rows at a time).
 int mtl_int4pack_mm(const void* x, int64_t M, int64_t K, const int32_t* packed,
                     int32_t group_size, const void* qsz, int64_t N, void* y, void* workspace,
                     int64_t ws_bytes, void* stream) {

@@ -159,7 +159,7 @@ def weight_int4pack_mm(x: torch.Tensor, packed: torch.Tensor, q_group_size: int,
     a concatenation along dim 0 is a concatenation along N, as with torch's tiles);
     ``qScaleAndZeros`` bf16 ``[K/g, N, 2]`` = (scale, zero) with
     ``w = (q - 8) * scale + zero`` (moss_tts_lite/gptq.py:87-97).  Returns bf16 ``[M, N]``.
-    M = 1 runs the full-K strip GEMV, 2 to 16 rows the skinny strip GEMM where it pays, more
+    M = 1 runs the full-K strip GEMV, 2 to 16 rows the skinny strip GEMM, more
     rows the prompt-length GEMM.  ``RuntimeError`` for a wrong shape, dtype or group size,
     as torch's operator raises.
     """
@@ -257,15 +257,14 @@ def strip_meta(scales: torch.Tensor, qzeros: torch.Tensor, group_size: int):
 
 def strip_rows_pays(m: int, k: int, n: int, gathered: bool = False) -> bool:
     """Whether the skinny strip GEMM beats the split-K GEMM for ``m`` rows of a ``k x n``
-    product on MI355X.  Each workgroup (one per CU) stages all m rows of x against the
-    n k / 512 weight bytes a CU streams, so it pays while m * 1024 <= 1.5 n (every m <= 16
-    on gate|up's 24576 columns, m <= 6 on down's 4096).  With the act-order gather, every
-    workgroup gathers all m * k channels: from x's rows held in LDS, which they fit at
-    m * k <= 32768, or else from memory, two bytes per load, which pays only on a wide
-    product (n >= 6 k: gate|up).  Measured: the gathered strip GEMM wins up to m = 8 on
-    q|k|v and o, m = 2 on down (to 4 with x resident), every m <= 16 on gate|up.  The C
-    drop-in mtl_int4pack_mm uses the first rule."""
-    if m < 1 or m > _MAX_M or 2 * m * 1024 > 3 * n:
+    product on MI355X.  Without the act-order gather it does at every m <= 16 on the four
+    decode shapes (measured: q|k|v 6.3-8.3 against 8.7-10.6 us, down 9.6-15.0 against
+    14.3-16.7).  With the gather, every workgroup gathers all m * k channels: from x's
+    rows held in LDS, which they fit at m * k <= 32768, or else from memory, two bytes per
+    load, which pays only on a wide product (n >= 6 k: gate|up).  Measured with the gather:
+    q|k|v and o ahead up to m = 8 (q|k|v 9.4 against 12.5 us at m = 8, 20.1 against 14.0 at
+    m = 12), gate|up at every m <= 16 (31.3 against 33.7 us at 16), down to m = 4."""
+    if m < 1 or m > _MAX_M:
         return False
     return not gathered or m * k <= 32768 or n >= 6 * k
 
