@@ -70,6 +70,12 @@ enum {
                              (w = (q - 8) * scale + zero), `qzeros` and zero_offset unused */
 };
 
+/* OR'ed into the xsplits argument of mtl_w4_gemm_residual (strip layouts): each split of
+ * xpart holds the gate partials in its first K floats and the up partials in the next K,
+ * instead of the 32-column gate|up interleave (a bf16-kept up_proj's output beside its
+ * int4 gate's). */
+enum { MTL_XPART_HALVES = 1 << 30 };
+
 /* Metadata format of mtl_w4_gemm_fused. */
 enum {
   MTL_META_GPTQ = 0,      /* scales fp16 [K/g,N] + qzeros int32 [K/g,N/8]; w=(q-z)*s  */
@@ -411,7 +417,8 @@ int mtl_w4_gemm_norm_partials_bf16(const void* h, const void* w, const float* sl
  * h_ord[n] = h[n]; h_ord NULL: no copy), and slots[b] = sum of h^2 over columns
  * 16b .. 16b+15 (what mtl_w4_gemm_norm_partials and mtl_bf16_gemv_argmax_norm consume).
  * x is bf16 [K] or, with xpart, SiLU*up of an interleaved gate|up GEMV's partials (as
- * mtl_w4_gemm_partials).  Layouts ROWS and TILED reduce split-K inside the kernel and
+ * mtl_w4_gemm_partials), or with xsplits | MTL_XPART_HALVES (strip layouts only) of
+ * [gate K | up K] splits.  Layouts ROWS and TILED reduce split-K inside the kernel and
  * need the workspace of mtl_gptq_gemm (counters zero before first use; every launch
  * leaves them zero); MTL_LAYOUT_STRIP needs none (workspace may be NULL).  N <= 16384.
  */

@@ -168,6 +168,7 @@ MTL_ERR_UNSUPPORTED = -7
 
 OUT_BF16, OUT_F32 = 0, 1
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_STRIP, LAYOUT_STRIP_QSZ = 0, 1, 2, 3
+XPART_HALVES = 1 << 30                # MTL_XPART_HALVES, OR'ed into mtl_w4_gemm_residual's xsplits
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 META_GPTQ, META_QSZ = 0, 1
 

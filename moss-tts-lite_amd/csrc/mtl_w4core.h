@@ -176,8 +176,9 @@ struct StripArgs {
   uint16_t* act;              // bf16 [N/2]: silu(gate) * up, 32-column gate|up interleave
   int xsplits, xpart_ld;
   float eps;
-  int K, N, group, zero_offset, kblocks;
-  int16_t xcd_order, fmt;
+  int K, N, group;
+  int16_t zero_offset, kblocks, xcd_order, fmt;
+  int16_t xhalves;            // xpart splits hold [gate K | up K] (else the 32-column interleave)
   mtl_strip_geometry geom;    // requested launch shape (all 0: automatic)
 };
 // The launch passes StripArgs by value: its 184 bytes put the kernel's arguments at 440

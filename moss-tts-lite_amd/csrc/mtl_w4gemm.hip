@@ -777,6 +777,7 @@ static StripArgs strip_args(int64_t K, const int32_t* w, const void* scales,
   a.x = nullptr;
   a.perm = nullptr;
   a.xpart = nullptr;
+  a.xhalves = 0;
   a.xsplits = 0;
   a.xpart_ld = 0;
   a.hn = a.wn = nullptr;
@@ -935,6 +936,9 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
   if ((!x && !xpart) || (x && xpart) || !qweight || !meta_given(layout, meta0, qzeros) || !h ||
       !slots)
     return MTL_ERR_INVALID_ARG;
+  const bool halves = xpart && (xsplits & MTL_XPART_HALVES);
+  if (xpart) xsplits &= ~MTL_XPART_HALVES;
+  if (halves && !is_strip(layout)) return MTL_ERR_UNSUPPORTED;
   if (const int st = check_layout(layout, 1, K, N, nullptr, group)) return st;
   if (group != 32 && group != 64 && group != 128 && group != 256) return MTL_ERR_GROUP;
   if (K <= 0 || N <= 0 || K % group != 0 || N % 8 != 0) return MTL_ERR_SHAPE;
@@ -956,6 +960,7 @@ static int w4_gemm_residual(const void* x, const float* xpart, int xsplits, int6
     sa.xpart = xpart;
     sa.xsplits = xsplits;
     sa.xpart_ld = (int)xpart_ld;
+    sa.xhalves = halves;
     sa.h = static_cast<uint16_t*>(h);
     sa.scatter = scatter;
     sa.h_ord = static_cast<uint16_t*>(h_ord);

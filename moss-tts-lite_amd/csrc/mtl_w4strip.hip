@@ -125,14 +125,16 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
       wv[r] = *reinterpret_cast<const u32x4*>(a.wn + (size_t)it * 8);
     } else {
       // channels 8it..8it+7 sit in one 32-column block of the gate|up interleave:
-      // gate columns 64*(j/32) + j%32, their up partners 32 columns to the right
+      // gate columns 64*(j/32) + j%32, their up partners 32 columns to the right; or
+      // (xhalves) gate column j, its up partner K columns to the right
       xv[r] = u32x4{0u, 0u, 0u, 0u};
       const int j0 = it * 8;
-      sbase[r] = a.xpart + 64 * (j0 >> 5) + (j0 & 31);
+      sbase[r] = a.xhalves ? a.xpart + j0 : a.xpart + 64 * (j0 >> 5) + (j0 & 31);
+      const int uo = a.xhalves ? a.K : 32;
       sg[r][0] = ld_f4(sbase[r]);
       sg[r][1] = ld_f4(sbase[r] + 4);
-      su[r][0] = ld_f4(sbase[r] + 32);
-      su[r][1] = ld_f4(sbase[r] + 36);
+      su[r][0] = ld_f4(sbase[r] + uo);
+      su[r][1] = ld_f4(sbase[r] + uo + 4);
     }
   }
   const bool stages = cs * 64 < ITEMS;         // wave-uniform: this wave stages items
@@ -248,7 +250,8 @@ __device__ __forceinline__ void strip_body(const StripArgs& a, const int bid, co
                       su[r][1].x, su[r][1].y, su[r][1].z, su[r][1].w};
         for (int sp = 1; sp < a.xsplits; ++sp) {     // further splits, summed in split order
           const float* p = sbase[r] + (size_t)sp * a.xpart_ld;
-          const float4 g0 = ld_f4(p), g1 = ld_f4(p + 4), u0 = ld_f4(p + 32), u1 = ld_f4(p + 36);
+          const int uo = a.xhalves ? a.K : 32;
+          const float4 g0 = ld_f4(p), g1 = ld_f4(p + 4), u0 = ld_f4(p + uo), u1 = ld_f4(p + uo + 4);
           g[0] += g0.x; g[1] += g0.y; g[2] += g0.z; g[3] += g0.w;
           g[4] += g1.x; g[5] += g1.y; g[6] += g1.z; g[7] += g1.w;
           u[0] += u0.x; u[1] += u0.y; u[2] += u0.z; u[3] += u0.w;

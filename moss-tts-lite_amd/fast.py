@@ -367,7 +367,7 @@ class FastDecoder:
                                             self.attn_ws.numel())),
             self._residual(self.x_o, None, lyr["o"], self.inv_perm_gu[li], self.x_gu, "o"),
         ]
-        if self.up_keep[li]:   # int4 gate and bf16 up into fp32 halves, then SiLU*up
+        if self.up_keep[li]:   # int4 gate and bf16 up into fp32 halves; down stages SiLU*up
             inter = cfg.intermediate
             gu = self.part["gate_up"]
             launches = self._with_bf16(
@@ -376,11 +376,9 @@ class FastDecoder:
                 lyr["post_attention_layernorm"], lyr["up_keep"], gu[inter:])
             self._keep_launches[(li, "up")] = len(launches)
             plan += launches + [
-                ("mtl_silu_mul_f32", (gu.data_ptr(), gu[inter:].data_ptr(), self.act.data_ptr(),
-                                      inter)),
-                self._residual(self.act, None, lyr["down"],
+                self._residual(None, "gate_up", lyr["down"],
                                None if last else self.inv_perm_qkv[li + 1],
-                               None if last else self.x_qkv),
+                               None if last else self.x_qkv, halves=True),
             ]
         elif self.strip_gemv["gate_up"]:   # SiLU*up in the epilogue; down reads the product
             plan += [
@@ -423,12 +421,15 @@ class FastDecoder:
                  p(qz), lin.out_features, lin.group_size, lin.zero_offset, layout,
                  self.act.data_ptr())), "gate_up")
 
-    def _residual(self, x, xpart_name, lin, scatter, h_ord, name="down"):
+    def _residual(self, x, xpart_name, lin, scatter, h_ord, name="down", halves=False):
+        """``halves``: the partials hold [gate | up] (a bf16-kept up_proj beside its int4
+        gate) instead of the 32-column gate|up interleave."""
         qw, layout, sc, qz = self._weight(lin, self.strip)
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         xpart = self.part[xpart_name] if xpart_name else None
+        xsplits = (self.splits[xpart_name] | (N.XPART_HALVES if halves else 0)) if xpart_name else 0
         return self._with_geometry(("mtl_w4_gemm_residual",
-                (p(x), p(xpart), self.splits[xpart_name] if xpart_name else 0,
+                (p(x), p(xpart), xsplits,
                  2 * lin.in_features if xpart_name else 0, lin.in_features, qw.data_ptr(),
                  sc.data_ptr(), p(qz), lin.out_features, lin.group_size,
                  lin.zero_offset, layout, self.h.data_ptr(), p(scatter), p(h_ord),
@@ -559,7 +560,7 @@ class FastDecoder:
         if self.v_keep[li] and name != "qkv":
             shift += self._keep_launches[(li, "v")] - 1                    # a separate bf16 v
         if self.up_keep[li] and name == "down":
-            shift += self._keep_launches[(li, "up")]                       # bf16 up?, SiLU*up
+            shift += self._keep_launches[(li, "up")] - 1                   # a separate bf16 up
         return self._layers[li][self._GEMV_AT[self.plan][name] + shift]
 
     def run_gemv(self, li: int, name: str) -> None:
