@@ -99,10 +99,25 @@ int mtl_residual_rmsnorm(const float* partials, int32_t splits, const void* resi
  *   workspace  mtl_decode_attention_workspace_bytes(n_heads, head_dim) bytes, 16-byte
  *              aligned, ZERO-FILLED before its first use (every launch leaves its
  *              counters zero again); one stream at a time.
- * head_dim must be 128; n_heads % n_kv_heads == 0, n_heads / n_kv_heads <= 8.
+ * head_dim must be 128; n_heads % n_kv_heads == 0, n_heads / n_kv_heads <= 8,
+ * n_kv_heads <= 127.
  * pos < 0 writes nothing; pos >= max_seq attends over [0, max_seq).
  */
 int64_t mtl_decode_attention_workspace_bytes(int32_t n_heads, int32_t head_dim);
+
+/*
+ * Hand-off of the chunk partials between the attention's workgroups (no counterpart in
+ * the reference: an implementation choice of mtl_decode_attention and
+ * mtl_decode_attention_fused, process-wide, read at each launch).
+ *   1 (default)  XCD-local: the chunks of one kv head run on one XCD (n_kv_heads a
+ *                multiple of 8, workgroups dispatched to the XCDs in turn by linear id),
+ *                so partials and the arrival count stay in that XCD's L2.  A launch that
+ *                finds a kv head's chunks on more than one XCD adds 1 to the uint32 at
+ *                byte 1016 of the workspace (the placement word, zero when it held).
+ *   0            agent-scope stores, release count and acquire fence (any placement).
+ * Returns MTL_ERR_INVALID_ARG for other values.
+ */
+int mtl_decode_attention_set_handoff(int32_t local);
 int mtl_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                          const int64_t* pos, void* out, const int32_t* out_index, int32_t n_heads,
                          int32_t n_kv_heads, int32_t head_dim, int64_t max_seq, float scale,

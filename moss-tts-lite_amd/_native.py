@@ -52,6 +52,7 @@ _SIGNATURES = {
                                    _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i64,
                                    ctypes.c_float, _c_void_p]),
     "mtl_decode_attention_workspace_bytes": (_i64, [_i32, _i32]),
+    "mtl_decode_attention_set_handoff": (_i32, [_i32]),
     "mtl_decode_attention": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _i32, _i32, _i32, _i64, ctypes.c_float, _c_void_p, _i64,
                                     _c_void_p]),

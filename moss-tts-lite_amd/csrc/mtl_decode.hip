@@ -337,6 +337,16 @@ constexpr int kAttnMaxChunks = 64;
 constexpr int kAttnMaxRep = 8;        // q heads per kv head
 constexpr int kAttnPart = 132;        // m, l, 2 pad, o[128]
 constexpr int kAttnCounterBytes = 1024;
+// The tile kernel's XCD-local hand-off keeps a 64-bit counter per kv head and, in the
+// last 8 bytes of the counter area, the number of launches whose chunk workgroups of one
+// kv head were found on more than one XCD.
+constexpr int kAttnPlacementWord = kAttnCounterBytes - 8;
+constexpr int kAttnMaxKvLocal = kAttnPlacementWord / 8;
+
+// XCD (XCC) id of the executing workgroup, hardware register XCC_ID bits [2:0].
+__device__ __forceinline__ uint32_t xcc_id() {
+  return (uint32_t)__builtin_amdgcn_s_getreg((2 << 11) | (0 << 6) | 20) & 7u;
+}
 
 // The first 8 split-K partials of one head's dims (t, t+64), loaded ahead of use; the
 // sum (with any further splits) comes later from head_sum.
@@ -401,9 +411,13 @@ struct AttnArgs {
 // The merge of one kv head's chunk partials (m, l, o[128]) per q head, in chunk order,
 // by the last workgroup of that kv head to finish; out[h*128 + d] (through out_index).
 // VALU: the wave reductions on the VALU (wave_max_valu, wave_sum_valu; the same bits).
-template <bool VALU>
+template <bool VALU, bool LOCAL = false>
 __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, int n_rep,
                                            int wave, int lane, float (*w_lds)[kAttnMaxChunks]) {
+  // LOCAL: the partials were written by workgroups of this XCD and sit in its L2; the
+  // loads bypass the CU's L1 (sc0) and read them there.  Otherwise the acquire fence of
+  // the completing workgroup made them visible and plain loads do.
+  constexpr int kPol = LOCAL ? 1 : 0;
   constexpr int D = 128;
   for (int hr = wave; hr < n_rep; hr += 4) {
     const int h = kvh * n_rep + hr;
@@ -420,7 +434,7 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(ph), (short)0, nch * kAttnPart * 4, 0x00020000);
     const u64 oiv = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(irs, i0 * 4, 0, 0));
-    const u64 ml = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(prs, lane * kAttnPart * 4, 0, 0));
+    const u64 ml = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(prs, lane * kAttnPart * 4, 0, kPol));
     float mc = __uint_as_float((uint32_t)ml);
     float lc = __uint_as_float((uint32_t)(ml >> 32));   // 0 past nch: the chunk drops out
     // chunk outputs 16 at a time; the first batch goes out with the loads above (peeled:
@@ -430,17 +444,21 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a, int kvh, int nch, 
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         ov[j] = __builtin_bit_cast(u64, __builtin_amdgcn_raw_buffer_load_b64(
-                                            prs, ((c0 + j) * kAttnPart + 4 + 2 * lane) * 4, 0, 0));
+                                            prs, ((c0 + j) * kAttnPart + 4 + 2 * lane) * 4, 0, kPol));
     };
     float o0 = 0.f, o1 = 0.f;
+    // the 16 weights in four 16-byte LDS reads; chunks at or past nch have weight 0 and
+    // partials read as 0, so their products add +0 and the sums need no branch
     auto add_batch = [&](int c0) {
+      const float4* wp = reinterpret_cast<const float4*>(&w_lds[wave][c0]);
+      const float4 w4[4] = {wp[0], wp[1], wp[2], wp[3]};
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        if (c0 + j < nch) {
-          const float wj = w_lds[wave][c0 + j];
-          o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
-          o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
-        }
+      for (int j = 0; j < 16; ++j) {
+        const float4 q = w4[j >> 2];
+        const float wj = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+        o0 = fmaf(wj, __uint_as_float((uint32_t)ov[j]), o0);
+        o1 = fmaf(wj, __uint_as_float((uint32_t)(ov[j] >> 32)), o1);
+      }
     };
     load_batch(0);
     {
@@ -473,7 +491,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
   __shared__ u32x4 q_lds[kAttnMaxRep][16];
   __shared__ u32x4 kpos[16], vpos[16];
   __shared__ float e_lds[4][kAttnBlock];
-  __shared__ float w_lds[4][kAttnMaxChunks];
+  __shared__ __attribute__((aligned(16))) float w_lds[4][kAttnMaxChunks];
   __shared__ int last_flag;
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int wave = wave_id(), lane = threadIdx.x & 63;
@@ -674,17 +692,19 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 // in the decode step.  The published (m, l, o[128]) per q
 // head and the merge are those of attn_decode_kernel.
 // ----------------------------------------------------------------------------------
-template <bool FROM_PART>
+template <bool FROM_PART, bool LOCAL>
 __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   constexpr int D = 128, P = kAttnBlock;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  __shared__ u32x4 k_lds[P][16];                // the chunk's K rows, 8 dims per item
-  __shared__ u32x4 v_lds[P][16];
-  __shared__ u32x4 q_lds[16][16];               // q heads (rows past n_rep zero)
+  // rows padded by one item: the MFMA operand reads take one item from each of 16 rows,
+  // which a 256-byte row stride would put in the same four LDS banks
+  __shared__ u32x4 k_lds[P][17];                // the chunk's K rows, 8 dims per item
+  __shared__ u32x4 v_lds[P][17];
+  __shared__ u32x4 q_lds[16][17];               // q heads (rows past n_rep zero)
   __shared__ float e_lds[kAttnMaxRep][P];       // exp(s - m) per q head and position
   __shared__ float red_m[4][16], red_l[4][16];  // per-wave max / sum per q head
-  __shared__ float w_lds[4][kAttnMaxChunks];
+  __shared__ __attribute__((aligned(16))) float w_lds[4][kAttnMaxChunks];
   __shared__ int last_flag;
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
@@ -778,12 +798,17 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   // 2. Scores s[p][h] = K[p] . q[h] on MFMA; lane l holds positions 16w + 4(l/16) + r of
   //    q head l%16.  Chunk softmax: max and sum per head across the 4 waves.
   f4 S = {0.f, 0.f, 0.f, 0.f};
+  u32x4 ka[4], qb[4];                           // all 8 operand reads in flight at once
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const bf16x8 A = __builtin_bit_cast(bf16x8, k_lds[16 * wave + (lane & 15)][4 * k + (lane >> 4)]);
-    const bf16x8 B = __builtin_bit_cast(bf16x8, q_lds[lane & 15][4 * k + (lane >> 4)]);
-    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, S, 0, 0, 0);
+    ka[k] = k_lds[16 * wave + (lane & 15)][4 * k + (lane >> 4)];
+    qb[k] = q_lds[lane & 15][4 * k + (lane >> 4)];
   }
+  __builtin_amdgcn_sched_barrier(0);            // keep the scheduler from re-pairing them
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[k]),
+                                                __builtin_bit_cast(bf16x8, qb[k]), S, 0, 0, 0);
   const int hd = lane & 15, g = lane >> 4;
   float sv[4], mloc = -INFINITY;
 #pragma unroll
@@ -819,11 +844,19 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
     float o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = 0.f;
+    // every LDS read of the quarter first (16 V items, the 16 probabilities as 4 x 16 B),
+    // so their latencies overlap; then the sums in position order
+    u32x4 vq[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vq[i] = v_lds[16 * pq + i][dg];
+    float4 eq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) eq[i] = reinterpret_cast<const float4*>(&e_lds[hr][16 * pq])[i];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int row = 16 * pq + i;
-      const float e = e_lds[hr][row];
-      const u32x4 v = v_lds[row][dg];
+      const float4 e4 = eq[i >> 2];
+      const float e = (i & 3) == 0 ? e4.x : (i & 3) == 1 ? e4.y : (i & 3) == 2 ? e4.z : e4.w;
+      const u32x4 v = vq[i];
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -836,21 +869,67 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
     const float mh = fmaxf(fmaxf(red_m[0][hr], red_m[1][hr]), fmaxf(red_m[2][hr], red_m[3][hr]));
     const float lh = (red_l[0][hr] + red_l[1][hr]) + (red_l[2][hr] + red_l[3][hr]);
     float* ph = a.part + ((size_t)(kvh * n_rep + hr) * kAttnMaxChunks + c) * kAttnPart;
-    if (lane == 0) {
-      __hip_atomic_store(ph, mh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ph + 1, lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (lane < 16) {
+    if (LOCAL) {
+      // plain stores: they end in this XCD's L2, where the merging workgroup reads them
+      if (lane == 0) *reinterpret_cast<float2*>(ph) = make_float2(mh, lh);
+      if (lane < 16) {
+        float4* po = reinterpret_cast<float4*>(ph + 4 + 8 * dg);
+        po[0] = make_float4(o[0], o[1], o[2], o[3]);
+        po[1] = make_float4(o[4], o[5], o[6], o[7]);
+      }
+    } else {
+      if (lane == 0) {
+        __hip_atomic_store(ph, mh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ph + 1, lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane < 16) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        __hip_atomic_store(ph + 4 + 8 * dg + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < 8; ++j)
+          __hip_atomic_store(ph + 4 + 8 * dg + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 
-  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order
-  //    (release count, acquire fence of the completing workgroup, as in attn_decode_kernel).
+  // 4. The last workgroup of this kv head merges its q heads' chunks in chunk order.
   __builtin_amdgcn_s_waitcnt(0);      // every partial store acknowledged before the count
   __syncthreads();
+  if (LOCAL) {
+    // XCD-local hand-off.  Workgroups are dispatched to the 8 XCDs in turn by linear id
+    // and the grid's x extent (the kv heads) is a multiple of 8, so every chunk of kv
+    // head kvh (linear ids kvh + gridDim.x * c) runs on one XCD and shares its L2: the
+    // partial stores above were acknowledged by that L2, and the count is an atomic
+    // there, so the last workgroup reads the partials from the L2 without the agent-scope
+    // write-back and invalidate.  Each workgroup adds 1 to the 7-bit field of its own XCD
+    // (8 fields); the count is their sum, and a count spread over two fields means the
+    // placement did not hold, which is recorded in the placement word.
+    if (t == 0) {
+      unsigned long long* cnt = reinterpret_cast<unsigned long long*>(a.counters) + kvh;
+      const unsigned long long add = 1ull << (7 * xcc_id());
+      const unsigned long long tot =
+          __hip_atomic_fetch_add(cnt, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+      int n = 0, fields = 0;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int f = (int)((tot >> (7 * x)) & 0x7full);
+        n += f;
+        fields += f != 0;
+      }
+      last_flag = n == nch;
+      if (n == nch) {
+        __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (fields > 1)
+          __hip_atomic_fetch_add(reinterpret_cast<uint32_t*>(
+                                     reinterpret_cast<char*>(a.counters) + kAttnPlacementWord),
+                                 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    attn_merge<true, true>(a, kvh, nch, n_rep, wave, lane, w_lds);
+    return;
+  }
+  // Agent-scope hand-off (release count, acquire fence of the completing workgroup, as in
+  // attn_decode_kernel).
   if (t == 0) {
     last_flag = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nch - 1);
@@ -1183,12 +1262,22 @@ static int attn_check(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int
                       const void* v_cache) {
   if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
   if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads != 0 ||
-      n_heads / n_kv_heads > kAttnMaxRep || n_kv_heads * 4 > kAttnCounterBytes ||
+      n_heads / n_kv_heads > kAttnMaxRep || n_kv_heads * 8 > kAttnPlacementWord ||
       max_seq < 1 || max_seq > (1 << 24))
     return MTL_ERR_SHAPE;
   if (!workspace || ws_bytes < mtl_decode_attention_workspace_bytes(n_heads, head_dim))
     return MTL_ERR_WORKSPACE;
   if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(workspace)) return MTL_ERR_ALIGN;
+  return MTL_OK;
+}
+
+// Hand-off of the tile attention's chunk partials: XCD-local (1, the default) or
+// agent-scope (0); mtl_decode_attention_set_handoff.
+static int g_attn_local_handoff = 1;
+
+int mtl_decode_attention_set_handoff(int32_t local) {
+  if (local != 0 && local != 1) return MTL_ERR_INVALID_ARG;
+  g_attn_local_handoff = local;
   return MTL_OK;
 }
 
@@ -1199,9 +1288,17 @@ static void attn_launch(AttnArgs& a, void* workspace, bool from_part, hipStream_
   int64_t ch = (a.max_seq + kAttnBlock - 1) / kAttnBlock;
   if (ch > kAttnMaxChunks) ch = kAttnMaxChunks;
   const dim3 grid(a.Hkv, (unsigned)ch);
+  // the XCD-local hand-off needs every chunk of a kv head on one XCD: kv heads a multiple
+  // of 8, so linear ids kvh + Hkv * c agree modulo 8
+  const bool local = g_attn_local_handoff && a.Hkv % 8 == 0 && a.Hkv <= kAttnMaxKvLocal;
   if (a.fixed_chunks) {
-    if (from_part) hipLaunchKernelGGL(attn_tile_kernel<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(attn_tile_kernel<false>, grid, dim3(256), 0, s, a);
+    if (from_part) {
+      if (local) hipLaunchKernelGGL((attn_tile_kernel<true, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((attn_tile_kernel<true, false>), grid, dim3(256), 0, s, a);
+    } else {
+      if (local) hipLaunchKernelGGL((attn_tile_kernel<false, true>), grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((attn_tile_kernel<false, false>), grid, dim3(256), 0, s, a);
+    }
   } else if (from_part) {
     hipLaunchKernelGGL(attn_decode_kernel<true>, grid, dim3(256), 0, s, a);
   } else {

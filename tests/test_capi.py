@@ -111,6 +111,11 @@ def test_decode_entry_validation(lib):
     assert lib.mtl_decode_attention_workspace_bytes(32, 128) == 1024 + 32 * 64 * 132 * 4
     assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, None, 32, 8, 128, 2048,
                                     C.c_float(0.1), None, 0, None) == N.MTL_ERR_WORKSPACE
+    # 128 kv heads would reach the placement word at byte 1016 of the counter area
+    assert lib.mtl_decode_attention(FAKE, FAKE, FAKE, FAKE, FAKE, None, 128, 128, 128, 2048,
+                                    C.c_float(0.1), FAKE, 1 << 30, None) == N.MTL_ERR_SHAPE
+    assert lib.mtl_decode_attention_set_handoff(2) == N.MTL_ERR_INVALID_ARG
+    assert lib.mtl_decode_attention_set_handoff(1) == N.MTL_OK
     assert lib.mtl_residual_rmsnorm(None, 0, FAKE, FAKE, FAKE, FAKE, None, 4098, eps,
                                     None) == N.MTL_ERR_SHAPE
     assert lib.mtl_residual_rmsnorm(FAKE, 0, FAKE, FAKE, FAKE, FAKE, None, 4096, eps,

@@ -612,6 +612,50 @@ def test_attention_fused_matches_two_kernel_path(dev, lib, pos, max_seq):
         assert torch.equal(a, b)
 
 
+def test_attention_local_handoff_matches_agent_scope(dev, lib):
+    # The XCD-local hand-off (chunk partials and the arrival count in one XCD's L2) gives
+    # the same bits as the agent-scope hand-off, launch after launch on one workspace, and
+    # the placement word stays zero (every kv head's chunks found on one XCD).
+    r = np.random.default_rng(77)
+    H, Hkv, splits, max_seq = 32, 8, 1, 1536
+    ncols = (H + 2 * Hkv) * 128
+    parts = torch.from_numpy((r.standard_normal((splits, ncols)) * 0.5).astype(np.float32)).to(dev)
+    qn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
+    kn = tb((1 + 0.1 * r.standard_normal(128)).astype(np.float32), dev)
+    cos, sin = oracle_tables(max_seq, dev)
+    cache = tb(r.standard_normal((2, Hkv, max_seq, 128)).astype(np.float32), dev)
+    out_index = torch.from_numpy(r.permutation(H * 128).astype(np.int32)).to(dev)
+    scale, eps = ctypes.c_float(128 ** -0.5), ctypes.c_float(1e-6)
+    positions = list(range(0, max_seq, 29)) + [63, 64, 65, 1279, max_seq - 1]
+    res = {}
+    try:
+        for local in (0, 1):
+            assert lib.mtl_decode_attention_set_handoff(local) == N.MTL_OK
+            ws = torch.zeros(int(lib.mtl_decode_attention_workspace_bytes(H, 128)),
+                             dtype=torch.uint8, device=dev)
+            kc, vc = cache[0].clone(), cache[1].clone()
+            outs = torch.zeros(len(positions), 3, H * 128, dtype=torch.bfloat16, device=dev)
+            for i, pos in enumerate(positions):
+                tpos = torch.tensor([pos], dtype=torch.int64, device=dev)
+                for rep in range(3):
+                    N.check(lib.mtl_decode_attention_fused(
+                        parts.data_ptr(), splits, qn.data_ptr(), kn.data_ptr(), cos.data_ptr(),
+                        sin.data_ptr(), kc.data_ptr(), vc.data_ptr(), tpos.data_ptr(),
+                        outs[i, rep].data_ptr(), out_index.data_ptr(), H, Hkv, 128, max_seq,
+                        scale, eps, ws.data_ptr(), ws.numel(), stream()), "attention fused")
+            torch.cuda.synchronize()
+            placement = int(ws[1016:1020].view(torch.int32).item())
+            print(f"hand-off local={local}: {len(positions) * 3} launches, placement word "
+                  f"{placement}")
+            assert placement == 0
+            assert not ws[:1024].any()       # counters back at zero
+            res[local] = (outs, kc, vc)
+    finally:
+        lib.mtl_decode_attention_set_handoff(1)
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
 def test_head_norm_argmax_matches_oracle(dev, lib):
     r = np.random.default_rng(50)
     V, K = 20011, 4096
