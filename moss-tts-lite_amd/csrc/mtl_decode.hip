@@ -852,16 +852,22 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
     float4 eq[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) eq[i] = reinterpret_cast<const float4*>(&e_lds[hr][16 * pq])[i];
+    // positions in pairs on v_dot2_f32_bf16: the probabilities are bf16 values already
+    // (rounded above), packed (e[p], e[p+1]); v_perm puts dims d of rows p and p+1 side by
+    // side, so one dot2 adds both positions' terms of one dim
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 16; i += 2) {
       const float4 e4 = eq[i >> 2];
-      const float e = (i & 3) == 0 ? e4.x : (i & 3) == 1 ? e4.y : (i & 3) == 2 ? e4.z : e4.w;
-      const u32x4 v = vq[i];
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+      const float e0 = (i & 3) == 0 ? e4.x : e4.z, e1 = (i & 3) == 0 ? e4.y : e4.w;
+      const uint32_t ep = (__float_as_uint(e0) >> 16) | (__float_as_uint(e1) & 0xffff0000u);
+      const u32x4 v0 = vq[i], v1 = vq[i + 1];
+      const uint32_t a4[4] = {v0.x, v0.y, v0.z, v0.w}, b4[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        o[2 * j] = fmaf(e, lo_bf(w4[j]), o[2 * j]);
-        o[2 * j + 1] = fmaf(e, hi_bf(w4[j]), o[2 * j + 1]);
+        const uint32_t lo = __builtin_amdgcn_perm(b4[j], a4[j], 0x05040100u);  // (a.lo, b.lo)
+        const uint32_t hi = __builtin_amdgcn_perm(b4[j], a4[j], 0x07060302u);  // (a.hi, b.hi)
+        o[2 * j] = dot2_bf16(lo, ep, o[2 * j]);
+        o[2 * j + 1] = dot2_bf16(hi, ep, o[2 * j + 1]);
       }
     }
 #pragma unroll
