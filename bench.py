@@ -434,6 +434,20 @@ def bench_decode(args, torch):
         b_ev.record()
         torch.cuda.synchronize()
         gemv_us[name] = a_ev.elapsed_time(b_ev) * 1e3 / reps
+    # the decode attention the same way (its q|k|v buffer as the last step left it), at the
+    # middle of the range: cache length 768, the range's mean
+    attn_pos = (CONFIG4_POSITIONS[0] + CONFIG4_POSITIONS[1]) // 2
+    dec.pos.fill_(attn_pos)
+    a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2e8))
+    a_ev.record()
+    for i in range(reps):
+        dec.run_attention(i % cfg.n_layers)
+    b_ev.record()
+    torch.cuda.synchronize()
+    attention_us = {"us": round(a_ev.elapsed_time(b_ev) * 1e3 / reps, 3), "cache_length": attn_pos + 1,
+                    "timing": "144 launches back to back over the 36 layers' caches, one event pair"}
     gu_us = gemv_us["gate_up"]
     gu_bytes = algo_bytes(1, cfg.hidden, 2 * cfg.intermediate, cfg.group_size, False)
     nv = cfg.n_kv_heads * cfg.head_dim
@@ -468,6 +482,7 @@ def bench_decode(args, torch):
                 "prefill_ms": {"tokens": prompt_len, "gpu": round(min(pf_gpu), 3),
                                "wall": round(min(pf_wall), 3)},
                 "gemv_us": {k: round(v, 3) for k, v in gemv_us.items()},
+                "attention_us": attention_us,
                 "module_gemv": module_gemv,
                 "gemv_gbs": {k: round(algo_bytes(1, kk, nn, cfg.group_size, False) / gemv_us[k]
                                       / 1e3, 1) for k, kk, nn in

@@ -567,6 +567,19 @@ class FastDecoder:
         """Issue only that GEMV (timing; its inputs are whatever the buffers hold)."""
         self._run([self.gemv_launch(li, name)])
 
+    def attention_launch(self, li: int):
+        """The (C function name, args) of one layer's decode attention as the step issues it
+        (the first launch of the layer whose name is an attention entry)."""
+        for launch in self._layers[li]:
+            if launch[0] in ("mtl_decode_attention_fused", "mtl_decode_attention"):
+                return launch
+        raise RuntimeError("this plan has no separate attention launch")
+
+    def run_attention(self, li: int) -> None:
+        """Issue only that layer's attention at the current position (timing: it rewrites
+        the cache row of that position from whatever the q|k|v buffer holds)."""
+        self._run([self.attention_launch(li)])
+
     def _run(self, plan) -> None:
         stream = torch.cuda.current_stream(self.dev).cuda_stream
         for name, args in plan:
