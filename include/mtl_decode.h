@@ -230,6 +230,19 @@ int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t*
                        void* out, int64_t ldo, int64_t rows, int64_t n, float eps, void* stream);
 
 /*
+ * The residual add of a K-split o or down GEMM and the next RMSNorm + gather in one launch
+ * (fast.py:230-250 on prompt rows): h[r] = bf16(bf16(sum over the splits of partials, in
+ * split order) + h[r]) in place (partials fp32 [splits][rows][n], from
+ * mtl_w4_gemm_prefill_partials), then out[r] as mtl_rmsnorm_gather of the new h.  The
+ * same bits as mtl_w4_gemm_prefill's residual launch followed by mtl_rmsnorm_gather.
+ * out must not be h; MTL_ERR_WORKSPACE when partials_bytes < splits * rows * n * 4.
+ */
+int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t partials_bytes,
+                                void* h, int64_t ldh, const void* w, const int32_t* gather,
+                                void* out, int64_t ldo, int64_t rows, int64_t n, float eps,
+                                void* stream);
+
+/*
  * q/k RMSNorm, RoPE and KV-cache write for `rows` rows at positions pos0 .. pos0+rows-1
  * (fast.py:226-237), the arithmetic of mtl_qk_norm_rope_kv per row.
  *   qkv    bf16 [rows, ldq], each row q | k | v ((n_heads + 2 n_kv_heads) * 128)

@@ -331,6 +331,23 @@ int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,
                             int32_t group_size, int32_t epilogue, int32_t out_dtype, void* y,
                             int64_t ldy, float* workspace, int64_t ws_bytes, void* stream);
 
+/*
+ * The prompt-length GEMM's K-split partial sums only, for a caller that adds the splits
+ * itself (mtl_residual_rmsnorm_gather: the split sum, the residual add and the next RMSNorm
+ * in one launch instead of the second launch and a norm launch).  partials fp32
+ * [splits][M][N] with splits = mtl_w4_gemm_prefill_partials_bytes(M, K, N) / (M * N * 4)
+ * (the split count of mtl_w4_gemm_prefill's workspace launch, or 1: the sums themselves);
+ * meta_format MTL_META_GPTQ (strip scales + zeros) or MTL_META_QSZ (qsz, zeros unused).
+ * Sums equal those mtl_w4_gemm_prefill adds in its second launch.  No counterpart in the
+ * reference: the split of its residual linear (fast.py:230-250) over two launches.
+ */
+int64_t mtl_w4_gemm_prefill_partials_bytes(int64_t M, int64_t K, int64_t N);
+int mtl_w4_gemm_prefill_partials(const void* x, int64_t M, int64_t ldx, int64_t K,
+                                 const int32_t* strip_weight, const void* meta,
+                                 const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                                 int32_t zero_offset, int32_t meta_format, float* partials,
+                                 int64_t partials_bytes, void* stream);
+
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,
                      void* stream);

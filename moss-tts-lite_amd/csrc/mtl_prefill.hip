@@ -47,12 +47,17 @@ __global__ void embed_rows_kernel(const int64_t* __restrict__ ids, int n_tables,
 constexpr int kRowNormMax = 16384;
 constexpr int kRowNormChunks = kRowNormMax / 2048;   // 8-element chunks per thread
 
+// With `part` (fp32 [splits][rows][n], the K-split sums of an o or down GEMM): first the
+// residual add of prefill_reduce_kernel<MTL_EPI_RESIDUAL>, h = bf16(bf16(sum of the splits in
+// split order) + h) written back to x in place, then the RMSNorm of that h: one launch for
+// the split sum, the residual and the next GEMM's input.
 __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
-    const uint16_t* x, int64_t ldx, const uint16_t* __restrict__ w,
-    const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n, float eps) {
+    uint16_t* x, int64_t ldx, const uint16_t* __restrict__ w,
+    const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n, float eps,
+    const float* __restrict__ part, int splits) {
   __shared__ uint16_t xs[kRowNormMax];
   __shared__ float red[4];
-  const uint16_t* xr = x + (size_t)blockIdx.x * ldx;
+  uint16_t* xr = x + (size_t)blockIdx.x * ldx;
   uint16_t* orow = out + (size_t)blockIdx.x * ldo;
   const int t = threadIdx.x;
   const int nch = n / 2048 + (t * 8 < n % 2048 ? 1 : 0);   // this thread's chunks
@@ -65,6 +70,35 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
     if (c < nch) {
       xv[c] = *reinterpret_cast<const u32x4*>(xr + 8 * t + 2048 * c);
       wv[c] = *reinterpret_cast<const u32x4*>(w + 8 * t + 2048 * c);
+    }
+  }
+  if (part) {
+    const size_t plane = (size_t)gridDim.x * n;
+    const float* prow = part + (size_t)blockIdx.x * n;
+#pragma unroll
+    for (int c = 0; c < kRowNormChunks; ++c) {
+      if (c < nch) {
+        const float* pc = prow + 8 * t + 2048 * c;
+        float4 lo = *reinterpret_cast<const float4*>(pc);
+        float4 hi = *reinterpret_cast<const float4*>(pc + 4);
+        for (int z = 1; z < splits; ++z) {
+          const float4 pl = *reinterpret_cast<const float4*>(pc + z * plane);
+          const float4 ph = *reinterpret_cast<const float4*>(pc + z * plane + 4);
+          lo.x += pl.x; lo.y += pl.y; lo.z += pl.z; lo.w += pl.w;
+          hi.x += ph.x; hi.y += ph.y; hi.z += ph.z; hi.w += ph.w;
+        }
+        const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const uint32_t a[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t e0 = f32_to_bf16(round_bf16(v[2 * j]) + lo_bf(a[j]));
+          const uint32_t e1 = f32_to_bf16(round_bf16(v[2 * j + 1]) + hi_bf(a[j]));
+          o[j] = e0 | (e1 << 16);
+        }
+        xv[c] = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(xr + 8 * t + 2048 * c) = xv[c];
+      }
     }
   }
   if (gather) {
@@ -377,9 +411,28 @@ int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t*
   if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return MTL_ERR_ALIGN;
   if (x == out && ldx != ldo) return MTL_ERR_INVALID_ARG;   // in place: the same row pitch
   hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
-                     (hipStream_t)stream, static_cast<const uint16_t*>(x), ldx,
+                     (hipStream_t)stream, const_cast<uint16_t*>(static_cast<const uint16_t*>(x)),
+                     ldx, static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out),
+                     ldo, (int)n, eps, nullptr, 0);
+  return launch_status();
+}
+
+int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t partials_bytes,
+                                void* h, int64_t ldh, const void* w, const int32_t* gather,
+                                void* out, int64_t ldo, int64_t rows, int64_t n, float eps,
+                                void* stream) {
+  if (!partials || !h || !w || !out) return MTL_ERR_INVALID_ARG;
+  if (splits < 1 || splits > 64 || rows < 1 || rows > (int64_t)1 << 30 || n <= 0 ||
+      n % 8 != 0 || n > kRowNormMax || ldh < n || ldo < n || ldh % 8 != 0 || ldo % 8 != 0)
+    return MTL_ERR_SHAPE;
+  if (partials_bytes < (int64_t)splits * rows * n * 4) return MTL_ERR_WORKSPACE;
+  if (!aligned16(partials) || !aligned16(h) || !aligned16(w) || !aligned16(out))
+    return MTL_ERR_ALIGN;
+  if (h == out) return MTL_ERR_INVALID_ARG;   // h is updated in place; out is the norm
+  hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<uint16_t*>(h), ldh,
                      static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out), ldo,
-                     (int)n, eps);
+                     (int)n, eps, partials, (int)splits);
   return launch_status();
 }
 

@@ -32,6 +32,7 @@ constexpr int kPfPitch = 17;                     // LDS items per x row: 16 + 1 
 constexpr int kPfWavesPerEU = 3;                 // 168 VGPRs: 3 workgroups per CU
 constexpr int kPfRing = 2;                       // weight blocks in flight per wave
 constexpr int kPfMaxSplits = 8;
+constexpr int kEpiPartials = -1;                 // host-side mode of prefill_gemm
 
 struct PrefillArgs {
   const uint16_t* x;          // bf16 [M, K], rows ldx apart, in the weight's input order
@@ -400,10 +401,10 @@ static int pf_device_cus() {
 }
 
 template <int GR, int EPI, int FMT>
-static void prefill_launch(const PrefillArgs& a, hipStream_t st) {
+static void prefill_launch(const PrefillArgs& a, hipStream_t st, bool reduce = true) {
   const dim3 grid(a.N / kPfCols, (a.M + kPfRows - 1) / kPfRows, a.splits), block(64 * kPfWaves);
   hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI, FMT>), grid, block, 0, st, a);
-  if (a.splits > 1) {
+  if (a.splits > 1 && reduce) {
     const int64_t ncols = EPI == MTL_EPI_SILU_MUL ? a.N / 2 : a.N;
     const int64_t threads = (int64_t)a.M * (ncols / 4);
     hipLaunchKernelGGL(prefill_reduce_kernel<EPI>, dim3((unsigned)((threads + 255) / 256)),
@@ -416,6 +417,18 @@ static void prefill_epi(const PrefillArgs& a, int epilogue, hipStream_t st) {
   if (epilogue == MTL_EPI_RESIDUAL) prefill_launch<GR, MTL_EPI_RESIDUAL, FMT>(a, st);
   else if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL, FMT>(a, st);
   else prefill_launch<GR, MTL_EPI_NONE, FMT>(a, st);
+}
+
+// The K-split partial sums only (no reduce launch): fp32 [splits][M][N] in a.part, or with
+// one split the fp32 sums written there as y.
+template <int FMT>
+static void prefill_group_partials(const PrefillArgs& a, hipStream_t st) {
+  switch (a.group) {
+    case 32: prefill_launch<1, MTL_EPI_NONE, FMT>(a, st, false); break;
+    case 64: prefill_launch<2, MTL_EPI_NONE, FMT>(a, st, false); break;
+    case 128: prefill_launch<4, MTL_EPI_NONE, FMT>(a, st, false); break;
+    default: prefill_launch<8, MTL_EPI_NONE, FMT>(a, st, false); break;
+  }
 }
 
 template <int FMT>
@@ -442,11 +455,19 @@ static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
                              int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
                              int64_t ldy, float* workspace, int64_t ws_bytes, int fmt,
                              hipStream_t st) {
-  if (!x || !strip_weight || !scales || !y) return MTL_ERR_INVALID_ARG;
-  if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL)
+  if (!x || !strip_weight || !scales || (!y && epilogue != kEpiPartials))
     return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL &&
+      epilogue != kEpiPartials)
+    return MTL_ERR_INVALID_ARG;
+  if (epilogue == kEpiPartials) {   // y unused: its checks read the partials' pitch
+    out_dtype = MTL_OUT_F32;
+    y = workspace;
+    ldy = N;
+  }
   if (out_dtype != MTL_OUT_BF16 && out_dtype != MTL_OUT_F32) return MTL_ERR_INVALID_ARG;
-  if (epilogue != MTL_EPI_NONE && out_dtype != MTL_OUT_BF16) return MTL_ERR_INVALID_ARG;
+  if (epilogue != MTL_EPI_NONE && epilogue != kEpiPartials && out_dtype != MTL_OUT_BF16)
+    return MTL_ERR_INVALID_ARG;
   if (group_size != 32 && group_size != 64 && group_size != 128 && group_size != 256)
     return MTL_ERR_GROUP;
   const int64_t ncols = epilogue == MTL_EPI_SILU_MUL ? N / 2 : N;
@@ -480,6 +501,23 @@ static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
   a.splits = need > 0 && workspace && ws_bytes >= need ? (int)(need / (M * N * 4)) : 1;
   a.kps = a.kblocks / a.splits;
   a.part = workspace;
+  if (epilogue == kEpiPartials) {
+    // the caller sums the splits (mtl_residual_rmsnorm_gather): as many splits as the
+    // shape takes, into `workspace`; with one split the sums go there as fp32 y
+    const int s = prefill_splits((N / kPfCols) * ((M + kPfRows - 1) / kPfRows), K / 128,
+                                 pf_device_cus());
+    if (!workspace || ws_bytes < (int64_t)s * M * N * 4) return MTL_ERR_WORKSPACE;
+    a.splits = s;
+    a.kps = a.kblocks / s;
+    if (s == 1) {
+      a.y = workspace;
+      a.ldy = N;
+      a.out_f32 = 1;
+    }
+    if (fmt == STRIP_META_QSZ) prefill_group_partials<STRIP_META_QSZ>(a, st);
+    else prefill_group_partials<STRIP_META_GPTQ>(a, st);
+    return launch_status();
+  }
   if (fmt == STRIP_META_QSZ) prefill_group<STRIP_META_QSZ>(a, epilogue, st);
   else prefill_group<STRIP_META_GPTQ>(a, epilogue, st);
   return launch_status();
@@ -508,6 +546,30 @@ int mtl_w4_gemm_prefill(const void* x, int64_t M, int64_t ldx, int64_t K,
   return prefill_gemm(x, M, ldx, K, strip_weight, strip_scales, strip_zeros, N, group_size,
                       zero_offset, epilogue, out_dtype, y, ldy, workspace, ws_bytes,
                       STRIP_META_GPTQ, (hipStream_t)stream);
+}
+
+int64_t mtl_w4_gemm_prefill_partials_bytes(int64_t M, int64_t K, int64_t N) {
+  if (M < 1 || K < 256 || K % 256 != 0 || N < kPfCols || N % kPfCols != 0) return 0;
+  const int s = prefill_splits((N / kPfCols) * ((M + kPfRows - 1) / kPfRows), K / 128,
+                               pf_device_cus());
+  return (int64_t)s * M * N * 4;
+}
+
+int mtl_w4_gemm_prefill_partials(const void* x, int64_t M, int64_t ldx, int64_t K,
+                                 const int32_t* strip_weight, const void* meta,
+                                 const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                                 int32_t zero_offset, int32_t meta_format, float* partials,
+                                 int64_t partials_bytes, void* stream) {
+  if (meta_format != MTL_META_GPTQ && meta_format != MTL_META_QSZ) return MTL_ERR_INVALID_ARG;
+  if (meta_format == MTL_META_GPTQ && !strip_zeros) return MTL_ERR_INVALID_ARG;
+  if (meta_format == MTL_META_GPTQ && !aligned16(strip_zeros)) return MTL_ERR_ALIGN;
+  if (!partials) return MTL_ERR_INVALID_ARG;
+  return prefill_gemm(x, M, ldx, K, strip_weight, meta,
+                      meta_format == MTL_META_GPTQ ? strip_zeros : nullptr, N, group_size,
+                      meta_format == MTL_META_GPTQ ? zero_offset : 0, kEpiPartials,
+                      MTL_OUT_F32, partials, N, partials, partials_bytes,
+                      meta_format == MTL_META_QSZ ? STRIP_META_QSZ : STRIP_META_GPTQ,
+                      (hipStream_t)stream);
 }
 
 int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,

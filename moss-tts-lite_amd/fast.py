@@ -148,6 +148,10 @@ class FastDecoder:
             raise ValueError("layers with a bf16-kept v_proj or up_proj run in the strip plan")
         self.fused = plan != "unfused"
         self.strip = plan == "strip"
+        # prompt rows: the o and down GEMMs leave their split partials and one launch adds
+        # them to the residual and forms the next RMSNorm (False: the GEMM's own residual
+        # launch, then the norm launch; the same bits)
+        self.fuse_residual_norm = True
         # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
         # keep the split-K kernel and hand their partials to the consumer
         self.strip_gemv = {name: self.strip and name not in split_k
@@ -663,6 +667,11 @@ class FastDecoder:
               "q": z(cfg.n_heads * cfg.head_dim), "attn": z(cfg.hidden),
               "act": z(cfg.intermediate),
               "gate": z(cfg.intermediate) if any(self.up_keep) else None}
+        lib = N.load()
+        nbytes = max(int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, cfg.hidden, cfg.hidden)),
+                     int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, cfg.intermediate,
+                                                                cfg.hidden)))
+        pf["part"] = torch.empty(max(nbytes, 16) // 4, dtype=torch.float32, device=dev)
         self._pf = pf
         return pf
 
@@ -684,6 +693,42 @@ class FastDecoder:
             qz.data_ptr(), lin.out_features, lin.group_size, lin.zero_offset, epilogue,
             N.OUT_BF16, y.data_ptr(), ldy, None if ws is None else ws.data_ptr(),
             0 if ws is None else ws.numel() * 4, stream), "mtl_w4_gemm_prefill")
+
+    def _prefill_partials(self, x, rows: int, lin, part: torch.Tensor, stream) -> int:
+        """The K-split partial sums of a prompt-length o or down GEMM into ``part``
+        (mtl_w4_gemm_prefill_partials); returns the split count for
+        mtl_residual_rmsnorm_gather."""
+        lib = N.load()
+        qw, layout = lin.stream_weight(True)
+        sc, qz = lin.strip_meta()
+        qsz = layout == N.LAYOUT_STRIP_QSZ
+        K, Nc = lin.in_features, lin.out_features
+        N.check(lib.mtl_w4_gemm_prefill_partials(
+            x.data_ptr(), rows, x.stride(0), K, qw.data_ptr(), sc.data_ptr(),
+            None if qsz else qz.data_ptr(), Nc, lin.group_size, 0 if qsz else lin.zero_offset,
+            N.META_QSZ if qsz else N.META_GPTQ, part.data_ptr(), part.numel() * 4, stream),
+            "mtl_w4_gemm_prefill_partials")
+        return int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, K, Nc)) // (rows * Nc * 4)
+
+    def _prefill_residual_norm(self, x_in, rows: int, lin, norm_w, gather, out, stream) -> None:
+        """``h += x_in @ lin`` and ``out = RMSNorm(h)`` gathered by ``gather``: the GEMM's
+        split partials, then the split sum, residual add and norm in one launch (the bits
+        of the GEMM's residual launch followed by mtl_rmsnorm_gather)."""
+        cfg, pf = self.m.cfg, self._pf
+        h, part = pf["h"], pf["part"]
+        if not self.fuse_residual_norm:
+            self._prefill_gemm(x_in, rows, lin, N.EPI_RESIDUAL, h, cfg.hidden, stream)
+            N.check(N.load().mtl_rmsnorm_gather(
+                h.data_ptr(), cfg.hidden, norm_w.data_ptr(),
+                None if gather is None else gather.data_ptr(), out.data_ptr(), cfg.hidden,
+                rows, cfg.hidden, ctypes.c_float(cfg.eps), stream), "mtl_rmsnorm_gather")
+            return
+        splits = self._prefill_partials(x_in, rows, lin, part, stream)
+        N.check(N.load().mtl_residual_rmsnorm_gather(
+            part.data_ptr(), splits, part.numel() * 4, h.data_ptr(), cfg.hidden,
+            norm_w.data_ptr(),
+            None if gather is None else gather.data_ptr(), out.data_ptr(), cfg.hidden, rows,
+            cfg.hidden, ctypes.c_float(cfg.eps), stream), "mtl_residual_rmsnorm_gather")
 
     def prefill_rows(self, ids: torch.Tensor, pos0: int = 0) -> torch.Tensor:
         """Every layer over the prompt rows ``ids`` (int64 ``[L, n_tables]``: one id per
@@ -709,12 +754,14 @@ class FastDecoder:
         N.check(lib.mtl_embed_rows(pf["ids"].data_ptr(), rows, self.table_ptrs.numel(),
                                    self.table_ptrs.data_ptr(), self.vocabs.data_ptr(), cfg.hidden,
                                    h.data_ptr(), st), "mtl_embed_rows")
+        n_layers = len(m.layers)
         for li, lyr in enumerate(m.layers):
             lq = lyr["qkv"]
-            N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
-                                           lyr["input_layernorm"].data_ptr(),
-                                           p(lq.perm), x.data_ptr(), cfg.hidden, rows,
-                                           cfg.hidden, eps, st), "mtl_rmsnorm_gather")
+            if li == 0:   # later layers' input norms ride on the previous down GEMM
+                N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
+                                               lyr["input_layernorm"].data_ptr(),
+                                               p(lq.perm), x.data_ptr(), cfg.hidden, rows,
+                                               cfg.hidden, eps, st), "mtl_rmsnorm_gather")
             self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
             if self.v_keep[li]:
                 # the bf16-kept v_proj (gptq.py:689-693) reads x in its natural order
@@ -733,12 +780,8 @@ class FastDecoder:
                 q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), rows, pos0,
                 attn.data_ptr(), cfg.hidden, p(self.inv_perm_o[li]), H, Hkv, D, cfg.max_seq,
                 scale, st), "mtl_prefill_attention")
-            self._prefill_gemm(attn, rows, lyr["o"], N.EPI_RESIDUAL, h, cfg.hidden, st)
-            N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
-                                           lyr["post_attention_layernorm"].data_ptr(),
-                                           p(lyr["gate_up"].perm), x.data_ptr(),
-                                           cfg.hidden, rows, cfg.hidden, eps, st),
-                    "mtl_rmsnorm_gather")
+            self._prefill_residual_norm(attn, rows, lyr["o"], lyr["post_attention_layernorm"],
+                                        lyr["gate_up"].perm, x, st)
             if self.up_keep[li]:
                 # int4 gate and the bf16-kept up_proj (gptq.py:689-693), then SiLU(gate) * up
                 # in bf16 as the reference's MLP forms it (model.py:40-44)
@@ -756,7 +799,12 @@ class FastDecoder:
             else:
                 self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_SILU_MUL, act,
                                    cfg.intermediate, st)
-            self._prefill_gemm(act, rows, lyr["down"], N.EPI_RESIDUAL, h, cfg.hidden, st)
+            if li + 1 < n_layers:   # the residual add and the next layer's input norm
+                nxt = m.layers[li + 1]
+                self._prefill_residual_norm(act, rows, lyr["down"], nxt["input_layernorm"],
+                                            nxt["qkv"].perm, x, st)
+            else:
+                self._prefill_gemm(act, rows, lyr["down"], N.EPI_RESIDUAL, h, cfg.hidden, st)
         return h[:rows]
 
     def _final_norm_row(self, h_row: torch.Tensor) -> None:

@@ -204,6 +204,34 @@ def test_prefill_gemm_validation(lib):
     assert lib.mtl_w4_gemm_prefill_workspace_bytes(256, 4100, 4096) == 0
 
 
+def test_prefill_partials_validation(lib):
+    # the split partials of a residual GEMM: their bytes (one plane when the grid fills the
+    # CUs), the metadata format, and a buffer short of the splits' planes
+    assert lib.mtl_w4_gemm_prefill_partials_bytes(1024, 1024, 4096) == 1024 * 4096 * 4
+    pb = lib.mtl_w4_gemm_prefill_partials_bytes(256, 4096, 4096)
+    assert pb > 256 * 4096 * 4 and pb % (256 * 4096 * 4) == 0
+    assert lib.mtl_w4_gemm_prefill_partials_bytes(256, 4100, 4096) == 0
+    pp = lambda fmt=N.META_GPTQ, zeros=FAKE, part=FAKE, nbytes=pb: \
+        lib.mtl_w4_gemm_prefill_partials(FAKE, 256, 4096, 4096, FAKE, FAKE, zeros, 4096,  # noqa: E731
+                                         128, 0, fmt, part, nbytes, None)
+    assert pp(fmt=2) == N.MTL_ERR_INVALID_ARG
+    assert pp(zeros=None) == N.MTL_ERR_INVALID_ARG          # GPTQ metadata has zeros
+    assert pp(part=None) == N.MTL_ERR_INVALID_ARG
+    assert pp(nbytes=pb - 4) == N.MTL_ERR_WORKSPACE
+    assert pp(fmt=N.META_QSZ, zeros=None, nbytes=pb - 4) == N.MTL_ERR_WORKSPACE
+    # the split sum + residual + RMSNorm: splits, the partials' bytes, out distinct from h
+    eps = ctypes.c_float(1e-6)
+    rn = lambda splits=4, nbytes=4 * 16 * 4096 * 4, h=FAKE, out=ctypes.c_void_p(0x2000), \
+        ldo=4096: lib.mtl_residual_rmsnorm_gather(FAKE, splits, nbytes, h, 4096, FAKE,  # noqa: E731
+                                                  None, out, ldo, 16, 4096, eps, None)
+    assert rn(splits=0) == N.MTL_ERR_SHAPE
+    assert rn(nbytes=4 * 16 * 4096 * 4 - 4) == N.MTL_ERR_WORKSPACE
+    assert rn(ldo=4000) == N.MTL_ERR_SHAPE
+    assert rn(h=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
+    assert rn(out=FAKE) == N.MTL_ERR_INVALID_ARG            # h is updated in place
+    assert rn(h=None) == N.MTL_ERR_INVALID_ARG
+
+
 def test_gemv_strip_validation(lib):
     gv = lambda k, n, g=128, perm=None, odt=0, x=FAKE, y=FAKE, w=FAKE: lib.mtl_w4_gemv_strip(  # noqa: E731
         x, k, perm, w, FAKE, FAKE, n, g, 0, odt, y, None)

@@ -5,6 +5,8 @@ product, bf16 output within 1e-2; the residual epilogue bit for bit against a nu
 restatement of bf16(bf16(y) + h) on the fp32 result, SiLU*up within 1 bf16 ulp of
 bf16(silu(bf16 g) * bf16 u) (float32 libm differences).
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -411,3 +413,112 @@ def test_moss_prefill_matches_stepwise(dev):
     assert int(dec.pos.item()) == 19
     assert rel_l2(fb(hb), fb(hs)) < 1e-2
     assert rel_l2(fb(kb), fb(model.k_cache)) < 1e-2 and rel_l2(fb(vb), fb(model.v_cache)) < 1e-2
+
+
+def _meta_weights(meta, m, k, n, dev, seed):
+    """Strip weight, meta and zeros of a random [k, n] int4 linear in either format."""
+    if meta == "gptq":
+        case = synth.gptq_case(k=k, n=n, m=1, group=128, act_order=False, seed=seed,
+                               ref_cols=np.arange(1))
+        qw, sc, qz = strip_linear(case, dev)
+        return qw, sc, qz, N.META_GPTQ
+    from oracle import gptq_ref as G
+    from tests.test_gemm_gpu import _qsz_weights
+    q, qsz = _qsz_weights(np.random.default_rng(seed), n, k, 128)
+    packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
+    return packed, t_bf16(qsz, dev), None, N.META_QSZ
+
+
+@pytest.mark.parametrize("meta", ["gptq", "qsz"])
+@pytest.mark.parametrize("m,k,n,splits", [(77, 1024, 512, 4), (256, 4096, 4096, 4),
+                                          (33, 12288, 4096, 8), (1, 2048, 1024, 8),
+                                          (1024, 1024, 4096, 1)])
+def test_residual_rmsnorm_gather_matches_two_launches(dev, lib, meta, m, k, n, splits):
+    # the GEMM's split partials, then one launch for the split sum, the residual add and
+    # the gathered RMSNorm: bit for bit the GEMM's residual launch followed by
+    # mtl_rmsnorm_gather (h and the norm); with one split the partials are the sums
+    print("residual+norm", meta, m, k, n, flush=True)
+    qw, meta_t, qz, fmt = _meta_weights(meta, m, k, n, dev, seed=m + k + n)
+    r = np.random.default_rng(m + n)
+    x = tb(r.standard_normal((m, k)), dev)
+    h0 = tb(3 * r.standard_normal((m, n)), dev)
+    w = tb(1 + 0.1 * r.standard_normal(n), dev)
+    perm = torch.from_numpy(r.permutation(n).astype(np.int32)).to(dev)
+    eps = ctypes.c_float(1e-6)
+    h_a = h0.clone()
+    if meta == "gptq":
+        ops.prefill_gemm(x, qw, meta_t, qz, n, 128, epilogue="residual", out=h_a)
+    else:
+        ops.prefill_gemm_qsz(x, qw, meta_t.reshape(k // 128, n, 2), 128, epilogue="residual",
+                             out=h_a)
+    out_a = torch.empty_like(h0)
+    N.check(lib.mtl_rmsnorm_gather(h_a.data_ptr(), n, w.data_ptr(), perm.data_ptr(),
+                                   out_a.data_ptr(), n, m, n, eps, stream()), "norm")
+    nbytes = int(lib.mtl_w4_gemm_prefill_partials_bytes(m, k, n))
+    assert nbytes == splits * m * n * 4
+    part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    # one float short of the splits' partials is refused before any launch
+    assert lib.mtl_w4_gemm_prefill_partials(
+        x.data_ptr(), m, k, k, qw.data_ptr(), meta_t.data_ptr(),
+        None if qz is None else qz.data_ptr(), n, 128, 0, fmt, part.data_ptr(), nbytes - 4,
+        stream()) == N.MTL_ERR_WORKSPACE
+    N.check(lib.mtl_w4_gemm_prefill_partials(
+        x.data_ptr(), m, k, k, qw.data_ptr(), meta_t.data_ptr(),
+        None if qz is None else qz.data_ptr(), n, 128, 0, fmt, part.data_ptr(), nbytes,
+        stream()), "partials")
+    h_b = h0.clone()
+    out_b = torch.zeros(m, n + 64, dtype=torch.bfloat16, device=dev)
+    N.check(lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes, h_b.data_ptr(),
+                                            n, w.data_ptr(), perm.data_ptr(), out_b.data_ptr(),
+                                            n + 64, m, n, eps, stream()), "residual norm")
+    torch.cuda.synchronize()
+    assert torch.equal(h_a, h_b) and not torch.equal(h_a, h0)
+    assert torch.equal(out_a, out_b[:, :n]) and not out_b[:, n:].any()
+    args = (w.data_ptr(), None, out_b.data_ptr(), n + 64, m, n, eps, stream())
+    assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes, h_b.data_ptr(), n,
+                                           w.data_ptr(), None, h_b.data_ptr(), n, m, n, eps,
+                                           stream()) == N.MTL_ERR_INVALID_ARG   # out is h
+    assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits + 1, nbytes, h_b.data_ptr(),
+                                           n, *args) == N.MTL_ERR_WORKSPACE
+
+
+def _prefill_both_ways(dec, model, rows_ids):
+    out = []
+    for fuse in (True, False):
+        model.k_cache.zero_()
+        model.v_cache.zero_()
+        dec.fuse_residual_norm = fuse
+        h = dec.prefill_rows(rows_ids).clone()
+        torch.cuda.synchronize()
+        out.append((h, model.k_cache.clone(), model.v_cache.clone()))
+    dec.fuse_residual_norm = True
+    return out
+
+
+@pytest.mark.parametrize("v_keep,L", [(False, 37), (True, 70), (False, 1)])
+def test_prefill_rows_fused_residual_norm_is_bitwise(dev, v_keep, L):
+    # prefill_rows with the o/down residual adds fused into the next norms leaves the same
+    # residual stream and K/V caches, bit for bit, as the GEMMs' own residual launches
+    from moss_tts_lite_amd.fast import FastDecoder
+    from tests._decode_case import build_case, small_config
+    cfg = small_config(n_layers=3)
+    model, _ = build_case(cfg, seed=90 + L, dev=dev, v_keep=v_keep)
+    dec = FastDecoder(model)
+    prompt = torch.from_numpy(np.random.default_rng(L).integers(0, cfg.vocab, (L, 1)))
+    (h1, k1, v1), (h2, k2, v2) = _prefill_both_ways(dec, model, prompt)
+    assert torch.equal(h1, h2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert k1[:, :, :L].any()
+
+
+def test_moss_prefill_rows_fused_residual_norm_is_bitwise(dev):
+    # the same on the reference's (codes, qsz) records with v_proj and up_proj kept bf16
+    from moss_tts_lite_amd.fast import FastMossDecoder
+    from tests import _moss_tiny as T
+    model = T.dispatch_backbone(T.generate(T.SEED, False), dev, max_seq=64,
+                                keep=[(0, "v"), (1, "v"), (0, "up")])
+    dec = FastMossDecoder(model)
+    assert dec.up_keep[0] and dec.v_keep[0]
+    fix = np.load(os.path.join(os.path.dirname(__file__), "golden", "moss_step_fixtures.npz"))
+    rows = torch.from_numpy(fix["rows"][:int(fix["prompt_rows"])])
+    (h1, k1, v1), (h2, k2, v2) = _prefill_both_ways(dec, model, rows)
+    assert torch.equal(h1, h2) and torch.equal(k1, k2) and torch.equal(v1, v2)
