@@ -235,7 +235,8 @@ int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t*
  * split order) + h[r]) in place (partials fp32 [splits][rows][n], from
  * mtl_w4_gemm_prefill_partials), then out[r] as mtl_rmsnorm_gather of the new h.  The
  * same bits as mtl_w4_gemm_prefill's residual launch followed by mtl_rmsnorm_gather.
- * out must not be h; MTL_ERR_WORKSPACE when partials_bytes < splits * rows * n * 4.
+ * splits 1..8; out must not be h; MTL_ERR_WORKSPACE when partials_bytes < splits * rows *
+ * n * 4.
  */
 int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t partials_bytes,
                                 void* h, int64_t ldh, const void* w, const int32_t* gather,
@@ -254,6 +255,25 @@ int mtl_qk_norm_rope_kv_rows(const void* qkv, int64_t ldq, int64_t rows, int64_t
                              const void* sin_tab, void* q_out, void* k_cache, void* v_cache,
                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                              int64_t max_seq, float eps, void* stream);
+
+/*
+ * mtl_qk_norm_rope_kv_rows on the q|k|v GEMM's K-split partial sums instead of its bf16
+ * output (mtl_w4_gemm_prefill_partials): the heads whose 128 columns lie below part_cols
+ * take bf16(sum of the splits in split order) from partials fp32 [splits][rows][part_cols],
+ * the same bits as the GEMM's split-sum launch writes; the heads past part_cols (a
+ * bf16-kept v_proj's, gptq.py:689-693) read qkv bf16 [rows, ldq] (NULL when part_cols
+ * covers every head).  part_cols a multiple of 128; splits 1..8; MTL_ERR_WORKSPACE when
+ * partials_bytes < splits * rows * part_cols * 4.  The split sum, the q/k norms, RoPE and
+ * the KV write in one launch (fast.py:220-237 on prompt rows).
+ */
+int mtl_qk_norm_rope_kv_rows_partials(const float* partials, int32_t splits,
+                                      int64_t partials_bytes, int64_t part_cols,
+                                      const void* qkv, int64_t ldq, int64_t rows, int64_t pos0,
+                                      const void* q_norm_w, const void* k_norm_w,
+                                      const void* cos_tab, const void* sin_tab, void* q_out,
+                                      void* k_cache, void* v_cache, int32_t n_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                                      float eps, void* stream);
 
 /*
  * Causal GQA attention of `rows` query rows at positions pos0 + r over cache positions

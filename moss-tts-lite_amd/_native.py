@@ -112,6 +112,11 @@ _SIGNATURES = {
     "mtl_w4_gemm_prefill_partials": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
                                             _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _i64,
                                             _c_void_p]),
+    "mtl_qk_norm_rope_kv_rows_partials": (_i32, [_c_void_p, _i32, _i64, _i64, _c_void_p, _i64,
+                                                 _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                                 _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                                 _i32, _i32, _i32, _i64, ctypes.c_float,
+                                                 _c_void_p]),
     "mtl_residual_rmsnorm_gather": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _i64, _c_void_p,
                                            _c_void_p, _c_void_p, _i64, _i64, _i64,
                                            ctypes.c_float, _c_void_p]),

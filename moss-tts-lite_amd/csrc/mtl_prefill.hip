@@ -46,6 +46,7 @@ __global__ void embed_rows_kernel(const int64_t* __restrict__ ids, int n_tables,
 // ----------------------------------------------------------------------------------
 constexpr int kRowNormMax = 16384;
 constexpr int kRowNormChunks = kRowNormMax / 2048;   // 8-element chunks per thread
+constexpr int kRowNormMaxSplits = 8;                 // K splits of a residual GEMM's partials
 
 // With `part` (fp32 [splits][rows][n], the K-split sums of an o or down GEMM): first the
 // residual add of prefill_reduce_kernel<MTL_EPI_RESIDUAL>, h = bf16(bf16(sum of the splits in
@@ -78,14 +79,24 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
 #pragma unroll
     for (int c = 0; c < kRowNormChunks; ++c) {
       if (c < nch) {
+        // every split's loads of the chunk first (one round trip, not one per split),
+        // then the sum in split order
         const float* pc = prow + 8 * t + 2048 * c;
-        float4 lo = *reinterpret_cast<const float4*>(pc);
-        float4 hi = *reinterpret_cast<const float4*>(pc + 4);
-        for (int z = 1; z < splits; ++z) {
-          const float4 pl = *reinterpret_cast<const float4*>(pc + z * plane);
-          const float4 ph = *reinterpret_cast<const float4*>(pc + z * plane + 4);
-          lo.x += pl.x; lo.y += pl.y; lo.z += pl.z; lo.w += pl.w;
-          hi.x += ph.x; hi.y += ph.y; hi.z += ph.z; hi.w += ph.w;
+        float4 pl[kRowNormMaxSplits], ph[kRowNormMaxSplits];
+#pragma unroll
+        for (int z = 0; z < kRowNormMaxSplits; ++z) {
+          if (z < splits) {
+            pl[z] = *reinterpret_cast<const float4*>(pc + z * plane);
+            ph[z] = *reinterpret_cast<const float4*>(pc + z * plane + 4);
+          }
+        }
+        float4 lo = pl[0], hi = ph[0];
+#pragma unroll
+        for (int z = 1; z < kRowNormMaxSplits; ++z) {
+          if (z < splits) {
+            lo.x += pl[z].x; lo.y += pl[z].y; lo.z += pl[z].z; lo.w += pl[z].w;
+            hi.x += ph[z].x; hi.y += ph[z].y; hi.z += ph[z].z; hi.w += ph[z].w;
+          }
         }
         const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         const uint32_t a[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
@@ -149,19 +160,48 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
 
 // ----------------------------------------------------------------------------------
 // q/k RMSNorm + RoPE + KV write for rows at positions pos0 + r (fast.py:226-237): one
-// 64-lane workgroup per (head, row), the decode kernel's arithmetic per row.
+// 64-lane workgroup per (head, row), the decode kernel's arithmetic per row.  With `part`
+// (fp32 [splits][rows][part_cols], the q|k|v GEMM's K-split sums), the heads below
+// part_cols take bf16(sum of the splits in split order), the bits the GEMM's split-sum
+// launch writes to qkv; the other heads (a bf16-kept v_proj's) read qkv.
 // ----------------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) qk_norm_rope_rows_kernel(
     const uint16_t* __restrict__ qkv, int64_t ldq, int64_t pos0,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
     const uint16_t* __restrict__ cos_tab, const uint16_t* __restrict__ sin_tab,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int H,
-    int Hkv, int64_t max_seq, float eps) {
+    int Hkv, int64_t max_seq, float eps, const float* __restrict__ part, int splits,
+    int64_t part_cols) {
   constexpr int D = 128;
   const int b = blockIdx.x, t = threadIdx.x;
   const int64_t r = blockIdx.y, pos = pos0 + r;
-  const uint16_t* src = qkv + r * ldq + (size_t)b * D;
-  const float x0 = bf16_to_f32(src[t]), x1 = bf16_to_f32(src[t + 64]);
+  float x0, x1;
+  if (part && (int64_t)(b + 1) * D <= part_cols) {
+    const size_t plane = (size_t)gridDim.y * part_cols;
+    const float* pc = part + r * part_cols + (size_t)b * D;
+    float p0[kRowNormMaxSplits], p1[kRowNormMaxSplits];
+#pragma unroll
+    for (int z = 0; z < kRowNormMaxSplits; ++z) {
+      if (z < splits) {
+        p0[z] = pc[z * plane + t];
+        p1[z] = pc[z * plane + t + 64];
+      }
+    }
+    float s0 = p0[0], s1 = p1[0];
+#pragma unroll
+    for (int z = 1; z < kRowNormMaxSplits; ++z) {
+      if (z < splits) {
+        s0 += p0[z];
+        s1 += p1[z];
+      }
+    }
+    x0 = bf16_to_f32((uint16_t)f32_to_bf16(s0));
+    x1 = bf16_to_f32((uint16_t)f32_to_bf16(s1));
+  } else {
+    const uint16_t* src = qkv + r * ldq + (size_t)b * D;
+    x0 = bf16_to_f32(src[t]);
+    x1 = bf16_to_f32(src[t + 64]);
+  }
   if (b >= H + Hkv) {   // v head: copied unchanged
     uint16_t* dst = vc + ((size_t)(b - H - Hkv) * max_seq + pos) * D;
     dst[t] = (uint16_t)f32_to_bf16(x0);
@@ -422,7 +462,7 @@ int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t p
                                 void* out, int64_t ldo, int64_t rows, int64_t n, float eps,
                                 void* stream) {
   if (!partials || !h || !w || !out) return MTL_ERR_INVALID_ARG;
-  if (splits < 1 || splits > 64 || rows < 1 || rows > (int64_t)1 << 30 || n <= 0 ||
+  if (splits < 1 || splits > kRowNormMaxSplits || rows < 1 || rows > (int64_t)1 << 30 || n <= 0 ||
       n % 8 != 0 || n > kRowNormMax || ldh < n || ldo < n || ldh % 8 != 0 || ldo % 8 != 0)
     return MTL_ERR_SHAPE;
   if (partials_bytes < (int64_t)splits * rows * n * 4) return MTL_ERR_WORKSPACE;
@@ -453,7 +493,37 @@ int mtl_qk_norm_rope_kv_rows(const void* qkv, int64_t ldq, int64_t rows, int64_t
                      static_cast<const uint16_t*>(k_norm_w), static_cast<const uint16_t*>(cos_tab),
                      static_cast<const uint16_t*>(sin_tab), static_cast<uint16_t*>(q_out),
                      static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), n_heads,
-                     n_kv_heads, max_seq, eps);
+                     n_kv_heads, max_seq, eps, nullptr, 0, 0);
+  return launch_status();
+}
+
+int mtl_qk_norm_rope_kv_rows_partials(const float* partials, int32_t splits,
+                                      int64_t partials_bytes, int64_t part_cols,
+                                      const void* qkv, int64_t ldq, int64_t rows, int64_t pos0,
+                                      const void* q_norm_w, const void* k_norm_w,
+                                      const void* cos_tab, const void* sin_tab, void* q_out,
+                                      void* k_cache, void* v_cache, int32_t n_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                                      float eps, void* stream) {
+  if (!partials || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out || !k_cache ||
+      !v_cache)
+    return MTL_ERR_INVALID_ARG;
+  if (head_dim != 128) return MTL_ERR_UNSUPPORTED;
+  const int64_t cols = (int64_t)(n_heads + 2 * n_kv_heads) * 128;
+  if (n_heads <= 0 || n_kv_heads <= 0 || rows < 1 || rows > 65535 || pos0 < 0 ||
+      pos0 + rows > max_seq || splits < 1 || splits > kRowNormMaxSplits || part_cols < 128 ||
+      part_cols % 128 != 0 || part_cols > cols)
+    return MTL_ERR_SHAPE;
+  if (part_cols < cols && (!qkv || ldq < cols)) return qkv ? MTL_ERR_SHAPE : MTL_ERR_INVALID_ARG;
+  if (partials_bytes < (int64_t)splits * rows * part_cols * 4) return MTL_ERR_WORKSPACE;
+  if (!aligned16(partials)) return MTL_ERR_ALIGN;
+  hipLaunchKernelGGL(qk_norm_rope_rows_kernel, dim3(n_heads + 2 * n_kv_heads, (unsigned)rows),
+                     dim3(64), 0, (hipStream_t)stream, static_cast<const uint16_t*>(qkv), ldq,
+                     pos0, static_cast<const uint16_t*>(q_norm_w),
+                     static_cast<const uint16_t*>(k_norm_w), static_cast<const uint16_t*>(cos_tab),
+                     static_cast<const uint16_t*>(sin_tab), static_cast<uint16_t*>(q_out),
+                     static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), n_heads,
+                     n_kv_heads, max_seq, eps, partials, (int)splits, part_cols);
   return launch_status();
 }
 

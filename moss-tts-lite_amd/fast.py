@@ -148,10 +148,10 @@ class FastDecoder:
             raise ValueError("layers with a bf16-kept v_proj or up_proj run in the strip plan")
         self.fused = plan != "unfused"
         self.strip = plan == "strip"
-        # prompt rows: the o and down GEMMs leave their split partials and one launch adds
-        # them to the residual and forms the next RMSNorm (False: the GEMM's own residual
-        # launch, then the norm launch; the same bits)
-        self.fuse_residual_norm = True
+        # prompt rows: the q|k|v, o and down GEMMs leave their split partials, and the next
+        # launch sums them (q/k norm + RoPE + KV write; residual add + the next RMSNorm)
+        # (False: the GEMMs' own split-sum launches, then those launches; the same bits)
+        self.fuse_split_sums = True
         # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
         # keep the split-K kernel and hand their partials to the consumer
         self.strip_gemv = {name: self.strip and name not in split_k
@@ -668,9 +668,9 @@ class FastDecoder:
               "act": z(cfg.intermediate),
               "gate": z(cfg.intermediate) if any(self.up_keep) else None}
         lib = N.load()
-        nbytes = max(int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, cfg.hidden, cfg.hidden)),
-                     int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, cfg.intermediate,
-                                                                cfg.hidden)))
+        nbytes = max(int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, k, n))
+                     for k, n in ((cfg.hidden, cfg.hidden), (cfg.intermediate, cfg.hidden),
+                                  (cfg.hidden, cfg.qkv_out)))
         pf["part"] = torch.empty(max(nbytes, 16) // 4, dtype=torch.float32, device=dev)
         self._pf = pf
         return pf
@@ -695,9 +695,9 @@ class FastDecoder:
             0 if ws is None else ws.numel() * 4, stream), "mtl_w4_gemm_prefill")
 
     def _prefill_partials(self, x, rows: int, lin, part: torch.Tensor, stream) -> int:
-        """The K-split partial sums of a prompt-length o or down GEMM into ``part``
-        (mtl_w4_gemm_prefill_partials); returns the split count for
-        mtl_residual_rmsnorm_gather."""
+        """The K-split partial sums of a prompt-length q|k|v, o or down GEMM into ``part``
+        (mtl_w4_gemm_prefill_partials); returns the split count for the launch that sums
+        them (mtl_qk_norm_rope_kv_rows_partials, mtl_residual_rmsnorm_gather)."""
         lib = N.load()
         qw, layout = lin.stream_weight(True)
         sc, qz = lin.strip_meta()
@@ -716,7 +716,7 @@ class FastDecoder:
         of the GEMM's residual launch followed by mtl_rmsnorm_gather)."""
         cfg, pf = self.m.cfg, self._pf
         h, part = pf["h"], pf["part"]
-        if not self.fuse_residual_norm:
+        if not self.fuse_split_sums:
             self._prefill_gemm(x_in, rows, lin, N.EPI_RESIDUAL, h, cfg.hidden, stream)
             N.check(N.load().mtl_rmsnorm_gather(
                 h.data_ptr(), cfg.hidden, norm_w.data_ptr(),
@@ -762,7 +762,11 @@ class FastDecoder:
                                                lyr["input_layernorm"].data_ptr(),
                                                p(lq.perm), x.data_ptr(), cfg.hidden, rows,
                                                cfg.hidden, eps, st), "mtl_rmsnorm_gather")
-            self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
+            fuse_qkv = self.fuse_split_sums
+            if fuse_qkv:
+                splits = self._prefill_partials(x, rows, lq, pf["part"], st)
+            else:
+                self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
             if self.v_keep[li]:
                 # the bf16-kept v_proj (gptq.py:689-693) reads x in its natural order
                 N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
@@ -771,11 +775,21 @@ class FastDecoder:
                                                cfg.hidden, eps, st), "mtl_rmsnorm_gather")
                 qkv[:rows, lq.out_features:] = torch.nn.functional.linear(
                     pf["x_nat"][:rows], lyr["v_keep"])
-            N.check(lib.mtl_qk_norm_rope_kv_rows(
-                qkv.data_ptr(), cfg.qkv_out, rows, pos0, lyr["q_norm"].data_ptr(),
-                lyr["k_norm"].data_ptr(), m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
-                q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), H, Hkv, D,
-                cfg.max_seq, eps, st), "mtl_qk_norm_rope_kv_rows")
+            if fuse_qkv:   # the split sum rides on the q/k norm launch
+                part = pf["part"]
+                N.check(lib.mtl_qk_norm_rope_kv_rows_partials(
+                    part.data_ptr(), splits, part.numel() * 4, lq.out_features,
+                    qkv.data_ptr() if self.v_keep[li] else None, cfg.qkv_out, rows, pos0,
+                    lyr["q_norm"].data_ptr(), lyr["k_norm"].data_ptr(), m.rope_cos.data_ptr(),
+                    m.rope_sin.data_ptr(), q.data_ptr(), m.k_cache[li].data_ptr(),
+                    m.v_cache[li].data_ptr(), H, Hkv, D, cfg.max_seq, eps, st),
+                    "mtl_qk_norm_rope_kv_rows_partials")
+            else:
+                N.check(lib.mtl_qk_norm_rope_kv_rows(
+                    qkv.data_ptr(), cfg.qkv_out, rows, pos0, lyr["q_norm"].data_ptr(),
+                    lyr["k_norm"].data_ptr(), m.rope_cos.data_ptr(), m.rope_sin.data_ptr(),
+                    q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), H, Hkv, D,
+                    cfg.max_seq, eps, st), "mtl_qk_norm_rope_kv_rows")
             N.check(lib.mtl_prefill_attention(
                 q.data_ptr(), m.k_cache[li].data_ptr(), m.v_cache[li].data_ptr(), rows, pos0,
                 attn.data_ptr(), cfg.hidden, p(self.inv_perm_o[li]), H, Hkv, D, cfg.max_seq,

@@ -230,6 +230,19 @@ def test_prefill_partials_validation(lib):
     assert rn(h=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
     assert rn(out=FAKE) == N.MTL_ERR_INVALID_ARG            # h is updated in place
     assert rn(h=None) == N.MTL_ERR_INVALID_ARG
+    assert rn(splits=9) == N.MTL_ERR_SHAPE                  # at most 8 splits
+    # the q|k|v split partials into the q/k norm + RoPE launch: the partial columns cover
+    # whole heads, the heads past them need the bf16 buffer, and the partials' bytes
+    qk = lambda splits=2, nbytes=2 * 16 * 6144 * 4, pcols=6144, qkv=None, ldq=6144: \
+        lib.mtl_qk_norm_rope_kv_rows_partials(FAKE, splits, nbytes, pcols, qkv, ldq, 16, 0,  # noqa: E731
+                                              FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 8,
+                                              128, 2048, eps, None)
+    assert qk(pcols=6100) == N.MTL_ERR_SHAPE
+    assert qk(pcols=6272) == N.MTL_ERR_SHAPE
+    assert qk(splits=0) == N.MTL_ERR_SHAPE
+    assert qk(pcols=5120) == N.MTL_ERR_INVALID_ARG          # v heads need qkv
+    assert qk(pcols=5120, qkv=FAKE, ldq=6000) == N.MTL_ERR_SHAPE
+    assert qk(nbytes=2 * 16 * 6144 * 4 - 4) == N.MTL_ERR_WORKSPACE
 
 
 def test_gemv_strip_validation(lib):

@@ -478,8 +478,57 @@ def test_residual_rmsnorm_gather_matches_two_launches(dev, lib, meta, m, k, n, s
     assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes, h_b.data_ptr(), n,
                                            w.data_ptr(), None, h_b.data_ptr(), n, m, n, eps,
                                            stream()) == N.MTL_ERR_INVALID_ARG   # out is h
-    assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits + 1, nbytes, h_b.data_ptr(),
+    assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes - 4, h_b.data_ptr(),
                                            n, *args) == N.MTL_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("m,part_heads", [(77, 48), (256, 48), (1, 48), (40, 40)])
+def test_qk_norm_rope_partials_match_two_launches(dev, lib, m, part_heads):
+    # the q|k|v GEMM's split partials summed inside the q/k norm + RoPE + KV write launch:
+    # q, the K and V cache rows bit for bit those of the GEMM's split-sum launch followed by
+    # mtl_qk_norm_rope_kv_rows; with 40 of 48 heads in the partials the v heads come from a
+    # bf16 buffer (a kept v_proj)
+    print("qk norm partials", m, part_heads, flush=True)
+    H, Hkv, D, S, k, pos0 = 32, 8, 128, 512, 1024, 17
+    cols, pcols = (H + 2 * Hkv) * D, part_heads * D
+    qw, sc, qz, fmt = _meta_weights("gptq", m, k, pcols, dev, seed=m + pcols)
+    r = np.random.default_rng(m)
+    x = tb(r.standard_normal((m, k)), dev)
+    qn, kn = tb(1 + 0.1 * r.standard_normal(D), dev), tb(1 + 0.1 * r.standard_normal(D), dev)
+    from moss_tts_lite_amd.model import rope_tables
+    cos, sin = rope_tables(S, D, 1e6, dev)
+    qkv = torch.zeros(m, cols, dtype=torch.bfloat16, device=dev)
+    if pcols < cols:
+        qkv[:, pcols:] = tb(r.standard_normal((m, cols - pcols)), dev)
+    ops.prefill_gemm(x, qw, sc, qz, pcols, 128, out=qkv[:, :pcols])
+    eps = ctypes.c_float(1e-6)
+    outs = []
+    for fused in (False, True):
+        q = torch.zeros(m, H * D, dtype=torch.bfloat16, device=dev)
+        kc = torch.zeros(Hkv, S, D, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        tail = (qn.data_ptr(), kn.data_ptr(), cos.data_ptr(), sin.data_ptr(), q.data_ptr(),
+                kc.data_ptr(), vc.data_ptr(), H, Hkv, D, S, eps, stream())
+        if fused:
+            nbytes = int(lib.mtl_w4_gemm_prefill_partials_bytes(m, k, pcols))
+            part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+            N.check(lib.mtl_w4_gemm_prefill_partials(
+                x.data_ptr(), m, k, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), pcols, 128,
+                0, fmt, part.data_ptr(), nbytes, stream()), "partials")
+            splits = nbytes // (m * pcols * 4)
+            v_src = qkv.data_ptr() if pcols < cols else None
+            N.check(lib.mtl_qk_norm_rope_kv_rows_partials(
+                part.data_ptr(), splits, nbytes, pcols, v_src, cols, m, pos0, *tail), "fused")
+            assert lib.mtl_qk_norm_rope_kv_rows_partials(
+                part.data_ptr(), splits, nbytes - 4, pcols, v_src, cols, m, pos0,
+                *tail) == N.MTL_ERR_WORKSPACE
+        else:
+            N.check(lib.mtl_qk_norm_rope_kv_rows(qkv.data_ptr(), cols, m, pos0, *tail), "rows")
+        torch.cuda.synchronize()
+        outs.append((q, kc, vc))
+    (q1, k1, v1), (q2, k2, v2) = outs
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert q1.any() and k1[:, pos0:pos0 + m].any() and v1[:, pos0:pos0 + m].any()
 
 
 def _prefill_both_ways(dec, model, rows_ids):
@@ -487,11 +536,11 @@ def _prefill_both_ways(dec, model, rows_ids):
     for fuse in (True, False):
         model.k_cache.zero_()
         model.v_cache.zero_()
-        dec.fuse_residual_norm = fuse
+        dec.fuse_split_sums = fuse
         h = dec.prefill_rows(rows_ids).clone()
         torch.cuda.synchronize()
         out.append((h, model.k_cache.clone(), model.v_cache.clone()))
-    dec.fuse_residual_norm = True
+    dec.fuse_split_sums = True
     return out
 
 
