@@ -236,12 +236,23 @@ int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t*
  * mtl_w4_gemm_prefill_partials), then out[r] as mtl_rmsnorm_gather of the new h.  The
  * same bits as mtl_w4_gemm_prefill's residual launch followed by mtl_rmsnorm_gather.
  * splits 1..8; out must not be h; MTL_ERR_WORKSPACE when partials_bytes < splits * rows *
- * n * 4.
+ * n * 4.  sums: NULL, or out staged as mtl_rmsnorm_gather_staged stages it.
  */
 int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t partials_bytes,
                                 void* h, int64_t ldh, const void* w, const int32_t* gather,
-                                void* out, int64_t ldo, int64_t rows, int64_t n, float eps,
-                                void* stream);
+                                void* out, int64_t ldo, float* sums, int64_t rows, int64_t n,
+                                float eps, void* stream);
+
+/*
+ * mtl_rmsnorm_gather with its output staged for mtl_w4_gemm_prefill_staged: each 8-channel
+ * item of out in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7), and sums fp32 [rows][n/32] the
+ * sums of out's 32-channel groups, as the GEMM's own staging forms them.  n % 32 == 0;
+ * gather 16-byte aligned.  mtl_residual_rmsnorm_gather stages the same way when its sums
+ * is not NULL.  No counterpart in the reference (its linears take the normed rows).
+ */
+int mtl_rmsnorm_gather_staged(const void* x, int64_t ldx, const void* w, const int32_t* gather,
+                              void* out, int64_t ldo, float* sums, int64_t rows, int64_t n,
+                              float eps, void* stream);
 
 /*
  * q/k RMSNorm, RoPE and KV-cache write for `rows` rows at positions pos0 .. pos0+rows-1

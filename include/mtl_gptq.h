@@ -333,20 +333,38 @@ int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,
 
 /*
  * The prompt-length GEMM's K-split partial sums only, for a caller that adds the splits
- * itself (mtl_residual_rmsnorm_gather: the split sum, the residual add and the next RMSNorm
- * in one launch instead of the second launch and a norm launch).  partials fp32
- * [splits][M][N] with splits = mtl_w4_gemm_prefill_partials_bytes(M, K, N) / (M * N * 4)
- * (the split count of mtl_w4_gemm_prefill's workspace launch, or 1: the sums themselves);
- * meta_format MTL_META_GPTQ (strip scales + zeros) or MTL_META_QSZ (qsz, zeros unused).
- * Sums equal those mtl_w4_gemm_prefill adds in its second launch.  No counterpart in the
- * reference: the split of its residual linear (fast.py:230-250) over two launches.
+ * itself (mtl_qk_norm_rope_kv_rows_partials, mtl_residual_rmsnorm_gather: the split sum
+ * and the next operation in one launch instead of the second launch and that one).
+ * partials fp32 [splits][M][N] with splits = mtl_w4_gemm_prefill_partials_bytes(M, K, N) /
+ * (M * N * 4) (the split count of mtl_w4_gemm_prefill's workspace launch, or 1: the sums
+ * themselves); meta_format MTL_META_GPTQ (strip scales + zeros) or MTL_META_QSZ (qsz, zeros
+ * unused); x_sums NULL (x plain) or x staged as mtl_w4_gemm_prefill_staged takes it.  Sums
+ * equal those mtl_w4_gemm_prefill adds in its second launch.  No counterpart in the
+ * reference: the split of its linears (fast.py:218-250) over two launches.
  */
 int64_t mtl_w4_gemm_prefill_partials_bytes(int64_t M, int64_t K, int64_t N);
-int mtl_w4_gemm_prefill_partials(const void* x, int64_t M, int64_t ldx, int64_t K,
-                                 const int32_t* strip_weight, const void* meta,
+int mtl_w4_gemm_prefill_partials(const void* x, const float* x_sums, int64_t M, int64_t ldx,
+                                 int64_t K, const int32_t* strip_weight, const void* meta,
                                  const int32_t* strip_zeros, int64_t N, int32_t group_size,
                                  int32_t zero_offset, int32_t meta_format, float* partials,
                                  int64_t partials_bytes, void* stream);
+
+/*
+ * mtl_w4_gemm_prefill (MTL_EPI_NONE or MTL_EPI_SILU_MUL) on x staged by its producer
+ * (mtl_rmsnorm_gather_staged, mtl_residual_rmsnorm_gather with sums): x bf16 [M, ldx] with
+ * each 8-channel item in pair order (x0,x4),(x1,x5),(x2,x6),(x3,x7), and x_sums fp32
+ * [M][K/32] the sums of its 32-channel groups.  The GEMM then copies x into LDS instead of
+ * reordering it and summing its groups in every workgroup; the results are the bits of
+ * mtl_w4_gemm_prefill(_qsz) on the same x in natural order.  meta_format as
+ * mtl_w4_gemm_prefill_partials.  No counterpart in the reference (fast.py:218-250 run the
+ * linears on the normed rows).
+ */
+int mtl_w4_gemm_prefill_staged(const void* x, const float* x_sums, int64_t M, int64_t ldx,
+                               int64_t K, const int32_t* strip_weight, const void* meta,
+                               const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                               int32_t zero_offset, int32_t meta_format, int32_t epilogue,
+                               int32_t out_dtype, void* y, int64_t ldy, float* workspace,
+                               int64_t ws_bytes, void* stream);
 
 /* Unpack qweight [K/8, N] -> codes uint8 [K, N] (index/parity checks). */
 int mtl_unpack_codes(const int32_t* qweight, int64_t K, int64_t N, uint8_t* codes,

@@ -109,17 +109,22 @@ _SIGNATURES = {
                                    _i64, _c_void_p]),
     "mtl_w4_gemm_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "mtl_w4_gemm_prefill_partials_bytes": (_i64, [_i64, _i64, _i64]),
-    "mtl_w4_gemm_prefill_partials": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
-                                            _c_void_p, _i64, _i32, _i32, _i32, _c_void_p, _i64,
-                                            _c_void_p]),
+    "mtl_w4_gemm_prefill_partials": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p,
+                                            _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                            _c_void_p, _i64, _c_void_p]),
+    "mtl_w4_gemm_prefill_staged": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p,
+                                          _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
+                                          _i32, _c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
     "mtl_qk_norm_rope_kv_rows_partials": (_i32, [_c_void_p, _i32, _i64, _i64, _c_void_p, _i64,
                                                  _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
                                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                  _i32, _i32, _i32, _i64, ctypes.c_float,
                                                  _c_void_p]),
     "mtl_residual_rmsnorm_gather": (_i32, [_c_void_p, _i32, _i64, _c_void_p, _i64, _c_void_p,
-                                           _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                           _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64,
                                            ctypes.c_float, _c_void_p]),
+    "mtl_rmsnorm_gather_staged": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                         _c_void_p, _i64, _i64, ctypes.c_float, _c_void_p]),
     "mtl_w4_gemm_prefill_qsz": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _i64,
                                        _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _i64,
                                        _c_void_p]),

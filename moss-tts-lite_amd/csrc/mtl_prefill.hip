@@ -9,6 +9,7 @@
 // online softmax in fp32.
 #include "mtl_common.h"
 #include "mtl_decode.h"
+#include "mtl_w4core.h"
 
 namespace mtl {
 
@@ -52,10 +53,14 @@ constexpr int kRowNormMaxSplits = 8;                 // K splits of a residual G
 // residual add of prefill_reduce_kernel<MTL_EPI_RESIDUAL>, h = bf16(bf16(sum of the splits in
 // split order) + h) written back to x in place, then the RMSNorm of that h: one launch for
 // the split sum, the residual and the next GEMM's input.
+// With `sums` the output is staged for the prompt-length GEMM (mtl_w4_gemm_prefill_staged):
+// each 8-channel item of the output row in pair order, and sums[row][g] the sum of its
+// 32-channel group g, formed as the GEMM's own staging forms it (a v_dot2 chain per item,
+// then the butterfly over 4 items).
 __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
     uint16_t* x, int64_t ldx, const uint16_t* __restrict__ w,
     const int32_t* __restrict__ gather, uint16_t* out, int64_t ldo, int n, float eps,
-    const float* __restrict__ part, int splits) {
+    const float* __restrict__ part, int splits, float* __restrict__ sums) {
   __shared__ uint16_t xs[kRowNormMax];
   __shared__ float red[4];
   uint16_t* xr = x + (size_t)blockIdx.x * ldx;
@@ -66,6 +71,17 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
   // gather indices (j = t + 256 i)
   u32x4 xv[kRowNormChunks], wv[kRowNormChunks];
   int32_t gi[4 * kRowNormChunks];
+  int4 gq[2 * kRowNormChunks];                  // staged: the gather indices of item t + 256 c
+  float* srow = sums ? sums + (size_t)blockIdx.x * (n >> 5) : nullptr;
+  // an output item (channels 8 q .. 8 q + 7, q = t + 256 c) in pair order, with the sum of
+  // its 32-channel group (lanes 4k .. 4k + 3 hold one group: n % 32 == 0)
+  auto staged_put = [&](const u32x4 v, int c) {
+    float sum;
+    const u32x4 pv = pair_order_dot(v, sum);
+    sum = group_sum_valu<4>(sum);
+    *reinterpret_cast<u32x4*>(orow + 8 * t + 2048 * c) = pv;
+    if ((t & 3) == 0) srow[(t + 256 * c) >> 2] = sum;
+  };
 #pragma unroll
   for (int c = 0; c < kRowNormChunks; ++c) {
     if (c < nch) {
@@ -112,7 +128,15 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
       }
     }
   }
-  if (gather) {
+  if (gather && sums) {
+#pragma unroll
+    for (int c = 0; c < kRowNormChunks; ++c) {
+      if (c < nch) {
+        gq[2 * c] = *reinterpret_cast<const int4*>(gather + 8 * t + 2048 * c);
+        gq[2 * c + 1] = *reinterpret_cast<const int4*>(gather + 8 * t + 2048 * c + 4);
+      }
+    }
+  } else if (gather) {
 #pragma unroll
     for (int i = 0; i < 4 * kRowNormChunks; ++i)
       if (t + 256 * i < n) gi[i] = gather[t + 256 * i];
@@ -147,12 +171,28 @@ __global__ void __launch_bounds__(256) rmsnorm_gather_kernel(
         const float y1 = round_bf16(hi_bf(b[j]) * round_bf16(hi_bf(a[j]) * r));
         o[j] = f32_to_bf16(y0) | (f32_to_bf16(y1) << 16);
       }
-      uint16_t* dst = gather ? xs : orow;
-      *reinterpret_cast<u32x4*>(dst + 8 * t + 2048 * c) = u32x4{o[0], o[1], o[2], o[3]};
+      if (sums && !gather) {
+        staged_put(u32x4{o[0], o[1], o[2], o[3]}, c);
+      } else {
+        uint16_t* dst = gather ? xs : orow;
+        *reinterpret_cast<u32x4*>(dst + 8 * t + 2048 * c) = u32x4{o[0], o[1], o[2], o[3]};
+      }
     }
   }
   if (!gather) return;
   __syncthreads();
+  if (sums) {
+#pragma unroll
+    for (int c = 0; c < kRowNormChunks; ++c) {
+      if (c < nch) {
+        const int4 g0 = gq[2 * c], g1 = gq[2 * c + 1];
+        auto e = [&](int i) { return (uint32_t)xs[i]; };
+        staged_put(u32x4{e(g0.x) | (e(g0.y) << 16), e(g0.z) | (e(g0.w) << 16),
+                         e(g1.x) | (e(g1.y) << 16), e(g1.z) | (e(g1.w) << 16)}, c);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4 * kRowNormChunks; ++i)
     if (t + 256 * i < n) orow[t + 256 * i] = xs[gi[i]];
@@ -453,15 +493,36 @@ int mtl_rmsnorm_gather(const void* x, int64_t ldx, const void* w, const int32_t*
   hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, const_cast<uint16_t*>(static_cast<const uint16_t*>(x)),
                      ldx, static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out),
-                     ldo, (int)n, eps, nullptr, 0);
+                     ldo, (int)n, eps, nullptr, 0, nullptr);
+  return launch_status();
+}
+
+int mtl_rmsnorm_gather_staged(const void* x, int64_t ldx, const void* w, const int32_t* gather,
+                              void* out, int64_t ldo, float* sums, int64_t rows, int64_t n,
+                              float eps, void* stream) {
+  if (!x || !w || !out || !sums) return MTL_ERR_INVALID_ARG;
+  if (rows < 1 || rows > (int64_t)1 << 30 || n <= 0 || n % 32 != 0 || n > kRowNormMax ||
+      ldx < n || ldo < n || ldx % 8 != 0 || ldo % 8 != 0 || rows * (n / 32) * 4 >= ((int64_t)1 << 31))
+    return MTL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out) || (gather && !aligned16(gather)) ||
+      (reinterpret_cast<uintptr_t>(sums) & 3u))
+    return MTL_ERR_ALIGN;
+  if (x == out && ldx != ldo) return MTL_ERR_INVALID_ARG;   // in place: the same row pitch
+  hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
+                     (hipStream_t)stream, const_cast<uint16_t*>(static_cast<const uint16_t*>(x)),
+                     ldx, static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out),
+                     ldo, (int)n, eps, nullptr, 0, sums);
   return launch_status();
 }
 
 int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t partials_bytes,
                                 void* h, int64_t ldh, const void* w, const int32_t* gather,
-                                void* out, int64_t ldo, int64_t rows, int64_t n, float eps,
-                                void* stream) {
+                                void* out, int64_t ldo, float* sums, int64_t rows, int64_t n,
+                                float eps, void* stream) {
   if (!partials || !h || !w || !out) return MTL_ERR_INVALID_ARG;
+  if (sums && (n % 32 != 0 || rows * (n / 32) * 4 >= ((int64_t)1 << 31))) return MTL_ERR_SHAPE;
+  if (sums && ((gather && !aligned16(gather)) || (reinterpret_cast<uintptr_t>(sums) & 3u)))
+    return MTL_ERR_ALIGN;
   if (splits < 1 || splits > kRowNormMaxSplits || rows < 1 || rows > (int64_t)1 << 30 || n <= 0 ||
       n % 8 != 0 || n > kRowNormMax || ldh < n || ldo < n || ldh % 8 != 0 || ldo % 8 != 0)
     return MTL_ERR_SHAPE;
@@ -472,7 +533,7 @@ int mtl_residual_rmsnorm_gather(const float* partials, int32_t splits, int64_t p
   hipLaunchKernelGGL(rmsnorm_gather_kernel, dim3((unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, static_cast<uint16_t*>(h), ldh,
                      static_cast<const uint16_t*>(w), gather, static_cast<uint16_t*>(out), ldo,
-                     (int)n, eps, partials, (int)splits);
+                     (int)n, eps, partials, (int)splits, sums);
   return launch_status();
 }
 

@@ -41,14 +41,20 @@ struct PrefillArgs {
   const uint32_t* qzeros;     // strip-ordered zero nibbles (GPTQ metadata)
   void* y;                    // see the epilogues
   float* part;                // splits > 1: fp32 partial sums [splits][M][N]
-  int64_t ldx, ldy;
+  const float* xsum;          // staged x: fp32 sums per 32 channels [M][K/32], rows ldsum apart
+  int64_t ldx, ldy, ldsum;
   int M, K, N, group, zero_offset, kblocks, out_f32;
   int splits, kps;            // K splits (blockIdx.z) of kps blocks each
 };
 
 // Sums over aligned groups of 4, 8 or 16 lanes: group_sum_valu (mtl_common.h).
 
-template <int GR, int EPI, int FMT>
+// PRE: x arrives staged by its producer (mtl_rmsnorm_gather_staged and the residual form):
+// each 8-channel item already in pair order, with fp32 sums per 32 channels, so the staging
+// copies items into LDS and forms the group sums from the 32-channel sums: (S0 + S1) +
+// (S2 + S3) is the order of group_sum_valu's butterfly, so the sums are the bits the
+// in-kernel staging computes.
+template <int GR, int EPI, int FMT, bool PRE = false>
 __global__ void __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(kPfWavesPerEU)))
 w4_prefill_kernel(PrefillArgs a) {
   constexpr int MB = GR <= 4 ? 4 / GR : 1;       // groups starting in one block
@@ -76,18 +82,48 @@ w4_prefill_kernel(PrefillArgs a) {
   const int xoff = (int)(srow * a.ldx * 2) + 16 * sitem;
   const int xrstep = (int)(16 * a.ldx * 2);      // 16 rows, a uniform offset
   u32x4 xv[4];
+  // PRE: the four 32-channel sums of the block for each of the thread's rows (every thread
+  // of a row loads them; the row's item-0 thread writes the group sums)
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(PRE ? a.xsum + (size_t)row0 * a.ldsum : nullptr), (short)0,
+      PRE ? (int)((((int64_t)(a.M - row0) - 1) * a.ldsum + (a.K >> 5)) * 4) : 0, 0x00020000);
+  const int soff = PRE ? (int)(srow * a.ldsum * 4) : 0;
+  const int srstep = PRE ? (int)(16 * a.ldsum * 4) : 0;
+  float4 sv[PRE ? 4 : 1];
   auto x_load = [&](int b) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       xv[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             xrsrc, xoff, r * xrstep + b * 256, 0));
+    if constexpr (PRE) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sv[r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               srs, soff, r * srstep + b * 16, 0));
+    }
   };
   auto x_store_part = [&](int buf, int r) {     // item set r: rows srow + 16 r
-    float sum;
-    const u32x4 pv = pair_order_dot(xv[r], sum);
-    sum = group_sum_valu<GI>(sum);
-    xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
-    if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
+    if constexpr (PRE) {
+      xa[buf][(srow + 16 * r) * kPfPitch + sitem] = xv[r];
+      if (sitem == 0) {
+        const float4 q = sv[r];
+        const int row = srow + 16 * r;
+        if (GR == 1) {
+          xs[buf][0][row] = q.x; xs[buf][MB > 1 ? 1 : 0][row] = q.y;
+          xs[buf][MB > 2 ? 2 : 0][row] = q.z; xs[buf][MB > 3 ? 3 : 0][row] = q.w;
+        } else if (GR == 2) {
+          xs[buf][0][row] = q.x + q.y; xs[buf][MB > 1 ? 1 : 0][row] = q.z + q.w;
+        } else {
+          xs[buf][0][row] = (q.x + q.y) + (q.z + q.w);
+        }
+      }
+    } else {
+      float sum;
+      const u32x4 pv = pair_order_dot(xv[r], sum);
+      sum = group_sum_valu<GI>(sum);
+      xa[buf][(srow + 16 * r) * kPfPitch + sitem] = pv;
+      if ((sitem & (GI - 1)) == 0) xs[buf][sitem / GI][srow + 16 * r] = sum;
+    }
   };
   auto x_store = [&](int buf) {
 #pragma unroll
@@ -400,10 +436,10 @@ static int pf_device_cus() {
   return g_pf_cus;
 }
 
-template <int GR, int EPI, int FMT>
+template <int GR, int EPI, int FMT, bool PRE = false>
 static void prefill_launch(const PrefillArgs& a, hipStream_t st, bool reduce = true) {
   const dim3 grid(a.N / kPfCols, (a.M + kPfRows - 1) / kPfRows, a.splits), block(64 * kPfWaves);
-  hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI, FMT>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((w4_prefill_kernel<GR, EPI, FMT, PRE>), grid, block, 0, st, a);
   if (a.splits > 1 && reduce) {
     const int64_t ncols = EPI == MTL_EPI_SILU_MUL ? a.N / 2 : a.N;
     const int64_t threads = (int64_t)a.M * (ncols / 4);
@@ -412,11 +448,23 @@ static void prefill_launch(const PrefillArgs& a, hipStream_t st, bool reduce = t
   }
 }
 
+// Staged x (a.xsum) comes with the plain and SiLU*up epilogues only.
 template <int GR, int FMT>
 static void prefill_epi(const PrefillArgs& a, int epilogue, hipStream_t st) {
+  if (a.xsum) {
+    if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL, FMT, true>(a, st);
+    else prefill_launch<GR, MTL_EPI_NONE, FMT, true>(a, st);
+    return;
+  }
   if (epilogue == MTL_EPI_RESIDUAL) prefill_launch<GR, MTL_EPI_RESIDUAL, FMT>(a, st);
   else if (epilogue == MTL_EPI_SILU_MUL) prefill_launch<GR, MTL_EPI_SILU_MUL, FMT>(a, st);
   else prefill_launch<GR, MTL_EPI_NONE, FMT>(a, st);
+}
+
+template <int GR, int FMT>
+static void prefill_partials_launch(const PrefillArgs& a, hipStream_t st) {
+  if (a.xsum) prefill_launch<GR, MTL_EPI_NONE, FMT, true>(a, st, false);
+  else prefill_launch<GR, MTL_EPI_NONE, FMT>(a, st, false);
 }
 
 // The K-split partial sums only (no reduce launch): fp32 [splits][M][N] in a.part, or with
@@ -424,10 +472,10 @@ static void prefill_epi(const PrefillArgs& a, int epilogue, hipStream_t st) {
 template <int FMT>
 static void prefill_group_partials(const PrefillArgs& a, hipStream_t st) {
   switch (a.group) {
-    case 32: prefill_launch<1, MTL_EPI_NONE, FMT>(a, st, false); break;
-    case 64: prefill_launch<2, MTL_EPI_NONE, FMT>(a, st, false); break;
-    case 128: prefill_launch<4, MTL_EPI_NONE, FMT>(a, st, false); break;
-    default: prefill_launch<8, MTL_EPI_NONE, FMT>(a, st, false); break;
+    case 32: prefill_partials_launch<1, FMT>(a, st); break;
+    case 64: prefill_partials_launch<2, FMT>(a, st); break;
+    case 128: prefill_partials_launch<4, FMT>(a, st); break;
+    default: prefill_partials_launch<8, FMT>(a, st); break;
   }
 }
 
@@ -447,16 +495,23 @@ static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
                         const int32_t* strip_weight, const void* scales, const int32_t* zeros,
                         int64_t N, int32_t group_size, int32_t zero_offset, int32_t epilogue,
                         int32_t out_dtype, void* y, int64_t ldy, float* workspace,
-                        int64_t ws_bytes, int fmt, hipStream_t st);
+                        int64_t ws_bytes, int fmt, hipStream_t st,
+                        const float* xsum = nullptr);
 
 static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
                              const int32_t* strip_weight, const void* scales,
                              const int32_t* zeros, int64_t N, int32_t group_size,
                              int32_t zero_offset, int32_t epilogue, int32_t out_dtype, void* y,
                              int64_t ldy, float* workspace, int64_t ws_bytes, int fmt,
-                             hipStream_t st) {
+                             hipStream_t st, const float* xsum) {
   if (!x || !strip_weight || !scales || (!y && epilogue != kEpiPartials))
     return MTL_ERR_INVALID_ARG;
+  // staged x: the plain, SiLU*up and partials epilogues; its 32-channel sums 16-byte rows
+  if (xsum && epilogue == MTL_EPI_RESIDUAL) return MTL_ERR_INVALID_ARG;
+  if (xsum && (!aligned16(xsum) || M * (K / 32) * 4 >= ((int64_t)1 << 31))) {
+    if (!aligned16(xsum)) return MTL_ERR_ALIGN;
+    return MTL_ERR_SHAPE;
+  }
   if (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_RESIDUAL && epilogue != MTL_EPI_SILU_MUL &&
       epilogue != kEpiPartials)
     return MTL_ERR_INVALID_ARG;
@@ -501,6 +556,8 @@ static int prefill_gemm(const void* x, int64_t M, int64_t ldx, int64_t K,
   a.splits = need > 0 && workspace && ws_bytes >= need ? (int)(need / (M * N * 4)) : 1;
   a.kps = a.kblocks / a.splits;
   a.part = workspace;
+  a.xsum = xsum;
+  a.ldsum = K / 32;
   if (epilogue == kEpiPartials) {
     // the caller sums the splits (mtl_residual_rmsnorm_gather): as many splits as the
     // shape takes, into `workspace`; with one split the sums go there as fp32 y
@@ -555,8 +612,8 @@ int64_t mtl_w4_gemm_prefill_partials_bytes(int64_t M, int64_t K, int64_t N) {
   return (int64_t)s * M * N * 4;
 }
 
-int mtl_w4_gemm_prefill_partials(const void* x, int64_t M, int64_t ldx, int64_t K,
-                                 const int32_t* strip_weight, const void* meta,
+int mtl_w4_gemm_prefill_partials(const void* x, const float* x_sums, int64_t M, int64_t ldx,
+                                 int64_t K, const int32_t* strip_weight, const void* meta,
                                  const int32_t* strip_zeros, int64_t N, int32_t group_size,
                                  int32_t zero_offset, int32_t meta_format, float* partials,
                                  int64_t partials_bytes, void* stream) {
@@ -569,7 +626,26 @@ int mtl_w4_gemm_prefill_partials(const void* x, int64_t M, int64_t ldx, int64_t 
                       meta_format == MTL_META_GPTQ ? zero_offset : 0, kEpiPartials,
                       MTL_OUT_F32, partials, N, partials, partials_bytes,
                       meta_format == MTL_META_QSZ ? STRIP_META_QSZ : STRIP_META_GPTQ,
-                      (hipStream_t)stream);
+                      (hipStream_t)stream, x_sums);
+}
+
+int mtl_w4_gemm_prefill_staged(const void* x, const float* x_sums, int64_t M, int64_t ldx,
+                               int64_t K, const int32_t* strip_weight, const void* meta,
+                               const int32_t* strip_zeros, int64_t N, int32_t group_size,
+                               int32_t zero_offset, int32_t meta_format, int32_t epilogue,
+                               int32_t out_dtype, void* y, int64_t ldy, float* workspace,
+                               int64_t ws_bytes, void* stream) {
+  if (meta_format != MTL_META_GPTQ && meta_format != MTL_META_QSZ) return MTL_ERR_INVALID_ARG;
+  if (meta_format == MTL_META_GPTQ && !strip_zeros) return MTL_ERR_INVALID_ARG;
+  if (meta_format == MTL_META_GPTQ && !aligned16(strip_zeros)) return MTL_ERR_ALIGN;
+  if (!x_sums || (epilogue != MTL_EPI_NONE && epilogue != MTL_EPI_SILU_MUL))
+    return MTL_ERR_INVALID_ARG;
+  return prefill_gemm(x, M, ldx, K, strip_weight, meta,
+                      meta_format == MTL_META_GPTQ ? strip_zeros : nullptr, N, group_size,
+                      meta_format == MTL_META_GPTQ ? zero_offset : 0, epilogue, out_dtype, y,
+                      ldy, workspace, ws_bytes,
+                      meta_format == MTL_META_QSZ ? STRIP_META_QSZ : STRIP_META_GPTQ,
+                      (hipStream_t)stream, x_sums);
 }
 
 int mtl_w4_gemm_prefill_qsz(const void* x, int64_t M, int64_t ldx, int64_t K,

@@ -152,6 +152,10 @@ class FastDecoder:
         # launch sums them (q/k norm + RoPE + KV write; residual add + the next RMSNorm)
         # (False: the GEMMs' own split-sum launches, then those launches; the same bits)
         self.fuse_split_sums = True
+        # with fuse_split_sums: the norms stage x for the q|k|v and gate|up GEMMs (pair order
+        # and 32-channel sums), so their workgroups copy it instead of reordering and summing
+        # it (False: each GEMM stages x itself; the same bits)
+        self.stage_prefill_x = True
         # strip plan: which GEMVs run as full-K strips (one "split"); the others (split_k)
         # keep the split-K kernel and hand their partials to the consumer
         self.strip_gemv = {name: self.strip and name not in split_k
@@ -672,6 +676,9 @@ class FastDecoder:
                      for k, n in ((cfg.hidden, cfg.hidden), (cfg.intermediate, cfg.hidden),
                                   (cfg.hidden, cfg.qkv_out)))
         pf["part"] = torch.empty(max(nbytes, 16) // 4, dtype=torch.float32, device=dev)
+        # the norms' output staged for the q|k|v and gate|up GEMMs: its 32-channel sums
+        pf["xsum"] = torch.empty(rows, max(cfg.hidden // 32, 1), dtype=torch.float32,
+                                 device=dev)
         self._pf = pf
         return pf
 
@@ -694,17 +701,39 @@ class FastDecoder:
             N.OUT_BF16, y.data_ptr(), ldy, None if ws is None else ws.data_ptr(),
             0 if ws is None else ws.numel() * 4, stream), "mtl_w4_gemm_prefill")
 
-    def _prefill_partials(self, x, rows: int, lin, part: torch.Tensor, stream) -> int:
+    def _prefill_staged(self) -> bool:
+        """Whether the prompt's norms stage x for the GEMMs (pair order and 32-channel sums,
+        mtl_rmsnorm_gather_staged / mtl_w4_gemm_prefill_staged)."""
+        return self.fuse_split_sums and self.stage_prefill_x and self.m.cfg.hidden % 32 == 0
+
+    def _prefill_gemm_staged(self, x, xsum, rows: int, lin, epilogue: int, y, ldy: int,
+                             stream) -> None:
+        """One prompt-length int4 GEMM on staged x (mtl_w4_gemm_prefill_staged)."""
+        qw, layout = lin.stream_weight(True)
+        sc, qz = lin.strip_meta()
+        qsz = layout == N.LAYOUT_STRIP_QSZ
+        ws = ops.prefill_workspace(self.dev, rows, lin.in_features, lin.out_features)
+        N.check(N.load().mtl_w4_gemm_prefill_staged(
+            x.data_ptr(), xsum.data_ptr(), rows, x.stride(0), lin.in_features, qw.data_ptr(),
+            sc.data_ptr(), None if qsz else qz.data_ptr(), lin.out_features, lin.group_size,
+            0 if qsz else lin.zero_offset, N.META_QSZ if qsz else N.META_GPTQ, epilogue,
+            N.OUT_BF16, y.data_ptr(), ldy, None if ws is None else ws.data_ptr(),
+            0 if ws is None else ws.numel() * 4, stream), "mtl_w4_gemm_prefill_staged")
+
+    def _prefill_partials(self, x, rows: int, lin, part: torch.Tensor, stream,
+                          xsum: torch.Tensor | None = None) -> int:
         """The K-split partial sums of a prompt-length q|k|v, o or down GEMM into ``part``
-        (mtl_w4_gemm_prefill_partials); returns the split count for the launch that sums
-        them (mtl_qk_norm_rope_kv_rows_partials, mtl_residual_rmsnorm_gather)."""
+        (mtl_w4_gemm_prefill_partials; ``xsum``: x staged); returns the split count for the
+        launch that sums them (mtl_qk_norm_rope_kv_rows_partials,
+        mtl_residual_rmsnorm_gather)."""
         lib = N.load()
         qw, layout = lin.stream_weight(True)
         sc, qz = lin.strip_meta()
         qsz = layout == N.LAYOUT_STRIP_QSZ
         K, Nc = lin.in_features, lin.out_features
         N.check(lib.mtl_w4_gemm_prefill_partials(
-            x.data_ptr(), rows, x.stride(0), K, qw.data_ptr(), sc.data_ptr(),
+            x.data_ptr(), None if xsum is None else xsum.data_ptr(), rows, x.stride(0), K,
+            qw.data_ptr(), sc.data_ptr(),
             None if qsz else qz.data_ptr(), Nc, lin.group_size, 0 if qsz else lin.zero_offset,
             N.META_QSZ if qsz else N.META_GPTQ, part.data_ptr(), part.numel() * 4, stream),
             "mtl_w4_gemm_prefill_partials")
@@ -713,7 +742,8 @@ class FastDecoder:
     def _prefill_residual_norm(self, x_in, rows: int, lin, norm_w, gather, out, stream) -> None:
         """``h += x_in @ lin`` and ``out = RMSNorm(h)`` gathered by ``gather``: the GEMM's
         split partials, then the split sum, residual add and norm in one launch (the bits
-        of the GEMM's residual launch followed by mtl_rmsnorm_gather)."""
+        of the GEMM's residual launch followed by mtl_rmsnorm_gather), out staged for the
+        next GEMM when the prompt stages x."""
         cfg, pf = self.m.cfg, self._pf
         h, part = pf["h"], pf["part"]
         if not self.fuse_split_sums:
@@ -727,8 +757,9 @@ class FastDecoder:
         N.check(N.load().mtl_residual_rmsnorm_gather(
             part.data_ptr(), splits, part.numel() * 4, h.data_ptr(), cfg.hidden,
             norm_w.data_ptr(),
-            None if gather is None else gather.data_ptr(), out.data_ptr(), cfg.hidden, rows,
-            cfg.hidden, ctypes.c_float(cfg.eps), stream), "mtl_residual_rmsnorm_gather")
+            None if gather is None else gather.data_ptr(), out.data_ptr(), cfg.hidden,
+            pf["xsum"].data_ptr() if self._prefill_staged() else None, rows, cfg.hidden,
+            ctypes.c_float(cfg.eps), stream), "mtl_residual_rmsnorm_gather")
 
     def prefill_rows(self, ids: torch.Tensor, pos0: int = 0) -> torch.Tensor:
         """Every layer over the prompt rows ``ids`` (int64 ``[L, n_tables]``: one id per
@@ -755,16 +786,23 @@ class FastDecoder:
                                    self.table_ptrs.data_ptr(), self.vocabs.data_ptr(), cfg.hidden,
                                    h.data_ptr(), st), "mtl_embed_rows")
         n_layers = len(m.layers)
+        staged = self._prefill_staged()
+        xsum = pf["xsum"] if staged else None
         for li, lyr in enumerate(m.layers):
             lq = lyr["qkv"]
-            if li == 0:   # later layers' input norms ride on the previous down GEMM
+            if li == 0 and staged:   # later layers' input norms ride on the previous down GEMM
+                N.check(lib.mtl_rmsnorm_gather_staged(
+                    h.data_ptr(), cfg.hidden, lyr["input_layernorm"].data_ptr(), p(lq.perm),
+                    x.data_ptr(), cfg.hidden, xsum.data_ptr(), rows, cfg.hidden, eps, st),
+                    "mtl_rmsnorm_gather_staged")
+            elif li == 0:
                 N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
                                                lyr["input_layernorm"].data_ptr(),
                                                p(lq.perm), x.data_ptr(), cfg.hidden, rows,
                                                cfg.hidden, eps, st), "mtl_rmsnorm_gather")
             fuse_qkv = self.fuse_split_sums
             if fuse_qkv:
-                splits = self._prefill_partials(x, rows, lq, pf["part"], st)
+                splits = self._prefill_partials(x, rows, lq, pf["part"], st, xsum)
             else:
                 self._prefill_gemm(x, rows, lq, N.EPI_NONE, qkv, cfg.qkv_out, st)
             if self.v_keep[li]:
@@ -800,9 +838,14 @@ class FastDecoder:
                 # int4 gate and the bf16-kept up_proj (gptq.py:689-693), then SiLU(gate) * up
                 # in bf16 as the reference's MLP forms it (model.py:40-44)
                 gate = pf["gate"]
-                self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_NONE, gate, cfg.intermediate, st)
+                if staged:
+                    self._prefill_gemm_staged(x, xsum, rows, lyr["gate_up"], N.EPI_NONE, gate,
+                                              cfg.intermediate, st)
+                else:
+                    self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_NONE, gate,
+                                       cfg.intermediate, st)
                 x_up = x
-                if lyr["gate_up"].perm is not None:   # up reads natural order
+                if lyr["gate_up"].perm is not None or staged:   # up reads natural order
                     x_up = pf["x_nat"]
                     N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), cfg.hidden,
                                                    lyr["post_attention_layernorm"].data_ptr(),
@@ -810,6 +853,9 @@ class FastDecoder:
                                                    cfg.hidden, eps, st), "mtl_rmsnorm_gather")
                 up = torch.nn.functional.linear(x_up[:rows], lyr["up_keep"])
                 torch.mul(torch.nn.functional.silu(gate[:rows]), up, out=act[:rows])
+            elif staged:
+                self._prefill_gemm_staged(x, xsum, rows, lyr["gate_up"], N.EPI_SILU_MUL, act,
+                                          cfg.intermediate, st)
             else:
                 self._prefill_gemm(x, rows, lyr["gate_up"], N.EPI_SILU_MUL, act,
                                    cfg.intermediate, st)

@@ -211,19 +211,21 @@ def test_prefill_partials_validation(lib):
     pb = lib.mtl_w4_gemm_prefill_partials_bytes(256, 4096, 4096)
     assert pb > 256 * 4096 * 4 and pb % (256 * 4096 * 4) == 0
     assert lib.mtl_w4_gemm_prefill_partials_bytes(256, 4100, 4096) == 0
-    pp = lambda fmt=N.META_GPTQ, zeros=FAKE, part=FAKE, nbytes=pb: \
-        lib.mtl_w4_gemm_prefill_partials(FAKE, 256, 4096, 4096, FAKE, FAKE, zeros, 4096,  # noqa: E731
-                                         128, 0, fmt, part, nbytes, None)
+    pp = lambda fmt=N.META_GPTQ, zeros=FAKE, part=FAKE, nbytes=pb, xs=None: \
+        lib.mtl_w4_gemm_prefill_partials(FAKE, xs, 256, 4096, 4096, FAKE, FAKE, zeros,  # noqa: E731
+                                         4096, 128, 0, fmt, part, nbytes, None)
     assert pp(fmt=2) == N.MTL_ERR_INVALID_ARG
     assert pp(zeros=None) == N.MTL_ERR_INVALID_ARG          # GPTQ metadata has zeros
     assert pp(part=None) == N.MTL_ERR_INVALID_ARG
     assert pp(nbytes=pb - 4) == N.MTL_ERR_WORKSPACE
     assert pp(fmt=N.META_QSZ, zeros=None, nbytes=pb - 4) == N.MTL_ERR_WORKSPACE
+    assert pp(xs=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN   # staged sums: 16-byte rows
+    assert pp(xs=FAKE, nbytes=pb - 4) == N.MTL_ERR_WORKSPACE
     # the split sum + residual + RMSNorm: splits, the partials' bytes, out distinct from h
     eps = ctypes.c_float(1e-6)
     rn = lambda splits=4, nbytes=4 * 16 * 4096 * 4, h=FAKE, out=ctypes.c_void_p(0x2000), \
-        ldo=4096: lib.mtl_residual_rmsnorm_gather(FAKE, splits, nbytes, h, 4096, FAKE,  # noqa: E731
-                                                  None, out, ldo, 16, 4096, eps, None)
+        ldo=4096, sums=None, n=4096: lib.mtl_residual_rmsnorm_gather(  # noqa: E731
+            FAKE, splits, nbytes, h, n, FAKE, None, out, ldo, sums, 16, n, eps, None)
     assert rn(splits=0) == N.MTL_ERR_SHAPE
     assert rn(nbytes=4 * 16 * 4096 * 4 - 4) == N.MTL_ERR_WORKSPACE
     assert rn(ldo=4000) == N.MTL_ERR_SHAPE
@@ -231,6 +233,22 @@ def test_prefill_partials_validation(lib):
     assert rn(out=FAKE) == N.MTL_ERR_INVALID_ARG            # h is updated in place
     assert rn(h=None) == N.MTL_ERR_INVALID_ARG
     assert rn(splits=9) == N.MTL_ERR_SHAPE                  # at most 8 splits
+    assert rn(sums=FAKE, n=4080, ldo=4080) == N.MTL_ERR_SHAPE   # staged: n % 32
+    assert rn(sums=ctypes.c_void_p(0x1002)) == N.MTL_ERR_ALIGN
+    # the norm staged for the GEMM: n % 32, the sums buffer, a 16-byte gather
+    sg = lambda n=4096, sums=FAKE, gather=None: lib.mtl_rmsnorm_gather_staged(  # noqa: E731
+        FAKE, n, FAKE, gather, ctypes.c_void_p(0x2000), n, sums, 16, n, eps, None)
+    assert sg(n=4080) == N.MTL_ERR_SHAPE
+    assert sg(sums=None) == N.MTL_ERR_INVALID_ARG
+    assert sg(gather=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
+    # the GEMM on staged x: plain and SiLU*up epilogues only, the sums required
+    gs = lambda epi=0, xs=FAKE, fmt=N.META_GPTQ: lib.mtl_w4_gemm_prefill_staged(  # noqa: E731
+        FAKE, xs, 256, 4096, 4096, FAKE, FAKE, FAKE, 4096, 128, 0, fmt, epi, 0, FAKE, 4096,
+        None, 0, None)
+    assert gs(epi=1) == N.MTL_ERR_INVALID_ARG               # the residual takes plain x
+    assert gs(xs=None) == N.MTL_ERR_INVALID_ARG
+    assert gs(fmt=2) == N.MTL_ERR_INVALID_ARG
+    assert gs(xs=ctypes.c_void_p(0x1008)) == N.MTL_ERR_ALIGN
     # the q|k|v split partials into the q/k norm + RoPE launch: the partial columns cover
     # whole heads, the heads past them need the bf16 buffer, and the partials' bytes
     qk = lambda splits=2, nbytes=2 * 16 * 6144 * 4, pcols=6144, qkv=None, ldq=6144: \

@@ -415,16 +415,16 @@ def test_moss_prefill_matches_stepwise(dev):
     assert rel_l2(fb(kb), fb(model.k_cache)) < 1e-2 and rel_l2(fb(vb), fb(model.v_cache)) < 1e-2
 
 
-def _meta_weights(meta, m, k, n, dev, seed):
+def _meta_weights(meta, m, k, n, dev, seed, group=128):
     """Strip weight, meta and zeros of a random [k, n] int4 linear in either format."""
     if meta == "gptq":
-        case = synth.gptq_case(k=k, n=n, m=1, group=128, act_order=False, seed=seed,
+        case = synth.gptq_case(k=k, n=n, m=1, group=group, act_order=False, seed=seed,
                                ref_cols=np.arange(1))
         qw, sc, qz = strip_linear(case, dev)
         return qw, sc, qz, N.META_GPTQ
     from oracle import gptq_ref as G
     from tests.test_gemm_gpu import _qsz_weights
-    q, qsz = _qsz_weights(np.random.default_rng(seed), n, k, 128)
+    q, qsz = _qsz_weights(np.random.default_rng(seed), n, k, group)
     packed = ops.convert_weight_to_int4pack(torch.from_numpy(G.prepack_u8(q)).to(dev), 8)
     return packed, t_bf16(qsz, dev), None, N.META_QSZ
 
@@ -459,25 +459,25 @@ def test_residual_rmsnorm_gather_matches_two_launches(dev, lib, meta, m, k, n, s
     part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     # one float short of the splits' partials is refused before any launch
     assert lib.mtl_w4_gemm_prefill_partials(
-        x.data_ptr(), m, k, k, qw.data_ptr(), meta_t.data_ptr(),
+        x.data_ptr(), None, m, k, k, qw.data_ptr(), meta_t.data_ptr(),
         None if qz is None else qz.data_ptr(), n, 128, 0, fmt, part.data_ptr(), nbytes - 4,
         stream()) == N.MTL_ERR_WORKSPACE
     N.check(lib.mtl_w4_gemm_prefill_partials(
-        x.data_ptr(), m, k, k, qw.data_ptr(), meta_t.data_ptr(),
+        x.data_ptr(), None, m, k, k, qw.data_ptr(), meta_t.data_ptr(),
         None if qz is None else qz.data_ptr(), n, 128, 0, fmt, part.data_ptr(), nbytes,
         stream()), "partials")
     h_b = h0.clone()
     out_b = torch.zeros(m, n + 64, dtype=torch.bfloat16, device=dev)
     N.check(lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes, h_b.data_ptr(),
                                             n, w.data_ptr(), perm.data_ptr(), out_b.data_ptr(),
-                                            n + 64, m, n, eps, stream()), "residual norm")
+                                            n + 64, None, m, n, eps, stream()), "residual norm")
     torch.cuda.synchronize()
     assert torch.equal(h_a, h_b) and not torch.equal(h_a, h0)
     assert torch.equal(out_a, out_b[:, :n]) and not out_b[:, n:].any()
-    args = (w.data_ptr(), None, out_b.data_ptr(), n + 64, m, n, eps, stream())
+    args = (w.data_ptr(), None, out_b.data_ptr(), n + 64, None, m, n, eps, stream())
     assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes, h_b.data_ptr(), n,
-                                           w.data_ptr(), None, h_b.data_ptr(), n, m, n, eps,
-                                           stream()) == N.MTL_ERR_INVALID_ARG   # out is h
+                                           w.data_ptr(), None, h_b.data_ptr(), n, None, m, n,
+                                           eps, stream()) == N.MTL_ERR_INVALID_ARG   # out is h
     assert lib.mtl_residual_rmsnorm_gather(part.data_ptr(), splits, nbytes - 4, h_b.data_ptr(),
                                            n, *args) == N.MTL_ERR_WORKSPACE
 
@@ -513,8 +513,8 @@ def test_qk_norm_rope_partials_match_two_launches(dev, lib, m, part_heads):
             nbytes = int(lib.mtl_w4_gemm_prefill_partials_bytes(m, k, pcols))
             part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
             N.check(lib.mtl_w4_gemm_prefill_partials(
-                x.data_ptr(), m, k, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), pcols, 128,
-                0, fmt, part.data_ptr(), nbytes, stream()), "partials")
+                x.data_ptr(), None, m, k, k, qw.data_ptr(), sc.data_ptr(), qz.data_ptr(), pcols,
+                128, 0, fmt, part.data_ptr(), nbytes, stream()), "partials")
             splits = nbytes // (m * pcols * 4)
             v_src = qkv.data_ptr() if pcols < cols else None
             N.check(lib.mtl_qk_norm_rope_kv_rows_partials(
@@ -529,6 +529,71 @@ def test_qk_norm_rope_partials_match_two_launches(dev, lib, m, part_heads):
     (q1, k1, v1), (q2, k2, v2) = outs
     assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
     assert q1.any() and k1[:, pos0:pos0 + m].any() and v1[:, pos0:pos0 + m].any()
+
+
+@pytest.mark.parametrize("meta,group", [("gptq", 128), ("gptq", 32), ("gptq", 256),
+                                        ("qsz", 32), ("qsz", 64), ("qsz", 128)])
+@pytest.mark.parametrize("m", [1, 77, 256])
+def test_staged_x_matches_plain_x(dev, lib, meta, group, m):
+    # the norm's output staged for the GEMM (pair order, 32-channel sums): un-paired it is
+    # the natural output, its sums are the rows' group sums, and the GEMM on it gives the
+    # bits of the GEMM on the natural rows with the plain, SiLU*up and partials epilogues
+    print("staged x", meta, group, m, flush=True)
+    k, n = 1024, 512
+    qw, meta_t, qz, fmt = _meta_weights(meta, m, k, n, dev, seed=group + m, group=group)
+    r = np.random.default_rng(group * 7 + m)
+    h = tb(3 * r.standard_normal((m, k)), dev)
+    w = tb(1 + 0.1 * r.standard_normal(k), dev)
+    perm = torch.from_numpy(r.permutation(k).astype(np.int32)).to(dev) if meta == "gptq" else None
+    pp = None if perm is None else perm.data_ptr()
+    eps = ctypes.c_float(1e-6)
+    x_nat = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
+    x_st = torch.empty_like(x_nat)
+    sums = torch.empty(m, k // 32, dtype=torch.float32, device=dev)
+    N.check(lib.mtl_rmsnorm_gather(h.data_ptr(), k, w.data_ptr(), pp, x_nat.data_ptr(), k, m, k,
+                                   eps, stream()), "norm")
+    N.check(lib.mtl_rmsnorm_gather_staged(h.data_ptr(), k, w.data_ptr(), pp, x_st.data_ptr(), k,
+                                          sums.data_ptr(), m, k, eps, stream()), "staged norm")
+    torch.cuda.synchronize()
+    unpaired = x_st.view(m, k // 8, 8)[:, :, [0, 2, 4, 6, 1, 3, 5, 7]].reshape(m, k)
+    assert torch.equal(unpaired, x_nat)
+    ref = x_nat.float().view(m, k // 32, 32).sum(-1)
+    assert torch.allclose(sums, ref, rtol=1e-5, atol=1e-4)
+    zp = None if qz is None else qz.data_ptr()
+    ws = ops.prefill_workspace(dev, m, k, n)
+    wsp, wsb = (None, 0) if ws is None else (ws.data_ptr(), ws.numel() * 4)
+
+    def plain(epi, y, odt, ldy):
+        if meta == "gptq":
+            return lib.mtl_w4_gemm_prefill(x_nat.data_ptr(), m, k, k, qw.data_ptr(),
+                                           meta_t.data_ptr(), zp, n, group, 0, epi, odt,
+                                           y.data_ptr(), ldy, wsp, wsb, stream())
+        return lib.mtl_w4_gemm_prefill_qsz(x_nat.data_ptr(), m, k, k, qw.data_ptr(),
+                                           meta_t.data_ptr(), n, group, epi, odt, y.data_ptr(),
+                                           ldy, wsp, wsb, stream())
+
+    def staged(epi, y, odt, ldy):
+        return lib.mtl_w4_gemm_prefill_staged(x_st.data_ptr(), sums.data_ptr(), m, k, k,
+                                              qw.data_ptr(), meta_t.data_ptr(), zp, n, group, 0,
+                                              fmt, epi, odt, y.data_ptr(), ldy, wsp, wsb,
+                                              stream())
+    for epi, odt, cols, dt in ((N.EPI_NONE, N.OUT_F32, n, torch.float32),
+                               (N.EPI_SILU_MUL, N.OUT_BF16, n // 2, torch.bfloat16)):
+        ya = torch.zeros(m, cols, dtype=dt, device=dev)
+        yb = torch.ones(m, cols, dtype=dt, device=dev)
+        N.check(plain(epi, ya, odt, cols), "plain")
+        N.check(staged(epi, yb, odt, cols), "staged")
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb), epi
+    nbytes = int(lib.mtl_w4_gemm_prefill_partials_bytes(m, k, n))
+    pa = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+    pb = torch.ones_like(pa)
+    for buf, xp, sp in ((pa, x_nat, None), (pb, x_st, sums.data_ptr())):
+        N.check(lib.mtl_w4_gemm_prefill_partials(
+            xp.data_ptr(), sp, m, k, k, qw.data_ptr(), meta_t.data_ptr(), zp, n, group, 0, fmt,
+            buf.data_ptr(), nbytes, stream()), "partials")
+    torch.cuda.synchronize()
+    assert torch.equal(pa, pb)
 
 
 def _prefill_both_ways(dec, model, rows_ids):
