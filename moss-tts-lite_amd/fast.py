@@ -672,9 +672,11 @@ class FastDecoder:
               "act": z(cfg.intermediate),
               "gate": z(cfg.intermediate) if any(self.up_keep) else None}
         lib = N.load()
-        nbytes = max(int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, k, n))
-                     for k, n in ((cfg.hidden, cfg.hidden), (cfg.intermediate, cfg.hidden),
-                                  (cfg.hidden, cfg.qkv_out)))
+        # the split count follows each GEMM's shape (a q|k without its kept v has fewer
+        # column tiles, so more splits): the largest of the layers' partial buffers
+        shapes = {(lyr[name].in_features, lyr[name].out_features)
+                  for lyr in self.m.layers for name in ("qkv", "o", "down")}
+        nbytes = max(int(lib.mtl_w4_gemm_prefill_partials_bytes(rows, k, n)) for k, n in shapes)
         pf["part"] = torch.empty(max(nbytes, 16) // 4, dtype=torch.float32, device=dev)
         # the norms' output staged for the q|k|v and gate|up GEMMs: its 32-channel sums
         pf["xsum"] = torch.empty(rows, max(cfg.hidden // 32, 1), dtype=torch.float32,
