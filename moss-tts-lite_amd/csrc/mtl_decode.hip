@@ -685,12 +685,12 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 // the position is read, and stages them in LDS.  Wave w scores positions 16w .. 16w+15
 // against every q head of the kv head with four v_mfma_f32_16x16x32_bf16 (A = K rows,
 // B = the q heads as columns).  The chunk softmax max and sum meet across the 4 waves
-// in LDS, and e * v is summed on the VALU: a wave per q head, a lane per 8 dims x 16
-// positions, reduced over the 4 position quarters.  Every cross-lane step of this kernel
-// (q/k RMSNorm, softmax, the quarter reduction, the merge) runs on the VALU (permlane swaps
-// and DPP, mtl_common.h) instead of ds_bpermute: the same bits, about 0.5 us less per launch
-// in the decode step.  The published (m, l, o[128]) per q
-// head and the merge are those of attn_decode_kernel.
+// in LDS, and O^T = V^T E^T runs on MFMA with the V^T operand read from the V rows by
+// ds_read_b64_tr_b16 (a wave per 32 dims, every q head at once).  Every cross-lane step of
+// this kernel (q/k RMSNorm, softmax, the merge) runs on the VALU (permlane swaps and DPP,
+// mtl_common.h) instead of ds_bpermute: the same bits, about 0.5 us less per launch in the
+// decode step.  The published (m, l, o[128]) per q head and the merge are those of
+// attn_decode_kernel.
 // ----------------------------------------------------------------------------------
 template <bool FROM_PART, bool LOCAL>
 __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
@@ -702,7 +702,7 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   __shared__ u32x4 k_lds[P][17];                // the chunk's K rows, 8 dims per item
   __shared__ u32x4 v_lds[P][17];
   __shared__ u32x4 q_lds[16][17];               // q heads (rows past n_rep zero)
-  __shared__ float e_lds[kAttnMaxRep][P];       // exp(s - m) per q head and position
+  __shared__ __attribute__((aligned(16))) float e_lds[kAttnMaxRep][P];   // exp(s - m), bf16 values
   __shared__ float red_m[4][16], red_l[4][16];  // per-wave max / sum per q head
   __shared__ __attribute__((aligned(16))) float w_lds[4][kAttnMaxChunks];
   __shared__ int last_flag;
@@ -835,63 +835,83 @@ __global__ void __launch_bounds__(256) attn_tile_kernel(AttnArgs a) {
   if (g == 0) red_l[wave][hd] = lsum;
   __syncthreads();
 
-  // 3. o[h] = sum_p e[h][p] v[p]: wave = q head (4 per pass), lane = 8 dims (l%16) x 16
-  //    positions (l/16 quarter); quarters reduced by shuffles; then publish (m, l, o).
-  const int dg = lane & 15, pq = lane >> 4;
-  for (int hp = 0; hp < n_rep; hp += 4) {
-    const int hr = hp + wave;
-    if (hr >= n_rep) break;                           // uniform over the wave
-    float o[8];
+  // 3. O^T (dims x q heads) = V^T (dims x positions) E^T (positions x heads) on MFMA:
+  //    wave w takes dims 32w .. 32w+31 (two 16-dim blocks) for every q head at once.  The
+  //    A operand V^T comes straight from the V rows in LDS through ds_read_b64_tr_b16: in
+  //    each 16-lane group, lane j reads 4 dims (4(j%4) ..) of position row j/4, and the
+  //    transpose hands lane i dim i of those 4 rows; two reads give a lane its 8
+  //    positions.  B = E^T: lane (g, hd) packs the bf16 probabilities (rounded above) of
+  //    head hd at its 8 positions.  Then publish (m, l, o).
+  {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const int hd2 = lane & 15, g2 = lane >> 4;
+    bf16x8 eb[2];                                  // B operands of the two 32-position steps
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = 0.f;
-    // every LDS read of the quarter first (16 V items, the 16 probabilities as 4 x 16 B),
-    // so their latencies overlap; then the sums in position order
-    u32x4 vq[16];
+    for (int ks = 0; ks < 2; ++ks) {
+      const float* er = &e_lds[hd2 < n_rep ? hd2 : 0][32 * ks + 8 * g2];
+      const float4 e0 = reinterpret_cast<const float4*>(er)[0];
+      const float4 e1 = reinterpret_cast<const float4*>(er)[1];
+      const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+      u32x4 w;
+      uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) vq[i] = v_lds[16 * pq + i][dg];
-    float4 eq[4];
+      for (int i = 0; i < 4; ++i)
+        wp[i] = hd2 < n_rep ? (__float_as_uint(ev[2 * i]) >> 16) |
+                                  (__float_as_uint(ev[2 * i + 1]) & 0xffff0000u)
+                            : 0u;
+      eb[ks] = __builtin_bit_cast(bf16x8, w);
+    }
+    // this lane's transpose-read addresses: row j/4 of its 8-row step, dims 4(j%4) ..
+    const int jr = (lane & 15) >> 2, jc = 4 * (lane & 3);
+    f4 acc[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) eq[i] = reinterpret_cast<const float4*>(&e_lds[hr][16 * pq])[i];
-    // positions in pairs on v_dot2_f32_bf16: the probabilities are bf16 values already
-    // (rounded above), packed (e[p], e[p+1]); v_perm puts dims d of rows p and p+1 side by
-    // side, so one dot2 adds both positions' terms of one dim
+    for (int mb = 0; mb < 2; ++mb) {
+      const int d0 = 32 * wave + 16 * mb + jc;     // first of this lane's 4 dims
+      s4 rv[2][2];
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      const float4 e4 = eq[i >> 2];
-      const float e0 = (i & 3) == 0 ? e4.x : e4.z, e1 = (i & 3) == 0 ? e4.y : e4.w;
-      const uint32_t ep = (__float_as_uint(e0) >> 16) | (__float_as_uint(e1) & 0xffff0000u);
-      const u32x4 v0 = vq[i], v1 = vq[i + 1];
-      const uint32_t a4[4] = {v0.x, v0.y, v0.z, v0.w}, b4[4] = {v1.x, v1.y, v1.z, v1.w};
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = __builtin_amdgcn_perm(b4[j], a4[j], 0x05040100u);  // (a.lo, b.lo)
-        const uint32_t hi = __builtin_amdgcn_perm(b4[j], a4[j], 0x07060302u);  // (a.hi, b.hi)
-        o[2 * j] = dot2_bf16(lo, ep, o[2 * j]);
-        o[2 * j + 1] = dot2_bf16(hi, ep, o[2 * j + 1]);
+        for (int hf = 0; hf < 2; ++hf) {
+          const int row = 32 * ks + 8 * g2 + 4 * hf + jr;
+          const uint16_t* src = reinterpret_cast<const uint16_t*>(v_lds[row]) + d0;
+          rv[ks][hf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (s4 __attribute__((address_space(3)))*)(src));
+        }
+      acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const s4 lo = rv[ks][0], hi = rv[ks][1];
+        const bf16x8 A = __builtin_bit_cast(
+            bf16x8, (short __attribute__((ext_vector_type(8)))){lo[0], lo[1], lo[2], lo[3],
+                                                                 hi[0], hi[1], hi[2], hi[3]});
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, eb[ks], acc[mb], 0, 0, 0);
       }
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = xor32_add(xor16_add(o[j]));
-    const float mh = fmaxf(fmaxf(red_m[0][hr], red_m[1][hr]), fmaxf(red_m[2][hr], red_m[3][hr]));
-    const float lh = (red_l[0][hr] + red_l[1][hr]) + (red_l[2][hr] + red_l[3][hr]);
-    float* ph = a.part + ((size_t)(kvh * n_rep + hr) * kAttnMaxChunks + c) * kAttnPart;
-    if (LOCAL) {
-      // plain stores: they end in this XCD's L2, where the merging workgroup reads them
-      if (lane == 0) *reinterpret_cast<float2*>(ph) = make_float2(mh, lh);
-      if (lane < 16) {
-        float4* po = reinterpret_cast<float4*>(ph + 4 + 8 * dg);
-        po[0] = make_float4(o[0], o[1], o[2], o[3]);
-        po[1] = make_float4(o[4], o[5], o[6], o[7]);
+    // acc[mb][r]: dim 32w + 16mb + 4g2 + r of q head hd2
+    if (hd2 < n_rep) {
+      float* ph = a.part + ((size_t)(kvh * n_rep + hd2) * kAttnMaxChunks + c) * kAttnPart;
+      if (wave == 0 && g2 == 0) {
+        const float mh = fmaxf(fmaxf(red_m[0][hd2], red_m[1][hd2]), fmaxf(red_m[2][hd2], red_m[3][hd2]));
+        const float lh = (red_l[0][hd2] + red_l[1][hd2]) + (red_l[2][hd2] + red_l[3][hd2]);
+        if (LOCAL) {
+          *reinterpret_cast<float2*>(ph) = make_float2(mh, lh);
+        } else {
+          __hip_atomic_store(ph, mh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(ph + 1, lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
-    } else {
-      if (lane == 0) {
-        __hip_atomic_store(ph, mh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(ph + 1, lh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (lane < 16) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          __hip_atomic_store(ph + 4 + 8 * dg + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int mb = 0; mb < 2; ++mb) {
+        float* po = ph + 4 + 32 * wave + 16 * mb + 4 * g2;
+        if (LOCAL) {
+          // plain stores: they end in this XCD's L2, where the merging workgroup reads them
+          *reinterpret_cast<float4*>(po) =
+              make_float4(acc[mb][0], acc[mb][1], acc[mb][2], acc[mb][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            __hip_atomic_store(po + r, acc[mb][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   }
