@@ -261,20 +261,21 @@ __global__ void __launch_bounds__(64) qk_norm_rope_rows_kernel(
 // at position pos0 + r attends to cache positions [0, pos0 + r]).
 //
 // Workgroup (kv head g, block of 16 rows); wave w serves q heads g * n_rep + w (+4).  Per
-// tile of 32 cache positions, staged once in LDS for the workgroup (K rows as they are,
-// V transposed to [dim][position]):
+// tile of 32 cache positions, staged once in LDS for the workgroup (K and V rows as they
+// are, 16-byte stores):
 //   S^T (positions x rows) = K Q^T: v_mfma_f32_16x16x32_bf16 with A = K rows, B = Q^T;
 //     lane (lg, lj) gets positions 16h + 4 lg + i of row lj, i = 0..3, h = 0, 1;
 //   online softmax per row (the lane's own column) in fp32;
 //   O^T (dims x rows) += V^T P^T: B = P^T is the lane's own 8 probabilities (bf16) with
 //     k index 8 lg + e standing for position 4 lg + e (e < 4) or 16 + 4 lg + e - 4, and A
-//     = V^T read from the transposed tile at the same positions.
+//     = V^T at the same positions, read from the V rows by ds_read_b64_tr_b16 (in each
+//     16-lane group lane j reads dims 4 (j % 4) .. of row j / 4, and the transpose hands
+//     lane i dim i of those 4 rows: two reads, positions 4 lg .. and 16 + 4 lg ..).
 // So no operand crosses lanes.  O^T / l goes out as bf16, each value to
 // out[r][out_index[c]] (the act-order input order of the o projection) or column c.
 // ----------------------------------------------------------------------------------
 constexpr int kPaRows = 16;
 constexpr int kPaKeys = 32;
-constexpr int kPaVtPitch = kPaKeys + 4;   // bf16 per V^T row: 72 bytes apart, bank spread
 
 struct PrefillAttnArgs {
   const uint16_t* q;        // bf16 [rows, H * 128]
@@ -292,16 +293,17 @@ __global__ void __launch_bounds__(512) prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int D = 128;
   // Two wave groups of 4 take alternate tiles (group g2: tiles 2 it + g2), each with its
   // own LDS tile; their (m, l, O) meet in LDS at the end.  The raw buffer holds the two
-  // K tiles ([32][16 items + 1 pad] u32x4 each), then the two V^T tiles, and after the
-  // loop the merge exchange.
+  // K tiles ([32][16 items + 1 pad] u32x4 each), then the two V tiles (the same form), and
+  // after the loop the merge exchange (4 x 32 x 64 + 4 x 2 x 64 floats: the same bytes).
   constexpr int kKItems = 2 * kPaKeys * 17;
-  __shared__ u32x4 lds_raw[kKItems + (2 * D * kPaVtPitch * 2) / 16];
+  __shared__ u32x4 lds_raw[2 * kKItems];
+  static_assert(2 * kKItems * 16 >= (4 * 32 * 64 + 4 * 2 * 64) * 4, "merge exchange");
   const int kvh = blockIdx.x, rb = blockIdx.y;
   const int t = threadIdx.x, wave = wave_id(), lane = t & 63;
   const int g2 = wave >> 2, hw = wave & 3, tg = t & 255;
   const int lg = lane >> 4, lj = lane & 15;
   u32x4* k_lds = lds_raw + g2 * kPaKeys * 17;                       // [32][17]
-  uint16_t* vt = reinterpret_cast<uint16_t*>(lds_raw + kKItems) + g2 * D * kPaVtPitch;
+  u32x4* v_lds = lds_raw + kKItems + g2 * kPaKeys * 17;             // [32][17]
   const int n_rep = a.H / a.Hkv;
   const int r0 = rb * kPaRows;
   const int my_row = r0 + lj;                          // this lane's query row
@@ -358,12 +360,7 @@ __global__ void __launch_bounds__(512) prefill_attn_kernel(PrefillAttnArgs a) {
       const int item = tg + 256 * j;
       const int kr = item >> 4, c8 = item & 15;
       k_lds[kr * 17 + c8] = kv[j];
-      const uint32_t vw[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[(8 * c8 + 2 * e) * kPaVtPitch + kr] = (uint16_t)(vw[e] & 0xffffu);
-        vt[(8 * c8 + 2 * e + 1) * kPaVtPitch + kr] = (uint16_t)(vw[e] >> 16);
-      }
+      v_lds[kr * 17 + c8] = vv[j];
     }
     __syncthreads();
     if (kt + 2 < ntiles) tile_load(kt + 2);
@@ -416,12 +413,20 @@ __global__ void __launch_bounds__(512) prefill_attn_kernel(PrefillAttnArgs a) {
       const u32x4 pw{cvt_pk_bf16(pv[0][0], pv[0][1]), cvt_pk_bf16(pv[0][2], pv[0][3]),
                      cvt_pk_bf16(pv[1][0], pv[1][1]), cvt_pk_bf16(pv[1][2], pv[1][3])};
       const bf16x8_t P = __builtin_bit_cast(bf16x8_t, pw);
+      typedef short s4 __attribute__((ext_vector_type(4)));
+      typedef short s8 __attribute__((ext_vector_type(8)));
+      // this lane's transpose-read rows (4 lg + lj / 4, and 16 more) and first dim
+      const uint16_t* vr0 = reinterpret_cast<const uint16_t*>(v_lds + (4 * lg + (lj >> 2)) * 17) +
+                            4 * (lj & 3);
+      const uint16_t* vr1 = vr0 + 16 * 17 * 8;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
-        const uint16_t* vrow = vt + (16 * d + lj) * kPaVtPitch;
-        const u32x2 v0 = *reinterpret_cast<const u32x2*>(vrow + 4 * lg);
-        const u32x2 v1 = *reinterpret_cast<const u32x2*>(vrow + 16 + 4 * lg);
-        const bf16x8_t A = __builtin_bit_cast(bf16x8_t, u32x4{v0.x, v0.y, v1.x, v1.y});
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (s4 __attribute__((address_space(3)))*)(vr0 + 16 * d));
+        const s4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (s4 __attribute__((address_space(3)))*)(vr1 + 16 * d));
+        const bf16x8_t A = __builtin_bit_cast(
+            bf16x8_t, s8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]});
         o[hi][d] = o[hi][d] * alpha;
         o[hi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, P, o[hi][d], 0, 0, 0);
       }
