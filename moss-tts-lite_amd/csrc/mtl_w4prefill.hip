@@ -413,12 +413,14 @@ __global__ void __launch_bounds__(256) prefill_reduce_kernel(PrefillArgs a) {
   }
 }
 
-// K splits for a launch of `tiles` workgroups over kb blocks: enough splits for about two
-// workgroups per CU, each split a whole number of ring turns (kPfRing blocks), at most
-// kPfMaxSplits.
+// K splits for a launch of `tiles` workgroups over kb blocks: enough splits for about three
+// workgroups per CU (the 3 that fit), each split a whole number of ring turns (kPfRing
+// blocks), at most kPfMaxSplits.  At 256 prompt rows this gives q|k|v 4 splits and down 6
+// (2 and 4 for two workgroups per CU: the prompt 7.71 -> 7.67 ms, min 7.65 -> 7.55, same
+// box; one per CU 7.75 against 7.30; four, which splits gate|up too, 8.29).
 static int prefill_splits(int64_t tiles, int64_t kb, int cus) {
   int s = 1;
-  while (s < kPfMaxSplits && tiles * s < 2 * cus) ++s;
+  while (s < kPfMaxSplits && tiles * s < 3 * cus) ++s;
   while (s > 1 && kb % ((int64_t)s * kPfRing) != 0) --s;
   return s;
 }

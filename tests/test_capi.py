@@ -207,7 +207,7 @@ def test_prefill_gemm_validation(lib):
 def test_prefill_partials_validation(lib):
     # the split partials of a residual GEMM: their bytes (one plane when the grid fills the
     # CUs), the metadata format, and a buffer short of the splits' planes
-    assert lib.mtl_w4_gemm_prefill_partials_bytes(1024, 1024, 4096) == 1024 * 4096 * 4
+    assert lib.mtl_w4_gemm_prefill_partials_bytes(2048, 1024, 4096) == 2048 * 4096 * 4
     pb = lib.mtl_w4_gemm_prefill_partials_bytes(256, 4096, 4096)
     assert pb > 256 * 4096 * 4 and pb % (256 * 4096 * 4) == 0
     assert lib.mtl_w4_gemm_prefill_partials_bytes(256, 4100, 4096) == 0

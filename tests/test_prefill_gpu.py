@@ -432,7 +432,7 @@ def _meta_weights(meta, m, k, n, dev, seed, group=128):
 @pytest.mark.parametrize("meta", ["gptq", "qsz"])
 @pytest.mark.parametrize("m,k,n,splits", [(77, 1024, 512, 4), (256, 4096, 4096, 4),
                                           (33, 12288, 4096, 8), (1, 2048, 1024, 8),
-                                          (1024, 1024, 4096, 1)])
+                                          (2048, 1024, 4096, 1)])
 def test_residual_rmsnorm_gather_matches_two_launches(dev, lib, meta, m, k, n, splits):
     # the GEMM's split partials, then one launch for the split sum, the residual add and
     # the gathered RMSNorm: bit for bit the GEMM's residual launch followed by
