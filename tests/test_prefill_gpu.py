@@ -597,16 +597,19 @@ def test_staged_x_matches_plain_x(dev, lib, meta, group, m):
 
 
 def _prefill_both_ways(dec, model, rows_ids):
+    # fused split sums on staged x, then on x the GEMMs stage themselves, then neither: the
+    # last two returned (the first checked against the second here)
     out = []
-    for fuse in (True, False):
+    for fuse, stage in ((True, True), (True, False), (False, False)):
         model.k_cache.zero_()
         model.v_cache.zero_()
-        dec.fuse_split_sums = fuse
+        dec.fuse_split_sums, dec.stage_prefill_x = fuse, stage
         h = dec.prefill_rows(rows_ids).clone()
         torch.cuda.synchronize()
         out.append((h, model.k_cache.clone(), model.v_cache.clone()))
-    dec.fuse_split_sums = True
-    return out
+    dec.fuse_split_sums, dec.stage_prefill_x = True, True
+    assert all(torch.equal(a, b) for a, b in zip(out[0], out[1]))
+    return out[1:]
 
 
 @pytest.mark.parametrize("v_keep,L", [(False, 37), (True, 70), (False, 1)])
